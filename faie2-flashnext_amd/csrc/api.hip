@@ -1,0 +1,264 @@
+// C ABI of libfaie2fn.so (declared in include/faie2fn.h).
+//
+// Section 1 keeps the reference's fn_* names and signatures (engine/faie2fn.cu:2492-2935) so its ctypes layer
+// (flashnext/fn.py) binds unchanged; the model-level ones report that this library carries only the
+// decode-attention path.  Sections 2 and 3 are this path's hooks: host arrays in / out (synchronous, device 0,
+// the reference's unit-test-hook style, faie2fn.cu:2745) and the device-buffer entry points an engine calls.
+#include "gdn.h"
+
+#include "../../include/faie2fn.h"
+
+#include <cstring>
+#include <vector>
+
+#define FN_API extern "C" __attribute__((visibility("default")))
+
+namespace fn {
+
+static std::string g_err;
+
+void set_error(const std::string &msg) { g_err = msg; }
+const char *error_cstr() { return g_err.c_str(); }
+
+}  // namespace fn
+
+using fn::set_error;
+
+// ---------------------------------------------------------------------------------------------
+// 1. reference API
+
+namespace {
+
+const char *kNoModel =
+    "not built: libfaie2fn.so carries the decode-attention path only (DeltaNet block + GQA decode); model loading, "
+    "the forward pass, GEMV, MoE and routing are not part of it";
+
+// switches the reference exposes for its forward; kept so scripts that set them still run
+int g_pdl = 1, g_early = 1, g_moe_var = 0, g_bench_hot = 0, g_use_graphs = 1;
+
+// device buffers of one host-hook call, released on every return path
+struct DevBufs {
+    std::vector<void *> ptrs;
+    ~DevBufs() {
+        for (void *p : ptrs) (void) hipFree(p);
+    }
+    template <typename T> int alloc(T **p, size_t n) {
+        *p = nullptr;
+        if (n == 0) n = 1;
+        hipError_t e = hipMalloc((void **) p, n * sizeof(T));
+        if (e != hipSuccess) {
+            set_error(std::string("hipMalloc(") + std::to_string(n * sizeof(T)) + " B) -> " + hipGetErrorString(e));
+            return -1;
+        }
+        ptrs.push_back(*p);
+        return 0;
+    }
+    template <typename T> int up(T **p, const T *h, size_t n) {
+        if (alloc(p, n)) return -1;
+        FN_CK(hipMemcpy(*p, h, n * sizeof(T), hipMemcpyHostToDevice));
+        return 0;
+    }
+};
+
+int use_device0() {
+    int n = 0;
+    FN_CK(hipGetDeviceCount(&n));
+    if (n < 1) FN_FAIL("no HIP device");
+    FN_CK(hipSetDevice(0));
+    return 0;
+}
+
+}  // namespace
+
+FN_API const char *fn_error(void) { return fn::error_cstr(); }
+FN_API void fn_free(void) {}
+FN_API int fn_load(const char *, const char *, int, int) { FN_FAIL(kNoModel); }
+FN_API int fn_split(void) { return -1; }
+FN_API double fn_dev_gb(int) { return -1; }
+FN_API int fn_n_past(void) { return -1; }
+FN_API double fn_last_ms(void) { return -1; }
+FN_API int fn_reset(void) { FN_FAIL("not loaded"); }
+FN_API int fn_use_graphs(int on) {
+    g_use_graphs = on != 0;
+    FN_FAIL("not loaded");
+}
+FN_API int fn_forward(const int32_t *, int, float *, int32_t *) { FN_FAIL("not loaded"); }
+FN_API int fn_debug_layers(float *) { FN_FAIL("not loaded"); }
+FN_API int fn_test_dequant(uint32_t, const uint8_t *, int, int, float *) { FN_FAIL(kNoModel); }
+FN_API void fn_gemv_override(int, int, int, int) {}
+FN_API void fn_gemv_waves(int) {}
+FN_API void fn_pdl(int on) { g_pdl = on != 0; }
+FN_API void fn_early(int on) { g_early = on != 0; }
+FN_API void fn_moe_var(int v) { g_moe_var = v; }
+FN_API void fn_moe_override(int, int, int, int) {}
+FN_API int fn_gemv_plan(uint32_t, int, int, int *) { FN_FAIL(kNoModel); }
+FN_API void fn_bench_hot(int on) { g_bench_hot = on; }
+FN_API int fn_bench_gemv(uint32_t, int, int, int, int, float *) { FN_FAIL(kNoModel); }
+FN_API int fn_bench_route(int, int, int, const float *, int, int *, float *, float *) { FN_FAIL(kNoModel); }
+FN_API int fn_test_gemv(uint32_t, const uint8_t *, int, int, const float *, int, float *) { FN_FAIL(kNoModel); }
+
+// ---------------------------------------------------------------------------------------------
+// 3. device entry points
+
+FN_API int fn_gdn_block_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int gate_act, int nt, int ring,
+                            const int32_t *pos, const float *qkv, const float *conv_w, float *conv_ring,
+                            const float *ab, const float *dt_bias, const float *ssm_a, float *S, const float *z,
+                            const float *norm_w, float eps, float *out, void *stream) {
+    fn::GdnBlock p{B, nkh, nvh, dk, dv, head_map, gate_act, nt, ring, eps, pos, qkv, conv_w, conv_ring, ab,
+                   dt_bias, ssm_a, S, z, norm_w, out};
+    return fn::gdn_block_launch(p, (hipStream_t) stream);
+}
+
+FN_API int fn_gdn_core_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int nt, const float *q,
+                           const float *k, const float *v, const float *beta, const float *g, float *S, float *o,
+                           void *stream) {
+    fn::GdnCore p{B, nkh, nvh, dk, dv, head_map, nt, q, k, v, beta, g, S, o};
+    return fn::gdn_core_launch(p, (hipStream_t) stream);
+}
+
+FN_API size_t fn_attn_work_bytes(int B, int nq, int nt, int hd, int nsplit) {
+    if (B < 1 || nq < 1 || nt < 1 || hd < 1 || nsplit < 1) return 0;
+    return fn::attn_work_bytes(B, nq, nt, hd, nsplit);
+}
+
+FN_API int fn_attn_nsplit(int B, int nkv, int nt, int ctx) { return fn::attn_pick_nsplit(B, nkv, nt, ctx); }
+
+FN_API int fn_attn_dev(int B, int nq, int nkv, int hd, int nrot, float theta, float eps, int nt, int max_ctx,
+                       const int32_t *pos, const float *qg, const float *k, const float *v, const float *wq,
+                       const float *wk, float *Kc, float *Vc, int nsplit, float *work, size_t work_bytes, float *og,
+                       void *stream) {
+    fn::AttnDecode p{B, nq, nkv, hd, nrot, nt, max_ctx, nsplit, theta, eps, pos, qg, k, v, wq, wk, Kc, Vc, work,
+                     work_bytes, og};
+    return fn::attn_decode_launch(p, (hipStream_t) stream);
+}
+
+FN_API int fn_advance_dev(int32_t *pos, int B, int nt, void *stream) {
+    return fn::advance_launch(pos, B, nt, (hipStream_t) stream);
+}
+
+FN_API int fn_fill_normal_dev(float *p, size_t n, uint64_t seed, float mean, float std, void *stream) {
+    return fn::fill_normal_launch(p, n, seed, mean, std, (hipStream_t) stream);
+}
+
+FN_API int fn_copy_dev(void *dst, const void *src, size_t bytes, void *stream) {
+    return fn::copy_launch(dst, src, bytes, (hipStream_t) stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// 2. host-array hooks
+
+FN_API int fn_test_gdn(int B, int nkh, int nvh, int dk, int dv, int head_map, int nt, const float *q, const float *k,
+                       const float *v, const float *beta, const float *g, float *S, float *o) {
+    if (B < 1 || nkh < 1 || nvh < 1 || nt < 1 || dk < 1 || dv < 1) FN_FAIL("gdn: bad shape");
+    if (!q || !k || !v || !beta || !g || !S || !o) FN_FAIL("gdn: null pointer");
+    if (use_device0()) return -1;
+    const size_t nq = (size_t) B * nt * nkh * dk, nv = (size_t) B * nt * nvh * dv, ns = (size_t) B * nt * nvh;
+    const size_t nS = (size_t) B * nvh * dk * dv;
+    DevBufs m;
+    float *dq, *dk_, *dv_, *db, *dg, *dS, *dO;
+    if (m.up(&dq, q, nq) || m.up(&dk_, k, nq) || m.up(&dv_, v, nv) || m.up(&db, beta, ns) || m.up(&dg, g, ns) ||
+        m.up(&dS, (const float *) S, nS) || m.alloc(&dO, nv))
+        return -1;
+    if (fn_gdn_core_dev(B, nkh, nvh, dk, dv, head_map, nt, dq, dk_, dv_, db, dg, dS, dO, nullptr)) return -1;
+    FN_CK(hipDeviceSynchronize());
+    FN_CK(hipMemcpy(S, dS, nS * 4, hipMemcpyDeviceToHost));
+    FN_CK(hipMemcpy(o, dO, nv * 4, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+FN_API int fn_test_gdn_block(int B, int nkh, int nvh, int dk, int dv, int head_map, int gate_act, int nt,
+                             const float *qkv, const float *conv_w, float *conv_state, const float *ab,
+                             const float *dt_bias, const float *ssm_a, float *S, const float *z, const float *norm_w,
+                             float eps, float *out) {
+    if (B < 1 || nkh < 1 || nvh < 1 || nt < 1 || dk < 1 || dv < 1) FN_FAIL("gdn: bad shape");
+    if (nt > 61) FN_FAIL("gdn: nt must be <= 61 in one call");
+    if (!qkv || !conv_w || !conv_state || !ab || !dt_bias || !ssm_a || !S || !z || !norm_w || !out)
+        FN_FAIL("gdn: null pointer");
+    if (use_device0()) return -1;
+    const size_t C = (size_t) 2 * nkh * dk + (size_t) nvh * dv;
+    int ring = 4;
+    while (ring < nt + 3) ring *= 2;
+    // host conv state [B][3][C] -> ring slots of positions -3, -2, -1 (pos = 0 inside the hook)
+    std::vector<float> rh((size_t) B * ring * C, 0.0f);
+    for (int b = 0; b < B; ++b)
+        for (int j = 0; j < 3; ++j)
+            std::memcpy(&rh[((size_t) b * ring + ((j - 3) & (ring - 1))) * C], conv_state + ((size_t) b * 3 + j) * C,
+                        C * 4);
+    std::vector<int32_t> ph(B, 0);
+    const size_t nx = (size_t) B * nt * C, nab = (size_t) B * nt * 2 * nvh, nz = (size_t) B * nt * nvh * dv;
+    const size_t nS = (size_t) B * nvh * dk * dv;
+    DevBufs m;
+    int32_t *dpos;
+    float *dx, *dw, *dr, *dab, *ddt, *dsa, *dS, *dz, *dnw, *dout;
+    if (m.up(&dpos, ph.data(), B) || m.up(&dx, qkv, nx) || m.up(&dw, conv_w, C * 4) || m.up(&dr, rh.data(), rh.size()) ||
+        m.up(&dab, ab, nab) || m.up(&ddt, dt_bias, nvh) || m.up(&dsa, ssm_a, nvh) || m.up(&dS, (const float *) S, nS) ||
+        m.up(&dz, z, nz) || m.up(&dnw, norm_w, dv) || m.alloc(&dout, nz))
+        return -1;
+    if (fn_gdn_block_dev(B, nkh, nvh, dk, dv, head_map, gate_act, nt, ring, dpos, dx, dw, dr, dab, ddt, dsa, dS, dz,
+                         dnw, eps, dout, nullptr))
+        return -1;
+    FN_CK(hipDeviceSynchronize());
+    FN_CK(hipMemcpy(S, dS, nS * 4, hipMemcpyDeviceToHost));
+    FN_CK(hipMemcpy(out, dout, nz * 4, hipMemcpyDeviceToHost));
+    FN_CK(hipMemcpy(rh.data(), dr, rh.size() * 4, hipMemcpyDeviceToHost));
+    // ring slots of positions nt-3 .. nt-1 -> [B][3][C]
+    for (int b = 0; b < B; ++b)
+        for (int j = 0; j < 3; ++j)
+            std::memcpy(conv_state + ((size_t) b * 3 + j) * C, &rh[((size_t) b * ring + ((nt - 3 + j) & (ring - 1))) * C],
+                        C * 4);
+    return 0;
+}
+
+FN_API int fn_test_attn(int B, int nq, int nkv, int hd, int nrot, float theta, float eps, int nt, int max_ctx,
+                        const int32_t *pos, const float *qg, const float *k, const float *v, const float *wq,
+                        const float *wk, float *Kc, float *Vc, int nsplit, float *og) {
+    if (B < 1 || nq < 1 || nkv < 1 || hd < 1 || nt < 1 || max_ctx < 1) FN_FAIL("attn: bad shape");
+    if (!pos || !qg || !k || !v || !wq || !wk || !Kc || !Vc || !og) FN_FAIL("attn: null pointer");
+    int maxpos = 0;
+    for (int b = 0; b < B; ++b) {
+        if (pos[b] < 0 || pos[b] + nt > max_ctx) FN_FAIL("attn: pos[b] + nt must lie in [0, max_ctx]");
+        maxpos = std::max(maxpos, pos[b]);
+    }
+    if (use_device0()) return -1;
+    const int mc = (max_ctx + 63) / 64 * 64;  // device cache rows, tile multiple
+    if (nsplit <= 0) nsplit = fn::attn_pick_nsplit(B, nkv, nt, maxpos + nt);
+    // reference layout [B][max_ctx][nkv][hd] -> key-tiled K / head-major V, rows < pos[b] only
+    const size_t per = (size_t) nkv * mc * hd;
+    std::vector<float> kh((size_t) B * per, 0.0f), vh((size_t) B * per, 0.0f);
+    for (int b = 0; b < B; ++b)
+        for (int p = 0; p < pos[b]; ++p)
+            for (int g = 0; g < nkv; ++g) {
+                const float *ks = Kc + (((size_t) b * max_ctx + p) * nkv + g) * hd;
+                const float *vs = Vc + (((size_t) b * max_ctx + p) * nkv + g) * hd;
+                float *kt = &kh[(((size_t) b * nkv + g) * (mc / 64) + p / 64) * 64 * hd + (size_t) (p % 64) * 4];
+                for (int c = 0; c < hd / 4; ++c) std::memcpy(kt + (size_t) c * 256, ks + c * 4, 16);
+                std::memcpy(&vh[(((size_t) b * nkv + g) * mc + p) * hd], vs, (size_t) hd * 4);
+            }
+    const size_t nqg = (size_t) B * nt * nq * 2 * hd, nkvn = (size_t) B * nt * nkv * hd, nog = (size_t) B * nt * nq * hd;
+    const size_t wb = fn::attn_work_bytes(B, nq, nt, hd, nsplit);
+    DevBufs m;
+    int32_t *dpos;
+    float *dqg, *dk_, *dv_, *dwq, *dwk, *dK, *dV, *dwork, *dog;
+    if (m.up(&dpos, pos, B) || m.up(&dqg, qg, nqg) || m.up(&dk_, k, nkvn) || m.up(&dv_, v, nkvn) ||
+        m.up(&dwq, wq, hd) || m.up(&dwk, wk, hd) || m.up(&dK, kh.data(), kh.size()) || m.up(&dV, vh.data(), vh.size()) ||
+        m.alloc(&dwork, wb / 4 + 1) || m.alloc(&dog, nog))
+        return -1;
+    if (fn_attn_dev(B, nq, nkv, hd, nrot, theta, eps, nt, mc, dpos, dqg, dk_, dv_, dwq, dwk, dK, dV, nsplit, dwork, wb,
+                    dog, nullptr))
+        return -1;
+    FN_CK(hipDeviceSynchronize());
+    FN_CK(hipMemcpy(og, dog, nog * 4, hipMemcpyDeviceToHost));
+    FN_CK(hipMemcpy(kh.data(), dK, kh.size() * 4, hipMemcpyDeviceToHost));
+    FN_CK(hipMemcpy(vh.data(), dV, vh.size() * 4, hipMemcpyDeviceToHost));
+    // appended rows back into the reference layout
+    for (int b = 0; b < B; ++b)
+        for (int p = pos[b]; p < pos[b] + nt; ++p)
+            for (int g = 0; g < nkv; ++g) {
+                float *kd = Kc + (((size_t) b * max_ctx + p) * nkv + g) * hd;
+                float *vd = Vc + (((size_t) b * max_ctx + p) * nkv + g) * hd;
+                const float *kt = &kh[(((size_t) b * nkv + g) * (mc / 64) + p / 64) * 64 * hd + (size_t) (p % 64) * 4];
+                for (int c = 0; c < hd / 4; ++c) std::memcpy(kd + c * 4, kt + (size_t) c * 256, 16);
+                std::memcpy(vd, &vh[(((size_t) b * nkv + g) * mc + p) * hd], (size_t) hd * 4);
+            }
+    return 0;
+}

@@ -1,0 +1,58 @@
+// Internal launch API of the DeltaNet and attention kernels (device pointers, caller stream).
+#pragma once
+
+#include "common.cuh"
+
+#include <algorithm>
+
+namespace fn {
+
+struct GdnBlock {
+    int B, nkh, nvh, dk, dv, head_map, gate_act, nt, ring;
+    float eps;
+    const int32_t *pos;                 // [B] tokens already seen (conv ring index)
+    const float *qkv;                   // [B][nt][C]
+    const float *conv_w;                // [C][4]
+    float *conv_ring;                   // [B][ring][C]
+    const float *ab;                    // [B][nt][2 nvh]
+    const float *dt_bias, *ssm_a;       // [nvh]
+    float *S;                           // [B][nvh][dk][dv]
+    const float *z;                     // [B][nt][nvh dv]
+    const float *norm_w;                // [dv]
+    float *out;                         // [B][nt][nvh dv]
+};
+
+struct GdnCore {
+    int B, nkh, nvh, dk, dv, head_map, nt;
+    const float *q, *k;                 // [B][nt][nkh][dk]
+    const float *v;                     // [B][nt][nvh][dv]
+    const float *beta, *g;              // [B][nt][nvh]
+    float *S;                           // [B][nvh][dk][dv]
+    float *o;                           // [B][nt][nvh][dv]
+};
+
+int gdn_block_launch(const GdnBlock &p, hipStream_t st);
+int gdn_core_launch(const GdnCore &p, hipStream_t st);
+
+struct AttnDecode {
+    int B, nq, nkv, hd, nrot, nt, max_ctx, nsplit;
+    float theta, eps;
+    const int32_t *pos;                 // [B] tokens already in the cache
+    const float *qg;                    // [B][nt][nq][2][hd] query then gate
+    const float *k, *v;                 // [B][nt][nkv][hd] new rows
+    const float *wq, *wk;               // [hd]
+    float *Kc, *Vc;                     // device cache layouts (see attn.hip)
+    float *work;                        // attn_work_bytes()
+    size_t work_bytes;
+    float *og;                          // [B][nt][nq][hd]
+};
+
+size_t attn_work_bytes(int B, int nq, int nt, int hd, int nsplit);
+int attn_pick_nsplit(int B, int nkv, int nt, int ctx);
+int attn_decode_launch(const AttnDecode &p, hipStream_t st);
+int advance_launch(int32_t *pos, int B, int nt, hipStream_t st);
+
+int fill_normal_launch(float *p, size_t n, uint64_t seed, float mean, float std, hipStream_t st);
+int copy_launch(void *dst, const void *src, size_t bytes, hipStream_t st);
+
+}  // namespace fn

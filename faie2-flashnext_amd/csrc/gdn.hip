@@ -1,0 +1,297 @@
+// Gated-DeltaNet decode for gfx950: the fused block (causal conv1d k=4 + SiLU, q/k L2-norm, gates, delta rule,
+// readout, gated RMSNorm) and the bare state core, one workgroup per (sequence, value head).
+//
+// Semantics follow k_gdn (reference engine/faie2fn.cu:1349-1431).  The kernel is organised for CDNA4, not as a
+// translation of the sm_120 one:
+//   * 256 threads (four wave64s) per head.  Thread (rg = tid / 32, cg = tid % 32) owns the 4 columns 4cg..4cg+3
+//     of the 16 state rows 16rg..16rg+15, i.e. 16 float4 registers.  Every wave load and store of S moves two
+//     contiguous 512-byte rows with 128-bit accesses, and S makes exactly one trip HBM -> VGPRs -> HBM per call.
+//   * One read pass computes both reductions the step needs, kv = S^T k and sq = S^T q (old S), because
+//       S' = g S + k d^T  with  d = beta (v - g kv)    =>    S'^T q = g sq + (k.q) d.
+//     The column partials of the 8 row groups are folded with a lane^32 permute (2 groups per wave) and
+//     one 2 KiB LDS exchange across the four waves; there is no serial 128-long FMA chain.
+//   * q/k are not normalised before the pass: the L2 factors are applied to the 4 per-column sums, so the
+//     norm reductions (wave DPP sums) overlap the S loads instead of sitting in front of them.
+//   * The causal conv state is a ring of R slots per sequence, R a power of two >= nt + 3: the raw input of
+//     position p lives in slot p & (R - 1).  A call reads the slots of positions pos-3..pos-1 and writes only the
+//     slots of its own last (up to) three positions, so value heads sharing a key head read their q/k taps with
+//     no race and no per-head copies (the reference keeps one copy per value head, faie2fn.cu:1353, 1378-1382).
+//     Taps inside the call's own tokens come straight from the qkv input.
+#include "gdn.h"
+
+#include <algorithm>
+
+namespace fn {
+
+namespace {
+
+constexpr int DK = 128, DV = 128;
+constexpr int THREADS = 256;
+constexpr int ROWS_PT = 16;  // state rows per thread
+
+struct GdnArgs {
+    int B, nkh, nvh, nt, ring, head_map, gate_act;
+    float eps;
+    const int32_t *pos;
+    const float *qkv, *conv_w;
+    float *ring_buf;
+    const float *ab, *dt_bias, *ssm_a;
+    float *S;
+    const float *z, *norm_w;
+    float *out;
+    const float *q, *k, *v, *beta, *g;  // core variant inputs
+};
+
+__device__ __forceinline__ float conv_tap(const GdnArgs &a, int b, int t, int C, int c, int j, int P) {
+    // raw input of channel c at position P - j (1 <= j <= 3) for token t of this call
+    if (t - j >= 0) return a.qkv[((size_t) b * a.nt + (t - j)) * C + c];
+    return a.ring_buf[((size_t) b * a.ring + ((P - j) & (a.ring - 1))) * C + c];
+}
+
+// causal depthwise conv (kernel 4, weights oldest tap first) + SiLU (faie2fn.cu:1392-1395)
+__device__ __forceinline__ float conv_silu(const GdnArgs &a, int b, int t, int C, int c, int P) {
+    const float4 w = reinterpret_cast<const float4 *>(a.conv_w)[c];
+    const float x0 = a.qkv[((size_t) b * a.nt + t) * C + c];
+    const float x1 = conv_tap(a, b, t, C, c, 1, P);
+    const float x2 = conv_tap(a, b, t, C, c, 2, P);
+    const float x3 = conv_tap(a, b, t, C, c, 3, P);
+    float acc = w.x * x3;
+    acc = fmaf(w.y, x2, acc);
+    acc = fmaf(w.z, x1, acc);
+    acc = fmaf(w.w, x0, acc);
+    return siluf_(acc);
+}
+
+template <bool FUSED> __global__ void __launch_bounds__(THREADS) k_gdn(const GdnArgs a) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int cg = tid & 31, rg = tid >> 5;
+    const int bh = blockIdx.x, b = bh / a.nvh, h = bh - b * a.nvh;
+    const int kh = a.head_map == 0 ? h % a.nkh : h / (a.nvh / a.nkh);
+    const int C = 2 * a.nkh * DK + a.nvh * DV;
+
+    __shared__ float4 qs4[DK / 4], ks4[DK / 4];  // raw q, k of the key head (this token)
+    __shared__ float vs[DV];                      // conv'd v of the value head
+    __shared__ float4 red[4][2][DV / 4];          // per-wave column partials of kv and sq
+    __shared__ float nrm[2][3];                   // per-wave sums q.q, k.k, q.k (waves 0, 1)
+
+    // 1. state tile into registers: issued first, everything below overlaps its latency
+    float4 s[ROWS_PT];
+    float4 *Sh = reinterpret_cast<float4 *>(a.S + (size_t) bh * DK * DV);
+#pragma unroll
+    for (int r = 0; r < ROWS_PT; ++r) s[r] = Sh[(rg * ROWS_PT + r) * (DV / 4) + cg];
+
+    const int pos = FUSED ? a.pos[b] : 0;
+    const float scale = 0.08838834764831845f;  // 1/sqrt(128), faie2fn.cu:1352
+
+    for (int t = 0; t < a.nt; ++t) {
+        const size_t bt = (size_t) b * a.nt + t;
+        if (t > 0) __syncthreads();  // the previous token's LDS reads are done
+
+        // 2. q, k (waves 0-1, channel i = tid) and v (waves 2-3, channel j = tid - 128)
+        if (tid < DK) {
+            float q, k;
+            if (FUSED) {
+                const int P = pos + t;
+                q = conv_silu(a, b, t, C, kh * DK + tid, P);
+                k = conv_silu(a, b, t, C, a.nkh * DK + kh * DK + tid, P);
+            } else {
+                q = a.q[(bt * a.nkh + kh) * DK + tid];
+                k = a.k[(bt * a.nkh + kh) * DK + tid];
+            }
+            reinterpret_cast<float *>(qs4)[tid] = q;
+            reinterpret_cast<float *>(ks4)[tid] = k;
+            const float sqq = wave_sum(q * q), skk = wave_sum(k * k), sqk = wave_sum(q * k);
+            if (lane == 0) {
+                nrm[wave][0] = sqq;
+                nrm[wave][1] = skk;
+                nrm[wave][2] = sqk;
+            }
+        } else {
+            const int j = tid - DK;
+            float vv;
+            if (FUSED) vv = conv_silu(a, b, t, C, 2 * a.nkh * DK + h * DV + j, pos + t);
+            else vv = a.v[(bt * a.nvh + h) * DV + j];
+            vs[j] = vv;
+        }
+
+        // 3. gates (uniform per head): beta = sigmoid(b), gamma = exp(ssm_a * softplus(a + dt_bias)), softplus
+        //    the identity above 20 (faie2fn.cu:1407-1410)
+        float beta, gamma;
+        if (FUSED) {
+            const float *abt = a.ab + bt * 2 * a.nvh;
+            beta = sigmoidf_(abt[a.nvh + h]);
+            const float x = abt[h] + a.dt_bias[h];
+            const float sp = x > 20.0f ? x : log1pf(expf(x));
+            gamma = expf(sp * a.ssm_a[h]);
+        } else {
+            beta = a.beta[bt * a.nvh + h];
+            gamma = expf(a.g[bt * a.nvh + h]);
+        }
+        __syncthreads();
+
+        // L2 factors x * rsqrt(sum x^2 + 1e-6) (faie2fn.cu:1399-1402); the core takes q, k as given
+        float rq = 1.0f, rk = 1.0f;
+        const float sqk = nrm[0][2] + nrm[1][2];
+        if (FUSED) {
+            rq = rsqrtf(nrm[0][0] + nrm[1][0] + 1e-6f);
+            rk = rsqrtf(nrm[0][1] + nrm[1][1] + 1e-6f);
+        }
+        const float kq = sqk * rq * rk;
+
+        // 4. one pass over the registers: column partials of S^T k and S^T q over this thread's 16 rows
+        float4 kvp = f4(0.0f), sqp = f4(0.0f);
+#pragma unroll
+        for (int r4 = 0; r4 < ROWS_PT / 4; ++r4) {
+            const float4 kk = ks4[rg * (ROWS_PT / 4) + r4];
+            const float4 qq = qs4[rg * (ROWS_PT / 4) + r4];
+            const float kr[4] = {kk.x, kk.y, kk.z, kk.w}, qr[4] = {qq.x, qq.y, qq.z, qq.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float4 sv = s[r4 * 4 + u];
+                kvp.x = fmaf(sv.x, kr[u], kvp.x);
+                kvp.y = fmaf(sv.y, kr[u], kvp.y);
+                kvp.z = fmaf(sv.z, kr[u], kvp.z);
+                kvp.w = fmaf(sv.w, kr[u], kvp.w);
+                sqp.x = fmaf(sv.x, qr[u], sqp.x);
+                sqp.y = fmaf(sv.y, qr[u], sqp.y);
+                sqp.z = fmaf(sv.z, qr[u], sqp.z);
+                sqp.w = fmaf(sv.w, qr[u], sqp.w);
+            }
+        }
+        // fold row groups 2w and 2w+1 (lanes l and l^32), then across waves through LDS
+        kvp.x += shfl_xor32(kvp.x); kvp.y += shfl_xor32(kvp.y); kvp.z += shfl_xor32(kvp.z); kvp.w += shfl_xor32(kvp.w);
+        sqp.x += shfl_xor32(sqp.x); sqp.y += shfl_xor32(sqp.y); sqp.z += shfl_xor32(sqp.z); sqp.w += shfl_xor32(sqp.w);
+        if (lane < 32) {
+            red[wave][0][cg] = kvp;
+            red[wave][1][cg] = sqp;
+        }
+        __syncthreads();
+        float4 kv = red[0][0][cg], sq = red[0][1][cg];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            const float4 x = red[w][0][cg], y = red[w][1][cg];
+            kv.x += x.x; kv.y += x.y; kv.z += x.z; kv.w += x.w;
+            sq.x += y.x; sq.y += y.y; sq.z += y.z; sq.w += y.w;
+        }
+
+        // 5. delta, readout, update.  kv and sq were taken over raw k and q: scale by rk and rq here.
+        const float4 v4 = reinterpret_cast<const float4 *>(vs)[cg];
+        float4 d, o;
+        d.x = (v4.x - gamma * (kv.x * rk)) * beta;
+        d.y = (v4.y - gamma * (kv.y * rk)) * beta;
+        d.z = (v4.z - gamma * (kv.z * rk)) * beta;
+        d.w = (v4.w - gamma * (kv.w * rk)) * beta;
+        o.x = fmaf(gamma, sq.x * rq, kq * d.x) * scale;
+        o.y = fmaf(gamma, sq.y * rq, kq * d.y) * scale;
+        o.z = fmaf(gamma, sq.z * rq, kq * d.z) * scale;
+        o.w = fmaf(gamma, sq.w * rq, kq * d.w) * scale;
+        const float4 dk4 = make_float4(d.x * rk, d.y * rk, d.z * rk, d.w * rk);  // k enters raw below
+#pragma unroll
+        for (int r4 = 0; r4 < ROWS_PT / 4; ++r4) {
+            const float4 kk = ks4[rg * (ROWS_PT / 4) + r4];
+            const float kr[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                float4 &sv = s[r4 * 4 + u];
+                sv.x = fmaf(kr[u], dk4.x, gamma * sv.x);
+                sv.y = fmaf(kr[u], dk4.y, gamma * sv.y);
+                sv.z = fmaf(kr[u], dk4.z, gamma * sv.z);
+                sv.w = fmaf(kr[u], dk4.w, gamma * sv.w);
+            }
+        }
+
+        // 6. output: wave 0 holds every column twice (row groups 0 and 1)
+        if (wave == 0) {
+            if (FUSED) {
+                // gated RMSNorm on = o * rsqrt(mean o^2 + eps) * w * act(z) (faie2fn.cu:1422-1424); the wave sum
+                // counts each column twice, exactly, so halve it
+                const float ss = 0.5f * wave_sum(o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w);
+                const float rn = rsqrtf(ss / DV + a.eps);
+                if (lane < 32) {
+                    const size_t oi = bt * a.nvh * DV + (size_t) h * DV + cg * 4;
+                    const float4 z4 = *reinterpret_cast<const float4 *>(a.z + oi);
+                    const float4 w4 = reinterpret_cast<const float4 *>(a.norm_w)[cg];
+                    float4 r;
+                    if (a.gate_act == 0) {
+                        r.x = o.x * rn * w4.x * sigmoidf_(z4.x);
+                        r.y = o.y * rn * w4.y * sigmoidf_(z4.y);
+                        r.z = o.z * rn * w4.z * sigmoidf_(z4.z);
+                        r.w = o.w * rn * w4.w * sigmoidf_(z4.w);
+                    } else {
+                        r.x = o.x * rn * w4.x * siluf_(z4.x);
+                        r.y = o.y * rn * w4.y * siluf_(z4.y);
+                        r.z = o.z * rn * w4.z * siluf_(z4.z);
+                        r.w = o.w * rn * w4.w * siluf_(z4.w);
+                    }
+                    *reinterpret_cast<float4 *>(a.out + oi) = r;
+                }
+            } else if (lane < 32) {
+                *reinterpret_cast<float4 *>(a.out + (bt * a.nvh + h) * DV + cg * 4) = o;
+            }
+        }
+    }
+
+    // 7. write back: state once, conv ring slots of this call's last (up to) three positions
+#pragma unroll
+    for (int r = 0; r < ROWS_PT; ++r) Sh[(rg * ROWS_PT + r) * (DV / 4) + cg] = s[r];
+    if (FUSED) {
+        const bool primary = a.head_map == 0 ? h < a.nkh : (h % (a.nvh / a.nkh)) == 0;
+        for (int t = max(0, a.nt - 3); t < a.nt; ++t) {
+            const int slot = (pos + t) & (a.ring - 1);
+            const float *x = a.qkv + ((size_t) b * a.nt + t) * C;
+            float *dst = a.ring_buf + ((size_t) b * a.ring + slot) * C;
+            if (tid < DK) {
+                if (primary) {
+                    const int cq = kh * DK + tid, ck = a.nkh * DK + kh * DK + tid;
+                    dst[cq] = x[cq];
+                    dst[ck] = x[ck];
+                }
+            } else {
+                const int cv = 2 * a.nkh * DK + h * DV + (tid - DK);
+                dst[cv] = x[cv];
+            }
+        }
+    }
+}
+
+int check_dims(int B, int nkh, int nvh, int dk, int dv, int head_map, int nt) {
+    if (B < 1 || nkh < 1 || nvh < 1 || nt < 1) FN_FAIL("gdn: B, nkh, nvh and nt must be >= 1");
+    if (dk != DK || dv != DV) FN_FAIL("gdn: only dk = dv = 128 is built");
+    if (nvh % nkh) FN_FAIL("gdn: nvh must be a multiple of nkh");
+    if (head_map != 0 && head_map != 1) FN_FAIL("gdn: head_map must be 0 (tiled h % nkh) or 1 (grouped)");
+    if ((size_t) B * nvh > 0x7fffffffu) FN_FAIL("gdn: too many heads");
+    return 0;
+}
+
+}  // namespace
+
+int gdn_block_launch(const GdnBlock &p, hipStream_t st) {
+    if (check_dims(p.B, p.nkh, p.nvh, p.dk, p.dv, p.head_map, p.nt)) return -1;
+    if (p.gate_act != 0 && p.gate_act != 1) FN_FAIL("gdn: gate_act must be 0 (sigmoid) or 1 (silu)");
+    if (p.ring < 4 || (p.ring & (p.ring - 1))) FN_FAIL("gdn: ring must be a power of two >= 4");
+    if (p.nt > p.ring - 3) FN_FAIL("gdn: nt must be <= ring - 3");
+    if (!p.pos || !p.qkv || !p.conv_w || !p.conv_ring || !p.ab || !p.dt_bias || !p.ssm_a || !p.S || !p.z ||
+        !p.norm_w || !p.out)
+        FN_FAIL("gdn: null pointer");
+    GdnArgs a{};
+    a.B = p.B; a.nkh = p.nkh; a.nvh = p.nvh; a.nt = p.nt; a.ring = p.ring; a.head_map = p.head_map;
+    a.gate_act = p.gate_act; a.eps = p.eps; a.pos = p.pos; a.qkv = p.qkv; a.conv_w = p.conv_w;
+    a.ring_buf = p.conv_ring; a.ab = p.ab; a.dt_bias = p.dt_bias; a.ssm_a = p.ssm_a; a.S = p.S; a.z = p.z;
+    a.norm_w = p.norm_w; a.out = p.out;
+    hipLaunchKernelGGL(k_gdn<true>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+int gdn_core_launch(const GdnCore &p, hipStream_t st) {
+    if (check_dims(p.B, p.nkh, p.nvh, p.dk, p.dv, p.head_map, p.nt)) return -1;
+    if (!p.q || !p.k || !p.v || !p.beta || !p.g || !p.S || !p.o) FN_FAIL("gdn: null pointer");
+    GdnArgs a{};
+    a.B = p.B; a.nkh = p.nkh; a.nvh = p.nvh; a.nt = p.nt; a.ring = 4; a.head_map = p.head_map;
+    a.q = p.q; a.k = p.k; a.v = p.v; a.beta = p.beta; a.g = p.g; a.S = p.S; a.out = p.o;
+    hipLaunchKernelGGL(k_gdn<false>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+}  // namespace fn

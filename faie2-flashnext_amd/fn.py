@@ -1,0 +1,177 @@
+"""ctypes host layer for libfaie2fn.so, the MI355X decode-attention engine of FAIE2-FlashNext.
+
+Linux counterpart of the reference's ``flashnext/fn.py`` (class ``FN``, flashnext/fn.py:21-66): the same
+argtypes for the reference's entry points, the same ``check()`` that turns a -1 into ``RuntimeError(fn_error())``,
+plus the path hooks of this library (``gdn``, ``gdn_block``, ``attn``) and thin wrappers of its device-buffer
+entry points.  The library path comes from the ``lib`` argument, else ``$FN_DLL``, else the ``libfaie2fn.so``
+built next to this file.  There is no fallback: if the library is missing the constructor raises.
+"""
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "libfaie2fn.so")
+VOCAB = 248320
+HCD = 10240
+NL = 48
+
+P = np.ctypeslib.ndpointer
+F32 = P(np.float32, flags="C_CONTIGUOUS")
+I32 = P(np.int32, flags="C_CONTIGUOUS")
+U8 = P(np.uint8, flags="C_CONTIGUOUS")
+VP = C.c_void_p
+
+# every symbol include/faie2fn.h declares
+SYMBOLS = (
+    "fn_error", "fn_free", "fn_load", "fn_split", "fn_dev_gb", "fn_n_past", "fn_last_ms", "fn_reset",
+    "fn_use_graphs", "fn_forward", "fn_debug_layers", "fn_test_dequant", "fn_gemv_override", "fn_gemv_waves",
+    "fn_pdl", "fn_early", "fn_moe_var", "fn_moe_override", "fn_gemv_plan", "fn_bench_hot", "fn_bench_gemv",
+    "fn_bench_route", "fn_test_gemv",
+    "fn_test_gdn", "fn_test_gdn_block", "fn_test_attn",
+    "fn_gdn_block_dev", "fn_gdn_core_dev", "fn_attn_dev", "fn_attn_work_bytes", "fn_attn_nsplit", "fn_advance_dev",
+    "fn_fill_normal_dev", "fn_copy_dev",
+)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class FN:
+    def __init__(self, lib=None):
+        path = lib or os.environ.get("FN_DLL") or LIB
+        if not os.path.exists(path):
+            raise RuntimeError(f"libfaie2fn.so not found at {path}: build it first (__graft_entry__.build())")
+        d = self.d = C.CDLL(path)
+        # the reference's bindings (flashnext/fn.py:26-34)
+        d.fn_error.restype = C.c_char_p
+        d.fn_load.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.c_int]
+        d.fn_forward.argtypes = [I32, C.c_int, C.c_void_p, C.c_void_p]
+        d.fn_debug_layers.argtypes = [C.c_void_p]
+        d.fn_test_dequant.argtypes = [C.c_uint32, U8, C.c_int, C.c_int, F32]
+        d.fn_test_gemv.argtypes = [C.c_uint32, U8, C.c_int, C.c_int, F32, C.c_int, F32]
+        d.fn_dev_gb.restype = C.c_double
+        d.fn_dev_gb.argtypes = [C.c_int]
+        d.fn_last_ms.restype = C.c_double
+        # path hooks
+        i = C.c_int
+        d.fn_test_gdn.argtypes = [i] * 7 + [F32] * 7
+        d.fn_test_gdn_block.argtypes = [i] * 8 + [F32] * 9 + [C.c_float, F32]
+        d.fn_test_attn.argtypes = ([i] * 5 + [C.c_float, C.c_float, i, i, I32] + [F32] * 7 + [i, F32])
+        d.fn_gdn_block_dev.argtypes = [i] * 9 + [VP] * 10 + [C.c_float, VP, VP]
+        d.fn_gdn_core_dev.argtypes = [i] * 7 + [VP] * 7 + [VP]
+        d.fn_attn_dev.argtypes = ([i] * 5 + [C.c_float, C.c_float, i, i] + [VP] * 8 + [i, VP, C.c_size_t, VP, VP])
+        d.fn_attn_work_bytes.restype = C.c_size_t
+        d.fn_attn_work_bytes.argtypes = [i] * 5
+        d.fn_attn_nsplit.argtypes = [i] * 4
+        d.fn_advance_dev.argtypes = [VP, i, i, VP]
+        d.fn_fill_normal_dev.argtypes = [VP, C.c_size_t, C.c_uint64, C.c_float, C.c_float, VP]
+        d.fn_copy_dev.argtypes = [VP, VP, C.c_size_t, VP]
+
+    def check(self, rc):
+        if rc != 0:
+            raise RuntimeError(self.d.fn_error().decode())
+
+    # ---- the reference's methods (flashnext/fn.py:40-66) ----
+    def load(self, shard1, shard2, max_ctx=32768, split=0):
+        self.check(self.d.fn_load(shard1.encode(), shard2.encode(), max_ctx, split))
+
+    def reset(self):
+        self.check(self.d.fn_reset())
+
+    def forward(self, tokens, logits=False):
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        am = np.zeros(len(t), np.int32)
+        lg = np.zeros((len(t), VOCAB), np.float32) if logits else None
+        self.check(self.d.fn_forward(t, len(t), lg.ctypes.data if logits else None, am.ctypes.data))
+        return (am, lg) if logits else am
+
+    def debug_layers(self, buf):
+        self.check(self.d.fn_debug_layers(buf.ctypes.data if buf is not None else None))
+
+    def dequant(self, qtype, raw, rows, cols):
+        out = np.zeros((rows, cols), np.float32)
+        self.check(self.d.fn_test_dequant(int(qtype), np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1), rows, cols,
+                                          out))
+        return out
+
+    def gemv(self, qtype, raw, rows, cols, x):
+        nt = x.shape[0]
+        y = np.zeros((nt, rows), np.float32)
+        self.check(self.d.fn_test_gemv(int(qtype), np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1), rows, cols,
+                                       _f32(x), nt, y))
+        return y
+
+    # ---- path hooks (host arrays, synchronous) ----
+    def gdn(self, q, k, v, beta, g, S, head_map=0):
+        """DeltaNet core.  q,k [B,nt,nkh,dk]; v [B,nt,nvh,dv]; beta, g [B,nt,nvh]; S [B,nvh,dk,dv] float32,
+        updated in place.  Returns o [B,nt,nvh,dv]."""
+        B, nt, nkh, dk = q.shape
+        nvh, dv = v.shape[2], v.shape[3]
+        if S.dtype != np.float32 or not S.flags.c_contiguous or S.shape != (B, nvh, dk, dv):
+            raise ValueError("S must be a C-contiguous float32 [B, nvh, dk, dv] array")
+        o = np.zeros((B, nt, nvh, dv), np.float32)
+        self.check(self.d.fn_test_gdn(B, nkh, nvh, dk, dv, head_map, nt, _f32(q), _f32(k), _f32(v), _f32(beta),
+                                      _f32(g), S, o))
+        return o
+
+    def gdn_block(self, qkv, conv_w, conv_state, ab, dt_bias, ssm_a, S, z, norm_w, nkh, nvh, dk=128, dv=128,
+                  head_map=0, gate_act=0, eps=1e-6):
+        """Fused DeltaNet block.  conv_state [B,3,C] and S [B,nvh,dk,dv] float32 are updated in place.
+        Returns out [B,nt,nvh*dv]."""
+        B, nt, Cc = qkv.shape
+        for name, arr, shape in (("conv_state", conv_state, (B, 3, Cc)), ("S", S, (B, nvh, dk, dv))):
+            if arr.dtype != np.float32 or not arr.flags.c_contiguous or arr.shape != shape:
+                raise ValueError(f"{name} must be a C-contiguous float32 {shape} array")
+        out = np.zeros((B, nt, nvh * dv), np.float32)
+        self.check(self.d.fn_test_gdn_block(B, nkh, nvh, dk, dv, head_map, gate_act, nt, _f32(qkv), _f32(conv_w),
+                                            conv_state, _f32(ab), _f32(dt_bias), _f32(ssm_a), S, _f32(z),
+                                            _f32(norm_w), float(eps), out))
+        return out
+
+    def attn(self, qg, k, v, wq, wk, Kc, Vc, pos, nrot=64, theta=1e7, eps=1e-6, nsplit=0):
+        """GQA decode.  qg [B,nt,nq,2,hd]; k, v [B,nt,nkv,hd]; Kc, Vc [B,max_ctx,nkv,hd] float32 (rows
+        pos[b]..pos[b]+nt-1 are written in place); pos [B].  Returns og [B,nt,nq,hd]."""
+        B, nt, nq, two, hd = qg.shape
+        nkv = k.shape[2]
+        max_ctx = Kc.shape[1]
+        for name, arr in (("Kc", Kc), ("Vc", Vc)):
+            if arr.dtype != np.float32 or not arr.flags.c_contiguous or arr.shape != (B, max_ctx, nkv, hd):
+                raise ValueError(f"{name} must be a C-contiguous float32 [B, max_ctx, nkv, hd] array")
+        og = np.zeros((B, nt, nq, hd), np.float32)
+        self.check(self.d.fn_test_attn(B, nq, nkv, hd, nrot, float(theta), float(eps), nt, max_ctx,
+                                       np.ascontiguousarray(pos, dtype=np.int32), _f32(qg), _f32(k), _f32(v), _f32(wq),
+                                       _f32(wk), Kc, Vc, int(nsplit), og))
+        return og
+
+    # ---- device entry points (integers are device addresses; stream is a HIP stream handle or 0) ----
+    def gdn_block_dev(self, B, nkh, nvh, nt, ring, pos, qkv, conv_w, conv_ring, ab, dt_bias, ssm_a, S, z, norm_w,
+                      out, stream=0, dk=128, dv=128, head_map=0, gate_act=0, eps=1e-6):
+        self.check(self.d.fn_gdn_block_dev(B, nkh, nvh, dk, dv, head_map, gate_act, nt, ring, pos, qkv, conv_w,
+                                           conv_ring, ab, dt_bias, ssm_a, S, z, norm_w, float(eps), out, stream))
+
+    def gdn_core_dev(self, B, nkh, nvh, nt, q, k, v, beta, g, S, o, stream=0, dk=128, dv=128, head_map=0):
+        self.check(self.d.fn_gdn_core_dev(B, nkh, nvh, dk, dv, head_map, nt, q, k, v, beta, g, S, o, stream))
+
+    def attn_work_bytes(self, B, nq, nt, nsplit, hd=256):
+        return int(self.d.fn_attn_work_bytes(B, nq, nt, hd, nsplit))
+
+    def attn_nsplit(self, B, nkv, nt, ctx):
+        return int(self.d.fn_attn_nsplit(B, nkv, nt, ctx))
+
+    def attn_dev(self, B, nq, nkv, nt, max_ctx, pos, qg, k, v, wq, wk, Kc, Vc, nsplit, work, work_bytes, og,
+                 stream=0, hd=256, nrot=64, theta=1e7, eps=1e-6):
+        self.check(self.d.fn_attn_dev(B, nq, nkv, hd, nrot, float(theta), float(eps), nt, max_ctx, pos, qg, k, v, wq,
+                                      wk, Kc, Vc, nsplit, work, work_bytes, og, stream))
+
+    def advance_dev(self, pos, B, nt, stream=0):
+        self.check(self.d.fn_advance_dev(pos, B, nt, stream))
+
+    def fill_normal_dev(self, ptr, n, seed, mean=0.0, std=1.0, stream=0):
+        self.check(self.d.fn_fill_normal_dev(ptr, n, seed, float(mean), float(std), stream))
+
+    def copy_dev(self, dst, src, nbytes, stream=0):
+        self.check(self.d.fn_copy_dev(dst, src, nbytes, stream))

@@ -1,0 +1,135 @@
+/*
+ * faie2fn.h -- C ABI of libfaie2fn.so, the MI355X (gfx950) decode-attention engine of FAIE2-FlashNext.
+ *
+ * Conventions (the reference's, engine/faie2fn.cu:111-118, 2492-2935; flashnext/fn.py:21-38):
+ *   - int entry points return 0 on success and -1 on error; the message is then read with fn_error().  The
+ *     pointer fn_error() returns stays valid until the next failing call.
+ *   - Calls are synchronous unless their name ends in _dev, and not re-entrant: one caller thread, process-global
+ *     state.  A _dev entry point only enqueues work on the HIP stream it is given (NULL = the null stream) and
+ *     returns; its pointers are device memory the caller owns.
+ *   - Host-array hooks (fn_test_*) take caller-owned, C-contiguous float32/int32 host arrays and copy them to and
+ *     from device 0 inside the call, as the reference's unit-test hooks do (faie2fn.cu:2745-2782).
+ *   - No torch type appears anywhere: plain pointers, sizes and a void* HIP stream.
+ */
+#ifndef FAIE2FN_H
+#define FAIE2FN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ======================================================================================================
+ * 1. The reference's C API, same names and C signatures (engine/faie2fn.cu, flashnext/fn.py:26-34), so that
+ *    flashnext/fn.py's argtypes bind unchanged.  This library carries the decode-attention path only: the
+ *    model-level entries (GGUF load, forward, GEMV, MoE, routing) return -1 with an fn_error() message that
+ *    says so, and the getters return -1 like the reference's do when no model is loaded.
+ * ====================================================================================================== */
+const char *fn_error(void);                                                   /* faie2fn.cu:2495 */
+void fn_free(void);                                                           /* faie2fn.cu:2497 */
+int fn_load(const char *shard1, const char *shard2, int max_ctx, int split);  /* faie2fn.cu:2524 */
+int fn_split(void);                                                           /* faie2fn.cu:2698 */
+double fn_dev_gb(int dv);                                                     /* faie2fn.cu:2699 */
+int fn_n_past(void);                                                          /* faie2fn.cu:2700 */
+double fn_last_ms(void);                                                      /* faie2fn.cu:2701 */
+int fn_reset(void);                                                           /* faie2fn.cu:2703 */
+int fn_use_graphs(int on);                                                    /* faie2fn.cu:2721 */
+int fn_forward(const int32_t *tokens, int nt, float *logits, int32_t *argmax);  /* faie2fn.cu:2733 */
+int fn_debug_layers(float *out);                                              /* faie2fn.cu:2739 */
+int fn_test_dequant(uint32_t type, const uint8_t *W, int rows, int cols, float *out);  /* faie2fn.cu:2751 */
+void fn_gemv_override(int wpt, int ks, int tb, int warps_per_sm);             /* faie2fn.cu:2786 */
+void fn_gemv_waves(int waves);                                                /* faie2fn.cu:2793 */
+void fn_pdl(int on);                                                          /* faie2fn.cu:2796 */
+void fn_early(int on);                                                        /* faie2fn.cu:2798 */
+void fn_moe_var(int v);                                                       /* faie2fn.cu:2799 */
+void fn_moe_override(int gu_wpt, int gu_tb, int dn_wpt, int dn_tb);           /* faie2fn.cu:2801 */
+int fn_gemv_plan(uint32_t type, int rows, int cols, int *out);                /* faie2fn.cu:2809 */
+void fn_bench_hot(int on);                                                    /* faie2fn.cu:2822 */
+int fn_bench_gemv(uint32_t type, int rows, int cols, int nt, int iters, float *ms);  /* faie2fn.cu:2823 */
+int fn_bench_route(int variant, int nt, int ks, const float *part, int iters, int *sel, float *wsel,
+                   float *ms);                                                /* faie2fn.cu:2875 */
+int fn_test_gemv(uint32_t type, const uint8_t *W, int rows, int cols, const float *x, int nt,
+                 float *y);                                                   /* faie2fn.cu:2916 */
+
+/* ======================================================================================================
+ * 2. Path hooks, host arrays (new; the reference reaches this path only through fn_forward, faie2fn.cu:2733,
+ *    and its model-free hooks follow the style of faie2fn.cu:2745).  Shapes: B sequences, nt tokens each.
+ *    head_map: 0 = tiled (value head h reads key head h % nkh, faie2fn.cu:1374), 1 = grouped (h / (nvh/nkh)).
+ *    gate_act: 0 = sigmoid (faie2fn.cu:1424), 1 = silu.  dk = dv = 128 and hd = 256 are the built sizes.
+ * ====================================================================================================== */
+
+/* DeltaNet state core, the delta rule of k_gdn (faie2fn.cu:1407-1421) on given normalised q, k:
+ *   q, k [B][nt][nkh][dk]; v [B][nt][nvh][dv]; beta, g [B][nt][nvh] (g = log decay, gamma = exp(g));
+ *   S [B][nvh][dk][dv] in/out (row = key index); o [B][nt][nvh][dv] out, o = S'^T q / sqrt(dk). */
+int fn_test_gdn(int B, int nkh, int nvh, int dk, int dv, int head_map, int nt, const float *q, const float *k,
+                const float *v, const float *beta, const float *g, float *S, float *o);
+
+/* Fused DeltaNet block, k_gdn (faie2fn.cu:1366-1431): conv1d k=4 + SiLU, q/k L2-norm, gates, delta rule,
+ * gated RMSNorm.  C = 2 nkh dk + nvh dv.
+ *   qkv [B][nt][C] (channels [q | k | v], faie2fn.cu:1377); conv_w [C][4] oldest tap first;
+ *   conv_state [B][3][C] in/out, raw inputs of the three previous tokens, oldest first;
+ *   ab [B][nt][2 nvh] alpha rows then beta rows (faie2fn.cu:1407-1408); dt_bias, ssm_a [nvh] (ssm_a = -exp(A_log));
+ *   S [B][nvh][dk][dv] in/out; z [B][nt][nvh dv]; norm_w [dv]; out [B][nt][nvh dv]. */
+int fn_test_gdn_block(int B, int nkh, int nvh, int dk, int dv, int head_map, int gate_act, int nt,
+                      const float *qkv, const float *conv_w, float *conv_state, const float *ab,
+                      const float *dt_bias, const float *ssm_a, float *S, const float *z, const float *norm_w,
+                      float eps, float *out);
+
+/* GQA decode, k_qk_norm_rope + k_attn_split (dense) + k_attn_combine (faie2fn.cu:1451-1478, 1612-1690).
+ *   pos [B]: tokens already in each sequence's cache; token t of sequence b sits at pos[b] + t.
+ *   qg [B][nt][nq][2][hd] query then gate per head (faie2fn.cu:50, 1463, 1686); k, v [B][nt][nkv][hd] new rows;
+ *   wq, wk [hd] RMSNorm weights (stored as the effective multiplier); Kc, Vc [B][max_ctx][nkv][hd] in/out in the
+ *   reference layout (faie2fn.cu:1461, 1477): rows < pos[b] are read, rows pos[b]..pos[b]+nt-1 are written;
+ *   nsplit: KV splits per (sequence, token, kv head), 0 = automatic; og [B][nt][nq][hd] out. */
+int fn_test_attn(int B, int nq, int nkv, int hd, int nrot, float theta, float eps, int nt, int max_ctx,
+                 const int32_t *pos, const float *qg, const float *k, const float *v, const float *wq,
+                 const float *wk, float *Kc, float *Vc, int nsplit, float *og);
+
+/* ======================================================================================================
+ * 3. Path entry points on device memory (new): what an engine's layer loop calls, asynchronously on its stream.
+ *    They are the same kernels as section 2 without copies or allocation.
+ * ====================================================================================================== */
+
+/* Fused DeltaNet block on device buffers.  Differences from fn_test_gdn_block:
+ *   pos [B] device int32: tokens already seen per sequence (advanced by the caller, e.g. fn_advance_dev);
+ *   conv_ring [B][ring][C] device: the raw input of position p sits in slot p & (ring - 1); ring is a power of
+ *   two >= 4 and nt <= ring - 3 (ring = 4 serves one-token decode). */
+int fn_gdn_block_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int gate_act, int nt, int ring,
+                     const int32_t *pos, const float *qkv, const float *conv_w, float *conv_ring, const float *ab,
+                     const float *dt_bias, const float *ssm_a, float *S, const float *z, const float *norm_w,
+                     float eps, float *out, void *stream);
+
+/* DeltaNet core on device buffers (layouts of fn_test_gdn). */
+int fn_gdn_core_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int nt, const float *q, const float *k,
+                    const float *v, const float *beta, const float *g, float *S, float *o, void *stream);
+
+/* GQA decode on device buffers.  Device cache layouts (max_ctx a multiple of 64):
+ *   Kc [B][nkv][max_ctx/64][hd/4][64][4] (key-tiled), Vc [B][nkv][max_ctx][hd];
+ *   pos [B] device int32 (not advanced here); work: fn_attn_work_bytes() bytes of device scratch. */
+int fn_attn_dev(int B, int nq, int nkv, int hd, int nrot, float theta, float eps, int nt, int max_ctx,
+                const int32_t *pos, const float *qg, const float *k, const float *v, const float *wq, const float *wk,
+                float *Kc, float *Vc, int nsplit, float *work, size_t work_bytes, float *og, void *stream);
+
+/* Scratch bytes fn_attn_dev needs for these shapes. */
+size_t fn_attn_work_bytes(int B, int nq, int nt, int hd, int nsplit);
+
+/* The split count fn_test_attn uses when given 0, for a context of ctx keys. */
+int fn_attn_nsplit(int B, int nkv, int nt, int ctx);
+
+/* pos[b] += nt for b < B, on the stream (the reference's k_advance, faie2fn.cu:1905). */
+int fn_advance_dev(int32_t *pos, int B, int nt, void *stream);
+
+/* Utilities with no counterpart in the reference (its GEMV bench fills inputs on the host, faie2fn.cu:2836-2840):
+ *   fn_fill_normal_dev: p[i] = mean + std * N(0,1), a function of (seed, i) only (splitmix64 + Box-Muller), for
+ *   synthetic inputs generated in HBM; fn_copy_dev: plain 16-byte-per-lane streaming copy of bytes (16-aligned),
+ *   the yardstick for achievable HBM bandwidth and the known-size kernel for counter calibration. */
+int fn_fill_normal_dev(float *p, size_t n, uint64_t seed, float mean, float std, void *stream);
+int fn_copy_dev(void *dst, const void *src, size_t bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FAIE2FN_H */

@@ -1,0 +1,121 @@
+"""Vectorised numpy float64 twin of the C oracle (TEST INFRASTRUCTURE ONLY).
+
+Written separately from fn_oracle.c, with a different structure (whole-batch tensor algebra, the rotate-half form of
+RoPE, an explicit convolution window), so that a slip in one restatement shows up as a disagreement between the two.
+Follows the same reference lines: engine/faie2fn.cu:1366-1431 (k_gdn), :1451-1478 (k_qk_norm_rope),
+:1612-1690 (k_attn_split + k_attn_combine), :2573-2576 (inv_freq).
+"""
+
+import numpy as np
+
+
+def _sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def _silu(x):
+    return x * _sigmoid(x)
+
+
+def key_head_index(nkh, nvh, head_map):
+    h = np.arange(nvh)
+    return h % nkh if head_map == 0 else h // (nvh // nkh)
+
+
+def gdn_core(q, k, v, beta, g, S, head_map=0):
+    """q,k [B,nt,nkh,dk] normalised; v [B,nt,nvh,dv]; beta, g [B,nt,nvh]; S [B,nvh,dk,dv] float64 in place."""
+    B, nt, nkh, dk = q.shape
+    nvh = v.shape[2]
+    kidx = key_head_index(nkh, nvh, head_map)
+    outs = []
+    for t in range(nt):
+        qt = q[:, t, kidx].astype(np.float64)          # [B,nvh,dk]
+        kt = k[:, t, kidx].astype(np.float64)
+        vt = v[:, t].astype(np.float64)                # [B,nvh,dv]
+        gam = np.exp(g[:, t].astype(np.float64))[..., None]   # [B,nvh,1]
+        bet = beta[:, t].astype(np.float64)[..., None]
+        kv = np.einsum("bhij,bhi->bhj", S, kt)
+        delta = (vt - gam * kv) * bet
+        S *= gam[..., None]
+        S += kt[..., :, None] * delta[..., None, :]
+        outs.append(np.einsum("bhij,bhi->bhj", S, qt) / np.sqrt(dk))
+    return np.stack(outs, axis=1)
+
+
+def gdn_block(qkv, conv_w, conv_state, ab, dt_bias, ssm_a, S, z, norm_w, nkh, nvh, dk=128, dv=128, head_map=0,
+              gate_act=0, eps=1e-6):
+    """Fused block; conv_state [B,3,C] float64 and S float64 updated in place; returns out [B,nt,nvh*dv]."""
+    B, nt, C = qkv.shape
+    w = conv_w.astype(np.float64)                      # [C,4]
+    outs = []
+    for t in range(nt):
+        x = qkv[:, t].astype(np.float64)               # [B,C]
+        win = np.concatenate([conv_state, x[:, None, :]], axis=1)   # [B,4,C] oldest first
+        y = _silu(np.einsum("btc,ct->bc", win, w))
+        conv_state[:] = win[:, 1:]
+        q = y[:, : nkh * dk].reshape(B, nkh, dk)
+        k = y[:, nkh * dk: 2 * nkh * dk].reshape(B, nkh, dk)
+        v = y[:, 2 * nkh * dk:].reshape(B, nvh, dv)
+        q = q / np.sqrt((q * q).sum(-1, keepdims=True) + 1e-6)
+        k = k / np.sqrt((k * k).sum(-1, keepdims=True) + 1e-6)
+        a = ab[:, t, :nvh].astype(np.float64) + dt_bias.astype(np.float64)
+        sp = np.where(a > 20.0, a, np.log1p(np.exp(np.minimum(a, 20.0))))
+        g = sp * ssm_a.astype(np.float64)
+        beta = _sigmoid(ab[:, t, nvh:].astype(np.float64))
+        o = gdn_core(q[:, None], k[:, None], v[:, None], beta[:, None], g[:, None], S, head_map)[:, 0]   # [B,nvh,dv]
+        r = 1.0 / np.sqrt((o * o).mean(-1, keepdims=True) + eps)
+        zz = z[:, t].astype(np.float64).reshape(B, nvh, dv)
+        gate = _sigmoid(zz) if gate_act == 0 else _silu(zz)
+        outs.append((o * r * norm_w.astype(np.float64) * gate).reshape(B, nvh * dv))
+    return np.stack(outs, axis=1)
+
+
+def rope_inv_freq(nrot, theta):
+    i = np.arange(nrot // 2, dtype=np.float64)
+    return (1.0 / theta ** (2.0 * i / nrot)).astype(np.float32)
+
+
+def _norm_rope(x, w, pos, nrot, inv, eps):
+    """x [..., hd] fp32, pos broadcastable to x[..., 0]; rotate-half form on the first nrot dims."""
+    x = x.astype(np.float64)
+    y = x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * w.astype(np.float64)
+    ang = (np.asarray(pos, np.float32)[..., None] * inv).astype(np.float32)   # fp32 product
+    cos = np.cos(ang.astype(np.float64))
+    sin = np.sin(ang.astype(np.float64))
+    cos = np.concatenate([cos, cos], -1)
+    sin = np.concatenate([sin, sin], -1)
+    rot = y[..., :nrot]
+    half = nrot // 2
+    rotated = np.concatenate([-rot[..., half:], rot[..., :half]], -1)
+    out = y.copy()
+    out[..., :nrot] = rot * cos + rotated * sin
+    return out
+
+
+def attn(qg, knew, vnew, wq, wk, Kc, Vc, pos, nrot=64, theta=1e7, eps=1e-6):
+    """Same contract as oracle.attn; dense softmax per (b, t, head) in float64."""
+    B, nt, nq, _, hd = qg.shape
+    nkv = knew.shape[2]
+    grp = nq // nkv
+    inv = rope_inv_freq(nrot, theta)
+    pos = np.asarray(pos, np.int64)
+    tpos = pos[:, None] + np.arange(nt)[None, :]                        # [B,nt]
+    Q = _norm_rope(qg[:, :, :, 0], wq, tpos[:, :, None], nrot, inv, eps)   # [B,nt,nq,hd]
+    Kn = _norm_rope(knew, wk, tpos[:, :, None], nrot, inv, eps)          # [B,nt,nkv,hd]
+    Vn = vnew.astype(np.float64)
+    og = np.zeros((B, nt, nq, hd))
+    for b in range(B):
+        p0 = int(pos[b])
+        Kall = np.concatenate([Kc[b, :p0].astype(np.float64), Kn[b]], 0)   # [p0+nt,nkv,hd]
+        Vall = np.concatenate([Vc[b, :p0].astype(np.float64), Vn[b]], 0)
+        for t in range(nt):
+            nk = p0 + t + 1
+            for g in range(nkv):
+                qh = Q[b, t, g * grp:(g + 1) * grp]                       # [grp,hd]
+                s = qh @ Kall[:nk, g].T / np.sqrt(hd)                      # [grp,nk]
+                s -= s.max(-1, keepdims=True)
+                p = np.exp(s)
+                o = (p @ Vall[:nk, g]) / p.sum(-1, keepdims=True)
+                gate = qg[b, t, g * grp:(g + 1) * grp, 1].astype(np.float64)
+                og[b, t, g * grp:(g + 1) * grp] = o * _sigmoid(gate)
+    return og, Kn, Vn

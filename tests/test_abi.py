@@ -1,0 +1,101 @@
+"""CPU checks of the C ABI: the library loads without a GPU, exports every symbol include/faie2fn.h declares, the
+reference's model-level entries fail with the reference's -1 + fn_error() convention, and argument validation
+rejects bad calls before any device work."""
+
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import fn
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "faie2fn.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fn_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert header_symbols() == sorted(fn.SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(fnlib):
+    for name in header_symbols():
+        assert hasattr(fnlib.d, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", fn.LIB], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\s[TW]\s+(fn_\w+)$", out, flags=re.M))
+    assert set(header_symbols()) <= exported
+
+
+def test_reference_entries_report_not_built(fnlib):
+    d = fnlib.d
+    assert d.fn_load(b"a.gguf", b"b.gguf", 4096, 0) == -1
+    assert b"decode-attention path only" in d.fn_error()
+    with pytest.raises(RuntimeError, match="not loaded"):
+        fnlib.reset()
+    with pytest.raises(RuntimeError, match="not loaded"):
+        fnlib.forward([1, 2, 3])
+    with pytest.raises(RuntimeError, match="decode-attention path only"):
+        fnlib.dequant(8, np.zeros(34, np.uint8), 1, 32)
+    with pytest.raises(RuntimeError, match="decode-attention path only"):
+        fnlib.gemv(8, np.zeros(34, np.uint8), 1, 32, np.zeros((1, 32), np.float32))
+    assert d.fn_split() == -1 and d.fn_n_past() == -1
+    assert d.fn_dev_gb(0) == -1.0 and d.fn_last_ms() == -1.0
+    d.fn_pdl(0), d.fn_early(0), d.fn_moe_var(1), d.fn_bench_hot(1), d.fn_free()
+
+
+def test_validation_before_device_work(fnlib):
+    d = fnlib.d
+    z = np.zeros(16, np.float32)
+    # dk != 128 is rejected by the launcher; shapes < 1 by the hook
+    assert d.fn_test_gdn(0, 1, 1, 128, 128, 0, 1, z, z, z, z, z, z, z) == -1
+    assert b"bad shape" in d.fn_error()
+    # device entry points validate before launching
+    assert d.fn_gdn_block_dev(1, 16, 32, 64, 64, 0, 0, 1, 4, *([None] * 10), 1e-6, None, None) == -1
+    assert b"dk = dv = 128" in d.fn_error()
+    assert d.fn_gdn_block_dev(1, 16, 32, 128, 128, 0, 0, 2, 4, *([None] * 10), 1e-6, None, None) == -1
+    assert b"ring - 3" in d.fn_error()
+    assert d.fn_gdn_block_dev(1, 16, 32, 128, 128, 0, 0, 1, 6, *([None] * 10), 1e-6, None, None) == -1
+    assert b"power of two" in d.fn_error()
+    assert d.fn_gdn_block_dev(1, 16, 30, 128, 128, 0, 0, 1, 4, *([None] * 10), 1e-6, None, None) == -1
+    assert b"multiple of nkh" in d.fn_error()
+    assert d.fn_gdn_block_dev(1, 16, 32, 128, 128, 0, 0, 1, 4, *([None] * 10), 1e-6, None, None) == -1
+    assert b"null pointer" in d.fn_error()
+    assert d.fn_attn_dev(1, 16, 2, 128, 64, 1e7, 1e-6, 1, 64, *([None] * 8), 1, None, 0, None, None) == -1
+    assert b"head_dim 256" in d.fn_error()
+    assert d.fn_attn_dev(1, 16, 2, 256, 64, 1e7, 1e-6, 1, 100, *([None] * 8), 1, None, 0, None, None) == -1
+    assert b"multiple of 64" in d.fn_error()
+    assert d.fn_attn_dev(1, 16, 3, 256, 64, 1e7, 1e-6, 1, 128, *([None] * 8), 1, None, 0, None, None) == -1
+    assert b"multiple of nkv" in d.fn_error()
+    assert d.fn_attn_dev(1, 16, 2, 256, 65, 1e7, 1e-6, 1, 128, *([None] * 8), 1, None, 0, None, None) == -1
+    assert b"nrot" in d.fn_error()
+    # the host hook checks positions against the cache before touching the device
+    qg = np.zeros((1, 1, 16, 2, 256), np.float32)
+    kv = np.zeros((1, 1, 2, 256), np.float32)
+    w = np.ones(256, np.float32)
+    K = np.zeros((1, 8, 2, 256), np.float32)
+    with pytest.raises(RuntimeError, match="max_ctx"):
+        fnlib.attn(qg, kv, kv, w, w, K, K.copy(), np.array([8], np.int32))
+    with pytest.raises(ValueError):
+        fnlib.gdn_block(np.zeros((1, 1, 8192), np.float32), np.zeros((8192, 4), np.float32),
+                        np.zeros((1, 3, 8192), np.float64), np.zeros((1, 1, 64), np.float32), np.zeros(32, np.float32),
+                        np.zeros(32, np.float32), np.zeros((1, 32, 128, 128), np.float32),
+                        np.zeros((1, 1, 4096), np.float32), np.zeros(128, np.float32), 16, 32)
+
+
+def test_attn_split_heuristic_and_workspace(fnlib):
+    # one tile per wave at least, about 1024 workgroups in total
+    assert fnlib.attn_nsplit(1, 2, 1, 131072) == 512
+    assert fnlib.attn_nsplit(16, 2, 1, 32768) == 32
+    assert fnlib.attn_nsplit(1, 2, 1, 4096) == 16
+    assert fnlib.attn_nsplit(1, 2, 1, 1) == 1
+    for B, nq, nt, ns in ((1, 16, 1, 512), (16, 16, 1, 32), (2, 24, 3, 7)):
+        wb = fnlib.attn_work_bytes(B, nq, nt, ns)
+        assert wb >= 4 * (B * nt * nq * 256 + B * nt * nq * ns * 258)
+    assert fnlib.attn_work_bytes(0, 16, 1, 1) == 0
