@@ -7,10 +7,12 @@
 //     byte crosses HBM once per token (the reference runs one block per query head and re-reads K/V GRP times).
 //   * The K cache is stored key-tiled: each tile of 64 positions is [hd/4][64][4] floats (64 KiB at hd = 256).
 //     Lane l of a wave owns key l of the tile and reads it 16 bytes at a time with fully coalesced 1 KiB wave
-//     loads; the query values it multiplies are wave-uniform and arrive through scalar loads (SGPR operands),
-//     so q.k costs GRP FMAs per 4 dims per key and needs no cross-lane reduction at all.
+//     loads; the query values it multiplies are wave-uniform LDS broadcasts, so q.k costs GRP FMAs per 4 dims per
+//     key and needs no cross-lane reduction at all.
 //   * V stays row-major; for p.V a lane owns 4 output dims, reads each V row with one coalesced 1 KiB wave load
 //     and takes the GRP probabilities of the key as LDS broadcasts.
+//   * K and V are read with the nontemporal hint and in batches of 16 loads per lane, so every wave keeps
+//     16 KiB in flight (the first version waited on each V row and spent ~40 HBM latencies per tile).
 //   * Each wave runs its own online softmax (running max per head via DPP/permlane wave max); the four waves
 //     merge in LDS and write one (m, l, o[hd]) partial per query head per split.
 //   * The combine kernel merges the splits with the log-sum-exp identity and applies o / L * sigmoid(gate).
@@ -84,10 +86,18 @@ __global__ void __launch_bounds__(HD) k_attn_prep(const AttnArgs a) {
 }
 
 // Split-K attention partials.  grid (nsplit, nkv, B nt), WAVES*64 threads.
+// Each wave walks its tiles; per tile the K reads go out in batches of 16 x 16 bytes per lane and the V rows in
+// batches of 16 coalesced 1 KiB rows, so a wave keeps 16 KiB of loads in flight instead of waiting on each one.
 template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
-    __shared__ float pb[WAVES][TILE][GRP];          // probabilities of the current tile, per wave
-    __shared__ float4 mo[WAVES][GRP][HD / 4];       // per-wave o for the merge
+    constexpr int NB = GRP > 8 ? 8 : 16;            // loads in flight per lane per batch
+    // LDS: q of the group and the per-wave tile probabilities while walking; the per-wave partials for the
+    // merge afterwards (same bytes)
+    constexpr int WALK = HD / 4 * GRP * 16 + WAVES * TILE * GRP * 4, MERGE = WAVES * GRP * HD * 4;
+    __shared__ __align__(16) unsigned char smem[WALK > MERGE ? WALK : MERGE];
     __shared__ float mm[WAVES][GRP], ml[WAVES][GRP];
+    float4 *qs = reinterpret_cast<float4 *>(smem);                                  // [HD/4][GRP]
+    float *pb = reinterpret_cast<float *>(smem + HD / 4 * GRP * 16);                // [WAVES][TILE][GRP]
+    float4 *mo = reinterpret_cast<float4 *>(smem);                                  // [WAVES][GRP][HD/4]
 
     const int sp = blockIdx.x, g = blockIdx.y, bt = blockIdx.z, b = bt / a.nt, t = bt - b * a.nt;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -98,8 +108,11 @@ template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(co
     const float scale = rsqrtf((float) HD);  // 1/16 at HD = 256 (faie2fn.cu:1646)
 
     const float4 *Qg = reinterpret_cast<const float4 *>(a.Q + ((size_t) bt * a.nkv + g) * HD * GRP);
+    for (int i = threadIdx.x; i < HD / 4 * GRP; i += WAVES * 64) qs[i] = Qg[i];
+    __syncthreads();
     const float *Kbase = a.Kc + ((size_t) b * a.nkv + g) * a.max_ctx * HD;
-    const float *Vbase = a.Vc + ((size_t) b * a.nkv + g) * a.max_ctx * HD;
+    const float4 *Vbase = reinterpret_cast<const float4 *>(a.Vc + ((size_t) b * a.nkv + g) * a.max_ctx * HD);
+    float *pw = pb + wave * TILE * GRP;
 
     float m[GRP], l[GRP];
     float4 o[GRP];
@@ -113,21 +126,26 @@ template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(co
     for (int tile = tile0 + wave; tile < tile1; tile += WAVES) {
         const int key0 = tile * TILE;
         const bool valid = key0 + lane < nk;
-        // scores: lane = key; K read as 16-byte chunks of the key-tiled layout, q as wave-uniform scalars
+        // scores: lane = key; K read as 16-byte chunks of the key-tiled layout (coalesced 1 KiB per wave load),
+        // q as LDS broadcasts
         const float4 *Kt = reinterpret_cast<const float4 *>(Kbase + (size_t) tile * TILE * HD);
         float s[GRP];
 #pragma unroll
         for (int hh = 0; hh < GRP; ++hh) s[hh] = 0.0f;
-#pragma unroll 8
-        for (int c = 0; c < HD / 4; ++c) {
-            const float4 kf = Kt[c * TILE + lane];
+        for (int cb = 0; cb < HD / 4; cb += NB) {
+            float4 kf[NB];
 #pragma unroll
-            for (int hh = 0; hh < GRP; ++hh) {
-                const float4 qv = Qg[c * GRP + hh];
-                s[hh] = fmaf(qv.x, kf.x, s[hh]);
-                s[hh] = fmaf(qv.y, kf.y, s[hh]);
-                s[hh] = fmaf(qv.z, kf.z, s[hh]);
-                s[hh] = fmaf(qv.w, kf.w, s[hh]);
+            for (int u = 0; u < NB; ++u) kf[u] = ld_nt(&Kt[(cb + u) * TILE + lane]);
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+#pragma unroll
+                for (int hh = 0; hh < GRP; ++hh) {
+                    const float4 qv = qs[(cb + u) * GRP + hh];
+                    s[hh] = fmaf(qv.x, kf[u].x, s[hh]);
+                    s[hh] = fmaf(qv.y, kf[u].y, s[hh]);
+                    s[hh] = fmaf(qv.z, kf[u].z, s[hh]);
+                    s[hh] = fmaf(qv.w, kf[u].w, s[hh]);
+                }
             }
         }
         // online softmax update (faie2fn.cu:1648-1663), one running max per head per wave
@@ -136,27 +154,36 @@ template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(co
             const float sc = valid ? s[hh] * scale : -INFINITY;
             const float mn = fmaxf(m[hh], wave_max(sc));  // finite: the tile holds >= 1 visible key
             const float corr = expf(m[hh] - mn);           // 0 while m is -inf
-            const float p = valid ? expf(sc - mn) : 0.0f;
-            l[hh] = fmaf(l[hh], corr, p);
+            const float pr = valid ? expf(sc - mn) : 0.0f;
+            l[hh] = fmaf(l[hh], corr, pr);
             o[hh].x *= corr; o[hh].y *= corr; o[hh].z *= corr; o[hh].w *= corr;
             m[hh] = mn;
-            pb[wave][lane][hh] = p;
+            pw[lane * GRP + hh] = pr;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // p.V: lane = 4 output dims, one coalesced V row per key
+        // p.V: lane = 4 output dims, one coalesced V row per key.  Rows past the last visible key are clamped to
+        // it (finite data, probability 0) so a batch never branches per key.
         const int nj = min(TILE, nk - key0);
-        const float4 *Vt = reinterpret_cast<const float4 *>(Vbase + (size_t) key0 * HD);
-        for (int jj = 0; jj < nj; ++jj) {
-            const float4 vf = Vt[(size_t) jj * (HD / 4) + lane];
+        for (int jb = 0; jb < nj; jb += NB) {
+            float4 vf[NB];
 #pragma unroll
-            for (int hh = 0; hh < GRP; ++hh) {
-                const float p = pb[wave][jj][hh];
-                o[hh].x = fmaf(p, vf.x, o[hh].x);
-                o[hh].y = fmaf(p, vf.y, o[hh].y);
-                o[hh].z = fmaf(p, vf.z, o[hh].z);
-                o[hh].w = fmaf(p, vf.w, o[hh].w);
+            for (int u = 0; u < NB; ++u) {
+                const int row = min(key0 + jb + u, nk - 1);
+                vf[u] = ld_nt(&Vbase[(size_t) row * (HD / 4) + lane]);
+            }
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const float *pj = pw + (jb + u) * GRP;
+#pragma unroll
+                for (int hh = 0; hh < GRP; ++hh) {
+                    const float pr = pj[hh];
+                    o[hh].x = fmaf(pr, vf[u].x, o[hh].x);
+                    o[hh].y = fmaf(pr, vf[u].y, o[hh].y);
+                    o[hh].z = fmaf(pr, vf[u].z, o[hh].z);
+                    o[hh].w = fmaf(pr, vf[u].w, o[hh].w);
+                }
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -164,7 +191,8 @@ template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(co
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 
-    // merge the waves
+    // merge the waves (the walk's LDS is reused for the per-wave partials)
+    __syncthreads();
 #pragma unroll
     for (int hh = 0; hh < GRP; ++hh) {
         const float lw = wave_sum(l[hh]);
@@ -172,7 +200,7 @@ template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(co
             mm[wave][hh] = m[hh];
             ml[wave][hh] = lw;
         }
-        mo[wave][hh][lane] = o[hh];
+        mo[(wave * GRP + hh) * (HD / 4) + lane] = o[hh];
     }
     __syncthreads();
     const int d = threadIdx.x;  // WAVES * 64 == HD
@@ -200,22 +228,56 @@ template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(co
     }
 }
 
-// merge splits + sigmoid output gate (faie2fn.cu:1670-1690).  grid (nq, B nt), HD threads
-__global__ void __launch_bounds__(HD) k_attn_combine(const AttnArgs a) {
-    const int h = blockIdx.x, bt = blockIdx.y, d = threadIdx.x;
-    const size_t base = ((size_t) bt * a.nq + h) * a.nsplit;
+// merge splits + sigmoid output gate (faie2fn.cu:1670-1690).  grid (nq, B nt), 256 threads.
+// Pass 1: the global max M over the splits' maxima.  Pass 2: wave w takes splits w, w+4, ...; lane l owns dims
+// 4l..4l+3 (one coalesced 1 KiB row per split), 8 rows in flight; the four waves' sums meet in LDS.
+__global__ void __launch_bounds__(256) k_attn_combine(const AttnArgs a) {
+    constexpr int NB = 8;
+    __shared__ float red[4];
+    __shared__ float4 acc[4][HD / 4];
+    __shared__ float lsum[4];
+    const int h = blockIdx.x, bt = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int ns = a.nsplit;
+    const size_t base = ((size_t) bt * a.nq + h) * ns;
+    const float *ml = a.part_ml + base * 2;
     float M = -INFINITY;
-    for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, a.part_ml[(base + s) * 2]);
-    float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < a.nsplit; ++s) {
-        const float m = a.part_ml[(base + s) * 2];
-        if (m == -INFINITY) continue;
-        const float w = expf(m - M);
-        L = fmaf(w, a.part_ml[(base + s) * 2 + 1], L);
-        O = fmaf(w, a.part_o[(base + s) * HD + d], O);
+    for (int s = tid; s < ns; s += 256) M = fmaxf(M, ml[2 * s]);
+    M = wave_max(M);
+    if (lane == 0) red[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float4 *po = reinterpret_cast<const float4 *>(a.part_o + base * HD);
+    float4 O = f4(0.0f);
+    float L = 0.0f;
+    for (int s0 = wave; s0 < ns; s0 += 4 * NB) {
+        float4 v[NB];
+        float w[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int s = min(s0 + 4 * u, ns - 1);
+            v[u] = po[(size_t) s * (HD / 4) + lane];
+            const float m = ml[2 * s];
+            // splits without keys (m = -inf) and the clamped repeats past the end weigh 0
+            w[u] = (s0 + 4 * u < ns && m != -INFINITY) ? expf(m - M) : 0.0f;
+            L = fmaf(w[u], w[u] != 0.0f ? ml[2 * s + 1] : 0.0f, L);
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            O.x = fmaf(w[u], v[u].x, O.x);
+            O.y = fmaf(w[u], v[u].y, O.y);
+            O.z = fmaf(w[u], v[u].z, O.z);
+            O.w = fmaf(w[u], v[u].w, O.w);
+        }
     }
+    acc[wave][lane] = O;
+    if (lane == 0) lsum[wave] = L;
+    __syncthreads();
+    const float Lt = lsum[0] + lsum[1] + lsum[2] + lsum[3];
+    const float *af = reinterpret_cast<const float *>(acc);
+    const int d = tid;  // 256 threads == HD
+    const float Ot = af[d] + af[HD + d] + af[2 * HD + d] + af[3 * HD + d];
     const float gate = a.qg[(((size_t) bt * a.nq + h) * 2 + 1) * HD + d];
-    a.og[((size_t) bt * a.nq + h) * HD + d] = (O / L) * sigmoidf_(gate);
+    a.og[((size_t) bt * a.nq + h) * HD + d] = (Ot / Lt) * sigmoidf_(gate);
 }
 
 __global__ void k_advance(int32_t *pos, int B, int nt) {
@@ -269,7 +331,7 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
         case 4: hipLaunchKernelGGL(k_attn_split<4>, dim3(p.nsplit, p.nkv, (unsigned) bt), dim3(WAVES * 64), 0, st, a); break;
         default: FN_FAIL("attn: query heads per kv head must be 4, 8 or 12");
     }
-    hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(HD), 0, st, a);
+    hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(256), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
 }

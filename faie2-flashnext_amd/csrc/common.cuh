@@ -87,4 +87,16 @@ __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x));
 
 __device__ __forceinline__ float4 f4(float a) { return make_float4(a, a, a, a); }
 
+// 16-byte loads and stores with the nontemporal hint (data touched once per call: keep it out of the caches'
+// reuse path)
+typedef float v4f_ __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_nt(const float4 *p) {
+    const v4f_ v = __builtin_nontemporal_load(reinterpret_cast<const v4f_ *>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_nt(float4 *p, float4 x) {
+    v4f_ v = {x.x, x.y, x.z, x.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<v4f_ *>(p));
+}
+
 }  // namespace fn

@@ -3,13 +3,15 @@
 //
 // Semantics follow k_gdn (reference engine/faie2fn.cu:1349-1431).  The kernel is organised for CDNA4, not as a
 // translation of the sm_120 one:
-//   * 256 threads (four wave64s) per head.  Thread (rg = tid / 32, cg = tid % 32) owns the 4 columns 4cg..4cg+3
-//     of the 16 state rows 16rg..16rg+15, i.e. 16 float4 registers.  Every wave load and store of S moves two
-//     contiguous 512-byte rows with 128-bit accesses, and S makes exactly one trip HBM -> VGPRs -> HBM per call.
+//   * 512 threads (eight wave64s) per head.  Thread (rg = tid / 32, cg = tid % 32) owns the 4 columns 4cg..4cg+3
+//     of the 8 state rows 8rg..8rg+7, i.e. 8 float4 registers.  Every wave load and store of S moves two
+//     contiguous 512-byte rows with 128-bit accesses, and S makes exactly one trip HBM -> VGPRs -> HBM per call,
+//     with the nontemporal hint on both legs (measured on MI355X: 62.2 -> 52.4 us per B = 64 layer-step; 256 or
+//     1024 threads per head and an XCD-contiguous head order were all slower).
 //   * One read pass computes both reductions the step needs, kv = S^T k and sq = S^T q (old S), because
 //       S' = g S + k d^T  with  d = beta (v - g kv)    =>    S'^T q = g sq + (k.q) d.
-//     The column partials of the 8 row groups are folded with a lane^32 permute (2 groups per wave) and
-//     one 2 KiB LDS exchange across the four waves; there is no serial 128-long FMA chain.
+//     The column partials of the 16 row groups are folded with a lane^32 permute (2 groups per wave) and
+//     one 4 KiB LDS exchange across the eight waves; there is no serial 128-long FMA chain.
 //   * q/k are not normalised before the pass: the L2 factors are applied to the 4 per-column sums, so the
 //     norm reductions (wave DPP sums) overlap the S loads instead of sitting in front of them.
 //   * The causal conv state is a ring of R slots per sequence, R a power of two >= nt + 3: the raw input of
@@ -25,9 +27,30 @@ namespace fn {
 
 namespace {
 
+#ifndef GDN_THREADS
+#define GDN_THREADS 512
+#endif
+#ifndef GDN_NT
+#define GDN_NT 1
+#endif
+#ifndef GDN_NT_ST
+#define GDN_NT_ST GDN_NT
+#endif
+#ifndef GDN_WPE
+#define GDN_WPE 1
+#endif
+
 constexpr int DK = 128, DV = 128;
-constexpr int THREADS = 256;
-constexpr int ROWS_PT = 16;  // state rows per thread
+constexpr int THREADS = GDN_THREADS;       // 256 or 512
+constexpr int WAVES = THREADS / 64;
+constexpr int ROWS_PT = DK * 32 / THREADS;  // state rows per thread (32 threads span a row)
+static_assert(THREADS == 256 || THREADS == 512 || THREADS == 1024, "one state tile per 4, 8 or 16 waves");
+
+__device__ __forceinline__ float4 ld_state(const float4 *p) { return GDN_NT ? ld_nt(p) : *p; }
+__device__ __forceinline__ void st_state(float4 *p, float4 v) {
+    if (GDN_NT_ST) st_nt(p, v);
+    else *p = v;
+}
 
 struct GdnArgs {
     int B, nkh, nvh, nt, ring, head_map, gate_act;
@@ -62,7 +85,8 @@ __device__ __forceinline__ float conv_silu(const GdnArgs &a, int b, int t, int C
     return siluf_(acc);
 }
 
-template <bool FUSED> __global__ void __launch_bounds__(THREADS) k_gdn(const GdnArgs a) {
+template <bool FUSED>
+__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GDN_WPE, 8))) k_gdn(const GdnArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int cg = tid & 31, rg = tid >> 5;
     const int bh = blockIdx.x, b = bh / a.nvh, h = bh - b * a.nvh;
@@ -71,14 +95,14 @@ template <bool FUSED> __global__ void __launch_bounds__(THREADS) k_gdn(const Gdn
 
     __shared__ float4 qs4[DK / 4], ks4[DK / 4];  // raw q, k of the key head (this token)
     __shared__ float vs[DV];                      // conv'd v of the value head
-    __shared__ float4 red[4][2][DV / 4];          // per-wave column partials of kv and sq
+    __shared__ float4 red[WAVES][2][DV / 4];      // per-wave column partials of kv and sq
     __shared__ float nrm[2][3];                   // per-wave sums q.q, k.k, q.k (waves 0, 1)
 
     // 1. state tile into registers: issued first, everything below overlaps its latency
     float4 s[ROWS_PT];
     float4 *Sh = reinterpret_cast<float4 *>(a.S + (size_t) bh * DK * DV);
 #pragma unroll
-    for (int r = 0; r < ROWS_PT; ++r) s[r] = Sh[(rg * ROWS_PT + r) * (DV / 4) + cg];
+    for (int r = 0; r < ROWS_PT; ++r) s[r] = ld_state(&Sh[(rg * ROWS_PT + r) * (DV / 4) + cg]);
 
     const int pos = FUSED ? a.pos[b] : 0;
     const float scale = 0.08838834764831845f;  // 1/sqrt(128), faie2fn.cu:1352
@@ -106,7 +130,7 @@ template <bool FUSED> __global__ void __launch_bounds__(THREADS) k_gdn(const Gdn
                 nrm[wave][1] = skk;
                 nrm[wave][2] = sqk;
             }
-        } else {
+        } else if (tid < DK + DV) {
             const int j = tid - DK;
             float vv;
             if (FUSED) vv = conv_silu(a, b, t, C, 2 * a.nkh * DK + h * DV + j, pos + t);
@@ -168,7 +192,7 @@ template <bool FUSED> __global__ void __launch_bounds__(THREADS) k_gdn(const Gdn
         __syncthreads();
         float4 kv = red[0][0][cg], sq = red[0][1][cg];
 #pragma unroll
-        for (int w = 1; w < 4; ++w) {
+        for (int w = 1; w < WAVES; ++w) {
             const float4 x = red[w][0][cg], y = red[w][1][cg];
             kv.x += x.x; kv.y += x.y; kv.z += x.z; kv.w += x.w;
             sq.x += y.x; sq.y += y.y; sq.z += y.z; sq.w += y.w;
@@ -233,7 +257,7 @@ template <bool FUSED> __global__ void __launch_bounds__(THREADS) k_gdn(const Gdn
 
     // 7. write back: state once, conv ring slots of this call's last (up to) three positions
 #pragma unroll
-    for (int r = 0; r < ROWS_PT; ++r) Sh[(rg * ROWS_PT + r) * (DV / 4) + cg] = s[r];
+    for (int r = 0; r < ROWS_PT; ++r) st_state(&Sh[(rg * ROWS_PT + r) * (DV / 4) + cg], s[r]);
     if (FUSED) {
         const bool primary = a.head_map == 0 ? h < a.nkh : (h % (a.nvh / a.nkh)) == 0;
         for (int t = max(0, a.nt - 3); t < a.nt; ++t) {
@@ -246,7 +270,7 @@ template <bool FUSED> __global__ void __launch_bounds__(THREADS) k_gdn(const Gdn
                     dst[cq] = x[cq];
                     dst[ck] = x[ck];
                 }
-            } else {
+            } else if (tid < DK + DV) {
                 const int cv = 2 * a.nkh * DK + h * DV + (tid - DK);
                 dst[cv] = x[cv];
             }
