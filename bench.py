@@ -152,6 +152,41 @@ class AttnStack:
         self.work.free()
 
 
+def hybrid_config4(lib, steps, warmup, B=16, ctx=32768, nl=48):
+    """Config 4 through the native path engine: 48 layers, attention iff (il + 1) % 4 == 0 (36 DeltaNet + 12 GQA),
+    B = 16, every sequence at context ctx (the first new token at position ctx - 1; the context grows by one per
+    step, as in decode).  Returns ms per step from HIP events on the engine's stream (hipGraph replay)."""
+    lib.path_init(B, nl, 4, NKH, NVH, 16, 2, ctx + warmup + steps + 64, 0, 0, 0)
+    try:
+        rng = np.random.default_rng(4)
+        for il in range(nl):
+            s = 4000 + il * 13
+            if (il + 1) % 4:
+                lay = fn_synth.BlockLayer(B=1, config=4, layer=il)
+                for kind, arr in (("CONV_W", lay.conv_w), ("DT_BIAS", lay.dt_bias), ("SSM_A", lay.ssm_a),
+                                  ("NORM_W", lay.norm_w)):
+                    hiprt.htod(lib.path_buffer(il, kind)[0], arr)
+                for i, (kind, std) in enumerate((("S", 0.02), ("QKV", 1.0), ("AB", 1.0), ("Z", 1.0))):
+                    p, n = lib.path_buffer(il, kind)
+                    lib.fill_normal_dev(p, n // 4, s + i, 0.0, std)
+            else:
+                for kind in ("WQ", "WK"):
+                    hiprt.htod(lib.path_buffer(il, kind)[0], rng.normal(1.0, 0.1, 256).astype(np.float32))
+                for i, kind in enumerate(("KC", "VC", "QG", "K", "V")):
+                    p, n = lib.path_buffer(il, kind)
+                    lib.fill_normal_dev(p, n // 4, s + i)
+        hiprt.htod(lib.path_buffer(0, "POS")[0], np.full(B, ctx - 1, np.int32))
+        hiprt.sync()
+        lib.use_graphs(True)
+        if warmup:
+            lib.path_step(warmup)
+        ms = lib.path_step(steps, timed=True)
+    finally:
+        lib.free()
+    nbytes = 36 * fn_synth.gdn_block_bytes(B) + 12 * fn_synth.attn_bytes(B, ctx)
+    return ms, nbytes
+
+
 def time_graph(stream, fn_launch, steps, warmup):
     """Capture fn_launch into a hipGraph, replay warmup times, then time `steps` replays with HIP events recorded
     on the same stream.  Returns ms per replay."""
@@ -196,7 +231,7 @@ def cpu_baseline(budget_s=12.0):
         oracle.gdn_block(qkv, lay.conv_w, conv, ab, lay.dt_bias, lay.ssm_a, S, z, lay.norm_w, NKH, NVH)
         n += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or n >= 400:
+        if el >= budget_s or n >= 4000:
             break
     per = el / n
     return {"value": round(fn_synth.gdn_block_bytes(64) / per / 1e9, 4), "unit": "GB/s",
@@ -264,6 +299,11 @@ def main():
             extra[f"config3_gqa_b{Bq}_ctx{ctx}"] = {"us_per_layer_step": round(ms * 1e3, 2),
                                                    "gbs": round(by / (ms * 1e-3) / 1e9, 1), "nsplit": nsplit}
             log(f"[bench] config 3 B={Bq} ctx={ctx}: {ms * 1e3:.1f} us, {by / (ms * 1e-3) / 1e9:.0f} GB/s")
+        ms, nbytes = hybrid_config4(lib, steps, warmup)
+        extra["config4_hybrid_b16_ctx32768"] = {"ms_per_step": round(ms, 4), "us_per_token": round(ms * 1e3 / 16, 2),
+                                               "tokens_per_s": round(16 * 1e3 / ms, 1), "bytes_per_step": nbytes,
+                                               "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                               "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
         for k, v in extra.items():
             log(f"[bench] {k}: {v}")
 

@@ -4,9 +4,7 @@
 // (flashnext/fn.py) binds unchanged; the model-level ones report that this library carries only the
 // decode-attention path.  Sections 2 and 3 are this path's hooks: host arrays in / out (synchronous, device 0,
 // the reference's unit-test-hook style, faie2fn.cu:2745) and the device-buffer entry points an engine calls.
-#include "gdn.h"
-
-#include "../../include/faie2fn.h"
+#include "engine.h"
 
 #include <cstring>
 #include <vector>
@@ -34,7 +32,7 @@ const char *kNoModel =
     "the forward pass, GEMV, MoE and routing are not part of it";
 
 // switches the reference exposes for its forward; kept so scripts that set them still run
-int g_pdl = 1, g_early = 1, g_moe_var = 0, g_bench_hot = 0, g_use_graphs = 1;
+int g_pdl = 1, g_early = 1, g_moe_var = 0, g_bench_hot = 0;
 
 // device buffers of one host-hook call, released on every return path
 struct DevBufs {
@@ -71,17 +69,14 @@ int use_device0() {
 }  // namespace
 
 FN_API const char *fn_error(void) { return fn::error_cstr(); }
-FN_API void fn_free(void) {}
+FN_API void fn_free(void) { fn::path_free(); }
 FN_API int fn_load(const char *, const char *, int, int) { FN_FAIL(kNoModel); }
-FN_API int fn_split(void) { return -1; }
-FN_API double fn_dev_gb(int) { return -1; }
-FN_API int fn_n_past(void) { return -1; }
-FN_API double fn_last_ms(void) { return -1; }
-FN_API int fn_reset(void) { FN_FAIL("not loaded"); }
-FN_API int fn_use_graphs(int on) {
-    g_use_graphs = on != 0;
-    FN_FAIL("not loaded");
-}
+FN_API int fn_split(void) { return fn::path_loaded() ? 0 : -1; }  // one GPU: every layer on device 0
+FN_API double fn_dev_gb(int dv) { return dv == 0 ? fn::path_dev_gb() : -1; }
+FN_API int fn_n_past(void) { return fn::path_n_past(); }
+FN_API double fn_last_ms(void) { return fn::path_last_ms(); }
+FN_API int fn_reset(void) { return fn::path_reset(); }
+FN_API int fn_use_graphs(int on) { return fn::path_use_graphs(on); }
 FN_API int fn_forward(const int32_t *, int, float *, int32_t *) { FN_FAIL("not loaded"); }
 FN_API int fn_debug_layers(float *) { FN_FAIL("not loaded"); }
 FN_API int fn_test_dequant(uint32_t, const uint8_t *, int, int, float *) { FN_FAIL(kNoModel); }
@@ -143,6 +138,16 @@ FN_API int fn_fill_normal_dev(float *p, size_t n, uint64_t seed, float mean, flo
 FN_API int fn_copy_dev(void *dst, const void *src, size_t bytes, void *stream) {
     return fn::copy_launch(dst, src, bytes, (hipStream_t) stream);
 }
+
+// ---------------------------------------------------------------------------------------------
+// 4. path engine
+
+FN_API int fn_path_init(int B, int nl, int attn_every, int nkh, int nvh, int nq, int nkv, int max_ctx, int head_map,
+                        int gate_act, int nsplit) {
+    return fn::path_init(B, nl, attn_every, nkh, nvh, nq, nkv, max_ctx, head_map, gate_act, nsplit);
+}
+FN_API int fn_path_buffer(int il, int kind, void **ptr, size_t *bytes) { return fn::path_buffer(il, kind, ptr, bytes); }
+FN_API int fn_path_step(int steps, float *ms) { return fn::path_step(steps, ms); }
 
 // ---------------------------------------------------------------------------------------------
 // 2. host-array hooks

@@ -228,37 +228,40 @@ template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(co
     }
 }
 
-// merge splits + sigmoid output gate (faie2fn.cu:1670-1690).  grid (nq, B nt), 256 threads.
-// Pass 1: the global max M over the splits' maxima.  Pass 2: wave w takes splits w, w+4, ...; lane l owns dims
-// 4l..4l+3 (one coalesced 1 KiB row per split), 8 rows in flight; the four waves' sums meet in LDS.
-__global__ void __launch_bounds__(256) k_attn_combine(const AttnArgs a) {
+// merge splits + sigmoid output gate (faie2fn.cu:1670-1690).  grid (nq, B nt), CW * 64 threads.
+// Pass 1: the global max M over the splits' maxima.  Pass 2: wave w takes splits w, w + CW, ...; lane l owns dims
+// 4l..4l+3 (one coalesced 1 KiB row per split) with NB rows in flight; the waves' sums meet in LDS.
+constexpr int CW = 16;
+__global__ void __launch_bounds__(CW * 64) k_attn_combine(const AttnArgs a) {
     constexpr int NB = 8;
-    __shared__ float red[4];
-    __shared__ float4 acc[4][HD / 4];
-    __shared__ float lsum[4];
+    __shared__ float red[CW];
+    __shared__ float4 acc[CW][HD / 4];
+    __shared__ float lsum[CW];
     const int h = blockIdx.x, bt = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int ns = a.nsplit;
     const size_t base = ((size_t) bt * a.nq + h) * ns;
     const float *ml = a.part_ml + base * 2;
     float M = -INFINITY;
-    for (int s = tid; s < ns; s += 256) M = fmaxf(M, ml[2 * s]);
+    for (int s = tid; s < ns; s += CW * 64) M = fmaxf(M, ml[2 * s]);
     M = wave_max(M);
     if (lane == 0) red[wave] = M;
     __syncthreads();
-    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    M = red[0];
+#pragma unroll
+    for (int w = 1; w < CW; ++w) M = fmaxf(M, red[w]);
     const float4 *po = reinterpret_cast<const float4 *>(a.part_o + base * HD);
     float4 O = f4(0.0f);
     float L = 0.0f;
-    for (int s0 = wave; s0 < ns; s0 += 4 * NB) {
+    for (int s0 = wave; s0 < ns; s0 += CW * NB) {
         float4 v[NB];
         float w[NB];
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
-            const int s = min(s0 + 4 * u, ns - 1);
-            v[u] = po[(size_t) s * (HD / 4) + lane];
+            const int s = min(s0 + CW * u, ns - 1);
+            v[u] = ld_nt(&po[(size_t) s * (HD / 4) + lane]);
             const float m = ml[2 * s];
             // splits without keys (m = -inf) and the clamped repeats past the end weigh 0
-            w[u] = (s0 + 4 * u < ns && m != -INFINITY) ? expf(m - M) : 0.0f;
+            w[u] = (s0 + CW * u < ns && m != -INFINITY) ? expf(m - M) : 0.0f;
             L = fmaf(w[u], w[u] != 0.0f ? ml[2 * s + 1] : 0.0f, L);
         }
 #pragma unroll
@@ -272,12 +275,17 @@ __global__ void __launch_bounds__(256) k_attn_combine(const AttnArgs a) {
     acc[wave][lane] = O;
     if (lane == 0) lsum[wave] = L;
     __syncthreads();
-    const float Lt = lsum[0] + lsum[1] + lsum[2] + lsum[3];
-    const float *af = reinterpret_cast<const float *>(acc);
-    const int d = tid;  // 256 threads == HD
-    const float Ot = af[d] + af[HD + d] + af[2 * HD + d] + af[3 * HD + d];
-    const float gate = a.qg[(((size_t) bt * a.nq + h) * 2 + 1) * HD + d];
-    a.og[((size_t) bt * a.nq + h) * HD + d] = (Ot / Lt) * sigmoidf_(gate);
+    if (tid < HD) {
+        const float *af = reinterpret_cast<const float *>(acc);
+        float Lt = 0.0f, Ot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < CW; ++w) {
+            Lt += lsum[w];
+            Ot += af[w * HD + tid];
+        }
+        const float gate = a.qg[(((size_t) bt * a.nq + h) * 2 + 1) * HD + tid];
+        a.og[((size_t) bt * a.nq + h) * HD + tid] = (Ot / Lt) * sigmoidf_(gate);
+    }
 }
 
 __global__ void k_advance(int32_t *pos, int B, int nt) {
@@ -331,7 +339,7 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
         case 4: hipLaunchKernelGGL(k_attn_split<4>, dim3(p.nsplit, p.nkv, (unsigned) bt), dim3(WAVES * 64), 0, st, a); break;
         default: FN_FAIL("attn: query heads per kv head must be 4, 8 or 12");
     }
-    hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(CW * 64), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
 }

@@ -33,11 +33,34 @@ SYMBOLS = (
     "fn_test_gdn", "fn_test_gdn_block", "fn_test_attn",
     "fn_gdn_block_dev", "fn_gdn_core_dev", "fn_attn_dev", "fn_attn_work_bytes", "fn_attn_nsplit", "fn_advance_dev",
     "fn_fill_normal_dev", "fn_copy_dev",
+    "fn_path_init", "fn_path_buffer", "fn_path_step",
 )
+
+# buffer kinds of fn_path_buffer (include/faie2fn.h)
+BUF = dict(S=0, CONV_RING=1, QKV=2, AB=3, Z=4, OUT=5, CONV_W=6, DT_BIAS=7, SSM_A=8, NORM_W=9, KC=10, VC=11, QG=12,
+           K=13, V=14, OG=15, WQ=16, WK=17, POS=18)
 
 
 def _f32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def kv_to_device(Kc, Vc):
+    """Reference-layout caches [B][T][nkv][hd] (T a multiple of 64) -> the device layouts of fn_attn_dev:
+    K key-tiled [B][nkv][T/64][hd/4][64][4], V head-major [B][nkv][T][hd]."""
+    B, T, nkv, hd = Kc.shape
+    if T % 64 or hd % 4:
+        raise ValueError("cache rows must be a multiple of 64 and head_dim a multiple of 4")
+    Kd = Kc.reshape(B, T // 64, 64, nkv, hd // 4, 4).transpose(0, 3, 1, 4, 2, 5)
+    Vd = Vc.transpose(0, 2, 1, 3)
+    return np.ascontiguousarray(Kd, np.float32), np.ascontiguousarray(Vd, np.float32)
+
+
+def kv_from_device(Kd, Vd, B, T, nkv, hd):
+    """Inverse of kv_to_device."""
+    K = np.asarray(Kd).reshape(B, nkv, T // 64, hd // 4, 64, 4).transpose(0, 2, 4, 1, 3, 5).reshape(B, T, nkv, hd)
+    V = np.asarray(Vd).reshape(B, nkv, T, hd).transpose(0, 2, 1, 3)
+    return np.ascontiguousarray(K), np.ascontiguousarray(V)
 
 
 class FN:
@@ -70,6 +93,11 @@ class FN:
         d.fn_advance_dev.argtypes = [VP, i, i, VP]
         d.fn_fill_normal_dev.argtypes = [VP, C.c_size_t, C.c_uint64, C.c_float, C.c_float, VP]
         d.fn_copy_dev.argtypes = [VP, VP, C.c_size_t, VP]
+        d.fn_path_init.argtypes = [i] * 11
+        d.fn_path_buffer.argtypes = [i, i, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]
+        d.fn_path_step.argtypes = [i, C.POINTER(C.c_float)]
+        d.fn_use_graphs.argtypes = [i]
+        d.fn_n_past.restype = C.c_int
 
     def check(self, rc):
         if rc != 0:
@@ -175,3 +203,27 @@ class FN:
 
     def copy_dev(self, dst, src, nbytes, stream=0):
         self.check(self.d.fn_copy_dev(dst, src, nbytes, stream))
+
+    # ---- path engine ----
+    def path_init(self, B, nl, attn_every=4, nkh=16, nvh=32, nq=16, nkv=2, max_ctx=4096, head_map=0, gate_act=0,
+                  nsplit=0):
+        self.check(self.d.fn_path_init(B, nl, attn_every, nkh, nvh, nq, nkv, max_ctx, head_map, gate_act, nsplit))
+
+    def path_buffer(self, il, kind):
+        """(device address, bytes) of buffer `kind` (a BUF name or number) of layer il."""
+        k = BUF[kind] if isinstance(kind, str) else int(kind)
+        p, n = C.c_void_p(), C.c_size_t()
+        self.check(self.d.fn_path_buffer(il, k, C.byref(p), C.byref(n)))
+        return p.value, n.value
+
+    def path_step(self, steps=1, timed=False):
+        """steps decode steps through all layers; returns HIP-event ms per step when timed."""
+        ms = C.c_float(0.0)
+        self.check(self.d.fn_path_step(steps, C.byref(ms) if timed else None))
+        return ms.value if timed else None
+
+    def use_graphs(self, on):
+        self.check(self.d.fn_use_graphs(1 if on else 0))
+
+    def free(self):
+        self.d.fn_free()

@@ -73,6 +73,19 @@ def mem_info():
     return f.value, t.value
 
 
+def htod(ptr, arr):
+    """Copy a host array to device address ptr (synchronous)."""
+    arr = np.ascontiguousarray(arr)
+    check(lib().hipMemcpy(ptr, arr.ctypes.data, arr.nbytes, _H2D), "hipMemcpy H2D")
+
+
+def dtoh(ptr, shape, dtype=np.float32):
+    """Copy device address ptr into a new host array of shape/dtype (synchronous)."""
+    out = np.empty(shape, dtype)
+    check(lib().hipMemcpy(out.ctypes.data, ptr, out.nbytes, _D2H), "hipMemcpy D2H")
+    return out
+
+
 class Buf:
     """A device allocation of nbytes, freed with free() or on garbage collection."""
 

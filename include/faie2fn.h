@@ -128,6 +128,49 @@ int fn_advance_dev(int32_t *pos, int B, int nt, void *stream);
 int fn_fill_normal_dev(float *p, size_t n, uint64_t seed, float mean, float std, void *stream);
 int fn_copy_dev(void *dst, const void *src, size_t bytes, void *stream);
 
+/* ======================================================================================================
+ * 4. Path engine (new): the reference's Engine + layer_forward + forward (faie2fn.cu:1937-2031, 2370-2490) for
+ *    this path only.  B sequences, nl layers; layer il is attention iff (il + 1) % attn_every == 0
+ *    (faie2fn.cu:76, attn_every = 4; 0 = DeltaNet only).  All state is engine-owned on device 0 and zeroed.
+ *    The projections around the path are not part of this library, so each layer reads its inputs from engine
+ *    buffers the caller fills (fn_path_buffer gives their device addresses) and writes its output to one.
+ *    Once fn_path_init has run, the reference's engine entry points act on this engine: fn_reset zeroes the
+ *    DeltaNet state, conv rings and positions (faie2fn.cu:2703-2717), fn_use_graphs switches hipGraph replay of
+ *    the step (default on), fn_n_past counts steps since reset, fn_dev_gb(0) is the engine's device memory in GB,
+ *    fn_last_ms is the host wall time of the last fn_path_step, fn_free releases everything.
+ * ====================================================================================================== */
+int fn_path_init(int B, int nl, int attn_every, int nkh, int nvh, int nq, int nkv, int max_ctx, int head_map,
+                 int gate_act, int nsplit);
+
+/* Buffer kinds of fn_path_buffer.  DeltaNet layers: S [B][nvh][128][128], conv ring [B][4][C], qkv [B][C],
+ * ab [B][2 nvh], z [B][nvh 128], out [B][nvh 128], conv_w [C][4], dt_bias [nvh], ssm_a [nvh], norm_w [128].
+ * Attention layers: Kc, Vc in the fn_attn_dev layouts, qg [B][nq][2][256], k, v [B][nkv][256], og [B][nq][256],
+ * wq, wk [256].  FN_BUF_POS (any il): the engine's int32 positions [B]. */
+#define FN_BUF_S 0
+#define FN_BUF_CONV_RING 1
+#define FN_BUF_QKV 2
+#define FN_BUF_AB 3
+#define FN_BUF_Z 4
+#define FN_BUF_OUT 5
+#define FN_BUF_CONV_W 6
+#define FN_BUF_DT_BIAS 7
+#define FN_BUF_SSM_A 8
+#define FN_BUF_NORM_W 9
+#define FN_BUF_KC 10
+#define FN_BUF_VC 11
+#define FN_BUF_QG 12
+#define FN_BUF_K 13
+#define FN_BUF_V 14
+#define FN_BUF_OG 15
+#define FN_BUF_WQ 16
+#define FN_BUF_WK 17
+#define FN_BUF_POS 18
+int fn_path_buffer(int il, int kind, void **ptr, size_t *bytes);
+
+/* steps decode steps (one token per sequence each) through all layers, then a stream synchronize; with ms
+ * non-NULL, the HIP-event time per step on the engine's stream is written there. */
+int fn_path_step(int steps, float *ms);
+
 #ifdef __cplusplus
 }
 #endif
