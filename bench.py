@@ -38,6 +38,17 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed PMC passes (FETCH_SIZE and WRITE_SIZE, each
+    scaled by what the counter reads for a plain copy of known size); None when the summary is absent."""
+    path = os.path.join(REPO, "profiles", "k_gdn_fused_b64_traffic.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 class GdnStack:
     """L fused DeltaNet layers of B sequences, every buffer distinct per layer, filled in HBM."""
 
@@ -247,6 +258,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--counters", action="store_true",
+                    help="counter-collection workload only: 3 plain copies of 1 GiB (the calibration kernel) and one "
+                         "eager pass of the config-2 stack (36 dispatches of the fused DeltaNet kernel)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build's path runs on one MI355X (no collectives); "
@@ -257,6 +271,21 @@ def main():
         raise RuntimeError("no HIP device visible")
     stream = hiprt.Stream()
     steps, warmup = max(1, args.steps), max(0, args.warmup)
+    if args.counters:
+        nb = 1 << 30
+        a, b = hiprt.Buf(nb), hiprt.Buf(nb)
+        lib.fill_normal_dev(a.ptr, nb // 4, 1)
+        for _ in range(3):
+            lib.copy_dev(b.ptr, a.ptr, nb, stream.handle)
+        stream.sync()
+        a.free(), b.free()
+        st = GdnStack(lib, 64, 36, seed=2)
+        st.launch(stream, advance=False)
+        stream.sync()
+        st.free()
+        print(json.dumps({"counters_workload": "copy 1 GiB x3 (k_copy), fused DeltaNet B=64 x36 (k_gdn<true>)",
+                          "copy_bytes": nb, "gdn_bytes_per_launch": fn_synth.gdn_block_bytes(64)}))
+        return
 
     # ---- headline: config 2 ----
     B, L = 64, 36
@@ -333,7 +362,7 @@ def main():
                                "(16 k-heads, 32 v-heads, dk=dv=128, conv k=4), one token per step, hipGraph replay",
                    "global_batch": B, "layers": L, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "k_gdn<true> (fused DeltaNet block)", "bytes_per_launch": bytes_layer,
                      "us_per_launch": round(ms_kern * 1e3, 3)},
         "cpu_baseline": cpu,
