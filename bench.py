@@ -328,6 +328,16 @@ def main():
             extra[f"config3_gqa_b{Bq}_ctx{ctx}"] = {"us_per_layer_step": round(ms * 1e3, 2),
                                                    "gbs": round(by / (ms * 1e-3) / 1e9, 1), "nsplit": nsplit}
             log(f"[bench] config 3 B={Bq} ctx={ctx}: {ms * 1e3:.1f} us, {by / (ms * 1e-3) / 1e9:.0f} GB/s")
+        # the host-array hook on the same layer-step (PCIe-inclusive: state, inputs and outputs cross the bus)
+        lay = fn_synth.BlockLayer(B=64, config=2, layer=0)
+        qkv, ab, z = lay.step()
+        S, conv = lay.S0.copy(), lay.conv0.copy()
+        lib.gdn_block(qkv, lay.conv_w, conv, ab, lay.dt_bias, lay.ssm_a, S, z, lay.norm_w, NKH, NVH)
+        t0 = time.perf_counter()
+        lib.gdn_block(qkv, lay.conv_w, conv, ab, lay.dt_bias, lay.ssm_a, S, z, lay.norm_w, NKH, NVH)
+        hook_ms = (time.perf_counter() - t0) * 1e3
+        extra["config2_host_hook_pcie_inclusive"] = {"ms_per_layer_step": round(hook_ms, 2),
+                                                     "gbs": round(fn_synth.gdn_block_bytes(64) / hook_ms / 1e6, 1)}
         ms, nbytes = hybrid_config4(lib, steps, warmup)
         extra["config4_hybrid_b16_ctx32768"] = {"ms_per_step": round(ms, 4), "us_per_token": round(ms * 1e3 / 16, 2),
                                                "tokens_per_s": round(16 * 1e3 / ms, 1), "bytes_per_step": nbytes,
