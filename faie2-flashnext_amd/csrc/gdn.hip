@@ -65,24 +65,42 @@ struct GdnArgs {
     const float *q, *k, *v, *beta, *g;  // core variant inputs
 };
 
-__device__ __forceinline__ float conv_tap(const GdnArgs &a, int b, int t, int C, int c, int j, int P) {
-    // raw input of channel c at position P - j (1 <= j <= 3) for token t of this call
-    if (t - j >= 0) return a.qkv[((size_t) b * a.nt + (t - j)) * C + c];
-    return a.ring_buf[((size_t) b * a.ring + ((P - j) & (a.ring - 1))) * C + c];
+// Causal depthwise conv (kernel 4, weights oldest tap first) + SiLU (faie2fn.cu:1392-1395) of one channel.
+// The raw inputs of the three previous positions ride in registers across the token loop (hist[0] oldest),
+// as the reference keeps them (faie2fn.cu:1378-1398); the ring is read once before the loop and written once after.
+struct ConvChan {
+    float4 w;
+    float hist[3];
+    float x;  // raw input of the current token
+    __device__ __forceinline__ float out() const {
+        float acc = w.x * hist[0];
+        acc = fmaf(w.y, hist[1], acc);
+        acc = fmaf(w.z, hist[2], acc);
+        acc = fmaf(w.w, x, acc);
+        return siluf_(acc);
+    }
+    __device__ __forceinline__ void shift(float next) {
+        hist[0] = hist[1];
+        hist[1] = hist[2];
+        hist[2] = x;
+        x = next;
+    }
+};
+
+__device__ __forceinline__ void conv_load(ConvChan &cc, const GdnArgs &a, const float *ring_b, const float *x_b, int C,
+                                          int c, int pos) {
+    cc.w = reinterpret_cast<const float4 *>(a.conv_w)[c];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) cc.hist[j] = ring_b[(size_t) ((pos - 3 + j) & (a.ring - 1)) * C + c];
+    cc.x = x_b[c];
 }
 
-// causal depthwise conv (kernel 4, weights oldest tap first) + SiLU (faie2fn.cu:1392-1395)
-__device__ __forceinline__ float conv_silu(const GdnArgs &a, int b, int t, int C, int c, int P) {
-    const float4 w = reinterpret_cast<const float4 *>(a.conv_w)[c];
-    const float x0 = a.qkv[((size_t) b * a.nt + t) * C + c];
-    const float x1 = conv_tap(a, b, t, C, c, 1, P);
-    const float x2 = conv_tap(a, b, t, C, c, 2, P);
-    const float x3 = conv_tap(a, b, t, C, c, 3, P);
-    float acc = w.x * x3;
-    acc = fmaf(w.y, x2, acc);
-    acc = fmaf(w.z, x1, acc);
-    acc = fmaf(w.w, x0, acc);
-    return siluf_(acc);
+// after the last token: raw inputs of this call's own last (up to) three positions into their ring slots
+__device__ __forceinline__ void conv_store(const ConvChan &cc, const GdnArgs &a, float *ring_b, int C, int c, int pos) {
+    const int last = pos + a.nt - 1;
+    ring_b[(size_t) (last & (a.ring - 1)) * C + c] = cc.x;
+    if (a.nt >= 2) ring_b[(size_t) ((last - 1) & (a.ring - 1)) * C + c] = cc.hist[2];
+    if (a.nt >= 3) ring_b[(size_t) ((last - 2) & (a.ring - 1)) * C + c] = cc.hist[1];
 }
 
 template <bool FUSED>
@@ -92,32 +110,65 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
     const int bh = blockIdx.x, b = bh / a.nvh, h = bh - b * a.nvh;
     const int kh = a.head_map == 0 ? h % a.nkh : h / (a.nvh / a.nkh);
     const int C = 2 * a.nkh * DK + a.nvh * DV;
+    const bool qk_thr = tid < DK, v_thr = tid >= DK && tid < DK + DV;  // wave-uniform roles
 
     __shared__ float4 qs4[DK / 4], ks4[DK / 4];  // raw q, k of the key head (this token)
     __shared__ float vs[DV];                      // conv'd v of the value head
     __shared__ float4 red[WAVES][2][DV / 4];      // per-wave column partials of kv and sq
     __shared__ float nrm[2][3];                   // per-wave sums q.q, k.k, q.k (waves 0, 1)
 
-    // 1. state tile into registers: issued first, everything below overlaps its latency
+    // 1. every input of the first token is requested before the state tile, so nothing waits behind S twice:
+    //    conv weights, ring taps and raw inputs (waves 0-3), z and the norm weight (wave 0)
+    const int pos = FUSED ? a.pos[b] : 0;
+    const float *x_b = a.qkv + (size_t) b * a.nt * C;
+    float *ring_b = a.ring_buf + (size_t) b * a.ring * C;
+    const int cq = kh * DK + tid, ck = a.nkh * DK + kh * DK + tid, cv = 2 * a.nkh * DK + h * DV + (tid - DK);
+    ConvChan c0{}, c1{};
+    float4 z4 = f4(0.0f), w4 = f4(0.0f);
+    if (FUSED) {
+        if (qk_thr) {
+            conv_load(c0, a, ring_b, x_b, C, cq, pos);
+            conv_load(c1, a, ring_b, x_b, C, ck, pos);
+        } else if (v_thr) {
+            conv_load(c0, a, ring_b, x_b, C, cv, pos);
+        }
+        if (wave == 0 && lane < 32) {
+            z4 = *reinterpret_cast<const float4 *>(a.z + (size_t) b * a.nt * a.nvh * DV + (size_t) h * DV + cg * 4);
+            w4 = reinterpret_cast<const float4 *>(a.norm_w)[cg];
+        }
+    }
+
+    // 2. state tile into registers
     float4 s[ROWS_PT];
     float4 *Sh = reinterpret_cast<float4 *>(a.S + (size_t) bh * DK * DV);
 #pragma unroll
     for (int r = 0; r < ROWS_PT; ++r) s[r] = ld_state(&Sh[(rg * ROWS_PT + r) * (DV / 4) + cg]);
 
-    const int pos = FUSED ? a.pos[b] : 0;
     const float scale = 0.08838834764831845f;  // 1/sqrt(128), faie2fn.cu:1352
 
     for (int t = 0; t < a.nt; ++t) {
         const size_t bt = (size_t) b * a.nt + t;
-        if (t > 0) __syncthreads();  // the previous token's LDS reads are done
+        if (t > 0) {
+            __syncthreads();  // the previous token's LDS reads are done
+            if (FUSED) {
+                const float *xt = x_b + (size_t) t * C;
+                if (qk_thr) {
+                    c0.shift(xt[cq]);
+                    c1.shift(xt[ck]);
+                } else if (v_thr) {
+                    c0.shift(xt[cv]);
+                }
+                if (wave == 0 && lane < 32)
+                    z4 = *reinterpret_cast<const float4 *>(a.z + bt * a.nvh * DV + (size_t) h * DV + cg * 4);
+            }
+        }
 
-        // 2. q, k (waves 0-1, channel i = tid) and v (waves 2-3, channel j = tid - 128)
-        if (tid < DK) {
+        // 3. q, k (waves 0-1, channel i = tid) and v (waves 2-3, channel j = tid - 128)
+        if (qk_thr) {
             float q, k;
             if (FUSED) {
-                const int P = pos + t;
-                q = conv_silu(a, b, t, C, kh * DK + tid, P);
-                k = conv_silu(a, b, t, C, a.nkh * DK + kh * DK + tid, P);
+                q = c0.out();
+                k = c1.out();
             } else {
                 q = a.q[(bt * a.nkh + kh) * DK + tid];
                 k = a.k[(bt * a.nkh + kh) * DK + tid];
@@ -130,15 +181,11 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
                 nrm[wave][1] = skk;
                 nrm[wave][2] = sqk;
             }
-        } else if (tid < DK + DV) {
-            const int j = tid - DK;
-            float vv;
-            if (FUSED) vv = conv_silu(a, b, t, C, 2 * a.nkh * DK + h * DV + j, pos + t);
-            else vv = a.v[(bt * a.nvh + h) * DV + j];
-            vs[j] = vv;
+        } else if (v_thr) {
+            vs[tid - DK] = FUSED ? c0.out() : a.v[(bt * a.nvh + h) * DV + (tid - DK)];
         }
 
-        // 3. gates (uniform per head): beta = sigmoid(b), gamma = exp(ssm_a * softplus(a + dt_bias)), softplus
+        // 4. gates (uniform per head): beta = sigmoid(b), gamma = exp(ssm_a * softplus(a + dt_bias)), softplus
         //    the identity above 20 (faie2fn.cu:1407-1410)
         float beta, gamma;
         if (FUSED) {
@@ -162,7 +209,7 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
         }
         const float kq = sqk * rq * rk;
 
-        // 4. one pass over the registers: column partials of S^T k and S^T q over this thread's 16 rows
+        // 5. one pass over the registers: column partials of S^T k and S^T q over this thread's rows
         float4 kvp = f4(0.0f), sqp = f4(0.0f);
 #pragma unroll
         for (int r4 = 0; r4 < ROWS_PT / 4; ++r4) {
@@ -198,7 +245,7 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
             sq.x += y.x; sq.y += y.y; sq.z += y.z; sq.w += y.w;
         }
 
-        // 5. delta, readout, update.  kv and sq were taken over raw k and q: scale by rk and rq here.
+        // 6. delta, readout, update.  kv and sq were taken over raw k and q: scale by rk and rq here.
         const float4 v4 = reinterpret_cast<const float4 *>(vs)[cg];
         float4 d, o;
         d.x = (v4.x - gamma * (kv.x * rk)) * beta;
@@ -224,7 +271,7 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
             }
         }
 
-        // 6. output: wave 0 holds every column twice (row groups 0 and 1)
+        // 7. output: wave 0 holds every column twice (row groups 0 and 1)
         if (wave == 0) {
             if (FUSED) {
                 // gated RMSNorm on = o * rsqrt(mean o^2 + eps) * w * act(z) (faie2fn.cu:1422-1424); the wave sum
@@ -232,9 +279,6 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
                 const float ss = 0.5f * wave_sum(o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w);
                 const float rn = rsqrtf(ss / DV + a.eps);
                 if (lane < 32) {
-                    const size_t oi = bt * a.nvh * DV + (size_t) h * DV + cg * 4;
-                    const float4 z4 = *reinterpret_cast<const float4 *>(a.z + oi);
-                    const float4 w4 = reinterpret_cast<const float4 *>(a.norm_w)[cg];
                     float4 r;
                     if (a.gate_act == 0) {
                         r.x = o.x * rn * w4.x * sigmoidf_(z4.x);
@@ -247,7 +291,7 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
                         r.z = o.z * rn * w4.z * siluf_(z4.z);
                         r.w = o.w * rn * w4.w * siluf_(z4.w);
                     }
-                    *reinterpret_cast<float4 *>(a.out + oi) = r;
+                    *reinterpret_cast<float4 *>(a.out + bt * a.nvh * DV + (size_t) h * DV + cg * 4) = r;
                 }
             } else if (lane < 32) {
                 *reinterpret_cast<float4 *>(a.out + (bt * a.nvh + h) * DV + cg * 4) = o;
@@ -255,25 +299,19 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
         }
     }
 
-    // 7. write back: state once, conv ring slots of this call's last (up to) three positions
+    // 8. write back: state once; ring slots of this call's last (up to) three positions from the registers.  The
+    //    q/k channels of a key head are written by one of its value heads only.
 #pragma unroll
     for (int r = 0; r < ROWS_PT; ++r) st_state(&Sh[(rg * ROWS_PT + r) * (DV / 4) + cg], s[r]);
     if (FUSED) {
         const bool primary = a.head_map == 0 ? h < a.nkh : (h % (a.nvh / a.nkh)) == 0;
-        for (int t = max(0, a.nt - 3); t < a.nt; ++t) {
-            const int slot = (pos + t) & (a.ring - 1);
-            const float *x = a.qkv + ((size_t) b * a.nt + t) * C;
-            float *dst = a.ring_buf + ((size_t) b * a.ring + slot) * C;
-            if (tid < DK) {
-                if (primary) {
-                    const int cq = kh * DK + tid, ck = a.nkh * DK + kh * DK + tid;
-                    dst[cq] = x[cq];
-                    dst[ck] = x[ck];
-                }
-            } else if (tid < DK + DV) {
-                const int cv = 2 * a.nkh * DK + h * DV + (tid - DK);
-                dst[cv] = x[cv];
+        if (qk_thr) {
+            if (primary) {
+                conv_store(c0, a, ring_b, C, cq, pos);
+                conv_store(c1, a, ring_b, C, ck, pos);
             }
+        } else if (v_thr) {
+            conv_store(c0, a, ring_b, C, cv, pos);
         }
     }
 }
