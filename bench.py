@@ -127,10 +127,10 @@ class AttnStack:
     """GQA decode layers (16 q heads, 2 kv heads, head dim 256, RoPE on 64 dims, theta 1e7) of B sequences at
     context ctx (the new token at pos = ctx - 1), L distinct layers with their own fp32 caches."""
 
-    def __init__(self, lib, B, ctx, L, seed, nq=16, nkv=2):
+    def __init__(self, lib, B, ctx, L, seed, nq=16, nkv=2, nsplit=0):
         self.lib, self.B, self.ctx, self.L, self.nq, self.nkv = lib, B, ctx, L, nq, nkv
         self.max_ctx = (ctx + 63) // 64 * 64
-        self.nsplit = lib.attn_nsplit(B, nkv, 1, ctx)
+        self.nsplit = nsplit or lib.attn_nsplit(B, nkv, 1, ctx)
         self.wb = lib.attn_work_bytes(B, nq, 1, self.nsplit)
         self.pos = hiprt.Buf.like(np.full(B, ctx - 1, np.int32))
         self.work = hiprt.Buf(self.wb)

@@ -11,10 +11,12 @@
 //     key and needs no cross-lane reduction at all.
 //   * V stays row-major; for p.V a lane owns 4 output dims, reads each V row with one coalesced 1 KiB wave load
 //     and takes the GRP probabilities of the key as LDS broadcasts.
-//   * K and V are read with the nontemporal hint and in batches of 16 loads per lane, so every wave keeps
-//     16 KiB in flight (the first version waited on each V row and spent ~40 HBM latencies per tile).
-//   * Each wave runs its own online softmax (running max per head via DPP/permlane wave max); the four waves
-//     merge in LDS and write one (m, l, o[hd]) partial per query head per split.
+//   * The four waves of a workgroup walk each 64-key tile together: each requests a quarter of the tile's K
+//     (16 chunks of every key) and a quarter of its V rows at the start, with the nontemporal hint, so a tile
+//     costs about two load latencies; partial scores meet in LDS, one wave per GRP/4 heads runs the online
+//     softmax (DPP wave max), and every wave accumulates p.V over its rows.  (A first version let each wave walk
+//     whole tiles alone: eight dependent load batches per tile, 36.5 us at B = 1, L = 4K against 18 us now.)
+//   * The workgroup writes one (m, l, o[hd]) partial per query head per split.
 //   * The combine kernel merges the splits with the log-sum-exp identity and applies o / L * sigmoid(gate).
 // Device cache layouts (max_ctx a multiple of 64):
 //   Kc: [B][nkv][max_ctx / 64][hd / 4][64][4]   Vc: [B][nkv][max_ctx][hd]
@@ -31,6 +33,7 @@ constexpr int HD = 256;     // head dim built (the reference's, faie2fn.cu:49)
 constexpr int TILE = 64;    // keys per tile (= wave size)
 constexpr int WAVES = 4;
 constexpr int MAXROT = 128;
+
 
 struct AttnArgs {
     int B, nq, nkv, nt, max_ctx, nsplit, nrot;
@@ -86,144 +89,142 @@ __global__ void __launch_bounds__(HD) k_attn_prep(const AttnArgs a) {
 }
 
 // Split-K attention partials.  grid (nsplit, nkv, B nt), WAVES*64 threads.
-// Each wave walks its tiles; per tile the K reads go out in batches of 16 x 16 bytes per lane and the V rows in
-// batches of 16 coalesced 1 KiB rows, so a wave keeps 16 KiB of loads in flight instead of waiting on each one.
+// The four waves walk one 64-key tile together: wave w reads K chunks 16w..16w+15 of every key (lane = key) and V
+// rows 16w..16w+15 (lane = 4 dims), both requested at the start of the tile; the partial scores meet in LDS; wave w
+// then runs the online softmax of heads w*GRP/4 .. (w+1)*GRP/4 - 1 (lane = key) and publishes p and the rescale
+// factors; each wave accumulates p.V over its 16 rows for all heads.  A tile costs about two load latencies instead
+// of eight, which is what a short context or a small batch is bound by.
 template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
-    constexpr int NB = GRP > 8 ? 8 : 16;            // loads in flight per lane per batch
-    // LDS: q of the group and the per-wave tile probabilities while walking; the per-wave partials for the
-    // merge afterwards (same bytes)
-    constexpr int WALK = HD / 4 * GRP * 16 + WAVES * TILE * GRP * 4, MERGE = WAVES * GRP * HD * 4;
+    constexpr int HPW = GRP / WAVES;                 // softmax heads per wave
+    constexpr int CPW = HD / 4 / WAVES;              // K chunks (of 4 dims) per wave = 16
+    constexpr int RPW = TILE / WAVES;                // V rows per wave = 16
+    static_assert(GRP % WAVES == 0, "heads split evenly over the waves");
+    constexpr int QB = HD / 4 * GRP * 16, SB = WAVES * GRP * TILE * 4, PB = TILE * GRP * 4, CB = GRP * 4;
+    constexpr int MERGE = WAVES * GRP * HD * 4, WALK = QB + SB + PB + CB;
     __shared__ __align__(16) unsigned char smem[WALK > MERGE ? WALK : MERGE];
-    __shared__ float mm[WAVES][GRP], ml[WAVES][GRP];
-    float4 *qs = reinterpret_cast<float4 *>(smem);                                  // [HD/4][GRP]
-    float *pb = reinterpret_cast<float *>(smem + HD / 4 * GRP * 16);                // [WAVES][TILE][GRP]
-    float4 *mo = reinterpret_cast<float4 *>(smem);                                  // [WAVES][GRP][HD/4]
+    __shared__ float mmax[GRP], msum[GRP];
+    float4 *qs = reinterpret_cast<float4 *>(smem);                  // [HD/4][GRP]
+    float *sp = reinterpret_cast<float *>(smem + QB);               // [WAVES][GRP][TILE] partial scores
+    float *pb = reinterpret_cast<float *>(smem + QB + SB);          // [TILE][GRP] probabilities
+    float *cr = reinterpret_cast<float *>(smem + QB + SB + PB);     // [GRP] rescale of this tile
+    float4 *mo = reinterpret_cast<float4 *>(smem);                  // [WAVES][GRP][HD/4] (after the walk)
 
-    const int sp = blockIdx.x, g = blockIdx.y, bt = blockIdx.z, b = bt / a.nt, t = bt - b * a.nt;
+    const int sp_i = blockIdx.x, g = blockIdx.y, bt = blockIdx.z, b = bt / a.nt, t = bt - b * a.nt;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nk = min(a.pos[b] + t + 1, a.max_ctx);  // keys 0 .. nk-1 are visible
+    const int nk = min(a.pos[b] + t + 1, a.max_ctx);
     const int ntiles = (nk + TILE - 1) / TILE;
     const int per = (ntiles + a.nsplit - 1) / a.nsplit;
-    const int tile0 = sp * per, tile1 = min(tile0 + per, ntiles);
-    const float scale = rsqrtf((float) HD);  // 1/16 at HD = 256 (faie2fn.cu:1646)
+    const int tile0 = sp_i * per, tile1 = min(tile0 + per, ntiles);
+    const float scale = rsqrtf((float) HD);
 
     const float4 *Qg = reinterpret_cast<const float4 *>(a.Q + ((size_t) bt * a.nkv + g) * HD * GRP);
     for (int i = threadIdx.x; i < HD / 4 * GRP; i += WAVES * 64) qs[i] = Qg[i];
-    __syncthreads();
     const float *Kbase = a.Kc + ((size_t) b * a.nkv + g) * a.max_ctx * HD;
     const float4 *Vbase = reinterpret_cast<const float4 *>(a.Vc + ((size_t) b * a.nkv + g) * a.max_ctx * HD);
-    float *pw = pb + wave * TILE * GRP;
 
-    float m[GRP], l[GRP];
+    float m[HPW], l[HPW];  // softmax state of this wave's heads (wave-uniform m, per-lane partial l)
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+        m[i] = -INFINITY;
+        l[i] = 0.0f;
+    }
     float4 o[GRP];
 #pragma unroll
-    for (int hh = 0; hh < GRP; ++hh) {
-        m[hh] = -INFINITY;
-        l[hh] = 0.0f;
-        o[hh] = f4(0.0f);
-    }
+    for (int hh = 0; hh < GRP; ++hh) o[hh] = f4(0.0f);
+    __syncthreads();
 
-    for (int tile = tile0 + wave; tile < tile1; tile += WAVES) {
+    for (int tile = tile0; tile < tile1; ++tile) {
         const int key0 = tile * TILE;
-        const bool valid = key0 + lane < nk;
-        // scores: lane = key; K read as 16-byte chunks of the key-tiled layout (coalesced 1 KiB per wave load),
-        // q as LDS broadcasts
         const float4 *Kt = reinterpret_cast<const float4 *>(Kbase + (size_t) tile * TILE * HD);
+        float4 kf[CPW], vf[RPW];
+#pragma unroll
+        for (int u = 0; u < CPW; ++u) kf[u] = ld_nt(&Kt[(wave * CPW + u) * TILE + lane]);
+#pragma unroll
+        for (int u = 0; u < RPW; ++u) {
+            const int row = min(key0 + wave * RPW + u, nk - 1);  // clamp past the last key: finite, weight 0
+            vf[u] = ld_nt(&Vbase[(size_t) row * (HD / 4) + lane]);
+        }
         float s[GRP];
 #pragma unroll
         for (int hh = 0; hh < GRP; ++hh) s[hh] = 0.0f;
-        for (int cb = 0; cb < HD / 4; cb += NB) {
-            float4 kf[NB];
 #pragma unroll
-            for (int u = 0; u < NB; ++u) kf[u] = ld_nt(&Kt[(cb + u) * TILE + lane]);
+        for (int u = 0; u < CPW; ++u) {
 #pragma unroll
-            for (int u = 0; u < NB; ++u) {
-#pragma unroll
-                for (int hh = 0; hh < GRP; ++hh) {
-                    const float4 qv = qs[(cb + u) * GRP + hh];
-                    s[hh] = fmaf(qv.x, kf[u].x, s[hh]);
-                    s[hh] = fmaf(qv.y, kf[u].y, s[hh]);
-                    s[hh] = fmaf(qv.z, kf[u].z, s[hh]);
-                    s[hh] = fmaf(qv.w, kf[u].w, s[hh]);
-                }
+            for (int hh = 0; hh < GRP; ++hh) {
+                const float4 qv = qs[(wave * CPW + u) * GRP + hh];
+                s[hh] = fmaf(qv.x, kf[u].x, s[hh]);
+                s[hh] = fmaf(qv.y, kf[u].y, s[hh]);
+                s[hh] = fmaf(qv.z, kf[u].z, s[hh]);
+                s[hh] = fmaf(qv.w, kf[u].w, s[hh]);
             }
         }
-        // online softmax update (faie2fn.cu:1648-1663), one running max per head per wave
+#pragma unroll
+        for (int hh = 0; hh < GRP; ++hh) sp[(wave * GRP + hh) * TILE + lane] = s[hh];
+        __syncthreads();
+        // online softmax of this wave's heads over the tile's keys (lane = key)
+        const bool valid = key0 + lane < nk;
+#pragma unroll
+        for (int i = 0; i < HPW; ++i) {
+            const int hh = wave * HPW + i;
+            float sc = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) sc += sp[(w * GRP + hh) * TILE + lane];
+            sc = valid ? sc * scale : -INFINITY;
+            const float mn = fmaxf(m[i], wave_max(sc));  // finite: the tile holds >= 1 visible key
+            const float corr = expf(m[i] - mn);           // 0 while m is -inf
+            const float pr = valid ? expf(sc - mn) : 0.0f;
+            l[i] = fmaf(l[i], corr, pr);
+            m[i] = mn;
+            pb[lane * GRP + hh] = pr;
+            if (lane == 0) cr[hh] = corr;
+        }
+        __syncthreads();
+        // p.V over this wave's 16 rows, every head
 #pragma unroll
         for (int hh = 0; hh < GRP; ++hh) {
-            const float sc = valid ? s[hh] * scale : -INFINITY;
-            const float mn = fmaxf(m[hh], wave_max(sc));  // finite: the tile holds >= 1 visible key
-            const float corr = expf(m[hh] - mn);           // 0 while m is -inf
-            const float pr = valid ? expf(sc - mn) : 0.0f;
-            l[hh] = fmaf(l[hh], corr, pr);
-            o[hh].x *= corr; o[hh].y *= corr; o[hh].z *= corr; o[hh].w *= corr;
-            m[hh] = mn;
-            pw[lane * GRP + hh] = pr;
+            const float c = cr[hh];
+            o[hh].x *= c; o[hh].y *= c; o[hh].z *= c; o[hh].w *= c;
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // p.V: lane = 4 output dims, one coalesced V row per key.  Rows past the last visible key are clamped to
-        // it (finite data, probability 0) so a batch never branches per key.
-        const int nj = min(TILE, nk - key0);
-        for (int jb = 0; jb < nj; jb += NB) {
-            float4 vf[NB];
 #pragma unroll
-            for (int u = 0; u < NB; ++u) {
-                const int row = min(key0 + jb + u, nk - 1);
-                vf[u] = ld_nt(&Vbase[(size_t) row * (HD / 4) + lane]);
-            }
+        for (int u = 0; u < RPW; ++u) {
+            const float *pj = pb + (wave * RPW + u) * GRP;
 #pragma unroll
-            for (int u = 0; u < NB; ++u) {
-                const float *pj = pw + (jb + u) * GRP;
-#pragma unroll
-                for (int hh = 0; hh < GRP; ++hh) {
-                    const float pr = pj[hh];
-                    o[hh].x = fmaf(pr, vf[u].x, o[hh].x);
-                    o[hh].y = fmaf(pr, vf[u].y, o[hh].y);
-                    o[hh].z = fmaf(pr, vf[u].z, o[hh].z);
-                    o[hh].w = fmaf(pr, vf[u].w, o[hh].w);
-                }
+            for (int hh = 0; hh < GRP; ++hh) {
+                const float pr = pj[hh];
+                o[hh].x = fmaf(pr, vf[u].x, o[hh].x);
+                o[hh].y = fmaf(pr, vf[u].y, o[hh].y);
+                o[hh].z = fmaf(pr, vf[u].z, o[hh].z);
+                o[hh].w = fmaf(pr, vf[u].w, o[hh].w);
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 
-    // merge the waves (the walk's LDS is reused for the per-wave partials)
-    __syncthreads();
+    // all waves share each head's running max, so their o sum without rescaling
 #pragma unroll
-    for (int hh = 0; hh < GRP; ++hh) {
-        const float lw = wave_sum(l[hh]);
+    for (int i = 0; i < HPW; ++i) {
+        const float lw = wave_sum(l[i]);
         if (lane == 0) {
-            mm[wave][hh] = m[hh];
-            ml[wave][hh] = lw;
+            mmax[wave * HPW + i] = m[i];
+            msum[wave * HPW + i] = lw;
         }
-        mo[(wave * GRP + hh) * (HD / 4) + lane] = o[hh];
     }
+    __syncthreads();  // the walk's LDS is free
+#pragma unroll
+    for (int hh = 0; hh < GRP; ++hh) mo[(wave * GRP + hh) * (HD / 4) + lane] = o[hh];
     __syncthreads();
-    const int d = threadIdx.x;  // WAVES * 64 == HD
+    const int d = threadIdx.x;
     const float *mof = reinterpret_cast<const float *>(mo);
 #pragma unroll
     for (int hh = 0; hh < GRP; ++hh) {
-        float M = -INFINITY;
+        float O = 0.0f;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) M = fmaxf(M, mm[w][hh]);
-        float L = 0.0f, O = 0.0f;
-        if (M != -INFINITY) {
-#pragma unroll
-            for (int w = 0; w < WAVES; ++w) {
-                const float e = expf(mm[w][hh] - M);  // 0 for an idle wave
-                L = fmaf(e, ml[w][hh], L);
-                O = fmaf(e, mof[(w * GRP + hh) * HD + d], O);
-            }
-        }
-        const size_t pi = ((size_t) bt * a.nq + g * GRP + hh) * a.nsplit + sp;
-        a.part_o[pi * HD + d] = O;
+        for (int w = 0; w < WAVES; ++w) O += mof[(w * GRP + hh) * HD + d];
+        const size_t pi = ((size_t) bt * a.nq + g * GRP + hh) * a.nsplit + sp_i;
+        const bool empty = tile0 >= tile1;
+        a.part_o[pi * HD + d] = empty ? 0.0f : O;
         if (d == 0) {
-            a.part_ml[pi * 2] = M;
-            a.part_ml[pi * 2 + 1] = L;
+            a.part_ml[pi * 2] = empty ? -INFINITY : mmax[hh];
+            a.part_ml[pi * 2 + 1] = empty ? 0.0f : msum[hh];
         }
     }
 }
@@ -301,12 +302,16 @@ size_t attn_work_bytes(int B, int nq, int nt, int hd, int nsplit) {
     return (q + po + pm) * sizeof(float) + 256;
 }
 
+// About 512 workgroups in all (two per CU at the split kernel's occupancy); a context of 256 tiles or more keeps at
+// least 4 tiles per workgroup (fewer, larger splits: less partial traffic for the combine), a shorter one goes as
+// wide as one tile per workgroup (latency-bound).  Measured on MI355X (B, L -> best nsplit): 1, 4K -> 64;
+// 1, 32K -> 128; 1, 128K -> 256; 16, 32K -> 16.
 int attn_pick_nsplit(int B, int nkv, int nt, int ctx) {
     const int tiles = std::max(1, (ctx + TILE - 1) / TILE);
-    const int most = std::max(1, (tiles + WAVES - 1) / WAVES);  // at least one tile per wave
     const long groups = std::max(1L, (long) B * nt * nkv);
-    const int want = (int) std::max(1L, (1024 + groups - 1) / groups);
-    return std::min(want, most);
+    long want = std::max(1L, (512 + groups - 1) / groups);
+    if (tiles >= 256) want = std::min<long>(want, tiles / 4);
+    return (int) std::max(1L, std::min<long>(want, tiles));
 }
 
 int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
@@ -333,10 +338,11 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
         a.inv_freq[i] = (float) (1.0 / std::pow((double) p.theta, (double) (2 * i) / p.nrot));
     if (bt > 65535u * 65535u) FN_FAIL("attn: batch too large");
     hipLaunchKernelGGL(k_attn_prep, dim3((unsigned) bt, p.nq + p.nkv), dim3(HD), 0, st, a);
+    const dim3 sg(p.nsplit, p.nkv, (unsigned) bt), sb(WAVES * 64);
     switch (grp) {
-        case 8: hipLaunchKernelGGL(k_attn_split<8>, dim3(p.nsplit, p.nkv, (unsigned) bt), dim3(WAVES * 64), 0, st, a); break;
-        case 12: hipLaunchKernelGGL(k_attn_split<12>, dim3(p.nsplit, p.nkv, (unsigned) bt), dim3(WAVES * 64), 0, st, a); break;
-        case 4: hipLaunchKernelGGL(k_attn_split<4>, dim3(p.nsplit, p.nkv, (unsigned) bt), dim3(WAVES * 64), 0, st, a); break;
+        case 8: hipLaunchKernelGGL(k_attn_split<8>, sg, sb, 0, st, a); break;
+        case 12: hipLaunchKernelGGL(k_attn_split<12>, sg, sb, 0, st, a); break;
+        case 4: hipLaunchKernelGGL(k_attn_split<4>, sg, sb, 0, st, a); break;
         default: FN_FAIL("attn: query heads per kv head must be 4, 8 or 12");
     }
     hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(CW * 64), 0, st, a);

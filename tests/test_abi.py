@@ -90,10 +90,11 @@ def test_validation_before_device_work(fnlib):
 
 
 def test_attn_split_heuristic_and_workspace(fnlib):
-    # one tile per wave at least, about 1024 workgroups in total
-    assert fnlib.attn_nsplit(1, 2, 1, 131072) == 512
-    assert fnlib.attn_nsplit(16, 2, 1, 32768) == 32
-    assert fnlib.attn_nsplit(1, 2, 1, 4096) == 16
+    # about 512 workgroups; long contexts keep >= 4 tiles per workgroup, short ones go one tile wide
+    assert fnlib.attn_nsplit(1, 2, 1, 131072) == 256
+    assert fnlib.attn_nsplit(1, 2, 1, 32768) == 128
+    assert fnlib.attn_nsplit(16, 2, 1, 32768) == 16
+    assert fnlib.attn_nsplit(1, 2, 1, 4096) == 64
     assert fnlib.attn_nsplit(1, 2, 1, 1) == 1
     for B, nq, nt, ns in ((1, 16, 1, 512), (16, 16, 1, 32), (2, 24, 3, 7)):
         wb = fnlib.attn_work_bytes(B, nq, nt, ns)
