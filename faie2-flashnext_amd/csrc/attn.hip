@@ -94,7 +94,44 @@ __global__ void __launch_bounds__(HD) k_attn_prep(const AttnArgs a) {
 // then runs the online softmax of heads w*GRP/4 .. (w+1)*GRP/4 - 1 (lane = key) and publishes p and the rescale
 // factors; each wave accumulates p.V over its 16 rows for all heads.  A tile costs about two load latencies instead
 // of eight, which is what a short context or a small batch is bound by.
-template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
+// RMSNorm of a 256-long row held as one float4 per lane (lane = dims 4l..4l+3): x * rsqrt(mean x^2 + eps) * w
+// (faie2fn.cu:1466-1467).  Call from wave-uniform control flow.
+__device__ __forceinline__ float4 rms_row(float4 x, float4 w, float eps) {
+    const float ss = wave_sum(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
+    const float r = rsqrtf(ss / HD + eps);
+    return make_float4(x.x * r * w.x, x.y * r * w.y, x.z * r * w.z, x.w * r * w.w);
+}
+
+// RoPE in place on a row stored in LDS as float4 chunks with stride `stride` (chunk c of the row at row4[c *
+// stride]): dims d < nrot, pairs (i, i + nrot/2) (faie2fn.cu:1438-1445, 1470-1474), with cos/sin of the fp32 angle
+// (float)P * inv_freq[i] taken from cs/sn.  One wave, lane = chunk; every read happens before any write.
+__device__ __forceinline__ void rope_row_lds(float4 *row4, int stride, int lane, int nrot, const float *cs,
+                                             const float *sn) {
+    const float *row = reinterpret_cast<const float *>(row4);
+    const int half = nrot / 2;
+    float y[4];
+    const bool act = 4 * lane < nrot;
+    if (act) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int d = 4 * lane + e, i = d < half ? d : d - half;
+            const float x0 = row[(i / 4) * stride * 4 + (i % 4)], x1 = row[((i + half) / 4) * stride * 4 + ((i + half) % 4)];
+            y[e] = d < half ? x0 * cs[i] - x1 * sn[i] : x1 * cs[i] + x0 * sn[i];
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (act) row4[lane * stride] = make_float4(y[0], y[1], y[2], y[3]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// PREP (one new token per sequence): the workgroup also does k_attn_prep's work for its group -- RMSNorm + RoPE of
+// its GRP query heads into LDS, and, in the workgroup whose split holds the new position, of the new key, which it
+// appends with the new value to the caches before its first tile load.
+template <int GRP, bool PREP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
     constexpr int HPW = GRP / WAVES;                 // softmax heads per wave
     constexpr int CPW = HD / 4 / WAVES;              // K chunks (of 4 dims) per wave = 16
     constexpr int RPW = TILE / WAVES;                // V rows per wave = 16
@@ -108,17 +145,47 @@ template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(co
     float *pb = reinterpret_cast<float *>(smem + QB + SB);          // [TILE][GRP] probabilities
     float *cr = reinterpret_cast<float *>(smem + QB + SB + PB);     // [GRP] rescale of this tile
     float4 *mo = reinterpret_cast<float4 *>(smem);                  // [WAVES][GRP][HD/4] (after the walk)
+    __shared__ float4 kn4[HD / 4], vn4[HD / 4];                      // new key and value (PREP)
+    __shared__ float rcs[MAXROT / 2], rsn[MAXROT / 2];                // cos / sin of the RoPE angles (PREP)
 
     const int sp_i = blockIdx.x, g = blockIdx.y, bt = blockIdx.z, b = bt / a.nt, t = bt - b * a.nt;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nk = min(a.pos[b] + t + 1, a.max_ctx);
+    const int P = a.pos[b] + t;
+    const int nk = min(P + 1, a.max_ctx);
     const int ntiles = (nk + TILE - 1) / TILE;
     const int per = (ntiles + a.nsplit - 1) / a.nsplit;
     const int tile0 = sp_i * per, tile1 = min(tile0 + per, ntiles);
     const float scale = rsqrtf((float) HD);
+    // the new key is visible (inside the cache) and falls in this split's tiles
+    const bool owner = PREP && P >= 0 && P < a.max_ctx && P / TILE >= tile0 && P / TILE < tile1;
 
-    const float4 *Qg = reinterpret_cast<const float4 *>(a.Q + ((size_t) bt * a.nkv + g) * HD * GRP);
-    for (int i = threadIdx.x; i < HD / 4 * GRP; i += WAVES * 64) qs[i] = Qg[i];
+    if (PREP) {
+        if (threadIdx.x < a.nrot / 2) {
+            const float ang = (float) P * a.inv_freq[threadIdx.x];  // fp32 angle (faie2fn.cu:1440)
+            rcs[threadIdx.x] = cosf(ang);
+            rsn[threadIdx.x] = sinf(ang);
+        }
+        const float4 wq = reinterpret_cast<const float4 *>(a.wq)[lane];
+#pragma unroll
+        for (int i = 0; i < HPW; ++i) {
+            const int hh = wave * HPW + i;
+            const float4 x = reinterpret_cast<const float4 *>(a.qg + ((size_t) bt * a.nq + g * GRP + hh) * 2 * HD)[lane];
+            qs[lane * GRP + hh] = rms_row(x, wq, a.eps);
+        }
+        if (owner && wave == 0) {
+            const size_t kv = ((size_t) bt * a.nkv + g) * HD;
+            kn4[lane] = rms_row(reinterpret_cast<const float4 *>(a.knew + kv)[lane],
+                                reinterpret_cast<const float4 *>(a.wk)[lane], a.eps);
+            vn4[lane] = reinterpret_cast<const float4 *>(a.vnew + kv)[lane];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < HPW; ++i) rope_row_lds(qs + wave * HPW + i, GRP, lane, a.nrot, rcs, rsn);
+        if (owner && wave == 0) rope_row_lds(kn4, 1, lane, a.nrot, rcs, rsn);
+    } else {
+        const float4 *Qg = reinterpret_cast<const float4 *>(a.Q + ((size_t) bt * a.nkv + g) * HD * GRP);
+        for (int i = threadIdx.x; i < HD / 4 * GRP; i += WAVES * 64) qs[i] = Qg[i];
+    }
     const float *Kbase = a.Kc + ((size_t) b * a.nkv + g) * a.max_ctx * HD;
     const float4 *Vbase = reinterpret_cast<const float4 *>(a.Vc + ((size_t) b * a.nkv + g) * a.max_ctx * HD);
 
@@ -131,6 +198,15 @@ template <int GRP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(co
     float4 o[GRP];
 #pragma unroll
     for (int hh = 0; hh < GRP; ++hh) o[hh] = f4(0.0f);
+    if (owner && wave == 0) {
+        // append the new row to the caches; the barrier below orders these stores before every wave's tile loads,
+        // so the new key is read back like any other
+        const float4 k = kn4[lane];
+        const float kk[4] = {k.x, k.y, k.z, k.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a.Kc[k_index(a.max_ctx, b, a.nkv, g, P, 4 * lane + e)] = kk[e];
+        reinterpret_cast<float4 *>(a.Vc + (((size_t) b * a.nkv + g) * a.max_ctx + P) * HD)[lane] = vn4[lane];
+    }
     __syncthreads();
 
     for (int tile = tile0; tile < tile1; ++tile) {
@@ -337,13 +413,20 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
     for (int i = 0; i < p.nrot / 2; ++i)
         a.inv_freq[i] = (float) (1.0 / std::pow((double) p.theta, (double) (2 * i) / p.nrot));
     if (bt > 65535u * 65535u) FN_FAIL("attn: batch too large");
-    hipLaunchKernelGGL(k_attn_prep, dim3((unsigned) bt, p.nq + p.nkv), dim3(HD), 0, st, a);
     const dim3 sg(p.nsplit, p.nkv, (unsigned) bt), sb(WAVES * 64);
-    switch (grp) {
-        case 8: hipLaunchKernelGGL(k_attn_split<8>, sg, sb, 0, st, a); break;
-        case 12: hipLaunchKernelGGL(k_attn_split<12>, sg, sb, 0, st, a); break;
-        case 4: hipLaunchKernelGGL(k_attn_split<4>, sg, sb, 0, st, a); break;
-        default: FN_FAIL("attn: query heads per kv head must be 4, 8 or 12");
+    if (grp != 4 && grp != 8 && grp != 12) FN_FAIL("attn: query heads per kv head must be 4, 8 or 12");
+    // one new token per sequence: the split kernel does the norm/RoPE/append itself (one launch fewer); several
+    // tokens see each other's new keys, so they go through k_attn_prep first
+    const bool fused = p.nt == 1;
+    if (!fused) hipLaunchKernelGGL(k_attn_prep, dim3((unsigned) bt, p.nq + p.nkv), dim3(HD), 0, st, a);
+    if (fused) {
+        if (grp == 8) hipLaunchKernelGGL((k_attn_split<8, true>), sg, sb, 0, st, a);
+        else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, true>), sg, sb, 0, st, a);
+        else hipLaunchKernelGGL((k_attn_split<4, true>), sg, sb, 0, st, a);
+    } else {
+        if (grp == 8) hipLaunchKernelGGL((k_attn_split<8, false>), sg, sb, 0, st, a);
+        else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, false>), sg, sb, 0, st, a);
+        else hipLaunchKernelGGL((k_attn_split<4, false>), sg, sb, 0, st, a);
     }
     hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(CW * 64), 0, st, a);
     FN_CK(hipGetLastError());
