@@ -163,6 +163,50 @@ class AttnStack:
         self.work.free()
 
 
+class QsaStack:
+    """The reference's sparse attention layer (indexer top 512 blocks of 4) at context ctx: L distinct layers with
+    their own K/V caches, raw index keys and block keys (built from the raw keys before timing)."""
+
+    def __init__(self, lib, B, ctx, L, seed, nq=16, nkv=2, top=512):
+        self.lib, self.B, self.ctx, self.L, self.nq, self.nkv, self.top = lib, B, ctx, L, nq, nkv, top
+        self.max_ctx = (ctx + 255) // 256 * 256
+        self.nsplit = lib.attn_nsplit(B, nkv, 1, 4 * top + 4)
+        self.wb = lib.attn_qsa_work_bytes(B, nq, 1, self.nsplit, self.max_ctx, top)
+        self.pos = hiprt.Buf.like(np.full(B, ctx - 1, np.int32))
+        self.work = hiprt.Buf(self.wb)
+        self.layers = []
+        rng = np.random.default_rng(seed)
+        for il in range(L):
+            cache = B * nkv * self.max_ctx * 256
+            d = {"K": hiprt.Buf.empty((cache,)), "V": hiprt.Buf.empty((cache,)),
+                 "IK": hiprt.Buf.empty((B * self.max_ctx * 128,)), "BK": hiprt.Buf.empty((B * self.max_ctx // 4 * 128,)),
+                 "qg": hiprt.Buf.empty((B, 1, nq, 2, 256)), "k": hiprt.Buf.empty((B, 1, nkv, 256)),
+                 "v": hiprt.Buf.empty((B, 1, nkv, 256)), "iqk": hiprt.Buf.empty((B, 1, 640)),
+                 "og": hiprt.Buf.empty((B, 1, nq, 256))}
+            for name, n in (("wq", 256), ("wk", 256), ("wqn", 128), ("wkn", 128)):
+                d[name] = hiprt.Buf.like(rng.normal(1.0, 0.1, n).astype(np.float32))
+            s = seed * 7727 + il * 37
+            for i, key in enumerate(("K", "V", "IK", "qg", "k", "v", "iqk")):
+                lib.fill_normal_dev(d[key].ptr, d[key].nbytes // 4, s + i)
+            lib.ix_blocks_dev(B, self.max_ctx, 0, (ctx - 1) // 4, d["IK"].ptr, d["wkn"].ptr, d["BK"].ptr)
+            self.layers.append(d)
+        hiprt.sync()
+
+    def launch(self, stream):
+        for d in self.layers:
+            self.lib.attn_qsa_dev(self.B, self.nq, self.nkv, 1, self.max_ctx, self.pos.ptr, d["qg"].ptr, d["k"].ptr,
+                                  d["v"].ptr, d["wq"].ptr, d["wk"].ptr, d["K"].ptr, d["V"].ptr, d["iqk"].ptr,
+                                  d["wqn"].ptr, d["wkn"].ptr, d["IK"].ptr, d["BK"].ptr, self.top, self.nsplit,
+                                  self.work.ptr, self.wb, d["og"].ptr, stream.handle)
+
+    def free(self):
+        for d in self.layers:
+            for b in d.values():
+                b.free()
+        self.pos.free()
+        self.work.free()
+
+
 def hybrid_config4(lib, steps, warmup, B=16, ctx=32768, nl=48):
     """Config 4 through the native path engine: 48 layers, attention iff (il + 1) % 4 == 0 (36 DeltaNet + 12 GQA),
     B = 16, every sequence at context ctx (the first new token at position ctx - 1; the context grows by one per
@@ -328,6 +372,15 @@ def main():
             extra[f"config3_gqa_b{Bq}_ctx{ctx}"] = {"us_per_layer_step": round(ms * 1e3, 2),
                                                    "gbs": round(by / (ms * 1e-3) / 1e9, 1), "nsplit": nsplit}
             log(f"[bench] config 3 B={Bq} ctx={ctx}: {ms * 1e3:.1f} us, {by / (ms * 1e-3) / 1e9:.0f} GB/s")
+        # config 3 through the reference's own attention: QSA indexer active past 2048 keys (top 512 blocks of 4)
+        for Bq, ctx, nl in ((1, 32768, 8), (1, 131072, 4), (16, 32768, 2)):
+            qs = QsaStack(lib, Bq, ctx, nl, seed=5)
+            ms = time_graph(stream, lambda: qs.launch(stream), steps, warmup) / nl
+            qs.free()
+            by = fn_synth.attn_qsa_bytes(Bq, ctx)
+            extra[f"config3_qsa_b{Bq}_ctx{ctx}"] = {"us_per_layer_step": round(ms * 1e3, 2), "algorithmic_bytes": by,
+                                                   "gbs": round(by / (ms * 1e-3) / 1e9, 1)}
+            log(f"[bench] config 3 QSA B={Bq} ctx={ctx}: {ms * 1e3:.1f} us")
         # the host-array hook on the same layer-step (PCIe-inclusive: state, inputs and outputs cross the bus)
         lay = fn_synth.BlockLayer(B=64, config=2, layer=0)
         qkv, ab, z = lay.step()

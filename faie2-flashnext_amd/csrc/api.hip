@@ -5,6 +5,7 @@
 // decode-attention path.  Sections 2 and 3 are this path's hooks: host arrays in / out (synchronous, device 0,
 // the reference's unit-test-hook style, faie2fn.cu:2745) and the device-buffer entry points an engine calls.
 #include "engine.h"
+#include "qsa.h"
 
 #include <cstring>
 #include <vector>
@@ -139,6 +140,29 @@ FN_API int fn_copy_dev(void *dst, const void *src, size_t bytes, void *stream) {
     return fn::copy_launch(dst, src, bytes, (hipStream_t) stream);
 }
 
+FN_API size_t fn_attn_qsa_work_bytes(int B, int nq, int nt, int hd, int nsplit, int max_ctx, int top) {
+    if (B < 1 || nq < 1 || nt < 1 || hd < 1 || nsplit < 1 || max_ctx < 1 || top < 1) return 0;
+    return fn::attn_qsa_work_bytes(B, nq, nt, hd, nsplit, max_ctx, top) + 256;
+}
+
+FN_API int fn_attn_qsa_dev(int B, int nq, int nkv, int hd, int nrot, float theta, float eps, int nt, int max_ctx,
+                           const int32_t *pos, const float *qg, const float *k, const float *v, const float *wq,
+                           const float *wk, float *Kc, float *Vc, const float *iqk, const float *wqn, const float *wkn,
+                           float *IKc, float *BKc, int top, int nsplit, float *work, size_t work_bytes, float *og,
+                           void *stream) {
+    fn::AttnDecode p{B, nq, nkv, hd, nrot, nt, max_ctx, nsplit, theta, eps, pos, qg, k, v, wq, wk, Kc, Vc, work,
+                     work_bytes, og};
+    fn::QsaIndexer ix{B, nt, max_ctx, top, nrot, theta, eps, pos, iqk, wqn, wkn, IKc, BKc};
+    return fn::attn_qsa_launch(p, ix, (hipStream_t) stream);
+}
+
+FN_API int fn_ix_blocks_dev(int B, int max_ctx, int j0, int j1, const float *IKc, const float *wkn, float *BKc,
+                            int nrot, float theta, float eps, void *stream) {
+    fn::QsaIndexer ix{B, 1, max_ctx, 512, nrot, theta, eps, nullptr, nullptr, nullptr, wkn, const_cast<float *>(IKc),
+                      BKc};
+    return fn::qsa_blocks_launch(ix, j0, j1, (hipStream_t) stream);
+}
+
 // ---------------------------------------------------------------------------------------------
 // 4. path engine
 
@@ -265,5 +289,100 @@ FN_API int fn_test_attn(int B, int nq, int nkv, int hd, int nrot, float theta, f
                 for (int c = 0; c < hd / 4; ++c) std::memcpy(kd + c * 4, kt + (size_t) c * 256, 16);
                 std::memcpy(vd, &vh[(((size_t) b * nkv + g) * mc + p) * hd], (size_t) hd * 4);
             }
+    return 0;
+}
+
+FN_API int fn_test_attn_qsa(int B, int nq, int nkv, int hd, int nrot, float theta, float eps, int nt, int max_ctx,
+                            const int32_t *pos, const float *qg, const float *k, const float *v, const float *wq,
+                            const float *wk, float *Kc, float *Vc, const float *iqk, const float *wqn, const float *wkn,
+                            float *IKc, int top, int nsplit, float *og, float *scores, uint8_t *mask) {
+    constexpr int IXD = 128, IXR = 4;
+    if (B < 1 || nq < 1 || nkv < 1 || hd < 1 || nt < 1 || max_ctx < 1 || top < 1) FN_FAIL("attn_qsa: bad shape");
+    if (!pos || !qg || !k || !v || !wq || !wk || !Kc || !Vc || !iqk || !wqn || !wkn || !IKc || !og)
+        FN_FAIL("attn_qsa: null pointer");
+    int minpos = max_ctx, maxpos = 0;
+    for (int b = 0; b < B; ++b) {
+        if (pos[b] < 0 || pos[b] + nt > max_ctx) FN_FAIL("attn_qsa: pos[b] + nt must lie in [0, max_ctx]");
+        minpos = std::min(minpos, pos[b]);
+        maxpos = std::max(maxpos, pos[b]);
+    }
+    if (use_device0()) return -1;
+    const int mc = (max_ctx + 255) / 256 * 256;
+    if (nsplit <= 0) nsplit = fn::attn_pick_nsplit(B, nkv, nt, top * IXR + IXR);  // split the attended keys
+    // K/V to the device layouts (rows < pos[b]), raw index keys as they are
+    const size_t per = (size_t) nkv * mc * hd;
+    std::vector<float> kh((size_t) B * per, 0.0f), vh((size_t) B * per, 0.0f), ikh((size_t) B * mc * IXD, 0.0f);
+    for (int b = 0; b < B; ++b) {
+        for (int p = 0; p < pos[b]; ++p)
+            for (int g = 0; g < nkv; ++g) {
+                const float *ks = Kc + (((size_t) b * max_ctx + p) * nkv + g) * hd;
+                const float *vs = Vc + (((size_t) b * max_ctx + p) * nkv + g) * hd;
+                float *kt = &kh[(((size_t) b * nkv + g) * (mc / 64) + p / 64) * 64 * hd + (size_t) (p % 64) * 4];
+                for (int c = 0; c < hd / 4; ++c) std::memcpy(kt + (size_t) c * 256, ks + c * 4, 16);
+                std::memcpy(&vh[(((size_t) b * nkv + g) * mc + p) * hd], vs, (size_t) hd * 4);
+            }
+        std::memcpy(&ikh[(size_t) b * mc * IXD], IKc + (size_t) b * max_ctx * IXD, (size_t) pos[b] * IXD * 4);
+    }
+    const size_t nqg = (size_t) B * nt * nq * 2 * hd, nkvn = (size_t) B * nt * nkv * hd, nog = (size_t) B * nt * nq * hd;
+    const size_t niqk = (size_t) B * nt * (4 * IXD + IXD), nbk = (size_t) B * (mc / IXR) * IXD;
+    const size_t wb = fn_attn_qsa_work_bytes(B, nq, nt, hd, nsplit, mc, top);
+    DevBufs m;
+    int32_t *dpos;
+    float *dqg, *dk_, *dv_, *dwq, *dwk, *dK, *dV, *dwork, *dog, *diqk, *dwqn, *dwkn, *dIK, *dBK;
+    if (m.up(&dpos, pos, B) || m.up(&dqg, qg, nqg) || m.up(&dk_, k, nkvn) || m.up(&dv_, v, nkvn) ||
+        m.up(&dwq, wq, hd) || m.up(&dwk, wk, hd) || m.up(&dK, kh.data(), kh.size()) || m.up(&dV, vh.data(), vh.size()) ||
+        m.alloc(&dwork, wb / 4 + 1) || m.alloc(&dog, nog) || m.up(&diqk, iqk, niqk) || m.up(&dwqn, wqn, IXD) ||
+        m.up(&dwkn, wkn, IXD) || m.up(&dIK, ikh.data(), ikh.size()) || m.alloc(&dBK, nbk))
+        return -1;
+    FN_CK(hipMemset(dwork, 0, wb));
+    // block keys complete before this call (the shortest sequence's; longer ones are rebuilt per sequence below)
+    for (int b = 0; b < B; ++b) {
+        fn::QsaIndexer one{1, 1, mc, top, nrot, theta, eps, nullptr, nullptr, nullptr, dwkn, dIK + (size_t) b * mc * IXD,
+                           dBK + (size_t) b * (mc / IXR) * IXD};
+        if (fn::qsa_blocks_launch(one, 0, pos[b] / IXR, nullptr)) return -1;
+    }
+    if (fn_attn_qsa_dev(B, nq, nkv, hd, nrot, theta, eps, nt, mc, dpos, dqg, dk_, dv_, dwq, dwk, dK, dV, diqk, dwqn,
+                        dwkn, dIK, dBK, top, nsplit, dwork, wb, dog, nullptr))
+        return -1;
+    FN_CK(hipDeviceSynchronize());
+    FN_CK(hipMemcpy(og, dog, nog * 4, hipMemcpyDeviceToHost));
+    FN_CK(hipMemcpy(kh.data(), dK, kh.size() * 4, hipMemcpyDeviceToHost));
+    FN_CK(hipMemcpy(vh.data(), dV, vh.size() * 4, hipMemcpyDeviceToHost));
+    FN_CK(hipMemcpy(ikh.data(), dIK, ikh.size() * 4, hipMemcpyDeviceToHost));
+    for (int b = 0; b < B; ++b) {
+        for (int p = pos[b]; p < pos[b] + nt; ++p) {
+            for (int g = 0; g < nkv; ++g) {
+                float *kd = Kc + (((size_t) b * max_ctx + p) * nkv + g) * hd;
+                float *vd = Vc + (((size_t) b * max_ctx + p) * nkv + g) * hd;
+                const float *kt = &kh[(((size_t) b * nkv + g) * (mc / 64) + p / 64) * 64 * hd + (size_t) (p % 64) * 4];
+                for (int c = 0; c < hd / 4; ++c) std::memcpy(kd + c * 4, kt + (size_t) c * 256, 16);
+                std::memcpy(vd, &vh[(((size_t) b * nkv + g) * mc + p) * hd], (size_t) hd * 4);
+            }
+            std::memcpy(IKc + ((size_t) b * max_ctx + p) * IXD, &ikh[((size_t) b * mc + p) * IXD], IXD * 4);
+        }
+    }
+    // indexer outputs: scores and the kept-block mask from the key lists
+    const size_t bt = (size_t) B * nt, nbmax = (size_t) max_ctx / IXR, aw = fn::attn_work_bytes(B, nq, nt, hd, nsplit);
+    const char *iw = reinterpret_cast<const char *>(dwork) + (aw + 255) / 256 * 256;
+    const float *dsc = reinterpret_cast<const float *>(iw) + bt * 4 * IXD;
+    const int32_t *dkeys = reinterpret_cast<const int32_t *>(dsc + bt * (mc / IXR));
+    if (scores) {
+        std::vector<float> sh(bt * (mc / IXR));
+        FN_CK(hipMemcpy(sh.data(), dsc, sh.size() * 4, hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < bt; ++i) std::memcpy(scores + i * nbmax, &sh[i * (mc / IXR)], nbmax * 4);
+    }
+    if (mask) {
+        const size_t ks = (size_t) top * IXR + IXR;
+        std::vector<int32_t> kl(bt * ks);
+        FN_CK(hipMemcpy(kl.data(), dkeys, kl.size() * 4, hipMemcpyDeviceToHost));
+        std::memset(mask, 0, bt * nbmax);
+        for (int b = 0; b < B; ++b)
+            for (int t = 0; t < nt; ++t) {
+                const size_t i = (size_t) b * nt + t;
+                const int nb = (pos[b] + t + 1) / IXR;
+                if (nb <= top) continue;
+                for (int r = 0; r < top; ++r) mask[i * nbmax + kl[i * ks + (size_t) r * IXR] / IXR] = 1;
+            }
+    }
     return 0;
 }

@@ -20,7 +20,7 @@
 //   * The combine kernel merges the splits with the log-sum-exp identity and applies o / L * sigmoid(gate).
 // Device cache layouts (max_ctx a multiple of 64):
 //   Kc: [B][nkv][max_ctx / 64][hd / 4][64][4]   Vc: [B][nkv][max_ctx][hd]
-#include "gdn.h"
+#include "qsa.h"
 
 #include <algorithm>
 #include <cmath>
@@ -45,6 +45,9 @@ struct AttnArgs {
     float *part_o;   // [B nt][nq][nsplit][HD]
     float *part_ml;  // [B nt][nq][nsplit][2]
     float *og;
+    const int32_t *keys;   // visible-key list per query (QSA) or null (dense)
+    const int32_t *nkeys;
+    int kstride;           // list stride per query
     float inv_freq[MAXROT / 2];
 };
 
@@ -131,7 +134,10 @@ __device__ __forceinline__ void rope_row_lds(float4 *row4, int stride, int lane,
 // PREP (one new token per sequence): the workgroup also does k_attn_prep's work for its group -- RMSNorm + RoPE of
 // its GRP query heads into LDS, and, in the workgroup whose split holds the new position, of the new key, which it
 // appends with the new value to the caches before its first tile load.
-template <int GRP, bool PREP> __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
+// LIST (sparse): the keys a query attends are the first nkeys entries of its key list (ascending positions); tile
+// slots index the list and K/V are gathered from the caches.
+template <int GRP, bool PREP, bool LIST = false>
+__global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
     constexpr int HPW = GRP / WAVES;                 // softmax heads per wave
     constexpr int CPW = HD / 4 / WAVES;              // K chunks (of 4 dims) per wave = 16
     constexpr int RPW = TILE / WAVES;                // V rows per wave = 16
@@ -151,7 +157,8 @@ template <int GRP, bool PREP> __global__ void __launch_bounds__(WAVES * 64) k_at
     const int sp_i = blockIdx.x, g = blockIdx.y, bt = blockIdx.z, b = bt / a.nt, t = bt - b * a.nt;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int P = a.pos[b] + t;
-    const int nk = min(P + 1, a.max_ctx);
+    const int32_t *klist = LIST ? a.keys + (size_t) bt * a.kstride : nullptr;
+    const int nk = LIST ? a.nkeys[bt] : min(P + 1, a.max_ctx);  // slots 0 .. nk-1 hold visible keys
     const int ntiles = (nk + TILE - 1) / TILE;
     const int per = (ntiles + a.nsplit - 1) / a.nsplit;
     const int tile0 = sp_i * per, tile1 = min(tile0 + per, ntiles);
@@ -211,14 +218,26 @@ template <int GRP, bool PREP> __global__ void __launch_bounds__(WAVES * 64) k_at
 
     for (int tile = tile0; tile < tile1; ++tile) {
         const int key0 = tile * TILE;
-        const float4 *Kt = reinterpret_cast<const float4 *>(Kbase + (size_t) tile * TILE * HD);
         float4 kf[CPW], vf[RPW];
+        if (LIST) {  // gather: this lane's key from its 64-key tile of the key-tiled layout
+            const int key = klist[min(key0 + lane, nk - 1)];
+            const float4 *Kt = reinterpret_cast<const float4 *>(Kbase + (size_t) (key / TILE) * TILE * HD);
 #pragma unroll
-        for (int u = 0; u < CPW; ++u) kf[u] = ld_nt(&Kt[(wave * CPW + u) * TILE + lane]);
+            for (int u = 0; u < CPW; ++u) kf[u] = ld_nt(&Kt[(wave * CPW + u) * TILE + (key % TILE)]);
 #pragma unroll
-        for (int u = 0; u < RPW; ++u) {
-            const int row = min(key0 + wave * RPW + u, nk - 1);  // clamp past the last key: finite, weight 0
-            vf[u] = ld_nt(&Vbase[(size_t) row * (HD / 4) + lane]);
+            for (int u = 0; u < RPW; ++u) {
+                const int row = klist[min(key0 + wave * RPW + u, nk - 1)];
+                vf[u] = ld_nt(&Vbase[(size_t) row * (HD / 4) + lane]);
+            }
+        } else {
+            const float4 *Kt = reinterpret_cast<const float4 *>(Kbase + (size_t) tile * TILE * HD);
+#pragma unroll
+            for (int u = 0; u < CPW; ++u) kf[u] = ld_nt(&Kt[(wave * CPW + u) * TILE + lane]);
+#pragma unroll
+            for (int u = 0; u < RPW; ++u) {
+                const int row = min(key0 + wave * RPW + u, nk - 1);  // clamp past the last key: finite, weight 0
+                vf[u] = ld_nt(&Vbase[(size_t) row * (HD / 4) + lane]);
+            }
         }
         float s[GRP];
 #pragma unroll
@@ -428,6 +447,49 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
         else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, false>), sg, sb, 0, st, a);
         else hipLaunchKernelGGL((k_attn_split<4, false>), sg, sb, 0, st, a);
     }
+    hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(CW * 64), 0, st, a);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+size_t attn_qsa_work_bytes(int B, int nq, int nt, int hd, int nsplit, int max_ctx, int top) {
+    return attn_work_bytes(B, nq, nt, hd, nsplit) + qsa_work_bytes(B, nt, max_ctx, top);
+}
+
+int attn_qsa_launch(const AttnDecode &p, const QsaIndexer &ix, hipStream_t st) {
+    if (p.B != ix.B || p.nt != ix.nt || p.max_ctx != ix.max_ctx || p.pos != ix.pos)
+        FN_FAIL("attn_qsa: the attention and indexer shapes disagree");
+    if (p.B < 1 || p.nt < 1 || p.nq < 1 || p.nkv < 1) FN_FAIL("attn: B, nt, nq and nkv must be >= 1");
+    if (p.hd != HD) FN_FAIL("attn: only head_dim 256 is built");
+    if (p.nq % p.nkv) FN_FAIL("attn: nq must be a multiple of nkv");
+    if (p.nrot < 0 || p.nrot > std::min(HD, MAXROT) || (p.nrot & 1)) FN_FAIL("attn: nrot must be even and <= 128");
+    if (p.nsplit < 1) FN_FAIL("attn: nsplit must be >= 1");
+    if (!p.pos || !p.qg || !p.k || !p.v || !p.wq || !p.wk || !p.Kc || !p.Vc || !p.work || !p.og)
+        FN_FAIL("attn: null pointer");
+    const size_t aw = attn_work_bytes(p.B, p.nq, p.nt, p.hd, p.nsplit);
+    if (p.work_bytes < attn_qsa_work_bytes(p.B, p.nq, p.nt, p.hd, p.nsplit, p.max_ctx, ix.top))
+        FN_FAIL("attn_qsa: workspace too small");
+    const int grp = p.nq / p.nkv;
+    if (grp != 4 && grp != 8 && grp != 12) FN_FAIL("attn: query heads per kv head must be 4, 8 or 12");
+    const int32_t *keys = nullptr, *nkeys = nullptr;
+    float *iwork = reinterpret_cast<float *>(reinterpret_cast<char *>(p.work) + (aw + 255) / 256 * 256);
+    if (qsa_select_launch(ix, iwork, p.work_bytes - (aw + 255) / 256 * 256, &keys, &nkeys, st)) return -1;
+    AttnArgs a{};
+    a.B = p.B; a.nq = p.nq; a.nkv = p.nkv; a.nt = p.nt; a.max_ctx = p.max_ctx; a.nsplit = p.nsplit;
+    a.nrot = p.nrot; a.eps = p.eps; a.pos = p.pos; a.qg = p.qg; a.knew = p.k; a.vnew = p.v; a.wq = p.wq;
+    a.wk = p.wk; a.Kc = p.Kc; a.Vc = p.Vc; a.og = p.og;
+    a.keys = keys; a.nkeys = nkeys; a.kstride = ix.top * 4 + 4;
+    const size_t bt = (size_t) p.B * p.nt;
+    a.Q = p.work;
+    a.part_o = a.Q + bt * p.nq * HD;
+    a.part_ml = a.part_o + bt * p.nq * p.nsplit * HD;
+    for (int i = 0; i < p.nrot / 2; ++i)
+        a.inv_freq[i] = (float) (1.0 / std::pow((double) p.theta, (double) (2 * i) / p.nrot));
+    const dim3 sg(p.nsplit, p.nkv, (unsigned) bt), sb(WAVES * 64);
+    hipLaunchKernelGGL(k_attn_prep, dim3((unsigned) bt, p.nq + p.nkv), dim3(HD), 0, st, a);
+    if (grp == 8) hipLaunchKernelGGL((k_attn_split<8, false, true>), sg, sb, 0, st, a);
+    else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, false, true>), sg, sb, 0, st, a);
+    else hipLaunchKernelGGL((k_attn_split<4, false, true>), sg, sb, 0, st, a);
     hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(CW * 64), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;

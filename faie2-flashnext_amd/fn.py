@@ -34,6 +34,7 @@ SYMBOLS = (
     "fn_gdn_block_dev", "fn_gdn_core_dev", "fn_attn_dev", "fn_attn_work_bytes", "fn_attn_nsplit", "fn_advance_dev",
     "fn_fill_normal_dev", "fn_copy_dev",
     "fn_path_init", "fn_path_buffer", "fn_path_step",
+    "fn_attn_qsa_dev", "fn_attn_qsa_work_bytes", "fn_ix_blocks_dev", "fn_test_attn_qsa",
 )
 
 # buffer kinds of fn_path_buffer (include/faie2fn.h)
@@ -97,6 +98,12 @@ class FN:
         d.fn_path_buffer.argtypes = [i, i, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]
         d.fn_path_step.argtypes = [i, C.POINTER(C.c_float)]
         d.fn_use_graphs.argtypes = [i]
+        f = C.c_float
+        d.fn_attn_qsa_dev.argtypes = [i] * 5 + [f, f, i, i] + [VP] * 13 + [i, i, VP, C.c_size_t, VP, VP]
+        d.fn_attn_qsa_work_bytes.restype = C.c_size_t
+        d.fn_attn_qsa_work_bytes.argtypes = [i] * 7
+        d.fn_ix_blocks_dev.argtypes = [i] * 4 + [VP] * 3 + [i, f, f, VP]
+        d.fn_test_attn_qsa.argtypes = [i] * 5 + [f, f, i, i, I32] + [F32] * 11 + [i, i, F32, VP, VP]
         d.fn_n_past.restype = C.c_int
 
     def check(self, rc):
@@ -175,6 +182,27 @@ class FN:
                                        _f32(wk), Kc, Vc, int(nsplit), og))
         return og
 
+    def attn_qsa(self, qg, k, v, wq, wk, Kc, Vc, iqk, wqn, wkn, IKc, pos, top=512, nsplit=0, nrot=64, theta=1e7,
+                 eps=1e-6):
+        """Sparse (QSA) GQA decode.  As attn(), plus iqk [B,nt,640], wqn, wkn [128], IKc [B,max_ctx,128] float32
+        (new raw index keys written in place).  Returns (og [B,nt,nq,hd], scores [B,nt,max_ctx/4],
+        mask [B,nt,max_ctx/4] uint8)."""
+        B, nt, nq, two, hd = qg.shape
+        nkv = k.shape[2]
+        max_ctx = Kc.shape[1]
+        for name, arr, shape in (("Kc", Kc, (B, max_ctx, nkv, hd)), ("Vc", Vc, (B, max_ctx, nkv, hd)),
+                                 ("IKc", IKc, (B, max_ctx, 128))):
+            if arr.dtype != np.float32 or not arr.flags.c_contiguous or arr.shape != shape:
+                raise ValueError(f"{name} must be a C-contiguous float32 {shape} array")
+        og = np.zeros((B, nt, nq, hd), np.float32)
+        sc = np.zeros((B, nt, max_ctx // 4), np.float32)
+        mask = np.zeros((B, nt, max_ctx // 4), np.uint8)
+        self.check(self.d.fn_test_attn_qsa(B, nq, nkv, hd, nrot, float(theta), float(eps), nt, max_ctx,
+                                           np.ascontiguousarray(pos, dtype=np.int32), _f32(qg), _f32(k), _f32(v),
+                                           _f32(wq), _f32(wk), Kc, Vc, _f32(iqk), _f32(wqn), _f32(wkn), IKc, int(top),
+                                           int(nsplit), og, sc.ctypes.data, mask.ctypes.data))
+        return og, sc, mask
+
     # ---- device entry points (integers are device addresses; stream is a HIP stream handle or 0) ----
     def gdn_block_dev(self, B, nkh, nvh, nt, ring, pos, qkv, conv_w, conv_ring, ab, dt_bias, ssm_a, S, z, norm_w,
                       out, stream=0, dk=128, dv=128, head_map=0, gate_act=0, eps=1e-6):
@@ -194,6 +222,18 @@ class FN:
                  stream=0, hd=256, nrot=64, theta=1e7, eps=1e-6):
         self.check(self.d.fn_attn_dev(B, nq, nkv, hd, nrot, float(theta), float(eps), nt, max_ctx, pos, qg, k, v, wq,
                                       wk, Kc, Vc, nsplit, work, work_bytes, og, stream))
+
+    def attn_qsa_work_bytes(self, B, nq, nt, nsplit, max_ctx, top=512, hd=256):
+        return int(self.d.fn_attn_qsa_work_bytes(B, nq, nt, hd, nsplit, max_ctx, top))
+
+    def attn_qsa_dev(self, B, nq, nkv, nt, max_ctx, pos, qg, k, v, wq, wk, Kc, Vc, iqk, wqn, wkn, IKc, BKc, top, nsplit,
+                     work, work_bytes, og, stream=0, hd=256, nrot=64, theta=1e7, eps=1e-6):
+        self.check(self.d.fn_attn_qsa_dev(B, nq, nkv, hd, nrot, float(theta), float(eps), nt, max_ctx, pos, qg, k, v,
+                                          wq, wk, Kc, Vc, iqk, wqn, wkn, IKc, BKc, top, nsplit, work, work_bytes, og,
+                                          stream))
+
+    def ix_blocks_dev(self, B, max_ctx, j0, j1, IKc, wkn, BKc, stream=0, nrot=64, theta=1e7, eps=1e-6):
+        self.check(self.d.fn_ix_blocks_dev(B, max_ctx, j0, j1, IKc, wkn, BKc, nrot, float(theta), float(eps), stream))
 
     def advance_dev(self, pos, B, nt, stream=0):
         self.check(self.d.fn_advance_dev(pos, B, nt, stream))

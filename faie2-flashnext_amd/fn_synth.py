@@ -119,3 +119,12 @@ def gdn_core_bytes(B, nkh=16, nvh=32):
 def attn_bytes(B, L, nq=16, nkv=2, hd=HD):
     """Algorithmic HBM bytes of one GQA decode layer-step: K + V read over L keys, q, gate and out, new k, v."""
     return B * (L * nkv * hd * 4 * 2 + 3 * nq * hd * 4 + 2 * nkv * hd * 4)
+
+
+def attn_qsa_bytes(B, L, top=512, nq=16, nkv=2, hd=HD, ixd=128):
+    """Algorithmic HBM bytes of one sparse (QSA) decode layer-step: the block keys of the complete blocks (scored),
+    K + V of the attended keys (top blocks of 4 and the tail), q, gate and out, the new k, v, the indexer input
+    and its new raw key."""
+    nb = L // 4
+    keys = min(L, 4 * top + (L - 4 * nb)) if nb > top else L
+    return B * (nb * ixd * 4 + keys * nkv * hd * 4 * 2 + 3 * nq * hd * 4 + 2 * nkv * hd * 4 + (5 * ixd + ixd) * 4)

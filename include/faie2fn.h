@@ -129,6 +129,42 @@ int fn_fill_normal_dev(float *p, size_t n, uint64_t seed, float mean, float std,
 int fn_copy_dev(void *dst, const void *src, size_t bytes, void *stream);
 
 /* ======================================================================================================
+ * 3b. QSA sparse attention (new): the reference's attention layer with its indexer (faie2fn.cu:1480-1607, the
+ *     masked k_attn_split :1628-1636, launch order :2396-2402).  Indexer shapes are the reference's: 4 query heads
+ *     of 128 dims, one raw index key of 128 dims per token, blocks of 4 keys, RoPE as the attention's.  A query with
+ *     more than `top` complete blocks (512 in the reference, faie2fn.cu:60) attends the keys of its `top`
+ *     highest-scoring blocks (ties at the threshold: lowest index first) plus the incomplete tail block; otherwise it
+ *     attends every key.
+ * ====================================================================================================== */
+
+/* As fn_attn_dev, plus: iqk [B][nt][640] (indexer query heads, then the raw index key), wqn, wkn [128] indexer norm
+ * weights; IKc [B][max_ctx][128] raw index keys (row pos[b]+t written); BKc block keys, device layout
+ * [B][max_ctx/256][32][64][4] (blocks completed by this call written); max_ctx a multiple of 256;
+ * work: fn_attn_qsa_work_bytes() bytes. */
+int fn_attn_qsa_dev(int B, int nq, int nkv, int hd, int nrot, float theta, float eps, int nt, int max_ctx,
+                    const int32_t *pos, const float *qg, const float *k, const float *v, const float *wq,
+                    const float *wk, float *Kc, float *Vc, const float *iqk, const float *wqn, const float *wkn,
+                    float *IKc, float *BKc, int top, int nsplit, float *work, size_t work_bytes, float *og,
+                    void *stream);
+size_t fn_attn_qsa_work_bytes(int B, int nq, int nt, int hd, int nsplit, int max_ctx, int top);
+
+/* Block keys of blocks [j0, j1) of every sequence from the raw index keys (the reference's k_ix_blocks over a
+ * range, faie2fn.cu:1509-1530): for prefill or for rebuilding BKc from IKc. */
+int fn_ix_blocks_dev(int B, int max_ctx, int j0, int j1, const float *IKc, const float *wkn, float *BKc, int nrot,
+                     float theta, float eps, void *stream);
+
+/* For the sparse step, fn_attn_nsplit(B, nkv, nt, 4 * top + 4) sizes the split of the attended keys. */
+
+/* Host-array hook of the sparse layer step, reference layouts: Kc, Vc [B][max_ctx][nkv][hd], IKc [B][max_ctx][128]
+ * in/out (rows < pos[b] read, new rows written).  Block keys of the blocks complete before the call are built from
+ * IKc inside the hook.  Optional outputs (NULL to skip): scores [B][nt][max_ctx/4] (entries < nb of queries with
+ * nb > top), mask [B][nt][max_ctx/4] (1 = block kept; all 0 for dense queries). */
+int fn_test_attn_qsa(int B, int nq, int nkv, int hd, int nrot, float theta, float eps, int nt, int max_ctx,
+                     const int32_t *pos, const float *qg, const float *k, const float *v, const float *wq,
+                     const float *wk, float *Kc, float *Vc, const float *iqk, const float *wqn, const float *wkn,
+                     float *IKc, int top, int nsplit, float *og, float *scores, uint8_t *mask);
+
+/* ======================================================================================================
  * 4. Path engine (new): the reference's Engine + layer_forward + forward (faie2fn.cu:1937-2031, 2370-2490) for
  *    this path only.  B sequences, nl layers; layer il is attention iff (il + 1) % attn_every == 0
  *    (faie2fn.cu:76, attn_every = 4; 0 = DeltaNet only).  All state is engine-owned on device 0 and zeroed.

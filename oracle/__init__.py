@@ -25,6 +25,7 @@ LIB_PATH = os.path.join(HERE, "liboracle_fn.so")
 _F32 = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _F64 = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
 _I32 = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_U8 = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 
 _lib = None
 
@@ -48,6 +49,12 @@ def lib():
         d.orc_rope_inv_freq.argtypes = [C.c_int, C.c_double, _F32]
         d.orc_attn.argtypes = ([C.c_int] * 5 + [C.c_double, C.c_double, C.c_int, _I32] + [_F32] * 5 +
                                [C.c_int, _F32, _F32, _F64, _F64, _F64])
+        d.orc_attn_masked.argtypes = ([C.c_int] * 5 + [C.c_double, C.c_double, C.c_int, _I32] + [_F32] * 5 +
+                                      [C.c_int, _F32, _F32, _U8, C.c_int, C.c_int, C.c_int, _F64, _F64, _F64])
+        d.orc_ix_prep.argtypes = ([C.c_int] * 6 + [C.c_double, C.c_double, C.c_int, _I32, _F32, _F32, _F32, _F64,
+                                                   _F32, _F64])
+        d.orc_ix_blocks.argtypes = ([C.c_int] * 4 + [C.c_double, C.c_double] + [C.c_int] * 3 + [_F32, _F32, _F64])
+        d.orc_ix_score.argtypes = [C.c_int] * 6 + [_I32, _F64, _F64, _F64]
         _lib = d
     return _lib
 
@@ -100,9 +107,10 @@ def rope_inv_freq(nrot, theta):
     return inv[: nrot // 2]
 
 
-def attn(qg, knew, vnew, wq, wk, Kc, Vc, pos, nrot=64, theta=1e7, eps=1e-6):
+def attn(qg, knew, vnew, wq, wk, Kc, Vc, pos, nrot=64, theta=1e7, eps=1e-6, mask=None, ixr=4, top=512):
     """GQA decode.  qg [B,nt,nq,2,hd]; knew, vnew [B,nt,nkv,hd]; Kc, Vc [B,max_ctx,nkv,hd] fp32 (rows < pos[b]
-    read); pos [B] int.  Returns (og [B,nt,nq,hd], k_rows [B,nt,nkv,hd], v_rows [B,nt,nkv,hd]) float64."""
+    read); pos [B] int; mask [B,nt,nblocks] uint8 (QSA block mask, applied to tokens with more than `top` complete
+    blocks of ixr keys) or None (dense).  Returns (og [B,nt,nq,hd], k_rows [B,nt,nkv,hd], v_rows) float64."""
     B, nt, nq, two, hd = qg.shape
     assert two == 2
     nkv = knew.shape[2]
@@ -112,9 +120,59 @@ def attn(qg, knew, vnew, wq, wk, Kc, Vc, pos, nrot=64, theta=1e7, eps=1e-6):
     kro = np.zeros((B, nt, nkv, hd), np.float64)
     vro = np.zeros((B, nt, nkv, hd), np.float64)
     og = np.zeros((B, nt, nq, hd), np.float64)
-    lib().orc_attn(B, nq, nkv, hd, nrot, float(theta), float(eps), nt, pos, _f32(qg), _f32(knew), _f32(vnew), _f32(wq),
-                   _f32(wk), max_ctx, _f32(Kc), _f32(Vc), kro, vro, og)
+    if mask is None:
+        lib().orc_attn(B, nq, nkv, hd, nrot, float(theta), float(eps), nt, pos, _f32(qg), _f32(knew), _f32(vnew),
+                       _f32(wq), _f32(wk), max_ctx, _f32(Kc), _f32(Vc), kro, vro, og)
+    else:
+        mask = np.ascontiguousarray(mask, dtype=np.uint8)
+        assert mask.shape[:2] == (B, nt)
+        lib().orc_attn_masked(B, nq, nkv, hd, nrot, float(theta), float(eps), nt, pos, _f32(qg), _f32(knew),
+                              _f32(vnew), _f32(wq), _f32(wk), max_ctx, _f32(Kc), _f32(Vc), mask, mask.shape[2], ixr, top,
+                              kro, vro, og)
     return og, kro, vro
+
+
+def ix_prep(iqk, wqn, wkn, IKc, BKc, pos, ixh=4, ixd=128, ixr=4, nrot=64, theta=1e7, eps=1e-6):
+    """QSA indexer prep.  iqk [B,nt,ixh*ixd+ixd]; IKc [B,max_ctx,ixd] float32 and BKc [B,max_ctx/ixr,ixd] float64
+    are updated in place (raw keys appended; blocks completed by this call filled).  Returns Qix [B,nt,ixh,ixd]."""
+    B, nt, row = iqk.shape
+    assert row == ixh * ixd + ixd
+    max_ctx = IKc.shape[1]
+    assert IKc.dtype == np.float32 and IKc.flags.c_contiguous and BKc.dtype == np.float64 and BKc.flags.c_contiguous
+    Qix = np.zeros((B, nt, ixh, ixd), np.float64)
+    lib().orc_ix_prep(B, nt, ixh, ixd, ixr, nrot, float(theta), float(eps), max_ctx,
+                      np.ascontiguousarray(pos, dtype=np.int32), _f32(iqk), _f32(wqn), _f32(wkn), Qix, IKc, BKc)
+    return Qix
+
+
+def ix_blocks(IKc, wkn, BKc, j0, j1, ixr=4, nrot=64, theta=1e7, eps=1e-6):
+    """Block keys of blocks [j0, j1) of every sequence from the raw keys, into BKc (float64, in place)."""
+    B, max_ctx, ixd = IKc.shape
+    lib().orc_ix_blocks(B, ixd, ixr, nrot, float(theta), float(eps), max_ctx, j0, j1, _f32(IKc), _f32(wkn), BKc)
+
+
+def ix_score(Qix, BKc, pos, max_ctx, ixr=4):
+    """scores [B,nt,max_ctx/ixr] float64 (entries past each token's complete blocks stay 0)."""
+    B, nt, ixh, ixd = Qix.shape
+    sc = np.zeros((B, nt, max_ctx // ixr), np.float64)
+    lib().orc_ix_score(B, nt, ixh, ixd, ixr, max_ctx, np.ascontiguousarray(pos, dtype=np.int32), _f64(Qix), _f64(BKc), sc)
+    return sc
+
+
+def ix_select(scores, pos, top=512, ixr=4):
+    """Block mask [B,nt,nblocks] uint8 of k_ix_select (faie2fn.cu:1557-1607): for a token with nb > top complete
+    blocks, the top highest-scoring ones, ties at the threshold kept lowest index first (a stable sort on the
+    descending score); other tokens get an all-zero mask (their attention is dense)."""
+    B, nt, nbmax = scores.shape
+    mask = np.zeros((B, nt, nbmax), np.uint8)
+    for b in range(B):
+        for t in range(nt):
+            nb = (int(pos[b]) + t + 1) // ixr
+            if nb <= top:
+                continue
+            order = np.argsort(-scores[b, t, :nb], kind="stable")
+            mask[b, t, order[:top]] = 1
+    return mask
 
 
 def relerr(got, ref):

@@ -217,9 +217,10 @@ static void norm_rope(int hd, int nrot, const float *inv, double eps, int pos, c
  *   og = softmax-weighted V * sigmoid(gate) (:1686-1689).
  * Kc, Vc [B][max_ctx][nkv][hd] fp32 are read for rows < pos[b] only.  Outputs: knew_o/vnew_o [B][nt][nkv][hd]
  * (the appended rows), og [B][nt][nq][hd]. */
-EXPORT void orc_attn(int B, int nq, int nkv, int hd, int nrot, double theta, double eps, int nt, const int *pos,
-                     const float *qg, const float *knew, const float *vnew, const float *wq, const float *wk,
-                     int max_ctx, const float *Kc, const float *Vc, double *knew_o, double *vnew_o, double *og) {
+EXPORT void orc_attn_masked(int B, int nq, int nkv, int hd, int nrot, double theta, double eps, int nt, const int *pos,
+                            const float *qg, const float *knew, const float *vnew, const float *wq, const float *wk,
+                            int max_ctx, const float *Kc, const float *Vc, const uint8_t *mask, int mstride, int ixr,
+                            int top, double *knew_o, double *vnew_o, double *og) {
     float *inv = (float *) malloc(sizeof(float) * (size_t) (nrot / 2 + 1));
     orc_rope_inv_freq(nrot, theta, inv);
     const int grp = nq / nkv;
@@ -243,8 +244,17 @@ EXPORT void orc_attn(int B, int nq, int nkv, int hd, int nrot, double theta, dou
                 double *sc = (double *) malloc(sizeof(double) * (size_t) nk);
                 const float *qrow = qg + (((size_t) b * nt + t) * nq + h) * 2 * hd;
                 norm_rope(hd, nrot, inv, eps, p, qrow, wq, qd);
+                /* with a block mask (QSA, faie2fn.cu:1628-1636): when the token has more than `top` complete blocks,
+                 * a key is visible iff its block is kept or it lies in the incomplete tail */
+                const int nb = (p + 1) / (ixr > 0 ? ixr : 1);
+                const int sel = mask != NULL && nb > top;
+                const uint8_t *mt = mask ? mask + ((size_t) b * nt + t) * mstride : NULL;
                 double mx = -INFINITY;
                 for (int key = 0; key < nk; ++key) {
+                    if (sel && key / ixr < nb && !mt[key / ixr]) {
+                        sc[key] = -INFINITY;
+                        continue;
+                    }
                     double s = 0.0;
                     if (key < pos[b]) {
                         const float *kr = Kc + (((size_t) b * max_ctx + key) * nkv + g) * hd;
@@ -259,6 +269,7 @@ EXPORT void orc_attn(int B, int nq, int nkv, int hd, int nrot, double theta, dou
                 double l = 0.0;
                 for (int d = 0; d < hd; ++d) acc[d] = 0.0;
                 for (int key = 0; key < nk; ++key) {
+                    if (sc[key] == -INFINITY) continue;
                     const double e = exp(sc[key] - mx);
                     l += e;
                     if (key < pos[b]) {
@@ -276,4 +287,111 @@ EXPORT void orc_attn(int B, int nq, int nkv, int hd, int nrot, double theta, dou
                 free(qd);
             }
     free(inv);
+}
+
+EXPORT void orc_attn(int B, int nq, int nkv, int hd, int nrot, double theta, double eps, int nt, const int *pos,
+                     const float *qg, const float *knew, const float *vnew, const float *wq, const float *wk,
+                     int max_ctx, const float *Kc, const float *Vc, double *knew_o, double *vnew_o, double *og) {
+    orc_attn_masked(B, nq, nkv, hd, nrot, theta, eps, nt, pos, qg, knew, vnew, wq, wk, max_ctx, Kc, Vc, NULL, 0, 1, 0,
+                    knew_o, vnew_o, og);
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * QSA indexer (faie2fn.cu:1480-1607): ixh query heads and one raw key of ixd dims per token, keys compressed into
+ * blocks of ixr consecutive positions, the top `top` blocks by score kept per query. */
+
+/* RMSNorm + RoPE of a row given in float64 (the block-key path averages fp32 raw keys first) */
+static void norm_rope_d(int d_, int nrot, const float *inv, double eps, int pos, const double *x, const float *w,
+                        double *y) {
+    double ss = 0.0;
+    for (int d = 0; d < d_; ++d) ss += x[d] * x[d];
+    const double r = 1.0 / sqrt(ss / d_ + eps);
+    for (int d = 0; d < d_; ++d) y[d] = x[d] * r * (double) w[d];
+    for (int i = 0; i < nrot / 2; ++i) {
+        const float ang = (float) pos * inv[i];
+        const double cs = cos((double) ang), sn = sin((double) ang);
+        const double a = y[i], b = y[i + nrot / 2];
+        y[i] = a * cs - b * sn;
+        y[i + nrot / 2] = b * cs + a * sn;
+    }
+}
+
+/* k_ix_qk + k_ix_blocks (faie2fn.cu:1482-1530) for nt new tokens of B sequences.
+ *   iqk [B][nt][ixh*ixd + ixd]: the indexer's query heads, then the raw index key;
+ *   Qix out [B][nt][ixh][ixd] = rope(rmsnorm(q_h) * wqn) at position pos[b] + t;
+ *   IKc [B][max_ctx][ixd] fp32 in/out: the raw key of token t stored at row pos[b] + t;
+ *   BKc [B][max_ctx/ixr][ixd] float64 in/out: every block completed by this call, j in [pos/ixr, (pos+nt)/ixr),
+ *   gets rope(rmsnorm(mean of its ixr raw keys) * wkn) at position ixr*j. */
+EXPORT void orc_ix_prep(int B, int nt, int ixh, int ixd, int ixr, int nrot, double theta, double eps, int max_ctx,
+                        const int *pos, const float *iqk, const float *wqn, const float *wkn, double *Qix, float *IKc,
+                        double *BKc) {
+    float *inv = (float *) malloc(sizeof(float) * (size_t) (nrot / 2 + 1));
+    orc_rope_inv_freq(nrot, theta, inv);
+    double *x = (double *) malloc(sizeof(double) * (size_t) ixd);
+    const int row = ixh * ixd + ixd, maxb = max_ctx / ixr;
+    for (int b = 0; b < B; ++b) {
+        for (int t = 0; t < nt; ++t) {
+            const float *r = iqk + ((size_t) b * nt + t) * row;
+            const int P = pos[b] + t;
+            for (int h = 0; h < ixh; ++h) {
+                for (int d = 0; d < ixd; ++d) x[d] = (double) r[h * ixd + d];
+                norm_rope_d(ixd, nrot, inv, eps, P, x, wqn, Qix + (((size_t) b * nt + t) * ixh + h) * ixd);
+            }
+            memcpy(IKc + ((size_t) b * max_ctx + P) * ixd, r + ixh * ixd, sizeof(float) * (size_t) ixd);
+        }
+        for (int j = pos[b] / ixr; j < (pos[b] + nt) / ixr; ++j) {
+            for (int d = 0; d < ixd; ++d) {
+                double m = 0.0;
+                for (int e = 0; e < ixr; ++e) m += (double) IKc[((size_t) b * max_ctx + (size_t) j * ixr + e) * ixd + d];
+                x[d] = m / ixr;
+            }
+            norm_rope_d(ixd, nrot, inv, eps, j * ixr, x, wkn, BKc + ((size_t) b * maxb + j) * ixd);
+        }
+    }
+    free(x);
+    free(inv);
+}
+
+/* block keys of blocks [j0, j1) of every sequence from the raw keys (k_ix_blocks over a range) */
+EXPORT void orc_ix_blocks(int B, int ixd, int ixr, int nrot, double theta, double eps, int max_ctx, int j0, int j1,
+                          const float *IKc, const float *wkn, double *BKc) {
+    float *inv = (float *) malloc(sizeof(float) * (size_t) (nrot / 2 + 1));
+    orc_rope_inv_freq(nrot, theta, inv);
+    double *x = (double *) malloc(sizeof(double) * (size_t) ixd);
+    const int maxb = max_ctx / ixr;
+    for (int b = 0; b < B; ++b)
+        for (int j = j0; j < j1; ++j) {
+            for (int d = 0; d < ixd; ++d) {
+                double m = 0.0;
+                for (int e = 0; e < ixr; ++e) m += (double) IKc[((size_t) b * max_ctx + (size_t) j * ixr + e) * ixd + d];
+                x[d] = m / ixr;
+            }
+            norm_rope_d(ixd, nrot, inv, eps, j * ixr, x, wkn, BKc + ((size_t) b * maxb + j) * ixd);
+        }
+    free(x);
+    free(inv);
+}
+
+/* k_ix_score (faie2fn.cu:1534-1555): scores[b][t][j] = sum_h relu(Qix[b][t][h] . BKc[b][j]) / sqrt(ixd) for the
+ * nb = (pos + t + 1) / ixr complete blocks of token t (entries past nb are left as they are). */
+EXPORT void orc_ix_score(int B, int nt, int ixh, int ixd, int ixr, int max_ctx, const int *pos, const double *Qix,
+                         const double *BKc, double *scores) {
+    const int maxb = max_ctx / ixr;
+    const int nt_ = nthreads();
+#pragma omp parallel for collapse(2) schedule(static) num_threads(nt_)
+    for (int b = 0; b < B; ++b)
+        for (int t = 0; t < nt; ++t) {
+            const int nb = (pos[b] + t + 1) / ixr;
+            for (int j = 0; j < nb; ++j) {
+                const double *k = BKc + ((size_t) b * maxb + j) * ixd;
+                double s = 0.0;
+                for (int h = 0; h < ixh; ++h) {
+                    const double *q = Qix + (((size_t) b * nt + t) * ixh + h) * ixd;
+                    double p = 0.0;
+                    for (int d = 0; d < ixd; ++d) p += q[d] * k[d];
+                    s += p > 0.0 ? p : 0.0;
+                }
+                scores[((size_t) b * nt + t) * maxb + j] = s / sqrt((double) ixd);
+            }
+        }
 }

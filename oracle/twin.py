@@ -119,3 +119,31 @@ def attn(qg, knew, vnew, wq, wk, Kc, Vc, pos, nrot=64, theta=1e7, eps=1e-6):
                 gate = qg[b, t, g * grp:(g + 1) * grp, 1].astype(np.float64)
                 og[b, t, g * grp:(g + 1) * grp] = o * _sigmoid(gate)
     return og, Kn, Vn
+
+
+def ix_prep(iqk, wqn, wkn, IKc, BKc, pos, ixh=4, ixd=128, ixr=4, nrot=64, theta=1e7, eps=1e-6):
+    """Twin of oracle.ix_prep (whole-batch numpy; same in-place contract)."""
+    B, nt, _ = iqk.shape
+    inv = rope_inv_freq(nrot, theta)
+    tpos = np.asarray(pos, np.int64)[:, None] + np.arange(nt)[None, :]
+    q = iqk[:, :, : ixh * ixd].reshape(B, nt, ixh, ixd)
+    Qix = _norm_rope(q, wqn, tpos[:, :, None], nrot, inv, eps)
+    for b in range(B):
+        p0 = int(pos[b])
+        IKc[b, p0:p0 + nt] = iqk[b, :, ixh * ixd:]
+        j = np.arange(p0 // ixr, (p0 + nt) // ixr)
+        if j.size:
+            means = IKc[b, : (j[-1] + 1) * ixr].astype(np.float64).reshape(-1, ixr, ixd).mean(1)[j]
+            BKc[b, j] = _norm_rope(means, wkn, (j * ixr)[:, None], nrot, inv, eps)
+    return Qix
+
+
+def ix_score(Qix, BKc, pos, max_ctx, ixr=4):
+    B, nt, ixh, ixd = Qix.shape
+    sc = np.zeros((B, nt, max_ctx // ixr))
+    for b in range(B):
+        for t in range(nt):
+            nb = (int(pos[b]) + t + 1) // ixr
+            dots = Qix[b, t] @ BKc[b, :nb].T                  # [ixh, nb]
+            sc[b, t, :nb] = np.maximum(dots, 0.0).sum(0) / np.sqrt(ixd)
+    return sc

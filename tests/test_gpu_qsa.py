@@ -1,0 +1,126 @@
+"""GPU parity of the QSA sparse attention (indexer + selection + attention over the kept keys).
+
+Checked separately, so that an exact selection rule is held to an exact standard:
+* scores against the float64 oracle (normwise <= 1e-5 over the complete blocks of each sparse query);
+* the kept-block set bit-exactly against the selection rule applied to the GPU's own scores (top blocks, ties at
+  the threshold lowest index first); against the oracle's float64 scores the sets may differ only at near-ties;
+* the attention output against the oracle's masked attention under the GPU's selection (<= 1e-5), and the
+  appended K, V and raw index-key rows.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def make_case(B, nt, max_ctx, pos, seed, nq=16, nkv=2, hd=256):
+    rng = np.random.default_rng(seed)
+    pos = np.asarray(pos, np.int32)
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    c = dict(qg=f(B, nt, nq, 2, hd), k=f(B, nt, nkv, hd), v=f(B, nt, nkv, hd), iqk=f(B, nt, 640),
+             wq=rng.normal(1, 0.1, hd).astype(np.float32), wk=rng.normal(1, 0.1, hd).astype(np.float32),
+             wqn=rng.normal(1, 0.1, 128).astype(np.float32), wkn=rng.normal(1, 0.1, 128).astype(np.float32),
+             Kc=np.zeros((B, max_ctx, nkv, hd), np.float32), Vc=np.zeros((B, max_ctx, nkv, hd), np.float32),
+             IKc=np.zeros((B, max_ctx, 128), np.float32), pos=pos)
+    for b in range(B):
+        n = int(pos[b])
+        c["Kc"][b, :n] = f(n, nkv, hd)
+        c["Vc"][b, :n] = f(n, nkv, hd)
+        c["IKc"][b, :n] = f(n, 128)
+    return c
+
+
+def run_and_check(fnlib, c, top):
+    B, nt = c["qg"].shape[:2]
+    max_ctx = c["Kc"].shape[1]
+    Kc, Vc, IKc = c["Kc"].copy(), c["Vc"].copy(), c["IKc"].copy()
+    og, sc, mask = fnlib.attn_qsa(c["qg"], c["k"], c["v"], c["wq"], c["wk"], Kc, Vc, c["iqk"], c["wqn"], c["wkn"], IKc,
+                                  c["pos"], top=top)
+    # oracle indexer on the same inputs
+    IK_ref = c["IKc"].copy()
+    BK_ref = np.zeros((B, max_ctx // 4, 128))
+    for b in range(B):
+        oracle.ix_blocks(IK_ref[b:b + 1], c["wkn"], BK_ref[b:b + 1], 0, int(c["pos"][b]) // 4)
+    Qix = oracle.ix_prep(c["iqk"], c["wqn"], c["wkn"], IK_ref, BK_ref, c["pos"])
+    sref = oracle.ix_score(Qix, BK_ref, c["pos"], max_ctx)
+    sparse = 0
+    for b in range(B):
+        for t in range(nt):
+            nb = (int(c["pos"][b]) + t + 1) // 4
+            if nb <= top:
+                assert not mask[b, t].any()
+                continue
+            sparse += 1
+            assert oracle.relerr(sc[b, t, :nb], sref[b, t, :nb]) <= TOL, (b, t)
+            # the selection rule, exactly, on the GPU's own scores
+            want = oracle.ix_select(sc[b:b + 1, t:t + 1].astype(np.float64), np.array([int(c["pos"][b]) + t]), top)
+            assert np.array_equal(mask[b, t], want[0, 0]), (b, t)
+            assert int(mask[b, t].sum()) == top
+            # against the float64 selection: only near-ties at the threshold may differ
+            ref_mask = oracle.ix_select(sref[b:b + 1, t:t + 1], np.array([int(c["pos"][b]) + t]), top)[0, 0]
+            diff = np.nonzero(ref_mask[:nb] != mask[b, t, :nb])[0]
+            if diff.size:
+                thr = np.sort(sref[b, t, :nb])[::-1][top - 1]
+                assert np.all(np.abs(sref[b, t, diff] - thr) <= 1e-5 * np.abs(sref[b, t, :nb]).max()), (b, t, diff)
+    # attention under the GPU's selection
+    ref_og, ref_k, ref_v = oracle.attn(c["qg"], c["k"], c["v"], c["wq"], c["wk"], c["Kc"], c["Vc"], c["pos"],
+                                       mask=mask, ixr=4, top=top)
+    got_k = np.stack([Kc[b, c["pos"][b]:c["pos"][b] + nt] for b in range(B)])
+    got_v = np.stack([Vc[b, c["pos"][b]:c["pos"][b] + nt] for b in range(B)])
+    got_ik = np.stack([IKc[b, c["pos"][b]:c["pos"][b] + nt] for b in range(B)])
+    e = (oracle.relerr(og, ref_og), oracle.relerr(got_k, ref_k), oracle.relerr(got_v, ref_v))
+    assert max(e) <= TOL, e
+    assert np.array_equal(got_ik, c["iqk"][:, :, 512:])
+    return sparse
+
+
+def test_qsa_sparse_and_dense_queries_in_one_batch(fnlib):
+    """top = 64 over up to 700 keys: sequence 0 sparse (nb 174 > 64), sequence 1 dense (nb 40), sequence 2 right at
+    the switch (nb 65)."""
+    _say("qsa B=3 top=64 mixed sparse/dense")
+    c = make_case(3, 1, 768, [699, 160, 260], seed=1)
+    assert run_and_check(fnlib, c, top=64) == 2
+
+
+def test_qsa_reference_budget(fnlib):
+    """The reference's budget: top 512 blocks of 4 (2048 keys) at a 3000-key context."""
+    _say("qsa B=1 L=3000 top=512")
+    c = make_case(1, 1, 3072, [2999], seed=2)
+    assert run_and_check(fnlib, c, top=512) == 1
+
+
+def test_qsa_multi_token_blocks_complete_inside_the_call(fnlib):
+    """nt = 5: blocks completed by this call's own new keys are built and scored (token t sees blocks
+    < (pos + t + 1) / 4)."""
+    _say("qsa nt=5 top=32")
+    c = make_case(2, 5, 512, [301, 255], seed=3)
+    run_and_check(fnlib, c, top=32)
+
+
+def test_qsa_ties_keep_lowest_index(fnlib):
+    """Identical raw keys make identical block scores everywhere: the kept blocks must be the lowest-index ones."""
+    _say("qsa ties")
+    c = make_case(1, 1, 1024, [999], seed=4)
+    c["IKc"][0, :999] = c["IKc"][0, 0]  # every complete block has the same mean ... but a RoPE'd key per position
+    Kc, Vc, IKc = c["Kc"].copy(), c["Vc"].copy(), c["IKc"].copy()
+    og, sc, mask = fnlib.attn_qsa(c["qg"], c["k"], c["v"], c["wq"], c["wk"], Kc, Vc, c["iqk"], c["wqn"], c["wkn"], IKc,
+                                  c["pos"], top=32)
+    nb = 1000 // 4
+    want = oracle.ix_select(sc.astype(np.float64), c["pos"], 32)
+    assert np.array_equal(mask, want)
+    # force exact ties: zero index queries give all-zero scores (relu of 0), so the first 32 blocks are kept
+    c["iqk"][:, :, :512] = 0
+    Kc, Vc, IKc = c["Kc"].copy(), c["Vc"].copy(), c["IKc"].copy()
+    og, sc, mask = fnlib.attn_qsa(c["qg"], c["k"], c["v"], c["wq"], c["wk"], Kc, Vc, c["iqk"], c["wqn"], c["wkn"], IKc,
+                                  c["pos"], top=32)
+    assert not sc[0, 0, :nb].any()
+    assert mask[0, 0, :32].all() and not mask[0, 0, 32:].any()

@@ -346,3 +346,93 @@ def test_softplus_threshold_and_gate():
         x = torch.tensor(float(ab2[0, 0, 0]) + float(lay.dt_bias[0]), dtype=torch.float64)
         gam = float(torch.exp(float(lay.ssm_a[0]) * torch.nn.functional.softplus(x)))
         assert np.allclose(S, gam * S1, rtol=1e-13, atol=1e-300)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# QSA indexer (faie2fn.cu:1480-1607)
+
+
+def _ix_case(seed, B=2, nt=3, L=1024, pos=(700, 333)):
+    rng = np.random.default_rng(seed)
+    iqk = f32(rng.standard_normal((B, nt, 640)))
+    wqn, wkn = f32(rng.normal(1, 0.1, 128)), f32(rng.normal(1, 0.1, 128))
+    IK = np.zeros((B, L, 128), np.float32)
+    pos = np.array(pos, np.int32)
+    for b in range(B):
+        IK[b, :pos[b]] = rng.standard_normal((pos[b], 128))
+    return iqk, wqn, wkn, IK, pos
+
+
+def test_twin_indexer():
+    iqk, wqn, wkn, IK, pos = _ix_case(1)
+    L = IK.shape[1]
+    BK1, BK2 = np.zeros((2, L // 4, 128)), np.zeros((2, L // 4, 128))
+    for b in range(2):
+        oracle.ix_blocks(IK[b:b + 1], wkn, BK1[b:b + 1], 0, int(pos[b]) // 4)
+    BK2[:] = BK1
+    IK1, IK2 = IK.copy(), IK.copy()
+    Q1 = oracle.ix_prep(iqk, wqn, wkn, IK1, BK1, pos)
+    Q2 = twin.ix_prep(iqk, wqn, wkn, IK2, BK2, pos)
+    assert oracle.relerr(Q1, Q2) < 1e-13 and np.array_equal(IK1, IK2) and oracle.relerr(BK1, BK2) < 1e-13
+    s1 = oracle.ix_score(Q1, BK1, pos, L)
+    s2 = twin.ix_score(Q2, BK2, pos, L)
+    assert oracle.relerr(s1, s2) < 1e-13
+
+
+def test_block_key_closed_form():
+    """A block of four equal raw keys has that key's norm as its mean; block j is roped at position 4j."""
+    rng = np.random.default_rng(5)
+    IK = np.zeros((1, 256, 128), np.float32)
+    x = f32(rng.standard_normal(128))
+    IK[0, 40:44] = x
+    w = f32(rng.normal(1, 0.1, 128))
+    BK = np.zeros((1, 64, 128))
+    oracle.ix_blocks(IK, w, BK, 10, 11)
+    ref = twin._norm_rope(x, w, 40, 64, oracle.rope_inv_freq(64, 1e7), 1e-6)
+    assert np.allclose(BK[0, 10], ref, atol=1e-14)
+
+
+def test_selection_rule():
+    """top-k by descending score; ties at the threshold keep the lowest index; queries with <= top complete blocks
+    are dense (empty mask)."""
+    rng = np.random.default_rng(6)
+    nb = 300
+    s = np.zeros((1, 2, 400))
+    s[0, :, :nb] = rng.random(nb)
+    m = oracle.ix_select(s, np.array([nb * 4 - 1]), top=50)
+    order = np.lexsort((np.arange(nb), -s[0, 0, :nb]))  # independent: lexsort, index as the tie key
+    assert set(np.nonzero(m[0, 0])[0]) == set(order[:50])
+    s2 = np.zeros((1, 1, 400))
+    s2[0, 0, :nb] = 0.5
+    s2[0, 0, [7, 99]] = 1.0
+    m2 = oracle.ix_select(s2, np.array([nb * 4 - 1]), top=5)
+    assert sorted(np.nonzero(m2[0, 0])[0]) == [0, 1, 2, 7, 99]
+    m3 = oracle.ix_select(s2, np.array([4 * 5 - 1]), top=5)  # nb = 5 <= top: dense
+    assert not m3.any()
+
+
+def test_masked_attention_reduces_to_dense():
+    """All blocks kept == dense; nothing kept leaves exactly the incomplete tail block visible."""
+    rng = np.random.default_rng(7)
+    B, nq, nkv, hd = 1, 8, 2, 32
+    qg = f32(rng.standard_normal((B, 1, nq, 2, hd)))
+    kn, vn = f32(rng.standard_normal((B, 1, nkv, hd))), f32(rng.standard_normal((B, 1, nkv, hd)))
+    w = np.ones(hd, np.float32)
+    K, V = f32(rng.standard_normal((B, 256, nkv, hd))), f32(rng.standard_normal((B, 256, nkv, hd)))
+    pos = np.array([205], np.int32)  # keys 0..205: 51 complete blocks (0..203) and the tail 204, 205
+    dense = oracle.attn(qg, kn, vn, w, w, K, V, pos, nrot=8)[0]
+    full = oracle.attn(qg, kn, vn, w, w, K, V, pos, nrot=8, mask=np.ones((1, 1, 64), np.uint8), top=4)[0]
+    assert np.allclose(full, dense, atol=1e-15)
+    few = oracle.attn(qg, kn, vn, w, w, K, V, pos, nrot=8, mask=np.zeros((1, 1, 64), np.uint8), top=100)[0]
+    assert np.allclose(few, dense, atol=1e-15)  # nb = 51 <= top: dense whatever the mask says
+    tail, kr, vr = oracle.attn(qg, kn, vn, w, w, K, V, pos, nrot=8, mask=np.zeros((1, 1, 64), np.uint8), top=4)
+    inv = oracle.rope_inv_freq(8, 1e7)
+    Q = twin._norm_rope(qg[0, 0, :, 0], w, 205, 8, inv, 1e-6)
+    gate = 1 / (1 + np.exp(-qg[0, 0, :, 1].astype(np.float64)))
+    for h in range(nq):
+        g = h // 4
+        keys = np.stack([K[0, 204, g].astype(np.float64), kr[0, 0, g]])
+        vals = np.stack([V[0, 204, g].astype(np.float64), vr[0, 0, g]])
+        sc = keys @ Q[h] / np.sqrt(hd)
+        p = np.exp(sc - sc.max())
+        assert np.allclose(tail[0, 0, h], (p @ vals) / p.sum() * gate[h], atol=1e-14)
