@@ -163,8 +163,9 @@ __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
     const int per = (ntiles + a.nsplit - 1) / a.nsplit;
     const int tile0 = sp_i * per, tile1 = min(tile0 + per, ntiles);
     const float scale = rsqrtf((float) HD);
-    // the new key is visible (inside the cache) and falls in this split's tiles
-    const bool owner = PREP && P >= 0 && P < a.max_ctx && P / TILE >= tile0 && P / TILE < tile1;
+    // the new key is visible (inside the cache) and its slot, the last one (nk - 1 = P for the dense walk, the end of
+    // the tail for a key list), falls in this split's tiles
+    const bool owner = PREP && P >= 0 && P < a.max_ctx && (nk - 1) / TILE >= tile0 && (nk - 1) / TILE < tile1;
 
     if (PREP) {
         if (threadIdx.x < a.nrot / 2) {
@@ -486,10 +487,16 @@ int attn_qsa_launch(const AttnDecode &p, const QsaIndexer &ix, hipStream_t st) {
     for (int i = 0; i < p.nrot / 2; ++i)
         a.inv_freq[i] = (float) (1.0 / std::pow((double) p.theta, (double) (2 * i) / p.nrot));
     const dim3 sg(p.nsplit, p.nkv, (unsigned) bt), sb(WAVES * 64);
-    hipLaunchKernelGGL(k_attn_prep, dim3((unsigned) bt, p.nq + p.nkv), dim3(HD), 0, st, a);
-    if (grp == 8) hipLaunchKernelGGL((k_attn_split<8, false, true>), sg, sb, 0, st, a);
-    else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, false, true>), sg, sb, 0, st, a);
-    else hipLaunchKernelGGL((k_attn_split<4, false, true>), sg, sb, 0, st, a);
+    if (p.nt == 1) {  // q norm + RoPE and the K/V append folded into the split kernel
+        if (grp == 8) hipLaunchKernelGGL((k_attn_split<8, true, true>), sg, sb, 0, st, a);
+        else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, true, true>), sg, sb, 0, st, a);
+        else hipLaunchKernelGGL((k_attn_split<4, true, true>), sg, sb, 0, st, a);
+    } else {
+        hipLaunchKernelGGL(k_attn_prep, dim3((unsigned) bt, p.nq + p.nkv), dim3(HD), 0, st, a);
+        if (grp == 8) hipLaunchKernelGGL((k_attn_split<8, false, true>), sg, sb, 0, st, a);
+        else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, false, true>), sg, sb, 0, st, a);
+        else hipLaunchKernelGGL((k_attn_split<4, false, true>), sg, sb, 0, st, a);
+    }
     hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(CW * 64), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;

@@ -5,7 +5,7 @@
 //   k_ix_blocks  the same block keys over a range of blocks (prefill / rebuilding a cache)
 //   k_ix_score   score(block j) = sum over the 4 heads of relu(q_h . BK_j) / sqrt(128); lane = block over a
 //                block-tiled key store, so each wave load is one coalesced 1 KiB row of 64 blocks
-//   k_ix_select  the top `top` blocks by score, ties at the threshold kept lowest index first, by a 4-pass radix
+//   k_ix_select  the top `top` blocks by score, ties at the threshold kept lowest index first, by a 3-pass radix
 //                select on the score bits in LDS histograms (the reference binary-searches 32 bit-passes); it emits
 //                the sorted list of visible keys (kept blocks, then the incomplete tail) that the attention split
 //                kernel gathers from.  A query with <= top complete blocks gets the dense list 0..pos.
@@ -120,71 +120,105 @@ __global__ void __launch_bounds__(256) k_ix_blocks(const IxArgs a) {
     if (j < a.j1) block_key(a, b, j, buf[wave], lane);
 }
 
-// grid (B nt, G), 256 threads; wave-strided over tiles of 64 blocks, lane = block
+// grid (B nt, G), 256 threads.  Workgroup y takes tiles y, y + G, ... of 64 blocks; lane = block, and wave w loads
+// dims 32w .. 32w+31 of the tile (8 coalesced 1 KiB rows), so one tile is 4 waves' loads in flight at once.  The
+// four waves' partial head dots meet in LDS; wave 0 applies the relu per head and stores the tile's 64 scores.
 __global__ void __launch_bounds__(256) k_ix_score(const IxArgs a) {
+    constexpr int CW = IXD / 4 / 4;  // float4 chunks per wave
     __shared__ float4 qs[IXD / 4][IXH];
+    __shared__ float part[2][4][IXH][BT];
     const int bt = blockIdx.x, b = bt / a.nt, t = bt - b * a.nt;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nb = min(a.pos[b] + t + 1, a.max_ctx) / IXR;
     if (nb <= a.top) return;  // dense: nothing to select
+    const int ntiles = (nb + BT - 1) / BT;
+    int tile = blockIdx.y;
+    if (tile >= ntiles) return;
+    const float4 *Bb = reinterpret_cast<const float4 *>(a.BKc) +
+                       ((size_t) b * (a.max_ctx / IXR / BT) * (IXD / 4) + wave * CW) * BT + lane;
+    float4 kf[CW];
+#pragma unroll
+    for (int c = 0; c < CW; ++c) kf[c] = ld_nt(&Bb[((size_t) tile * (IXD / 4) + c) * BT]);
     for (int i = threadIdx.x; i < IXH * IXD / 4; i += 256) {
         const int h = i / (IXD / 4), c = i % (IXD / 4);
         qs[c][h] = reinterpret_cast<const float4 *>(a.Qix + ((size_t) bt * IXH + h) * IXD)[c];
     }
     __syncthreads();
     const float inv = 1.0f / sqrtf((float) IXD);
-    const int ntiles = (nb + BT - 1) / BT;
-    const float4 *Bb = reinterpret_cast<const float4 *>(a.BKc) + (size_t) b * (a.max_ctx / IXR / BT) * (IXD / 4) * BT;
-    for (int tile = blockIdx.y * 4 + wave; tile < ntiles; tile += gridDim.y * 4) {
-        const float4 *Bt = Bb + (size_t) tile * (IXD / 4) * BT;
+    float *out = a.scores + (size_t) bt * (a.max_ctx / IXR);
+    for (int it = 0; tile < ntiles; tile += gridDim.y, ++it) {
         float s[IXH] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int cb = 0; cb < IXD / 4; cb += 16) {
-            float4 kf[16];
+        for (int c = 0; c < CW; ++c)
 #pragma unroll
-            for (int u = 0; u < 16; ++u) kf[u] = ld_nt(&Bt[(cb + u) * BT + lane]);
+            for (int h = 0; h < IXH; ++h) {
+                const float4 q = qs[wave * CW + c][h];
+                s[h] = fmaf(q.x, kf[c].x, s[h]);
+                s[h] = fmaf(q.y, kf[c].y, s[h]);
+                s[h] = fmaf(q.z, kf[c].z, s[h]);
+                s[h] = fmaf(q.w, kf[c].w, s[h]);
+            }
+        const int next = tile + gridDim.y;
+        if (next < ntiles) {
 #pragma unroll
-            for (int u = 0; u < 16; ++u)
-#pragma unroll
-                for (int h = 0; h < IXH; ++h) {
-                    const float4 q = qs[cb + u][h];
-                    s[h] = fmaf(q.x, kf[u].x, s[h]);
-                    s[h] = fmaf(q.y, kf[u].y, s[h]);
-                    s[h] = fmaf(q.z, kf[u].z, s[h]);
-                    s[h] = fmaf(q.w, kf[u].w, s[h]);
-                }
+            for (int c = 0; c < CW; ++c) kf[c] = ld_nt(&Bb[((size_t) next * (IXD / 4) + c) * BT]);
         }
-        const int j = tile * BT + lane;
-        float r = 0.0f;
+        float (*pt)[IXH][BT] = part[it & 1];  // alternating buffers: one barrier per tile
 #pragma unroll
-        for (int h = 0; h < IXH; ++h) r += fmaxf(s[h], 0.0f);
-        if (j < nb) a.scores[(size_t) bt * (a.max_ctx / IXR) + j] = r * inv;
+        for (int h = 0; h < IXH; ++h) pt[wave][h][lane] = s[h];
+        __syncthreads();
+        if (wave == 0) {
+            float r = 0.0f;
+#pragma unroll
+            for (int h = 0; h < IXH; ++h) r += fmaxf(pt[0][h][lane] + pt[1][h][lane] + pt[2][h][lane] + pt[3][h][lane], 0.0f);
+            const int j = tile * BT + lane;
+            if (j < nb) out[j] = r * inv;
+        }
     }
 }
 
-// exclusive prefix count of `flag` over the 1024 threads (index order) and the total, through LDS
-__device__ __forceinline__ int block_excl_count(bool flag, int *wsum, int &total) {
+// exclusive prefix sums of x and y over the 1024 threads in thread order, and their totals (wsum: 32 ints of LDS)
+__device__ __forceinline__ int2 block_excl_scan2(int x, int y, int2 *wsum, int2 &total) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const unsigned long long m = __ballot(flag);
-    const int before_in_wave = __popcll(m & ((1ull << lane) - 1ull));
+    int ix = x, iy = y;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int vx = __shfl_up(ix, off), vy = __shfl_up(iy, off);
+        if (lane >= off) {
+            ix += vx;
+            iy += vy;
+        }
+    }
+    __syncthreads();  // wsum free
+    if (lane == 63) wsum[wave] = make_int2(ix, iy);
     __syncthreads();
-    if (lane == 0) wsum[wave] = __popcll(m);
-    __syncthreads();
-    int before = before_in_wave, tot = 0;
+    int2 before = make_int2(ix - x, iy - y), tot = make_int2(0, 0);
 #pragma unroll
     for (int w = 0; w < 16; ++w) {
-        const int c = wsum[w];
-        before += w < wave ? c : 0;
-        tot += c;
+        const int2 c = wsum[w];
+        if (w < wave) {
+            before.x += c.x;
+            before.y += c.y;
+        }
+        tot.x += c.x;
+        tot.y += c.y;
     }
     total = tot;
     return before;
 }
 
-// grid B nt, 1024 threads
+// grid B nt, 1024 threads.  Thread t owns the contiguous blocks t*per .. t*per+per-1, per = ceil(nb / 1024) rounded
+// up to a multiple of 4 so that they load as float4; with PER > 0 the scores stay in registers (nb <= 1024 PER), with
+// PER == 0 every pass re-reads them (L2-resident).  Radix select on the score bits (scores are >= +0, so their bits
+// order like the values): 11-bit digits [30:20], [19:9] and 9-bit [8:0], each pass a 2048-bin LDS histogram of the
+// entries that match the digits fixed so far, then a block scan (descending) for the digit at which the count from
+// the top reaches `need`.  The histogram has 8 copies, by lane % 8, in different banks: lanes of one atomic
+// instruction that share a digit mostly hit different words.
+template <int PER>
 __global__ void __launch_bounds__(1024) k_ix_select(const IxArgs a) {
-    __shared__ int hist[256];
-    __shared__ int wsum[16];
+    constexpr int NBIN = 2048, NC = 8, HS = NBIN + 1, MAXPER = PER > 0 ? PER : 4;
+    __shared__ int hist[NC * HS];
+    __shared__ int2 wsum[16];
     __shared__ unsigned sh_prefix;
     __shared__ int sh_need;
     const int bt = blockIdx.x, b = bt / a.nt, t = bt - b * a.nt, tid = threadIdx.x;
@@ -196,77 +230,90 @@ __global__ void __launch_bounds__(1024) k_ix_select(const IxArgs a) {
         if (tid == 0) a.nkeys[bt] = P + 1;
         return;
     }
+    // this row of scores is max_ctx / 4 long, a multiple of 64: a float4 that starts below nb stays inside it
     const unsigned *s = reinterpret_cast<const unsigned *>(a.scores + (size_t) bt * (a.max_ctx / IXR));
-    // radix select, most significant byte first: the bits of the top-th largest score (scores are >= 0, so their
-    // bits order like the values) and how many of the entries equal to it are kept
+    const int per = ((nb + 1023) / 1024 + 3) & ~3, j0 = min(tid * per, nb), jn = min(j0 + per, nb);
+    unsigned v[MAXPER];
+    if (PER > 0) {
+#pragma unroll
+        for (int i = 0; i < MAXPER; i += 4) {
+            uint4 u = make_uint4(0u, 0u, 0u, 0u);
+            if (j0 + i < jn) u = *reinterpret_cast<const uint4 *>(s + j0 + i);
+            v[i] = u.x; v[i + 1] = u.y; v[i + 2] = u.z; v[i + 3] = u.w;
+        }
+    }
+    int *hl = hist + (tid & (NC - 1)) * HS;
     unsigned prefix = 0, pmask = 0;
     int need = a.top;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int i = tid; i < 256; i += 1024) hist[i] = 0;
+    constexpr int SHIFT[3] = {20, 9, 0};
+#pragma unroll
+    for (int pass = 0; pass < 3; ++pass) {
+        const int shift = SHIFT[pass];
+        for (int i = tid; i < NC * HS; i += 1024) hist[i] = 0;
         __syncthreads();
-        for (int j = tid; j < nb; j += 1024) {
-            const unsigned u = s[j];
-            if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1);
+        if (PER > 0) {
+#pragma unroll
+            for (int i = 0; i < MAXPER; ++i)
+                if (j0 + i < jn && (v[i] & pmask) == prefix) atomicAdd(&hl[(v[i] >> shift) & (NBIN - 1)], 1);
+        } else {
+            for (int j = j0; j < jn; ++j) {
+                const unsigned u = s[j];
+                if ((u & pmask) == prefix) atomicAdd(&hl[(u >> shift) & (NBIN - 1)], 1);
+            }
         }
         __syncthreads();
-        if (tid < 64) {  // wave 0: digit where the count from the top reaches `need`
-            const int l = tid;  // lane l holds digits 255-4l .. 252-4l (descending)
-            int c[4], sum = 0;
+        // thread t holds digits 2047-2t and 2046-2t: the scan in thread order runs over the digits descending
+        int c0 = 0, c1 = 0;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                c[e] = hist[255 - 4 * l - e];
-                sum += c[e];
-            }
-            // inclusive scan of the lane sums over the wave (descending digit order)
-            int incl = sum;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const int v = __shfl_up(incl, off);
-                if (l >= off) incl += v;
-            }
-            const int excl = incl - sum;
-            const bool here = excl < need && incl >= need;
-            const unsigned long long m = __ballot(here);
-            const int owner = __ffsll((long long) m) - 1;
-            if (l == owner) {
-                int acc = excl, d = 0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (acc + c[e] >= need) {
-                        d = 255 - 4 * l - e;
-                        break;
-                    }
-                    acc += c[e];
-                }
-                sh_prefix = prefix | ((unsigned) d << shift);
-                sh_need = need - acc;  // entries still to take among those with this digit
-            }
+        for (int c = 0; c < NC; ++c) {
+            c0 += hist[c * HS + NBIN - 1 - 2 * tid];
+            c1 += hist[c * HS + NBIN - 2 - 2 * tid];
+        }
+        int2 tot;
+        const int excl = block_excl_scan2(c0 + c1, 0, wsum, tot).x;
+        if (excl < need && excl + c0 + c1 >= need) {  // exactly one thread: counts are >= 0 and the total >= need
+            const bool first = excl + c0 >= need;
+            const unsigned d = first ? NBIN - 1 - 2 * tid : NBIN - 2 - 2 * tid;
+            sh_prefix = prefix | (d << shift);
+            sh_need = need - (first ? excl : excl + c0);  // entries still to take among those with this digit
         }
         __syncthreads();
         prefix = sh_prefix;
         need = sh_need;
-        pmask |= 255u << shift;
-        __syncthreads();
+        pmask |= (pass == 2 ? 511u : 2047u) << shift;
     }
-    const unsigned thr = prefix;  // `need` entries equal to thr are kept, lowest index first
-    // emit the kept blocks in index order: block j's keys 4j..4j+3 at list slot 4 * (kept blocks before j)
-    int base_kept = 0, base_eq = 0;
-    for (int j0 = 0; j0 < nb; j0 += 1024) {
-        const int j = j0 + tid;
-        const unsigned u = j < nb ? s[j] : 0u;
-        const bool eq = j < nb && u == thr;
-        int eq_total;
-        const int eq_before = block_excl_count(eq, wsum, eq_total);
-        const bool keep = j < nb && (u > thr || (eq && base_eq + eq_before < need));
-        int kept_total;
-        const int kept_before = block_excl_count(keep, wsum, kept_total);
-        if (keep) {
-            const int slot = (base_kept + kept_before) * IXR;
+    const unsigned thr = prefix;  // every entry above thr is kept, and the first `need` entries equal to it
+    // this thread's entries above / equal, then one scan gives each thread its list slot and its equal-rank
+    int gt = 0, eq = 0;
+    if (PER > 0) {
 #pragma unroll
-            for (int e = 0; e < IXR; ++e) keys[slot + e] = j * IXR + e;
+        for (int i = 0; i < MAXPER; ++i)
+            if (j0 + i < jn) {
+                gt += v[i] > thr;
+                eq += v[i] == thr;
+            }
+    } else {
+        for (int j = j0; j < jn; ++j) {
+            const unsigned u = s[j];
+            gt += u > thr;
+            eq += u == thr;
         }
-        base_kept += kept_total;
-        base_eq += eq_total;
+    }
+    int2 tot;
+    const int2 before = block_excl_scan2(gt, eq, wsum, tot);
+    int slot = before.x + min(before.y, need), eq_rank = before.y;
+    int4 *kv = reinterpret_cast<int4 *>(keys);
+    auto emit = [&](int j, unsigned u) {
+        const bool keep = u > thr || (u == thr && eq_rank < need);
+        eq_rank += u == thr;
+        if (keep) kv[slot++] = make_int4(j * IXR, j * IXR + 1, j * IXR + 2, j * IXR + 3);
+    };
+    if (PER > 0) {
+#pragma unroll
+        for (int i = 0; i < MAXPER; ++i)
+            if (j0 + i < jn) emit(j0 + i, v[i]);
+    } else {
+        for (int j = j0; j < jn; ++j) emit(j, s[j]);
     }
     // the incomplete tail block is always visible (faie2fn.cu:1630)
     const int tail0 = nb * IXR;
@@ -311,11 +358,18 @@ int qsa_select_launch(const QsaIndexer &p, float *work, size_t work_bytes, const
     a.nkeys = a.keys + bt * ((size_t) p.top * IXR + IXR);
     *keys = a.keys;
     *nkeys = a.nkeys;
+    // about 1024 workgroups of scoring over all queries, at most one per tile
     const int tiles = p.max_ctx / IXR / BT;
-    const int G = std::max(1, std::min(128, (tiles + 3) / 4));
+    const int G = (int) std::max<size_t>(1, std::min<size_t>(tiles, (1024 + bt - 1) / bt));
+    const int nbmax = p.max_ctx / IXR;
     hipLaunchKernelGGL(k_ix_prep, dim3(p.B), dim3(256), 0, st, a);
     hipLaunchKernelGGL(k_ix_score, dim3((unsigned) bt, G), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(k_ix_select, dim3((unsigned) bt), dim3(1024), 0, st, a);
+    if (nbmax <= 1024 * 8)
+        hipLaunchKernelGGL(k_ix_select<8>, dim3((unsigned) bt), dim3(1024), 0, st, a);
+    else if (nbmax <= 1024 * 32)
+        hipLaunchKernelGGL(k_ix_select<32>, dim3((unsigned) bt), dim3(1024), 0, st, a);
+    else
+        hipLaunchKernelGGL(k_ix_select<0>, dim3((unsigned) bt), dim3(1024), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
 }

@@ -124,3 +124,12 @@ def test_qsa_ties_keep_lowest_index(fnlib):
                                   c["pos"], top=32)
     assert not sc[0, 0, :nb].any()
     assert mask[0, 0, :32].all() and not mask[0, 0, 32:].any()
+
+
+@pytest.mark.parametrize("max_ctx,pos,top", [(16384, 12001, 512), (33024, 30001, 700), (131328, 9999, 512)])
+def test_qsa_select_storage_paths(fnlib, max_ctx, pos, top):
+    """The selection keeps each thread's scores in registers up to 8 blocks a thread (here 3), up to 32 (here 8, for a
+    cache past 8192 blocks) and re-reads them from memory for caches past 32768 blocks."""
+    _say(f"qsa select paths max_ctx={max_ctx} pos={pos} top={top}")
+    c = make_case(1, 1, max_ctx, [pos], seed=5 + pos % 7)
+    assert run_and_check(fnlib, c, top=top) == 1
