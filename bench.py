@@ -10,7 +10,10 @@ Also reported (``extra``): config 0 (DeltaNet core, B = 1), config 1 (fused bloc
 (GQA decode at 4K / 32K / 128K context, B = 1 and 16), config 4 (hybrid 36 + 12 layers, B = 16, context 32K),
 the streaming-copy yardstick, and the float64 CPU oracle timed on this box's host cores (``cpu_baseline``).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+Also (``extra``): the GEMV of the projections around the path (GGUF formats, cold weights) at the reference model's
+and BASELINE's shapes.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu] [--gemv] [--counters]
 """
 
 import argparse
@@ -268,6 +271,32 @@ def copy_yardstick(lib, stream, nbytes=1 << 30, reps=20):
     return 2 * nbytes / (ms * 1e-3) / 1e9
 
 
+# the projections on the path: reference model (hidden 2560; flashnext/inspect_fn.txt:77-100, 132-137) and BASELINE
+# hidden 2048 (8192 mixed channels in, 4096 value channels out)
+GEMV_SHAPES = (("qkv_iq4xs", 23, 10240, 2560), ("ssm_out_q8_0", 8, 2560, 6144), ("z_q6k", 14, 6144, 2560),
+               ("attn_q_iq4xs", 23, 12288, 2560), ("attn_v_q6k", 14, 512, 2560), ("ab_bf16", 30, 96, 2560),
+               ("qkv2048_iq4xs", 23, 8192, 2048), ("ssm_out2048_q8_0", 8, 2048, 4096))
+
+
+def gemv_bytes(qtype, rows, cols, nt):
+    """Algorithmic bytes of one GEMV call: the weight once, x and y once."""
+    return rows * fn.row_bytes(qtype, cols) + 4 * nt * (rows + cols)
+
+
+def gemv_extras(lib, iters=50, nts=(1, 8)):
+    """µs per call and GB/s of the projection GEMVs, weights cold (each call reads its own copy; the copies exceed
+    the Infinity Cache), calls replayed as one hipGraph (fn_bench_gemv)."""
+    out = {}
+    lib.bench_hot(False)
+    for name, t, rows, cols in GEMV_SHAPES:
+        for nt in nts:
+            ms = lib.bench_gemv(t, rows, cols, nt=nt, iters=iters)
+            by = gemv_bytes(t, rows, cols, nt)
+            out[f"gemv_{name}_{rows}x{cols}_nt{nt}"] = {"us": round(ms * 1e3, 2), "bytes": by,
+                                                        "gbs": round(by / (ms * 1e-3) / 1e9, 1)}
+    return out
+
+
 def cpu_baseline(budget_s=12.0):
     """The float64 C oracle (OpenMP over all host cores) on a bounded sample of the headline workload: B = 64
     sequences of one layer, decode steps repeated until about budget_s seconds of CPU work.  Same unit as value."""
@@ -302,6 +331,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gemv", action="store_true", help="projection GEMV timings only (fn_bench_gemv legs)")
     ap.add_argument("--counters", action="store_true",
                     help="counter-collection workload only: 3 plain copies of 1 GiB (the calibration kernel) and one "
                          "eager pass of the config-2 stack (36 dispatches of the fused DeltaNet kernel)")
@@ -315,6 +345,12 @@ def main():
         raise RuntimeError("no HIP device visible")
     stream = hiprt.Stream()
     steps, warmup = max(1, args.steps), max(0, args.warmup)
+    if args.gemv:
+        res = gemv_extras(lib)
+        for k, v in res.items():
+            log(f"[bench] {k}: {v}")
+        print(json.dumps({"gemv": res}), flush=True)
+        return
     if args.counters:
         nb = 1 << 30
         a, b = hiprt.Buf(nb), hiprt.Buf(nb)
@@ -391,6 +427,7 @@ def main():
         hook_ms = (time.perf_counter() - t0) * 1e3
         extra["config2_host_hook_pcie_inclusive"] = {"ms_per_layer_step": round(hook_ms, 2),
                                                      "gbs": round(fn_synth.gdn_block_bytes(64) / hook_ms / 1e6, 1)}
+        extra.update(gemv_extras(lib))
         ms, nbytes = hybrid_config4(lib, steps, warmup)
         extra["config4_hybrid_b16_ctx32768"] = {"ms_per_step": round(ms, 4), "us_per_token": round(ms * 1e3 / 16, 2),
                                                "tokens_per_s": round(16 * 1e3 / ms, 1), "bytes_per_step": nbytes,

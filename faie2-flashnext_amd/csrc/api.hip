@@ -6,6 +6,7 @@
 // the reference's unit-test-hook style, faie2fn.cu:2745) and the device-buffer entry points an engine calls.
 #include "engine.h"
 #include "qsa.h"
+#include "hostbuf.h"
 
 #include <cstring>
 #include <vector>
@@ -21,7 +22,9 @@ const char *error_cstr() { return g_err.c_str(); }
 
 }  // namespace fn
 
+using fn::DevBufs;
 using fn::set_error;
+using fn::use_device0;
 
 // ---------------------------------------------------------------------------------------------
 // 1. reference API
@@ -29,43 +32,11 @@ using fn::set_error;
 namespace {
 
 const char *kNoModel =
-    "not built: libfaie2fn.so carries the decode-attention path only (DeltaNet block + GQA decode); model loading, "
-    "the forward pass, GEMV, MoE and routing are not part of it";
+    "not built: libfaie2fn.so carries the decode-attention path (DeltaNet block, GQA and QSA decode) and the GEMV "
+    "of its projections; model loading, the forward pass, MoE and routing are not part of it";
 
 // switches the reference exposes for its forward; kept so scripts that set them still run
-int g_pdl = 1, g_early = 1, g_moe_var = 0, g_bench_hot = 0;
-
-// device buffers of one host-hook call, released on every return path
-struct DevBufs {
-    std::vector<void *> ptrs;
-    ~DevBufs() {
-        for (void *p : ptrs) (void) hipFree(p);
-    }
-    template <typename T> int alloc(T **p, size_t n) {
-        *p = nullptr;
-        if (n == 0) n = 1;
-        hipError_t e = hipMalloc((void **) p, n * sizeof(T));
-        if (e != hipSuccess) {
-            set_error(std::string("hipMalloc(") + std::to_string(n * sizeof(T)) + " B) -> " + hipGetErrorString(e));
-            return -1;
-        }
-        ptrs.push_back(*p);
-        return 0;
-    }
-    template <typename T> int up(T **p, const T *h, size_t n) {
-        if (alloc(p, n)) return -1;
-        FN_CK(hipMemcpy(*p, h, n * sizeof(T), hipMemcpyHostToDevice));
-        return 0;
-    }
-};
-
-int use_device0() {
-    int n = 0;
-    FN_CK(hipGetDeviceCount(&n));
-    if (n < 1) FN_FAIL("no HIP device");
-    FN_CK(hipSetDevice(0));
-    return 0;
-}
+int g_pdl = 1, g_early = 1, g_moe_var = 0;
 
 }  // namespace
 
@@ -80,18 +51,11 @@ FN_API int fn_reset(void) { return fn::path_reset(); }
 FN_API int fn_use_graphs(int on) { return fn::path_use_graphs(on); }
 FN_API int fn_forward(const int32_t *, int, float *, int32_t *) { FN_FAIL("not loaded"); }
 FN_API int fn_debug_layers(float *) { FN_FAIL("not loaded"); }
-FN_API int fn_test_dequant(uint32_t, const uint8_t *, int, int, float *) { FN_FAIL(kNoModel); }
-FN_API void fn_gemv_override(int, int, int, int) {}
-FN_API void fn_gemv_waves(int) {}
 FN_API void fn_pdl(int on) { g_pdl = on != 0; }
 FN_API void fn_early(int on) { g_early = on != 0; }
 FN_API void fn_moe_var(int v) { g_moe_var = v; }
 FN_API void fn_moe_override(int, int, int, int) {}
-FN_API int fn_gemv_plan(uint32_t, int, int, int *) { FN_FAIL(kNoModel); }
-FN_API void fn_bench_hot(int on) { g_bench_hot = on; }
-FN_API int fn_bench_gemv(uint32_t, int, int, int, int, float *) { FN_FAIL(kNoModel); }
 FN_API int fn_bench_route(int, int, int, const float *, int, int *, float *, float *) { FN_FAIL(kNoModel); }
-FN_API int fn_test_gemv(uint32_t, const uint8_t *, int, int, const float *, int, float *) { FN_FAIL(kNoModel); }
 
 // ---------------------------------------------------------------------------------------------
 // 3. device entry points

@@ -1,0 +1,62 @@
+// Internal API of the GGUF weight formats and the GEMV of the projections around the decode path
+// (quant.hip).  Type ids are the GGUF ones the reference uses (engine/faie2fn.cu:78-81).
+#pragma once
+
+#include "common.cuh"
+
+#include <cstddef>
+
+namespace fn {
+
+enum : uint32_t {
+    QT_Q8_0 = 8, QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14, QT_IQ4_NL = 20, QT_IQ4_XS = 23, QT_BF16 = 30,
+};
+
+// Packed ("plane") layout of a rows x cols weight.  A GGUF row is a run of blocks, each an array of structs
+// (scales and quants interleaved, 2-byte aligned at best).  The packed layout moves every field of the format
+// into its own plane, [rows][blocks per row][field bytes], so that each lane of the GEMV reads its group's quants
+// and scales with naturally aligned 16/8/2-byte loads.  Bytes are moved, never changed: the packed weight holds
+// exactly the GGUF bytes (plus alignment padding between planes).
+struct QLayout {
+    uint32_t type = 0;
+    int rows = 0, cols = 0;
+    int qk = 0;                 // values per GGUF block
+    int bb = 0;                 // bytes per GGUF block
+    int nplanes = 0;
+    int fbytes[3] = {0, 0, 0};  // bytes per block in each plane
+    int foff[3] = {0, 0, 0};    // offset of each plane's field inside the GGUF block
+    size_t rs[3] = {0, 0, 0};   // row stride of each plane
+    size_t off[3] = {0, 0, 0};  // byte offset of each plane in the packed buffer
+    size_t bytes = 0;           // packed bytes in all
+    size_t row_bytes = 0;       // GGUF bytes per row
+};
+
+// false (and an fn_error message) for a type this library does not read or a shape it cannot split into whole
+// blocks of 32 values
+bool qlayout(uint32_t type, int rows, int cols, QLayout &L);
+
+// Launch plan of one GEMV (the values fn_gemv_plan reports, include/faie2fn.h).  It depends on the shape only, never
+// on the number of tokens, so token t of an nt-token call gets the same bits as a one-token call on x[t].
+struct GemvPlan {
+    int gv = 32;      // values per group (a lane's unit of work)
+    int waves = 8;    // waves per workgroup
+    int ks = 1;       // workgroups along a row (split-K; partials are summed in a second, fixed-order pass)
+    int rpw = 32;     // rows per workgroup (8 waves x 64 / lpr rows)
+    int lpr = 16;     // lanes per row (16, 32 or 64)
+    int ntiles = 0;   // row tiles (workgroups along the rows)
+    int ngroups = 0;  // groups per row
+};
+
+GemvPlan gemv_plan(const QLayout &L);
+void gemv_override(int ks);   // 0 = no split-K (the default plan)
+size_t gemv_work_bytes(const QLayout &L, int nt);
+
+// GGUF rows (device) -> packed planes (device); stream-ordered
+int quant_pack_launch(const QLayout &L, const uint8_t *raw, uint8_t *packed, hipStream_t st);
+// packed planes -> float rows [rows][cols], bit for bit the GGUF decode of the format
+int quant_dequant_launch(const QLayout &L, const uint8_t *packed, float *out, hipStream_t st);
+// y[t][r] = sum_c W[r][c] x[t][c] for t < nt (1..8); x [nt][cols], y [nt][rows]; work: gemv_work_bytes() bytes
+int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, float *y, float *work,
+                size_t work_bytes, hipStream_t st);
+
+}  // namespace fn

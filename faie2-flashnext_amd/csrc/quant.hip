@@ -1,0 +1,643 @@
+// GGUF weight formats and the GEMV of the projections around the decode path, for gfx950.
+//
+// The reference decodes its weights with ggml's arithmetic (engine/faie2fn.cu:343-689) and runs them through a
+// tiled, split-K GEMV (faie2fn.cu:690-1042, 2033-2116) whose test hooks are fn_test_dequant / fn_test_gemv
+// (faie2fn.cu:2751-2782, 2916-2935).  This file is a gfx950 design of the same operations:
+//
+//   * packing (quant_pack_launch): every field of a format goes to its own plane (QLayout), so each lane reads
+//     its group's quants with 16-byte loads and its scales with 8/2-byte loads, all naturally aligned;
+//   * decoding: one lane decodes one group of 32 values into exact small-integer floats q[32] plus, per half of
+//     16 values, a scale s and an offset m, such that the GGUF value is fl(s * q - m) rounded once -- the value
+//     ggml's dequantize_row_* computes (s * q is exact for every format whose m is not zero);
+//   * GEMV: 16 lanes per row, four rows per wave, four waves per workgroup; each lane walks the row's groups
+//     with stride 16, keeps the next group's loads in flight while it does the current one's FMAs, and the row
+//     sum is a 16-lane DPP reduction.  Short rows split K over workgroups whose partials a second pass adds in a
+//     fixed order, so results do not depend on timing.  For formats without an offset the scale multiplies the
+//     16-value dot product instead of each weight.
+#include "quant.h"
+
+#include <algorithm>
+
+namespace fn {
+
+namespace {
+
+constexpr int MAXNT = 8;
+
+// ------------------------------------------------------------------------------------------------------------
+// the IQ4 codebook (the GGUF format's 16 non-uniform levels), and its signed bytes packed four to a word for
+// byte-permute lookups: word k holds entries 4k..4k+3, entry 4k in the low byte
+
+constexpr int kIq4Levels[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+constexpr uint32_t pack4(int k) {
+    return (uint32_t) (uint8_t) kIq4Levels[4 * k] | (uint32_t) (uint8_t) kIq4Levels[4 * k + 1] << 8 |
+           (uint32_t) (uint8_t) kIq4Levels[4 * k + 2] << 16 | (uint32_t) (uint8_t) kIq4Levels[4 * k + 3] << 24;
+}
+constexpr uint32_t KV0 = pack4(0), KV1 = pack4(1), KV2 = pack4(2), KV3 = pack4(3);
+static_assert(KV0 == 0xBFAD9881u && KV3 == 0x71594535u, "IQ4 level packing");
+
+// four nibble indices (one per byte, 0..15) -> their four signed levels as bytes.  v_perm_b32 picks bytes out of
+// an 8-byte pair by selector 0..7, so levels 0..7 and 8..15 are looked up separately with the low 3 bits and the
+// index's bit 3 then chooses between the two results byte by byte.
+__device__ __forceinline__ uint32_t iq4_levels(uint32_t n) {
+    const uint32_t s = n & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(KV1, KV0, s);
+    const uint32_t hi = __builtin_amdgcn_perm(KV3, KV2, s);
+    const uint32_t sel = ((n >> 1) & 0x04040404u) | 0x03020100u;
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+__device__ __forceinline__ float sbyte(uint32_t w, int k) { return (float) ((int32_t) (w << (24 - 8 * k)) >> 24); }
+__device__ __forceinline__ float h2f(uint32_t bits) {
+    return (float) __builtin_bit_cast(_Float16, (unsigned short) (bits & 0xFFFFu));
+}
+// byte k (0..11) of the 12 bytes w0 w1 w2
+__device__ __forceinline__ uint32_t byte12(uint32_t w0, uint32_t w1, uint32_t w2, int k) {
+    const uint32_t w = k < 4 ? w0 : (k < 8 ? w1 : w2);
+    return (w >> (8 * (k & 3))) & 0xFFu;
+}
+
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void ld16(const uint8_t *p, uint32_t *w) {
+    const v4u v = *reinterpret_cast<const v4u *>(p);
+    w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+}
+__device__ __forceinline__ void ld8(const uint8_t *p, uint32_t *w) {
+    const v2u v = *reinterpret_cast<const v2u *>(p);
+    w[0] = v.x, w[1] = v.y;
+}
+__device__ __forceinline__ uint32_t ld2(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
+
+// planes of a packed weight as the kernels see them
+struct PP {
+    const uint8_t *p0, *p1, *p2;
+    size_t rs0, rs1, rs2;
+};
+
+// the three planes of one row
+struct RP {
+    const uint8_t *b0, *b1, *b2;
+};
+__device__ __forceinline__ RP row_planes(const PP &P, int row) {
+    return RP{P.p0 + (size_t) row * P.rs0, P.p1 + (size_t) row * P.rs1, P.p2 + (size_t) row * P.rs2};
+}
+
+// one decoded group: GGUF value j = fl(s[j / 16] * q[j] - m[j / 16])
+struct Grp {
+    float q[32];
+    float s[2], m[2];
+};
+
+template <uint32_t TY> struct Q;
+
+// groups a GEMV lane keeps in flight per batch for a format of nw raw words per group (two batches live at once)
+constexpr int prefetch_groups(int nw) { return nw <= 8 ? 4 : (nw <= 12 ? 2 : 1); }
+
+// BF16: a group is 32 consecutive values (64 bytes); q holds the values themselves, s = 1
+template <> struct Q<QT_BF16> {
+    static constexpr int NW = 16;
+    static constexpr int U = prefetch_groups(NW);
+    static constexpr bool MIN = false;
+    __device__ static void load(const RP &R, int g, uint32_t *w) {
+        const uint8_t *p = R.b0 + 64 * g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ld16(p + 16 * i, w + 4 * i);
+    }
+    __device__ static void unpack(const uint32_t *w, int, Grp &o) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            o.q[2 * i] = __uint_as_float(w[i] << 16);
+            o.q[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+        }
+        o.s[0] = o.s[1] = 1.0f;
+        o.m[0] = o.m[1] = 0.0f;
+    }
+};
+
+// Q8_0: 32 int8 quants, one fp16 scale (ggml: y = d * q)
+template <> struct Q<QT_Q8_0> {
+    static constexpr int NW = 9;
+    static constexpr int U = prefetch_groups(NW);
+    static constexpr bool MIN = false;
+    __device__ static void load(const RP &R, int g, uint32_t *w) {
+        const uint8_t *q = R.b0 + 32 * g;
+        ld16(q, w);
+        ld16(q + 16, w + 4);
+        w[8] = ld2(R.b1 + 2 * g);
+    }
+    __device__ static void unpack(const uint32_t *w, int, Grp &o) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o.q[4 * i + k] = sbyte(w[i], k);
+        o.s[0] = o.s[1] = h2f(w[8]);
+        o.m[0] = o.m[1] = 0.0f;
+    }
+};
+
+// IQ4_NL: 16 bytes of nibble indices (byte b: low nibble = value b, high nibble = value b + 16), fp16 scale
+// (ggml: y = d * level)
+template <> struct Q<QT_IQ4_NL> {
+    static constexpr int NW = 5;
+    static constexpr int U = prefetch_groups(NW);
+    static constexpr bool MIN = false;
+    __device__ static void load(const RP &R, int g, uint32_t *w) {
+        ld16(R.b0 + 16 * g, w);
+        w[4] = ld2(R.b1 + 2 * g);
+    }
+    __device__ static void levels(const uint32_t *w, Grp &o) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = iq4_levels(w[i] & 0x0F0F0F0Fu), hi = iq4_levels((w[i] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                o.q[4 * i + k] = sbyte(lo, k);
+                o.q[16 + 4 * i + k] = sbyte(hi, k);
+            }
+        }
+    }
+    __device__ static void unpack(const uint32_t *w, int, Grp &o) {
+        levels(w, o);
+        o.s[0] = o.s[1] = h2f(w[4]);
+        o.m[0] = o.m[1] = 0.0f;
+    }
+};
+
+// IQ4_XS: super-blocks of 256 (d fp16, scales_h u16, scales_l[4], qs[128]); group ib has a 6-bit scale ls and
+// the IQ4_NL nibble layout (ggml: dl = d * (ls - 32), y = dl * level)
+template <> struct Q<QT_IQ4_XS> {
+    static constexpr int NW = 6;
+    static constexpr int U = prefetch_groups(NW);
+    static constexpr bool MIN = false;
+    __device__ static void load(const RP &R, int g, uint32_t *w) {
+        ld16(R.b0 + 16 * g, w);  // super-block g / 8 at 128 (g / 8), group g % 8 at 16 (g % 8) inside it
+        ld8(R.b1 + 8 * (g >> 3), w + 4);
+    }
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o) {
+        const int ib = g & 7;
+        Q<QT_IQ4_NL>::levels(w, o);
+        const uint32_t sl = (w[5] >> (8 * (ib >> 1))) >> (4 * (ib & 1)) & 0xFu;
+        const uint32_t sh = (w[4] >> (16 + 2 * ib)) & 3u;
+        const float dl = h2f(w[4]) * (float) ((int) (sl | sh << 4) - 32);
+        o.s[0] = o.s[1] = dl;
+        o.m[0] = o.m[1] = 0.0f;
+    }
+};
+
+// 6-bit scale and min of group ib from the 12 packed scale bytes of Q4_K / Q5_K (ggml get_scale_min_k4)
+__device__ __forceinline__ void scale_min_k(const uint32_t *h, int ib, float &sc, float &mn) {
+    const uint32_t b_ib = byte12(h[0], h[1], h[2], ib), b_4 = byte12(h[0], h[1], h[2], ib + 4);
+    if (ib < 4) {
+        sc = (float) (b_ib & 63u);
+        mn = (float) (b_4 & 63u);
+    } else {
+        const uint32_t b_m4 = byte12(h[0], h[1], h[2], ib - 4);
+        sc = (float) ((b_4 & 0xFu) | (b_m4 >> 6) << 4);
+        mn = (float) ((b_4 >> 4) | (b_ib >> 6) << 4);
+    }
+}
+
+// Q4_K: super-blocks of 256 (d, dmin fp16, 12 scale bytes, qs[128]); group ib reads the low (even ib) or high
+// (odd ib) nibbles of qs[32 (ib/2) .. +31] (ggml: y = d*sc * q - dmin*m)
+template <> struct Q<QT_Q4_K> {
+    static constexpr int NW = 12;
+    static constexpr int U = prefetch_groups(NW);
+    static constexpr bool MIN = true;
+    __device__ static void load(const RP &R, int g, uint32_t *w) {
+        const uint8_t *q = R.b0 + 16 * (g & ~1);  // the 32 bytes of groups 2k and 2k + 1
+        ld16(q, w);
+        ld16(q + 16, w + 4);
+        ld16(R.b1 + 16 * (g >> 3), w + 8);
+    }
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o) {
+        const int ib = g & 7, sh = 4 * (ib & 1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o.q[4 * i + k] = (float) ((w[i] >> (8 * k + sh)) & 0xFu);
+        float sc, mn;
+        scale_min_k(w + 9, ib, sc, mn);
+        o.s[0] = o.s[1] = h2f(w[8]) * sc;
+        o.m[0] = o.m[1] = h2f(w[8] >> 16) * mn;
+    }
+};
+
+// Q5_K: Q4_K plus a fifth bit per value: bit ib of qh[j] (ggml: q = nibble + 16 * bit)
+template <> struct Q<QT_Q5_K> {
+    static constexpr int NW = 20;
+    static constexpr int U = prefetch_groups(NW);
+    static constexpr bool MIN = true;
+    __device__ static void load(const RP &R, int g, uint32_t *w) {
+        const uint8_t *q = R.b0 + 16 * (g & ~1);
+        ld16(q, w);
+        ld16(q + 16, w + 4);
+        const uint8_t *h = R.b1 + 32 * (g >> 3);
+        ld16(h, w + 8);
+        ld16(h + 16, w + 12);
+        ld16(R.b2 + 16 * (g >> 3), w + 16);
+    }
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o) {
+        const int ib = g & 7, sh = 4 * (ib & 1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                o.q[4 * i + k] = (float) (((w[i] >> (8 * k + sh)) & 0xFu) | ((w[8 + i] >> (8 * k + ib)) & 1u) << 4);
+        float sc, mn;
+        scale_min_k(w + 17, ib, sc, mn);
+        o.s[0] = o.s[1] = h2f(w[16]) * sc;
+        o.m[0] = o.m[1] = h2f(w[16] >> 16) * mn;
+    }
+};
+
+// Q6_K: super-blocks of 256 (ql[128], qh[64], int8 scales[16], d fp16).  Value 128 n + 32 qu + l (n < 2, qu < 4,
+// l < 32): low 4 bits from nibble (qu >> 1) of ql[64 n + 32 (qu & 1) + l], high 2 bits from bits 2 qu of
+// qh[32 n + l], scale scales[8 n + 2 qu + l / 16] (ggml: y = d * sc * (q - 32))
+template <> struct Q<QT_Q6_K> {
+    static constexpr int NW = 18;
+    static constexpr int U = prefetch_groups(NW);
+    static constexpr bool MIN = false;
+    __device__ static void load(const RP &R, int g, uint32_t *w) {
+        const int ib = g & 7, n = ib >> 2, qu = ib & 3, sb = g >> 3;
+        const uint8_t *l = R.b0 + 128 * sb + 64 * n + 32 * (qu & 1);
+        ld16(l, w);
+        ld16(l + 16, w + 4);
+        const uint8_t *h = R.b1 + 64 * sb + 32 * n;
+        ld16(h, w + 8);
+        ld16(h + 16, w + 12);
+        const uint8_t *t = R.b2 + 18 * sb;
+        w[16] = ld2(t + 8 * n + 2 * qu);
+        w[17] = ld2(t + 16);
+    }
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o) {
+        const int qu = g & 3, lsh = 4 * (qu >> 1), hsh = 2 * qu;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                o.q[4 * i + k] =
+                    (float) ((int) (((w[i] >> (8 * k + lsh)) & 0xFu) | ((w[8 + i] >> (8 * k + hsh)) & 3u) << 4) - 32);
+        const float d = h2f(w[17]);
+        o.s[0] = d * sbyte(w[16], 0);
+        o.s[1] = d * sbyte(w[16], 1);
+        o.m[0] = o.m[1] = 0.0f;
+    }
+};
+
+template <uint32_t TY> __device__ __forceinline__ void decode(const PP &P, int row, int g, Grp &o) {
+    uint32_t w[Q<TY>::NW];
+    Q<TY>::load(row_planes(P, row), g, w);
+    Q<TY>::unpack(w, g, o);
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// kernels
+
+// GGUF rows -> planes: one thread per (row, block), plain byte copies (load-time work)
+__global__ void k_pack(QLayout L, const uint8_t *__restrict__ raw, uint8_t *__restrict__ out) {
+    const size_t nb = (size_t) (L.cols / L.qk);
+    const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t) L.rows * nb) return;
+    const size_t row = i / nb, blk = i % nb;
+    const uint8_t *src = raw + row * L.row_bytes + blk * L.bb;
+    for (int p = 0; p < L.nplanes; ++p) {
+        uint8_t *dst = out + L.off[p] + row * L.rs[p] + blk * L.fbytes[p];
+        for (int b = 0; b < L.fbytes[p]; ++b) dst[b] = src[L.foff[p] + b];
+    }
+}
+
+// planes -> float rows, one thread per (row, group of 32), the GGUF value fl(s * q - m) rounded once
+template <uint32_t TY> __global__ void k_dequant(PP P, int rows, int G, int cols, float *__restrict__ out) {
+    const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t) rows * G) return;
+    const int row = (int) (i / G), g = (int) (i % G);
+    Grp o;
+    decode<TY>(P, row, g, o);
+    float4 *dst = reinterpret_cast<float4 *>(out + (size_t) row * cols + (size_t) g * 32);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int h = c >> 2;
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float q = o.q[4 * c + k];
+            v[k] = TY == QT_BF16 ? q : __builtin_fmaf(o.s[h], q, -o.m[h]);
+        }
+        dst[c] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
+// groups of x per LDS chunk for NT tokens: NT * KC groups * 128 B <= 32 KB, and at least one group per lane of a row
+// (NT * LPR * 128 B <= 64 KB); KC is a multiple of LPR so that the lane that owns a group (lane = group mod LPR) does
+// not depend on the chunking
+template <int NT, int LPR> constexpr int kc_groups() {
+    return (256 / NT) / LPR * LPR > LPR ? (256 / NT) / LPR * LPR : LPR;
+}
+
+// sum over the LPR lanes of a row (16: one DPP row, 32: half a wave, 64: the wave); every lane of the row gets it
+template <int LPR> __device__ __forceinline__ float lane_row_sum(float v) {
+    if constexpr (LPR == 16) return row_sum(v);
+    else if constexpr (LPR == 32) return half_sum(v);
+    else return wave_sum(v);
+}
+
+// one group's contribution to the NT accumulators; x of the group sits in LDS as float4 column c of token t at
+// xs[(t * 8 + c) * KCP + gr].  The arithmetic (and its order) does not depend on NT: token t of an NT-token call
+// gets the bits a one-token call gets.
+template <uint32_t TY, int NT>
+__device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float4 *xs, int KCP, int gr, float *acc) {
+    Grp o;
+    Q<TY>::unpack(w, g, o);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if constexpr (Q<TY>::MIN) {
+            float wv[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) wv[j] = __builtin_fmaf(o.s[h], o.q[16 * h + j], -o.m[h]);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                float a = acc[t];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float4 xv = xs[(t * 8 + 4 * h + c) * KCP + gr];
+                    a = __builtin_fmaf(wv[4 * c], xv.x, a);
+                    a = __builtin_fmaf(wv[4 * c + 1], xv.y, a);
+                    a = __builtin_fmaf(wv[4 * c + 2], xv.z, a);
+                    a = __builtin_fmaf(wv[4 * c + 3], xv.w, a);
+                }
+                acc[t] = a;
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float4 xv = xs[(t * 8 + 4 * h + c) * KCP + gr];
+                    d0 = __builtin_fmaf(o.q[16 * h + 4 * c], xv.x, d0);
+                    d1 = __builtin_fmaf(o.q[16 * h + 4 * c + 1], xv.y, d1);
+                    d0 = __builtin_fmaf(o.q[16 * h + 4 * c + 2], xv.z, d0);
+                    d1 = __builtin_fmaf(o.q[16 * h + 4 * c + 3], xv.w, d1);
+                }
+                acc[t] = __builtin_fmaf(o.s[h], d0 + d1, acc[t]);
+            }
+        }
+    }
+}
+
+// GEMV rows of one workgroup: 8 waves = 8 * (64 / LPR) rows starting at tile * 8 * (64 / LPR), groups [g0, g1);
+// LPR lanes per row, lane li owning the row's groups li, li + LPR, ...  The workgroup walks its groups in chunks of
+// KC: the chunk of x (all NT tokens) is loaded first, then the first U groups of every lane, then x goes to LDS
+// (transposed so that the lanes of a row read consecutive float4: no bank conflicts); each lane then keeps the next
+// U groups' loads in flight while it does the FMAs of the current U.  out[t * rows + row] = the row's sum.
+template <uint32_t TY, int NT, int LPR>
+__device__ __forceinline__ void gemv_rows(const PP &P, int rows, int tile, int g0, int g1, const float *__restrict__ x,
+                                          int cols, float *__restrict__ out, float4 *xs) {
+    constexpr int KC = kc_groups<NT, LPR>(), KCP = KC + 1, NW = Q<TY>::NW, U = Q<TY>::U, RPW = 64 / LPR;
+    constexpr int NXT = NT * 8 * KC / 512;  // float4 of x per thread per chunk
+    const int tid = threadIdx.x, lane = tid & 63, li = lane % LPR;
+    const int row = tile * 8 * RPW + (tid >> 6) * RPW + lane / LPR;
+    const bool live = row < rows;
+    const RP R = row_planes(P, live ? row : 0);
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    for (int c0 = g0; c0 < g1; c0 += KC) {
+        const int c1 = min(g1, c0 + KC), nch = c1 - c0, nx = NT * 8 * nch;
+        float4 xr[NXT];
+#pragma unroll
+        for (int j = 0; j < NXT; ++j) {
+            const int e = tid + 512 * j;
+            if (e < nx) {
+                const int tg = e >> 3, t = tg / nch, gr = tg - t * nch;
+                xr[j] = *reinterpret_cast<const float4 *>(x + (size_t) t * cols + (size_t) (c0 + gr) * 32 + 4 * (e & 7));
+            }
+        }
+        int g = live ? c0 + li : c1;
+        uint32_t wa[U][NW];
+        if (g < c1) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) Q<TY>::load(R, min(g + LPR * u, c1 - 1), wa[u]);
+        }
+        __syncthreads();  // every wave is done reading the previous chunk
+#pragma unroll
+        for (int j = 0; j < NXT; ++j) {
+            const int e = tid + 512 * j;
+            if (e < nx) {
+                const int tg = e >> 3, t = tg / nch, gr = tg - t * nch;
+                xs[(t * 8 + (e & 7)) * KCP + gr] = xr[j];
+            }
+        }
+        __syncthreads();
+        while (g < c1) {
+            const int gn = g + LPR * U;
+            uint32_t wb[U][NW];
+            if (gn < c1) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) Q<TY>::load(R, min(gn + LPR * u, c1 - 1), wb[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (g + LPR * u < c1) accumulate<TY, NT>(wa[u], g + LPR * u, xs, KCP, g + LPR * u - c0, acc);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int i = 0; i < NW; ++i) wa[u][i] = wb[u][i];
+            g = gn;
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = lane_row_sum<LPR>(acc[t]);
+    if (li == 0 && live) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) out[(size_t) t * rows + row] = acc[t];
+    }
+}
+
+template <int NT, int LPR> constexpr int xs_float4() { return NT * 8 * (kc_groups<NT, LPR>() + 1); }
+
+// one format: grid (row tiles, K splits of gps groups); split s writes its partial sums to out + s * NT * rows
+template <uint32_t TY, int NT, int LPR>
+__global__ void __launch_bounds__(512) k_gemv(PP P, int rows, int G, int gps, const float *__restrict__ x, int cols,
+                                                float *__restrict__ out) {
+    __shared__ float4 xs[xs_float4<NT, LPR>()];
+    const int g0 = blockIdx.y * gps, g1 = min(G, g0 + gps);
+    gemv_rows<TY, NT, LPR>(P, rows, blockIdx.x, g0, g1, x, cols, out + (size_t) blockIdx.y * NT * rows, xs);
+}
+
+// y[i] = sum over splits s = 0..ks-1 of part[s][i], in that order
+__global__ void k_gemv_reduce(const float *__restrict__ part, int ks, int n, float *__restrict__ y) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float s = part[i];
+    for (int k = 1; k < ks; ++k) s += part[(size_t) k * n + i];
+    y[i] = s;
+}
+
+int g_ov_ks = 0;
+
+PP planes(const QLayout &L, const uint8_t *packed) {
+    PP P{packed + L.off[0], packed + L.off[1], packed + L.off[2], L.rs[0], L.rs[1], L.rs[2]};
+    return P;
+}
+
+template <uint32_t TY, int LPR>
+int gemv_tl(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, int nt, float *out, hipStream_t st) {
+    const dim3 grid((unsigned) pl.ntiles, (unsigned) pl.ks), block(512);
+    const int gps = (pl.ngroups + pl.ks - 1) / pl.ks;
+    switch (nt) {
+#define FN_GEMV_NT(N)                                                                                               \
+    case N:                                                                                                         \
+        hipLaunchKernelGGL((k_gemv<TY, N, LPR>), grid, block, 0, st, P, L.rows, pl.ngroups, gps, x, L.cols, out); \
+        break;
+        FN_GEMV_NT(1) FN_GEMV_NT(2) FN_GEMV_NT(3) FN_GEMV_NT(4) FN_GEMV_NT(5) FN_GEMV_NT(6) FN_GEMV_NT(7) FN_GEMV_NT(8)
+#undef FN_GEMV_NT
+        default: FN_FAIL("gemv: nt must be 1..8");
+    }
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+template <uint32_t TY>
+int gemv_t(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, int nt, float *out, hipStream_t st) {
+    switch (pl.lpr) {
+        case 16: return gemv_tl<TY, 16>(L, pl, P, x, nt, out, st);
+        case 32: return gemv_tl<TY, 32>(L, pl, P, x, nt, out, st);
+        default: return gemv_tl<TY, 64>(L, pl, P, x, nt, out, st);
+    }
+}
+
+}  // namespace
+
+bool qlayout(uint32_t type, int rows, int cols, QLayout &L) {
+    struct F {
+        int qk, bb, np, fo[3], fb[3];
+    };
+    F f{};
+    switch (type) {
+        case QT_BF16: f = {32, 64, 1, {0, 0, 0}, {64, 0, 0}}; break;
+        case QT_Q8_0: f = {32, 34, 2, {2, 0, 0}, {32, 2, 0}}; break;
+        case QT_IQ4_NL: f = {32, 18, 2, {2, 0, 0}, {16, 2, 0}}; break;
+        case QT_IQ4_XS: f = {256, 136, 2, {8, 0, 0}, {128, 8, 0}}; break;
+        case QT_Q4_K: f = {256, 144, 2, {16, 0, 0}, {128, 16, 0}}; break;
+        case QT_Q5_K: f = {256, 176, 3, {48, 16, 0}, {128, 32, 16}}; break;
+        case QT_Q6_K: f = {256, 210, 3, {0, 128, 192}, {128, 64, 18}}; break;
+        default:
+            set_error("unsupported type " + std::to_string(type) +
+                      " (this library reads BF16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS)");
+            return false;
+    }
+    if (rows < 1 || cols < 1 || cols % f.qk) {
+        set_error("unsupported shape: rows >= 1 and cols a multiple of " + std::to_string(f.qk) + " for type " +
+                  std::to_string(type));
+        return false;
+    }
+    L = QLayout{};
+    L.type = type;
+    L.rows = rows;
+    L.cols = cols;
+    L.qk = f.qk;
+    L.bb = f.bb;
+    L.nplanes = f.np;
+    const size_t nb = (size_t) cols / f.qk;
+    L.row_bytes = nb * f.bb;
+    size_t off = 0;
+    for (int p = 0; p < f.np; ++p) {
+        L.fbytes[p] = f.fb[p];
+        L.foff[p] = f.fo[p];
+        L.rs[p] = nb * f.fb[p];
+        L.off[p] = off;
+        off += (L.rs[p] * rows + 255) / 256 * 256;
+    }
+    L.bytes = off;
+    return true;
+}
+
+void gemv_override(int ks) { g_ov_ks = std::max(0, ks); }
+
+GemvPlan gemv_plan(const QLayout &L) {
+    GemvPlan p;
+    p.ngroups = L.cols / 32;
+    // lanes per row: enough that a lane has at most a few groups (its loads go out in one or two batches), and
+    // enough lanes in all (waves = rows * lpr / 64) to fill the 256 CUs when the rows are few
+    int lpr = p.ngroups >= 128 ? 64 : (p.ngroups >= 48 ? 32 : 16);
+    while (lpr < 64 && p.ngroups > lpr && (size_t) L.rows * lpr / 64 < 2048) lpr *= 2;
+    p.lpr = lpr;
+    p.rpw = 8 * (64 / lpr);
+    p.ntiles = (L.rows + p.rpw - 1) / p.rpw;
+    p.ks = g_ov_ks ? std::min(g_ov_ks, p.ngroups) : 1;
+    return p;
+}
+
+size_t gemv_work_bytes(const QLayout &L, int nt) {
+    const GemvPlan p = gemv_plan(L);
+    return p.ks > 1 ? (size_t) p.ks * nt * L.rows * 4 : 0;
+}
+
+int quant_pack_launch(const QLayout &L, const uint8_t *raw, uint8_t *packed, hipStream_t st) {
+    if (!raw || !packed) FN_FAIL("pack: null pointer");
+    const size_t n = (size_t) L.rows * (L.cols / L.qk);
+    hipLaunchKernelGGL(k_pack, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, L, raw, packed);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+int quant_dequant_launch(const QLayout &L, const uint8_t *packed, float *out, hipStream_t st) {
+    if (!packed || !out) FN_FAIL("dequant: null pointer");
+    if ((uintptr_t) out % 16 || (uintptr_t) packed % 16) FN_FAIL("dequant: pointers must be 16-byte aligned");
+    const PP P = planes(L, packed);
+    const int G = L.cols / 32;
+    const size_t n = (size_t) L.rows * G;
+    const dim3 grid((unsigned) ((n + 255) / 256)), block(256);
+    switch (L.type) {
+        case QT_BF16: hipLaunchKernelGGL(k_dequant<QT_BF16>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
+        case QT_Q8_0: hipLaunchKernelGGL(k_dequant<QT_Q8_0>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
+        case QT_IQ4_NL: hipLaunchKernelGGL(k_dequant<QT_IQ4_NL>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
+        case QT_IQ4_XS: hipLaunchKernelGGL(k_dequant<QT_IQ4_XS>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
+        case QT_Q4_K: hipLaunchKernelGGL(k_dequant<QT_Q4_K>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
+        case QT_Q5_K: hipLaunchKernelGGL(k_dequant<QT_Q5_K>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
+        case QT_Q6_K: hipLaunchKernelGGL(k_dequant<QT_Q6_K>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
+        default: FN_FAIL("dequant: unsupported type");
+    }
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, float *y, float *work,
+                size_t work_bytes, hipStream_t st) {
+    if (nt < 1 || nt > MAXNT) FN_FAIL("gemv: nt must be 1..8");
+    if (!packed || !x || !y) FN_FAIL("gemv: null pointer");
+    if ((uintptr_t) packed % 16 || (uintptr_t) x % 16) FN_FAIL("gemv: weight and x must be 16-byte aligned");
+    const GemvPlan pl = gemv_plan(L);
+    float *out = y;
+    if (pl.ks > 1) {
+        const size_t need = (size_t) pl.ks * nt * L.rows * 4;
+        if (!work || work_bytes < need) FN_FAIL("gemv: work buffer smaller than fn_gemv_work_bytes()");
+        out = work;
+    }
+    const PP P = planes(L, packed);
+    int rc = 0;
+    switch (L.type) {
+        case QT_BF16: rc = gemv_t<QT_BF16>(L, pl, P, x, nt, out, st); break;
+        case QT_Q8_0: rc = gemv_t<QT_Q8_0>(L, pl, P, x, nt, out, st); break;
+        case QT_IQ4_NL: rc = gemv_t<QT_IQ4_NL>(L, pl, P, x, nt, out, st); break;
+        case QT_IQ4_XS: rc = gemv_t<QT_IQ4_XS>(L, pl, P, x, nt, out, st); break;
+        case QT_Q4_K: rc = gemv_t<QT_Q4_K>(L, pl, P, x, nt, out, st); break;
+        case QT_Q5_K: rc = gemv_t<QT_Q5_K>(L, pl, P, x, nt, out, st); break;
+        case QT_Q6_K: rc = gemv_t<QT_Q6_K>(L, pl, P, x, nt, out, st); break;
+        default: FN_FAIL("gemv: unsupported type");
+    }
+    if (rc) return rc;
+    if (pl.ks > 1) {
+        const int n = nt * L.rows;
+        hipLaunchKernelGGL(k_gemv_reduce, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, work, pl.ks, n, y);
+        FN_CK(hipGetLastError());
+    }
+    return 0;
+}
+
+}  // namespace fn
+

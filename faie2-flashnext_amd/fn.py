@@ -35,7 +35,18 @@ SYMBOLS = (
     "fn_fill_normal_dev", "fn_copy_dev",
     "fn_path_init", "fn_path_buffer", "fn_path_step",
     "fn_attn_qsa_dev", "fn_attn_qsa_work_bytes", "fn_ix_blocks_dev", "fn_test_attn_qsa",
+    "fn_gemv_packed_bytes", "fn_gemv_pack_dev", "fn_dequant_dev", "fn_gemv_work_bytes", "fn_gemv_dev",
 )
+
+# GGUF type ids of the weight formats this library reads (engine/faie2fn.cu:78-81), and (values, bytes) per block
+QTYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ4_XS=23, BF16=30)
+QBLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18), 23: (256, 136), 30: (1, 2)}
+
+
+def row_bytes(qtype, cols):
+    """GGUF bytes of one row of `cols` values."""
+    qk, bb = QBLOCK[int(qtype)]
+    return cols // qk * bb
 
 # buffer kinds of fn_path_buffer (include/faie2fn.h)
 BUF = dict(S=0, CONV_RING=1, QKV=2, AB=3, Z=4, OUT=5, CONV_W=6, DT_BIAS=7, SSM_A=8, NORM_W=9, KC=10, VC=11, QG=12,
@@ -105,6 +116,18 @@ class FN:
         d.fn_ix_blocks_dev.argtypes = [i] * 4 + [VP] * 3 + [i, f, f, VP]
         d.fn_test_attn_qsa.argtypes = [i] * 5 + [f, f, i, i, I32] + [F32] * 11 + [i, i, F32, VP, VP]
         d.fn_n_past.restype = C.c_int
+        u32, sz = C.c_uint32, C.c_size_t
+        d.fn_gemv_plan.argtypes = [u32, i, i, I32]
+        d.fn_bench_gemv.argtypes = [u32, i, i, i, i, C.POINTER(C.c_float)]
+        d.fn_gemv_override.argtypes = [i] * 4
+        d.fn_bench_hot.argtypes = [i]
+        d.fn_gemv_packed_bytes.restype = sz
+        d.fn_gemv_packed_bytes.argtypes = [u32, i, i]
+        d.fn_gemv_pack_dev.argtypes = [u32, VP, i, i, VP, VP]
+        d.fn_dequant_dev.argtypes = [u32, VP, i, i, VP, VP]
+        d.fn_gemv_work_bytes.restype = sz
+        d.fn_gemv_work_bytes.argtypes = [u32, i, i, i]
+        d.fn_gemv_dev.argtypes = [u32, VP, i, i, VP, i, VP, VP, sz, VP]
 
     def check(self, rc):
         if rc != 0:
@@ -139,6 +162,25 @@ class FN:
         self.check(self.d.fn_test_gemv(int(qtype), np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1), rows, cols,
                                        _f32(x), nt, y))
         return y
+
+    def gemv_plan(self, qtype, rows, cols):
+        """{values per group, waves per workgroup, split-K, rows per workgroup, groups in flight, row tiles,
+        groups per row} of a weight."""
+        out = np.zeros(7, np.int32)
+        self.check(self.d.fn_gemv_plan(int(qtype), rows, cols, out))
+        return [int(v) for v in out]
+
+    def bench_gemv(self, qtype, rows, cols, nt=1, iters=50):
+        """ms per GEMV call, weights cold (fn_bench_hot(0)) or hot."""
+        ms = C.c_float(0.0)
+        self.check(self.d.fn_bench_gemv(int(qtype), rows, cols, nt, iters, C.byref(ms)))
+        return ms.value
+
+    def gemv_override(self, ks=0):
+        self.d.fn_gemv_override(0, int(ks), 0, 0)
+
+    def bench_hot(self, on):
+        self.d.fn_bench_hot(1 if on else 0)
 
     # ---- path hooks (host arrays, synchronous) ----
     def gdn(self, q, k, v, beta, g, S, head_map=0):
@@ -243,6 +285,21 @@ class FN:
 
     def copy_dev(self, dst, src, nbytes, stream=0):
         self.check(self.d.fn_copy_dev(dst, src, nbytes, stream))
+
+    def gemv_packed_bytes(self, qtype, rows, cols):
+        return int(self.d.fn_gemv_packed_bytes(int(qtype), rows, cols))
+
+    def gemv_work_bytes(self, qtype, rows, cols, nt):
+        return int(self.d.fn_gemv_work_bytes(int(qtype), rows, cols, nt))
+
+    def gemv_pack_dev(self, qtype, raw, rows, cols, packed, stream=0):
+        self.check(self.d.fn_gemv_pack_dev(int(qtype), raw, rows, cols, packed, stream))
+
+    def dequant_dev(self, qtype, packed, rows, cols, out, stream=0):
+        self.check(self.d.fn_dequant_dev(int(qtype), packed, rows, cols, out, stream))
+
+    def gemv_dev(self, qtype, packed, rows, cols, x, nt, y, work, work_bytes, stream=0):
+        self.check(self.d.fn_gemv_dev(int(qtype), packed, rows, cols, x, nt, y, work, work_bytes, stream))
 
     # ---- path engine ----
     def path_init(self, B, nl, attn_every=4, nkh=16, nvh=32, nq=16, nkv=2, max_ctx=4096, head_map=0, gate_act=0,

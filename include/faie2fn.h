@@ -23,9 +23,11 @@ extern "C" {
 
 /* ======================================================================================================
  * 1. The reference's C API, same names and C signatures (engine/faie2fn.cu, flashnext/fn.py:26-34), so that
- *    flashnext/fn.py's argtypes bind unchanged.  This library carries the decode-attention path only: the
- *    model-level entries (GGUF load, forward, GEMV, MoE, routing) return -1 with an fn_error() message that
- *    says so, and the getters return -1 like the reference's do when no model is loaded.
+ *    flashnext/fn.py's argtypes bind unchanged.  This library carries the decode-attention path and the GEMV of
+ *    its projections: the GEMV hooks (fn_test_dequant, fn_test_gemv, fn_gemv_plan, fn_bench_gemv,
+ *    fn_gemv_override, fn_bench_hot) work as in the reference for the formats of section 5; the model-level
+ *    entries (GGUF load, forward, MoE, routing) return -1 with an fn_error() message that says so, and the
+ *    getters return -1 like the reference's do when no model is loaded.
  * ====================================================================================================== */
 const char *fn_error(void);                                                   /* faie2fn.cu:2495 */
 void fn_free(void);                                                           /* faie2fn.cu:2497 */
@@ -38,6 +40,7 @@ int fn_reset(void);                                                           /*
 int fn_use_graphs(int on);                                                    /* faie2fn.cu:2721 */
 int fn_forward(const int32_t *tokens, int nt, float *logits, int32_t *argmax);  /* faie2fn.cu:2733 */
 int fn_debug_layers(float *out);                                              /* faie2fn.cu:2739 */
+/* GGUF rows W (rows x cols of `type`, the file's bytes) -> out [rows][cols] float32, bit for bit ggml's decode. */
 int fn_test_dequant(uint32_t type, const uint8_t *W, int rows, int cols, float *out);  /* faie2fn.cu:2751 */
 void fn_gemv_override(int wpt, int ks, int tb, int warps_per_sm);             /* faie2fn.cu:2786 */
 void fn_gemv_waves(int waves);                                                /* faie2fn.cu:2793 */
@@ -45,11 +48,19 @@ void fn_pdl(int on);                                                          /*
 void fn_early(int on);                                                        /* faie2fn.cu:2798 */
 void fn_moe_var(int v);                                                       /* faie2fn.cu:2799 */
 void fn_moe_override(int gu_wpt, int gu_tb, int dn_wpt, int dn_tb);           /* faie2fn.cu:2801 */
+/* Launch plan of a rows x cols weight: out[7] = {values per group (32), waves per workgroup, split-K workgroups
+ * per row, rows per workgroup, lanes per row, row tiles, groups per row}.  Same 7-int shape as the reference's
+ * {cv, wpt, ks, tb, nbuf, ntiles, nch}, this library's plan in it; like the reference's it depends on the shape
+ * only, never on the number of tokens. */
 int fn_gemv_plan(uint32_t type, int rows, int cols, int *out);                /* faie2fn.cu:2809 */
 void fn_bench_hot(int on);                                                    /* faie2fn.cu:2822 */
+/* ms per GEMV call of nt tokens (1..8) on random bytes of the format, iters calls replayed as one hipGraph, each
+ * reading its own copy of the weight (copies beyond the 256 MB Infinity Cache, 512 MiB written before the timed
+ * replay) unless fn_bench_hot(1). */
 int fn_bench_gemv(uint32_t type, int rows, int cols, int nt, int iters, float *ms);  /* faie2fn.cu:2823 */
 int fn_bench_route(int variant, int nt, int ks, const float *part, int iters, int *sel, float *wsel,
                    float *ms);                                                /* faie2fn.cu:2875 */
+/* y [nt][rows] = W x for GGUF rows W and x [nt][cols], nt 1..8 (packed, then the GEMV of section 5). */
 int fn_test_gemv(uint32_t type, const uint8_t *W, int rows, int cols, const float *x, int nt,
                  float *y);                                                   /* faie2fn.cu:2916 */
 
@@ -206,6 +217,32 @@ int fn_path_buffer(int il, int kind, void **ptr, size_t *bytes);
 /* steps decode steps (one token per sequence each) through all layers, then a stream synchronize; with ms
  * non-NULL, the HIP-event time per step on the engine's stream is written there. */
 int fn_path_step(int steps, float *ms);
+
+/* ======================================================================================================
+ * 5. GGUF weights and the GEMV of the projections around the path (the reference's dequantisers and tiled GEMV,
+ *    engine/faie2fn.cu:343-1042, 2033-2116; its callers on the path: the qkv / z / ab projections before k_gdn
+ *    and ssm_out after it, the q / k / v projections before the attention and o_proj after it, :2386-2403).
+ *    Types are GGUF type ids: 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K, 20 IQ4_NL, 23 IQ4_XS, 30 BF16.  cols must be a
+ *    whole number of blocks (32 values, 256 for the K and IQ4_XS formats).  An engine packs each weight once
+ *    (fn_gemv_pack_dev: every field of the format in its own aligned plane, the same bytes) and then calls
+ *    fn_gemv_dev per token batch.  All _dev pointers must be 16-byte aligned.
+ * ====================================================================================================== */
+
+/* Bytes of the packed layout of a rows x cols weight (0 if the type or shape is not supported). */
+size_t fn_gemv_packed_bytes(uint32_t type, int rows, int cols);
+
+/* GGUF rows raw [rows][row bytes] (device) -> packed (device, fn_gemv_packed_bytes() bytes). */
+int fn_gemv_pack_dev(uint32_t type, const uint8_t *raw, int rows, int cols, uint8_t *packed, void *stream);
+
+/* packed -> out [rows][cols] float32 (device), bit for bit ggml's decode (what fn_test_dequant returns). */
+int fn_dequant_dev(uint32_t type, const uint8_t *packed, int rows, int cols, float *out, void *stream);
+
+/* Scratch bytes fn_gemv_dev needs for nt tokens (0 when the plan does not split K). */
+size_t fn_gemv_work_bytes(uint32_t type, int rows, int cols, int nt);
+
+/* y [nt][rows] = W x, x [nt][cols], nt 1..8, on device buffers; split-K partials (if any) in work. */
+int fn_gemv_dev(uint32_t type, const uint8_t *packed, int rows, int cols, const float *x, int nt, float *y,
+                float *work, size_t work_bytes, void *stream);
 
 #ifdef __cplusplus
 }

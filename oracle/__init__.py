@@ -10,7 +10,8 @@ Two independent restatements of the reference arithmetic live here:
 
 Pinning status of each function (what checks it beyond retyping its formula) is recorded in the tests:
 ``tests/test_oracle_pins.py`` (closed forms, invariants, exact rational brute force, the transformers Qwen3-Next
-library routines) and ``tests/test_oracle_twin.py`` (C oracle == numpy twin).
+library routines, C oracle == numpy twin) and ``tests/test_quant_pins.py`` (the GGUF weight decode: numpy twin,
+blocks packed from chosen codes, library fp16 / bf16 conversions).
 """
 
 import ctypes as C
@@ -55,6 +56,11 @@ def lib():
                                                    _F32, _F64])
         d.orc_ix_blocks.argtypes = ([C.c_int] * 4 + [C.c_double, C.c_double] + [C.c_int] * 3 + [_F32, _F32, _F64])
         d.orc_ix_score.argtypes = [C.c_int] * 6 + [_I32, _F64, _F64, _F64]
+        d.orc_f16_to_f32.argtypes = [C.c_uint16]
+        d.orc_f16_to_f32.restype = C.c_float
+        d.orc_qblock.argtypes = [C.c_uint32, C.POINTER(C.c_int), C.POINTER(C.c_int)]
+        d.orc_dequant.argtypes = [C.c_uint32, _U8, C.c_int, C.c_int, _F32]
+        d.orc_gemv.argtypes = [C.c_uint32, _U8, C.c_int, C.c_int, _F32, C.c_int, _F64]
         _lib = d
     return _lib
 
@@ -173,6 +179,35 @@ def ix_select(scores, pos, top=512, ixr=4):
             order = np.argsort(-scores[b, t, :nb], kind="stable")
             mask[b, t, order[:top]] = 1
     return mask
+
+
+def qblock(qtype):
+    """(values, bytes) per GGUF block of a weight format this oracle decodes."""
+    qk, bb = C.c_int(), C.c_int()
+    if not lib().orc_qblock(int(qtype), C.byref(qk), C.byref(bb)):
+        raise ValueError(f"unsupported type {qtype}")
+    return qk.value, bb.value
+
+
+def f16_to_f32(bits):
+    return float(lib().orc_f16_to_f32(int(bits)))
+
+
+def dequant(qtype, raw, rows, cols):
+    """GGUF rows -> float32 [rows][cols], the values ggml's dequantize_row_* returns."""
+    out = np.zeros((rows, cols), np.float32)
+    if lib().orc_dequant(int(qtype), np.ascontiguousarray(raw, np.uint8).reshape(-1), rows, cols, out):
+        raise ValueError("unsupported type or shape")
+    return out
+
+
+def gemv(qtype, raw, rows, cols, x):
+    """float64 y [nt][rows] = decoded W @ x[t] for x [nt][cols]."""
+    x = _f32(np.atleast_2d(x))
+    y = np.zeros((x.shape[0], rows), np.float64)
+    if lib().orc_gemv(int(qtype), np.ascontiguousarray(raw, np.uint8).reshape(-1), rows, cols, x, x.shape[0], y):
+        raise ValueError("unsupported type or shape")
+    return y
 
 
 def relerr(got, ref):

@@ -1,0 +1,194 @@
+/*
+ * quant_oracle.c -- CPU restatement of the GGUF weight decode and the GEMV of the projections around the path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker for the dequant / GEMV kernels of libfaie2fn.so: only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.  The product path never calls it.
+ *
+ * The reference decodes weights with ggml's arithmetic (engine/faie2fn.cu:343-689, "ggml-quants.c arithmetic",
+ * :345) and gates its GPU decode bit for bit against gguf-py (flashnext/test_fn_quants.py:30-37, dequant error
+ * exactly 0; GEMV within 1e-5 of float64 on the decoded weights).  Neither ggml nor gguf-py is in this image, so
+ * this file restates ggml's dequantize_row_* (ggml/src/ggml-quants.c, the published block formats of GGUF) loop by
+ * loop, on the same block byte layouts the reference's DQ<T> decoders read (faie2fn.cu:441-655):
+ *   - every product ggml forms in float is formed here in float, in ggml's order, so that each value is the float
+ *     ggml returns: for Q4_K / Q5_K the product d1 * q is exact and the one rounding is in "- m1" (fmaf is that
+ *     single rounding); for Q6_K (d * sc) is exact and the rounding is in "* q"; for IQ4_XS (d * (ls - 32)) is
+ *     exact and the rounding is in "* level".
+ *   - fp16 scales are decoded from their bits (sign, 5-bit exponent, 10-bit fraction; subnormals, inf, NaN) with
+ *     ldexp, exactly; bf16 is its bits in the high half of a float.
+ * The GEMV oracle is the float64 dot product of those float values with x.
+ *
+ * Block layouts (bytes), values per block in brackets:
+ *   BF16 [1]     2: bf16 bits
+ *   Q8_0 [32]    34: d f16 | qs int8[32]
+ *   IQ4_NL [32]  18: d f16 | qs[16] (byte j: low nibble -> value j, high nibble -> value j + 16)
+ *   IQ4_XS [256] 136: d f16 | scales_h u16 | scales_l[4] | qs[128] (16 bytes per group of 32, IQ4_NL order)
+ *   Q4_K [256]   144: d f16 | dmin f16 | scales[12] | qs[128]
+ *   Q5_K [256]   176: d f16 | dmin f16 | scales[12] | qh[32] | qs[128]
+ *   Q6_K [256]   210: ql[128] | qh[64] | scales int8[16] | d f16
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define EXPORT __attribute__((visibility("default")))
+
+/* the 16 levels of the IQ4 formats (GGUF kvalues_iq4nl) */
+static const int8_t IQ4_LEVELS[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+EXPORT float orc_f16_to_f32(uint16_t h) {
+    const int sign = h >> 15, e = (h >> 10) & 0x1F, f = h & 0x3FF;
+    float v;
+    if (e == 0) v = ldexpf((float) f, -24);                 /* subnormal (and zero) */
+    else if (e == 31) v = f ? NAN : INFINITY;
+    else v = ldexpf((float) (1024 + f), e - 25);            /* (1 + f / 1024) * 2^(e - 15) */
+    return sign ? -v : v;
+}
+
+static float f16(const uint8_t *p) { return orc_f16_to_f32((uint16_t) (p[0] | p[1] << 8)); }
+
+/* ggml get_scale_min_k4 (faie2fn.cu:432-440): 6-bit scale and min of group j from the 12 packed bytes */
+static void scale_min_k4(int j, const uint8_t *q, int *d, int *m) {
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* values per block and bytes per block; 0 for a type this oracle does not decode */
+EXPORT int orc_qblock(uint32_t type, int *qk, int *bytes) {
+    switch (type) {
+        case 30: *qk = 1; *bytes = 2; return 1;
+        case 8: *qk = 32; *bytes = 34; return 1;
+        case 20: *qk = 32; *bytes = 18; return 1;
+        case 23: *qk = 256; *bytes = 136; return 1;
+        case 12: *qk = 256; *bytes = 144; return 1;
+        case 13: *qk = 256; *bytes = 176; return 1;
+        case 14: *qk = 256; *bytes = 210; return 1;
+        default: return 0;
+    }
+}
+
+/* one GGUF row of `cols` values -> y[cols] */
+static void dq_row(uint32_t type, const uint8_t *r, int cols, float *y) {
+    switch (type) {
+        case 30: /* BF16 */
+            for (int j = 0; j < cols; ++j) {
+                const uint32_t bits = (uint32_t) (r[2 * j] | r[2 * j + 1] << 8) << 16;
+                memcpy(&y[j], &bits, 4);
+            }
+            break;
+        case 8: /* Q8_0: y = d * q */
+            for (int b = 0; b < cols / 32; ++b, r += 34, y += 32) {
+                const float d = f16(r);
+                for (int j = 0; j < 32; ++j) y[j] = d * (float) (int8_t) r[2 + j];
+            }
+            break;
+        case 20: /* IQ4_NL: y = d * level */
+            for (int b = 0; b < cols / 32; ++b, r += 18, y += 32) {
+                const float d = f16(r);
+                const uint8_t *qs = r + 2;
+                for (int j = 0; j < 16; ++j) {
+                    y[j] = d * (float) IQ4_LEVELS[qs[j] & 0xF];
+                    y[j + 16] = d * (float) IQ4_LEVELS[qs[j] >> 4];
+                }
+            }
+            break;
+        case 23: /* IQ4_XS: dl = d * (ls - 32), y = dl * level */
+            for (int b = 0; b < cols / 256; ++b, r += 136) {
+                const float d = f16(r);
+                const int sh = r[2] | r[3] << 8;
+                const uint8_t *sl = r + 4, *qs = r + 8;
+                for (int ib = 0; ib < 8; ++ib, y += 32, qs += 16) {
+                    const int ls = ((sl[ib / 2] >> 4 * (ib % 2)) & 0xF) | (((sh >> 2 * ib) & 3) << 4);
+                    const float dl = d * (float) (ls - 32);
+                    for (int j = 0; j < 16; ++j) {
+                        y[j] = dl * (float) IQ4_LEVELS[qs[j] & 0xF];
+                        y[j + 16] = dl * (float) IQ4_LEVELS[qs[j] >> 4];
+                    }
+                }
+            }
+            break;
+        case 12: /* Q4_K: y = d*sc * q - dmin*m */
+            for (int b = 0; b < cols / 256; ++b, r += 144) {
+                const float d = f16(r), dmin = f16(r + 2);
+                const uint8_t *sc = r + 4, *q = r + 16;
+                for (int p = 0; p < 4; ++p, q += 32) {
+                    int s1, m1, s2, m2;
+                    scale_min_k4(2 * p, sc, &s1, &m1);
+                    scale_min_k4(2 * p + 1, sc, &s2, &m2);
+                    const float d1 = d * (float) s1, n1 = dmin * (float) m1;
+                    const float d2 = d * (float) s2, n2 = dmin * (float) m2;
+                    for (int l = 0; l < 32; ++l) *y++ = fmaf(d1, (float) (q[l] & 0xF), -n1);
+                    for (int l = 0; l < 32; ++l) *y++ = fmaf(d2, (float) (q[l] >> 4), -n2);
+                }
+            }
+            break;
+        case 13: /* Q5_K: Q4_K with a fifth bit from qh */
+            for (int b = 0; b < cols / 256; ++b, r += 176) {
+                const float d = f16(r), dmin = f16(r + 2);
+                const uint8_t *sc = r + 4, *qh = r + 16, *ql = r + 48;
+                for (int p = 0; p < 4; ++p, ql += 32) {
+                    int s1, m1, s2, m2;
+                    scale_min_k4(2 * p, sc, &s1, &m1);
+                    scale_min_k4(2 * p + 1, sc, &s2, &m2);
+                    const float d1 = d * (float) s1, n1 = dmin * (float) m1;
+                    const float d2 = d * (float) s2, n2 = dmin * (float) m2;
+                    const int u1 = 1 << (2 * p), u2 = 2 << (2 * p);
+                    for (int l = 0; l < 32; ++l) *y++ = fmaf(d1, (float) ((ql[l] & 0xF) + (qh[l] & u1 ? 16 : 0)), -n1);
+                    for (int l = 0; l < 32; ++l) *y++ = fmaf(d2, (float) ((ql[l] >> 4) + (qh[l] & u2 ? 16 : 0)), -n2);
+                }
+            }
+            break;
+        case 14: /* Q6_K: y = d * sc * (q - 32) */
+            for (int b = 0; b < cols / 256; ++b, r += 210) {
+                const float d = f16(r + 208);
+                const uint8_t *ql = r, *qh = r + 128;
+                const int8_t *sc = (const int8_t *) (r + 192);
+                for (int n = 0; n < 2; ++n, ql += 64, qh += 32, sc += 8, y += 128)
+                    for (int l = 0; l < 32; ++l) {
+                        const int is = l / 16;
+                        const int q1 = ((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32;
+                        const int q2 = ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                        const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                        const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                        y[l] = d * (float) sc[is] * (float) q1;
+                        y[l + 32] = d * (float) sc[is + 2] * (float) q2;
+                        y[l + 64] = d * (float) sc[is + 4] * (float) q3;
+                        y[l + 96] = d * (float) sc[is + 6] * (float) q4;
+                    }
+            }
+            break;
+    }
+}
+
+/* rows GGUF rows of `cols` values -> out [rows][cols]; -1 for an unsupported type or shape */
+EXPORT int orc_dequant(uint32_t type, const uint8_t *W, int rows, int cols, float *out) {
+    int qk, bb;
+    if (!orc_qblock(type, &qk, &bb) || cols % qk || rows < 1) return -1;
+    const size_t rb = (size_t) cols / qk * bb;
+    for (int r = 0; r < rows; ++r) dq_row(type, W + (size_t) r * rb, cols, out + (size_t) r * cols);
+    return 0;
+}
+
+/* y [nt][rows] = sum_c W[r][c] x[t][c] in float64 over the decoded float weights */
+EXPORT int orc_gemv(uint32_t type, const uint8_t *W, int rows, int cols, const float *x, int nt, double *y) {
+    int qk, bb;
+    if (!orc_qblock(type, &qk, &bb) || cols % qk || rows < 1) return -1;
+    const size_t rb = (size_t) cols / qk * bb;
+    float *w = (float *) malloc(sizeof(float) * (size_t) cols);
+    for (int r = 0; r < rows; ++r) {
+        dq_row(type, W + (size_t) r * rb, cols, w);
+        for (int t = 0; t < nt; ++t) {
+            double s = 0.0;
+            const float *xt = x + (size_t) t * cols;
+            for (int c = 0; c < cols; ++c) s += (double) w[c] * (double) xt[c];
+            y[(size_t) t * rows + r] = s;
+        }
+    }
+    free(w);
+    return 0;
+}

@@ -147,3 +147,72 @@ def ix_score(Qix, BKc, pos, max_ctx, ixr=4):
             dots = Qix[b, t] @ BKc[b, :nb].T                  # [ixh, nb]
             sc[b, t, :nb] = np.maximum(dots, 0.0).sum(0) / np.sqrt(ixd)
     return sc
+
+
+# ------------------------------------------------------------------------------------------------------------
+# GGUF weight decode, vectorised over blocks (the structure of gguf-py's quants.py: split each block into its
+# fields as arrays, then whole-array float32 arithmetic in ggml's order).  Independent of quant_oracle.c, which
+# walks ggml's per-row loops; both follow the reference's decoders (engine/faie2fn.cu:441-655).
+
+IQ4_LEVELS = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float32)
+_BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18), 23: (256, 136), 30: (1, 2)}
+
+
+def _f16(b):
+    return np.ascontiguousarray(b).view(np.float16).astype(np.float32)
+
+
+def _k_scales(sc):
+    """6-bit scales and mins of the 8 groups of a Q4_K / Q5_K super-block from its 12 scale bytes [n, 12]."""
+    sc = sc.astype(np.uint8)
+    d = np.concatenate([sc[:, 0:4] & 63, (sc[:, 8:12] & 15) | ((sc[:, 0:4] >> 6) << 4)], axis=1)
+    m = np.concatenate([sc[:, 4:8] & 63, (sc[:, 8:12] >> 4) | ((sc[:, 4:8] >> 6) << 4)], axis=1)
+    return d.astype(np.float32), m.astype(np.float32)
+
+
+def dequant(qtype, raw, rows, cols):
+    """GGUF rows -> float32 [rows, cols]."""
+    qk, bb = _BLOCK[int(qtype)]
+    raw = np.ascontiguousarray(raw, np.uint8).reshape(rows, cols // qk * bb)
+    if qtype == 30:
+        return (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(rows, cols)
+    blk = raw.reshape(-1, bb)
+    n = blk.shape[0]
+    if qtype == 8:
+        y = _f16(blk[:, :2]) * blk[:, 2:].view(np.int8).astype(np.float32)
+    elif qtype == 20:
+        qs = blk[:, 2:]
+        y = _f16(blk[:, :2]) * IQ4_LEVELS[np.concatenate([qs & 15, qs >> 4], axis=1)]
+    elif qtype == 23:
+        d = _f16(blk[:, 0:2])
+        sh = np.ascontiguousarray(blk[:, 2:4]).view(np.uint16).astype(np.int32)
+        sl = blk[:, 4:8].astype(np.int32)
+        ib = np.arange(8)
+        ls = ((sl[:, ib // 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4)
+        dl = d * (ls - 32).astype(np.float32)
+        qs = blk[:, 8:].reshape(n, 8, 16)
+        lev = IQ4_LEVELS[np.concatenate([qs & 15, qs >> 4], axis=2)]
+        y = dl[:, :, None] * lev
+    elif qtype in (12, 13):
+        d, dmin = _f16(blk[:, 0:2]), _f16(blk[:, 2:4])
+        s, m = _k_scales(blk[:, 4:16])
+        qs = blk[:, 16:144] if qtype == 12 else blk[:, 48:176]
+        qs = qs.reshape(n, 4, 1, 32)
+        q = np.concatenate([qs & 15, qs >> 4], axis=2).reshape(n, 8, 32).astype(np.int32)
+        if qtype == 13:
+            qh = blk[:, 16:48].astype(np.int32)
+            q = q | (((qh[:, None, :] >> np.arange(8)[None, :, None]) & 1) << 4)
+        y = (d * s)[:, :, None] * q.astype(np.float32) - (dmin * m)[:, :, None]
+    elif qtype == 14:
+        ql = blk[:, 0:128].reshape(n, 2, 2, 32).astype(np.int32)   # [half][first / second 32 bytes][l]
+        qh = blk[:, 128:192].reshape(n, 2, 1, 32).astype(np.int32)
+        sc = blk[:, 192:208].view(np.int8).reshape(n, 2, 4, 2).astype(np.float32)
+        d = _f16(blk[:, 208:210]).reshape(n, 1, 1, 1)
+        low = np.concatenate([ql & 15, ql >> 4], axis=2)           # quarters 0..3: bytes 0-31 lo, 32-63 lo, hi, hi
+        high = (qh >> (2 * np.arange(4)).reshape(1, 1, 4, 1)) & 3
+        q = (low | (high << 4)) - 32                                 # [n][half][quarter][l]
+        scale = np.repeat(d * sc, 16, axis=3)                        # sc[8 half + 2 quarter + l // 16]
+        y = scale * q.astype(np.float32)
+    else:
+        raise ValueError(f"unsupported type {qtype}")
+    return np.ascontiguousarray(y, np.float32).reshape(rows, cols)

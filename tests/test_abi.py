@@ -36,15 +36,13 @@ def test_library_exports_every_declared_symbol(fnlib):
 def test_reference_entries_report_not_built(fnlib):
     d = fnlib.d
     assert d.fn_load(b"a.gguf", b"b.gguf", 4096, 0) == -1
-    assert b"decode-attention path only" in d.fn_error()
+    assert b"not built" in d.fn_error()
     with pytest.raises(RuntimeError, match="not loaded"):
         fnlib.reset()
     with pytest.raises(RuntimeError, match="not loaded"):
         fnlib.forward([1, 2, 3])
-    with pytest.raises(RuntimeError, match="decode-attention path only"):
-        fnlib.dequant(8, np.zeros(34, np.uint8), 1, 32)
-    with pytest.raises(RuntimeError, match="decode-attention path only"):
-        fnlib.gemv(8, np.zeros(34, np.uint8), 1, 32, np.zeros((1, 32), np.float32))
+    assert d.fn_bench_route(0, 1, 1, None, 1, None, None, None) == -1
+    assert b"not built" in d.fn_error()
     assert d.fn_split() == -1 and d.fn_n_past() == -1
     assert d.fn_dev_gb(0) == -1.0 and d.fn_last_ms() == -1.0
     d.fn_pdl(0), d.fn_early(0), d.fn_moe_var(1), d.fn_bench_hot(1), d.fn_free()
@@ -100,3 +98,38 @@ def test_attn_split_heuristic_and_workspace(fnlib):
         wb = fnlib.attn_work_bytes(B, nq, nt, ns)
         assert wb >= 4 * (B * nt * nq * 256 + B * nt * nq * ns * 258)
     assert fnlib.attn_work_bytes(0, 16, 1, 1) == 0
+
+
+def test_gemv_hooks_validate_before_device_work(fnlib):
+    """The reference's GEMV hooks reject unsupported formats and shapes with -1 + fn_error() (faie2fn.cu:2753,
+    2918) before touching a device."""
+    z8 = np.zeros(1 << 16, np.uint8)
+    x = np.zeros((9, 256), np.float32)
+    with pytest.raises(RuntimeError, match="unsupported type 21"):        # IQ3_S: not read by this library
+        fnlib.dequant(21, z8, 1, 256)
+    with pytest.raises(RuntimeError, match="unsupported shape"):          # K-quant row not a whole super-block
+        fnlib.dequant(12, z8, 1, 288)
+    with pytest.raises(RuntimeError, match="nt must be 1..8"):
+        fnlib.gemv(8, z8, 1, 256, x)
+    with pytest.raises(RuntimeError, match="unsupported type 0"):         # F32 has no block decode
+        fnlib.gemv(0, z8, 1, 256, x[:1])
+    assert fnlib.gemv_packed_bytes(21, 4, 256) == 0 and fnlib.gemv_work_bytes(8, 4, 256, 9) == 0
+    with pytest.raises(RuntimeError, match="unsupported"):
+        fnlib.gemv_plan(1, 4, 256)
+
+
+def test_gemv_plan_shapes(fnlib):
+    """Plans of the projection shapes around the path (BASELINE hidden 2048 and the reference model's 2560)."""
+    for qtype, rows, cols in [(23, 10240, 2560), (8, 2560, 6144), (30, 96, 2560), (14, 512, 2560), (23, 8192, 2048)]:
+        gv, waves, ks, rpw, lpr, ntiles, ngroups = fnlib.gemv_plan(qtype, rows, cols)
+        assert (gv, waves) == (32, 8) and lpr in (16, 32, 64) and rpw == 8 * 64 // lpr
+        assert ntiles == (rows + rpw - 1) // rpw and ngroups == cols // 32
+        assert 1 <= ks <= ngroups
+        assert fnlib.gemv_work_bytes(qtype, rows, cols, 3) == (ks * 3 * rows * 4 if ks > 1 else 0)
+        assert fnlib.gemv_packed_bytes(qtype, rows, cols) >= rows * fn.row_bytes(qtype, cols)
+    assert fnlib.gemv_plan(23, 10240, 2560)[2] == 1           # no split-K by default
+    fnlib.gemv_override(3)
+    try:
+        assert fnlib.gemv_plan(23, 10240, 2560)[2] == 3
+    finally:
+        fnlib.gemv_override(0)

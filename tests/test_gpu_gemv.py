@@ -1,0 +1,154 @@
+"""GPU parity of the GGUF decode and the projection GEMV against the oracle.
+
+The reference's quant gate (flashnext/test_fn_quants.py:30-37): the GPU decode equals the CPU decode exactly
+(error 0), and the GEMV of 8 tokens is within 1e-5 (max|gpu - ref| / max|ref|) of float64 math on the decoded
+weights.  Shapes are those of the projections on the path: the stacked DeltaNet input (qkv), its output (ssm_out),
+the attention q / k / v / o projections and the alpha/beta rows, at the reference model's hidden size 2560 and at
+BASELINE's 2048, plus ragged row counts.  Weights are random bytes with finite fp16 / bf16 scales (the reference's
+real tensors are not in this image).
+
+Every case prints what names it before the GPU call.
+"""
+
+import numpy as np
+import pytest
+
+import fn
+import hiprt
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+TYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ4_XS=23, BF16=30)
+RNG = np.random.default_rng(31)
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def random_finite(qtype, rows, cols, rng):
+    qk, bb = oracle.qblock(qtype)
+    raw = rng.integers(0, 256, size=rows * (cols // qk) * bb, dtype=np.uint8)
+    blk = raw.reshape(-1, bb)
+    for b in {30: [1], 8: [1], 20: [1], 23: [1], 12: [1, 3], 13: [1, 3], 14: [209]}[qtype]:
+        blk[:, b] &= 0xBF
+    return raw
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("rows,cols", [(1, 256), (37, 768), (64, 2560)])
+def test_dequant_bit_exact(fnlib, name, rows, cols):
+    t = TYPES[name]
+    _say(f"dequant {name} {rows}x{cols}")
+    raw = random_finite(t, rows, cols, RNG)
+    got = fnlib.dequant(t, raw, rows, cols)
+    ref = oracle.dequant(t, raw, rows, cols)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+# (type, rows, cols): the path's projections in the reference model (engine/faie2fn.cu:2386-2403;
+# flashnext/inspect_fn.txt:77, 95-100, 132-137) and at BASELINE's hidden 2048
+PATH_SHAPES = [
+    ("IQ4_XS", 10240, 2560),   # attn_qkv (DeltaNet in)
+    ("Q8_0", 2560, 6144),      # ssm_out / attn_output
+    ("BF16", 96, 2560),        # ssm_alpha + ssm_beta rows
+    ("Q6_K", 512, 2560),       # attn_v
+    ("IQ4_XS", 512, 2560),     # attn_k
+    ("Q6_K", 6144, 2560),      # attn_gate (z) of layer 1
+    ("IQ4_XS", 8192, 2048),    # BASELINE qkv: 8192 mixed channels from hidden 2048
+    ("Q8_0", 2048, 4096),      # BASELINE ssm_out
+]
+
+
+@pytest.mark.parametrize("name,rows,cols", PATH_SHAPES)
+@pytest.mark.parametrize("nt", [1, 8])
+def test_gemv_path_shapes(fnlib, name, rows, cols, nt):
+    t = TYPES[name]
+    _say(f"gemv {name} {rows}x{cols} nt={nt} plan={fnlib.gemv_plan(t, rows, cols)}")
+    raw = random_finite(t, rows, cols, RNG)
+    x = RNG.standard_normal((nt, cols)).astype(np.float32)
+    y = fnlib.gemv(t, raw, rows, cols, x)
+    ref = oracle.gemv(t, raw, rows, cols, x)
+    assert oracle.relerr(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("rows,nt", [(1, 1), (17, 3), (100, 5), (333, 8)])
+def test_gemv_formats_ragged(fnlib, name, rows, nt):
+    t = TYPES[name]
+    cols = 768
+    _say(f"gemv {name} {rows}x{cols} nt={nt}")
+    raw = random_finite(t, rows, cols, RNG)
+    x = RNG.standard_normal((nt, cols)).astype(np.float32)
+    y = fnlib.gemv(t, raw, rows, cols, x)
+    ref = oracle.gemv(t, raw, rows, cols, x)
+    assert oracle.relerr(y, ref) <= TOL
+    # every row on its own is right too (no row of a partial tile is dropped or shifted)
+    assert np.all(np.abs(y - ref) <= TOL * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("ks", [1, 2, 5, 80])
+def test_gemv_split_k_invariance(fnlib, ks):
+    t, rows, cols, nt = 23, 256, 2560, 4
+    _say(f"gemv split-K ks={ks}")
+    raw = random_finite(t, rows, cols, RNG)
+    x = RNG.standard_normal((nt, cols)).astype(np.float32)
+    ref = oracle.gemv(t, raw, rows, cols, x)
+    fnlib.gemv_override(ks)
+    try:
+        assert fnlib.gemv_plan(t, rows, cols)[2] == ks
+        y = fnlib.gemv(t, raw, rows, cols, x)
+    finally:
+        fnlib.gemv_override(0)
+    assert oracle.relerr(y, ref) <= TOL
+
+
+def test_gemv_tokens_independent(fnlib):
+    """Token t of an nt-token call equals a one-token call on x[t] (the split order does not depend on nt)."""
+    t, rows, cols = 8, 700, 2048
+    _say("gemv nt=6 vs 6 x nt=1")
+    raw = random_finite(t, rows, cols, RNG)
+    x = RNG.standard_normal((6, cols)).astype(np.float32)
+    y = fnlib.gemv(t, raw, rows, cols, x)
+    for i in range(6):
+        assert np.array_equal(y[i], fnlib.gemv(t, raw, rows, cols, x[i:i + 1])[0])
+
+
+def test_device_entry_points(fnlib):
+    """pack once, then dequant and GEMV on device buffers: the same values as the host hooks."""
+    t, rows, cols, nt = 14, 300, 2560, 3
+    _say("gemv device entry points Q6_K 300x2560 nt=3")
+    raw = random_finite(t, rows, cols, RNG)
+    x = RNG.standard_normal((nt, cols)).astype(np.float32)
+    draw = hiprt.Buf.like(raw)
+    packed = hiprt.Buf(fnlib.gemv_packed_bytes(t, rows, cols), np.uint8)
+    wb = fnlib.gemv_work_bytes(t, rows, cols, nt)
+    work = hiprt.Buf(max(wb, 16), np.uint8)
+    dx, dy = hiprt.Buf.like(x), hiprt.Buf.empty((nt, rows))
+    dW = hiprt.Buf.empty((rows, cols))
+    fnlib.gemv_pack_dev(t, draw.ptr, rows, cols, packed.ptr)
+    fnlib.dequant_dev(t, packed.ptr, rows, cols, dW.ptr)
+    fnlib.gemv_dev(t, packed.ptr, rows, cols, dx.ptr, nt, dy.ptr, work.ptr, wb)
+    hiprt.sync()
+    W = dW.download((rows, cols))
+    y = dy.download((nt, rows))
+    assert np.array_equal(W.view(np.uint32), oracle.dequant(t, raw, rows, cols).view(np.uint32))
+    assert np.array_equal(y, fnlib.gemv(t, raw, rows, cols, x))
+    # a split-K plan needs its work buffer, and a short one is refused before any launch
+    fnlib.gemv_override(2)
+    try:
+        wb2 = fnlib.gemv_work_bytes(t, rows, cols, nt)
+        assert wb2 == 2 * nt * rows * 4
+        with pytest.raises(RuntimeError, match="work buffer"):
+            fnlib.gemv_dev(t, packed.ptr, rows, cols, dx.ptr, nt, dy.ptr, work.ptr, wb2 - 4)
+    finally:
+        fnlib.gemv_override(0)
+
+
+def test_bench_gemv_runs(fnlib):
+    _say("bench_gemv IQ4_XS 10240x2560 nt=1, 8 iters")
+    ms = fnlib.bench_gemv(23, 10240, 2560, nt=1, iters=8)
+    assert 0.0 < ms < 5.0
+

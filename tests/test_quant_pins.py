@@ -1,0 +1,247 @@
+"""Pins of the GGUF weight decode in the oracle (CPU only).
+
+The reference gates its GPU decode bit for bit against gguf-py (flashnext/test_fn_quants.py:30-37) on slices of the
+real model; neither gguf-py, ggml nor the model is in this image, and the reference ships no fixture of decoded
+weights.  The oracle's decode (oracle/quant_oracle.c) is therefore pinned by:
+
+* the independent numpy twin (oracle/twin.py, gguf-py's vectorised structure) on random bytes of every format;
+* blocks *packed* from chosen integer codes, scales and mins by the packers below, written from the field
+  descriptions of each format in the opposite direction (codes -> bytes), and decoded back to the exact value
+  s * q - m rounded once to float32 -- a transposed nibble, a wrong bit position, a swapped scale/min or a wrong
+  group order in either direction fails it;
+* library conversions: numpy's float16 -> float32 over all 65536 fp16 bit patterns, torch's bfloat16 -> float32;
+* special blocks: all-zero, unit scales.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+import oracle.twin as twin
+
+RNG = np.random.default_rng(7)
+TYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ4_XS=23, BF16=30)
+LEVELS = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+
+
+def f16_bits(x):
+    return int(np.float16(x).view(np.uint16))
+
+
+def rand_f16_scale(rng, lo=-6, hi=2):
+    """A random normal fp16 value (sign, exponent in [lo, hi), random fraction) as (bits, exact float)."""
+    e = int(rng.integers(lo, hi))
+    v = (1.0 + int(rng.integers(0, 1024)) / 1024.0) * 2.0 ** e * (1 if rng.random() < 0.5 else -1)
+    return f16_bits(v), v
+
+
+def random_finite(qtype, rows, cols, rng):
+    """Random GGUF bytes of a format with every fp16 / bf16 field finite (exponent MSB cleared)."""
+    qk, bb = oracle.qblock(qtype)
+    raw = rng.integers(0, 256, size=rows * (cols // qk) * bb, dtype=np.uint8)
+    blk = raw.reshape(-1, bb)
+    hi_bytes = {30: [1], 8: [1], 20: [1], 23: [1], 12: [1, 3], 13: [1, 3], 14: [209]}[qtype]
+    for b in hi_bytes:
+        blk[:, b] &= 0xBF
+    return raw
+
+
+# ---------------------------------------------------------------------------------------------------------
+# packers: codes -> GGUF bytes, one block at a time
+
+
+def pack_q8_0(d_bits, q):
+    return np.concatenate([np.array([d_bits & 255, d_bits >> 8], np.uint8), np.asarray(q, np.int8).view(np.uint8)])
+
+
+def pack_iq4_nl(d_bits, idx):
+    idx = np.asarray(idx)
+    qs = (idx[:16] | (idx[16:] << 4)).astype(np.uint8)
+    return np.concatenate([np.array([d_bits & 255, d_bits >> 8], np.uint8), qs])
+
+
+def pack_iq4_xs(d_bits, ls, idx):
+    """ls [8] 6-bit group scales, idx [256] level indices."""
+    sh, sl = 0, np.zeros(4, np.uint8)
+    qs = np.zeros(128, np.uint8)
+    for g in range(8):
+        sl[g // 2] |= (ls[g] & 15) << (4 * (g % 2))
+        sh |= (ls[g] >> 4) << (2 * g)
+        gi = np.asarray(idx[32 * g:32 * g + 32])
+        qs[16 * g:16 * g + 16] = gi[:16] | (gi[16:] << 4)
+    head = np.array([d_bits & 255, d_bits >> 8, sh & 255, sh >> 8], np.uint8)
+    return np.concatenate([head, sl, qs])
+
+
+def pack_k_scales(sc, mn):
+    """8 six-bit scales and mins -> the 12 bytes of a Q4_K / Q5_K super-block."""
+    out = np.zeros(12, np.uint8)
+    for j in range(4):
+        out[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        out[j + 4] = (mn[j] & 63) | ((mn[j + 4] >> 4) << 6)
+        out[j + 8] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    return out
+
+
+def pack_q4_k(d_bits, dm_bits, sc, mn, q):
+    """q [256] 4-bit codes; group g = values 32 g .. 32 g + 31."""
+    qs = np.zeros(128, np.uint8)
+    for g in range(8):
+        qs[32 * (g // 2):32 * (g // 2) + 32] |= (np.asarray(q[32 * g:32 * g + 32]) << (4 * (g % 2))).astype(np.uint8)
+    head = np.array([d_bits & 255, d_bits >> 8, dm_bits & 255, dm_bits >> 8], np.uint8)
+    return np.concatenate([head, pack_k_scales(sc, mn), qs])
+
+
+def pack_q5_k(d_bits, dm_bits, sc, mn, q):
+    """q [256] 5-bit codes."""
+    q = np.asarray(q)
+    qh = np.zeros(32, np.uint8)
+    for g in range(8):
+        qh |= ((q[32 * g:32 * g + 32] >> 4) << g).astype(np.uint8)
+    b4 = pack_q4_k(d_bits, dm_bits, sc, mn, q & 15)
+    return np.concatenate([b4[:16], qh, b4[16:]])
+
+
+def pack_q6_k(d_bits, sc, c):
+    """c [256] 6-bit codes (value = d * sc * (c - 32)), sc [16] int8."""
+    ql, qh = np.zeros(128, np.uint8), np.zeros(64, np.uint8)
+    for v in range(256):
+        n, k, l = v // 128, (v % 128) // 32, v % 32
+        ql[64 * n + 32 * (k & 1) + l] |= (c[v] & 15) << (4 * (k >> 1))
+        qh[32 * n + l] |= (c[v] >> 4) << (2 * k)
+    return np.concatenate([ql, qh, np.asarray(sc, np.int8).view(np.uint8),
+                           np.array([d_bits & 255, d_bits >> 8], np.uint8)])
+
+
+def f32_once(x):
+    """A float64 value that is exact, rounded once to float32."""
+    return np.float32(x)
+
+
+# ---------------------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("rows,cols", [(3, 256), (7, 768), (1, 2560)])
+def test_oracle_matches_numpy_twin(name, rows, cols):
+    t = TYPES[name]
+    raw = random_finite(t, rows, cols, RNG)
+    a, b = oracle.dequant(t, raw, rows, cols), twin.dequant(t, raw, rows, cols)
+    assert np.isfinite(a).all()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_f16_decode_all_bit_patterns():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([oracle.f16_to_f32(int(b)) for b in bits], np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_bf16_matches_torch():
+    torch = pytest.importorskip("torch")
+    raw = random_finite(30, 4, 512, RNG)
+    ref = torch.from_numpy(raw.view(np.int16).copy()).view(torch.bfloat16).float().numpy().reshape(4, 512)
+    assert np.array_equal(oracle.dequant(30, raw, 4, 512).view(np.uint32), ref.view(np.uint32))
+
+
+def test_q8_0_packed_codes():
+    blocks, want = [], []
+    for _ in range(8):
+        db, d = rand_f16_scale(RNG)
+        q = RNG.integers(-128, 128, size=32)
+        blocks.append(pack_q8_0(db, q))
+        want += [f32_once(d * v) for v in q]
+    got = oracle.dequant(8, np.concatenate(blocks), 1, 256)[0]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_iq4_nl_packed_codes():
+    blocks, want = [], []
+    for _ in range(8):
+        db, d = rand_f16_scale(RNG)
+        idx = RNG.integers(0, 16, size=32)
+        blocks.append(pack_iq4_nl(db, idx))
+        want += [f32_once(d * LEVELS[i]) for i in idx]
+    got = oracle.dequant(20, np.concatenate(blocks), 1, 256)[0]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_iq4_xs_packed_codes():
+    blocks, want = [], []
+    for _ in range(3):
+        db, d = rand_f16_scale(RNG)
+        ls = RNG.integers(0, 64, size=8)
+        idx = RNG.integers(0, 16, size=256)
+        blocks.append(pack_iq4_xs(db, ls, idx))
+        for v in range(256):
+            dl = np.float32(d * (int(ls[v // 32]) - 32))    # exact: 11 x 6 significant bits
+            want.append(f32_once(float(dl) * LEVELS[idx[v]]))
+    got = oracle.dequant(23, np.concatenate(blocks), 1, 768)[0]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+@pytest.mark.parametrize("qtype", [12, 13])
+def test_k_quants_packed_codes(qtype):
+    blocks, want = [], []
+    for _ in range(3):
+        db, d = rand_f16_scale(RNG)
+        mb, dm = rand_f16_scale(RNG)
+        sc, mn = RNG.integers(0, 64, size=8), RNG.integers(0, 64, size=8)
+        q = RNG.integers(0, 16 if qtype == 12 else 32, size=256)
+        blocks.append((pack_q4_k if qtype == 12 else pack_q5_k)(db, mb, sc, mn, q))
+        for v in range(256):
+            g = v // 32
+            want.append(f32_once(d * int(sc[g]) * int(q[v]) - dm * int(mn[g])))   # exact in float64, one rounding
+    got = oracle.dequant(qtype, np.concatenate(blocks), 1, 768)[0]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_q6_k_packed_codes():
+    blocks, want = [], []
+    for _ in range(3):
+        db, d = rand_f16_scale(RNG)
+        sc = RNG.integers(-128, 128, size=16)
+        c = RNG.integers(0, 64, size=256)
+        blocks.append(pack_q6_k(db, sc, c))
+        for v in range(256):
+            n, k, l = v // 128, (v % 128) // 32, v % 32
+            ds = np.float32(d * int(sc[8 * n + 2 * k + l // 16]))  # exact: 11 x 8 significant bits
+            want.append(f32_once(float(ds) * (int(c[v]) - 32)))
+    got = oracle.dequant(14, np.concatenate(blocks), 1, 768)[0]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_zero_block_decodes_to_zero(name):
+    """All-zero bytes: every scale is +0, so every value is zero whatever the code's offset (IQ4 level -127, Q6_K
+    code - 32, Q4_K/Q5_K min)."""
+    t = TYPES[name]
+    qk, bb = oracle.qblock(t)
+    cols = max(qk, 256)
+    assert np.all(oracle.dequant(t, np.zeros(cols // qk * bb, np.uint8), 1, cols) == 0)
+
+
+def test_unit_scales_expose_codes():
+    one = f16_bits(1.0)
+    # Q8_0 with d = 1 returns the int8 codes themselves
+    q = np.arange(-16, 16)
+    assert np.array_equal(oracle.dequant(8, pack_q8_0(one, q), 1, 32)[0], q.astype(np.float32))
+    # Q6_K with d = 1 and scales 1 returns code - 32 in value order
+    c = RNG.integers(0, 64, size=256)
+    got = oracle.dequant(14, pack_q6_k(one, np.ones(16, np.int64), c), 1, 256)[0]
+    assert np.array_equal(got, (c - 32).astype(np.float32))
+    # Q4_K with d = 1, scale 1, min 0 returns the 4-bit codes
+    q4 = RNG.integers(0, 16, size=256)
+    got = oracle.dequant(12, pack_q4_k(one, one, np.ones(8, np.int64), np.zeros(8, np.int64), q4), 1, 256)[0]
+    assert np.array_equal(got, q4.astype(np.float32))
+
+
+def test_gemv_oracle_is_float64_dot_of_decoded_rows():
+    raw = random_finite(23, 9, 512, RNG)
+    x = RNG.standard_normal((3, 512)).astype(np.float32)
+    W = oracle.dequant(23, raw, 9, 512).astype(np.float64)
+    ref = x.astype(np.float64) @ W.T
+    assert np.allclose(oracle.gemv(23, raw, 9, 512, x), ref, rtol=1e-13, atol=1e-10)
