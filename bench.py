@@ -6,7 +6,8 @@ per layer (4.6 GB of fp32 state, far above the 256 MB Infinity Cache).  One step
 sequences through all 36 layers, replayed as one hipGraph; inputs are resident in HBM before the timed region.
 ``value`` is the algorithmic HBM bytes of the step (285,360,896 B per layer) per second of the timed region.
 
-Also reported (``extra``): config 0 (DeltaNet core, B = 1), config 1 (fused block, B = 1, 36 layers), config 3
+Also reported (``extra``): config 0 (DeltaNet core, B = 1), config 1 (fused block, B = 1, 36 layers), config 2 as
+speculative verify steps (nt new tokens, the previous step's accepted tokens committed by replay), config 3
 (GQA decode at 4K / 32K / 128K context, B = 1 and 16), config 4 (hybrid 36 + 12 layers, B = 16, context 32K),
 the streaming-copy yardstick, and the float64 CPU oracle timed on this box's host cores (``cpu_baseline``).
 
@@ -95,6 +96,47 @@ class GdnStack:
             for b in d.values():
                 b.free()
         self.pos.free()
+
+
+class VerifyStack:
+    """Speculative verify steps with deferred commit (fn_gdn_verify_dev): L fused DeltaNet layers of B sequences,
+    nt new tokens per step and kr accepted tokens of the previous step replayed into the committed state first."""
+
+    def __init__(self, lib, B, L, nt, kr, seed):
+        self.lib, self.B, self.L, self.nt = lib, B, L, nt
+        self.ring = 8 if nt <= 5 else 16  # a power of two >= nt + 3 (nt rows of the previous step may be replayed)
+        self.pos = hiprt.Buf.like(np.full(B, 100, np.int32))
+        self.kr = hiprt.Buf.like(np.full(B, kr, np.int32))
+        self.layers = []
+        for il in range(L):
+            lay = fn_synth.BlockLayer(B=1, config=2, layer=il)
+            d = {"S": hiprt.Buf.empty((B, NVH, DK, DK)), "ring": hiprt.Buf.empty((B, self.ring, C)),
+                 "qkv": hiprt.Buf.empty((B, nt, C)), "z": hiprt.Buf.empty((B, nt, NVH * DK)),
+                 "ab": hiprt.Buf.empty((B, nt, 2 * NVH)), "rqkv": hiprt.Buf.empty((B, nt, C)),
+                 "rab": hiprt.Buf.empty((B, nt, 2 * NVH)), "out": hiprt.Buf.empty((B, nt, NVH * DK)),
+                 "conv_w": hiprt.Buf.like(lay.conv_w), "dt": hiprt.Buf.like(lay.dt_bias),
+                 "sa": hiprt.Buf.like(lay.ssm_a), "nw": hiprt.Buf.like(lay.norm_w)}
+            s = seed * 1000033 + il * 19
+            lib.fill_normal_dev(d["S"].ptr, B * NVH * DK * DK, s + 1, 0.0, 0.02)
+            for i, key in enumerate(("ring", "qkv", "z", "ab", "rqkv", "rab")):
+                lib.fill_normal_dev(d[key].ptr, d[key].nbytes // 4, s + 2 + i)
+            self.layers.append(d)
+        hiprt.sync()
+
+    def launch(self, stream):
+        self.lib.advance_by_dev(self.pos.ptr, self.kr.ptr, self.B, stream.handle)
+        for d in self.layers:
+            self.lib.gdn_verify_dev(self.B, NKH, NVH, self.nt, self.ring, self.pos.ptr, self.kr.ptr, self.nt,
+                                    d["rqkv"].ptr, d["rab"].ptr, d["qkv"].ptr, d["conv_w"].ptr, d["ring"].ptr,
+                                    d["ab"].ptr, d["dt"].ptr, d["sa"].ptr, d["S"].ptr, d["z"].ptr, d["nw"].ptr,
+                                    d["out"].ptr, stream.handle)
+
+    def free(self):
+        for d in self.layers:
+            for b in d.values():
+                b.free()
+        self.pos.free()
+        self.kr.free()
 
 
 class CoreStack:
@@ -398,6 +440,17 @@ def main():
         extra["config1_block_b1"] = {"ms_per_step": round(ms, 4), "us_per_layer_step": round(ms * 1e3 / 36, 2),
                                      "tokens_per_s": round(1e3 / ms, 1),
                                      "gbs": round(36 * fn_synth.gdn_block_bytes(1) / (ms * 1e-3) / 1e9, 1)}
+        # config 2 as speculative verify steps: nt = 4 new tokens per sequence per step, the previous step's
+        # accepted tokens (kr of them) replayed into the committed state first; one S read + write per step
+        for nt_v, kr_v in ((4, 2), (4, 4), (8, 4)):
+            vs = VerifyStack(lib, 64, 36, nt_v, kr_v, seed=6)
+            ms = time_graph(stream, lambda: vs.launch(stream), steps, warmup)
+            vs.free()
+            by = fn_synth.gdn_verify_bytes(64, nt_v, kr_v)
+            extra[f"config2_verify_b64_nt{nt_v}_kr{kr_v}"] = {
+                "ms_per_step": round(ms, 4), "us_per_layer_step": round(ms * 1e3 / 36, 2),
+                "draft_tokens_per_s": round(64 * nt_v * 1e3 / ms, 1), "gbs": round(36 * by / (ms * 1e-3) / 1e9, 1)}
+            log(f"[bench] config 2 verify nt={nt_v} kr={kr_v}: {ms * 1e3 / 36:.2f} us/layer-step")
         # config 3: GQA decode
         for Bq, ctx, nl in ((1, 4096, 32), (1, 32768, 8), (1, 131072, 2), (16, 32768, 2)):
             at = AttnStack(lib, Bq, ctx, nl, seed=3)
@@ -463,7 +516,7 @@ def main():
                    "global_batch": B, "layers": L, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "k_gdn<true> (fused DeltaNet block)", "bytes_per_launch": bytes_layer,
+                     "kernel": "k_gdn<1> (fused DeltaNet block)", "bytes_per_launch": bytes_layer,
                      "us_per_launch": round(ms_kern * 1e3, 3)},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -69,6 +69,21 @@ FN_API int fn_gdn_block_dev(int B, int nkh, int nvh, int dk, int dv, int head_ma
     return fn::gdn_block_launch(p, (hipStream_t) stream);
 }
 
+FN_API int fn_gdn_verify_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int gate_act, int nt, int ring,
+                             const int32_t *pos, const int32_t *kr, int rnt, const float *rqkv, const float *rab,
+                             const float *qkv, const float *conv_w, float *conv_ring, const float *ab,
+                             const float *dt_bias, const float *ssm_a, float *S, const float *z, const float *norm_w,
+                             float eps, float *out, void *stream) {
+    fn::GdnVerify p{{B, nkh, nvh, dk, dv, head_map, gate_act, nt, ring, eps, pos, qkv, conv_w, conv_ring, ab, dt_bias,
+                     ssm_a, S, z, norm_w, out},
+                    kr, rnt, rqkv, rab};
+    return fn::gdn_verify_launch(p, (hipStream_t) stream);
+}
+
+FN_API int fn_advance_by_dev(int32_t *pos, const int32_t *kr, int B, void *stream) {
+    return fn::advance_by_launch(pos, kr, B, (hipStream_t) stream);
+}
+
 FN_API int fn_gdn_core_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int nt, const float *q,
                            const float *k, const float *v, const float *beta, const float *g, float *S, float *o,
                            void *stream) {

@@ -390,6 +390,11 @@ __global__ void k_advance(int32_t *pos, int B, int nt) {
     if (b < B) pos[b] += nt;
 }
 
+__global__ void k_advance_by(int32_t *pos, const int32_t *kr, int B) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < B) pos[b] += kr[b];
+}
+
 }  // namespace
 
 size_t attn_work_bytes(int B, int nq, int nt, int hd, int nsplit) {
@@ -505,6 +510,13 @@ int attn_qsa_launch(const AttnDecode &p, const QsaIndexer &ix, hipStream_t st) {
 int advance_launch(int32_t *pos, int B, int nt, hipStream_t st) {
     if (!pos || B < 1) FN_FAIL("advance: bad arguments");
     hipLaunchKernelGGL(k_advance, dim3((B + 255) / 256), dim3(256), 0, st, pos, B, nt);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+int advance_by_launch(int32_t *pos, const int32_t *kr, int B, hipStream_t st) {
+    if (!pos || !kr || B < 1) FN_FAIL("advance_by: bad arguments");
+    hipLaunchKernelGGL(k_advance_by, dim3((B + 255) / 256), dim3(256), 0, st, pos, kr, B);
     FN_CK(hipGetLastError());
     return 0;
 }

@@ -31,7 +31,18 @@ struct GdnCore {
     float *o;                           // [B][nt][nvh][dv]
 };
 
+// A verify step with deferred commit: blk.pos[b] is the position of the first new token; the kr[b] <= rnt tokens
+// before it (positions pos - kr .. pos - 1) are the previous call's, replayed from rqkv [B][rnt][C] and
+// rab [B][rnt][2 nvh] into the committed state first; the blk.nt new tokens get outputs and leave state untouched.
+struct GdnVerify {
+    GdnBlock blk;
+    const int32_t *kr;
+    int rnt;
+    const float *rqkv, *rab;
+};
+
 int gdn_block_launch(const GdnBlock &p, hipStream_t st);
+int gdn_verify_launch(const GdnVerify &p, hipStream_t st);
 int gdn_core_launch(const GdnCore &p, hipStream_t st);
 
 struct AttnDecode {
@@ -51,6 +62,7 @@ size_t attn_work_bytes(int B, int nq, int nt, int hd, int nsplit);
 int attn_pick_nsplit(int B, int nkv, int nt, int ctx);
 int attn_decode_launch(const AttnDecode &p, hipStream_t st);
 int advance_launch(int32_t *pos, int B, int nt, hipStream_t st);
+int advance_by_launch(int32_t *pos, const int32_t *kr, int B, hipStream_t st);  // pos[b] += kr[b]
 
 int fill_normal_launch(float *p, size_t n, uint64_t seed, float mean, float std, hipStream_t st);
 int copy_launch(void *dst, const void *src, size_t bytes, hipStream_t st);

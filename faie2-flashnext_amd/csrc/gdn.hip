@@ -39,6 +39,11 @@ namespace {
 #ifndef GDN_WPE
 #define GDN_WPE 1
 #endif
+#ifndef GDN_VERIFY_WPE
+// the verify step runs several tokens per call, where two workgroups per CU (four waves per SIMD, 128 VGPRs, a few
+// spills) beat one: B = 64, 4 new + 2 replayed tokens, 125 -> 101 us per layer-step on MI355X
+#define GDN_VERIFY_WPE 4
+#endif
 
 constexpr int DK = 128, DV = 128;
 constexpr int THREADS = GDN_THREADS;       // 256 or 512
@@ -63,6 +68,9 @@ struct GdnArgs {
     const float *z, *norm_w;
     float *out;
     const float *q, *k, *v, *beta, *g;  // core variant inputs
+    const int32_t *kr;                  // verify: tokens of the previous call to commit first, per sequence
+    int rnt;                            // verify: token stride of the replay inputs
+    const float *rqkv, *rab;            // verify: the previous call's qkv [B][rnt][C] and ab [B][rnt][2 nvh]
 };
 
 // Causal depthwise conv (kernel 4, weights oldest tap first) + SiLU (faie2fn.cu:1392-1395) of one channel.
@@ -103,8 +111,24 @@ __device__ __forceinline__ void conv_store(const ConvChan &cc, const GdnArgs &a,
     if (a.nt >= 3) ring_b[(size_t) ((last - 2) & (a.ring - 1)) * C + c] = cc.hist[1];
 }
 
-template <bool FUSED>
-__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GDN_WPE, 8))) k_gdn(const GdnArgs a) {
+// MODE 0: the bare core; 1: the fused block (every token committed); 2: the fused block as a verify step with
+// deferred commit -- first the kr[b] tokens of the previous call that the caller accepted are replayed from their
+// saved inputs (no output), the state and ring after them are written (the committed state), then the nt new tokens
+// run on the state in registers only: their outputs are written, their state is not.
+// mid-loop, once token u = n has been shifted in (n >= 1 tokens processed, the last at position end - 1): the raw
+// inputs of positions end-3 .. end-1 are hist[0..2]; write the slots of the ones this call processed (the last
+// min(n, 3))
+__device__ __forceinline__ void conv_store_hist(const ConvChan &cc, const GdnArgs &a, float *ring_b, int C, int c, int end,
+                                                int n) {
+    ring_b[(size_t) ((end - 1) & (a.ring - 1)) * C + c] = cc.hist[2];
+    if (n >= 2) ring_b[(size_t) ((end - 2) & (a.ring - 1)) * C + c] = cc.hist[1];
+    if (n >= 3) ring_b[(size_t) ((end - 3) & (a.ring - 1)) * C + c] = cc.hist[0];
+}
+
+template <int MODE>
+__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(MODE == 2 ? GDN_VERIFY_WPE : GDN_WPE, 8)))
+k_gdn(const GdnArgs a) {
+    constexpr bool FUSED = MODE >= 1, VERIFY = MODE == 2;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int cg = tid & 31, rg = tid >> 5;
     const int bh = blockIdx.x, b = bh / a.nvh, h = bh - b * a.nvh;
@@ -119,24 +143,30 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
 
     // 1. every input of the first token is requested before the state tile, so nothing waits behind S twice:
     //    conv weights, ring taps and raw inputs (waves 0-3), z and the norm weight (wave 0)
-    const int pos = FUSED ? a.pos[b] : 0;
+    // verify: pos is the position of the first new token; the kr replayed tokens sit at pos - kr .. pos - 1
+    const int kr = VERIFY ? max(0, min(a.kr[b], a.rnt)) : 0, ntot = kr + a.nt;  // clamped: never past the replay rows
+    const int pos = FUSED ? a.pos[b] - kr : 0;  // position of the first token this call processes
     const float *x_b = a.qkv + (size_t) b * a.nt * C;
+    const float *rx_b = VERIFY ? a.rqkv + (size_t) b * a.rnt * C : x_b;
     float *ring_b = a.ring_buf + (size_t) b * a.ring * C;
     const int cq = kh * DK + tid, ck = a.nkh * DK + kh * DK + tid, cv = 2 * a.nkh * DK + h * DV + (tid - DK);
     ConvChan c0{}, c1{};
     float4 z4 = f4(0.0f), w4 = f4(0.0f);
     if (FUSED) {
+        const float *x0 = kr > 0 ? rx_b : x_b;  // raw input of the first token
         if (qk_thr) {
-            conv_load(c0, a, ring_b, x_b, C, cq, pos);
-            conv_load(c1, a, ring_b, x_b, C, ck, pos);
+            conv_load(c0, a, ring_b, x0, C, cq, pos);
+            conv_load(c1, a, ring_b, x0, C, ck, pos);
         } else if (v_thr) {
-            conv_load(c0, a, ring_b, x_b, C, cv, pos);
+            conv_load(c0, a, ring_b, x0, C, cv, pos);
         }
         if (wave == 0 && lane < 32) {
-            z4 = *reinterpret_cast<const float4 *>(a.z + (size_t) b * a.nt * a.nvh * DV + (size_t) h * DV + cg * 4);
+            if (kr == 0)
+                z4 = *reinterpret_cast<const float4 *>(a.z + (size_t) b * a.nt * a.nvh * DV + (size_t) h * DV + cg * 4);
             w4 = reinterpret_cast<const float4 *>(a.norm_w)[cg];
         }
     }
+    const bool primary = a.head_map == 0 ? h < a.nkh : (h % (a.nvh / a.nkh)) == 0;
 
     // 2. state tile into registers
     float4 s[ROWS_PT];
@@ -146,20 +176,73 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
 
     const float scale = 0.08838834764831845f;  // 1/sqrt(128), faie2fn.cu:1352
 
-    for (int t = 0; t < a.nt; ++t) {
-        const size_t bt = (size_t) b * a.nt + t;
-        if (t > 0) {
+    // Inputs of token u of this call: its raw conv channels, z (wave 0) and alpha/beta logits.  The next token's are
+    // requested one iteration ahead, so a multi-token call (verify, prefill) does not wait a memory round trip per
+    // token.
+    float ga = 0.0f, gb = 0.0f, dtb = 0.0f, ssa = 0.0f;  // this token's alpha, beta logits; the head's gate params
+    float nx0 = 0.0f, nx1 = 0.0f, na = 0.0f, nb = 0.0f;  // next token's raw channels and logits
+    float4 nz = f4(0.0f);
+#define GDN_PREFETCH(U_)                                                                                           \
+    do {                                                                                                          \
+        const int u_ = (U_);                                                                                      \
+        const bool rp_ = VERIFY && u_ < kr;                                                                       \
+        const float *xt_ = rp_ ? rx_b + (size_t) u_ * C : x_b + (size_t) (u_ - kr) * C;                           \
+        const float *abt_ = rp_ ? a.rab + ((size_t) b * a.rnt + u_) * 2 * a.nvh                                  \
+                                : a.ab + ((size_t) b * a.nt + (u_ - kr)) * 2 * a.nvh;                             \
+        if (qk_thr) {                                                                                             \
+            nx0 = xt_[cq];                                                                                        \
+            nx1 = xt_[ck];                                                                                        \
+        } else if (v_thr) {                                                                                       \
+            nx0 = xt_[cv];                                                                                        \
+        }                                                                                                         \
+        if (wave == 0 && lane < 32 && !rp_)                                                                       \
+            nz = *reinterpret_cast<const float4 *>(a.z + ((size_t) b * a.nt + (u_ - kr)) * a.nvh * DV +          \
+                                                   (size_t) h * DV + cg * 4);                                     \
+        na = abt_[h];                                                                                             \
+        nb = abt_[a.nvh + h];                                                                                     \
+    } while (0)
+    if (FUSED) {
+        const float *ab0 = kr > 0 ? a.rab + (size_t) b * a.rnt * 2 * a.nvh : a.ab + (size_t) b * a.nt * 2 * a.nvh;
+        ga = ab0[h];
+        gb = ab0[a.nvh + h];
+        dtb = a.dt_bias[h];
+        ssa = a.ssm_a[h];
+        if (ntot > 1) GDN_PREFETCH(1);
+    }
+
+    for (int u = 0; u < ntot; ++u) {
+        // token u: a replayed one (u < kr, inputs from the previous call, no output) or new token t = u - kr
+        const bool replay = VERIFY && u < kr;
+        const int t = u - kr;
+        const size_t bt = (size_t) b * a.nt + (replay ? 0 : t);
+        if (u > 0) {
             __syncthreads();  // the previous token's LDS reads are done
             if (FUSED) {
-                const float *xt = x_b + (size_t) t * C;
                 if (qk_thr) {
-                    c0.shift(xt[cq]);
-                    c1.shift(xt[ck]);
+                    c0.shift(nx0);
+                    c1.shift(nx1);
                 } else if (v_thr) {
-                    c0.shift(xt[cv]);
+                    c0.shift(nx0);
                 }
-                if (wave == 0 && lane < 32)
-                    z4 = *reinterpret_cast<const float4 *>(a.z + bt * a.nvh * DV + (size_t) h * DV + cg * 4);
+                if (!replay) z4 = nz;
+                ga = na;
+                gb = nb;
+                if (u + 1 < ntot) GDN_PREFETCH(u + 1);
+            }
+        }
+        if (VERIFY && u == kr && kr > 0) {
+            // the committed state, before the first new token moves the registers on: S after the replayed tokens,
+            // and the ring slots of the replayed positions (the last up to three; after the shift above hist holds
+            // the raw inputs of positions pos + kr - 3 .. pos + kr - 1)
+#pragma unroll
+            for (int r = 0; r < ROWS_PT; ++r) st_state(&Sh[(rg * ROWS_PT + r) * (DV / 4) + cg], s[r]);
+            if (qk_thr) {
+                if (primary) {
+                    conv_store_hist(c0, a, ring_b, C, cq, pos + kr, kr);
+                    conv_store_hist(c1, a, ring_b, C, ck, pos + kr, kr);
+                }
+            } else if (v_thr) {
+                conv_store_hist(c0, a, ring_b, C, cv, pos + kr, kr);
             }
         }
 
@@ -189,11 +272,10 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
         //    the identity above 20 (faie2fn.cu:1407-1410)
         float beta, gamma;
         if (FUSED) {
-            const float *abt = a.ab + bt * 2 * a.nvh;
-            beta = sigmoidf_(abt[a.nvh + h]);
-            const float x = abt[h] + a.dt_bias[h];
+            beta = sigmoidf_(gb);
+            const float x = ga + dtb;
             const float sp = x > 20.0f ? x : log1pf(expf(x));
-            gamma = expf(sp * a.ssm_a[h]);
+            gamma = expf(sp * ssa);
         } else {
             beta = a.beta[bt * a.nvh + h];
             gamma = expf(a.g[bt * a.nvh + h]);
@@ -272,7 +354,7 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
         }
 
         // 7. output: wave 0 holds every column twice (row groups 0 and 1)
-        if (wave == 0) {
+        if (wave == 0 && !replay) {
             if (FUSED) {
                 // gated RMSNorm on = o * rsqrt(mean o^2 + eps) * w * act(z) (faie2fn.cu:1422-1424); the wave sum
                 // counts each column twice, exactly, so halve it
@@ -300,11 +382,12 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
     }
 
     // 8. write back: state once; ring slots of this call's last (up to) three positions from the registers.  The
-    //    q/k channels of a key head are written by one of its value heads only.
+    //    q/k channels of a key head are written by one of its value heads only.  A verify step wrote its committed
+    //    state above and leaves the new tokens' state uncommitted.
+    if (VERIFY) return;
 #pragma unroll
     for (int r = 0; r < ROWS_PT; ++r) st_state(&Sh[(rg * ROWS_PT + r) * (DV / 4) + cg], s[r]);
     if (FUSED) {
-        const bool primary = a.head_map == 0 ? h < a.nkh : (h % (a.nvh / a.nkh)) == 0;
         if (qk_thr) {
             if (primary) {
                 conv_store(c0, a, ring_b, C, cq, pos);
@@ -315,6 +398,8 @@ __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(GD
         }
     }
 }
+
+#undef GDN_PREFETCH
 
 int check_dims(int B, int nkh, int nvh, int dk, int dv, int head_map, int nt) {
     if (B < 1 || nkh < 1 || nvh < 1 || nt < 1) FN_FAIL("gdn: B, nkh, nvh and nt must be >= 1");
@@ -340,7 +425,7 @@ int gdn_block_launch(const GdnBlock &p, hipStream_t st) {
     a.gate_act = p.gate_act; a.eps = p.eps; a.pos = p.pos; a.qkv = p.qkv; a.conv_w = p.conv_w;
     a.ring_buf = p.conv_ring; a.ab = p.ab; a.dt_bias = p.dt_bias; a.ssm_a = p.ssm_a; a.S = p.S; a.z = p.z;
     a.norm_w = p.norm_w; a.out = p.out;
-    hipLaunchKernelGGL(k_gdn<true>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
+    hipLaunchKernelGGL(k_gdn<1>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
 }
@@ -351,7 +436,31 @@ int gdn_core_launch(const GdnCore &p, hipStream_t st) {
     GdnArgs a{};
     a.B = p.B; a.nkh = p.nkh; a.nvh = p.nvh; a.nt = p.nt; a.ring = 4; a.head_map = p.head_map;
     a.q = p.q; a.k = p.k; a.v = p.v; a.beta = p.beta; a.g = p.g; a.S = p.S; a.out = p.o;
-    hipLaunchKernelGGL(k_gdn<false>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
+    hipLaunchKernelGGL(k_gdn<0>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+}  // namespace fn
+
+namespace fn {
+
+int gdn_verify_launch(const GdnVerify &p, hipStream_t st) {
+    const GdnBlock &q = p.blk;
+    if (check_dims(q.B, q.nkh, q.nvh, q.dk, q.dv, q.head_map, q.nt)) return -1;
+    if (q.gate_act != 0 && q.gate_act != 1) FN_FAIL("gdn: gate_act must be 0 (sigmoid) or 1 (silu)");
+    if (q.ring < 4 || (q.ring & (q.ring - 1))) FN_FAIL("gdn: ring must be a power of two >= 4");
+    if (p.rnt < 0 || p.rnt > q.ring - 3) FN_FAIL("gdn_verify: rnt (most tokens committed per call) must be <= ring - 3");
+    if (!q.pos || !q.qkv || !q.conv_w || !q.conv_ring || !q.ab || !q.dt_bias || !q.ssm_a || !q.S || !q.z ||
+        !q.norm_w || !q.out || !p.kr || (p.rnt > 0 && (!p.rqkv || !p.rab)))
+        FN_FAIL("gdn_verify: null pointer");
+    GdnArgs a{};
+    a.B = q.B; a.nkh = q.nkh; a.nvh = q.nvh; a.nt = q.nt; a.ring = q.ring; a.head_map = q.head_map;
+    a.gate_act = q.gate_act; a.eps = q.eps; a.pos = q.pos; a.qkv = q.qkv; a.conv_w = q.conv_w;
+    a.ring_buf = q.conv_ring; a.ab = q.ab; a.dt_bias = q.dt_bias; a.ssm_a = q.ssm_a; a.S = q.S; a.z = q.z;
+    a.norm_w = q.norm_w; a.out = q.out;
+    a.kr = p.kr; a.rnt = p.rnt; a.rqkv = p.rqkv; a.rab = p.rab;
+    hipLaunchKernelGGL(k_gdn<2>, dim3(q.B * q.nvh), dim3(THREADS), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
 }

@@ -128,3 +128,15 @@ def attn_qsa_bytes(B, L, top=512, nq=16, nkv=2, hd=HD, ixd=128):
     nb = L // 4
     keys = min(L, 4 * top + (L - 4 * nb)) if nb > top else L
     return B * (nb * ixd * 4 + keys * nkv * hd * 4 * 2 + 3 * nq * hd * 4 + 2 * nkv * hd * 4 + (5 * ixd + ixd) * 4)
+
+
+def gdn_verify_bytes(B, nt, kr, nkh=16, nvh=32):
+    """Algorithmic HBM bytes of one fused DeltaNet verify layer-step (deferred commit) for B sequences with nt new
+    tokens and kr replayed (committed) tokens each: S read + write once, conv state read + write (3 taps of C
+    channels), the replayed tokens' qkv and alpha/beta, the new tokens' qkv, z, alpha/beta in and outputs; per
+    layer the parameters once."""
+    C = 2 * nkh * DK + nvh * DV
+    per_seq = (2 * nvh * DK * DV * 4 + 2 * 3 * C * 4 + kr * (C + 2 * nvh) * 4
+               + nt * (C + nvh * DV + 2 * nvh) * 4 + nt * nvh * DV * 4)
+    per_layer = C * 4 * 4 + DV * 4 + 2 * nvh * 4
+    return B * per_seq + per_layer

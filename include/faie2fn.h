@@ -112,6 +112,25 @@ int fn_gdn_block_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int 
                      const float *dt_bias, const float *ssm_a, float *S, const float *z, const float *norm_w,
                      float eps, float *out, void *stream);
 
+/* A verify step of the fused DeltaNet block with deferred commit (speculative decoding; the reference's engine
+ * family verifies drafts by replay-commit, reference DESIGN.md:287-293, and FN's k_gdn already takes nt <= 8
+ * tokens of one sequence, faie2fn.cu:1390).  For sequence b, pos[b] is the position of the first new token and
+ * the kr[b] tokens before it (0 <= kr[b] <= rnt) are the previous call's accepted ones: the kernel first replays
+ * them from their saved inputs rqkv [B][rnt][C] and rab [B][rnt][2 nvh] (the previous call's qkv and ab) into the
+ * state, writes S and the ring as the committed state, then runs the nt new tokens on that state in registers
+ * only: out [B][nt][nvh dv] gets their outputs, S and the ring never hold them.  One read and one write of S per
+ * call, as in plain decode; the new tokens' outputs are bit-identical to decoding them one by one after the
+ * committed prefix.  ring >= rnt + 3; kr[b] outside [0, rnt] is clamped into it.  Advance pos by the accepted counts with fn_advance_by_dev before the step
+ * (the attention layers of the step then append the new tokens at pos, pos + 1, ... as usual). */
+int fn_gdn_verify_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int gate_act, int nt, int ring,
+                      const int32_t *pos, const int32_t *kr, int rnt, const float *rqkv, const float *rab,
+                      const float *qkv, const float *conv_w, float *conv_ring, const float *ab, const float *dt_bias,
+                      const float *ssm_a, float *S, const float *z, const float *norm_w, float eps, float *out,
+                      void *stream);
+
+/* pos[b] += kr[b] for b < B, on the stream (k_advance with per-sequence counts). */
+int fn_advance_by_dev(int32_t *pos, const int32_t *kr, int B, void *stream);
+
 /* DeltaNet core on device buffers (layouts of fn_test_gdn). */
 int fn_gdn_core_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int nt, const float *q, const float *k,
                     const float *v, const float *beta, const float *g, float *S, float *o, void *stream);

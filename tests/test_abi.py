@@ -133,3 +133,18 @@ def test_gemv_plan_shapes(fnlib):
         assert fnlib.gemv_plan(23, 10240, 2560)[2] == 3
     finally:
         fnlib.gemv_override(0)
+
+
+def test_verify_validates_before_device_work(fnlib):
+    """fn_gdn_verify_dev rejects a replay stride that does not fit the ring and missing replay inputs before any
+    launch."""
+    d = fnlib.d
+    p = [1] * 11  # non-null stand-ins for rqkv .. norm_w: validation fails before anything is dereferenced
+    assert len(d.fn_gdn_verify_dev.argtypes) == 26
+    # rnt = 2 with ring 4: 2 + 3 taps > 4
+    assert d.fn_gdn_verify_dev(1, 16, 32, 128, 128, 0, 0, 1, 4, 1, 1, 2, *p, 1e-6, 1, None) == -1
+    assert b"ring - 3" in d.fn_error()
+    # rnt = 1 but no replay inputs
+    assert d.fn_gdn_verify_dev(1, 16, 32, 128, 128, 0, 0, 1, 4, 1, 1, 1, None, None, *p[:9], 1e-6, 1, None) == -1
+    assert b"null pointer" in d.fn_error()
+    assert d.fn_advance_by_dev(None, None, 1, None) == -1
