@@ -4,10 +4,13 @@
 // Semantics follow k_gdn (reference engine/faie2fn.cu:1349-1431).  The kernel is organised for CDNA4, not as a
 // translation of the sm_120 one:
 //   * 512 threads (eight wave64s) per head.  Thread (rg = tid / 32, cg = tid % 32) owns the 4 columns 4cg..4cg+3
-//     of the 8 state rows 8rg..8rg+7, i.e. 8 float4 registers.  Every wave load and store of S moves two
-//     contiguous 512-byte rows with 128-bit accesses, and S makes exactly one trip HBM -> VGPRs -> HBM per call,
-//     with the nontemporal hint on both legs (measured on MI355X: 62.2 -> 52.4 us per B = 64 layer-step; 256 or
-//     1024 threads per head and an XCD-contiguous head order were all slower).
+//     of the 8 state rows rg, rg + 16, ..., rg + 112, i.e. 8 float4 registers.  Every wave load and store of S
+//     moves two contiguous 512-byte rows with 128-bit accesses, and the eight waves' r-th accesses together sweep
+//     rows 16r .. 16r + 15, 8 KiB in a row, so the tile streams through HBM in address order (row groups of 8
+//     consecutive rows per thread scatter each sweep over the whole 64 KiB; on MI355X the bare tile pass takes
+//     43.8 instead of 49.1 us at B = 64).  S makes exactly one trip HBM -> VGPRs -> HBM per call, with the
+//     nontemporal hint on both legs (62.2 -> 52.4 us per B = 64 layer-step; 256 or 1024 threads per head and an
+//     XCD-contiguous head order were all slower).
 //   * One read pass computes both reductions the step needs, kv = S^T k and sq = S^T q (old S), because
 //       S' = g S + k d^T  with  d = beta (v - g kv)    =>    S'^T q = g sq + (k.q) d.
 //     The column partials of the 16 row groups are folded with a lane^32 permute (2 groups per wave) and
@@ -49,6 +52,7 @@ constexpr int DK = 128, DV = 128;
 constexpr int THREADS = GDN_THREADS;       // 256 or 512
 constexpr int WAVES = THREADS / 64;
 constexpr int ROWS_PT = DK * 32 / THREADS;  // state rows per thread (32 threads span a row)
+constexpr int RSTEP = THREADS / 32;         // row groups: thread row group rg owns rows rg, rg + RSTEP, ...
 static_assert(THREADS == 256 || THREADS == 512 || THREADS == 1024, "one state tile per 4, 8 or 16 waves");
 
 __device__ __forceinline__ float4 ld_state(const float4 *p) { return GDN_NT ? ld_nt(p) : *p; }
@@ -111,7 +115,8 @@ __device__ __forceinline__ void conv_store(const ConvChan &cc, const GdnArgs &a,
     if (a.nt >= 3) ring_b[(size_t) ((last - 2) & (a.ring - 1)) * C + c] = cc.hist[1];
 }
 
-// MODE 0: the bare core; 1: the fused block (every token committed); 2: the fused block as a verify step with
+// MODE 0: the bare core; 1: the fused block (every token committed); 3: the fused block for exactly one token (the
+// decode step: no token loop, no next-token prefetch, fewer registers); 2: the fused block as a verify step with
 // deferred commit -- first the kr[b] tokens of the previous call that the caller accepted are replayed from their
 // saved inputs (no output), the state and ring after them are written (the committed state), then the nt new tokens
 // run on the state in registers only: their outputs are written, their state is not.
@@ -128,7 +133,7 @@ __device__ __forceinline__ void conv_store_hist(const ConvChan &cc, const GdnArg
 template <int MODE>
 __global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(MODE == 2 ? GDN_VERIFY_WPE : GDN_WPE, 8)))
 k_gdn(const GdnArgs a) {
-    constexpr bool FUSED = MODE >= 1, VERIFY = MODE == 2;
+    constexpr bool FUSED = MODE >= 1, VERIFY = MODE == 2, ONE = MODE == 3;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int cg = tid & 31, rg = tid >> 5;
     const int bh = blockIdx.x, b = bh / a.nvh, h = bh - b * a.nvh;
@@ -144,7 +149,8 @@ k_gdn(const GdnArgs a) {
     // 1. every input of the first token is requested before the state tile, so nothing waits behind S twice:
     //    conv weights, ring taps and raw inputs (waves 0-3), z and the norm weight (wave 0)
     // verify: pos is the position of the first new token; the kr replayed tokens sit at pos - kr .. pos - 1
-    const int kr = VERIFY ? max(0, min(a.kr[b], a.rnt)) : 0, ntot = kr + a.nt;  // clamped: never past the replay rows
+    const int kr = VERIFY ? max(0, min(a.kr[b], a.rnt)) : 0;  // clamped: never past the replay rows
+    const int ntot = ONE ? 1 : kr + a.nt;
     const int pos = FUSED ? a.pos[b] - kr : 0;  // position of the first token this call processes
     const float *x_b = a.qkv + (size_t) b * a.nt * C;
     const float *rx_b = VERIFY ? a.rqkv + (size_t) b * a.rnt * C : x_b;
@@ -172,7 +178,7 @@ k_gdn(const GdnArgs a) {
     float4 s[ROWS_PT];
     float4 *Sh = reinterpret_cast<float4 *>(a.S + (size_t) bh * DK * DV);
 #pragma unroll
-    for (int r = 0; r < ROWS_PT; ++r) s[r] = ld_state(&Sh[(rg * ROWS_PT + r) * (DV / 4) + cg]);
+    for (int r = 0; r < ROWS_PT; ++r) s[r] = ld_state(&Sh[(rg + RSTEP * r) * (DV / 4) + cg]);
 
     const float scale = 0.08838834764831845f;  // 1/sqrt(128), faie2fn.cu:1352
 
@@ -207,7 +213,7 @@ k_gdn(const GdnArgs a) {
         gb = ab0[a.nvh + h];
         dtb = a.dt_bias[h];
         ssa = a.ssm_a[h];
-        if (ntot > 1) GDN_PREFETCH(1);
+        if (!ONE && ntot > 1) GDN_PREFETCH(1);
     }
 
     for (int u = 0; u < ntot; ++u) {
@@ -227,7 +233,7 @@ k_gdn(const GdnArgs a) {
                 if (!replay) z4 = nz;
                 ga = na;
                 gb = nb;
-                if (u + 1 < ntot) GDN_PREFETCH(u + 1);
+                if (!ONE && u + 1 < ntot) GDN_PREFETCH(u + 1);
             }
         }
         if (VERIFY && u == kr && kr > 0) {
@@ -235,7 +241,7 @@ k_gdn(const GdnArgs a) {
             // and the ring slots of the replayed positions (the last up to three; after the shift above hist holds
             // the raw inputs of positions pos + kr - 3 .. pos + kr - 1)
 #pragma unroll
-            for (int r = 0; r < ROWS_PT; ++r) st_state(&Sh[(rg * ROWS_PT + r) * (DV / 4) + cg], s[r]);
+            for (int r = 0; r < ROWS_PT; ++r) st_state(&Sh[(rg + RSTEP * r) * (DV / 4) + cg], s[r]);
             if (qk_thr) {
                 if (primary) {
                     conv_store_hist(c0, a, ring_b, C, cq, pos + kr, kr);
@@ -292,24 +298,20 @@ k_gdn(const GdnArgs a) {
         const float kq = sqk * rq * rk;
 
         // 5. one pass over the registers: column partials of S^T k and S^T q over this thread's rows
+        const float *ksf = reinterpret_cast<const float *>(ks4), *qsf = reinterpret_cast<const float *>(qs4);
         float4 kvp = f4(0.0f), sqp = f4(0.0f);
 #pragma unroll
-        for (int r4 = 0; r4 < ROWS_PT / 4; ++r4) {
-            const float4 kk = ks4[rg * (ROWS_PT / 4) + r4];
-            const float4 qq = qs4[rg * (ROWS_PT / 4) + r4];
-            const float kr[4] = {kk.x, kk.y, kk.z, kk.w}, qr[4] = {qq.x, qq.y, qq.z, qq.w};
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float4 sv = s[r4 * 4 + u];
-                kvp.x = fmaf(sv.x, kr[u], kvp.x);
-                kvp.y = fmaf(sv.y, kr[u], kvp.y);
-                kvp.z = fmaf(sv.z, kr[u], kvp.z);
-                kvp.w = fmaf(sv.w, kr[u], kvp.w);
-                sqp.x = fmaf(sv.x, qr[u], sqp.x);
-                sqp.y = fmaf(sv.y, qr[u], sqp.y);
-                sqp.z = fmaf(sv.z, qr[u], sqp.z);
-                sqp.w = fmaf(sv.w, qr[u], sqp.w);
-            }
+        for (int r = 0; r < ROWS_PT; ++r) {
+            const float kr = ksf[rg + RSTEP * r], qr = qsf[rg + RSTEP * r];
+            const float4 sv = s[r];
+            kvp.x = fmaf(sv.x, kr, kvp.x);
+            kvp.y = fmaf(sv.y, kr, kvp.y);
+            kvp.z = fmaf(sv.z, kr, kvp.z);
+            kvp.w = fmaf(sv.w, kr, kvp.w);
+            sqp.x = fmaf(sv.x, qr, sqp.x);
+            sqp.y = fmaf(sv.y, qr, sqp.y);
+            sqp.z = fmaf(sv.z, qr, sqp.z);
+            sqp.w = fmaf(sv.w, qr, sqp.w);
         }
         // fold row groups 2w and 2w+1 (lanes l and l^32), then across waves through LDS
         kvp.x += shfl_xor32(kvp.x); kvp.y += shfl_xor32(kvp.y); kvp.z += shfl_xor32(kvp.z); kvp.w += shfl_xor32(kvp.w);
@@ -340,17 +342,13 @@ k_gdn(const GdnArgs a) {
         o.w = fmaf(gamma, sq.w * rq, kq * d.w) * scale;
         const float4 dk4 = make_float4(d.x * rk, d.y * rk, d.z * rk, d.w * rk);  // k enters raw below
 #pragma unroll
-        for (int r4 = 0; r4 < ROWS_PT / 4; ++r4) {
-            const float4 kk = ks4[rg * (ROWS_PT / 4) + r4];
-            const float kr[4] = {kk.x, kk.y, kk.z, kk.w};
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                float4 &sv = s[r4 * 4 + u];
-                sv.x = fmaf(kr[u], dk4.x, gamma * sv.x);
-                sv.y = fmaf(kr[u], dk4.y, gamma * sv.y);
-                sv.z = fmaf(kr[u], dk4.z, gamma * sv.z);
-                sv.w = fmaf(kr[u], dk4.w, gamma * sv.w);
-            }
+        for (int r = 0; r < ROWS_PT; ++r) {
+            const float kr = ksf[rg + RSTEP * r];
+            float4 &sv = s[r];
+            sv.x = fmaf(kr, dk4.x, gamma * sv.x);
+            sv.y = fmaf(kr, dk4.y, gamma * sv.y);
+            sv.z = fmaf(kr, dk4.z, gamma * sv.z);
+            sv.w = fmaf(kr, dk4.w, gamma * sv.w);
         }
 
         // 7. output: wave 0 holds every column twice (row groups 0 and 1)
@@ -386,7 +384,7 @@ k_gdn(const GdnArgs a) {
     //    state above and leaves the new tokens' state uncommitted.
     if (VERIFY) return;
 #pragma unroll
-    for (int r = 0; r < ROWS_PT; ++r) st_state(&Sh[(rg * ROWS_PT + r) * (DV / 4) + cg], s[r]);
+    for (int r = 0; r < ROWS_PT; ++r) st_state(&Sh[(rg + RSTEP * r) * (DV / 4) + cg], s[r]);
     if (FUSED) {
         if (qk_thr) {
             if (primary) {
@@ -425,7 +423,8 @@ int gdn_block_launch(const GdnBlock &p, hipStream_t st) {
     a.gate_act = p.gate_act; a.eps = p.eps; a.pos = p.pos; a.qkv = p.qkv; a.conv_w = p.conv_w;
     a.ring_buf = p.conv_ring; a.ab = p.ab; a.dt_bias = p.dt_bias; a.ssm_a = p.ssm_a; a.S = p.S; a.z = p.z;
     a.norm_w = p.norm_w; a.out = p.out;
-    hipLaunchKernelGGL(k_gdn<1>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
+    if (p.nt == 1) hipLaunchKernelGGL(k_gdn<3>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
+    else hipLaunchKernelGGL(k_gdn<1>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
 }
