@@ -37,14 +37,30 @@ constexpr uint32_t pack4(int k) {
 constexpr uint32_t KV0 = pack4(0), KV1 = pack4(1), KV2 = pack4(2), KV3 = pack4(3);
 static_assert(KV0 == 0xBFAD9881u && KV3 == 0x71594535u, "IQ4 level packing");
 
-// four nibble indices (one per byte, 0..15) -> their four signed levels as bytes.  v_perm_b32 picks bytes out of
-// an 8-byte pair by selector 0..7, so levels 0..7 and 8..15 are looked up separately with the low 3 bits and the
-// index's bit 3 then chooses between the two results byte by byte.
-__device__ __forceinline__ uint32_t iq4_levels(uint32_t n) {
-    const uint32_t s = n & 0x07070707u;
-    const uint32_t lo = __builtin_amdgcn_perm(KV1, KV0, s);
-    const uint32_t hi = __builtin_amdgcn_perm(KV3, KV2, s);
-    const uint32_t sel = ((n >> 1) & 0x04040404u) | 0x03020100u;
+// a constant held in a VGPR the compiler cannot see through: gfx9 VOP3 encodings take no literal, so a VOP3 op
+// such as v_and_or_b32 with two 32-bit constants is only emitted when they sit in registers
+__device__ __forceinline__ uint32_t vconst(uint32_t c) {
+    uint32_t r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
+    return r;
+}
+
+struct Iq4Tab {
+    uint32_t kv0, kv1, kv2, kv3, m7, m4, sel0;
+    __device__ __forceinline__ Iq4Tab()
+        : kv0(vconst(KV0)), kv1(vconst(KV1)), kv2(vconst(KV2)), kv3(vconst(KV3)), m7(vconst(0x07070707u)),
+          m4(vconst(0x04040404u)), sel0(vconst(0x03020100u)) {}
+};
+
+// four nibble indices -> their four signed levels as bytes.  v_perm_b32 picks bytes out of an 8-byte pair by
+// selector 0..7, so levels 0..7 and 8..15 are looked up separately with the low 3 bits and the index's bit 3 then
+// chooses between the two results byte by byte.  The indices are the nibbles of w at bit offset SH (0: low nibbles,
+// 4: high nibbles): 3 perms, 2 shifts and 2 and-ors per four levels.
+template <int SH> __device__ __forceinline__ uint32_t iq4_levels(uint32_t w, const Iq4Tab &T) {
+    const uint32_t s = (w >> SH) & T.m7;
+    const uint32_t lo = __builtin_amdgcn_perm(T.kv1, T.kv0, s);
+    const uint32_t hi = __builtin_amdgcn_perm(T.kv3, T.kv2, s);
+    const uint32_t sel = ((w >> (SH + 1)) & T.m4) | T.sel0;
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
@@ -106,7 +122,7 @@ template <> struct Q<QT_BF16> {
 #pragma unroll
         for (int i = 0; i < 4; ++i) ld16(p + 16 * i, w + 4 * i);
     }
-    __device__ static void unpack(const uint32_t *w, int, Grp &o) {
+    __device__ static void unpack(const uint32_t *w, int, Grp &o, const Iq4Tab &T) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             o.q[2 * i] = __uint_as_float(w[i] << 16);
@@ -128,7 +144,7 @@ template <> struct Q<QT_Q8_0> {
         ld16(q + 16, w + 4);
         w[8] = ld2(R.b1 + 2 * g);
     }
-    __device__ static void unpack(const uint32_t *w, int, Grp &o) {
+    __device__ static void unpack(const uint32_t *w, int, Grp &o, const Iq4Tab &T) {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -148,10 +164,10 @@ template <> struct Q<QT_IQ4_NL> {
         ld16(R.b0 + 16 * g, w);
         w[4] = ld2(R.b1 + 2 * g);
     }
-    __device__ static void levels(const uint32_t *w, Grp &o) {
+    __device__ static void levels(const uint32_t *w, Grp &o, const Iq4Tab &T) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = iq4_levels(w[i] & 0x0F0F0F0Fu), hi = iq4_levels((w[i] >> 4) & 0x0F0F0F0Fu);
+            const uint32_t lo = iq4_levels<0>(w[i], T), hi = iq4_levels<4>(w[i], T);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 o.q[4 * i + k] = sbyte(lo, k);
@@ -159,8 +175,8 @@ template <> struct Q<QT_IQ4_NL> {
             }
         }
     }
-    __device__ static void unpack(const uint32_t *w, int, Grp &o) {
-        levels(w, o);
+    __device__ static void unpack(const uint32_t *w, int, Grp &o, const Iq4Tab &T) {
+        levels(w, o, T);
         o.s[0] = o.s[1] = h2f(w[4]);
         o.m[0] = o.m[1] = 0.0f;
     }
@@ -176,9 +192,9 @@ template <> struct Q<QT_IQ4_XS> {
         ld16(R.b0 + 16 * g, w);  // super-block g / 8 at 128 (g / 8), group g % 8 at 16 (g % 8) inside it
         ld8(R.b1 + 8 * (g >> 3), w + 4);
     }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o) {
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
         const int ib = g & 7;
-        Q<QT_IQ4_NL>::levels(w, o);
+        Q<QT_IQ4_NL>::levels(w, o, T);
         const uint32_t sl = (w[5] >> (8 * (ib >> 1))) >> (4 * (ib & 1)) & 0xFu;
         const uint32_t sh = (w[4] >> (16 + 2 * ib)) & 3u;
         const float dl = h2f(w[4]) * (float) ((int) (sl | sh << 4) - 32);
@@ -212,7 +228,7 @@ template <> struct Q<QT_Q4_K> {
         ld16(q + 16, w + 4);
         ld16(R.b1 + 16 * (g >> 3), w + 8);
     }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o) {
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
         const int ib = g & 7, sh = 4 * (ib & 1);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -239,7 +255,7 @@ template <> struct Q<QT_Q5_K> {
         ld16(h + 16, w + 12);
         ld16(R.b2 + 16 * (g >> 3), w + 16);
     }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o) {
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
         const int ib = g & 7, sh = 4 * (ib & 1);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -272,7 +288,7 @@ template <> struct Q<QT_Q6_K> {
         w[16] = ld2(t + 8 * n + 2 * qu);
         w[17] = ld2(t + 16);
     }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o) {
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
         const int qu = g & 3, lsh = 4 * (qu >> 1), hsh = 2 * qu;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -289,8 +305,9 @@ template <> struct Q<QT_Q6_K> {
 
 template <uint32_t TY> __device__ __forceinline__ void decode(const PP &P, int row, int g, Grp &o) {
     uint32_t w[Q<TY>::NW];
+    const Iq4Tab T;
     Q<TY>::load(row_planes(P, row), g, w);
-    Q<TY>::unpack(w, g, o);
+    Q<TY>::unpack(w, g, o, T);
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -348,9 +365,10 @@ template <int LPR> __device__ __forceinline__ float lane_row_sum(float v) {
 // xs[(t * 8 + c) * KCP + gr].  The arithmetic (and its order) does not depend on NT: token t of an NT-token call
 // gets the bits a one-token call gets.
 template <uint32_t TY, int NT>
-__device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float4 *xs, int KCP, int gr, float *acc) {
+__device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float4 *xs, int KCP, int gr, float *acc,
+                                           const Iq4Tab &T) {
     Grp o;
-    Q<TY>::unpack(w, g, o);
+    Q<TY>::unpack(w, g, o, T);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         if constexpr (Q<TY>::MIN) {
@@ -402,6 +420,7 @@ __device__ __forceinline__ void gemv_rows(const PP &P, int rows, int tile, int g
     const int row = tile * 8 * RPW + (tid >> 6) * RPW + lane / LPR;
     const bool live = row < rows;
     const RP R = row_planes(P, live ? row : 0);
+    const Iq4Tab T;  // (IQ4 formats) the level table in registers, once
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
@@ -432,20 +451,27 @@ __device__ __forceinline__ void gemv_rows(const PP &P, int rows, int tile, int g
             }
         }
         __syncthreads();
+        // two batches in turn (wa, wb): each batch's FMAs run while the other's loads are in flight
+        uint32_t wb[U][NW];
         while (g < c1) {
-            const int gn = g + LPR * U;
-            uint32_t wb[U][NW];
+            int gn = g + LPR * U;
             if (gn < c1) {
 #pragma unroll
                 for (int u = 0; u < U; ++u) Q<TY>::load(R, min(gn + LPR * u, c1 - 1), wb[u]);
             }
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                if (g + LPR * u < c1) accumulate<TY, NT>(wa[u], g + LPR * u, xs, KCP, g + LPR * u - c0, acc);
+                if (g + LPR * u < c1) accumulate<TY, NT>(wa[u], g + LPR * u, xs, KCP, g + LPR * u - c0, acc, T);
+            g = gn;
+            if (g >= c1) break;
+            gn = g + LPR * U;
+            if (gn < c1) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) Q<TY>::load(R, min(gn + LPR * u, c1 - 1), wa[u]);
+            }
 #pragma unroll
             for (int u = 0; u < U; ++u)
-#pragma unroll
-                for (int i = 0; i < NW; ++i) wa[u][i] = wb[u][i];
+                if (g + LPR * u < c1) accumulate<TY, NT>(wb[u], g + LPR * u, xs, KCP, g + LPR * u - c0, acc, T);
             g = gn;
         }
     }
