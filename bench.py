@@ -405,7 +405,7 @@ def main():
         st.launch(stream, advance=False)
         stream.sync()
         st.free()
-        print(json.dumps({"counters_workload": "copy 1 GiB x3 (k_copy), fused DeltaNet B=64 x36 (k_gdn<true>)",
+        print(json.dumps({"counters_workload": "copy 1 GiB x3 (k_copy), fused DeltaNet B=64 x36 (k_gdn<3>)",
                           "copy_bytes": nb, "gdn_bytes_per_launch": fn_synth.gdn_block_bytes(64)}))
         return
 
@@ -516,7 +516,7 @@ def main():
                    "global_batch": B, "layers": L, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "k_gdn<1> (fused DeltaNet block)", "bytes_per_launch": bytes_layer,
+                     "kernel": "k_gdn<3> (fused DeltaNet block, one token)", "bytes_per_launch": bytes_layer,
                      "us_per_launch": round(ms_kern * 1e3, 3)},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -84,7 +84,7 @@ FN_API int fn_gemv_plan(uint32_t type, int rows, int cols, int *out) {
 }
 
 // the reference's knobs: waves per SM and tile shape belong to its CUDA tiling; split-K is the one that applies
-FN_API void fn_gemv_override(int, int ks, int, int) { fn::gemv_override(ks); }
+FN_API void fn_gemv_override(int wpt, int ks, int tb, int warps_per_sm) { fn::gemv_override(wpt, ks, tb, warps_per_sm); }
 FN_API void fn_gemv_waves(int) {}
 FN_API void fn_bench_hot(int on) { g_bench_hot = on; }
 

@@ -48,7 +48,9 @@ struct GemvPlan {
 };
 
 GemvPlan gemv_plan(const QLayout &L);
-void gemv_override(int ks);   // 0 = no split-K (the default plan)
+// benchmarking: force lanes per row (16 / 32 / 64), split-K, the kernel (1 = per-tile k_gemv, 2 = persistent
+// k_gemv_p where x fits its LDS) and the resident waves per CU the persistent grid is sized for; 0 = automatic
+void gemv_override(int lpr, int ks, int kernel, int waves_per_cu);
 size_t gemv_work_bytes(const QLayout &L, int nt);
 
 // GGUF rows (device) -> packed planes (device); stream-ordered

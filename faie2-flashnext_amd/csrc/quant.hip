@@ -426,14 +426,11 @@ __device__ __forceinline__ void gemv_rows(const PP &P, int rows, int tile, int g
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
     for (int c0 = g0; c0 < g1; c0 += KC) {
         const int c1 = min(g1, c0 + KC), nch = c1 - c0, nx = NT * 8 * nch;
-        float4 xr[NXT];
+        float4 xr[NXT];  // loads clamped to the last element (unconditional: the array stays in registers)
 #pragma unroll
         for (int j = 0; j < NXT; ++j) {
-            const int e = tid + 512 * j;
-            if (e < nx) {
-                const int tg = e >> 3, t = tg / nch, gr = tg - t * nch;
-                xr[j] = *reinterpret_cast<const float4 *>(x + (size_t) t * cols + (size_t) (c0 + gr) * 32 + 4 * (e & 7));
-            }
+            const int e = min(tid + 512 * j, nx - 1), tg = e >> 3, t = tg / nch, gr = tg - t * nch;
+            xr[j] = *reinterpret_cast<const float4 *>(x + (size_t) t * cols + (size_t) (c0 + gr) * 32 + 4 * (e & 7));
         }
         int g = live ? c0 + li : c1;
         uint32_t wa[U][NW];
@@ -494,6 +491,118 @@ __global__ void __launch_bounds__(512) k_gemv(PP P, int rows, int G, int gps, co
     gemv_rows<TY, NT, LPR>(P, rows, blockIdx.x, g0, g1, x, cols, out + (size_t) blockIdx.y * NT * rows, xs);
 }
 
+// LDS of the persistent GEMV: x of every token and every group of the split, staged once per workgroup
+constexpr int kPersistLds = 160 * 1024;  // all of a CU's LDS (then one workgroup per CU)
+constexpr int xs_pitch(int ng) { return ng | 1; }  // odd pitch: the transposed x writes are conflict-free
+
+// batch j of row-set s: groups g0 + li + LPR (U j + u), u < U, of row s RPW + lane / LPR.  Row and group are
+// clamped into the weight: a lane past the last row or group loads a valid address whose value it never uses.
+template <uint32_t TY, int LPR>
+__device__ __forceinline__ void load_batch(const PP &P, int rows, int s, int j, int lane, int g0, int g1,
+                                           uint32_t (&w)[Q<TY>::U][Q<TY>::NW]) {
+    constexpr int U = Q<TY>::U;
+    const RP R = row_planes(P, min(s * (64 / LPR) + lane / LPR, rows - 1));
+    const int gb = g0 + lane % LPR + LPR * U * j;
+#pragma unroll
+    for (int u = 0; u < U; ++u) Q<TY>::load(R, min(gb + LPR * u, g1 - 1), w[u]);
+}
+
+template <uint32_t TY, int NT, int LPR>
+__device__ __forceinline__ void acc_batch(const uint32_t (&w)[Q<TY>::U][Q<TY>::NW], int j, int lane, int g0, int g1,
+                                          const float4 *xs, int KCP, float *acc, const Iq4Tab &T) {
+    constexpr int U = Q<TY>::U;
+    const int gb = g0 + lane % LPR + LPR * U * j;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (gb + LPR * u < g1) accumulate<TY, NT>(w[u], gb + LPR * u, xs, KCP, gb + LPR * u - g0, acc, T);
+}
+
+// end of a row-set: the row sums (every lane of a row gets them) stored by the row's first lane; accumulators reset
+template <int NT, int LPR>
+__device__ __forceinline__ void flush_rows(int s, int lane, int rows, float *acc, float *__restrict__ out) {
+    const int row = s * (64 / LPR) + lane / LPR;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = lane_row_sum<LPR>(acc[t]);
+    if (lane % LPR == 0 && row < rows) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) out[(size_t) t * rows + row] = acc[t];
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+}
+
+// Persistent GEMV, for a split whose x fits the LDS: the workgroup stages x of groups [g0, g1) once; then each wave
+// walks its own row-sets (64 / LPR rows each) s = global wave id, + waves in the grid, ..., in batches of U groups
+// per lane, keeping the next batch's loads (the next row-set's, at the end of one) in flight while it does the
+// FMAs of the current one.  The grid is sized to the workgroups that are resident at once, so no workgroup waits
+// for another to finish.  A row's arithmetic is that of k_gemv: lane li sums its groups li, li + LPR, ... in
+// ascending order, then the row's LPR lanes are summed, so the two kernels give the same bits.
+template <uint32_t TY, int NT, int LPR>
+__global__ void __launch_bounds__(512) k_gemv_p(PP P, int rows, int G, int gps, const float *__restrict__ x, int cols,
+                                                  float *__restrict__ out) {
+    extern __shared__ float4 xs[];
+    constexpr int NW = Q<TY>::NW, U = Q<TY>::U, RPW = 64 / LPR, XB = NT <= 2 ? 4 : 8;
+    const int g0 = blockIdx.y * gps, g1 = min(G, g0 + gps), ng = g1 - g0, KCP = xs_pitch(gps);
+    if (ng <= 0) return;  // (the plan gives every split a group; whole workgroup, before any barrier)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int NS = (rows + RPW - 1) / RPW, NB = (ng + LPR * U - 1) / (LPR * U), nws = gridDim.x * 8;
+    out += (size_t) blockIdx.y * NT * rows;
+    // the wave's batches in order: (s, j), then (s1, j1) = next(s, j), ...; wave-uniform, so the row reductions run
+    // on whole waves
+    int s = blockIdx.x * 8 + (tid >> 6), j = 0, s1, j1;
+    const auto next = [NB, nws](int s_, int j_, int &sn, int &jn) {
+        sn = j_ + 1 == NB ? s_ + nws : s_;
+        jn = j_ + 1 == NB ? 0 : j_ + 1;
+    };
+    next(s, j, s1, j1);
+    uint32_t wa[U][NW], wb[U][NW];
+    // x [NT][cols] -> xs[(t * 8 + c) * KCP + gr] (float4 c of group g0 + gr of token t).  The first part of x is
+    // requested before the first two weight batches, so that its LDS writes wait for x alone.
+    const int nx = NT * 8 * ng;
+    for (int e0 = 0; e0 < nx; e0 += 512 * XB) {
+        float4 xr[XB];  // loads clamped to the last element (unconditional: the array stays in registers)
+#pragma unroll
+        for (int k = 0; k < XB; ++k) {
+            const int e = min(e0 + tid + 512 * k, nx - 1), tg = e >> 3, t = tg / ng, gr = tg - t * ng;
+            xr[k] = *reinterpret_cast<const float4 *>(x + (size_t) t * cols + (size_t) (g0 + gr) * 32 + 4 * (e & 7));
+        }
+        if (e0 == 0) {
+            if (s < NS) load_batch<TY, LPR>(P, rows, s, j, lane, g0, g1, wa);
+            if (s1 < NS) load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wb);
+        }
+#pragma unroll
+        for (int k = 0; k < XB; ++k) {
+            const int e = e0 + tid + 512 * k;
+            if (e < nx) {
+                const int tg = e >> 3, t = tg / ng, gr = tg - t * ng;
+                xs[(t * 8 + (e & 7)) * KCP + gr] = xr[k];
+            }
+        }
+    }
+    __syncthreads();
+    const Iq4Tab T;
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    // two batches in flight: while one is summed, the other (and then the one after it) is loading
+    while (s < NS) {
+        acc_batch<TY, NT, LPR>(wa, j, lane, g0, g1, xs, KCP, acc, T);
+        if (j == NB - 1) flush_rows<NT, LPR>(s, lane, rows, acc, out);
+        s = s1;
+        j = j1;
+        next(s, j, s1, j1);
+        if (s >= NS) break;
+        if (s1 < NS) load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wa);
+        acc_batch<TY, NT, LPR>(wb, j, lane, g0, g1, xs, KCP, acc, T);
+        if (j == NB - 1) flush_rows<NT, LPR>(s, lane, rows, acc, out);
+        s = s1;
+        j = j1;
+        next(s, j, s1, j1);
+        if (s >= NS) break;
+        if (s1 < NS) load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wb);
+    }
+}
+
 // y[i] = sum over splits s = 0..ks-1 of part[s][i], in that order
 __global__ void k_gemv_reduce(const float *__restrict__ part, int ks, int n, float *__restrict__ y) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -503,17 +612,64 @@ __global__ void k_gemv_reduce(const float *__restrict__ part, int ks, int n, flo
     y[i] = s;
 }
 
-int g_ov_ks = 0;
+int g_ov_ks = 0, g_ov_lpr = 0, g_ov_kernel = 0, g_ov_wpc = 0;
+
+// compute units of the current device (queried once)
+int cu_count() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
 
 PP planes(const QLayout &L, const uint8_t *packed) {
     PP P{packed + L.off[0], packed + L.off[1], packed + L.off[2], L.rs[0], L.rs[1], L.rs[2]};
     return P;
 }
 
+// persistent launch: workgroups = those resident at once (registers and LDS), at most one per 8 row-sets
+template <uint32_t TY, int NT, int LPR>
+int gemv_persist(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, float *out, size_t lds,
+                 hipStream_t st) {
+    static int by_regs = 0;  // workgroups per CU that the kernel's registers allow
+    const auto kern = k_gemv_p<TY, NT, LPR>;
+    if (!by_regs) {
+        int n = 0;
+        FN_CK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 512, 0));
+        by_regs = std::max(1, n);
+    }
+    int per_cu = std::min(by_regs, std::max(1, (int) ((160 * 1024) / std::max<size_t>(lds, 1))));
+    if (g_ov_wpc) per_cu = std::max(1, g_ov_wpc / 8);
+    const int ns = (L.rows + 64 / LPR - 1) / (64 / LPR);
+    const int nwg = std::min((ns + 7) / 8, cu_count() * per_cu);
+    const int gps = (pl.ngroups + pl.ks - 1) / pl.ks;
+    hipLaunchKernelGGL(kern, dim3((unsigned) nwg, (unsigned) pl.ks), dim3(512), lds, st, P, L.rows, pl.ngroups, gps, x,
+                       L.cols, out);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
 template <uint32_t TY, int LPR>
 int gemv_tl(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, int nt, float *out, hipStream_t st) {
     const dim3 grid((unsigned) pl.ntiles, (unsigned) pl.ks), block(512);
     const int gps = (pl.ngroups + pl.ks - 1) / pl.ks;
+    const size_t lds = (size_t) nt * 8 * xs_pitch(gps) * sizeof(float4);
+    if (g_ov_kernel != 1 && lds <= (size_t) kPersistLds) {
+        switch (nt) {
+#define FN_GEMV_NT(N) \
+    case N: return gemv_persist<TY, N, LPR>(L, pl, P, x, out, lds, st);
+            FN_GEMV_NT(1) FN_GEMV_NT(2) FN_GEMV_NT(3) FN_GEMV_NT(4) FN_GEMV_NT(5) FN_GEMV_NT(6) FN_GEMV_NT(7)
+            FN_GEMV_NT(8)
+#undef FN_GEMV_NT
+            default: FN_FAIL("gemv: nt must be 1..8");
+        }
+    }
     switch (nt) {
 #define FN_GEMV_NT(N)                                                                                               \
     case N:                                                                                                         \
@@ -582,19 +738,28 @@ bool qlayout(uint32_t type, int rows, int cols, QLayout &L) {
     return true;
 }
 
-void gemv_override(int ks) { g_ov_ks = std::max(0, ks); }
+void gemv_override(int lpr, int ks, int kernel, int waves_per_cu) {
+    g_ov_lpr = (lpr == 16 || lpr == 32 || lpr == 64) ? lpr : 0;
+    g_ov_ks = std::max(0, ks);
+    g_ov_kernel = (kernel == 1 || kernel == 2) ? kernel : 0;
+    g_ov_wpc = std::max(0, waves_per_cu);
+}
 
 GemvPlan gemv_plan(const QLayout &L) {
     GemvPlan p;
     p.ngroups = L.cols / 32;
-    // lanes per row: enough that a lane has at most a few groups (its loads go out in one or two batches), and
-    // enough lanes in all (waves = rows * lpr / 64) to fill the 256 CUs when the rows are few
-    int lpr = p.ngroups >= 128 ? 64 : (p.ngroups >= 48 ? 32 : 16);
-    while (lpr < 64 && p.ngroups > lpr && (size_t) L.rows * lpr / 64 < 2048) lpr *= 2;
-    p.lpr = lpr;
-    p.rpw = 8 * (64 / lpr);
+    // lanes per row (measured on the projection shapes, nt 1 and 8): a few groups per lane, fewer lanes per row for
+    // very tall weights (more row-sets per wave to stream through), and enough lanes in all (rows * lpr / 64 waves)
+    // to spread a short weight over the CUs
+    const int G = p.ngroups;
+    int lpr = G >= 160 ? 32 : (G >= 128 ? 64 : (G >= 48 ? (L.rows >= 32768 ? 16 : 32) : 16));
+    while (lpr < 64 && G > lpr && (size_t) L.rows * lpr / 64 < 1024) lpr *= 2;
+    p.lpr = g_ov_lpr ? g_ov_lpr : lpr;
+    p.rpw = 8 * (64 / p.lpr);
     p.ntiles = (L.rows + p.rpw - 1) / p.rpw;
     p.ks = g_ov_ks ? std::min(g_ov_ks, p.ngroups) : 1;
+    const int gps = (p.ngroups + p.ks - 1) / p.ks;
+    p.ks = (p.ngroups + gps - 1) / gps;  // every split holds at least one group
     return p;
 }
 

@@ -179,8 +179,10 @@ class FN:
         self.check(self.d.fn_bench_gemv(int(qtype), rows, cols, nt, iters, C.byref(ms)))
         return ms.value
 
-    def gemv_override(self, ks=0):
-        self.d.fn_gemv_override(0, int(ks), 0, 0)
+    def gemv_override(self, ks=0, lpr=0, kernel=0, waves_per_cu=0):
+        """Force the GEMV plan (0 = automatic): split-K, lanes per row, kernel (1 per-tile, 2 persistent) and the
+        resident waves per CU the persistent grid is sized for."""
+        self.d.fn_gemv_override(int(lpr), int(ks), int(kernel), int(waves_per_cu))
 
     def bench_hot(self, on):
         self.d.fn_bench_hot(1 if on else 0)

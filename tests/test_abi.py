@@ -133,6 +133,14 @@ def test_gemv_plan_shapes(fnlib):
         assert fnlib.gemv_plan(23, 10240, 2560)[2] == 3
     finally:
         fnlib.gemv_override(0)
+    auto = fnlib.gemv_plan(8, 2560, 6144)
+    fnlib.gemv_override(lpr=16)                                  # forced lanes per row; an invalid value is ignored
+    try:
+        assert fnlib.gemv_plan(23, 10240, 2560)[3:5] == [32, 16]
+        fnlib.gemv_override(lpr=48)
+        assert fnlib.gemv_plan(8, 2560, 6144) == auto
+    finally:
+        fnlib.gemv_override(0)
 
 
 def test_verify_validates_before_device_work(fnlib):

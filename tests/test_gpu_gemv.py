@@ -105,6 +105,40 @@ def test_gemv_split_k_invariance(fnlib, ks):
     assert oracle.relerr(y, ref) <= TOL
 
 
+# (type, rows, cols, nt): several batches per row-set (Q6_K / BF16 keep one group per lane in flight), ragged rows,
+# row-sets beyond one per wave (rows large for the grid, and a grid sized for 8 waves per CU), x at the LDS limit
+PERSIST_CASES = [
+    ("IQ4_XS", 10240, 2560, 1),
+    ("Q6_K", 6144, 2560, 3),
+    ("Q8_0", 2560, 6144, 2),
+    ("BF16", 333, 768, 8),
+    ("Q5_K", 1000, 4096, 4),
+    ("Q4_K", 40961, 512, 1),
+    ("IQ4_NL", 3001, 2944, 8),
+    ("Q8_0", 700, 4608, 8),     # 148 KB of x in LDS
+]
+
+
+@pytest.mark.parametrize("name,rows,cols,nt", PERSIST_CASES)
+@pytest.mark.parametrize("wpc", [0, 8])
+def test_gemv_persistent_matches_per_tile(fnlib, name, rows, cols, nt, wpc):
+    """The persistent kernel (x staged once per workgroup, waves walking row-sets) and the per-tile kernel give the
+    same bits: a row's groups are summed by the same lanes in the same order."""
+    t = TYPES[name]
+    _say(f"gemv persistent vs per-tile {name} {rows}x{cols} nt={nt} waves/CU={wpc or 'auto'}")
+    raw = random_finite(t, rows, cols, RNG)
+    x = RNG.standard_normal((nt, cols)).astype(np.float32)
+    try:
+        fnlib.gemv_override(kernel=1)
+        y1 = fnlib.gemv(t, raw, rows, cols, x)
+        fnlib.gemv_override(kernel=2, waves_per_cu=wpc)
+        y2 = fnlib.gemv(t, raw, rows, cols, x)
+    finally:
+        fnlib.gemv_override(0)
+    assert np.array_equal(y1, y2)
+    assert oracle.relerr(y2, oracle.gemv(t, raw, rows, cols, x)) <= TOL
+
+
 def test_gemv_tokens_independent(fnlib):
     """Token t of an nt-token call equals a one-token call on x[t] (the split order does not depend on nt)."""
     t, rows, cols = 8, 700, 2048
