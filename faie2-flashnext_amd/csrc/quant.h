@@ -41,15 +41,15 @@ struct GemvPlan {
     int gv = 32;      // values per group (a lane's unit of work)
     int waves = 8;    // waves per workgroup
     int ks = 1;       // workgroups along a row (split-K; partials are summed in a second, fixed-order pass)
-    int rpw = 32;     // rows per workgroup (8 waves x 64 / lpr rows)
+    int rpw = 32;     // rows per workgroup pass (8 waves x 64 / lpr)
     int lpr = 16;     // lanes per row (16, 32 or 64)
     int ntiles = 0;   // row tiles (workgroups along the rows)
     int ngroups = 0;  // groups per row
 };
 
 GemvPlan gemv_plan(const QLayout &L);
-// benchmarking: force lanes per row (16 / 32 / 64), split-K, the kernel (1 = per-tile k_gemv, 2 = persistent
-// k_gemv_p where x fits its LDS) and the resident waves per CU the persistent grid is sized for; 0 = automatic
+// benchmarking and tests: force lanes per row (16 / 32 / 64), split-K, the x staging (1 = chunks of lpr groups,
+// the path of an x too large for the LDS) and the resident waves per CU a persistent grid is sized for; 0 = automatic
 void gemv_override(int lpr, int ks, int kernel, int waves_per_cu);
 size_t gemv_work_bytes(const QLayout &L, int nt);
 

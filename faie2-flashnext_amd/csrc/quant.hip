@@ -347,13 +347,6 @@ template <uint32_t TY> __global__ void k_dequant(PP P, int rows, int G, int cols
     }
 }
 
-// groups of x per LDS chunk for NT tokens: NT * KC groups * 128 B <= 32 KB, and at least one group per lane of a row
-// (NT * LPR * 128 B <= 64 KB); KC is a multiple of LPR so that the lane that owns a group (lane = group mod LPR) does
-// not depend on the chunking
-template <int NT, int LPR> constexpr int kc_groups() {
-    return (256 / NT) / LPR * LPR > LPR ? (256 / NT) / LPR * LPR : LPR;
-}
-
 // sum over the LPR lanes of a row (16: one DPP row, 32: half a wave, 64: the wave); every lane of the row gets it
 template <int LPR> __device__ __forceinline__ float lane_row_sum(float v) {
     if constexpr (LPR == 16) return row_sum(v);
@@ -361,11 +354,11 @@ template <int LPR> __device__ __forceinline__ float lane_row_sum(float v) {
     else return wave_sum(v);
 }
 
-// one group's contribution to the NT accumulators; x of the group sits in LDS as float4 column c of token t at
-// xs[(t * 8 + c) * KCP + gr].  The arithmetic (and its order) does not depend on NT: token t of an NT-token call
-// gets the bits a one-token call gets.
+// one group's contribution to the NT accumulators; xg points at the group's x in LDS: float4 c of token t at
+// xg[t * 8 + c] (offsets known at compile time).  The arithmetic (and its order) does not depend on NT: token t of
+// an NT-token call gets the bits a one-token call gets.
 template <uint32_t TY, int NT>
-__device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float4 *xs, int KCP, int gr, float *acc,
+__device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float4 *xg, float *acc,
                                            const Iq4Tab &T) {
     Grp o;
     Q<TY>::unpack(w, g, o, T);
@@ -380,7 +373,7 @@ __device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float
                 float a = acc[t];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    const float4 xv = xs[(t * 8 + 4 * h + c) * KCP + gr];
+                    const float4 xv = xg[t * 8 + 4 * h + c];
                     a = __builtin_fmaf(wv[4 * c], xv.x, a);
                     a = __builtin_fmaf(wv[4 * c + 1], xv.y, a);
                     a = __builtin_fmaf(wv[4 * c + 2], xv.z, a);
@@ -394,7 +387,7 @@ __device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float
                 float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    const float4 xv = xs[(t * 8 + 4 * h + c) * KCP + gr];
+                    const float4 xv = xg[t * 8 + 4 * h + c];
                     d0 = __builtin_fmaf(o.q[16 * h + 4 * c], xv.x, d0);
                     d1 = __builtin_fmaf(o.q[16 * h + 4 * c + 1], xv.y, d1);
                     d0 = __builtin_fmaf(o.q[16 * h + 4 * c + 2], xv.z, d0);
@@ -406,115 +399,58 @@ __device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float
     }
 }
 
-// GEMV rows of one workgroup: 8 waves = 8 * (64 / LPR) rows starting at tile * 8 * (64 / LPR), groups [g0, g1);
-// LPR lanes per row, lane li owning the row's groups li, li + LPR, ...  The workgroup walks its groups in chunks of
-// KC: the chunk of x (all NT tokens) is loaded first, then the first U groups of every lane, then x goes to LDS
-// (transposed so that the lanes of a row read consecutive float4: no bank conflicts); each lane then keeps the next
-// U groups' loads in flight while it does the FMAs of the current U.  out[t * rows + row] = the row's sum.
-template <uint32_t TY, int NT, int LPR>
-__device__ __forceinline__ void gemv_rows(const PP &P, int rows, int tile, int g0, int g1, const float *__restrict__ x,
-                                          int cols, float *__restrict__ out, float4 *xs) {
-    constexpr int KC = kc_groups<NT, LPR>(), KCP = KC + 1, NW = Q<TY>::NW, U = Q<TY>::U, RPW = 64 / LPR;
-    constexpr int NXT = NT * 8 * KC / 512;  // float4 of x per thread per chunk
-    const int tid = threadIdx.x, lane = tid & 63, li = lane % LPR;
-    const int row = tile * 8 * RPW + (tid >> 6) * RPW + lane / LPR;
-    const bool live = row < rows;
-    const RP R = row_planes(P, live ? row : 0);
-    const Iq4Tab T;  // (IQ4 formats) the level table in registers, once
-    float acc[NT];
+// x of tokens [0, NT) and groups [c0, c0 + nch) -> LDS, group-major: float4 c of token t of group c0 + gr at
+// xs[gr * xs_stride(NT) + t * 8 + c].  The stride is odd (in float4), so the lanes of a row, which read consecutive
+// groups, hit distinct bank quads, and every read's offset inside a group is an immediate.  One pass moves XB float4
+// per thread; its loads are clamped to the last element, so the pass's array stays in registers.
+constexpr int xs_stride(int nt) { return nt * 8 + 1; }
+
+template <int NT, int XB> struct XPass {
+    float4 r[XB];
+    __device__ __forceinline__ void load(const float *__restrict__ x, int cols, int c0, int nch, int e0, int tid,
+                                         int nth) {
+        const int nx = NT * 8 * nch;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
-    for (int c0 = g0; c0 < g1; c0 += KC) {
-        const int c1 = min(g1, c0 + KC), nch = c1 - c0, nx = NT * 8 * nch;
-        float4 xr[NXT];  // loads clamped to the last element (unconditional: the array stays in registers)
-#pragma unroll
-        for (int j = 0; j < NXT; ++j) {
-            const int e = min(tid + 512 * j, nx - 1), tg = e >> 3, t = tg / nch, gr = tg - t * nch;
-            xr[j] = *reinterpret_cast<const float4 *>(x + (size_t) t * cols + (size_t) (c0 + gr) * 32 + 4 * (e & 7));
+        for (int k = 0; k < XB; ++k) {
+            const int e = min(e0 + tid + nth * k, nx - 1), tg = e >> 3, t = tg / nch, gr = tg - t * nch;
+            r[k] = *reinterpret_cast<const float4 *>(x + (size_t) t * cols + (size_t) (c0 + gr) * 32 + 4 * (e & 7));
         }
-        int g = live ? c0 + li : c1;
-        uint32_t wa[U][NW];
-        if (g < c1) {
+    }
+    __device__ __forceinline__ void store(float4 *xs, int nch, int e0, int tid, int nth) const {
+        const int nx = NT * 8 * nch;
 #pragma unroll
-            for (int u = 0; u < U; ++u) Q<TY>::load(R, min(g + LPR * u, c1 - 1), wa[u]);
-        }
-        __syncthreads();  // every wave is done reading the previous chunk
-#pragma unroll
-        for (int j = 0; j < NXT; ++j) {
-            const int e = tid + 512 * j;
+        for (int k = 0; k < XB; ++k) {
+            const int e = e0 + tid + nth * k;
             if (e < nx) {
                 const int tg = e >> 3, t = tg / nch, gr = tg - t * nch;
-                xs[(t * 8 + (e & 7)) * KCP + gr] = xr[j];
+                xs[gr * xs_stride(NT) + t * 8 + (e & 7)] = r[k];
             }
         }
-        __syncthreads();
-        // two batches in turn (wa, wb): each batch's FMAs run while the other's loads are in flight
-        uint32_t wb[U][NW];
-        while (g < c1) {
-            int gn = g + LPR * U;
-            if (gn < c1) {
-#pragma unroll
-                for (int u = 0; u < U; ++u) Q<TY>::load(R, min(gn + LPR * u, c1 - 1), wb[u]);
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (g + LPR * u < c1) accumulate<TY, NT>(wa[u], g + LPR * u, xs, KCP, g + LPR * u - c0, acc, T);
-            g = gn;
-            if (g >= c1) break;
-            gn = g + LPR * U;
-            if (gn < c1) {
-#pragma unroll
-                for (int u = 0; u < U; ++u) Q<TY>::load(R, min(gn + LPR * u, c1 - 1), wa[u]);
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (g + LPR * u < c1) accumulate<TY, NT>(wb[u], g + LPR * u, xs, KCP, g + LPR * u - c0, acc, T);
-            g = gn;
-        }
     }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = lane_row_sum<LPR>(acc[t]);
-    if (li == 0 && live) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) out[(size_t) t * rows + row] = acc[t];
-    }
-}
+};
 
-template <int NT, int LPR> constexpr int xs_float4() { return NT * 8 * (kc_groups<NT, LPR>() + 1); }
-
-// one format: grid (row tiles, K splits of gps groups); split s writes its partial sums to out + s * NT * rows
-template <uint32_t TY, int NT, int LPR>
-__global__ void __launch_bounds__(512) k_gemv(PP P, int rows, int G, int gps, const float *__restrict__ x, int cols,
-                                                float *__restrict__ out) {
-    __shared__ float4 xs[xs_float4<NT, LPR>()];
-    const int g0 = blockIdx.y * gps, g1 = min(G, g0 + gps);
-    gemv_rows<TY, NT, LPR>(P, rows, blockIdx.x, g0, g1, x, cols, out + (size_t) blockIdx.y * NT * rows, xs);
-}
-
-// LDS of the persistent GEMV: x of every token and every group of the split, staged once per workgroup
-constexpr int kPersistLds = 160 * 1024;  // all of a CU's LDS (then one workgroup per CU)
-constexpr int xs_pitch(int ng) { return ng | 1; }  // odd pitch: the transposed x writes are conflict-free
-
-// batch j of row-set s: groups g0 + li + LPR (U j + u), u < U, of row s RPW + lane / LPR.  Row and group are
-// clamped into the weight: a lane past the last row or group loads a valid address whose value it never uses.
+// batch j of row-set s over the groups [c0, c1): groups c0 + li + LPR (U j + u), u < U, of row s RPW + lane / LPR.
+// Row and group are clamped into the weight: a lane past the last row or group loads a valid address whose value
+// it never uses.
 template <uint32_t TY, int LPR>
-__device__ __forceinline__ void load_batch(const PP &P, int rows, int s, int j, int lane, int g0, int g1,
+__device__ __forceinline__ void load_batch(const PP &P, int rows, int s, int j, int lane, int c0, int c1,
                                            uint32_t (&w)[Q<TY>::U][Q<TY>::NW]) {
     constexpr int U = Q<TY>::U;
     const RP R = row_planes(P, min(s * (64 / LPR) + lane / LPR, rows - 1));
-    const int gb = g0 + lane % LPR + LPR * U * j;
+    const int gb = c0 + lane % LPR + LPR * U * j;
 #pragma unroll
-    for (int u = 0; u < U; ++u) Q<TY>::load(R, min(gb + LPR * u, g1 - 1), w[u]);
+    for (int u = 0; u < U; ++u) Q<TY>::load(R, min(gb + LPR * u, c1 - 1), w[u]);
 }
 
 template <uint32_t TY, int NT, int LPR>
-__device__ __forceinline__ void acc_batch(const uint32_t (&w)[Q<TY>::U][Q<TY>::NW], int j, int lane, int g0, int g1,
-                                          const float4 *xs, int KCP, float *acc, const Iq4Tab &T) {
+__device__ __forceinline__ void acc_batch(const uint32_t (&w)[Q<TY>::U][Q<TY>::NW], int j, int lane, int c0, int c1,
+                                          const float4 *xs, float *acc, const Iq4Tab &T) {
     constexpr int U = Q<TY>::U;
-    const int gb = g0 + lane % LPR + LPR * U * j;
+    const int gb = c0 + lane % LPR + LPR * U * j;
 #pragma unroll
     for (int u = 0; u < U; ++u)
-        if (gb + LPR * u < g1) accumulate<TY, NT>(w[u], gb + LPR * u, xs, KCP, gb + LPR * u - g0, acc, T);
+        if (gb + LPR * u < c1)
+            accumulate<TY, NT>(w[u], gb + LPR * u, xs + (gb + LPR * u - c0) * xs_stride(NT), acc, T);
 }
 
 // end of a row-set: the row sums (every lane of a row gets them) stored by the row's first lane; accumulators reset
@@ -531,21 +467,25 @@ __device__ __forceinline__ void flush_rows(int s, int lane, int rows, float *acc
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
 }
 
-// Persistent GEMV, for a split whose x fits the LDS: the workgroup stages x of groups [g0, g1) once; then each wave
-// walks its own row-sets (64 / LPR rows each) s = global wave id, + waves in the grid, ..., in batches of U groups
-// per lane, keeping the next batch's loads (the next row-set's, at the end of one) in flight while it does the
-// FMAs of the current one.  The grid is sized to the workgroups that are resident at once, so no workgroup waits
-// for another to finish.  A row's arithmetic is that of k_gemv: lane li sums its groups li, li + LPR, ... in
-// ascending order, then the row's LPR lanes are summed, so the two kernels give the same bits.
+// GEMV of one split (blockIdx.y) of the groups: [g0, g1), g0 = blockIdx.y * gps.  A wave works on row-sets of
+// 64 / LPR rows, LPR lanes per row; lane li of a row sums its groups li, li + LPR, ... in ascending order into one
+// accumulator per token, then the row's LPR lanes are summed.  That arithmetic is the same in both kernels below,
+// for every launch shape and token count, so token t of an nt-token call gets the bits of a one-token call on x[t].
+//
+// k_gemv, for a split whose x fits the LDS: the workgroup stages x once, then each wave walks its own row-sets
+// s = global wave id, + waves in the grid, ..., in batches of U groups per lane, with the next batch's loads (the
+// next row-set's, at the end of one) in flight while it sums the current one.  The host sizes the grid to the
+// workgroups resident at once, so no workgroup waits for another to finish.
 template <uint32_t TY, int NT, int LPR>
-__global__ void __launch_bounds__(512) k_gemv_p(PP P, int rows, int G, int gps, const float *__restrict__ x, int cols,
-                                                  float *__restrict__ out) {
+__global__ void __launch_bounds__(512) k_gemv(PP P, int rows, int G, int gps, const float *__restrict__ x, int cols,
+                                                float *__restrict__ out) {
     extern __shared__ float4 xs[];
     constexpr int NW = Q<TY>::NW, U = Q<TY>::U, RPW = 64 / LPR, XB = NT <= 2 ? 4 : 8;
-    const int g0 = blockIdx.y * gps, g1 = min(G, g0 + gps), ng = g1 - g0, KCP = xs_pitch(gps);
+    const int g0 = blockIdx.y * gps, g1 = min(G, g0 + gps), ng = g1 - g0;
     if (ng <= 0) return;  // (the plan gives every split a group; whole workgroup, before any barrier)
     const int tid = threadIdx.x, lane = tid & 63;
-    const int NS = (rows + RPW - 1) / RPW, NB = (ng + LPR * U - 1) / (LPR * U), nws = gridDim.x * 8;
+    const int NS = (rows + RPW - 1) / RPW, nws = gridDim.x * 8;
+    const int NB = (ng + LPR * U - 1) / (LPR * U);
     out += (size_t) blockIdx.y * NT * rows;
     // the wave's batches in order: (s, j), then (s1, j1) = next(s, j), ...; wave-uniform, so the row reductions run
     // on whole waves
@@ -556,8 +496,8 @@ __global__ void __launch_bounds__(512) k_gemv_p(PP P, int rows, int G, int gps, 
     };
     next(s, j, s1, j1);
     uint32_t wa[U][NW], wb[U][NW];
-    // x [NT][cols] -> xs[(t * 8 + c) * KCP + gr] (float4 c of group g0 + gr of token t).  The first part of x is
-    // requested before the first two weight batches, so that its LDS writes wait for x alone.
+    // x [NT][cols] -> xs (the layout of XPass).  The first part of x is requested before the first two weight
+    // batches, so that its LDS writes wait for x alone.
     const int nx = NT * 8 * ng;
     for (int e0 = 0; e0 < nx; e0 += 512 * XB) {
         float4 xr[XB];  // loads clamped to the last element (unconditional: the array stays in registers)
@@ -575,25 +515,25 @@ __global__ void __launch_bounds__(512) k_gemv_p(PP P, int rows, int G, int gps, 
             const int e = e0 + tid + 512 * k;
             if (e < nx) {
                 const int tg = e >> 3, t = tg / ng, gr = tg - t * ng;
-                xs[(t * 8 + (e & 7)) * KCP + gr] = xr[k];
+                xs[gr * xs_stride(NT) + t * 8 + (e & 7)] = xr[k];
             }
         }
     }
     __syncthreads();
-    const Iq4Tab T;
+    const Iq4Tab T;  // (IQ4 formats) the level table in registers, once
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
     // two batches in flight: while one is summed, the other (and then the one after it) is loading
     while (s < NS) {
-        acc_batch<TY, NT, LPR>(wa, j, lane, g0, g1, xs, KCP, acc, T);
+        acc_batch<TY, NT, LPR>(wa, j, lane, g0, g1, xs, acc, T);
         if (j == NB - 1) flush_rows<NT, LPR>(s, lane, rows, acc, out);
         s = s1;
         j = j1;
         next(s, j, s1, j1);
         if (s >= NS) break;
         if (s1 < NS) load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wa);
-        acc_batch<TY, NT, LPR>(wb, j, lane, g0, g1, xs, KCP, acc, T);
+        acc_batch<TY, NT, LPR>(wb, j, lane, g0, g1, xs, acc, T);
         if (j == NB - 1) flush_rows<NT, LPR>(s, lane, rows, acc, out);
         s = s1;
         j = j1;
@@ -601,6 +541,47 @@ __global__ void __launch_bounds__(512) k_gemv_p(PP P, int rows, int G, int gps, 
         if (s >= NS) break;
         if (s1 < NS) load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wb);
     }
+}
+
+// k_gemv_c, for an x too large for the LDS: x goes through it in chunks of kc groups (a multiple of LPR, so a
+// group's lane does not depend on the chunking); the workgroup's 8 waves take one row-set each and walk the chunks
+// together.  Grid: one workgroup per 8 row-sets.
+template <uint32_t TY, int NT, int LPR>
+__global__ void __launch_bounds__(512) k_gemv_c(PP P, int rows, int G, int gps, int kc, const float *__restrict__ x,
+                                                  int cols, float *__restrict__ out) {
+    extern __shared__ float4 xs[];
+    constexpr int NW = Q<TY>::NW, U = Q<TY>::U, RPW = 64 / LPR, XB = NT <= 2 ? 4 : 8;
+    const int g0 = blockIdx.y * gps, g1 = min(G, g0 + gps);
+    if (g1 <= g0) return;  // (the plan gives every split a group; whole workgroup, before any barrier)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int s = blockIdx.x * 8 + (tid >> 6);
+    const bool live = s < (rows + RPW - 1) / RPW;  // wave-uniform
+    out += (size_t) blockIdx.y * NT * rows;
+    const Iq4Tab T;
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    uint32_t wa[U][NW], wb[U][NW];
+    XPass<NT, XB> xp;
+    for (int c0 = g0; c0 < g1; c0 += kc) {
+        const int c1 = min(g1, c0 + kc), nch = c1 - c0, NB = (nch + LPR * U - 1) / (LPR * U);
+        __syncthreads();  // every wave is done reading the previous chunk
+        for (int e0 = 0; e0 < NT * 8 * nch; e0 += 512 * XB) {
+            xp.load(x, cols, c0, nch, e0, tid, 512);
+            if (e0 == 0 && live) load_batch<TY, LPR>(P, rows, s, 0, lane, c0, c1, wa);
+            xp.store(xs, nch, e0, tid, 512);
+        }
+        __syncthreads();
+        if (!live) continue;
+        for (int j = 0; j < NB; j += 2) {
+            if (j + 1 < NB) load_batch<TY, LPR>(P, rows, s, j + 1, lane, c0, c1, wb);
+            acc_batch<TY, NT, LPR>(wa, j, lane, c0, c1, xs, acc, T);
+            if (j + 1 >= NB) break;
+            if (j + 2 < NB) load_batch<TY, LPR>(P, rows, s, j + 2, lane, c0, c1, wa);
+            acc_batch<TY, NT, LPR>(wb, j + 1, lane, c0, c1, xs, acc, T);
+        }
+    }
+    if (live) flush_rows<NT, LPR>(s, lane, rows, acc, out);
 }
 
 // y[i] = sum over splits s = 0..ks-1 of part[s][i], in that order
@@ -613,6 +594,7 @@ __global__ void k_gemv_reduce(const float *__restrict__ part, int ks, int n, flo
 }
 
 int g_ov_ks = 0, g_ov_lpr = 0, g_ov_kernel = 0, g_ov_wpc = 0;
+constexpr int kLdsPerCu = 160 * 1024;  // LDS of a CDNA4 CU (the most one workgroup can take)
 
 // compute units of the current device (queried once)
 int cu_count() {
@@ -633,54 +615,53 @@ PP planes(const QLayout &L, const uint8_t *packed) {
     return P;
 }
 
-// persistent launch: workgroups = those resident at once (registers and LDS), at most one per 8 row-sets
+// One GEMV launch.  x of the split in the LDS at once when it fits the CU's 160 KB: k_gemv on a grid of the
+// workgroups resident at once.  Else k_gemv_c with chunks of the largest multiple of LPR groups whose x fits 80 KB
+// (two workgroups per CU), evened out.
 template <uint32_t TY, int NT, int LPR>
-int gemv_persist(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, float *out, size_t lds,
-                 hipStream_t st) {
-    static int by_regs = 0;  // workgroups per CU that the kernel's registers allow
-    const auto kern = k_gemv_p<TY, NT, LPR>;
-    if (!by_regs) {
-        int n = 0;
-        FN_CK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 512, 0));
-        by_regs = std::max(1, n);
+int gemv_nt(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, float *out, hipStream_t st) {
+    const int gps = (pl.ngroups + pl.ks - 1) / pl.ks, ns = (L.rows + 64 / LPR - 1) / (64 / LPR);
+    int nwg = (ns + 7) / 8;
+    constexpr int XS = xs_stride(NT) * (int) sizeof(float4);  // LDS bytes per group of x
+    if (gps <= kLdsPerCu / XS && g_ov_kernel != 1) {
+        const auto kern = k_gemv<TY, NT, LPR>;
+        static int by_regs = 0;  // workgroups per CU the kernel's registers allow
+        if (!by_regs) {
+            int n = 0;
+            FN_CK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 512, 0));
+            by_regs = std::max(1, n);
+        }
+        const size_t lds = (size_t) gps * XS;
+        int per_cu = std::min(by_regs, std::max(1, (int) (kLdsPerCu / lds)));
+        if (g_ov_wpc) per_cu = std::max(1, g_ov_wpc / 8);
+        nwg = std::min(nwg, cu_count() * per_cu);
+        hipLaunchKernelGGL(kern, dim3((unsigned) nwg, (unsigned) pl.ks), dim3(512), lds, st, P, L.rows, pl.ngroups,
+                           gps, x, L.cols, out);
+    } else {
+        int kc = g_ov_kernel == 1 ? LPR : std::max(LPR, kLdsPerCu / 2 / XS / LPR * LPR);
+        const int nch = (gps + kc - 1) / kc;
+        kc = std::min(kc, ((gps + nch - 1) / nch + LPR - 1) / LPR * LPR);
+        const size_t lds = (size_t) kc * XS;
+        hipLaunchKernelGGL((k_gemv_c<TY, NT, LPR>), dim3((unsigned) nwg, (unsigned) pl.ks), dim3(512), lds, st, P,
+                           L.rows, pl.ngroups, gps, kc, x, L.cols, out);
     }
-    int per_cu = std::min(by_regs, std::max(1, (int) ((160 * 1024) / std::max<size_t>(lds, 1))));
-    if (g_ov_wpc) per_cu = std::max(1, g_ov_wpc / 8);
-    const int ns = (L.rows + 64 / LPR - 1) / (64 / LPR);
-    const int nwg = std::min((ns + 7) / 8, cu_count() * per_cu);
-    const int gps = (pl.ngroups + pl.ks - 1) / pl.ks;
-    hipLaunchKernelGGL(kern, dim3((unsigned) nwg, (unsigned) pl.ks), dim3(512), lds, st, P, L.rows, pl.ngroups, gps, x,
-                       L.cols, out);
     FN_CK(hipGetLastError());
     return 0;
 }
 
 template <uint32_t TY, int LPR>
 int gemv_tl(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, int nt, float *out, hipStream_t st) {
-    const dim3 grid((unsigned) pl.ntiles, (unsigned) pl.ks), block(512);
-    const int gps = (pl.ngroups + pl.ks - 1) / pl.ks;
-    const size_t lds = (size_t) nt * 8 * xs_pitch(gps) * sizeof(float4);
-    if (g_ov_kernel != 1 && lds <= (size_t) kPersistLds) {
-        switch (nt) {
-#define FN_GEMV_NT(N) \
-    case N: return gemv_persist<TY, N, LPR>(L, pl, P, x, out, lds, st);
-            FN_GEMV_NT(1) FN_GEMV_NT(2) FN_GEMV_NT(3) FN_GEMV_NT(4) FN_GEMV_NT(5) FN_GEMV_NT(6) FN_GEMV_NT(7)
-            FN_GEMV_NT(8)
-#undef FN_GEMV_NT
-            default: FN_FAIL("gemv: nt must be 1..8");
-        }
-    }
     switch (nt) {
-#define FN_GEMV_NT(N)                                                                                               \
-    case N:                                                                                                         \
-        hipLaunchKernelGGL((k_gemv<TY, N, LPR>), grid, block, 0, st, P, L.rows, pl.ngroups, gps, x, L.cols, out); \
-        break;
-        FN_GEMV_NT(1) FN_GEMV_NT(2) FN_GEMV_NT(3) FN_GEMV_NT(4) FN_GEMV_NT(5) FN_GEMV_NT(6) FN_GEMV_NT(7) FN_GEMV_NT(8)
-#undef FN_GEMV_NT
+        case 1: return gemv_nt<TY, 1, LPR>(L, pl, P, x, out, st);
+        case 2: return gemv_nt<TY, 2, LPR>(L, pl, P, x, out, st);
+        case 3: return gemv_nt<TY, 3, LPR>(L, pl, P, x, out, st);
+        case 4: return gemv_nt<TY, 4, LPR>(L, pl, P, x, out, st);
+        case 5: return gemv_nt<TY, 5, LPR>(L, pl, P, x, out, st);
+        case 6: return gemv_nt<TY, 6, LPR>(L, pl, P, x, out, st);
+        case 7: return gemv_nt<TY, 7, LPR>(L, pl, P, x, out, st);
+        case 8: return gemv_nt<TY, 8, LPR>(L, pl, P, x, out, st);
         default: FN_FAIL("gemv: nt must be 1..8");
     }
-    FN_CK(hipGetLastError());
-    return 0;
 }
 
 template <uint32_t TY>
@@ -752,7 +733,8 @@ GemvPlan gemv_plan(const QLayout &L) {
     // very tall weights (more row-sets per wave to stream through), and enough lanes in all (rows * lpr / 64 waves)
     // to spread a short weight over the CUs
     const int G = p.ngroups;
-    int lpr = G >= 160 ? 32 : (G >= 128 ? 64 : (G >= 48 ? (L.rows >= 32768 ? 16 : 32) : 16));
+    const bool q6 = L.type == QT_Q6_K;  // one group in flight per lane and batch: more groups per lane pay off
+    int lpr = G >= 160 ? 32 : (G >= 128 ? 64 : (G >= 48 ? (L.rows >= 32768 || (q6 && L.rows >= 4096) ? 16 : 32) : 16));
     while (lpr < 64 && G > lpr && (size_t) L.rows * lpr / 64 < 1024) lpr *= 2;
     p.lpr = g_ov_lpr ? g_ov_lpr : lpr;
     p.rpw = 8 * (64 / p.lpr);

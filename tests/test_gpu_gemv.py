@@ -106,8 +106,9 @@ def test_gemv_split_k_invariance(fnlib, ks):
 
 
 # (type, rows, cols, nt): several batches per row-set (Q6_K / BF16 keep one group per lane in flight), ragged rows,
-# row-sets beyond one per wave (rows large for the grid, and a grid sized for 8 waves per CU), x at the LDS limit
-PERSIST_CASES = [
+# row-sets beyond one per wave (rows large for the grid, and a grid sized for 8 waves per CU), x at the LDS limit,
+# a short weight
+STAGING_CASES = [
     ("IQ4_XS", 10240, 2560, 1),
     ("Q6_K", 6144, 2560, 3),
     ("Q8_0", 2560, 6144, 2),
@@ -116,16 +117,19 @@ PERSIST_CASES = [
     ("Q4_K", 40961, 512, 1),
     ("IQ4_NL", 3001, 2944, 8),
     ("Q8_0", 700, 4608, 8),     # 148 KB of x in LDS
+    ("IQ4_XS", 130, 2560, 5),   # a short weight
 ]
 
 
-@pytest.mark.parametrize("name,rows,cols,nt", PERSIST_CASES)
+@pytest.mark.parametrize("name,rows,cols,nt", STAGING_CASES)
 @pytest.mark.parametrize("wpc", [0, 8])
-def test_gemv_persistent_matches_per_tile(fnlib, name, rows, cols, nt, wpc):
-    """The persistent kernel (x staged once per workgroup, waves walking row-sets) and the per-tile kernel give the
-    same bits: a row's groups are summed by the same lanes in the same order."""
+def test_gemv_chunked_x_matches_one_stage(fnlib, name, rows, cols, nt, wpc):
+    """x staged in chunks of lpr groups (k_gemv_c, the path of an x too large for the LDS) and x staged once (k_gemv:
+    persistent waves walking row-sets, grid sized for wpc waves per CU) give the same bits: a row's groups are summed
+    by the same lanes in the same order."""
     t = TYPES[name]
-    _say(f"gemv persistent vs per-tile {name} {rows}x{cols} nt={nt} waves/CU={wpc or 'auto'}")
+    _say(f"gemv chunked vs one-stage x {name} {rows}x{cols} nt={nt} waves/CU={wpc or 'auto'} "
+         f"plan={fnlib.gemv_plan(t, rows, cols)}")
     raw = random_finite(t, rows, cols, RNG)
     x = RNG.standard_normal((nt, cols)).astype(np.float32)
     try:
