@@ -326,8 +326,10 @@ __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
 }
 
 // merge splits + sigmoid output gate (faie2fn.cu:1670-1690).  grid (nq, B nt), CW * 64 threads.
-// Pass 1: the global max M over the splits' maxima.  Pass 2: wave w takes splits w, w + CW, ...; lane l owns dims
-// 4l..4l+3 (one coalesced 1 KiB row per split) with NB rows in flight; the waves' sums meet in LDS.
+// Wave w takes splits w, w + CW, ...; lane l owns dims 4l..4l+3 (one coalesced 1 KiB row per split) with NB rows in
+// flight.  The first NB rows of every wave, their (m, l) and the gate are all requested at the start, before the
+// global max M over the splits is known, so a merge of up to CW * NB splits costs one memory round trip; the waves'
+// sums meet in LDS.
 constexpr int CW = 16;
 __global__ void __launch_bounds__(CW * 64) k_attn_combine(const AttnArgs a) {
     constexpr int NB = 8;
@@ -338,6 +340,17 @@ __global__ void __launch_bounds__(CW * 64) k_attn_combine(const AttnArgs a) {
     const int ns = a.nsplit;
     const size_t base = ((size_t) bt * a.nq + h) * ns;
     const float *ml = a.part_ml + base * 2;
+    const float4 *po = reinterpret_cast<const float4 *>(a.part_o + base * HD);
+    const float gate = tid < HD ? a.qg[(((size_t) bt * a.nq + h) * 2 + 1) * HD + tid] : 0.0f;
+    float4 v[NB];
+    float mv[NB], lv[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        const int s = min(wave + CW * u, ns - 1);
+        v[u] = ld_nt(&po[(size_t) s * (HD / 4) + lane]);
+        mv[u] = ml[2 * s];
+        lv[u] = ml[2 * s + 1];
+    }
     float M = -INFINITY;
     for (int s = tid; s < ns; s += CW * 64) M = fmaxf(M, ml[2 * s]);
     M = wave_max(M);
@@ -346,27 +359,27 @@ __global__ void __launch_bounds__(CW * 64) k_attn_combine(const AttnArgs a) {
     M = red[0];
 #pragma unroll
     for (int w = 1; w < CW; ++w) M = fmaxf(M, red[w]);
-    const float4 *po = reinterpret_cast<const float4 *>(a.part_o + base * HD);
     float4 O = f4(0.0f);
     float L = 0.0f;
-    for (int s0 = wave; s0 < ns; s0 += CW * NB) {
-        float4 v[NB];
-        float w[NB];
+    for (int s0 = wave;;) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            // splits without keys (m = -inf) and the clamped repeats past the end weigh 0
+            const float w = (s0 + CW * u < ns && mv[u] != -INFINITY) ? expf(mv[u] - M) : 0.0f;
+            L = fmaf(w, w != 0.0f ? lv[u] : 0.0f, L);
+            O.x = fmaf(w, v[u].x, O.x);
+            O.y = fmaf(w, v[u].y, O.y);
+            O.z = fmaf(w, v[u].z, O.z);
+            O.w = fmaf(w, v[u].w, O.w);
+        }
+        s0 += CW * NB;
+        if (s0 >= ns) break;
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             const int s = min(s0 + CW * u, ns - 1);
             v[u] = ld_nt(&po[(size_t) s * (HD / 4) + lane]);
-            const float m = ml[2 * s];
-            // splits without keys (m = -inf) and the clamped repeats past the end weigh 0
-            w[u] = (s0 + CW * u < ns && m != -INFINITY) ? expf(m - M) : 0.0f;
-            L = fmaf(w[u], w[u] != 0.0f ? ml[2 * s + 1] : 0.0f, L);
-        }
-#pragma unroll
-        for (int u = 0; u < NB; ++u) {
-            O.x = fmaf(w[u], v[u].x, O.x);
-            O.y = fmaf(w[u], v[u].y, O.y);
-            O.z = fmaf(w[u], v[u].z, O.z);
-            O.w = fmaf(w[u], v[u].w, O.w);
+            mv[u] = ml[2 * s];
+            lv[u] = ml[2 * s + 1];
         }
     }
     acc[wave][lane] = O;
@@ -380,7 +393,6 @@ __global__ void __launch_bounds__(CW * 64) k_attn_combine(const AttnArgs a) {
             Lt += lsum[w];
             Ot += af[w * HD + tid];
         }
-        const float gate = a.qg[(((size_t) bt * a.nq + h) * 2 + 1) * HD + tid];
         a.og[((size_t) bt * a.nq + h) * HD + tid] = (Ot / Lt) * sigmoidf_(gate);
     }
 }
