@@ -29,6 +29,9 @@ const char *error_cstr();
         return -1;                                                                                         \
     } while (0)
 
+// compute units of the current device (queried once; 256, MI355X, if the query fails)
+int device_cus();
+
 // ---------------------------------------------------------------------------------------------
 // wave64 cross-lane primitives.  Rotations inside a row of 16 lanes go through DPP (row_ror), the exchange
 // between the two rows of each 32-lane half through ds_swizzle (bit mode, xor 16), and the two halves of the

@@ -596,19 +596,6 @@ __global__ void k_gemv_reduce(const float *__restrict__ part, int ks, int n, flo
 int g_ov_ks = 0, g_ov_lpr = 0, g_ov_kernel = 0, g_ov_wpc = 0;
 constexpr int kLdsPerCu = 160 * 1024;  // LDS of a CDNA4 CU (the most one workgroup can take)
 
-// compute units of the current device (queried once)
-int cu_count() {
-    static int n = 0;
-    if (!n) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-            n = v;
-        else
-            n = 256;
-    }
-    return n;
-}
 
 PP planes(const QLayout &L, const uint8_t *packed) {
     PP P{packed + L.off[0], packed + L.off[1], packed + L.off[2], L.rs[0], L.rs[1], L.rs[2]};
@@ -634,7 +621,7 @@ int gemv_nt(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, f
         const size_t lds = (size_t) gps * XS;
         int per_cu = std::min(by_regs, std::max(1, (int) (kLdsPerCu / lds)));
         if (g_ov_wpc) per_cu = std::max(1, g_ov_wpc / 8);
-        nwg = std::min(nwg, cu_count() * per_cu);
+        nwg = std::min(nwg, device_cus() * per_cu);
         hipLaunchKernelGGL(kern, dim3((unsigned) nwg, (unsigned) pl.ks), dim3(512), lds, st, P, L.rows, pl.ngroups,
                            gps, x, L.cols, out);
     } else {

@@ -38,6 +38,18 @@ __global__ void __launch_bounds__(256) k_copy(float4 *__restrict__ dst, const fl
 
 }  // namespace
 
+int device_cus() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0, v = 0;
+        n = hipGetDevice(&dev) == hipSuccess &&
+                    hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0
+                ? v
+                : 256;
+    }
+    return n;
+}
+
 int fill_normal_launch(float *p, size_t n, uint64_t seed, float mean, float std, hipStream_t st) {
     if (!p && n) FN_FAIL("fill: null pointer");
     if (!n) return 0;
