@@ -48,8 +48,9 @@ struct GemvPlan {
 };
 
 GemvPlan gemv_plan(const QLayout &L);
-// benchmarking and tests: force lanes per row (16 / 32 / 64), split-K, the x staging (1 = chunks of lpr groups,
-// the path of an x too large for the LDS) and the resident waves per CU a persistent grid is sized for; 0 = automatic
+// benchmarking and tests: force lanes per row (16 / 32 / 64), split-K, the kernel (1 = x staged in chunks of lpr
+// groups, the path of an x too large for the LDS; 2 = x staged once; 3 / 4 = x staged once with the deep / short
+// walk) and the resident waves per CU a persistent grid is sized for; 0 = automatic
 void gemv_override(int lpr, int ks, int kernel, int waves_per_cu);
 size_t gemv_work_bytes(const QLayout &L, int nt);
 

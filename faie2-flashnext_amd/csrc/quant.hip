@@ -475,21 +475,21 @@ __device__ __forceinline__ void flush_rows(int s, int lane, int rows, float *acc
 // k_gemv, for a split whose x fits the LDS: the workgroup stages x once, then each wave walks its own row-sets
 // s = global wave id, + waves in the grid, ..., in batches of U groups per lane, with the next batch's loads (the
 // next row-set's, at the end of one) in flight while it sums the current one.  The host sizes the grid to the
-// workgroups resident at once, so no workgroup waits for another to finish.
+// workgroups resident at once, so no workgroup waits for another to finish.  Two walks, picked by the host from the
+// batches per wave (same bits):
+
+// short walk (a wave has a few batches): a batch is loaded only when the wave has it.  The compiler's wait counts
+// then merge the paths with and without the load and wait as if nothing newer were in flight, which costs nothing
+// at this depth and saves the surplus loads of the deep walk
 template <uint32_t TY, int NT, int LPR>
-__global__ void __launch_bounds__(512) k_gemv(PP P, int rows, int G, int gps, const float *__restrict__ x, int cols,
-                                                float *__restrict__ out) {
-    extern __shared__ float4 xs[];
-    constexpr int NW = Q<TY>::NW, U = Q<TY>::U, RPW = 64 / LPR, XB = NT <= 2 ? 4 : 8;
-    const int g0 = blockIdx.y * gps, g1 = min(G, g0 + gps), ng = g1 - g0;
-    if (ng <= 0) return;  // (the plan gives every split a group; whole workgroup, before any barrier)
+__device__ __forceinline__ void gemv_walk_short(const PP &P, int rows, int g0, int g1, int ng, int NS, int nws,
+                                                int NB, const float *__restrict__ x, int cols,
+                                                float *__restrict__ out, float4 *xs) {
+    constexpr int NW = Q<TY>::NW, U = Q<TY>::U, XB = NT <= 2 ? 4 : 8;
     const int tid = threadIdx.x, lane = tid & 63;
-    const int NS = (rows + RPW - 1) / RPW, nws = gridDim.x * 8;
-    const int NB = (ng + LPR * U - 1) / (LPR * U);
-    out += (size_t) blockIdx.y * NT * rows;
     // the wave's batches in order: (s, j), then (s1, j1) = next(s, j), ...; wave-uniform, so the row reductions run
     // on whole waves
-    int s = blockIdx.x * 8 + (tid >> 6), j = 0, s1, j1;
+    int s = blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(tid >> 6), j = 0, s1, j1;
     const auto next = [NB, nws](int s_, int j_, int &sn, int &jn) {
         sn = j_ + 1 == NB ? s_ + nws : s_;
         jn = j_ + 1 == NB ? 0 : j_ + 1;
@@ -541,6 +541,75 @@ __global__ void __launch_bounds__(512) k_gemv(PP P, int rows, int G, int gps, co
         if (s >= NS) break;
         if (s1 < NS) load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wb);
     }
+}
+
+// deep walk (many batches per wave): a steady-state pipeline whose wait counts stay exact
+template <uint32_t TY, int NT, int LPR>
+__device__ __forceinline__ void gemv_walk_deep(const PP &P, int rows, int g0, int g1, int ng, int NS, int nws, int NB,
+                                               const float *__restrict__ x, int cols, float *__restrict__ out,
+                                               float4 *xs) {
+    constexpr int NW = Q<TY>::NW, U = Q<TY>::U, XB = NT <= 2 ? 4 : 8;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // The wave's batches: b = 0 .. n-1, batch b = groups batch b % NB of row-set w0 + (b / NB) * nws.  Everything
+    // here is wave-uniform; readfirstlane makes that visible to the compiler, so the loops branch on scalars.
+    const int w0 = blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = w0 < NS ? ((NS - 1 - w0) / nws + 1) * NB : 0;
+    uint32_t wa[U][NW], wb[U][NW];
+    const Iq4Tab T;  // (IQ4 formats) the level table in registers, once
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    // x [NT][cols] -> xs (the layout of XPass).  The first part of x is requested before the wave's first one or two
+    // weight batches, so that its LDS writes wait for x alone.  A wave with one batch or none takes a short path
+    // with no prefetch; every wave passes the one barrier either way.
+    XPass<NT, XB> xp;
+    for (int e0 = 0; e0 < NT * 8 * ng; e0 += 512 * XB) {
+        xp.load(x, cols, g0, ng, e0, tid, 512);
+        if (e0 == 0) {
+            const int b1 = n > 1 ? 1 : 0;
+            load_batch<TY, LPR>(P, rows, w0, 0, lane, g0, g1, wa);
+            load_batch<TY, LPR>(P, rows, w0 + (b1 / NB) * nws, b1 % NB, lane, g0, g1, wb);
+        }
+        xp.store(xs, ng, e0, tid, 512);
+    }
+    __syncthreads();
+#define FN_GEMV_LOAD(W, B) load_batch<TY, LPR>(P, rows, w0 + ((B) / NB) * nws, (B) % NB, lane, g0, g1, W)
+#define FN_GEMV_SUM(W, B)                                                                      \
+    do {                                                                                       \
+        acc_batch<TY, NT, LPR>(W, (B) % NB, lane, g0, g1, xs, acc, T);                         \
+        if ((B) % NB == NB - 1) flush_rows<NT, LPR>(w0 + ((B) / NB) * nws, lane, rows, acc, out); \
+    } while (0)
+    // Steady state: two batches in flight while one is summed.  Every pass issues the same loads and the loop leaves
+    // only at its test, so the compiler's wait counts stay exact (a path that skips a load makes them assume nothing
+    // newer is in flight, and each wait would then drain the prefetched batch too).  The last two or three batches
+    // go after the loop.
+    int b = 0;
+    for (; b + 3 < n; b += 2) {
+        FN_GEMV_SUM(wa, b);
+        FN_GEMV_LOAD(wa, b + 2);
+        FN_GEMV_SUM(wb, b + 1);
+        FN_GEMV_LOAD(wb, b + 3);
+    }
+    if (b < n) FN_GEMV_SUM(wa, b);
+    if (b + 2 < n) FN_GEMV_LOAD(wa, b + 2);
+    if (b + 1 < n) FN_GEMV_SUM(wb, b + 1);
+    if (b + 2 < n) FN_GEMV_SUM(wa, b + 2);
+#undef FN_GEMV_SUM
+#undef FN_GEMV_LOAD
+}
+
+template <uint32_t TY, int NT, int LPR, bool DEEP>
+__global__ void __launch_bounds__(512) k_gemv(PP P, int rows, int G, int gps, const float *__restrict__ x, int cols,
+                                                float *__restrict__ out) {
+    extern __shared__ float4 xs[];
+    constexpr int U = Q<TY>::U, RPW = 64 / LPR;
+    const int g0 = blockIdx.y * gps, g1 = min(G, g0 + gps), ng = g1 - g0;
+    if (ng <= 0) return;  // (the plan gives every split a group; whole workgroup, before any barrier)
+    const int NS = (rows + RPW - 1) / RPW, nws = gridDim.x * 8;
+    const int NB = (ng + LPR * U - 1) / (LPR * U);
+    out += (size_t) blockIdx.y * NT * rows;
+    if constexpr (DEEP) gemv_walk_deep<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs);
+    else gemv_walk_short<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs);
 }
 
 // k_gemv_c, for an x too large for the LDS: x goes through it in chunks of kc groups (a multiple of LPR, so a
@@ -611,17 +680,20 @@ int gemv_nt(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, f
     int nwg = (ns + 7) / 8;
     constexpr int XS = xs_stride(NT) * (int) sizeof(float4);  // LDS bytes per group of x
     if (gps <= kLdsPerCu / XS && g_ov_kernel != 1) {
-        const auto kern = k_gemv<TY, NT, LPR>;
-        static int by_regs = 0;  // workgroups per CU the kernel's registers allow
+        static int by_regs = 0;  // workgroups per CU the registers allow (the deep walk's, the larger of the two)
         if (!by_regs) {
             int n = 0;
-            FN_CK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 512, 0));
+            FN_CK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv<TY, NT, LPR, true>, 512, 0));
             by_regs = std::max(1, n);
         }
         const size_t lds = (size_t) gps * XS;
         int per_cu = std::min(by_regs, std::max(1, (int) (kLdsPerCu / lds)));
         if (g_ov_wpc) per_cu = std::max(1, g_ov_wpc / 8);
         nwg = std::min(nwg, device_cus() * per_cu);
+        // batches of the busiest wave; from 4 on the deep walk's exact waits pay for its surplus loads (measured)
+        const int nb = (gps + LPR * Q<TY>::U - 1) / (LPR * Q<TY>::U), per_wave = (ns + 8 * nwg - 1) / (8 * nwg) * nb;
+        const bool deep = g_ov_kernel == 3 || (g_ov_kernel != 4 && per_wave >= 4);
+        const auto kern = deep ? k_gemv<TY, NT, LPR, true> : k_gemv<TY, NT, LPR, false>;
         hipLaunchKernelGGL(kern, dim3((unsigned) nwg, (unsigned) pl.ks), dim3(512), lds, st, P, L.rows, pl.ngroups,
                            gps, x, L.cols, out);
     } else {
@@ -709,7 +781,7 @@ bool qlayout(uint32_t type, int rows, int cols, QLayout &L) {
 void gemv_override(int lpr, int ks, int kernel, int waves_per_cu) {
     g_ov_lpr = (lpr == 16 || lpr == 32 || lpr == 64) ? lpr : 0;
     g_ov_ks = std::max(0, ks);
-    g_ov_kernel = (kernel == 1 || kernel == 2) ? kernel : 0;
+    g_ov_kernel = (kernel >= 1 && kernel <= 4) ? kernel : 0;
     g_ov_wpc = std::max(0, waves_per_cu);
 }
 

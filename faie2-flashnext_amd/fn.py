@@ -180,8 +180,8 @@ class FN:
         return ms.value
 
     def gemv_override(self, ks=0, lpr=0, kernel=0, waves_per_cu=0):
-        """Force the GEMV plan (0 = automatic): split-K, lanes per row, kernel (1 per-tile, 2 persistent) and the
-        resident waves per CU the persistent grid is sized for."""
+        """Force the GEMV plan (0 = automatic): split-K, lanes per row, kernel (1 x in chunks, 2 x staged once, 3 / 4
+        x staged once with the deep / short walk) and the resident waves per CU the persistent grid is sized for."""
         self.d.fn_gemv_override(int(lpr), int(ks), int(kernel), int(waves_per_cu))
 
     def bench_hot(self, on):

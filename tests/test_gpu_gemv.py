@@ -125,8 +125,8 @@ STAGING_CASES = [
 @pytest.mark.parametrize("wpc", [0, 8])
 def test_gemv_chunked_x_matches_one_stage(fnlib, name, rows, cols, nt, wpc):
     """x staged in chunks of lpr groups (k_gemv_c, the path of an x too large for the LDS) and x staged once (k_gemv:
-    persistent waves walking row-sets, grid sized for wpc waves per CU) give the same bits: a row's groups are summed
-    by the same lanes in the same order."""
+    persistent waves walking row-sets, grid sized for wpc waves per CU, with the deep and with the short walk) give
+    the same bits: a row's groups are summed by the same lanes in the same order."""
     t = TYPES[name]
     _say(f"gemv chunked vs one-stage x {name} {rows}x{cols} nt={nt} waves/CU={wpc or 'auto'} "
          f"plan={fnlib.gemv_plan(t, rows, cols)}")
@@ -135,12 +135,14 @@ def test_gemv_chunked_x_matches_one_stage(fnlib, name, rows, cols, nt, wpc):
     try:
         fnlib.gemv_override(kernel=1)
         y1 = fnlib.gemv(t, raw, rows, cols, x)
-        fnlib.gemv_override(kernel=2, waves_per_cu=wpc)
-        y2 = fnlib.gemv(t, raw, rows, cols, x)
+        fnlib.gemv_override(kernel=3, waves_per_cu=wpc)
+        y3 = fnlib.gemv(t, raw, rows, cols, x)
+        fnlib.gemv_override(kernel=4, waves_per_cu=wpc)
+        y4 = fnlib.gemv(t, raw, rows, cols, x)
     finally:
         fnlib.gemv_override(0)
-    assert np.array_equal(y1, y2)
-    assert oracle.relerr(y2, oracle.gemv(t, raw, rows, cols, x)) <= TOL
+    assert np.array_equal(y1, y3) and np.array_equal(y1, y4)
+    assert oracle.relerr(y3, oracle.gemv(t, raw, rows, cols, x)) <= TOL
 
 
 def test_gemv_tokens_independent(fnlib):
