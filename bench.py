@@ -168,6 +168,88 @@ class CoreStack:
                 b.free()
 
 
+# GGUF bytes of a rows x cols weight with finite scales: random quant bytes, and the high byte of every fp16 / bf16
+# scale kept below the all-ones exponent (the scale byte offsets inside each block, per format)
+_SCALE_HI = {8: [1], 14: [209], 23: [1], 30: [1]}
+
+
+def random_gguf(qtype, rows, cols, rng):
+    raw = rng.integers(0, 256, size=rows * fn.row_bytes(qtype, cols), dtype=np.uint8)
+    blk = raw.reshape(-1, fn.QBLOCK[qtype][1])
+    for off in _SCALE_HI[qtype]:
+        blk[:, off] &= 0x3F
+    return raw
+
+
+class LayerStack:
+    """L DeltaNet decode layers of one sequence with the projections either side of the block, at BASELINE's hidden
+    2048: GEMV qkv (IQ4_XS 8192 x 2048), z (Q6_K 4096 x 2048) and alpha/beta (BF16 64 x 2048) from the layer input,
+    the fused block, GEMV ssm_out (Q8_0 2048 x 4096) back to the hidden size.  Every layer has its own weights (packed
+    once, copied per layer: 29.6 MB a layer, 1.07 GB for 36, beyond the Infinity Cache) and state.  The launches go in
+    order on one stream (capturing the three input GEMVs as parallel graph branches measured slower: 33.5 against
+    27.9 µs a layer, the joins cost more than the overlap gives)."""
+
+    HID = 2048
+    PROJ = (("qkv", 23, C, 2048), ("z", 14, NVH * DK, 2048), ("ab", 30, 2 * NVH, 2048), ("o", 8, 2048, NVH * DK))
+
+    def __init__(self, lib, L, seed):
+        self.lib, self.L = lib, L
+        rng = np.random.default_rng(seed)
+        self.pos = hiprt.Buf.like(np.zeros(1, np.int32))
+        tmpl = {}
+        for name, t, r, c in self.PROJ:
+            raw = hiprt.Buf.like(random_gguf(t, r, c, rng))
+            pk = hiprt.Buf(lib.gemv_packed_bytes(t, r, c), np.uint8)
+            lib.gemv_pack_dev(t, raw.ptr, r, c, pk.ptr)
+            hiprt.sync()
+            raw.free()
+            tmpl[name] = pk
+        self.layers = []
+        for il in range(L):
+            lay = fn_synth.BlockLayer(B=1, config=1, layer=il)
+            d = {"x": hiprt.Buf.empty((self.HID,)), "y": hiprt.Buf.empty((self.HID,)),
+                 "qkv": hiprt.Buf.empty((1, 1, C)), "z": hiprt.Buf.empty((1, 1, NVH * DK)),
+                 "ab": hiprt.Buf.empty((1, 1, 2 * NVH)), "on": hiprt.Buf.empty((1, 1, NVH * DK)),
+                 "S": hiprt.Buf.empty((1, NVH, DK, DK)), "ring": hiprt.Buf.empty((1, 4, C)),
+                 "conv_w": hiprt.Buf.like(lay.conv_w), "dt": hiprt.Buf.like(lay.dt_bias),
+                 "sa": hiprt.Buf.like(lay.ssm_a), "nw": hiprt.Buf.like(lay.norm_w)}
+            for name, *_ in self.PROJ:
+                d["w_" + name] = hiprt.Buf(tmpl[name].nbytes, np.uint8)
+                lib.copy_dev(d["w_" + name].ptr, tmpl[name].ptr, tmpl[name].nbytes)
+            s = seed * 1000003 + il * 17
+            lib.fill_normal_dev(d["x"].ptr, self.HID, s + 1)
+            lib.fill_normal_dev(d["S"].ptr, NVH * DK * DK, s + 2, 0.0, 0.02)
+            lib.fill_normal_dev(d["ring"].ptr, 4 * C, s + 3)
+            self.layers.append(d)
+        hiprt.sync()
+        for b in tmpl.values():
+            b.free()
+
+    def _gemv(self, d, name, x, y, stream):
+        _, t, r, c = next(p for p in self.PROJ if p[0] == name)
+        self.lib.gemv_dev(t, d["w_" + name].ptr, r, c, x.ptr, 1, y.ptr, None, 0, stream.handle)
+
+    def launch(self, stream):
+        for d in self.layers:
+            for name in ("qkv", "z", "ab"):
+                self._gemv(d, name, d["x"], d[name], stream)
+            self.lib.gdn_block_dev(1, NKH, NVH, 1, 4, self.pos.ptr, d["qkv"].ptr, d["conv_w"].ptr, d["ring"].ptr,
+                                   d["ab"].ptr, d["dt"].ptr, d["sa"].ptr, d["S"].ptr, d["z"].ptr, d["nw"].ptr,
+                                   d["on"].ptr, stream.handle)
+            self._gemv(d, "o", d["on"], d["y"], stream)
+
+    def bytes_per_layer(self):
+        """Algorithmic bytes of one layer: the four weights once, the block's bytes, the GEMVs' x and y."""
+        w = sum(r * fn.row_bytes(t, c) + 4 * (r + c) for _, t, r, c in self.PROJ)
+        return w + fn_synth.gdn_block_bytes(1)
+
+    def free(self):
+        for d in self.layers:
+            for b in d.values():
+                b.free()
+        self.pos.free()
+
+
 class AttnStack:
     """GQA decode layers (16 q heads, 2 kv heads, head dim 256, RoPE on 64 dims, theta 1e7) of B sequences at
     context ctx (the new token at pos = ctx - 1), L distinct layers with their own fp32 caches."""
@@ -440,6 +522,15 @@ def main():
         extra["config1_block_b1"] = {"ms_per_step": round(ms, 4), "us_per_layer_step": round(ms * 1e3 / 36, 2),
                                      "tokens_per_s": round(1e3 / ms, 1),
                                      "gbs": round(36 * fn_synth.gdn_block_bytes(1) / (ms * 1e-3) / 1e9, 1)}
+        # config 1 with the projections: a whole DeltaNet layer of one sequence (GEMVs in, block, GEMV out)
+        ls = LayerStack(lib, 36, seed=4)
+        ms = time_graph(stream, lambda: ls.launch(stream), steps, warmup)
+        by = ls.bytes_per_layer()
+        ls.free()
+        extra["config1_layer_with_projections_b1"] = {
+            "us_per_layer_step": round(ms * 1e3 / 36, 2), "tokens_per_s": round(1e3 / ms, 1), "bytes_per_layer": by,
+            "gbs": round(36 * by / (ms * 1e-3) / 1e9, 1)}
+        log(f"[bench] config 1 layer with projections: {ms * 1e3 / 36:.2f} us/layer-step")
         # config 2 as speculative verify steps: nt = 4 new tokens per sequence per step, the previous step's
         # accepted tokens (kr of them) replayed into the committed state first; one S read + write per step
         for nt_v, kr_v in ((4, 2), (4, 4), (8, 4)):
