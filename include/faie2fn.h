@@ -42,6 +42,10 @@ int fn_forward(const int32_t *tokens, int nt, float *logits, int32_t *argmax);  
 int fn_debug_layers(float *out);                                              /* faie2fn.cu:2739 */
 /* GGUF rows W (rows x cols of `type`, the file's bytes) -> out [rows][cols] float32, bit for bit ggml's decode. */
 int fn_test_dequant(uint32_t type, const uint8_t *W, int rows, int cols, float *out);  /* faie2fn.cu:2751 */
+/* Force the plan of GEMVs launched from now on, 0 = automatic (the reference's arguments, this library's meaning):
+ * wpt = lanes per row (16, 32 or 64), ks = split-K workgroups per row, tb = kernel (1 x staged in chunks, 2 x
+ * staged once, 3 / 4 x staged once with the deep / short walk), warps_per_sm = resident waves per CU that a
+ * persistent grid is sized for.  Every choice gives the same bits except ks > 1. */
 void fn_gemv_override(int wpt, int ks, int tb, int warps_per_sm);             /* faie2fn.cu:2786 */
 void fn_gemv_waves(int waves);                                                /* faie2fn.cu:2793 */
 void fn_pdl(int on);                                                          /* faie2fn.cu:2796 */
