@@ -325,6 +325,275 @@ __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
     }
 }
 
+// ---- several new tokens per sequence (verify / chunked prefill): one K/V pass for all of them on the matrix cores
+//
+// For nt > 1 the nt * GRP query rows of a (sequence, kv head) form a small matrix (R = nt * GRP rows), so the work is
+// two thin GEMMs per key block instead of R dot products, and every token reads the same K/V.  k_attn_split_mt reads
+// each K/V byte of its split once for all R rows and runs the products on v_mfma_f32_16x16x4f32, in fp32 like the
+// single-token kernel.  Both products are taken transposed so that one lane holds one query row throughout:
+//   S^T[key][row] = sum_d K[key][d] Q[row][d]      A = K (lane: key l%16, dim slot l/16), B = Q (lane: row l%16)
+//   O^T[d][row]  += sum_key V[key][d] P[row][key]  A = V (lane: dim l%16, key slot l/16), B = P (lane: row l%16)
+// The S^T result leaves lane l with row l%16 and keys 4(l/16)..4(l/16)+3 of the 16-key block, which is exactly the
+// B operand the P.V product needs (key slot l/16 of step s = key 4(l/16)+s), and the O^T result leaves lane l with row
+// l%16 too, so the online-softmax rescale of O is a per-lane multiply with no data movement.  The contraction slots
+// are free to permute as long as both operands agree: in S^T, step (u, e) pairs dim 16u + 4(l/16) + e of K (lane l
+// reads 16-byte chunk 4u + l/16 of its key from the key-tiled cache) with the same dim of Q; in O^T, output tile
+// (c, e) maps MFMA row i to dim 64c + 4i + e, so lane l's V load is one float4 (dims 64c + 4(l%16) ...) and its
+// accumulators cover 16 consecutive dims 64c + 16(l/16) + 4r + e of its row.
+// Work split: KW waves walk the split's 16-key blocks interleaved (wave kw takes blocks kw, kw + KW, ..., so the
+// waves of a workgroup together stream whole 64-key tiles), each with its own softmax state, and RW row groups of
+// NRW 16-row blocks cover the R rows; the KW partial states merge in LDS with the log-sum-exp identity at the end and
+// the workgroup writes the same (m, l, o) partial per (token, head, split) as k_attn_split, for k_attn_combine.
+// Token t (row r = t * GRP + h) sees keys < min(pos + t + 1, max_ctx) (faie2fn.cu:1609-1668 per query, causal over
+// the new tokens).  One wave per SIMD (up to 512 registers): two 16-key blocks of K and V in flight (256 registers)
+// while the other is multiplied.
+constexpr int MT_OS = HD + 4;  // LDS row stride (floats) of the merge buffer: a wave's 16 rows land on distinct banks
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// K of the 16-key block starting at key kb: lane l takes 16-byte chunk 4u + l/16 of key kb + l%16 (keys past nkmax
+// are clamped: finite values, masked later)
+__device__ __forceinline__ void mt_load_k(float4 (&k)[16], const float4 *Kb, int kb, int nkmax, int lane) {
+    const int key = min(kb + (lane & 15), nkmax - 1);
+    const float4 *kt = Kb + (size_t) (key / TILE) * (TILE * HD / 4) + (key % TILE);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) k[u] = ld_nt(kt + (4 * u + (lane >> 4)) * TILE);
+}
+// V of the block: v[4s + c] = dims 64c + 4(l%16) .. +3 of key kb + 4(l/16) + s
+__device__ __forceinline__ void mt_load_v(float4 (&v)[16], const float4 *Vb, int kb, int nkmax, int lane) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int row = min(kb + 4 * (lane >> 4) + s, nkmax - 1);
+        const float4 *vr = Vb + (size_t) row * (HD / 4) + (lane & 15);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[4 * s + c] = ld_nt(vr + 16 * c);
+    }
+}
+
+// Scores of one 16-key block for this wave's NRW row blocks and the online-softmax step: p = probabilities (lane l:
+// row l%16, keys kb + 4(l/16) + r), o rescaled to the new running max.
+template <int NRW>
+__device__ __forceinline__ void mt_scores(const float4 (&k)[16], int kb, const float4 *qs, v4f (&o)[NRW][16],
+                                          float (&m)[NRW], float (&l)[NRW], const int (&lim)[NRW], int lane,
+                                          v4f (&p)[NRW]) {
+    float corr[NRW];
+    // Q is re-read from LDS every block (an opaque offset keeps the compiler from hoisting 64 registers per row block
+    // out of the walk; ds_read_b128 of consecutive lanes is conflict-free)
+    int qo = lane;
+    asm volatile("" : "+v"(qo));
+#pragma unroll
+    for (int j = 0; j < NRW; ++j) {
+        v4f s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+#pragma unroll
+        for (int u = 0; u < 16; u += 2) {
+            const float4 q0 = qs[(j * 16 + u) * 64 + qo], q1 = qs[(j * 16 + u + 1) * 64 + qo];
+            s0 = mfma4(k[u].x, q0.x, s0);
+            s1 = mfma4(k[u + 1].x, q1.x, s1);
+            s0 = mfma4(k[u].y, q0.y, s0);
+            s1 = mfma4(k[u + 1].y, q1.y, s1);
+            s0 = mfma4(k[u].z, q0.z, s0);
+            s1 = mfma4(k[u + 1].z, q1.z, s1);
+            s0 = mfma4(k[u].w, q0.w, s0);
+            s1 = mfma4(k[u + 1].w, q1.w, s1);
+        }
+        const float scale = rsqrtf((float) HD);
+        const int key = kb + 4 * (lane >> 4);
+        float sc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] = key + r < lim[j] ? (s0[r] + s1[r]) * scale : -INFINITY;
+        float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        mx = fmaxf(mx, swz_xor16(mx));
+        mx = fmaxf(mx, shfl_xor32(mx));  // max over the row's 16 keys (lanes l, l^16, l^32, l^48)
+        const float mn = fmaxf(m[j], mx);
+        corr[j] = mn == -INFINITY ? 1.0f : expf(m[j] - mn);  // 0 on the row's first visible block
+        float ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[j][r] = sc[r] == -INFINITY ? 0.0f : expf(sc[r] - mn);
+            ps += p[j][r];
+        }
+        l[j] = fmaf(l[j], corr[j], ps);
+        m[j] = mn;
+    }
+    bool rescale = false;
+#pragma unroll
+    for (int j = 0; j < NRW; ++j) rescale |= corr[j] != 1.0f;
+    if (__builtin_amdgcn_ballot_w64(rescale)) {  // x * 1.0f == x: skipping the multiply when no row's max moved is exact
+#pragma unroll
+        for (int j = 0; j < NRW; ++j)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) o[j][t] *= corr[j];
+    }
+}
+
+// o += V^T P^T for one block
+template <int NRW>
+__device__ __forceinline__ void mt_pv(const float4 (&v)[16], const v4f (&p)[NRW], v4f (&o)[NRW][16]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int j = 0; j < NRW; ++j) {
+                o[j][4 * c + 0] = mfma4(v[4 * s + c].x, p[j][s], o[j][4 * c + 0]);
+                o[j][4 * c + 1] = mfma4(v[4 * s + c].y, p[j][s], o[j][4 * c + 1]);
+                o[j][4 * c + 2] = mfma4(v[4 * s + c].z, p[j][s], o[j][4 * c + 2]);
+                o[j][4 * c + 3] = mfma4(v[4 * s + c].w, p[j][s], o[j][4 * c + 3]);
+            }
+}
+
+// grid (nsplit, nkv, B), RW * KW waves; dynamic LDS: max(RW * NRW * 16 KiB of Q, RW * KW * 16 * MT_OS * 4 B)
+template <int NRW>
+__global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+k_attn_split_mt(const AttnArgs a, int grp, int RW, int KW) {
+    extern __shared__ float4 mt_lds[];
+    __shared__ float2 mls[WAVES][NRW * 16];
+    const int sp_i = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nth = RW * KW * 64, rw = wave / KW, kw = wave - rw * KW;
+    const int R = a.nt * grp;
+    const int P0 = a.pos[b];
+    const int nkmax = min(P0 + a.nt, a.max_ctx);  // keys visible to the last token
+    const int ntiles = nkmax > 0 ? (nkmax + TILE - 1) / TILE : 0;
+    const int per = (ntiles + a.nsplit - 1) / a.nsplit;
+    const int tile0 = min(sp_i * per, ntiles), tile1 = min(tile0 + per, ntiles);
+    const int k0 = tile0 * TILE, k1 = min(tile1 * TILE, nkmax);
+    const int nblk = k1 > k0 ? (k1 - k0 + 15) / 16 : 0;
+    const int nw = nblk > kw ? (nblk - 1 - kw) / KW + 1 : 0;  // this wave's blocks
+
+    // Q of all row blocks into LDS: [row block][u][lane] float4, lane l = (row l%16, chunk 4u + l/16); rows >= R zero
+    const float4 *Qg = reinterpret_cast<const float4 *>(a.Q);
+    for (int i = tid; i < RW * NRW * 1024; i += nth) {
+        const int rb = i >> 10, u = (i >> 6) & 15, l = i & 63;
+        const int row = rb * 16 + (l & 15), c = 4 * u + (l >> 4);
+        float4 q = f4(0.0f);
+        if (row < R) {
+            const int t = row / grp, h = row - t * grp;
+            q = Qg[(((size_t) (b * a.nt + t) * a.nkv + g) * (HD / 4) + c) * grp + h];
+        }
+        mt_lds[i] = q;
+    }
+    __syncthreads();
+
+    const float4 *qs = mt_lds + rw * NRW * 1024;
+    const float4 *Kb = reinterpret_cast<const float4 *>(a.Kc + ((size_t) b * a.nkv + g) * a.max_ctx * HD);
+    const float4 *Vb = reinterpret_cast<const float4 *>(a.Vc + ((size_t) b * a.nkv + g) * a.max_ctx * HD);
+    v4f o[NRW][16];
+    float m[NRW], l[NRW];
+    int lim[NRW];
+#pragma unroll
+    for (int j = 0; j < NRW; ++j) {
+        m[j] = -INFINITY;
+        l[j] = 0.0f;
+        const int t = min(((rw * NRW + j) * 16 + (lane & 15)) / grp, a.nt - 1);
+        lim[j] = min(min(P0 + t + 1, a.max_ctx), k1);
+#pragma unroll
+        for (int t2 = 0; t2 < 16; ++t2) o[j][t2] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    if (nw > 0 && NRW == 1) {
+        // one row block: two whole blocks in flight (pairs of blocks; an odd count gets one block past k1, fully
+        // masked, to keep the loop free of conditionals, which keeps the wait counts exact: A's loads are awaited
+        // while B's 32 are still in flight)
+        const int npair = (nw + 1) / 2;
+        float4 ka[16], va[16], kb2[16], vb2[16];
+        v4f p[NRW];
+        mt_load_k(ka, Kb, k0 + kw * 16, nkmax, lane);
+        mt_load_v(va, Vb, k0 + kw * 16, nkmax, lane);
+        mt_load_k(kb2, Kb, k0 + (kw + KW) * 16, nkmax, lane);
+        mt_load_v(vb2, Vb, k0 + (kw + KW) * 16, nkmax, lane);
+        int pr = 0;
+        for (; pr + 1 < npair; ++pr) {
+            const int kb = k0 + (kw + 2 * pr * KW) * 16;
+            mt_scores<NRW>(ka, kb, qs, o, m, l, lim, lane, p);
+            mt_pv<NRW>(va, p, o);
+            mt_load_k(ka, Kb, kb + 2 * KW * 16, nkmax, lane);
+            mt_load_v(va, Vb, kb + 2 * KW * 16, nkmax, lane);
+            mt_scores<NRW>(kb2, kb + KW * 16, qs, o, m, l, lim, lane, p);
+            mt_pv<NRW>(vb2, p, o);
+            mt_load_k(kb2, Kb, kb + 3 * KW * 16, nkmax, lane);
+            mt_load_v(vb2, Vb, kb + 3 * KW * 16, nkmax, lane);
+        }
+        const int kb = k0 + (kw + 2 * pr * KW) * 16;
+        mt_scores<NRW>(ka, kb, qs, o, m, l, lim, lane, p);
+        mt_pv<NRW>(va, p, o);
+        mt_scores<NRW>(kb2, kb + KW * 16, qs, o, m, l, lim, lane, p);
+        mt_pv<NRW>(vb2, p, o);
+    } else if (nw > 0) {
+        // two row blocks: twice the products per block, so half a block in flight hides the load latency -- the
+        // next block's K is requested once the scores are done, its V once P.V is done
+        float4 kf[16], vf[16];
+        v4f p[NRW];
+        mt_load_k(kf, Kb, k0 + kw * 16, nkmax, lane);
+        mt_load_v(vf, Vb, k0 + kw * 16, nkmax, lane);
+        int i = 0;
+        for (; i + 1 < nw; ++i) {
+            const int kb = k0 + (kw + i * KW) * 16;
+            mt_scores<NRW>(kf, kb, qs, o, m, l, lim, lane, p);
+            mt_load_k(kf, Kb, kb + KW * 16, nkmax, lane);
+            mt_pv<NRW>(vf, p, o);
+            mt_load_v(vf, Vb, kb + KW * 16, nkmax, lane);
+        }
+        mt_scores<NRW>(kf, k0 + (kw + i * KW) * 16, qs, o, m, l, lim, lane, p);
+        mt_pv<NRW>(vf, p, o);
+    }
+
+    // merge the KW key streams of each row group (log-sum-exp), then write the split partials
+#pragma unroll
+    for (int j = 0; j < NRW; ++j) {
+        l[j] += swz_xor16(l[j]);
+        l[j] += shfl_xor32(l[j]);
+        if (lane < 16) mls[wave][j * 16 + lane] = make_float2(m[j], l[j]);
+    }
+    __syncthreads();  // Q is dead: the LDS becomes the merge buffer
+    float *ob = reinterpret_cast<float *>(mt_lds);
+#pragma unroll
+    for (int j = 0; j < NRW; ++j) {
+        {
+            const int row = lane & 15;
+            float M = -INFINITY;
+            for (int w = 0; w < KW; ++w) M = fmaxf(M, mls[rw * KW + w][j * 16 + row].x);
+            const float sc = m[j] == -INFINITY ? 0.0f : expf(m[j] - M);
+            float *dst = ob + (wave * 16 + row) * MT_OS + 16 * (lane >> 4);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<float4 *>(dst + 64 * c + 4 * q) =
+                        make_float4(o[j][4 * c][q] * sc, o[j][4 * c + 1][q] * sc, o[j][4 * c + 2][q] * sc,
+                                    o[j][4 * c + 3][q] * sc);
+        }
+        __syncthreads();
+        for (int i = tid; i < RW * 16 * 64; i += nth) {
+            const int rg = i >> 10, row = (i >> 6) & 15, d4 = i & 63;
+            const int rowg = (rg * NRW + j) * 16 + row;
+            if (rowg < R) {
+                float4 O = f4(0.0f);
+                for (int w = 0; w < KW; ++w) {
+                    const float4 x = *reinterpret_cast<const float4 *>(ob + ((rg * KW + w) * 16 + row) * MT_OS + 4 * d4);
+                    O.x += x.x; O.y += x.y; O.z += x.z; O.w += x.w;
+                }
+                const int t = rowg / grp, h = rowg - t * grp;
+                const size_t pi = ((size_t) (b * a.nt + t) * a.nq + g * grp + h) * a.nsplit + sp_i;
+                reinterpret_cast<float4 *>(a.part_o + pi * HD)[d4] = O;
+                if (d4 == 0) {
+                    float M = -INFINITY, L = 0.0f;
+                    for (int w = 0; w < KW; ++w) M = fmaxf(M, mls[rg * KW + w][j * 16 + row].x);
+                    for (int w = 0; w < KW; ++w) {
+                        const float2 ml = mls[rg * KW + w][j * 16 + row];
+                        if (ml.x != -INFINITY) L = fmaf(expf(ml.x - M), ml.y, L);
+                    }
+                    a.part_ml[pi * 2] = M;
+                    a.part_ml[pi * 2 + 1] = L;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // merge splits + sigmoid output gate (faie2fn.cu:1670-1690).  grid (nq, B nt), CW * 64 threads.
 // Wave w takes splits w, w + CW, ...; lane l owns dims 4l..4l+3 (one coalesced 1 KiB row per split) with NB rows in
 // flight.  The first NB rows of every wave, their (m, l) and the gate are all requested at the start, before the
@@ -415,13 +684,19 @@ size_t attn_work_bytes(int B, int nq, int nt, int hd, int nsplit) {
     return (q + po + pm) * sizeof(float) + 256;
 }
 
-// About 512 workgroups in all (two per CU at the split kernel's occupancy); a context of 256 tiles or more keeps at
-// least 4 tiles per workgroup (fewer, larger splits: less partial traffic for the combine), a shorter one goes as
-// wide as one tile per workgroup (latency-bound).  Measured on MI355X (B, L -> best nsplit): 1, 4K -> 64;
+// One new token: about 512 workgroups in all (two per CU at the split kernel's occupancy); a context of 256 tiles or
+// more keeps at least 4 tiles per workgroup (fewer, larger splits: less partial traffic for the combine), a shorter
+// one goes as wide as one tile per workgroup (latency-bound).  Measured on MI355X (B, L -> best nsplit): 1, 4K -> 64;
 // 1, 32K -> 128; 1, 128K -> 256; 16, 32K -> 16.
+// Several new tokens: k_attn_split_mt's grid has no token dimension and holds one workgroup per CU, so one
+// workgroup per CU in all.
 int attn_pick_nsplit(int B, int nkv, int nt, int ctx) {
     const int tiles = std::max(1, (ctx + TILE - 1) / TILE);
-    const long groups = std::max(1L, (long) B * nt * nkv);
+    if (nt > 1) {
+        const long groups = std::max(1L, (long) B * nkv), cus = device_cus();
+        return (int) std::max(1L, std::min<long>((cus + groups - 1) / groups, tiles));
+    }
+    const long groups = std::max(1L, (long) B * nkv);
     long want = std::max(1L, (512 + groups - 1) / groups);
     if (tiles >= 256) want = std::min<long>(want, tiles / 4);
     return (int) std::max(1L, std::min<long>(want, tiles));
@@ -456,10 +731,18 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
     // tokens see each other's new keys, so they go through k_attn_prep first
     const bool fused = p.nt == 1;
     if (!fused) hipLaunchKernelGGL(k_attn_prep, dim3((unsigned) bt, p.nq + p.nkv), dim3(HD), 0, st, a);
+    const int nr = (p.nt * grp + 15) / 16;  // 16-row blocks of the multi-token query matrix
     if (fused) {
         if (grp == 8) hipLaunchKernelGGL((k_attn_split<8, true>), sg, sb, 0, st, a);
         else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, true>), sg, sb, 0, st, a);
         else hipLaunchKernelGGL((k_attn_split<4, true>), sg, sb, 0, st, a);
+    } else if (nr <= 8 && p.B <= 65535) {
+        // rows in groups of NRW 16-row blocks (RW groups), KW key streams per group, at most 4 waves
+        const int nrw = nr == 1 ? 1 : 2, rw = (nr + nrw - 1) / nrw, kw = std::max(1, WAVES / rw);
+        const size_t lds = std::max((size_t) rw * nrw * 16 * HD * 4, (size_t) rw * kw * 16 * MT_OS * 4);
+        const dim3 mg(p.nsplit, p.nkv, p.B), mb(rw * kw * 64);
+        if (nrw == 1) hipLaunchKernelGGL(k_attn_split_mt<1>, mg, mb, lds, st, a, grp, rw, kw);
+        else hipLaunchKernelGGL(k_attn_split_mt<2>, mg, mb, lds, st, a, grp, rw, kw);
     } else {
         if (grp == 8) hipLaunchKernelGGL((k_attn_split<8, false>), sg, sb, 0, st, a);
         else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, false>), sg, sb, 0, st, a);

@@ -62,20 +62,70 @@ def test_attn_multi_token(fnlib):
     _check(fnlib, case)
 
 
+def _mt_case(B, nq, nkv, nt, pos, max_ctx, seed):
+    """nt new tokens per sequence at positions pos[b] .. pos[b] + nt - 1, cache rows below pos[b] filled."""
+    rng = np.random.default_rng(seed)
+    case = fn_synth.AttnCase(B=B, L=1, nq=nq, nkv=nkv, seed=seed, max_ctx=max_ctx)
+    for b in range(B):
+        case.Kc[b, :pos[b]] = rng.standard_normal((pos[b], nkv, 256), dtype=np.float32)
+        case.Vc[b, :pos[b]] = rng.standard_normal((pos[b], nkv, 256), dtype=np.float32)
+    case.qg = rng.standard_normal((B, nt, nq, 2, 256)).astype(np.float32)
+    case.k = rng.standard_normal((B, nt, nkv, 256)).astype(np.float32)
+    case.v = rng.standard_normal((B, nt, nkv, 256)).astype(np.float32)
+    case.pos = np.array(pos, np.int32)
+    return case
+
+
+# (nq, nkv, nt, positions, max_ctx): R = nt * nq / nkv query rows per kv head in 16-row blocks -- 1 block (one row
+# block per wave, two K/V blocks in flight), 2 (two per wave, half-block pipeline), 3 (two row groups, the second
+# half padding), 4, 6 (three waves), 8 (four row groups, one key stream), 9 (above the matrix-core kernel's 8 blocks:
+# the per-token kernel); positions 0 (the first token sees only itself), tile edges, the end of the cache
+MT_SHAPES = [
+    (16, 2, 2, [200, 0], 256),
+    (8, 2, 3, [700], 768),
+    (16, 2, 4, [1000, 63, 5], 1088),
+    (24, 2, 4, [777, 60], 832),
+    (16, 2, 8, [1500, 120], 1536),
+    (24, 2, 8, [900], 960),
+    (16, 2, 16, [640], 704),
+    (16, 2, 17, [500], 576),
+    (16, 2, 4, [1020], 1024),
+    (32, 4, 4, [333, 64], 448),
+]
+
+
+@pytest.mark.parametrize("nq,nkv,nt,pos,max_ctx", MT_SHAPES)
+def test_attn_multi_token_shapes(fnlib, nq, nkv, nt, pos, max_ctx):
+    _say(f"attn multi-token nq={nq} nkv={nkv} nt={nt} pos={pos} max_ctx={max_ctx}")
+    _check(fnlib, _mt_case(len(pos), nq, nkv, nt, pos, max_ctx, seed=nt * 100 + nq + pos[0]))
+
+
+def test_attn_multi_token_split_invariant(fnlib):
+    """nt = 4: the result does not depend on the split count (splits of odd and even 16-key block counts, splits
+    past the last token's keys, splits that only the later tokens see into)."""
+    _say("attn multi-token nsplit invariance L=3000 nt=4")
+    case = _mt_case(2, 16, 2, 4, [2996, 1900], 3008, seed=77)
+    outs = [_check(fnlib, case, nsplit=s) for s in (1, 3, 7, 16, 47, 64, 0)]
+    for o in outs[1:]:
+        assert oracle.relerr(o, outs[0]) <= 2e-6
+
+
 def test_attn_reference_group_12(fnlib):
     """The reference model's own head shape: 24 query heads over 2 kv heads (faie2fn.cu:47-48)."""
     _say("attn nq=24 nkv=2")
     _check(fnlib, fn_synth.AttnCase(B=1, L=513, nq=24))
 
 
-@pytest.mark.parametrize("B,L,pick", [(16, 32768, [0, 7, 15]), (1, 131072, [0])])
-def test_attn_full_size_device(fnlib, B, L, pick):
+@pytest.mark.parametrize("B,L,nt,pick", [(16, 32768, 1, [0, 7, 15]), (1, 131072, 1, [0]), (16, 32768, 4, [0, 15]),
+                                         (1, 32768, 8, [0])])
+def test_attn_full_size_device(fnlib, B, L, nt, pick):
     """BASELINE config 3 at full size through the device entry point: caches filled in HBM, the oracle run on a
-    subset of the sequences (they are independent), compared on og and the appended K/V row."""
+    subset of the sequences (they are independent), compared on og and the appended K/V rows.  nt > 1: the last nt
+    positions are the new tokens (a verify step at full context)."""
     import fn
     import hiprt
 
-    _say(f"attn full size B={B} L={L}, oracle on sequences {pick}")
+    _say(f"attn full size B={B} L={L} nt={nt}, oracle on sequences {pick}")
     nq, nkv, hd = 16, 2, 256
     rng = np.random.default_rng(L + B)
     per_seq = nkv * L * hd
@@ -83,19 +133,19 @@ def test_attn_full_size_device(fnlib, B, L, pick):
     V = hiprt.Buf.empty((B * per_seq,))
     fnlib.fill_normal_dev(K.ptr, B * per_seq, 11)
     fnlib.fill_normal_dev(V.ptr, B * per_seq, 12)
-    qg = rng.standard_normal((B, 1, nq, 2, hd)).astype(np.float32)
-    kn = rng.standard_normal((B, 1, nkv, hd)).astype(np.float32)
-    vn = rng.standard_normal((B, 1, nkv, hd)).astype(np.float32)
+    qg = rng.standard_normal((B, nt, nq, 2, hd)).astype(np.float32)
+    kn = rng.standard_normal((B, nt, nkv, hd)).astype(np.float32)
+    vn = rng.standard_normal((B, nt, nkv, hd)).astype(np.float32)
     wq = rng.normal(1, 0.1, hd).astype(np.float32)
     wk = rng.normal(1, 0.1, hd).astype(np.float32)
-    pos = np.full(B, L - 1, np.int32)
+    pos = np.full(B, L - nt, np.int32)
     d = {n: hiprt.Buf.like(x) for n, x in (("qg", qg), ("k", kn), ("v", vn), ("wq", wq), ("wk", wk), ("pos", pos))}
-    nsplit = fnlib.attn_nsplit(B, nkv, 1, L)
-    wb = fnlib.attn_work_bytes(B, nq, 1, nsplit)
+    nsplit = fnlib.attn_nsplit(B, nkv, nt, L)
+    wb = fnlib.attn_work_bytes(B, nq, nt, nsplit)
     work = hiprt.Buf(wb)
-    og = hiprt.Buf.empty((B, 1, nq, hd))
-    fnlib.attn_dev(B, nq, nkv, 1, L, d["pos"].ptr, d["qg"].ptr, d["k"].ptr, d["v"].ptr, d["wq"].ptr, d["wk"].ptr, K.ptr,
-                   V.ptr, nsplit, work.ptr, wb, og.ptr, None)
+    og = hiprt.Buf.empty((B, nt, nq, hd))
+    fnlib.attn_dev(B, nq, nkv, nt, L, d["pos"].ptr, d["qg"].ptr, d["k"].ptr, d["v"].ptr, d["wq"].ptr, d["wk"].ptr,
+                   K.ptr, V.ptr, nsplit, work.ptr, wb, og.ptr, None)
     hiprt.sync()
     got = og.download()
     for b in pick:
@@ -103,7 +153,8 @@ def test_attn_full_size_device(fnlib, B, L, pick):
         Vd = hiprt.dtoh(V.ptr + b * per_seq * 4, (per_seq,))
         Kr, Vr = fn.kv_from_device(Kd, Vd, 1, L, nkv, hd)
         ref_og, ref_k, ref_v = oracle.attn(qg[b:b + 1], kn[b:b + 1], vn[b:b + 1], wq, wk, Kr, Vr, pos[b:b + 1])
-        e = (oracle.relerr(got[b:b + 1], ref_og), oracle.relerr(Kr[:, L - 1:L], ref_k), oracle.relerr(Vr[:, L - 1:L], ref_v))
+        e = (oracle.relerr(got[b:b + 1], ref_og), oracle.relerr(Kr[:, L - nt:L], ref_k),
+             oracle.relerr(Vr[:, L - nt:L], ref_v))
         assert max(e) <= TOL, (b, e)
     for x in (K, V, work, og, *d.values()):
         x.free()
