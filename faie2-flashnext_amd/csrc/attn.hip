@@ -345,13 +345,47 @@ __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
 // NRW 16-row blocks cover the R rows; the KW partial states merge in LDS with the log-sum-exp identity at the end and
 // the workgroup writes the same (m, l, o) partial per (token, head, split) as k_attn_split, for k_attn_combine.
 // Token t (row r = t * GRP + h) sees keys < min(pos + t + 1, max_ctx) (faie2fn.cu:1609-1668 per query, causal over
-// the new tokens).  One wave per SIMD (up to 512 registers): two 16-key blocks of K and V in flight (256 registers)
-// while the other is multiplied.
+// the new tokens).  One wave per SIMD (up to 512 registers; the O accumulators and the K operands live in AGPRs).
+// One row block per wave (R <= 16): two 16-key blocks of K and V in flight while the other is multiplied.  Two row
+// blocks: twice the products per block, so half a block in flight suffices, and the walk is software pipelined --
+// the softmax step of block i is cut into stages woven between the score products of block i + 1.
+// Measured on MI355X (B = 16, 32K context, 16 query / 2 kv heads): with the K/V loads made cache-resident the layer
+// step is only 5-6 % faster, so the kernel is bound by the matrix cores and the instructions between them, not by
+// HBM: at nt = 8 the products alone take 490 us at the 2.14 GHz this load runs at, the kernel ~700 us.  Two waves per
+// SIMD with one row block each were slower (each wave loads K/V for its own 16 rows: twice the loads).
 constexpr int MT_OS = HD + 4;  // LDS row stride (floats) of the merge buffer: a wave's 16 rows land on distinct banks
+constexpr float MT_SLACK = 8.0f;  // growth of a row's max (natural-log units) that triggers a rescale
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// max / sum of the values of lanes l and l ^ 16, and of l and l ^ 32, through v_permlane16_swap / v_permlane32_swap
+// (VALU lane swaps, no LDS round trip): swapping two copies of x leaves the pair {x[l & ~16], x[l | 16]} (resp. 32)
+// in the same order in both lanes, so both get the same bits.  Issued as inline asm: this compiler's
+// __builtin_amdgcn_permlane16_swap / 32_swap lowering folds an add or max of the two results into one result
+// doubled.  The s_nop 1 covers the wait states a VALU write needs before a permlane reads it.  (Not volatile: a pure
+// function of its inputs, free to move, so it does not order the surrounding code.)
+__device__ __forceinline__ float2 swap16(float x) {
+    float a = x, b = x;
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return make_float2(a, b);
+}
+__device__ __forceinline__ float2 swap32(float x) {
+    float a = x, b = x;
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return make_float2(a, b);
+}
+__device__ __forceinline__ float max_x16_x32(float x) {
+    float2 r = swap16(x);
+    r = swap32(fmaxf(r.x, r.y));
+    return fmaxf(r.x, r.y);
+}
+__device__ __forceinline__ float sum_x16_x32(float x) {
+    float2 r = swap16(x);
+    r = swap32(r.x + r.y);
+    return r.x + r.y;
 }
 
 // K of the 16-key block starting at key kb: lane l takes 16-byte chunk 4u + l/16 of key kb + l%16 (keys past nkmax
@@ -375,59 +409,177 @@ __device__ __forceinline__ void mt_load_v(float4 (&v)[16], const float4 *Vb, int
 
 // Scores of one 16-key block for this wave's NRW row blocks and the online-softmax step: p = probabilities (lane l:
 // row l%16, keys kb + 4(l/16) + r), o rescaled to the new running max.
+// S^T of one 16-key block for this wave's NRW row blocks (lane l: row l%16, keys 4(l/16) .. 4(l/16)+3 of the block).
+// Q comes from LDS ([row block][u][lane] float4, lane l = row l%16, chunk 4u + l/16; ds_read_b128 of consecutive
+// lanes is conflict-free), one u ahead: the reads of step u + 1 are in flight while the 4 * NRW products of step u
+// run.  (Held in registers instead, Q would take 64 of the 256 VGPRs per row block that MFMA operands must come
+// from, which two row blocks with their K and V block do not leave.)
 template <int NRW>
-__device__ __forceinline__ void mt_scores(const float4 (&k)[16], int kb, const float4 *qs, v4f (&o)[NRW][16],
-                                          float (&m)[NRW], float (&l)[NRW], const int (&lim)[NRW], int lane,
-                                          v4f (&p)[NRW]) {
-    float corr[NRW];
-    // Q is re-read from LDS every block (an opaque offset keeps the compiler from hoisting 64 registers per row block
-    // out of the walk; ds_read_b128 of consecutive lanes is conflict-free)
+__device__ __forceinline__ void mt_qk(const float4 (&k)[16], const float4 *qs, int lane, int kb, v4f (&S)[NRW]) {
+    v4f s0[NRW], s1[NRW];
+    float4 qc[NRW];
+    // the read offset goes through an empty asm that also takes the block's first key: opaque and different per
+    // block, so the compiler neither hoists the 64 * NRW registers of Q reads out of the walk nor orders them
     int qo = lane;
-    asm volatile("" : "+v"(qo));
+    asm("" : "+v"(qo) : "v"(kb));
 #pragma unroll
     for (int j = 0; j < NRW; ++j) {
-        v4f s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = s0;
+        s0[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        s1[j] = s0[j];
+        qc[j] = qs[(j * 16) * 64 + qo];
+    }
 #pragma unroll
-        for (int u = 0; u < 16; u += 2) {
-            const float4 q0 = qs[(j * 16 + u) * 64 + qo], q1 = qs[(j * 16 + u + 1) * 64 + qo];
-            s0 = mfma4(k[u].x, q0.x, s0);
-            s1 = mfma4(k[u + 1].x, q1.x, s1);
-            s0 = mfma4(k[u].y, q0.y, s0);
-            s1 = mfma4(k[u + 1].y, q1.y, s1);
-            s0 = mfma4(k[u].z, q0.z, s0);
-            s1 = mfma4(k[u + 1].z, q1.z, s1);
-            s0 = mfma4(k[u].w, q0.w, s0);
-            s1 = mfma4(k[u + 1].w, q1.w, s1);
+    for (int u = 0; u < 16; ++u) {
+        float4 qn[NRW];
+#pragma unroll
+        for (int j = 0; j < NRW; ++j) qn[j] = qs[(j * 16 + (u + 1) % 16) * 64 + qo];  // u = 15: a harmless re-read
+#pragma unroll
+        for (int j = 0; j < NRW; ++j) {
+            v4f &acc = (u & 1) ? s1[j] : s0[j];
+            acc = mfma4(k[u].x, qc[j].x, acc);
+            acc = mfma4(k[u].y, qc[j].y, acc);
+            acc = mfma4(k[u].z, qc[j].z, acc);
+            acc = mfma4(k[u].w, qc[j].w, acc);
         }
+#pragma unroll
+        for (int j = 0; j < NRW; ++j) qc[j] = qn[j];
+    }
+#pragma unroll
+    for (int j = 0; j < NRW; ++j) S[j] = s0[j] + s1[j];
+}
+
+// Online-softmax step of a block whose keys start at kb: p = probabilities of the lane's 4 keys against the row's
+// reference max, corr = the factor o and l take (1 unless the reference moved).  The row keeps its reference until a
+// block exceeds it by more than MT_SLACK, so p <= e^MT_SLACK and o is rescaled rarely (o / l and the split merge
+// only need one reference per row).  exp(d) = 2^(d log2 e) on v_exp_f32: d <= MT_SLACK, and the two roundings
+// before the exponential cost at most ~2e-6 relative on the smallest weights (|d| ~ 30), ~1e-7 near the max.
+template <int NRW>
+__device__ __forceinline__ void mt_softmax(const v4f (&S)[NRW], int kb, float (&m)[NRW], float (&l)[NRW],
+                                           const int (&lim)[NRW], int lane, v4f (&p)[NRW], float (&corr)[NRW]) {
+    constexpr float LOG2E = 1.4426950408889634f;
+#pragma unroll
+    for (int j = 0; j < NRW; ++j) {
         const float scale = rsqrtf((float) HD);
         const int key = kb + 4 * (lane >> 4);
         float sc[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[r] = key + r < lim[j] ? (s0[r] + s1[r]) * scale : -INFINITY;
-        float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        mx = fmaxf(mx, swz_xor16(mx));
-        mx = fmaxf(mx, shfl_xor32(mx));  // max over the row's 16 keys (lanes l, l^16, l^32, l^48)
-        const float mn = fmaxf(m[j], mx);
-        corr[j] = mn == -INFINITY ? 1.0f : expf(m[j] - mn);  // 0 on the row's first visible block
+        for (int r = 0; r < 4; ++r) sc[r] = key + r < lim[j] ? S[j][r] * scale : -INFINITY;
+        // max over the row's 16 keys (lanes l, l^16, l^32, l^48)
+        const float mx = max_x16_x32(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+        const bool first = m[j] == -INFINITY, moved = !first && mx > m[j] + MT_SLACK;
+        const float mn = first || moved ? mx : m[j];
+        corr[j] = moved ? __builtin_amdgcn_exp2f((m[j] - mn) * LOG2E) : 1.0f;  // o, l are 0 while no key was seen
         float ps = 0.0f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            p[j][r] = sc[r] == -INFINITY ? 0.0f : expf(sc[r] - mn);
+            p[j][r] = sc[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((sc[r] - mn) * LOG2E);
             ps += p[j][r];
         }
         l[j] = fmaf(l[j], corr[j], ps);
         m[j] = mn;
     }
+}
+
+// The softmax step of mt_softmax cut into 5 stages per row block (t = 5 j + stage), for interleaving with the next
+// block's products; same arithmetic in the same order.
+template <int NRW>
+struct MtSoft {
+    float sc[NRW][4], mx[NRW];
+};
+template <int NRW>
+__device__ __forceinline__ void mt_soft_stage(int t, MtSoft<NRW> &st, const v4f (&S)[NRW], int kb, float (&m)[NRW],
+                                              float (&l)[NRW], const int (&lim)[NRW], int lane, v4f (&p)[NRW],
+                                              float (&corr)[NRW]) {
+    constexpr float LOG2E = 1.4426950408889634f;
+    const int j = t / 5, ph = t % 5;
+    if (j >= NRW) return;
+    if (ph == 0) {
+        const float scale = rsqrtf((float) HD);
+        const int key = kb + 4 * (lane >> 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st.sc[j][r] = key + r < lim[j] ? S[j][r] * scale : -INFINITY;
+        st.mx[j] = fmaxf(fmaxf(st.sc[j][0], st.sc[j][1]), fmaxf(st.sc[j][2], st.sc[j][3]));
+    } else if (ph == 1) {
+        const float2 r = swap16(st.mx[j]);
+        st.mx[j] = fmaxf(r.x, r.y);
+    } else if (ph == 2) {
+        const float2 r = swap32(st.mx[j]);
+        const float mx = fmaxf(r.x, r.y);
+        const bool first = m[j] == -INFINITY, moved = !first && mx > m[j] + MT_SLACK;
+        const float mn = first || moved ? mx : m[j];
+        corr[j] = moved ? __builtin_amdgcn_exp2f((m[j] - mn) * LOG2E) : 1.0f;
+        m[j] = mn;
+    } else if (ph == 3) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+            p[j][r] = st.sc[j][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((st.sc[j][r] - m[j]) * LOG2E);
+    } else {
+#pragma unroll
+        for (int r = 2; r < 4; ++r)
+            p[j][r] = st.sc[j][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((st.sc[j][r] - m[j]) * LOG2E);
+        l[j] = fmaf(l[j], corr[j], ((p[j][0] + p[j][1]) + p[j][2]) + p[j][3]);
+    }
+}
+
+// mt_qk of the block at kbq into Sn, with the softmax step of the previous block (scores S, first key kb) woven in:
+// stage u runs after the products of dim step u, fenced by scheduling barriers (this compiler otherwise puts all of
+// the VALU work before or after the products, where nothing overlaps it).
+template <int NRW>
+__device__ __forceinline__ void mt_qk_soft(const float4 (&k)[16], const float4 *qs, int lane, int kbq, v4f (&Sn)[NRW],
+                                           const v4f (&S)[NRW], int kb, float (&m)[NRW], float (&l)[NRW],
+                                           const int (&lim)[NRW], v4f (&p)[NRW], float (&corr)[NRW]) {
+    MtSoft<NRW> st;
+    v4f s0[NRW], s1[NRW];
+    float4 qc[NRW];
+    int qo = lane;
+    asm("" : "+v"(qo) : "v"(kbq));
+#pragma unroll
+    for (int j = 0; j < NRW; ++j) {
+        s0[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        s1[j] = s0[j];
+        qc[j] = qs[(j * 16) * 64 + qo];
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        float4 qn[NRW];
+#pragma unroll
+        for (int j = 0; j < NRW; ++j) qn[j] = qs[(j * 16 + (u + 1) % 16) * 64 + qo];
+#pragma unroll
+        for (int j = 0; j < NRW; ++j) {
+            v4f &acc = (u & 1) ? s1[j] : s0[j];
+            acc = mfma4(k[u].x, qc[j].x, acc);
+            acc = mfma4(k[u].y, qc[j].y, acc);
+            acc = mfma4(k[u].z, qc[j].z, acc);
+            acc = mfma4(k[u].w, qc[j].w, acc);
+        }
+#pragma unroll
+        for (int j = 0; j < NRW; ++j) qc[j] = qn[j];
+        __builtin_amdgcn_sched_barrier(0);
+        mt_soft_stage<NRW>(u, st, S, kb, m, l, lim, lane, p, corr);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int j = 0; j < NRW; ++j) Sn[j] = s0[j] + s1[j];
+}
+
+template <int NRW>
+__device__ __forceinline__ void mt_rescale(v4f (&o)[NRW][16], const float (&corr)[NRW]) {
     bool rescale = false;
 #pragma unroll
     for (int j = 0; j < NRW; ++j) rescale |= corr[j] != 1.0f;
-    if (__builtin_amdgcn_ballot_w64(rescale)) {  // x * 1.0f == x: skipping the multiply when no row's max moved is exact
+    if (__builtin_amdgcn_ballot_w64(rescale)) {  // x * 1.0f == x: the rows that kept their reference are unchanged
 #pragma unroll
         for (int j = 0; j < NRW; ++j)
 #pragma unroll
             for (int t = 0; t < 16; ++t) o[j][t] *= corr[j];
     }
 }
+
+// scores, softmax step and P.V of one block, in sequence
+template <int NRW>
+__device__ __forceinline__ void mt_block(const float4 (&k)[16], const float4 (&v)[16], int kb, const float4 *qs,
+                                         v4f (&o)[NRW][16], float (&m)[NRW], float (&l)[NRW], const int (&lim)[NRW],
+                                         int lane);
 
 // o += V^T P^T for one block
 template <int NRW>
@@ -445,7 +597,19 @@ __device__ __forceinline__ void mt_pv(const float4 (&v)[16], const v4f (&p)[NRW]
             }
 }
 
-// grid (nsplit, nkv, B), RW * KW waves; dynamic LDS: max(RW * NRW * 16 KiB of Q, RW * KW * 16 * MT_OS * 4 B)
+template <int NRW>
+__device__ __forceinline__ void mt_block(const float4 (&k)[16], const float4 (&v)[16], int kb, const float4 *qs,
+                                         v4f (&o)[NRW][16], float (&m)[NRW], float (&l)[NRW], const int (&lim)[NRW],
+                                         int lane) {
+    v4f S[NRW], p[NRW];
+    float corr[NRW];
+    mt_qk<NRW>(k, qs, lane, kb, S);
+    mt_softmax<NRW>(S, kb, m, l, lim, lane, p, corr);
+    mt_rescale<NRW>(o, corr);
+    mt_pv<NRW>(v, p, o);
+}
+
+// grid (nsplit, nkv, B), RW * KW <= 4 waves; dynamic LDS: max(RW * NRW * 16 KiB of Q, RW * KW * 16 * MT_OS * 4 B)
 template <int NRW>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 k_attn_split_mt(const AttnArgs a, int grp, int RW, int KW) {
@@ -469,15 +633,14 @@ k_attn_split_mt(const AttnArgs a, int grp, int RW, int KW) {
     for (int i = tid; i < RW * NRW * 1024; i += nth) {
         const int rb = i >> 10, u = (i >> 6) & 15, l = i & 63;
         const int row = rb * 16 + (l & 15), c = 4 * u + (l >> 4);
-        float4 q = f4(0.0f);
+        float4 qv = f4(0.0f);
         if (row < R) {
             const int t = row / grp, h = row - t * grp;
-            q = Qg[(((size_t) (b * a.nt + t) * a.nkv + g) * (HD / 4) + c) * grp + h];
+            qv = Qg[(((size_t) (b * a.nt + t) * a.nkv + g) * (HD / 4) + c) * grp + h];
         }
-        mt_lds[i] = q;
+        mt_lds[i] = qv;
     }
     __syncthreads();
-
     const float4 *qs = mt_lds + rw * NRW * 1024;
     const float4 *Kb = reinterpret_cast<const float4 *>(a.Kc + ((size_t) b * a.nkv + g) * a.max_ctx * HD);
     const float4 *Vb = reinterpret_cast<const float4 *>(a.Vc + ((size_t) b * a.nkv + g) * a.max_ctx * HD);
@@ -499,7 +662,6 @@ k_attn_split_mt(const AttnArgs a, int grp, int RW, int KW) {
         // while B's 32 are still in flight)
         const int npair = (nw + 1) / 2;
         float4 ka[16], va[16], kb2[16], vb2[16];
-        v4f p[NRW];
         mt_load_k(ka, Kb, k0 + kw * 16, nkmax, lane);
         mt_load_v(va, Vb, k0 + kw * 16, nkmax, lane);
         mt_load_k(kb2, Kb, k0 + (kw + KW) * 16, nkmax, lane);
@@ -507,44 +669,59 @@ k_attn_split_mt(const AttnArgs a, int grp, int RW, int KW) {
         int pr = 0;
         for (; pr + 1 < npair; ++pr) {
             const int kb = k0 + (kw + 2 * pr * KW) * 16;
-            mt_scores<NRW>(ka, kb, qs, o, m, l, lim, lane, p);
-            mt_pv<NRW>(va, p, o);
+            mt_block<NRW>(ka, va, kb, qs, o, m, l, lim, lane);
             mt_load_k(ka, Kb, kb + 2 * KW * 16, nkmax, lane);
             mt_load_v(va, Vb, kb + 2 * KW * 16, nkmax, lane);
-            mt_scores<NRW>(kb2, kb + KW * 16, qs, o, m, l, lim, lane, p);
-            mt_pv<NRW>(vb2, p, o);
+            mt_block<NRW>(kb2, vb2, kb + KW * 16, qs, o, m, l, lim, lane);
             mt_load_k(kb2, Kb, kb + 3 * KW * 16, nkmax, lane);
             mt_load_v(vb2, Vb, kb + 3 * KW * 16, nkmax, lane);
         }
         const int kb = k0 + (kw + 2 * pr * KW) * 16;
-        mt_scores<NRW>(ka, kb, qs, o, m, l, lim, lane, p);
-        mt_pv<NRW>(va, p, o);
-        mt_scores<NRW>(kb2, kb + KW * 16, qs, o, m, l, lim, lane, p);
-        mt_pv<NRW>(vb2, p, o);
+        mt_block<NRW>(ka, va, kb, qs, o, m, l, lim, lane);
+        mt_block<NRW>(kb2, vb2, kb + KW * 16, qs, o, m, l, lim, lane);
     } else if (nw > 0) {
         // two row blocks: twice the products per block, so half a block in flight hides the load latency -- the
-        // next block's K is requested once the scores are done, its V once P.V is done
+        // next block's K is requested once its predecessor's scores are done, its V once P.V is done.  Software
+        // pipelined: the softmax step of block i (VALU) sits next to the scores of block i + 1 (MFMA) so the two can
+        // overlap; the scheduling barriers keep each load where the pipeline puts it (hoisted above the products that
+        // still read the previous block, it would hold two blocks' registers at once and spill).
         float4 kf[16], vf[16];
-        v4f p[NRW];
-        mt_load_k(kf, Kb, k0 + kw * 16, nkmax, lane);
-        mt_load_v(vf, Vb, k0 + kw * 16, nkmax, lane);
+        v4f S[NRW];
+        auto kbl = [&](int i) { return k0 + (kw + i * KW) * 16; };  // first key of this wave's block i
+        mt_load_k(kf, Kb, kbl(0), nkmax, lane);
+        mt_load_v(vf, Vb, kbl(0), nkmax, lane);
+        mt_qk<NRW>(kf, qs, lane, kbl(0), S);
+        __builtin_amdgcn_sched_barrier(0);
+        mt_load_k(kf, Kb, kbl(1), nkmax, lane);  // past the wave's last block when nw = 1: in bounds, unused
+        __builtin_amdgcn_sched_barrier(0);
         int i = 0;
         for (; i + 1 < nw; ++i) {
-            const int kb = k0 + (kw + i * KW) * 16;
-            mt_scores<NRW>(kf, kb, qs, o, m, l, lim, lane, p);
-            mt_load_k(kf, Kb, kb + KW * 16, nkmax, lane);
+            v4f p[NRW];
+            float corr[NRW];
+            v4f Sn[NRW];
+            mt_qk_soft<NRW>(kf, qs, lane, kbl(i + 1), Sn, S, kbl(i), m, l, lim, p, corr);
+#pragma unroll
+            for (int j = 0; j < NRW; ++j) S[j] = Sn[j];
+            __builtin_amdgcn_sched_barrier(0);
+            mt_load_k(kf, Kb, kbl(i + 2), nkmax, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            mt_rescale<NRW>(o, corr);
             mt_pv<NRW>(vf, p, o);
-            mt_load_v(vf, Vb, kb + KW * 16, nkmax, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            mt_load_v(vf, Vb, kbl(i + 1), nkmax, lane);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        mt_scores<NRW>(kf, k0 + (kw + i * KW) * 16, qs, o, m, l, lim, lane, p);
+        v4f p[NRW];
+        float corr[NRW];
+        mt_softmax<NRW>(S, kbl(i), m, l, lim, lane, p, corr);
+        mt_rescale<NRW>(o, corr);
         mt_pv<NRW>(vf, p, o);
     }
 
     // merge the KW key streams of each row group (log-sum-exp), then write the split partials
 #pragma unroll
     for (int j = 0; j < NRW; ++j) {
-        l[j] += swz_xor16(l[j]);
-        l[j] += shfl_xor32(l[j]);
+        l[j] = sum_x16_x32(l[j]);
         if (lane < 16) mls[wave][j * 16 + lane] = make_float2(m[j], l[j]);
     }
     __syncthreads();  // Q is dead: the LDS becomes the merge buffer
@@ -594,18 +771,21 @@ k_attn_split_mt(const AttnArgs a, int grp, int RW, int KW) {
     }
 }
 
-// merge splits + sigmoid output gate (faie2fn.cu:1670-1690).  grid (nq, B nt), CW * 64 threads.
-// Wave w takes splits w, w + CW, ...; lane l owns dims 4l..4l+3 (one coalesced 1 KiB row per split) with NB rows in
+// merge splits + sigmoid output gate (faie2fn.cu:1670-1690).  grid (nq, B nt), cw * 64 threads, 4 <= cw <= CW.
+// Wave w takes splits w, w + cw, ...; lane l owns dims 4l..4l+3 (one coalesced 1 KiB row per split) with NB rows in
 // flight.  The first NB rows of every wave, their (m, l) and the gate are all requested at the start, before the
-// global max M over the splits is known, so a merge of up to CW * NB splits costs one memory round trip; the waves'
-// sums meet in LDS.
-constexpr int CW = 16;
+// global max M over the splits is known, so a merge of up to cw * NB splits costs one memory round trip; the waves'
+// sums meet in LDS.  The host sizes cw to the split count (combine_waves), so a merge of few splits does not hold
+// 16 waves.
+constexpr int CW = 16, CNB = 8;
+int combine_waves(int nsplit) { return std::min(CW, std::max(4, (nsplit + CNB - 1) / CNB)); }
 __global__ void __launch_bounds__(CW * 64) k_attn_combine(const AttnArgs a) {
-    constexpr int NB = 8;
+    constexpr int NB = CNB;
     __shared__ float red[CW];
     __shared__ float4 acc[CW][HD / 4];
     __shared__ float lsum[CW];
     const int h = blockIdx.x, bt = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int cw = blockDim.x >> 6;
     const int ns = a.nsplit;
     const size_t base = ((size_t) bt * a.nq + h) * ns;
     const float *ml = a.part_ml + base * 2;
@@ -615,37 +795,37 @@ __global__ void __launch_bounds__(CW * 64) k_attn_combine(const AttnArgs a) {
     float mv[NB], lv[NB];
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
-        const int s = min(wave + CW * u, ns - 1);
+        const int s = min(wave + cw * u, ns - 1);
         v[u] = ld_nt(&po[(size_t) s * (HD / 4) + lane]);
         mv[u] = ml[2 * s];
         lv[u] = ml[2 * s + 1];
     }
     float M = -INFINITY;
-    for (int s = tid; s < ns; s += CW * 64) M = fmaxf(M, ml[2 * s]);
+    for (int s = tid; s < ns; s += cw * 64) M = fmaxf(M, ml[2 * s]);
     M = wave_max(M);
     if (lane == 0) red[wave] = M;
     __syncthreads();
     M = red[0];
 #pragma unroll
-    for (int w = 1; w < CW; ++w) M = fmaxf(M, red[w]);
+    for (int w = 1; w < cw; ++w) M = fmaxf(M, red[w]);
     float4 O = f4(0.0f);
     float L = 0.0f;
     for (int s0 = wave;;) {
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             // splits without keys (m = -inf) and the clamped repeats past the end weigh 0
-            const float w = (s0 + CW * u < ns && mv[u] != -INFINITY) ? expf(mv[u] - M) : 0.0f;
+            const float w = (s0 + cw * u < ns && mv[u] != -INFINITY) ? expf(mv[u] - M) : 0.0f;
             L = fmaf(w, w != 0.0f ? lv[u] : 0.0f, L);
             O.x = fmaf(w, v[u].x, O.x);
             O.y = fmaf(w, v[u].y, O.y);
             O.z = fmaf(w, v[u].z, O.z);
             O.w = fmaf(w, v[u].w, O.w);
         }
-        s0 += CW * NB;
+        s0 += cw * NB;
         if (s0 >= ns) break;
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
-            const int s = min(s0 + CW * u, ns - 1);
+            const int s = min(s0 + cw * u, ns - 1);
             v[u] = ld_nt(&po[(size_t) s * (HD / 4) + lane]);
             mv[u] = ml[2 * s];
             lv[u] = ml[2 * s + 1];
@@ -658,7 +838,7 @@ __global__ void __launch_bounds__(CW * 64) k_attn_combine(const AttnArgs a) {
         const float *af = reinterpret_cast<const float *>(acc);
         float Lt = 0.0f, Ot = 0.0f;
 #pragma unroll
-        for (int w = 0; w < CW; ++w) {
+        for (int w = 0; w < cw; ++w) {
             Lt += lsum[w];
             Ot += af[w * HD + tid];
         }
@@ -748,7 +928,7 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
         else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, false>), sg, sb, 0, st, a);
         else hipLaunchKernelGGL((k_attn_split<4, false>), sg, sb, 0, st, a);
     }
-    hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(CW * 64), 0, st, a);
+    hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(combine_waves(p.nsplit) * 64), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
 }
@@ -797,7 +977,7 @@ int attn_qsa_launch(const AttnDecode &p, const QsaIndexer &ix, hipStream_t st) {
         else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, false, true>), sg, sb, 0, st, a);
         else hipLaunchKernelGGL((k_attn_split<4, false, true>), sg, sb, 0, st, a);
     }
-    hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(CW * 64), 0, st, a);
+    hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(combine_waves(p.nsplit) * 64), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
 }

@@ -110,6 +110,20 @@ def test_attn_multi_token_split_invariant(fnlib):
         assert oracle.relerr(o, outs[0]) <= 2e-6
 
 
+@pytest.mark.parametrize("nq,nt", [(16, 4), (16, 2), (24, 8)])
+def test_attn_multi_token_growing_scores(fnlib, nq, nt):
+    """Scores that grow along the context (key scale 1 -> 21) and one outlier key 40x: the running max of every row
+    moves many times mid-walk, so the multi-token kernel's rescale of o and l runs (it rescales once a block's max
+    exceeds the row's reference by more than 8)."""
+    _say(f"attn multi-token growing scores nq={nq} nt={nt}")
+    L = 2000
+    case = _mt_case(2, nq, 2, nt, [L - nt, 1234], 2048, seed=91 + nq + nt)
+    ramp = (1.0 + 20.0 * np.arange(2048) / L).astype(np.float32)
+    case.Kc *= ramp[None, :, None, None]
+    case.Kc[0, 1500] *= 40.0
+    _check(fnlib, case)
+
+
 def test_attn_reference_group_12(fnlib):
     """The reference model's own head shape: 24 query heads over 2 kv heads (faie2fn.cu:47-48)."""
     _say("attn nq=24 nkv=2")
