@@ -252,22 +252,22 @@ class LayerStack:
 
 class AttnStack:
     """GQA decode layers (16 q heads, 2 kv heads, head dim 256, RoPE on 64 dims, theta 1e7) of B sequences at
-    context ctx (the new token at pos = ctx - 1), L distinct layers with their own fp32 caches."""
+    context ctx (the nt new tokens at pos = ctx - nt .. ctx - 1), L distinct layers with their own fp32 caches."""
 
-    def __init__(self, lib, B, ctx, L, seed, nq=16, nkv=2, nsplit=0):
-        self.lib, self.B, self.ctx, self.L, self.nq, self.nkv = lib, B, ctx, L, nq, nkv
+    def __init__(self, lib, B, ctx, L, seed, nq=16, nkv=2, nsplit=0, nt=1):
+        self.lib, self.B, self.ctx, self.L, self.nq, self.nkv, self.nt = lib, B, ctx, L, nq, nkv, nt
         self.max_ctx = (ctx + 63) // 64 * 64
-        self.nsplit = nsplit or lib.attn_nsplit(B, nkv, 1, ctx)
-        self.wb = lib.attn_work_bytes(B, nq, 1, self.nsplit)
-        self.pos = hiprt.Buf.like(np.full(B, ctx - 1, np.int32))
+        self.nsplit = nsplit or lib.attn_nsplit(B, nkv, nt, ctx)
+        self.wb = lib.attn_work_bytes(B, nq, nt, self.nsplit)
+        self.pos = hiprt.Buf.like(np.full(B, ctx - nt, np.int32))
         self.work = hiprt.Buf(self.wb)
         self.layers = []
         rng = np.random.default_rng(seed)
         for il in range(L):
             cache = B * nkv * self.max_ctx * 256
             d = {"K": hiprt.Buf.empty((cache,)), "V": hiprt.Buf.empty((cache,)),
-                 "qg": hiprt.Buf.empty((B, 1, nq, 2, 256)), "k": hiprt.Buf.empty((B, 1, nkv, 256)),
-                 "v": hiprt.Buf.empty((B, 1, nkv, 256)), "og": hiprt.Buf.empty((B, 1, nq, 256)),
+                 "qg": hiprt.Buf.empty((B, nt, nq, 2, 256)), "k": hiprt.Buf.empty((B, nt, nkv, 256)),
+                 "v": hiprt.Buf.empty((B, nt, nkv, 256)), "og": hiprt.Buf.empty((B, nt, nq, 256)),
                  "wq": hiprt.Buf.like(rng.normal(1.0, 0.1, 256).astype(np.float32)),
                  "wk": hiprt.Buf.like(rng.normal(1.0, 0.1, 256).astype(np.float32))}
             s = seed * 104729 + il * 31
@@ -278,7 +278,7 @@ class AttnStack:
 
     def launch(self, stream, layers=None):
         for d in (self.layers if layers is None else layers):
-            self.lib.attn_dev(self.B, self.nq, self.nkv, 1, self.max_ctx, self.pos.ptr, d["qg"].ptr, d["k"].ptr,
+            self.lib.attn_dev(self.B, self.nq, self.nkv, self.nt, self.max_ctx, self.pos.ptr, d["qg"].ptr, d["k"].ptr,
                               d["v"].ptr, d["wq"].ptr, d["wk"].ptr, d["K"].ptr, d["V"].ptr, self.nsplit,
                               self.work.ptr, self.wb, d["og"].ptr, stream.handle)
 
@@ -459,6 +459,9 @@ def main():
     ap.add_argument("--counters", action="store_true",
                     help="counter-collection workload only: 3 plain copies of 1 GiB (the calibration kernel) and one "
                          "eager pass of the config-2 stack (36 dispatches of the fused DeltaNet kernel)")
+    ap.add_argument("--counters-attn", action="store_true",
+                    help="counter-collection workload only: 5 eager multi-token GQA layer-steps at B=16, 32K context, "
+                         "nt=8 then 5 at nt=4 (k_attn_split_mt<2>)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build's path runs on one MI355X (no collectives); "
@@ -474,6 +477,17 @@ def main():
         for k, v in res.items():
             log(f"[bench] {k}: {v}")
         print(json.dumps({"gemv": res}), flush=True)
+        return
+    if args.counters_attn:
+        for ntq in (8, 4):
+            at = AttnStack(lib, 16, 32768, 1, seed=4, nt=ntq)
+            for _ in range(5):
+                at.launch(stream)
+            stream.sync()
+            at.free()
+        print(json.dumps({"counters_workload": "multi-token GQA B=16 ctx=32768: 5 x nt=8 then 5 x nt=4",
+                          "flops_nt8": fn_synth.attn_flops(16, 32768, nt=8),
+                          "flops_nt4": fn_synth.attn_flops(16, 32768, nt=4)}))
         return
     if args.counters:
         nb = 1 << 30
@@ -552,6 +566,20 @@ def main():
             extra[f"config3_gqa_b{Bq}_ctx{ctx}"] = {"us_per_layer_step": round(ms * 1e3, 2),
                                                    "gbs": round(by / (ms * 1e-3) / 1e9, 1), "nsplit": nsplit}
             log(f"[bench] config 3 B={Bq} ctx={ctx}: {ms * 1e3:.1f} us, {by / (ms * 1e-3) / 1e9:.0f} GB/s")
+        # config 3 multi-token (speculative verify / chunked prefill): nt new tokens per sequence share one K/V pass
+        # on the matrix cores; GB/s counts K/V once, TFLOP/s the fp32 products (peak 157.3)
+        for Bq, ctx, nl, ntq in ((1, 32768, 8, 4), (16, 32768, 2, 4), (16, 32768, 2, 8)):
+            at = AttnStack(lib, Bq, ctx, nl, seed=4, nt=ntq)
+            ms = time_graph(stream, lambda: at.launch(stream), steps, warmup) / nl
+            nsplit = at.nsplit
+            at.free()
+            by, fl = fn_synth.attn_bytes(Bq, ctx, nt=ntq), fn_synth.attn_flops(Bq, ctx, nt=ntq)
+            extra[f"config3_gqa_b{Bq}_ctx{ctx}_nt{ntq}"] = {
+                "us_per_layer_step": round(ms * 1e3, 2), "draft_tokens_per_s": round(Bq * ntq * 1e3 / ms, 1),
+                "gbs": round(by / (ms * 1e-3) / 1e9, 1), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+                "nsplit": nsplit}
+            log(f"[bench] config 3 B={Bq} ctx={ctx} nt={ntq}: {ms * 1e3:.1f} us, {by / (ms * 1e-3) / 1e9:.0f} GB/s, "
+                f"{fl / (ms * 1e-3) / 1e12:.1f} TFLOP/s")
         # config 3 through the reference's own attention: QSA indexer active past 2048 keys (top 512 blocks of 4)
         for Bq, ctx, nl in ((1, 32768, 8), (1, 131072, 4), (16, 32768, 2)):
             qs = QsaStack(lib, Bq, ctx, nl, seed=5)

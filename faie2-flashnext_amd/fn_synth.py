@@ -116,9 +116,17 @@ def gdn_core_bytes(B, nkh=16, nvh=32):
     return B * (2 * nvh * DK * DV * 4 + (2 * nkh * DK + 2 * nvh * DV + 2 * nvh) * 4)
 
 
-def attn_bytes(B, L, nq=16, nkv=2, hd=HD):
-    """Algorithmic HBM bytes of one GQA decode layer-step: K + V read over L keys, q, gate and out, new k, v."""
-    return B * (L * nkv * hd * 4 * 2 + 3 * nq * hd * 4 + 2 * nkv * hd * 4)
+def attn_bytes(B, L, nq=16, nkv=2, hd=HD, nt=1):
+    """Algorithmic HBM bytes of one GQA decode layer-step: K + V read once over L keys, and per new token q, gate and
+    out, new k, v (nt new tokens at positions L - nt .. L - 1 share the one K/V pass)."""
+    return B * (L * nkv * hd * 4 * 2 + nt * (3 * nq * hd * 4 + 2 * nkv * hd * 4))
+
+
+def attn_flops(B, L, nq=16, nkv=2, hd=HD, nt=1):
+    """Algorithmic flops of the same step: q.k and p.v, 2 hd multiply-adds each, for every (query head, token, visible
+    key) -- token t of nt sees L - nt + t + 1 keys."""
+    keys = nt * (L - nt) + nt * (nt + 1) // 2
+    return B * nq * keys * 4 * hd
 
 
 def attn_qsa_bytes(B, L, top=512, nq=16, nkv=2, hd=HD, ixd=128):
