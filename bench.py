@@ -369,6 +369,36 @@ def hybrid_config4(lib, steps, warmup, B=16, ctx=32768, nl=48):
     return ms, nbytes
 
 
+def hybrid_verify(lib, stream, steps, warmup, B=16, ctx=32768, nt=4, kr=2, nl=48):
+    """Config 4's layer stack as a speculative verify step: 36 DeltaNet layers through fn_gdn_verify_dev (kr accepted
+    tokens of the previous step committed, nt new tokens run) and 12 GQA layers through fn_attn_dev with nt new
+    tokens at context ctx, in the hybrid order (attention iff (il + 1) % 4 == 0), one hipGraph per step.  Returns ms
+    per step and the algorithmic bytes of a step."""
+    vs = VerifyStack(lib, B, nl - nl // 4, nt, kr, seed=8)
+    at = AttnStack(lib, B, ctx, nl // 4, seed=9, nt=nt)
+    try:
+        def launch():
+            lib.advance_by_dev(vs.pos.ptr, vs.kr.ptr, B, stream.handle)
+            gi = ai = 0
+            for il in range(nl):
+                if (il + 1) % 4:
+                    d = vs.layers[gi]
+                    gi += 1
+                    lib.gdn_verify_dev(B, NKH, NVH, nt, vs.ring, vs.pos.ptr, vs.kr.ptr, nt, d["rqkv"].ptr,
+                                       d["rab"].ptr, d["qkv"].ptr, d["conv_w"].ptr, d["ring"].ptr, d["ab"].ptr,
+                                       d["dt"].ptr, d["sa"].ptr, d["S"].ptr, d["z"].ptr, d["nw"].ptr, d["out"].ptr,
+                                       stream.handle)
+                else:
+                    at.launch(stream, layers=[at.layers[ai]])
+                    ai += 1
+        ms = time_graph(stream, launch, steps, warmup)
+    finally:
+        vs.free()
+        at.free()
+    nbytes = (nl - nl // 4) * fn_synth.gdn_verify_bytes(B, nt, kr) + (nl // 4) * fn_synth.attn_bytes(B, ctx, nt=nt)
+    return ms, nbytes
+
+
 def time_graph(stream, fn_launch, steps, warmup):
     """Capture fn_launch into a hipGraph, replay warmup times, then time `steps` replays with HIP events recorded
     on the same stream.  Returns ms per replay."""
@@ -601,6 +631,12 @@ def main():
                                                      "gbs": round(fn_synth.gdn_block_bytes(64) / hook_ms / 1e6, 1)}
         extra.update(gemv_extras(lib))
         ms, nbytes = hybrid_config4(lib, steps, warmup)
+        ms_v, by_v = hybrid_verify(lib, stream, steps, warmup)
+        extra["config4_hybrid_verify_b16_ctx32768_nt4_kr2"] = {
+            "ms_per_step": round(ms_v, 4), "draft_tokens_per_s": round(16 * 4 * 1e3 / ms_v, 1),
+            "bytes_per_step": by_v, "gbs": round(by_v / (ms_v * 1e-3) / 1e9, 1)}
+        log(f"[bench] config 4 as a verify step (nt 4, kr 2): {ms_v:.3f} ms/step, "
+            f"{16 * 4 * 1e3 / ms_v:.0f} draft tokens/s")
         extra["config4_hybrid_b16_ctx32768"] = {"ms_per_step": round(ms, 4), "us_per_token": round(ms * 1e3 / 16, 2),
                                                "tokens_per_s": round(16 * 1e3 / ms, 1), "bytes_per_step": nbytes,
                                                "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
