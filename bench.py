@@ -187,7 +187,8 @@ class LayerStack:
     the fused block, GEMV ssm_out (Q8_0 2048 x 4096) back to the hidden size.  Every layer has its own weights (packed
     once, copied per layer: 29.6 MB a layer, 1.07 GB for 36, beyond the Infinity Cache) and state.  The launches go in
     order on one stream (capturing the three input GEMVs as parallel graph branches measured slower: 33.5 against
-    27.9 µs a layer, the joins cost more than the overlap gives)."""
+    27.9 µs a layer, the joins cost more than the overlap gives).  launch_fused runs the alpha/beta projection inside
+    the block (fn_gdn_block_xab_dev over the raw BF16 rows) instead of its own GEMV: four launches a layer."""
 
     HID = 2048
     PROJ = (("qkv", 23, C, 2048), ("z", 14, NVH * DK, 2048), ("ab", 30, 2 * NVH, 2048), ("o", 8, 2048, NVH * DK))
@@ -202,7 +203,10 @@ class LayerStack:
             pk = hiprt.Buf(lib.gemv_packed_bytes(t, r, c), np.uint8)
             lib.gemv_pack_dev(t, raw.ptr, r, c, pk.ptr)
             hiprt.sync()
-            raw.free()
+            if name == "ab":
+                tmpl["ab_raw"] = raw  # GGUF BF16 rows, as the fused block reads them
+            else:
+                raw.free()
             tmpl[name] = pk
         self.layers = []
         for il in range(L):
@@ -213,7 +217,7 @@ class LayerStack:
                  "S": hiprt.Buf.empty((1, NVH, DK, DK)), "ring": hiprt.Buf.empty((1, 4, C)),
                  "conv_w": hiprt.Buf.like(lay.conv_w), "dt": hiprt.Buf.like(lay.dt_bias),
                  "sa": hiprt.Buf.like(lay.ssm_a), "nw": hiprt.Buf.like(lay.norm_w)}
-            for name, *_ in self.PROJ:
+            for name in [p[0] for p in self.PROJ] + ["ab_raw"]:
                 d["w_" + name] = hiprt.Buf(tmpl[name].nbytes, np.uint8)
                 lib.copy_dev(d["w_" + name].ptr, tmpl[name].ptr, tmpl[name].nbytes)
             s = seed * 1000003 + il * 17
@@ -236,6 +240,15 @@ class LayerStack:
             self.lib.gdn_block_dev(1, NKH, NVH, 1, 4, self.pos.ptr, d["qkv"].ptr, d["conv_w"].ptr, d["ring"].ptr,
                                    d["ab"].ptr, d["dt"].ptr, d["sa"].ptr, d["S"].ptr, d["z"].ptr, d["nw"].ptr,
                                    d["on"].ptr, stream.handle)
+            self._gemv(d, "o", d["on"], d["y"], stream)
+
+    def launch_fused(self, stream):
+        for d in self.layers:
+            for name in ("qkv", "z"):
+                self._gemv(d, name, d["x"], d[name], stream)
+            self.lib.gdn_block_xab_dev(1, NKH, NVH, 4, self.pos.ptr, d["qkv"].ptr, d["conv_w"].ptr, d["ring"].ptr,
+                                       d["x"].ptr, self.HID, d["w_ab_raw"].ptr, d["dt"].ptr, d["sa"].ptr, d["S"].ptr,
+                                       d["z"].ptr, d["nw"].ptr, d["on"].ptr, stream.handle)
             self._gemv(d, "o", d["on"], d["y"], stream)
 
     def bytes_per_layer(self):
@@ -569,12 +582,17 @@ def main():
         # config 1 with the projections: a whole DeltaNet layer of one sequence (GEMVs in, block, GEMV out)
         ls = LayerStack(lib, 36, seed=4)
         ms = time_graph(stream, lambda: ls.launch(stream), steps, warmup)
+        ms_f = time_graph(stream, lambda: ls.launch_fused(stream), steps, warmup)
         by = ls.bytes_per_layer()
         ls.free()
         extra["config1_layer_with_projections_b1"] = {
             "us_per_layer_step": round(ms * 1e3 / 36, 2), "tokens_per_s": round(1e3 / ms, 1), "bytes_per_layer": by,
             "gbs": round(36 * by / (ms * 1e-3) / 1e9, 1)}
-        log(f"[bench] config 1 layer with projections: {ms * 1e3 / 36:.2f} us/layer-step")
+        extra["config1_layer_with_projections_fused_ab_b1"] = {
+            "us_per_layer_step": round(ms_f * 1e3 / 36, 2), "tokens_per_s": round(1e3 / ms_f, 1),
+            "bytes_per_layer": by, "gbs": round(36 * by / (ms_f * 1e-3) / 1e9, 1)}
+        log(f"[bench] config 1 layer with projections: {ms * 1e3 / 36:.2f} us/layer-step; alpha/beta projection "
+            f"fused into the block: {ms_f * 1e3 / 36:.2f}")
         # config 2 as speculative verify steps: nt = 4 new tokens per sequence per step, the previous step's
         # accepted tokens (kr of them) replayed into the committed state first; one S read + write per step
         for nt_v, kr_v in ((4, 2), (4, 4), (8, 4)):

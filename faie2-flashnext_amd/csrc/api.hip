@@ -69,6 +69,20 @@ FN_API int fn_gdn_block_dev(int B, int nkh, int nvh, int dk, int dv, int head_ma
     return fn::gdn_block_launch(p, (hipStream_t) stream);
 }
 
+FN_API int fn_gdn_block_xab_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int gate_act, int ring,
+                                const int32_t *pos, const float *qkv, const float *conv_w, float *conv_ring,
+                                const float *x, int hidden, const uint16_t *w_ab, const float *dt_bias,
+                                const float *ssm_a, float *S, const float *z, const float *norm_w, float eps,
+                                float *out, void *stream) {
+    fn::GdnBlock p{B, nkh, nvh, dk, dv, head_map, gate_act, 1, ring, eps, pos, qkv, conv_w, conv_ring, nullptr,
+                   dt_bias, ssm_a, S, z, norm_w, out};
+    p.x = x;
+    p.wab = w_ab;
+    p.hidden = hidden;
+    if (!w_ab) FN_FAIL("gdn: null pointer");
+    return fn::gdn_block_launch(p, (hipStream_t) stream);
+}
+
 FN_API int fn_gdn_verify_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int gate_act, int nt, int ring,
                              const int32_t *pos, const int32_t *kr, int rnt, const float *rqkv, const float *rab,
                              const float *qkv, const float *conv_w, float *conv_ring, const float *ab,

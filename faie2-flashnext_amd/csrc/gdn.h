@@ -20,6 +20,11 @@ struct GdnBlock {
     const float *z;                     // [B][nt][nvh dv]
     const float *norm_w;                // [dv]
     float *out;                         // [B][nt][nvh dv]
+    // alpha/beta projection fused into the block (nt = 1; ab unused): ab = wab . x, x [B][hidden] fp32,
+    // wab [2 nvh][hidden] BF16 rows (alpha rows then beta rows)
+    const float *x = nullptr;
+    const uint16_t *wab = nullptr;
+    int hidden = 0;
 };
 
 struct GdnCore {

@@ -75,7 +75,13 @@ struct GdnArgs {
     const int32_t *kr;                  // verify: tokens of the previous call to commit first, per sequence
     int rnt;                            // verify: token stride of the replay inputs
     const float *rqkv, *rab;            // verify: the previous call's qkv [B][rnt][C] and ab [B][rnt][2 nvh]
+    const float *x;                     // one-token block with the alpha/beta projection fused: x [B][hidden]
+    const uint16_t *wab;                //   and the BF16 weight [2 nvh][hidden] (null: ab is given)
+    int hidden;
 };
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
 
 // Causal depthwise conv (kernel 4, weights oldest tap first) + SiLU (faie2fn.cu:1392-1395) of one channel.
 // The raw inputs of the three previous positions ride in registers across the token loop (hist[0] oldest),
@@ -145,6 +151,7 @@ k_gdn(const GdnArgs a) {
     __shared__ float vs[DV];                      // conv'd v of the value head
     __shared__ float4 red[WAVES][2][DV / 4];      // per-wave column partials of kv and sq
     __shared__ float nrm[2][3];                   // per-wave sums q.q, k.k, q.k (waves 0, 1)
+    __shared__ float2 abp[WAVES];                 // fused alpha/beta projection: per-wave partial dots
 
     // 1. every input of the first token is requested before the state tile, so nothing waits behind S twice:
     //    conv weights, ring taps and raw inputs (waves 0-3), z and the norm weight (wave 0)
@@ -173,6 +180,30 @@ k_gdn(const GdnArgs a) {
         }
     }
     const bool primary = a.head_map == 0 ? h < a.nkh : (h % (a.nvh / a.nkh)) == 0;
+    // fused alpha/beta projection (one token): this head's two rows of the BF16 weight against the sequence's x,
+    // requested before the state tile so their wait never includes it; thread tid takes elements 4 tid + 2048 k,
+    // the waves' partial dots meet in LDS and are summed in wave order (deterministic)
+    const bool xab = ONE && a.wab != nullptr;
+    if (xab) {
+        const float *xb = a.x + (size_t) b * a.hidden;
+        const uint16_t *wa = a.wab + (size_t) h * a.hidden, *wb = a.wab + (size_t) (a.nvh + h) * a.hidden;
+        float pa = 0.0f, pb = 0.0f;
+        for (int i = 4 * tid; i < a.hidden; i += 4 * THREADS) {
+            const float4 xv = *reinterpret_cast<const float4 *>(xb + i);
+            const uint2 ua = *reinterpret_cast<const uint2 *>(wa + i), ub = *reinterpret_cast<const uint2 *>(wb + i);
+            pa = fmaf(bf16_lo(ua.x), xv.x, pa);
+            pa = fmaf(bf16_hi(ua.x), xv.y, pa);
+            pa = fmaf(bf16_lo(ua.y), xv.z, pa);
+            pa = fmaf(bf16_hi(ua.y), xv.w, pa);
+            pb = fmaf(bf16_lo(ub.x), xv.x, pb);
+            pb = fmaf(bf16_hi(ub.x), xv.y, pb);
+            pb = fmaf(bf16_lo(ub.y), xv.z, pb);
+            pb = fmaf(bf16_hi(ub.y), xv.w, pb);
+        }
+        pa = wave_sum(pa);
+        pb = wave_sum(pb);
+        if (lane == 0) abp[wave] = make_float2(pa, pb);
+    }
 
     // 2. state tile into registers
     float4 s[ROWS_PT];
@@ -208,9 +239,11 @@ k_gdn(const GdnArgs a) {
         nb = abt_[a.nvh + h];                                                                                     \
     } while (0)
     if (FUSED) {
-        const float *ab0 = kr > 0 ? a.rab + (size_t) b * a.rnt * 2 * a.nvh : a.ab + (size_t) b * a.nt * 2 * a.nvh;
-        ga = ab0[h];
-        gb = ab0[a.nvh + h];
+        if (!xab) {
+            const float *ab0 = kr > 0 ? a.rab + (size_t) b * a.rnt * 2 * a.nvh : a.ab + (size_t) b * a.nt * 2 * a.nvh;
+            ga = ab0[h];
+            gb = ab0[a.nvh + h];
+        }
         dtb = a.dt_bias[h];
         ssa = a.ssm_a[h];
         if (!ONE && ntot > 1) GDN_PREFETCH(1);
@@ -274,8 +307,18 @@ k_gdn(const GdnArgs a) {
             vs[tid - DK] = FUSED ? c0.out() : a.v[(bt * a.nvh + h) * DV + (tid - DK)];
         }
 
+        __syncthreads();
         // 4. gates (uniform per head): beta = sigmoid(b), gamma = exp(ssm_a * softplus(a + dt_bias)), softplus
         //    the identity above 20 (faie2fn.cu:1407-1410)
+        if (xab) {
+            ga = abp[0].x;
+            gb = abp[0].y;
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) {
+                ga += abp[w].x;
+                gb += abp[w].y;
+            }
+        }
         float beta, gamma;
         if (FUSED) {
             beta = sigmoidf_(gb);
@@ -286,7 +329,6 @@ k_gdn(const GdnArgs a) {
             beta = a.beta[bt * a.nvh + h];
             gamma = expf(a.g[bt * a.nvh + h]);
         }
-        __syncthreads();
 
         // L2 factors x * rsqrt(sum x^2 + 1e-6) (faie2fn.cu:1399-1402); the core takes q, k as given
         float rq = 1.0f, rk = 1.0f;
@@ -415,14 +457,19 @@ int gdn_block_launch(const GdnBlock &p, hipStream_t st) {
     if (p.gate_act != 0 && p.gate_act != 1) FN_FAIL("gdn: gate_act must be 0 (sigmoid) or 1 (silu)");
     if (p.ring < 4 || (p.ring & (p.ring - 1))) FN_FAIL("gdn: ring must be a power of two >= 4");
     if (p.nt > p.ring - 3) FN_FAIL("gdn: nt must be <= ring - 3");
-    if (!p.pos || !p.qkv || !p.conv_w || !p.conv_ring || !p.ab || !p.dt_bias || !p.ssm_a || !p.S || !p.z ||
-        !p.norm_w || !p.out)
+    const bool xab = p.wab != nullptr;
+    if (!p.pos || !p.qkv || !p.conv_w || !p.conv_ring || (!xab && !p.ab) || !p.dt_bias || !p.ssm_a || !p.S || !p.z ||
+        !p.norm_w || !p.out || (xab && !p.x))
         FN_FAIL("gdn: null pointer");
+    if (xab && p.nt != 1) FN_FAIL("gdn: the fused alpha/beta projection takes one token (nt = 1)");
+    if (xab && (p.hidden < 4 || p.hidden % 4)) FN_FAIL("gdn: hidden must be a positive multiple of 4");
+    if (xab && ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.wab)) & 15))
+        FN_FAIL("gdn: x and w_ab must be 16-byte aligned");
     GdnArgs a{};
     a.B = p.B; a.nkh = p.nkh; a.nvh = p.nvh; a.nt = p.nt; a.ring = p.ring; a.head_map = p.head_map;
     a.gate_act = p.gate_act; a.eps = p.eps; a.pos = p.pos; a.qkv = p.qkv; a.conv_w = p.conv_w;
     a.ring_buf = p.conv_ring; a.ab = p.ab; a.dt_bias = p.dt_bias; a.ssm_a = p.ssm_a; a.S = p.S; a.z = p.z;
-    a.norm_w = p.norm_w; a.out = p.out;
+    a.norm_w = p.norm_w; a.out = p.out; a.x = p.x; a.wab = p.wab; a.hidden = p.hidden;
     if (p.nt == 1) hipLaunchKernelGGL(k_gdn<3>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
     else hipLaunchKernelGGL(k_gdn<1>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
     FN_CK(hipGetLastError());

@@ -36,7 +36,7 @@ SYMBOLS = (
     "fn_path_init", "fn_path_buffer", "fn_path_step",
     "fn_attn_qsa_dev", "fn_attn_qsa_work_bytes", "fn_ix_blocks_dev", "fn_test_attn_qsa",
     "fn_gemv_packed_bytes", "fn_gemv_pack_dev", "fn_dequant_dev", "fn_gemv_work_bytes", "fn_gemv_dev",
-    "fn_gdn_verify_dev", "fn_advance_by_dev",
+    "fn_gdn_verify_dev", "fn_advance_by_dev", "fn_gdn_block_xab_dev",
 )
 
 # GGUF type ids of the weight formats this library reads (engine/faie2fn.cu:78-81), and (values, bytes) per block
@@ -100,6 +100,7 @@ class FN:
         d.fn_gdn_block_dev.argtypes = [i] * 9 + [VP] * 10 + [C.c_float, VP, VP]
         d.fn_gdn_core_dev.argtypes = [i] * 7 + [VP] * 7 + [VP]
         d.fn_gdn_verify_dev.argtypes = [i] * 9 + [VP, VP, i] + [VP] * 11 + [C.c_float, VP, VP]
+        d.fn_gdn_block_xab_dev.argtypes = [i] * 8 + [VP] * 5 + [i] + [VP] * 6 + [C.c_float, VP, VP]
         d.fn_advance_by_dev.argtypes = [VP, VP, i, VP]
         d.fn_attn_dev.argtypes = ([i] * 5 + [C.c_float, C.c_float, i, i] + [VP] * 8 + [i, VP, C.c_size_t, VP, VP])
         d.fn_attn_work_bytes.restype = C.c_size_t
@@ -255,6 +256,14 @@ class FN:
                       out, stream=0, dk=128, dv=128, head_map=0, gate_act=0, eps=1e-6):
         self.check(self.d.fn_gdn_block_dev(B, nkh, nvh, dk, dv, head_map, gate_act, nt, ring, pos, qkv, conv_w,
                                            conv_ring, ab, dt_bias, ssm_a, S, z, norm_w, float(eps), out, stream))
+
+    def gdn_block_xab_dev(self, B, nkh, nvh, ring, pos, qkv, conv_w, conv_ring, x, hidden, w_ab, dt_bias, ssm_a, S,
+                          z, norm_w, out, stream=0, dk=128, dv=128, head_map=0, gate_act=0, eps=1e-6):
+        """One decode token of the fused block with the alpha/beta projection inside: ab = w_ab . x (w_ab BF16
+        [2 nvh][hidden], x fp32 [B][hidden], both device pointers) instead of a precomputed ab."""
+        self.check(self.d.fn_gdn_block_xab_dev(B, nkh, nvh, dk, dv, head_map, gate_act, ring, pos, qkv, conv_w,
+                                               conv_ring, x, hidden, w_ab, dt_bias, ssm_a, S, z, norm_w, float(eps),
+                                               out, stream))
 
     def gdn_verify_dev(self, B, nkh, nvh, nt, ring, pos, kr, rnt, rqkv, rab, qkv, conv_w, conv_ring, ab, dt_bias,
                        ssm_a, S, z, norm_w, out, stream=0, dk=128, dv=128, head_map=0, gate_act=0, eps=1e-6):

@@ -116,6 +116,17 @@ int fn_gdn_block_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int 
                      const float *dt_bias, const float *ssm_a, float *S, const float *z, const float *norm_w,
                      float eps, float *out, void *stream);
 
+/* One decode token of the fused DeltaNet block with the alpha/beta projection fused in: replaces the ab GEMV and
+ * the k_gdn launch that follows it (faie2fn.cu:2388-2389) with one launch.  As fn_gdn_block_dev with nt = 1, except
+ * that ab is computed inside: ab[b][j] = sum_i w_ab[j][i] * x[b][i] in fp32 (BF16 weights widened exactly),
+ *   x [B][hidden] device fp32 (the layer's input, the x the reference's gemv(L.ab, d.x, ...) reads),
+ *   w_ab [2 nvh][hidden] device BF16 rows as GGUF stores them (alpha rows 0..nvh-1, then beta rows), the weight
+ *   whose GEMV gives ab; hidden a positive multiple of 4, x and w_ab 16-byte aligned. */
+int fn_gdn_block_xab_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int gate_act, int ring,
+                         const int32_t *pos, const float *qkv, const float *conv_w, float *conv_ring, const float *x,
+                         int hidden, const uint16_t *w_ab, const float *dt_bias, const float *ssm_a, float *S,
+                         const float *z, const float *norm_w, float eps, float *out, void *stream);
+
 /* A verify step of the fused DeltaNet block with deferred commit (speculative decoding; the reference's engine
  * family verifies drafts by replay-commit, reference DESIGN.md:287-293, and FN's k_gdn already takes nt <= 8
  * tokens of one sequence, faie2fn.cu:1390).  For sequence b, pos[b] is the position of the first new token and

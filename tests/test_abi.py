@@ -156,3 +156,22 @@ def test_verify_validates_before_device_work(fnlib):
     assert d.fn_gdn_verify_dev(1, 16, 32, 128, 128, 0, 0, 1, 4, 1, 1, 1, None, None, *p[:9], 1e-6, 1, None) == -1
     assert b"null pointer" in d.fn_error()
     assert d.fn_advance_by_dev(None, None, 1, None) == -1
+
+
+def test_block_xab_validates_before_device_work(fnlib):
+    """fn_gdn_block_xab_dev rejects a missing weight or input, a hidden size that is not a positive multiple of 4 and
+    misaligned x / w_ab before any launch (the pointers are stand-ins: validation fails before any is used)."""
+    d = fnlib.d
+    assert len(d.fn_gdn_block_xab_dev.argtypes) == 23
+    a = 4096  # aligned stand-in address
+
+    def call(x=a, hidden=2048, w=a):
+        return d.fn_gdn_block_xab_dev(1, 16, 32, 128, 128, 0, 0, 4, a, a, a, a, x, hidden, w, a, a, a, a, a, 1e-6, a,
+                                      None)
+
+    assert call(w=None) == -1 and b"null pointer" in d.fn_error()
+    assert call(x=None) == -1 and b"null pointer" in d.fn_error()
+    assert call(hidden=2046) == -1 and b"multiple of 4" in d.fn_error()
+    assert call(hidden=0) == -1 and b"multiple of 4" in d.fn_error()
+    assert call(x=a + 4) == -1 and b"16-byte aligned" in d.fn_error()
+    assert call(w=a + 8) == -1 and b"16-byte aligned" in d.fn_error()

@@ -135,3 +135,53 @@ def test_block_batch64_subset(fnlib):
                                lay.norm_w, 16, 32)
         e = (oracle.relerr(out[pick], ref), oracle.relerr(S_gpu[pick], S_ref), oracle.relerr(c_gpu[pick], c_ref))
         assert max(e) <= TOL, (step, e)
+
+
+def _bf16(a):
+    """float32 -> BF16 bits, round to nearest even."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _bf16_f64(r):
+    return (r.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("B,hidden", [(3, 2048), (2, 4), (2, 2052), (2, 6144), (64, 2048)])
+def test_block_xab_device(fnlib, B, hidden):
+    """fn_gdn_block_xab_dev (alpha/beta projection fused into the block): 5 decode steps, each against the oracle
+    fed ab = w_ab . x in float64 over the same BF16 weights; hidden sizes one thread's share (4), not a multiple of
+    the workgroup's stride (2052) and three strides (6144); B = 64 with the oracle on a subset."""
+    import hiprt
+
+    _say(f"gdn block with fused alpha/beta projection, B={B}, hidden={hidden}, 5 steps")
+    nvh, ring = 32, 4
+    lay = fn_synth.BlockLayer(B=B, config=1, layer=7)
+    C = lay.C
+    rng = np.random.default_rng(hidden + B)
+    wab = _bf16(rng.normal(0.0, 1.0 / np.sqrt(hidden), (2 * nvh, hidden)))
+    wab64 = _bf16_f64(wab)
+    pick = list(range(B)) if B <= 4 else [0, 31, 63]
+    pos = hiprt.Buf.like(np.zeros(B, np.int32))
+    d_ring, d_S = hiprt.Buf.like(np.zeros((B, ring, C), np.float32)), hiprt.Buf.like(lay.S0)
+    d_w, d_dt, d_sa, d_nw = (hiprt.Buf.like(x) for x in (lay.conv_w, lay.dt_bias, lay.ssm_a, lay.norm_w))
+    d_wab = hiprt.Buf.like(wab)
+    d_x, d_qkv, d_z = hiprt.Buf.empty((B, hidden)), hiprt.Buf.empty((B, 1, C)), hiprt.Buf.empty((B, 1, nvh * 128))
+    out = hiprt.Buf.empty((B, 1, nvh * 128))
+    S_ref = lay.S0[pick].astype(np.float64)
+    c_ref = np.zeros((len(pick), 3, C))
+    for step in range(5):
+        qkv, _, z = lay.step()
+        x = rng.standard_normal((B, hidden)).astype(np.float32)
+        d_qkv.upload(qkv), d_z.upload(z), d_x.upload(x)
+        fnlib.gdn_block_xab_dev(B, 16, nvh, ring, pos.ptr, d_qkv.ptr, d_w.ptr, d_ring.ptr, d_x.ptr, hidden, d_wab.ptr,
+                                d_dt.ptr, d_sa.ptr, d_S.ptr, d_z.ptr, d_nw.ptr, out.ptr, None)
+        fnlib.advance_dev(pos.ptr, B, 1, None)
+        hiprt.sync()
+        ab = (x[pick].astype(np.float64) @ wab64.T)[:, None, :]
+        ref = oracle.gdn_block(qkv[pick], lay.conv_w, c_ref, ab, lay.dt_bias, lay.ssm_a, S_ref, z[pick], lay.norm_w,
+                               16, 32)
+        e = (oracle.relerr(out.download()[pick], ref), oracle.relerr(d_S.download()[pick], S_ref))
+        assert max(e) <= TOL, (step, e)
+    for bf in (pos, d_ring, d_S, d_w, d_dt, d_sa, d_nw, d_wab, d_x, d_qkv, d_z, out):
+        bf.free()
