@@ -575,12 +575,6 @@ __device__ __forceinline__ void mt_rescale(v4f (&o)[NRW][16], const float (&corr
     }
 }
 
-// scores, softmax step and P.V of one block, in sequence
-template <int NRW>
-__device__ __forceinline__ void mt_block(const float4 (&k)[16], const float4 (&v)[16], int kb, const float4 *qs,
-                                         v4f (&o)[NRW][16], float (&m)[NRW], float (&l)[NRW], const int (&lim)[NRW],
-                                         int lane);
-
 // o += V^T P^T for one block
 template <int NRW>
 __device__ __forceinline__ void mt_pv(const float4 (&v)[16], const v4f (&p)[NRW], v4f (&o)[NRW][16]) {
@@ -597,6 +591,7 @@ __device__ __forceinline__ void mt_pv(const float4 (&v)[16], const v4f (&p)[NRW]
             }
 }
 
+// scores, softmax step and P.V of one block, in sequence
 template <int NRW>
 __device__ __forceinline__ void mt_block(const float4 (&k)[16], const float4 (&v)[16], int kb, const float4 *qs,
                                          v4f (&o)[NRW][16], float (&m)[NRW], float (&l)[NRW], const int (&lim)[NRW],
