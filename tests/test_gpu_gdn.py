@@ -147,14 +147,17 @@ def _bf16_f64(r):
     return (r.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-@pytest.mark.parametrize("B,hidden", [(3, 2048), (2, 4), (2, 2052), (2, 6144), (64, 2048)])
-def test_block_xab_device(fnlib, B, hidden):
+@pytest.mark.parametrize("B,hidden,head_map,gate_act", [(3, 2048, 0, 0), (2, 4, 0, 0), (2, 2052, 0, 0), (2, 6144, 0, 0),
+                                                       (64, 2048, 0, 0), (3, 2048, 1, 1)])
+def test_block_xab_device(fnlib, B, hidden, head_map, gate_act):
     """fn_gdn_block_xab_dev (alpha/beta projection fused into the block): 5 decode steps, each against the oracle
     fed ab = w_ab . x in float64 over the same BF16 weights; hidden sizes one thread's share (4), not a multiple of
-    the workgroup's stride (2052) and three strides (6144); B = 64 with the oracle on a subset."""
+    the workgroup's stride (2052) and three strides (6144); B = 64 with the oracle on a subset; the grouped head map
+    with the SiLU gate."""
     import hiprt
 
-    _say(f"gdn block with fused alpha/beta projection, B={B}, hidden={hidden}, 5 steps")
+    _say(f"gdn block with fused alpha/beta projection, B={B}, hidden={hidden}, head_map={head_map}, "
+         f"gate_act={gate_act}, 5 steps")
     nvh, ring = 32, 4
     lay = fn_synth.BlockLayer(B=B, config=1, layer=7)
     C = lay.C
@@ -175,12 +178,13 @@ def test_block_xab_device(fnlib, B, hidden):
         x = rng.standard_normal((B, hidden)).astype(np.float32)
         d_qkv.upload(qkv), d_z.upload(z), d_x.upload(x)
         fnlib.gdn_block_xab_dev(B, 16, nvh, ring, pos.ptr, d_qkv.ptr, d_w.ptr, d_ring.ptr, d_x.ptr, hidden, d_wab.ptr,
-                                d_dt.ptr, d_sa.ptr, d_S.ptr, d_z.ptr, d_nw.ptr, out.ptr, None)
+                                d_dt.ptr, d_sa.ptr, d_S.ptr, d_z.ptr, d_nw.ptr, out.ptr, None, head_map=head_map,
+                                gate_act=gate_act)
         fnlib.advance_dev(pos.ptr, B, 1, None)
         hiprt.sync()
         ab = (x[pick].astype(np.float64) @ wab64.T)[:, None, :]
         ref = oracle.gdn_block(qkv[pick], lay.conv_w, c_ref, ab, lay.dt_bias, lay.ssm_a, S_ref, z[pick], lay.norm_w,
-                               16, 32)
+                               16, 32, head_map=head_map, gate_act=gate_act)
         e = (oracle.relerr(out.download()[pick], ref), oracle.relerr(d_S.download()[pick], S_ref))
         assert max(e) <= TOL, (step, e)
     for bf in (pos, d_ring, d_S, d_w, d_dt, d_sa, d_nw, d_wab, d_x, d_qkv, d_z, out):
