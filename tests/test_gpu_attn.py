@@ -124,6 +124,26 @@ def test_attn_multi_token_growing_scores(fnlib, nq, nt):
     _check(fnlib, case)
 
 
+@pytest.mark.parametrize("seed", range(20))
+def test_attn_random_shapes(fnlib, seed):
+    """Seeded random shapes across both split kernels: 1, 2 or 4 kv heads, groups of 4, 8 or 12 query heads, 1 to 10
+    new tokens (up to 120 query rows per kv head), 1 to 3 sequences at independent positions (0 and the end of the
+    cache included), split counts from automatic to more splits than tiles."""
+    rng = np.random.default_rng(7000 + seed)
+    nkv = int(rng.choice([1, 2, 4]))
+    grp = int(rng.choice([4, 8, 12]))
+    nt = int(rng.integers(1, 11))
+    B = int(rng.integers(1, 4))
+    max_ctx = 64 * int(rng.integers(1, 24))
+    if max_ctx < nt:
+        max_ctx = 64
+    choices = [0, max_ctx - nt] + [int(v) for v in rng.integers(0, max_ctx - nt + 1, size=3)]
+    pos = [int(rng.choice(choices)) for _ in range(B)]
+    nsplit = int(rng.choice([0, 1, 3, 7, 32]))
+    _say(f"attn random seed={seed}: nq={nkv * grp} nkv={nkv} nt={nt} pos={pos} max_ctx={max_ctx} nsplit={nsplit}")
+    _check(fnlib, _mt_case(B, nkv * grp, nkv, nt, pos, max_ctx, seed=seed), nsplit=nsplit)
+
+
 def test_attn_reference_group_12(fnlib):
     """The reference model's own head shape: 24 query heads over 2 kv heads (faie2fn.cu:47-48)."""
     _say("attn nq=24 nkv=2")
