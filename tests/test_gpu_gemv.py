@@ -145,6 +145,25 @@ def test_gemv_chunked_x_matches_one_stage(fnlib, name, rows, cols, nt, wpc):
     assert oracle.relerr(y3, oracle.gemv(t, raw, rows, cols, x)) <= TOL
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_gemv_random_shapes(fnlib, seed):
+    """Seeded random format, rows (1 to 5000, ragged), columns (a multiple of the format's block, up to 8192: x
+    larger than the LDS at high nt goes through the chunked kernel) and nt (1 to 8), against the oracle."""
+    rng = np.random.default_rng(9100 + seed)
+    name = str(rng.choice(list(TYPES)))
+    t = TYPES[name]
+    qk = oracle.qblock(t)[0]
+    blk = max(qk, 32)
+    rows = int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 5001))]))
+    cols = blk * int(rng.integers(1, 8192 // blk + 1))
+    nt = int(rng.integers(1, 9))
+    _say(f"gemv random seed={seed}: {name} {rows}x{cols} nt={nt} plan={fnlib.gemv_plan(t, rows, cols)}")
+    raw = random_finite(t, rows, cols, rng)
+    x = rng.standard_normal((nt, cols)).astype(np.float32)
+    y = fnlib.gemv(t, raw, rows, cols, x)
+    assert oracle.relerr(y, oracle.gemv(t, raw, rows, cols, x)) <= TOL
+
+
 def test_gemv_tokens_independent(fnlib):
     """Token t of an nt-token call equals a one-token call on x[t] (the split order does not depend on nt)."""
     t, rows, cols = 8, 700, 2048
