@@ -361,22 +361,7 @@ __device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// max / sum of the values of lanes l and l ^ 16, and of l and l ^ 32, through v_permlane16_swap / v_permlane32_swap
-// (VALU lane swaps, no LDS round trip): swapping two copies of x leaves the pair {x[l & ~16], x[l | 16]} (resp. 32)
-// in the same order in both lanes, so both get the same bits.  Issued as inline asm: this compiler's
-// __builtin_amdgcn_permlane16_swap / 32_swap lowering folds an add or max of the two results into one result
-// doubled.  The s_nop 1 covers the wait states a VALU write needs before a permlane reads it.  (Not volatile: a pure
-// function of its inputs, free to move, so it does not order the surrounding code.)
-__device__ __forceinline__ float2 swap16(float x) {
-    float a = x, b = x;
-    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return make_float2(a, b);
-}
-__device__ __forceinline__ float2 swap32(float x) {
-    float a = x, b = x;
-    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return make_float2(a, b);
-}
+// max / sum over the lanes l, l ^ 16, l ^ 32, l ^ 48 (swap16 / swap32: VALU lane swaps, the same bits in every lane)
 __device__ __forceinline__ float max_x16_x32(float x) {
     float2 r = swap16(x);
     r = swap32(fmaxf(r.x, r.y));

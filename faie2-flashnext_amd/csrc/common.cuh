@@ -102,4 +102,63 @@ __device__ __forceinline__ void st_nt(float4 *p, float4 x) {
     __builtin_nontemporal_store(v, reinterpret_cast<v4f_ *>(p));
 }
 
+// Raw buffer access: a descriptor over [p, p + bytes) in four SGPRs, addressed per access by a VGPR byte offset and
+// an SGPR one.  A long-lived per-lane address is then one VGPR, where a pointer plus an index is a 64-bit VGPR pair
+// that the compiler hoists out of a loop (and spills under pressure); and a wave-uniform address stays a vector load
+// (counted in vmcnt), never a scalar one (lgkmcnt, which every LDS wait also drains).  Accesses past `bytes` read 0
+// and drop writes (the hardware range check).  aux 2 sets the nontemporal bit.
+typedef __amdgpu_buffer_rsrc_t brsrc;
+__device__ __forceinline__ brsrc buf(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short) 0, (int) bytes, 0x00020000);
+}
+__device__ __forceinline__ float bld(brsrc r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int) voff, (int) soff, 0));
+}
+// (whole-vector bit casts: this compiler's __builtin_bit_cast of a single ext_vector element reads element 0)
+typedef unsigned v4u_ __attribute__((ext_vector_type(4)));
+template <int AUX = 0> __device__ __forceinline__ float4 bld4(brsrc r, uint32_t voff, uint32_t soff) {
+    const v4f_ v = __builtin_bit_cast(v4f_, __builtin_amdgcn_raw_buffer_load_b128(r, (int) voff, (int) soff, AUX));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void bst(brsrc r, uint32_t voff, uint32_t soff, float x) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), r, (int) voff, (int) soff, 0);
+}
+template <int AUX = 0> __device__ __forceinline__ void bst4(brsrc r, uint32_t voff, uint32_t soff, float4 x) {
+    const v4f_ v = {x.x, x.y, x.z, x.w};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_, v), r, (int) voff, (int) soff, AUX);
+}
+
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for every outstanding global load and store
+// of the wave (s_waitcnt vmcnt(0)); this one waits for the wave's LDS and scalar-memory operations (lgkmcnt(0))
+// only, so global loads issued ahead of it stay in flight across it.  For LDS exchanges: global memory written
+// before it is not ordered for the other waves.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The values of lanes l & ~16 and l | 16 (swap16), or l & ~32 and l | 32 (swap32), through v_permlane16_swap /
+// v_permlane32_swap (VALU lane swaps, no LDS round trip): swapping two copies of x leaves the pair in the same
+// order in both lanes, so r.x + r.y or max(r.x, r.y) gives every lane of the pair the same bits, and r.x + r.y
+// equals x + (x of lane l ^ 32) bit for bit.  Inline asm: this compiler's __builtin_amdgcn_permlane16_swap /
+// 32_swap lowering folds an add or max of the two results into one result doubled.  The s_nop 1 covers the wait
+// states a VALU write needs before a permlane reads it.  (Not volatile: a pure function of its input, free to move,
+// so it does not order the surrounding code.)
+__device__ __forceinline__ float2 swap16(float x) {
+    float a = x, b = x;
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return make_float2(a, b);
+}
+__device__ __forceinline__ float2 swap32(float x) {
+    float a = x, b = x;
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return make_float2(a, b);
+}
+// x + x of lane l ^ 32, the same bits in both lanes of the pair
+__device__ __forceinline__ float add_xor32(float x) {
+    const float2 r = swap32(x);
+    return r.x + r.y;
+}
+
 }  // namespace fn

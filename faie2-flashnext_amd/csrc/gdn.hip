@@ -13,8 +13,11 @@
 //     XCD-contiguous head order were all slower).
 //   * One read pass computes both reductions the step needs, kv = S^T k and sq = S^T q (old S), because
 //       S' = g S + k d^T  with  d = beta (v - g kv)    =>    S'^T q = g sq + (k.q) d.
-//     The column partials of the 16 row groups are folded with a lane^32 permute (2 groups per wave) and
+//     The column partials of the 16 row groups are folded with a v_permlane32_swap (2 groups per wave) and
 //     one 4 KiB LDS exchange across the eight waves; there is no serial 128-long FMA chain.
+//   * Per-lane global access goes through raw buffer descriptors (one VGPR offset per address) and the barriers
+//     order LDS only, so a multi-token call keeps the next token's loads in flight across a token (no barrier and
+//     no spilled-address reload drains them): the verify step at B = 64, 4 new + 2 replayed tokens, 114 -> 94 us.
 //   * q/k are not normalised before the pass: the L2 factors are applied to the 4 per-column sums, so the
 //     norm reductions (wave DPP sums) overlap the S loads instead of sitting in front of them.
 //   * The causal conv state is a ring of R slots per sequence, R a power of two >= nt + 3: the raw input of
@@ -48,6 +51,13 @@ namespace {
 #define GDN_VERIFY_WPE 4
 #endif
 
+#ifndef GDN_ONE_LDS_PAD
+// k_gdn<3> (the decode step) fits in 78 VGPRs, which would let three workgroups (six waves per SIMD) share a CU;
+// two interleave their state streams better (B = 64: 49.4 against 50.8 us per layer-step on MI355X).  The launch
+// reserves this much dynamic LDS, unused, so that three do not fit in the CU's 160 KiB and two do.
+#define GDN_ONE_LDS_PAD 57344
+#endif
+
 constexpr int DK = 128, DV = 128;
 constexpr int THREADS = GDN_THREADS;       // 256 or 512
 constexpr int WAVES = THREADS / 64;
@@ -55,10 +65,13 @@ constexpr int ROWS_PT = DK * 32 / THREADS;  // state rows per thread (32 threads
 constexpr int RSTEP = THREADS / 32;         // row groups: thread row group rg owns rows rg, rg + RSTEP, ...
 static_assert(THREADS == 256 || THREADS == 512 || THREADS == 1024, "one state tile per 4, 8 or 16 waves");
 
-__device__ __forceinline__ float4 ld_state(const float4 *p) { return GDN_NT ? ld_nt(p) : *p; }
-__device__ __forceinline__ void st_state(float4 *p, float4 v) {
-    if (GDN_NT_ST) st_nt(p, v);
-    else *p = v;
+// the thread's float4 of state register r: byte offset so (row rg, columns 4cg..) in the head's tile, plus r row
+// blocks of RSTEP rows
+__device__ __forceinline__ float4 ld_state(brsrc S, uint32_t so, int r) {
+    return bld4<GDN_NT ? 2 : 0>(S, so, (uint32_t) r * RSTEP * DV * 4);
+}
+__device__ __forceinline__ void st_state(brsrc S, uint32_t so, int r, float4 v) {
+    bst4<GDN_NT_ST ? 2 : 0>(S, so, (uint32_t) r * RSTEP * DV * 4, v);
 }
 
 struct GdnArgs {
@@ -105,20 +118,28 @@ struct ConvChan {
     }
 };
 
-__device__ __forceinline__ void conv_load(ConvChan &cc, const GdnArgs &a, const float *ring_b, const float *x_b, int C,
-                                          int c, int pos) {
-    cc.w = reinterpret_cast<const float4 *>(a.conv_w)[c];
+// The ring of one sequence is a buffer of a.ring rows of C channels; a channel is the lane's byte offset oc = 4 c,
+// the slot of position p the row offset slot_off(p).
+__device__ __forceinline__ uint32_t slot_off(const GdnArgs &a, int C, int p) {
+    return (uint32_t) (p & (a.ring - 1)) * C * 4;
+}
+
+// x0: the raw input row of the call's first token
+__device__ __forceinline__ void conv_load(ConvChan &cc, const GdnArgs &a, brsrc ring, brsrc x0, int C, uint32_t oc,
+                                          int pos) {
+    cc.w = bld4(buf(a.conv_w, C * 16), 4 * oc, 0);
 #pragma unroll
-    for (int j = 0; j < 3; ++j) cc.hist[j] = ring_b[(size_t) ((pos - 3 + j) & (a.ring - 1)) * C + c];
-    cc.x = x_b[c];
+    for (int j = 0; j < 3; ++j) cc.hist[j] = bld(ring, oc, slot_off(a, C, pos - 3 + j));
+    cc.x = bld(x0, oc, 0);
 }
 
 // after the last token: raw inputs of this call's own last (up to) three positions into their ring slots
-__device__ __forceinline__ void conv_store(const ConvChan &cc, const GdnArgs &a, float *ring_b, int C, int c, int pos) {
+__device__ __forceinline__ void conv_store(const ConvChan &cc, const GdnArgs &a, brsrc ring, int C, uint32_t oc,
+                                           int pos) {
     const int last = pos + a.nt - 1;
-    ring_b[(size_t) (last & (a.ring - 1)) * C + c] = cc.x;
-    if (a.nt >= 2) ring_b[(size_t) ((last - 1) & (a.ring - 1)) * C + c] = cc.hist[2];
-    if (a.nt >= 3) ring_b[(size_t) ((last - 2) & (a.ring - 1)) * C + c] = cc.hist[1];
+    bst(ring, oc, slot_off(a, C, last), cc.x);
+    if (a.nt >= 2) bst(ring, oc, slot_off(a, C, last - 1), cc.hist[2]);
+    if (a.nt >= 3) bst(ring, oc, slot_off(a, C, last - 2), cc.hist[1]);
 }
 
 // MODE 0: the bare core; 1: the fused block (every token committed); 3: the fused block for exactly one token (the
@@ -129,11 +150,11 @@ __device__ __forceinline__ void conv_store(const ConvChan &cc, const GdnArgs &a,
 // mid-loop, once token u = n has been shifted in (n >= 1 tokens processed, the last at position end - 1): the raw
 // inputs of positions end-3 .. end-1 are hist[0..2]; write the slots of the ones this call processed (the last
 // min(n, 3))
-__device__ __forceinline__ void conv_store_hist(const ConvChan &cc, const GdnArgs &a, float *ring_b, int C, int c, int end,
-                                                int n) {
-    ring_b[(size_t) ((end - 1) & (a.ring - 1)) * C + c] = cc.hist[2];
-    if (n >= 2) ring_b[(size_t) ((end - 2) & (a.ring - 1)) * C + c] = cc.hist[1];
-    if (n >= 3) ring_b[(size_t) ((end - 3) & (a.ring - 1)) * C + c] = cc.hist[0];
+__device__ __forceinline__ void conv_store_hist(const ConvChan &cc, const GdnArgs &a, brsrc ring, int C, uint32_t oc,
+                                                int end, int n) {
+    bst(ring, oc, slot_off(a, C, end - 1), cc.hist[2]);
+    if (n >= 2) bst(ring, oc, slot_off(a, C, end - 2), cc.hist[1]);
+    if (n >= 3) bst(ring, oc, slot_off(a, C, end - 3), cc.hist[0]);
 }
 
 template <int MODE>
@@ -161,22 +182,21 @@ k_gdn(const GdnArgs a) {
     const int pos = FUSED ? a.pos[b] - kr : 0;  // position of the first token this call processes
     const float *x_b = a.qkv + (size_t) b * a.nt * C;
     const float *rx_b = VERIFY ? a.rqkv + (size_t) b * a.rnt * C : x_b;
-    float *ring_b = a.ring_buf + (size_t) b * a.ring * C;
-    const int cq = kh * DK + tid, ck = a.nkh * DK + kh * DK + tid, cv = 2 * a.nkh * DK + h * DV + (tid - DK);
+    const brsrc ring = buf(a.ring_buf + (size_t) b * a.ring * C, a.ring * C * 4);
+    // byte offsets of this thread's channels in a row of C: c0 carries q (waves 0-1) or v (waves 2-3), c1 carries k;
+    // of its 4 columns in a row of DV (z, norm weight, output)
+    const uint32_t o0 = 4u * (qk_thr ? kh * DK + tid : 2 * a.nkh * DK + h * DV + (tid - DK));
+    const uint32_t o1 = 4u * (a.nkh * DK + kh * DK + tid);
+    const uint32_t oz = 16u * cg;
     ConvChan c0{}, c1{};
     float4 z4 = f4(0.0f), w4 = f4(0.0f);
     if (FUSED) {
-        const float *x0 = kr > 0 ? rx_b : x_b;  // raw input of the first token
-        if (qk_thr) {
-            conv_load(c0, a, ring_b, x0, C, cq, pos);
-            conv_load(c1, a, ring_b, x0, C, ck, pos);
-        } else if (v_thr) {
-            conv_load(c0, a, ring_b, x0, C, cv, pos);
-        }
+        const brsrc x0 = buf(kr > 0 ? rx_b : x_b, C * 4);  // raw input row of the first token
+        if (qk_thr || v_thr) conv_load(c0, a, ring, x0, C, o0, pos);
+        if (qk_thr) conv_load(c1, a, ring, x0, C, o1, pos);
         if (wave == 0 && lane < 32) {
-            if (kr == 0)
-                z4 = *reinterpret_cast<const float4 *>(a.z + (size_t) b * a.nt * a.nvh * DV + (size_t) h * DV + cg * 4);
-            w4 = reinterpret_cast<const float4 *>(a.norm_w)[cg];
+            if (kr == 0) z4 = bld4(buf(a.z + (size_t) b * a.nt * a.nvh * DV + (size_t) h * DV, DV * 4), oz, 0);
+            w4 = bld4(buf(a.norm_w, DV * 4), oz, 0);
         }
     }
     const bool primary = a.head_map == 0 ? h < a.nkh : (h % (a.nvh / a.nkh)) == 0;
@@ -207,15 +227,18 @@ k_gdn(const GdnArgs a) {
 
     // 2. state tile into registers
     float4 s[ROWS_PT];
-    float4 *Sh = reinterpret_cast<float4 *>(a.S + (size_t) bh * DK * DV);
+    const brsrc Sb = buf(a.S + (size_t) bh * DK * DV, DK * DV * 4);
+    const uint32_t so = 16u * (rg * (DV / 4) + cg);  // the thread's float4 of row rg
 #pragma unroll
-    for (int r = 0; r < ROWS_PT; ++r) s[r] = ld_state(&Sh[(rg + RSTEP * r) * (DV / 4) + cg]);
+    for (int r = 0; r < ROWS_PT; ++r) s[r] = ld_state(Sb, so, r);
 
     const float scale = 0.08838834764831845f;  // 1/sqrt(128), faie2fn.cu:1352
 
     // Inputs of token u of this call: its raw conv channels, z (wave 0) and alpha/beta logits.  The next token's are
     // requested one iteration ahead, so a multi-token call (verify, prefill) does not wait a memory round trip per
-    // token.
+    // token: the loop's barriers order LDS only (lds_barrier), every one of these is a vector (buffer) load, and no
+    // per-lane address is a 64-bit pair the compiler could keep across the loop and spill (a scratch reload waits
+    // for every load issued before it, the prefetch included).
     float ga = 0.0f, gb = 0.0f, dtb = 0.0f, ssa = 0.0f;  // this token's alpha, beta logits; the head's gate params
     float nx0 = 0.0f, nx1 = 0.0f, na = 0.0f, nb = 0.0f;  // next token's raw channels and logits
     float4 nz = f4(0.0f);
@@ -226,17 +249,13 @@ k_gdn(const GdnArgs a) {
         const float *xt_ = rp_ ? rx_b + (size_t) u_ * C : x_b + (size_t) (u_ - kr) * C;                           \
         const float *abt_ = rp_ ? a.rab + ((size_t) b * a.rnt + u_) * 2 * a.nvh                                  \
                                 : a.ab + ((size_t) b * a.nt + (u_ - kr)) * 2 * a.nvh;                             \
-        if (qk_thr) {                                                                                             \
-            nx0 = xt_[cq];                                                                                        \
-            nx1 = xt_[ck];                                                                                        \
-        } else if (v_thr) {                                                                                       \
-            nx0 = xt_[cv];                                                                                        \
-        }                                                                                                         \
+        const brsrc xr_ = buf(xt_, C * 4), abr_ = buf(abt_, 2 * a.nvh * 4);                                     \
+        if (qk_thr || v_thr) nx0 = bld(xr_, o0, 0);                                                              \
+        if (qk_thr) nx1 = bld(xr_, o1, 0);                                                                        \
         if (wave == 0 && lane < 32 && !rp_)                                                                       \
-            nz = *reinterpret_cast<const float4 *>(a.z + ((size_t) b * a.nt + (u_ - kr)) * a.nvh * DV +          \
-                                                   (size_t) h * DV + cg * 4);                                     \
-        na = abt_[h];                                                                                             \
-        nb = abt_[a.nvh + h];                                                                                     \
+            nz = bld4(buf(a.z + ((size_t) b * a.nt + (u_ - kr)) * a.nvh * DV + (size_t) h * DV, DV * 4), oz, 0); \
+        na = bld(abr_, 0, 4 * h);                                                                                 \
+        nb = bld(abr_, 0, 4 * (a.nvh + h));                                                                       \
     } while (0)
     if (FUSED) {
         if (!xab) {
@@ -255,7 +274,7 @@ k_gdn(const GdnArgs a) {
         const int t = u - kr;
         const size_t bt = (size_t) b * a.nt + (replay ? 0 : t);
         if (u > 0) {
-            __syncthreads();  // the previous token's LDS reads are done
+            lds_barrier();  // the previous token's LDS reads are done
             if (FUSED) {
                 if (qk_thr) {
                     c0.shift(nx0);
@@ -274,14 +293,14 @@ k_gdn(const GdnArgs a) {
             // and the ring slots of the replayed positions (the last up to three; after the shift above hist holds
             // the raw inputs of positions pos + kr - 3 .. pos + kr - 1)
 #pragma unroll
-            for (int r = 0; r < ROWS_PT; ++r) st_state(&Sh[(rg + RSTEP * r) * (DV / 4) + cg], s[r]);
+            for (int r = 0; r < ROWS_PT; ++r) st_state(Sb, so, r, s[r]);
             if (qk_thr) {
                 if (primary) {
-                    conv_store_hist(c0, a, ring_b, C, cq, pos + kr, kr);
-                    conv_store_hist(c1, a, ring_b, C, ck, pos + kr, kr);
+                    conv_store_hist(c0, a, ring, C, o0, pos + kr, kr);
+                    conv_store_hist(c1, a, ring, C, o1, pos + kr, kr);
                 }
             } else if (v_thr) {
-                conv_store_hist(c0, a, ring_b, C, cv, pos + kr, kr);
+                conv_store_hist(c0, a, ring, C, o0, pos + kr, kr);
             }
         }
 
@@ -307,7 +326,7 @@ k_gdn(const GdnArgs a) {
             vs[tid - DK] = FUSED ? c0.out() : a.v[(bt * a.nvh + h) * DV + (tid - DK)];
         }
 
-        __syncthreads();
+        lds_barrier();
         // 4. gates (uniform per head): beta = sigmoid(b), gamma = exp(ssm_a * softplus(a + dt_bias)), softplus
         //    the identity above 20 (faie2fn.cu:1407-1410)
         if (xab) {
@@ -356,13 +375,13 @@ k_gdn(const GdnArgs a) {
             sqp.w = fmaf(sv.w, qr, sqp.w);
         }
         // fold row groups 2w and 2w+1 (lanes l and l^32), then across waves through LDS
-        kvp.x += shfl_xor32(kvp.x); kvp.y += shfl_xor32(kvp.y); kvp.z += shfl_xor32(kvp.z); kvp.w += shfl_xor32(kvp.w);
-        sqp.x += shfl_xor32(sqp.x); sqp.y += shfl_xor32(sqp.y); sqp.z += shfl_xor32(sqp.z); sqp.w += shfl_xor32(sqp.w);
+        kvp.x = add_xor32(kvp.x); kvp.y = add_xor32(kvp.y); kvp.z = add_xor32(kvp.z); kvp.w = add_xor32(kvp.w);
+        sqp.x = add_xor32(sqp.x); sqp.y = add_xor32(sqp.y); sqp.z = add_xor32(sqp.z); sqp.w = add_xor32(sqp.w);
         if (lane < 32) {
             red[wave][0][cg] = kvp;
             red[wave][1][cg] = sqp;
         }
-        __syncthreads();
+        lds_barrier();
         float4 kv = red[0][0][cg], sq = red[0][1][cg];
 #pragma unroll
         for (int w = 1; w < WAVES; ++w) {
@@ -413,10 +432,10 @@ k_gdn(const GdnArgs a) {
                         r.z = o.z * rn * w4.z * siluf_(z4.z);
                         r.w = o.w * rn * w4.w * siluf_(z4.w);
                     }
-                    *reinterpret_cast<float4 *>(a.out + bt * a.nvh * DV + (size_t) h * DV + cg * 4) = r;
+                    bst4(buf(a.out + bt * a.nvh * DV + (size_t) h * DV, DV * 4), oz, 0, r);
                 }
             } else if (lane < 32) {
-                *reinterpret_cast<float4 *>(a.out + (bt * a.nvh + h) * DV + cg * 4) = o;
+                bst4(buf(a.out + (bt * a.nvh + h) * DV, DV * 4), oz, 0, o);
             }
         }
     }
@@ -426,15 +445,15 @@ k_gdn(const GdnArgs a) {
     //    state above and leaves the new tokens' state uncommitted.
     if (VERIFY) return;
 #pragma unroll
-    for (int r = 0; r < ROWS_PT; ++r) st_state(&Sh[(rg + RSTEP * r) * (DV / 4) + cg], s[r]);
+    for (int r = 0; r < ROWS_PT; ++r) st_state(Sb, so, r, s[r]);
     if (FUSED) {
         if (qk_thr) {
             if (primary) {
-                conv_store(c0, a, ring_b, C, cq, pos);
-                conv_store(c1, a, ring_b, C, ck, pos);
+                conv_store(c0, a, ring, C, o0, pos);
+                conv_store(c1, a, ring, C, o1, pos);
             }
         } else if (v_thr) {
-            conv_store(c0, a, ring_b, C, cv, pos);
+            conv_store(c0, a, ring, C, o0, pos);
         }
     }
 }
@@ -470,7 +489,7 @@ int gdn_block_launch(const GdnBlock &p, hipStream_t st) {
     a.gate_act = p.gate_act; a.eps = p.eps; a.pos = p.pos; a.qkv = p.qkv; a.conv_w = p.conv_w;
     a.ring_buf = p.conv_ring; a.ab = p.ab; a.dt_bias = p.dt_bias; a.ssm_a = p.ssm_a; a.S = p.S; a.z = p.z;
     a.norm_w = p.norm_w; a.out = p.out; a.x = p.x; a.wab = p.wab; a.hidden = p.hidden;
-    if (p.nt == 1) hipLaunchKernelGGL(k_gdn<3>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
+    if (p.nt == 1) hipLaunchKernelGGL(k_gdn<3>, dim3(p.B * p.nvh), dim3(THREADS), GDN_ONE_LDS_PAD, st, a);
     else hipLaunchKernelGGL(k_gdn<1>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
