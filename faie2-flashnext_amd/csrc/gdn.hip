@@ -168,10 +168,14 @@ k_gdn(const GdnArgs a) {
     const int C = 2 * a.nkh * DK + a.nvh * DV;
     const bool qk_thr = tid < DK, v_thr = tid >= DK && tid < DK + DV;  // wave-uniform roles
 
-    __shared__ float4 qs4[DK / 4], ks4[DK / 4];  // raw q, k of the key head (this token)
-    __shared__ float vs[DV];                      // conv'd v of the value head
-    __shared__ float4 red[WAVES][2][DV / 4];      // per-wave column partials of kv and sq
-    __shared__ float nrm[2][3];                   // per-wave sums q.q, k.k, q.k (waves 0, 1)
+    // The per-token exchange is double-buffered by token parity in multi-token calls: token u + 2 writes a buffer
+    // only after every wave has passed token u + 1's barriers, i.e. finished reading token u, so the loop needs no
+    // barrier of its own between tokens.
+    constexpr int NBUF = ONE ? 1 : 2;
+    __shared__ float4 qs4[NBUF][DK / 4], ks4[NBUF][DK / 4];  // raw q, k of the key head (this token)
+    __shared__ float vs[NBUF][DV];                            // conv'd v of the value head
+    __shared__ float4 red[NBUF][WAVES][2][DV / 4];            // per-wave column partials of kv and sq
+    __shared__ float nrm[NBUF][2][3];                         // per-wave sums q.q, k.k, q.k (waves 0, 1)
     __shared__ float2 abp[WAVES];                 // fused alpha/beta projection: per-wave partial dots
 
     // 1. every input of the first token is requested before the state tile, so nothing waits behind S twice:
@@ -272,9 +276,9 @@ k_gdn(const GdnArgs a) {
         // token u: a replayed one (u < kr, inputs from the previous call, no output) or new token t = u - kr
         const bool replay = VERIFY && u < kr;
         const int t = u - kr;
+        const int pb = NBUF == 1 ? 0 : (u & 1);  // exchange buffer of this token
         const size_t bt = (size_t) b * a.nt + (replay ? 0 : t);
         if (u > 0) {
-            lds_barrier();  // the previous token's LDS reads are done
             if (FUSED) {
                 if (qk_thr) {
                     c0.shift(nx0);
@@ -314,16 +318,16 @@ k_gdn(const GdnArgs a) {
                 q = a.q[(bt * a.nkh + kh) * DK + tid];
                 k = a.k[(bt * a.nkh + kh) * DK + tid];
             }
-            reinterpret_cast<float *>(qs4)[tid] = q;
-            reinterpret_cast<float *>(ks4)[tid] = k;
+            reinterpret_cast<float *>(qs4[pb])[tid] = q;
+            reinterpret_cast<float *>(ks4[pb])[tid] = k;
             const float sqq = wave_sum(q * q), skk = wave_sum(k * k), sqk = wave_sum(q * k);
             if (lane == 0) {
-                nrm[wave][0] = sqq;
-                nrm[wave][1] = skk;
-                nrm[wave][2] = sqk;
+                nrm[pb][wave][0] = sqq;
+                nrm[pb][wave][1] = skk;
+                nrm[pb][wave][2] = sqk;
             }
         } else if (v_thr) {
-            vs[tid - DK] = FUSED ? c0.out() : a.v[(bt * a.nvh + h) * DV + (tid - DK)];
+            vs[pb][tid - DK] = FUSED ? c0.out() : a.v[(bt * a.nvh + h) * DV + (tid - DK)];
         }
 
         lds_barrier();
@@ -351,15 +355,15 @@ k_gdn(const GdnArgs a) {
 
         // L2 factors x * rsqrt(sum x^2 + 1e-6) (faie2fn.cu:1399-1402); the core takes q, k as given
         float rq = 1.0f, rk = 1.0f;
-        const float sqk = nrm[0][2] + nrm[1][2];
+        const float sqk = nrm[pb][0][2] + nrm[pb][1][2];
         if (FUSED) {
-            rq = rsqrtf(nrm[0][0] + nrm[1][0] + 1e-6f);
-            rk = rsqrtf(nrm[0][1] + nrm[1][1] + 1e-6f);
+            rq = rsqrtf(nrm[pb][0][0] + nrm[pb][1][0] + 1e-6f);
+            rk = rsqrtf(nrm[pb][0][1] + nrm[pb][1][1] + 1e-6f);
         }
         const float kq = sqk * rq * rk;
 
         // 5. one pass over the registers: column partials of S^T k and S^T q over this thread's rows
-        const float *ksf = reinterpret_cast<const float *>(ks4), *qsf = reinterpret_cast<const float *>(qs4);
+        const float *ksf = reinterpret_cast<const float *>(ks4[pb]), *qsf = reinterpret_cast<const float *>(qs4[pb]);
         float4 kvp = f4(0.0f), sqp = f4(0.0f);
 #pragma unroll
         for (int r = 0; r < ROWS_PT; ++r) {
@@ -378,20 +382,20 @@ k_gdn(const GdnArgs a) {
         kvp.x = add_xor32(kvp.x); kvp.y = add_xor32(kvp.y); kvp.z = add_xor32(kvp.z); kvp.w = add_xor32(kvp.w);
         sqp.x = add_xor32(sqp.x); sqp.y = add_xor32(sqp.y); sqp.z = add_xor32(sqp.z); sqp.w = add_xor32(sqp.w);
         if (lane < 32) {
-            red[wave][0][cg] = kvp;
-            red[wave][1][cg] = sqp;
+            red[pb][wave][0][cg] = kvp;
+            red[pb][wave][1][cg] = sqp;
         }
         lds_barrier();
-        float4 kv = red[0][0][cg], sq = red[0][1][cg];
+        float4 kv = red[pb][0][0][cg], sq = red[pb][0][1][cg];
 #pragma unroll
         for (int w = 1; w < WAVES; ++w) {
-            const float4 x = red[w][0][cg], y = red[w][1][cg];
+            const float4 x = red[pb][w][0][cg], y = red[pb][w][1][cg];
             kv.x += x.x; kv.y += x.y; kv.z += x.z; kv.w += x.w;
             sq.x += y.x; sq.y += y.y; sq.z += y.z; sq.w += y.w;
         }
 
         // 6. delta, readout, update.  kv and sq were taken over raw k and q: scale by rk and rq here.
-        const float4 v4 = reinterpret_cast<const float4 *>(vs)[cg];
+        const float4 v4 = reinterpret_cast<const float4 *>(vs[pb])[cg];
         float4 d, o;
         d.x = (v4.x - gamma * (kv.x * rk)) * beta;
         d.y = (v4.y - gamma * (kv.y * rk)) * beta;
