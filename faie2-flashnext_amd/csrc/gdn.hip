@@ -3,8 +3,10 @@
 //
 // Semantics follow k_gdn (reference engine/faie2fn.cu:1349-1431).  The kernel is organised for CDNA4, not as a
 // translation of the sm_120 one:
-//   * 512 threads (eight wave64s) per head.  Thread (rg = tid / 32, cg = tid % 32) owns the 4 columns 4cg..4cg+3
-//     of the 8 state rows rg, rg + 16, ..., rg + 112, i.e. 8 float4 registers.  Every wave load and store of S
+//   * 512 threads (eight wave64s) per head in the one-token kernels.  Thread (rg = tid / 32, cg = tid % 32) owns the
+//     4 columns 4cg..4cg+3 of the 8 state rows rg, rg + 16, ..., rg + 112, i.e. 8 float4 registers.  The
+//     multi-token kernels run 256 threads per head, each owning the two row groups 2rg and 2rg + 1, and reproduce
+//     the 512-thread arithmetic bit for bit.  Every wave load and store of S
 //     moves two contiguous 512-byte rows with 128-bit accesses, and the eight waves' r-th accesses together sweep
 //     rows 16r .. 16r + 15, 8 KiB in a row, so the tile streams through HBM in address order (row groups of 8
 //     consecutive rows per thread scatter each sweep over the whole 64 KiB; on MI355X the bare tile pass takes
@@ -46,9 +48,8 @@ namespace {
 #define GDN_WPE 1
 #endif
 #ifndef GDN_VERIFY_WPE
-// the verify step runs several tokens per call, where two workgroups per CU (four waves per SIMD, 128 VGPRs, a few
-// spills) beat one: B = 64, 4 new + 2 replayed tokens, 125 -> 101 us per layer-step on MI355X
-#define GDN_VERIFY_WPE 4
+// the verify step (256 threads per head) in 155 VGPRs: three workgroups per CU
+#define GDN_VERIFY_WPE 3
 #endif
 
 #ifndef GDN_ONE_LDS_PAD
@@ -59,19 +60,27 @@ namespace {
 #endif
 
 constexpr int DK = 128, DV = 128;
-constexpr int THREADS = GDN_THREADS;       // 256 or 512
-constexpr int WAVES = THREADS / 64;
-constexpr int ROWS_PT = DK * 32 / THREADS;  // state rows per thread (32 threads span a row)
-constexpr int RSTEP = THREADS / 32;         // row groups: thread row group rg owns rows rg, rg + RSTEP, ...
-static_assert(THREADS == 256 || THREADS == 512 || THREADS == 1024, "one state tile per 4, 8 or 16 waves");
+constexpr int THREADS = GDN_THREADS;  // threads per head of the one-token kernels (decode, bare core)
+#ifndef GDN_MT_THREADS
+// The multi-token kernels run the per-token reduction chain nt + kr times per call, which makes them VALU-bound
+// rather than memory-bound: with 256 threads per head the cross-wave sum of the column partials is repeated by half
+// as many threads, and three heads share a CU instead of two (B = 64, 4 new + 2 replayed tokens: 92.0 -> 80.7 us
+// per layer-step; 8 + 4: 158.8 -> 131.4 us).  The one-token decode stays at 512 (memory-bound: 256 measured equal
+// at B = 64 and slower at B = 1, 5.26 against 4.94 us).
+#define GDN_MT_THREADS 256
+#endif
+constexpr int MT_THREADS = GDN_MT_THREADS;  // threads per head of the multi-token kernels (prefill, verify)
+static_assert(THREADS == 256 || THREADS == 512, "one state tile per 4 or 8 waves");
+static_assert(MT_THREADS == 256 || MT_THREADS == 512, "one state tile per 4 or 8 waves");
 
-// the thread's float4 of state register r: byte offset so (row rg, columns 4cg..) in the head's tile, plus r row
-// blocks of RSTEP rows
+// The state tile in registers: 16 row groups g of 8 rows (g, g + 16, ..., g + 112), 32 column groups of 4 columns.
+// Row r of group g is at byte offset so(g, column group) + r * 16 rows.
+constexpr int NG = 16, GROWS = DK / NG;
 __device__ __forceinline__ float4 ld_state(brsrc S, uint32_t so, int r) {
-    return bld4<GDN_NT ? 2 : 0>(S, so, (uint32_t) r * RSTEP * DV * 4);
+    return bld4<GDN_NT ? 2 : 0>(S, so, (uint32_t) r * NG * DV * 4);
 }
 __device__ __forceinline__ void st_state(brsrc S, uint32_t so, int r, float4 v) {
-    bst4<GDN_NT_ST ? 2 : 0>(S, so, (uint32_t) r * RSTEP * DV * 4, v);
+    bst4<GDN_NT_ST ? 2 : 0>(S, so, (uint32_t) r * NG * DV * 4, v);
 }
 
 struct GdnArgs {
@@ -157,9 +166,16 @@ __device__ __forceinline__ void conv_store_hist(const ConvChan &cc, const GdnArg
     if (n >= 3) bst(ring, oc, slot_off(a, C, end - 3), cc.hist[0]);
 }
 
-template <int MODE>
-__global__ void __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(MODE == 2 ? GDN_VERIFY_WPE : GDN_WPE, 8)))
+template <int MODE, int NTH = (MODE == 1 || MODE == 2) ? MT_THREADS : THREADS>
+__global__ void __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(MODE == 2 ? GDN_VERIFY_WPE : GDN_WPE, 8)))
 k_gdn(const GdnArgs a) {
+    constexpr int WAVES = NTH / 64;
+    // Every thread count computes the 512-thread kernel's arithmetic bit for bit (a verify step must reproduce
+    // one-token decode exactly): the column partials of a row group are chained in row order, groups 2m and 2m + 1
+    // are added, and the 8 sums are added in m order.  A thread owns CH = 512 / NTH consecutive row groups
+    // CH rg + j of column group cg: with 512 threads groups 2m and 2m + 1 sit in lanes l and l ^ 32 of wave m, with
+    // 256 threads in one thread.
+    constexpr int CH = 512 / NTH;
     constexpr bool FUSED = MODE >= 1, VERIFY = MODE == 2, ONE = MODE == 3;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int cg = tid & 31, rg = tid >> 5;
@@ -174,7 +190,7 @@ k_gdn(const GdnArgs a) {
     constexpr int NBUF = ONE ? 1 : 2;
     __shared__ float4 qs4[NBUF][DK / 4], ks4[NBUF][DK / 4];  // raw q, k of the key head (this token)
     __shared__ float vs[NBUF][DV];                            // conv'd v of the value head
-    __shared__ float4 red[NBUF][WAVES][2][DV / 4];            // per-wave column partials of kv and sq
+    __shared__ float4 red[NBUF][NG / 2][2][DV / 4];           // folded column partials of kv and sq
     __shared__ float nrm[NBUF][2][3];                         // per-wave sums q.q, k.k, q.k (waves 0, 1)
     __shared__ float2 abp[WAVES];                 // fused alpha/beta projection: per-wave partial dots
 
@@ -212,7 +228,7 @@ k_gdn(const GdnArgs a) {
         const float *xb = a.x + (size_t) b * a.hidden;
         const uint16_t *wa = a.wab + (size_t) h * a.hidden, *wb = a.wab + (size_t) (a.nvh + h) * a.hidden;
         float pa = 0.0f, pb = 0.0f;
-        for (int i = 4 * tid; i < a.hidden; i += 4 * THREADS) {
+        for (int i = 4 * tid; i < a.hidden; i += 4 * NTH) {
             const float4 xv = *reinterpret_cast<const float4 *>(xb + i);
             const uint2 ua = *reinterpret_cast<const uint2 *>(wa + i), ub = *reinterpret_cast<const uint2 *>(wb + i);
             pa = fmaf(bf16_lo(ua.x), xv.x, pa);
@@ -230,11 +246,13 @@ k_gdn(const GdnArgs a) {
     }
 
     // 2. state tile into registers
-    float4 s[ROWS_PT];
+    float4 s[CH][GROWS];
     const brsrc Sb = buf(a.S + (size_t) bh * DK * DV, DK * DV * 4);
-    const uint32_t so = 16u * (rg * (DV / 4) + cg);  // the thread's float4 of row rg
+    const uint32_t so = 16u * (CH * rg * (DV / 4) + cg);  // the thread's float4 of row CH rg; group j is j rows on
 #pragma unroll
-    for (int r = 0; r < ROWS_PT; ++r) s[r] = ld_state(Sb, so, r);
+    for (int j = 0; j < CH; ++j)
+#pragma unroll
+        for (int r = 0; r < GROWS; ++r) s[j][r] = ld_state(Sb, so + j * DV * 4, r);
 
     const float scale = 0.08838834764831845f;  // 1/sqrt(128), faie2fn.cu:1352
 
@@ -297,7 +315,9 @@ k_gdn(const GdnArgs a) {
             // and the ring slots of the replayed positions (the last up to three; after the shift above hist holds
             // the raw inputs of positions pos + kr - 3 .. pos + kr - 1)
 #pragma unroll
-            for (int r = 0; r < ROWS_PT; ++r) st_state(Sb, so, r, s[r]);
+            for (int j = 0; j < CH; ++j)
+#pragma unroll
+                for (int r = 0; r < GROWS; ++r) st_state(Sb, so + j * DV * 4, r, s[j][r]);
             if (qk_thr) {
                 if (primary) {
                     conv_store_hist(c0, a, ring, C, o0, pos + kr, kr);
@@ -364,31 +384,44 @@ k_gdn(const GdnArgs a) {
 
         // 5. one pass over the registers: column partials of S^T k and S^T q over this thread's rows
         const float *ksf = reinterpret_cast<const float *>(ks4[pb]), *qsf = reinterpret_cast<const float *>(qs4[pb]);
-        float4 kvp = f4(0.0f), sqp = f4(0.0f);
+        float4 kvp[CH], sqp[CH];
 #pragma unroll
-        for (int r = 0; r < ROWS_PT; ++r) {
-            const float kr = ksf[rg + RSTEP * r], qr = qsf[rg + RSTEP * r];
-            const float4 sv = s[r];
-            kvp.x = fmaf(sv.x, kr, kvp.x);
-            kvp.y = fmaf(sv.y, kr, kvp.y);
-            kvp.z = fmaf(sv.z, kr, kvp.z);
-            kvp.w = fmaf(sv.w, kr, kvp.w);
-            sqp.x = fmaf(sv.x, qr, sqp.x);
-            sqp.y = fmaf(sv.y, qr, sqp.y);
-            sqp.z = fmaf(sv.z, qr, sqp.z);
-            sqp.w = fmaf(sv.w, qr, sqp.w);
+        for (int j = 0; j < CH; ++j) {
+            kvp[j] = sqp[j] = f4(0.0f);
+#pragma unroll
+            for (int r = 0; r < GROWS; ++r) {
+                const int row = CH * rg + j + NG * r;
+                const float kr = ksf[row], qr = qsf[row];
+                const float4 sv = s[j][r];
+                kvp[j].x = fmaf(sv.x, kr, kvp[j].x);
+                kvp[j].y = fmaf(sv.y, kr, kvp[j].y);
+                kvp[j].z = fmaf(sv.z, kr, kvp[j].z);
+                kvp[j].w = fmaf(sv.w, kr, kvp[j].w);
+                sqp[j].x = fmaf(sv.x, qr, sqp[j].x);
+                sqp[j].y = fmaf(sv.y, qr, sqp[j].y);
+                sqp[j].z = fmaf(sv.z, qr, sqp[j].z);
+                sqp[j].w = fmaf(sv.w, qr, sqp[j].w);
+            }
         }
-        // fold row groups 2w and 2w+1 (lanes l and l^32), then across waves through LDS
-        kvp.x = add_xor32(kvp.x); kvp.y = add_xor32(kvp.y); kvp.z = add_xor32(kvp.z); kvp.w = add_xor32(kvp.w);
-        sqp.x = add_xor32(sqp.x); sqp.y = add_xor32(sqp.y); sqp.z = add_xor32(sqp.z); sqp.w = add_xor32(sqp.w);
-        if (lane < 32) {
-            red[pb][wave][0][cg] = kvp;
-            red[pb][wave][1][cg] = sqp;
+        // fold row groups 2m and 2m + 1 (lanes l and l ^ 32, or the thread's two groups), then the 8 folded sums
+        // through LDS
+        float4 kvf, sqf;
+        if constexpr (CH == 1) {
+            kvf = make_float4(add_xor32(kvp[0].x), add_xor32(kvp[0].y), add_xor32(kvp[0].z), add_xor32(kvp[0].w));
+            sqf = make_float4(add_xor32(sqp[0].x), add_xor32(sqp[0].y), add_xor32(sqp[0].z), add_xor32(sqp[0].w));
+        } else {
+            kvf = make_float4(kvp[0].x + kvp[1].x, kvp[0].y + kvp[1].y, kvp[0].z + kvp[1].z, kvp[0].w + kvp[1].w);
+            sqf = make_float4(sqp[0].x + sqp[1].x, sqp[0].y + sqp[1].y, sqp[0].z + sqp[1].z, sqp[0].w + sqp[1].w);
+        }
+        if (CH == 2 || lane < 32) {
+            const int m = CH == 1 ? wave : rg;
+            red[pb][m][0][cg] = kvf;
+            red[pb][m][1][cg] = sqf;
         }
         lds_barrier();
         float4 kv = red[pb][0][0][cg], sq = red[pb][0][1][cg];
 #pragma unroll
-        for (int w = 1; w < WAVES; ++w) {
+        for (int w = 1; w < NG / 2; ++w) {
             const float4 x = red[pb][w][0][cg], y = red[pb][w][1][cg];
             kv.x += x.x; kv.y += x.y; kv.z += x.z; kv.w += x.w;
             sq.x += y.x; sq.y += y.y; sq.z += y.z; sq.w += y.w;
@@ -407,16 +440,18 @@ k_gdn(const GdnArgs a) {
         o.w = fmaf(gamma, sq.w * rq, kq * d.w) * scale;
         const float4 dk4 = make_float4(d.x * rk, d.y * rk, d.z * rk, d.w * rk);  // k enters raw below
 #pragma unroll
-        for (int r = 0; r < ROWS_PT; ++r) {
-            const float kr = ksf[rg + RSTEP * r];
-            float4 &sv = s[r];
-            sv.x = fmaf(kr, dk4.x, gamma * sv.x);
-            sv.y = fmaf(kr, dk4.y, gamma * sv.y);
-            sv.z = fmaf(kr, dk4.z, gamma * sv.z);
-            sv.w = fmaf(kr, dk4.w, gamma * sv.w);
-        }
+        for (int j = 0; j < CH; ++j)
+#pragma unroll
+            for (int r = 0; r < GROWS; ++r) {
+                const float kr = ksf[CH * rg + j + NG * r];
+                float4 &sv = s[j][r];
+                sv.x = fmaf(kr, dk4.x, gamma * sv.x);
+                sv.y = fmaf(kr, dk4.y, gamma * sv.y);
+                sv.z = fmaf(kr, dk4.z, gamma * sv.z);
+                sv.w = fmaf(kr, dk4.w, gamma * sv.w);
+            }
 
-        // 7. output: wave 0 holds every column twice (row groups 0 and 1)
+        // 7. output: wave 0 holds every column twice (lanes l and l + 32)
         if (wave == 0 && !replay) {
             if (FUSED) {
                 // gated RMSNorm on = o * rsqrt(mean o^2 + eps) * w * act(z) (faie2fn.cu:1422-1424); the wave sum
@@ -449,7 +484,9 @@ k_gdn(const GdnArgs a) {
     //    state above and leaves the new tokens' state uncommitted.
     if (VERIFY) return;
 #pragma unroll
-    for (int r = 0; r < ROWS_PT; ++r) st_state(Sb, so, r, s[r]);
+    for (int j = 0; j < CH; ++j)
+#pragma unroll
+        for (int r = 0; r < GROWS; ++r) st_state(Sb, so + j * DV * 4, r, s[j][r]);
     if (FUSED) {
         if (qk_thr) {
             if (primary) {
@@ -494,7 +531,7 @@ int gdn_block_launch(const GdnBlock &p, hipStream_t st) {
     a.ring_buf = p.conv_ring; a.ab = p.ab; a.dt_bias = p.dt_bias; a.ssm_a = p.ssm_a; a.S = p.S; a.z = p.z;
     a.norm_w = p.norm_w; a.out = p.out; a.x = p.x; a.wab = p.wab; a.hidden = p.hidden;
     if (p.nt == 1) hipLaunchKernelGGL(k_gdn<3>, dim3(p.B * p.nvh), dim3(THREADS), GDN_ONE_LDS_PAD, st, a);
-    else hipLaunchKernelGGL(k_gdn<1>, dim3(p.B * p.nvh), dim3(THREADS), 0, st, a);
+    else hipLaunchKernelGGL(k_gdn<1>, dim3(p.B * p.nvh), dim3(MT_THREADS), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
 }
@@ -529,7 +566,7 @@ int gdn_verify_launch(const GdnVerify &p, hipStream_t st) {
     a.ring_buf = q.conv_ring; a.ab = q.ab; a.dt_bias = q.dt_bias; a.ssm_a = q.ssm_a; a.S = q.S; a.z = q.z;
     a.norm_w = q.norm_w; a.out = q.out;
     a.kr = p.kr; a.rnt = p.rnt; a.rqkv = p.rqkv; a.rab = p.rab;
-    hipLaunchKernelGGL(k_gdn<2>, dim3(q.B * q.nvh), dim3(THREADS), 0, st, a);
+    hipLaunchKernelGGL(k_gdn<2>, dim3(q.B * q.nvh), dim3(MT_THREADS), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
 }
