@@ -498,6 +498,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gdn-only", action="store_true",
+                    help="of the extra legs run only the DeltaNet ones (copy yardstick, configs 0 and 1, verify)")
     ap.add_argument("--gemv", action="store_true", help="projection GEMV timings only (fn_bench_gemv legs)")
     ap.add_argument("--counters", action="store_true",
                     help="counter-collection workload only: 3 plain copies of 1 GiB (the calibration kernel) and one "
@@ -604,6 +606,7 @@ def main():
                 "ms_per_step": round(ms, 4), "us_per_layer_step": round(ms * 1e3 / 36, 2),
                 "draft_tokens_per_s": round(64 * nt_v * 1e3 / ms, 1), "gbs": round(36 * by / (ms * 1e-3) / 1e9, 1)}
             log(f"[bench] config 2 verify nt={nt_v} kr={kr_v}: {ms * 1e3 / 36:.2f} us/layer-step")
+    if not args.no_extra and not args.gdn_only:
         # config 3: GQA decode
         for Bq, ctx, nl in ((1, 4096, 32), (1, 32768, 8), (1, 131072, 2), (16, 32768, 2)):
             at = AttnStack(lib, Bq, ctx, nl, seed=3)
@@ -659,8 +662,8 @@ def main():
                                                "tokens_per_s": round(16 * 1e3 / ms, 1), "bytes_per_step": nbytes,
                                                "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                                                "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
-        for k, v in extra.items():
-            log(f"[bench] {k}: {v}")
+    for k, v in extra.items():
+        log(f"[bench] {k}: {v}")
 
     cpu = None
     if not args.no_cpu:
