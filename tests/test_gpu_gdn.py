@@ -77,6 +77,26 @@ def test_block_multi_token(fnlib, nt):
         assert max(e) <= TOL, (call, e)
 
 
+@pytest.mark.parametrize("nt,head_map", [(2, 0), (4, 1), (7, 0)])
+def test_block_multi_token_bitwise_equals_steps(fnlib, nt, head_map):
+    """One call of nt tokens (the multi-token kernel, 256 threads per head) reproduces nt one-token calls (the
+    decode kernel, 512 threads per head) bit for bit: outputs, state and conv state."""
+    _say(f"gdn block nt={nt} head_map={head_map} vs {nt} x nt=1, bitwise, B=3")
+    lay = fn_synth.BlockLayer(B=3, config=1, layer=11)
+    st = [lay.step() for _ in range(nt)]
+    qkv, ab, z = (np.concatenate([s[i] for s in st], axis=1) for i in range(3))
+    S_a, c_a = lay.S0.copy(), lay.conv0.copy()
+    out_a = fnlib.gdn_block(qkv, lay.conv_w, c_a, ab, lay.dt_bias, lay.ssm_a, S_a, z, lay.norm_w, 16, 32,
+                            head_map=head_map)
+    S_b, c_b = lay.S0.copy(), lay.conv0.copy()
+    out_b = np.concatenate([fnlib.gdn_block(s[0], lay.conv_w, c_b, s[1], lay.dt_bias, lay.ssm_a, S_b, s[2],
+                                            lay.norm_w, 16, 32, head_map=head_map) for s in st], axis=1)
+    assert out_a.shape == out_b.shape
+    assert np.array_equal(out_a, out_b), np.abs(out_a - out_b).max()
+    assert np.array_equal(S_a, S_b), np.abs(S_a - S_b).max()
+    assert np.array_equal(c_a, c_b)
+
+
 def test_block_device_ring_advances(fnlib):
     """Device entry point with the conv ring and a device position advanced by fn_advance_dev: 12 decode steps of
     B=3 sequences at different starting positions, checked against the oracle every step."""
