@@ -151,6 +151,16 @@ __device__ __forceinline__ void conv_store(const ConvChan &cc, const GdnArgs &a,
     if (a.nt >= 3) bst(ring, oc, slot_off(a, C, last - 2), cc.hist[1]);
 }
 
+// Gates of one head and token (uniform per head): beta = sigmoid(b), gamma = exp(ssm_a * softplus(a + dt_bias)),
+// softplus the identity above 20 (faie2fn.cu:1407-1410).  One function for the one-token and the lane-parallel
+// (multi-token) callers, so both compute the same bits.
+__device__ __forceinline__ void gdn_gates(float ga, float gb, float dtb, float ssa, float &beta, float &gamma) {
+    beta = sigmoidf_(gb);
+    const float x = ga + dtb;
+    const float sp = x > 20.0f ? x : log1pf(expf(x));
+    gamma = expf(sp * ssa);
+}
+
 // MODE 0: the bare core; 1: the fused block (every token committed); 3: the fused block for exactly one token (the
 // decode step: no token loop, no next-token prefetch, fewer registers); 2: the fused block as a verify step with
 // deferred commit -- first the kr[b] tokens of the previous call that the caller accepted are replayed from their
@@ -245,6 +255,26 @@ k_gdn(const GdnArgs a) {
         if (lane == 0) abp[wave] = make_float2(pa, pb);
     }
 
+    // multi-token calls: lane i holds the logits (then the gates) of token u0 + i of each run of 64 tokens, computed
+    // once for the run instead of once per token by every thread
+    const auto lane_logits = [&](int u0, float &la, float &lb) {
+        const int uu = u0 + lane;
+        la = lb = 0.0f;
+        if (uu < ntot) {
+            const float *abt = VERIFY && uu < kr ? a.rab + ((size_t) b * a.rnt + uu) * 2 * a.nvh
+                                                 : a.ab + ((size_t) b * a.nt + (uu - kr)) * 2 * a.nvh;
+            la = abt[h];
+            lb = abt[a.nvh + h];
+        }
+    };
+    float ga = 0.0f, gb = 0.0f, dtb = 0.0f, ssa = 0.0f;  // one token's alpha, beta logits; the head's gate params
+    float lbeta = 0.0f, lgamma = 0.0f;                   // multi-token: gates of token u0 + lane
+    if (FUSED) {
+        if (!ONE) lane_logits(0, ga, gb);
+        dtb = a.dt_bias[h];
+        ssa = a.ssm_a[h];
+    }
+
     // 2. state tile into registers
     float4 s[CH][GROWS];
     const brsrc Sb = buf(a.S + (size_t) bh * DK * DV, DK * DV * 4);
@@ -253,6 +283,7 @@ k_gdn(const GdnArgs a) {
     for (int j = 0; j < CH; ++j)
 #pragma unroll
         for (int r = 0; r < GROWS; ++r) s[j][r] = ld_state(Sb, so + j * DV * 4, r);
+    if (FUSED && !ONE) gdn_gates(ga, gb, dtb, ssa, lbeta, lgamma);  // under the tile's loads
 
     const float scale = 0.08838834764831845f;  // 1/sqrt(128), faie2fn.cu:1352
 
@@ -261,220 +292,218 @@ k_gdn(const GdnArgs a) {
     // token: the loop's barriers order LDS only (lds_barrier), every one of these is a vector (buffer) load, and no
     // per-lane address is a 64-bit pair the compiler could keep across the loop and spill (a scratch reload waits
     // for every load issued before it, the prefetch included).
-    float ga = 0.0f, gb = 0.0f, dtb = 0.0f, ssa = 0.0f;  // this token's alpha, beta logits; the head's gate params
-    float nx0 = 0.0f, nx1 = 0.0f, na = 0.0f, nb = 0.0f;  // next token's raw channels and logits
+    float nx0 = 0.0f, nx1 = 0.0f;  // next token's raw channels
     float4 nz = f4(0.0f);
 #define GDN_PREFETCH(U_)                                                                                           \
     do {                                                                                                          \
         const int u_ = (U_);                                                                                      \
         const bool rp_ = VERIFY && u_ < kr;                                                                       \
         const float *xt_ = rp_ ? rx_b + (size_t) u_ * C : x_b + (size_t) (u_ - kr) * C;                           \
-        const float *abt_ = rp_ ? a.rab + ((size_t) b * a.rnt + u_) * 2 * a.nvh                                  \
-                                : a.ab + ((size_t) b * a.nt + (u_ - kr)) * 2 * a.nvh;                             \
-        const brsrc xr_ = buf(xt_, C * 4), abr_ = buf(abt_, 2 * a.nvh * 4);                                     \
+        const brsrc xr_ = buf(xt_, C * 4);                                                                        \
         if (qk_thr || v_thr) nx0 = bld(xr_, o0, 0);                                                              \
         if (qk_thr) nx1 = bld(xr_, o1, 0);                                                                        \
         if (wave == 0 && lane < 32 && !rp_)                                                                       \
             nz = bld4(buf(a.z + ((size_t) b * a.nt + (u_ - kr)) * a.nvh * DV + (size_t) h * DV, DV * 4), oz, 0); \
-        na = bld(abr_, 0, 4 * h);                                                                                 \
-        nb = bld(abr_, 0, 4 * (a.nvh + h));                                                                       \
     } while (0)
     if (FUSED) {
-        if (!xab) {
-            const float *ab0 = kr > 0 ? a.rab + (size_t) b * a.rnt * 2 * a.nvh : a.ab + (size_t) b * a.nt * 2 * a.nvh;
+        if (ONE && !xab) {
+            const float *ab0 = a.ab + (size_t) b * a.nt * 2 * a.nvh;
             ga = ab0[h];
             gb = ab0[a.nvh + h];
         }
-        dtb = a.dt_bias[h];
-        ssa = a.ssm_a[h];
         if (!ONE && ntot > 1) GDN_PREFETCH(1);
     }
 
-    for (int u = 0; u < ntot; ++u) {
-        // token u: a replayed one (u < kr, inputs from the previous call, no output) or new token t = u - kr
-        const bool replay = VERIFY && u < kr;
-        const int t = u - kr;
-        const int pb = NBUF == 1 ? 0 : (u & 1);  // exchange buffer of this token
-        const size_t bt = (size_t) b * a.nt + (replay ? 0 : t);
-        if (u > 0) {
-            if (FUSED) {
-                if (qk_thr) {
-                    c0.shift(nx0);
-                    c1.shift(nx1);
-                } else if (v_thr) {
-                    c0.shift(nx0);
+    // runs of up to 64 tokens: the gates of a run are computed lane-parallel before it
+    for (int u0 = 0; u0 < ntot; u0 += 64) {
+    if (FUSED && !ONE && u0 > 0) {
+        lane_logits(u0, ga, gb);
+        gdn_gates(ga, gb, dtb, ssa, lbeta, lgamma);
+    }
+    for (int u = u0; u < min(u0 + 64, ntot); ++u) {
+            // token u: a replayed one (u < kr, inputs from the previous call, no output) or new token t = u - kr
+            const bool replay = VERIFY && u < kr;
+            const int t = u - kr;
+            const int pb = NBUF == 1 ? 0 : (u & 1);  // exchange buffer of this token
+            const size_t bt = (size_t) b * a.nt + (replay ? 0 : t);
+            if (u > 0) {
+                if (FUSED) {
+                    if (qk_thr) {
+                        c0.shift(nx0);
+                        c1.shift(nx1);
+                    } else if (v_thr) {
+                        c0.shift(nx0);
+                    }
+                    if (!replay) z4 = nz;
+                    if (!ONE && u + 1 < ntot) GDN_PREFETCH(u + 1);
                 }
-                if (!replay) z4 = nz;
-                ga = na;
-                gb = nb;
-                if (!ONE && u + 1 < ntot) GDN_PREFETCH(u + 1);
             }
-        }
-        if (VERIFY && u == kr && kr > 0) {
-            // the committed state, before the first new token moves the registers on: S after the replayed tokens,
-            // and the ring slots of the replayed positions (the last up to three; after the shift above hist holds
-            // the raw inputs of positions pos + kr - 3 .. pos + kr - 1)
-#pragma unroll
-            for (int j = 0; j < CH; ++j)
-#pragma unroll
-                for (int r = 0; r < GROWS; ++r) st_state(Sb, so + j * DV * 4, r, s[j][r]);
-            if (qk_thr) {
-                if (primary) {
+            if (VERIFY && u == kr && kr > 0) {
+                // the committed state, before the first new token moves the registers on: S after the replayed tokens,
+                // and the ring slots of the replayed positions (the last up to three; after the shift above hist holds
+                // the raw inputs of positions pos + kr - 3 .. pos + kr - 1)
+    #pragma unroll
+                for (int j = 0; j < CH; ++j)
+    #pragma unroll
+                    for (int r = 0; r < GROWS; ++r) st_state(Sb, so + j * DV * 4, r, s[j][r]);
+                if (qk_thr) {
+                    if (primary) {
+                        conv_store_hist(c0, a, ring, C, o0, pos + kr, kr);
+                        conv_store_hist(c1, a, ring, C, o1, pos + kr, kr);
+                    }
+                } else if (v_thr) {
                     conv_store_hist(c0, a, ring, C, o0, pos + kr, kr);
-                    conv_store_hist(c1, a, ring, C, o1, pos + kr, kr);
+                }
+            }
+
+            // 3. q, k (waves 0-1, channel i = tid) and v (waves 2-3, channel j = tid - 128)
+            if (qk_thr) {
+                float q, k;
+                if (FUSED) {
+                    q = c0.out();
+                    k = c1.out();
+                } else {
+                    q = a.q[(bt * a.nkh + kh) * DK + tid];
+                    k = a.k[(bt * a.nkh + kh) * DK + tid];
+                }
+                reinterpret_cast<float *>(qs4[pb])[tid] = q;
+                reinterpret_cast<float *>(ks4[pb])[tid] = k;
+                const float sqq = wave_sum(q * q), skk = wave_sum(k * k), sqk = wave_sum(q * k);
+                if (lane == 0) {
+                    nrm[pb][wave][0] = sqq;
+                    nrm[pb][wave][1] = skk;
+                    nrm[pb][wave][2] = sqk;
                 }
             } else if (v_thr) {
-                conv_store_hist(c0, a, ring, C, o0, pos + kr, kr);
-            }
-        }
-
-        // 3. q, k (waves 0-1, channel i = tid) and v (waves 2-3, channel j = tid - 128)
-        if (qk_thr) {
-            float q, k;
-            if (FUSED) {
-                q = c0.out();
-                k = c1.out();
-            } else {
-                q = a.q[(bt * a.nkh + kh) * DK + tid];
-                k = a.k[(bt * a.nkh + kh) * DK + tid];
-            }
-            reinterpret_cast<float *>(qs4[pb])[tid] = q;
-            reinterpret_cast<float *>(ks4[pb])[tid] = k;
-            const float sqq = wave_sum(q * q), skk = wave_sum(k * k), sqk = wave_sum(q * k);
-            if (lane == 0) {
-                nrm[pb][wave][0] = sqq;
-                nrm[pb][wave][1] = skk;
-                nrm[pb][wave][2] = sqk;
-            }
-        } else if (v_thr) {
-            vs[pb][tid - DK] = FUSED ? c0.out() : a.v[(bt * a.nvh + h) * DV + (tid - DK)];
-        }
-
-        lds_barrier();
-        // 4. gates (uniform per head): beta = sigmoid(b), gamma = exp(ssm_a * softplus(a + dt_bias)), softplus
-        //    the identity above 20 (faie2fn.cu:1407-1410)
-        if (xab) {
-            ga = abp[0].x;
-            gb = abp[0].y;
-#pragma unroll
-            for (int w = 1; w < WAVES; ++w) {
-                ga += abp[w].x;
-                gb += abp[w].y;
-            }
-        }
-        float beta, gamma;
-        if (FUSED) {
-            beta = sigmoidf_(gb);
-            const float x = ga + dtb;
-            const float sp = x > 20.0f ? x : log1pf(expf(x));
-            gamma = expf(sp * ssa);
-        } else {
-            beta = a.beta[bt * a.nvh + h];
-            gamma = expf(a.g[bt * a.nvh + h]);
-        }
-
-        // L2 factors x * rsqrt(sum x^2 + 1e-6) (faie2fn.cu:1399-1402); the core takes q, k as given
-        float rq = 1.0f, rk = 1.0f;
-        const float sqk = nrm[pb][0][2] + nrm[pb][1][2];
-        if (FUSED) {
-            rq = rsqrtf(nrm[pb][0][0] + nrm[pb][1][0] + 1e-6f);
-            rk = rsqrtf(nrm[pb][0][1] + nrm[pb][1][1] + 1e-6f);
-        }
-        const float kq = sqk * rq * rk;
-
-        // 5. one pass over the registers: column partials of S^T k and S^T q over this thread's rows
-        const float *ksf = reinterpret_cast<const float *>(ks4[pb]), *qsf = reinterpret_cast<const float *>(qs4[pb]);
-        float4 kvp[CH], sqp[CH];
-#pragma unroll
-        for (int j = 0; j < CH; ++j) {
-            kvp[j] = sqp[j] = f4(0.0f);
-#pragma unroll
-            for (int r = 0; r < GROWS; ++r) {
-                const int row = CH * rg + j + NG * r;
-                const float kr = ksf[row], qr = qsf[row];
-                const float4 sv = s[j][r];
-                kvp[j].x = fmaf(sv.x, kr, kvp[j].x);
-                kvp[j].y = fmaf(sv.y, kr, kvp[j].y);
-                kvp[j].z = fmaf(sv.z, kr, kvp[j].z);
-                kvp[j].w = fmaf(sv.w, kr, kvp[j].w);
-                sqp[j].x = fmaf(sv.x, qr, sqp[j].x);
-                sqp[j].y = fmaf(sv.y, qr, sqp[j].y);
-                sqp[j].z = fmaf(sv.z, qr, sqp[j].z);
-                sqp[j].w = fmaf(sv.w, qr, sqp[j].w);
-            }
-        }
-        // fold row groups 2m and 2m + 1 (lanes l and l ^ 32, or the thread's two groups), then the 8 folded sums
-        // through LDS
-        float4 kvf, sqf;
-        if constexpr (CH == 1) {
-            kvf = make_float4(add_xor32(kvp[0].x), add_xor32(kvp[0].y), add_xor32(kvp[0].z), add_xor32(kvp[0].w));
-            sqf = make_float4(add_xor32(sqp[0].x), add_xor32(sqp[0].y), add_xor32(sqp[0].z), add_xor32(sqp[0].w));
-        } else {
-            kvf = make_float4(kvp[0].x + kvp[1].x, kvp[0].y + kvp[1].y, kvp[0].z + kvp[1].z, kvp[0].w + kvp[1].w);
-            sqf = make_float4(sqp[0].x + sqp[1].x, sqp[0].y + sqp[1].y, sqp[0].z + sqp[1].z, sqp[0].w + sqp[1].w);
-        }
-        if (CH == 2 || lane < 32) {
-            const int m = CH == 1 ? wave : rg;
-            red[pb][m][0][cg] = kvf;
-            red[pb][m][1][cg] = sqf;
-        }
-        lds_barrier();
-        float4 kv = red[pb][0][0][cg], sq = red[pb][0][1][cg];
-#pragma unroll
-        for (int w = 1; w < NG / 2; ++w) {
-            const float4 x = red[pb][w][0][cg], y = red[pb][w][1][cg];
-            kv.x += x.x; kv.y += x.y; kv.z += x.z; kv.w += x.w;
-            sq.x += y.x; sq.y += y.y; sq.z += y.z; sq.w += y.w;
-        }
-
-        // 6. delta, readout, update.  kv and sq were taken over raw k and q: scale by rk and rq here.
-        const float4 v4 = reinterpret_cast<const float4 *>(vs[pb])[cg];
-        float4 d, o;
-        d.x = (v4.x - gamma * (kv.x * rk)) * beta;
-        d.y = (v4.y - gamma * (kv.y * rk)) * beta;
-        d.z = (v4.z - gamma * (kv.z * rk)) * beta;
-        d.w = (v4.w - gamma * (kv.w * rk)) * beta;
-        o.x = fmaf(gamma, sq.x * rq, kq * d.x) * scale;
-        o.y = fmaf(gamma, sq.y * rq, kq * d.y) * scale;
-        o.z = fmaf(gamma, sq.z * rq, kq * d.z) * scale;
-        o.w = fmaf(gamma, sq.w * rq, kq * d.w) * scale;
-        const float4 dk4 = make_float4(d.x * rk, d.y * rk, d.z * rk, d.w * rk);  // k enters raw below
-#pragma unroll
-        for (int j = 0; j < CH; ++j)
-#pragma unroll
-            for (int r = 0; r < GROWS; ++r) {
-                const float kr = ksf[CH * rg + j + NG * r];
-                float4 &sv = s[j][r];
-                sv.x = fmaf(kr, dk4.x, gamma * sv.x);
-                sv.y = fmaf(kr, dk4.y, gamma * sv.y);
-                sv.z = fmaf(kr, dk4.z, gamma * sv.z);
-                sv.w = fmaf(kr, dk4.w, gamma * sv.w);
+                vs[pb][tid - DK] = FUSED ? c0.out() : a.v[(bt * a.nvh + h) * DV + (tid - DK)];
             }
 
-        // 7. output: wave 0 holds every column twice (lanes l and l + 32)
-        if (wave == 0 && !replay) {
-            if (FUSED) {
-                // gated RMSNorm on = o * rsqrt(mean o^2 + eps) * w * act(z) (faie2fn.cu:1422-1424); the wave sum
-                // counts each column twice, exactly, so halve it
-                const float ss = 0.5f * wave_sum(o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w);
-                const float rn = rsqrtf(ss / DV + a.eps);
-                if (lane < 32) {
-                    float4 r;
-                    if (a.gate_act == 0) {
-                        r.x = o.x * rn * w4.x * sigmoidf_(z4.x);
-                        r.y = o.y * rn * w4.y * sigmoidf_(z4.y);
-                        r.z = o.z * rn * w4.z * sigmoidf_(z4.z);
-                        r.w = o.w * rn * w4.w * sigmoidf_(z4.w);
-                    } else {
-                        r.x = o.x * rn * w4.x * siluf_(z4.x);
-                        r.y = o.y * rn * w4.y * siluf_(z4.y);
-                        r.z = o.z * rn * w4.z * siluf_(z4.z);
-                        r.w = o.w * rn * w4.w * siluf_(z4.w);
-                    }
-                    bst4(buf(a.out + bt * a.nvh * DV + (size_t) h * DV, DV * 4), oz, 0, r);
+            lds_barrier();
+            // 4. gates (uniform per head): beta = sigmoid(b), gamma = exp(ssm_a * softplus(a + dt_bias)), softplus
+            //    the identity above 20 (faie2fn.cu:1407-1410)
+            if (xab) {
+                ga = abp[0].x;
+                gb = abp[0].y;
+    #pragma unroll
+                for (int w = 1; w < WAVES; ++w) {
+                    ga += abp[w].x;
+                    gb += abp[w].y;
                 }
-            } else if (lane < 32) {
-                bst4(buf(a.out + (bt * a.nvh + h) * DV, DV * 4), oz, 0, o);
+            }
+            float beta, gamma;
+            if (FUSED && ONE) {
+                gdn_gates(ga, gb, dtb, ssa, beta, gamma);
+            } else if (FUSED) {
+                beta = readlane(lbeta, u - u0);
+                gamma = readlane(lgamma, u - u0);
+            } else {
+                beta = a.beta[bt * a.nvh + h];
+                gamma = expf(a.g[bt * a.nvh + h]);
+            }
+
+            // L2 factors x * rsqrt(sum x^2 + 1e-6) (faie2fn.cu:1399-1402); the core takes q, k as given
+            float rq = 1.0f, rk = 1.0f;
+            const float sqk = nrm[pb][0][2] + nrm[pb][1][2];
+            if (FUSED) {
+                rq = rsqrtf(nrm[pb][0][0] + nrm[pb][1][0] + 1e-6f);
+                rk = rsqrtf(nrm[pb][0][1] + nrm[pb][1][1] + 1e-6f);
+            }
+            const float kq = sqk * rq * rk;
+
+            // 5. one pass over the registers: column partials of S^T k and S^T q over this thread's rows
+            const float *ksf = reinterpret_cast<const float *>(ks4[pb]), *qsf = reinterpret_cast<const float *>(qs4[pb]);
+            float4 kvp[CH], sqp[CH];
+    #pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                kvp[j] = sqp[j] = f4(0.0f);
+    #pragma unroll
+                for (int r = 0; r < GROWS; ++r) {
+                    const int row = CH * rg + j + NG * r;
+                    const float kr = ksf[row], qr = qsf[row];
+                    const float4 sv = s[j][r];
+                    kvp[j].x = fmaf(sv.x, kr, kvp[j].x);
+                    kvp[j].y = fmaf(sv.y, kr, kvp[j].y);
+                    kvp[j].z = fmaf(sv.z, kr, kvp[j].z);
+                    kvp[j].w = fmaf(sv.w, kr, kvp[j].w);
+                    sqp[j].x = fmaf(sv.x, qr, sqp[j].x);
+                    sqp[j].y = fmaf(sv.y, qr, sqp[j].y);
+                    sqp[j].z = fmaf(sv.z, qr, sqp[j].z);
+                    sqp[j].w = fmaf(sv.w, qr, sqp[j].w);
+                }
+            }
+            // fold row groups 2m and 2m + 1 (lanes l and l ^ 32, or the thread's two groups), then the 8 folded sums
+            // through LDS
+            float4 kvf, sqf;
+            if constexpr (CH == 1) {
+                kvf = make_float4(add_xor32(kvp[0].x), add_xor32(kvp[0].y), add_xor32(kvp[0].z), add_xor32(kvp[0].w));
+                sqf = make_float4(add_xor32(sqp[0].x), add_xor32(sqp[0].y), add_xor32(sqp[0].z), add_xor32(sqp[0].w));
+            } else {
+                kvf = make_float4(kvp[0].x + kvp[1].x, kvp[0].y + kvp[1].y, kvp[0].z + kvp[1].z, kvp[0].w + kvp[1].w);
+                sqf = make_float4(sqp[0].x + sqp[1].x, sqp[0].y + sqp[1].y, sqp[0].z + sqp[1].z, sqp[0].w + sqp[1].w);
+            }
+            if (CH == 2 || lane < 32) {
+                const int m = CH == 1 ? wave : rg;
+                red[pb][m][0][cg] = kvf;
+                red[pb][m][1][cg] = sqf;
+            }
+            lds_barrier();
+            float4 kv = red[pb][0][0][cg], sq = red[pb][0][1][cg];
+    #pragma unroll
+            for (int w = 1; w < NG / 2; ++w) {
+                const float4 x = red[pb][w][0][cg], y = red[pb][w][1][cg];
+                kv.x += x.x; kv.y += x.y; kv.z += x.z; kv.w += x.w;
+                sq.x += y.x; sq.y += y.y; sq.z += y.z; sq.w += y.w;
+            }
+
+            // 6. delta, readout, update.  kv and sq were taken over raw k and q: scale by rk and rq here.
+            const float4 v4 = reinterpret_cast<const float4 *>(vs[pb])[cg];
+            float4 d, o;
+            d.x = (v4.x - gamma * (kv.x * rk)) * beta;
+            d.y = (v4.y - gamma * (kv.y * rk)) * beta;
+            d.z = (v4.z - gamma * (kv.z * rk)) * beta;
+            d.w = (v4.w - gamma * (kv.w * rk)) * beta;
+            o.x = fmaf(gamma, sq.x * rq, kq * d.x) * scale;
+            o.y = fmaf(gamma, sq.y * rq, kq * d.y) * scale;
+            o.z = fmaf(gamma, sq.z * rq, kq * d.z) * scale;
+            o.w = fmaf(gamma, sq.w * rq, kq * d.w) * scale;
+            const float4 dk4 = make_float4(d.x * rk, d.y * rk, d.z * rk, d.w * rk);  // k enters raw below
+    #pragma unroll
+            for (int j = 0; j < CH; ++j)
+    #pragma unroll
+                for (int r = 0; r < GROWS; ++r) {
+                    const float kr = ksf[CH * rg + j + NG * r];
+                    float4 &sv = s[j][r];
+                    sv.x = fmaf(kr, dk4.x, gamma * sv.x);
+                    sv.y = fmaf(kr, dk4.y, gamma * sv.y);
+                    sv.z = fmaf(kr, dk4.z, gamma * sv.z);
+                    sv.w = fmaf(kr, dk4.w, gamma * sv.w);
+                }
+
+            // 7. output: wave 0 holds every column twice (lanes l and l + 32)
+            if (wave == 0 && !replay) {
+                if (FUSED) {
+                    // gated RMSNorm on = o * rsqrt(mean o^2 + eps) * w * act(z) (faie2fn.cu:1422-1424); the wave sum
+                    // counts each column twice, exactly, so halve it
+                    const float ss = 0.5f * wave_sum(o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w);
+                    const float rn = rsqrtf(ss / DV + a.eps);
+                    if (lane < 32) {
+                        float4 r;
+                        if (a.gate_act == 0) {
+                            r.x = o.x * rn * w4.x * sigmoidf_(z4.x);
+                            r.y = o.y * rn * w4.y * sigmoidf_(z4.y);
+                            r.z = o.z * rn * w4.z * sigmoidf_(z4.z);
+                            r.w = o.w * rn * w4.w * sigmoidf_(z4.w);
+                        } else {
+                            r.x = o.x * rn * w4.x * siluf_(z4.x);
+                            r.y = o.y * rn * w4.y * siluf_(z4.y);
+                            r.z = o.z * rn * w4.z * siluf_(z4.z);
+                            r.w = o.w * rn * w4.w * siluf_(z4.w);
+                        }
+                        bst4(buf(a.out + bt * a.nvh * DV + (size_t) h * DV, DV * 4), oz, 0, r);
+                    }
+                } else if (lane < 32) {
+                    bst4(buf(a.out + (bt * a.nvh + h) * DV, DV * 4), oz, 0, o);
+                }
             }
         }
     }
