@@ -105,6 +105,11 @@ struct GdnArgs {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
 
+// sigmoid / SiLU on the per-token path with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of the IEEE
+// division sequence: within a few ulp of x / (1 + e^-x), and the one-token and multi-token kernels share them
+__device__ __forceinline__ float sigmoid_r(float x) { return __builtin_amdgcn_rcpf(1.0f + expf(-x)); }
+__device__ __forceinline__ float silu_r(float x) { return x * sigmoid_r(x); }
+
 // Causal depthwise conv (kernel 4, weights oldest tap first) + SiLU (faie2fn.cu:1392-1395) of one channel.
 // The raw inputs of the three previous positions ride in registers across the token loop (hist[0] oldest),
 // as the reference keeps them (faie2fn.cu:1378-1398); the ring is read once before the loop and written once after.
@@ -117,7 +122,7 @@ struct ConvChan {
         acc = fmaf(w.y, hist[1], acc);
         acc = fmaf(w.z, hist[2], acc);
         acc = fmaf(w.w, x, acc);
-        return siluf_(acc);
+        return silu_r(acc);
     }
     __device__ __forceinline__ void shift(float next) {
         hist[0] = hist[1];
@@ -489,15 +494,15 @@ k_gdn(const GdnArgs a) {
                     if (lane < 32) {
                         float4 r;
                         if (a.gate_act == 0) {
-                            r.x = o.x * rn * w4.x * sigmoidf_(z4.x);
-                            r.y = o.y * rn * w4.y * sigmoidf_(z4.y);
-                            r.z = o.z * rn * w4.z * sigmoidf_(z4.z);
-                            r.w = o.w * rn * w4.w * sigmoidf_(z4.w);
+                            r.x = o.x * rn * w4.x * sigmoid_r(z4.x);
+                            r.y = o.y * rn * w4.y * sigmoid_r(z4.y);
+                            r.z = o.z * rn * w4.z * sigmoid_r(z4.z);
+                            r.w = o.w * rn * w4.w * sigmoid_r(z4.w);
                         } else {
-                            r.x = o.x * rn * w4.x * siluf_(z4.x);
-                            r.y = o.y * rn * w4.y * siluf_(z4.y);
-                            r.z = o.z * rn * w4.z * siluf_(z4.z);
-                            r.w = o.w * rn * w4.w * siluf_(z4.w);
+                            r.x = o.x * rn * w4.x * silu_r(z4.x);
+                            r.y = o.y * rn * w4.y * silu_r(z4.y);
+                            r.z = o.z * rn * w4.z * silu_r(z4.z);
+                            r.w = o.w * rn * w4.w * silu_r(z4.w);
                         }
                         bst4(buf(a.out + bt * a.nvh * DV + (size_t) h * DV, DV * 4), oz, 0, r);
                     }
