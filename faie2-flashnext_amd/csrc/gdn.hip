@@ -347,9 +347,9 @@ k_gdn(const GdnArgs a) {
                 // the committed state, before the first new token moves the registers on: S after the replayed tokens,
                 // and the ring slots of the replayed positions (the last up to three; after the shift above hist holds
                 // the raw inputs of positions pos + kr - 3 .. pos + kr - 1)
-    #pragma unroll
+#pragma unroll
                 for (int j = 0; j < CH; ++j)
-    #pragma unroll
+#pragma unroll
                     for (int r = 0; r < GROWS; ++r) st_state(Sb, so + j * DV * 4, r, s[j][r]);
                 if (qk_thr) {
                     if (primary) {
@@ -389,7 +389,7 @@ k_gdn(const GdnArgs a) {
             if (xab) {
                 ga = abp[0].x;
                 gb = abp[0].y;
-    #pragma unroll
+#pragma unroll
                 for (int w = 1; w < WAVES; ++w) {
                     ga += abp[w].x;
                     gb += abp[w].y;
@@ -418,10 +418,10 @@ k_gdn(const GdnArgs a) {
             // 5. one pass over the registers: column partials of S^T k and S^T q over this thread's rows
             const float *ksf = reinterpret_cast<const float *>(ks4[pb]), *qsf = reinterpret_cast<const float *>(qs4[pb]);
             float4 kvp[CH], sqp[CH];
-    #pragma unroll
+#pragma unroll
             for (int j = 0; j < CH; ++j) {
                 kvp[j] = sqp[j] = f4(0.0f);
-    #pragma unroll
+#pragma unroll
                 for (int r = 0; r < GROWS; ++r) {
                     const int row = CH * rg + j + NG * r;
                     const float kr = ksf[row], qr = qsf[row];
@@ -453,7 +453,7 @@ k_gdn(const GdnArgs a) {
             }
             lds_barrier();
             float4 kv = red[pb][0][0][cg], sq = red[pb][0][1][cg];
-    #pragma unroll
+#pragma unroll
             for (int w = 1; w < NG / 2; ++w) {
                 const float4 x = red[pb][w][0][cg], y = red[pb][w][1][cg];
                 kv.x += x.x; kv.y += x.y; kv.z += x.z; kv.w += x.w;
@@ -472,9 +472,9 @@ k_gdn(const GdnArgs a) {
             o.z = fmaf(gamma, sq.z * rq, kq * d.z) * scale;
             o.w = fmaf(gamma, sq.w * rq, kq * d.w) * scale;
             const float4 dk4 = make_float4(d.x * rk, d.y * rk, d.z * rk, d.w * rk);  // k enters raw below
-    #pragma unroll
+#pragma unroll
             for (int j = 0; j < CH; ++j)
-    #pragma unroll
+#pragma unroll
                 for (int r = 0; r < GROWS; ++r) {
                     const float kr = ksf[CH * rg + j + NG * r];
                     float4 &sv = s[j][r];
