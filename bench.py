@@ -54,21 +54,27 @@ def measured_traffic():
 
 
 class GdnStack:
-    """L fused DeltaNet layers of B sequences, every buffer distinct per layer, filled in HBM."""
+    """L fused DeltaNet layers of B sequences, every buffer distinct per layer, filled in HBM; nt tokens per call
+    (nt > 1: the multi-token block, a chunked prefill step; the conv ring then holds the next power of two >= nt + 3
+    slots)."""
 
-    def __init__(self, lib, B, L, seed):
-        self.lib, self.B, self.L = lib, B, L
+    def __init__(self, lib, B, L, seed, nt=1):
+        self.lib, self.B, self.L, self.nt = lib, B, L, nt
+        self.ring = 4
+        while self.ring < nt + 3:
+            self.ring *= 2
+        R = self.ring
         self.pos = hiprt.Buf.like(np.zeros(B, np.int32))
         self.layers = []
         for il in range(L):
             lay = fn_synth.BlockLayer(B=1, config=2, layer=il)  # per-layer parameters (small, host-generated)
             d = {
                 "S": hiprt.Buf.empty((B, NVH, DK, DK)),
-                "ring": hiprt.Buf.empty((B, 4, C)),
-                "qkv": hiprt.Buf.empty((B, 1, C)),
-                "z": hiprt.Buf.empty((B, 1, NVH * DK)),
-                "ab": hiprt.Buf.empty((B, 1, 2 * NVH)),
-                "out": hiprt.Buf.empty((B, 1, NVH * DK)),
+                "ring": hiprt.Buf.empty((B, R, C)),
+                "qkv": hiprt.Buf.empty((B, nt, C)),
+                "z": hiprt.Buf.empty((B, nt, NVH * DK)),
+                "ab": hiprt.Buf.empty((B, nt, 2 * NVH)),
+                "out": hiprt.Buf.empty((B, nt, NVH * DK)),
                 "conv_w": hiprt.Buf.like(lay.conv_w),
                 "dt": hiprt.Buf.like(lay.dt_bias),
                 "sa": hiprt.Buf.like(lay.ssm_a),
@@ -76,20 +82,20 @@ class GdnStack:
             }
             s = seed * 1000003 + il * 17
             lib.fill_normal_dev(d["S"].ptr, B * NVH * DK * DK, s + 1, 0.0, 0.02)
-            lib.fill_normal_dev(d["ring"].ptr, B * 4 * C, s + 2)
-            lib.fill_normal_dev(d["qkv"].ptr, B * C, s + 3)
-            lib.fill_normal_dev(d["z"].ptr, B * NVH * DK, s + 4)
-            lib.fill_normal_dev(d["ab"].ptr, B * 2 * NVH, s + 5)
+            lib.fill_normal_dev(d["ring"].ptr, B * R * C, s + 2)
+            lib.fill_normal_dev(d["qkv"].ptr, B * nt * C, s + 3)
+            lib.fill_normal_dev(d["z"].ptr, B * nt * NVH * DK, s + 4)
+            lib.fill_normal_dev(d["ab"].ptr, B * nt * 2 * NVH, s + 5)
             self.layers.append(d)
         hiprt.sync()
 
     def launch(self, stream, advance=True):
         for d in self.layers:
-            self.lib.gdn_block_dev(self.B, NKH, NVH, 1, 4, self.pos.ptr, d["qkv"].ptr, d["conv_w"].ptr, d["ring"].ptr,
-                                   d["ab"].ptr, d["dt"].ptr, d["sa"].ptr, d["S"].ptr, d["z"].ptr, d["nw"].ptr,
-                                   d["out"].ptr, stream.handle)
+            self.lib.gdn_block_dev(self.B, NKH, NVH, self.nt, self.ring, self.pos.ptr, d["qkv"].ptr, d["conv_w"].ptr,
+                                   d["ring"].ptr, d["ab"].ptr, d["dt"].ptr, d["sa"].ptr, d["S"].ptr, d["z"].ptr,
+                                   d["nw"].ptr, d["out"].ptr, stream.handle)
         if advance:
-            self.lib.advance_dev(self.pos.ptr, self.B, 1, stream.handle)
+            self.lib.advance_dev(self.pos.ptr, self.B, self.nt, stream.handle)
 
     def free(self):
         for d in self.layers:
@@ -606,6 +612,16 @@ def main():
                 "ms_per_step": round(ms, 4), "us_per_layer_step": round(ms * 1e3 / 36, 2),
                 "draft_tokens_per_s": round(64 * nt_v * 1e3 / ms, 1), "gbs": round(36 * by / (ms * 1e-3) / 1e9, 1)}
             log(f"[bench] config 2 verify nt={nt_v} kr={kr_v}: {ms * 1e3 / 36:.2f} us/layer-step")
+        # config 2 as a chunked prefill step: nt tokens per call through the committed multi-token block (the bytes
+        # are the verify formula with nothing replayed)
+        g4 = GdnStack(lib, 64, 36, seed=7, nt=4)
+        ms = time_graph(stream, lambda: g4.launch(stream, advance=False), steps, warmup)
+        g4.free()
+        by = fn_synth.gdn_verify_bytes(64, 4, 0)
+        extra["config2_prefill_b64_nt4"] = {
+            "ms_per_step": round(ms, 4), "us_per_layer_step": round(ms * 1e3 / 36, 2),
+            "tokens_per_s": round(64 * 4 * 1e3 / ms, 1), "gbs": round(36 * by / (ms * 1e-3) / 1e9, 1)}
+        log(f"[bench] config 2 prefill nt=4: {ms * 1e3 / 36:.2f} us/layer-step")
     if not args.no_extra and not args.gdn_only:
         # config 3: GQA decode
         for Bq, ctx, nl in ((1, 4096, 32), (1, 32768, 8), (1, 131072, 2), (16, 32768, 2)):
