@@ -1,6 +1,6 @@
 """Benchmark of the FAIE2-FlashNext decode-attention path on one MI355X.
 
-Headline (``value``): BASELINE config 2 -- the fused gated-DeltaNet block at batch 64 (hidden 2048: 16 key heads,
+Headline (``value``): config 2 -- the fused gated-DeltaNet block at batch 64 (hidden 2048: 16 key heads,
 32 value heads, dk = dv = 128, mixed channel 8192), a stack of 36 layers with distinct state, weights and inputs
 per layer (4.6 GB of fp32 state, far above the 256 MB Infinity Cache).  One step = one decode token for all 64
 sequences through all 36 layers, replayed as one hipGraph; inputs are resident in HBM before the timed region.
@@ -12,7 +12,7 @@ speculative verify steps (nt new tokens, the previous step's accepted tokens com
 the streaming-copy yardstick, and the float64 CPU oracle timed on this box's host cores (``cpu_baseline``).
 
 Also (``extra``): the GEMV of the projections around the path (GGUF formats, cold weights) at the reference model's
-and BASELINE's shapes.
+and the benchmark configs' shapes (hidden 2048).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu] [--gemv] [--counters]
 """
@@ -188,8 +188,8 @@ def random_gguf(qtype, rows, cols, rng):
 
 
 class LayerStack:
-    """L DeltaNet decode layers of one sequence with the projections either side of the block, at BASELINE's hidden
-    2048: GEMV qkv (IQ4_XS 8192 x 2048), z (Q6_K 4096 x 2048) and alpha/beta (BF16 64 x 2048) from the layer input,
+    """L DeltaNet decode layers of one sequence with the projections either side of the block, at the benchmark
+    configs' hidden 2048: GEMV qkv (IQ4_XS 8192 x 2048), z (Q6_K 4096 x 2048) and alpha/beta (BF16 64 x 2048) from the layer input,
     the fused block, GEMV ssm_out (Q8_0 2048 x 4096) back to the hidden size.  Every layer has its own weights (packed
     once, copied per layer: 29.6 MB a layer, 1.07 GB for 36, beyond the Infinity Cache) and state.  The launches go in
     order on one stream (capturing the three input GEMVs as parallel graph branches measured slower: 33.5 against
@@ -444,8 +444,8 @@ def copy_yardstick(lib, stream, nbytes=1 << 30, reps=20):
     return 2 * nbytes / (ms * 1e-3) / 1e9
 
 
-# the projections on the path: reference model (hidden 2560; flashnext/inspect_fn.txt:77-100, 132-137) and BASELINE
-# hidden 2048 (8192 mixed channels in, 4096 value channels out)
+# the projections on the path: reference model (hidden 2560; flashnext/inspect_fn.txt:77-100, 132-137) and the benchmark
+# configs' hidden 2048 (8192 mixed channels in, 4096 value channels out)
 GEMV_SHAPES = (("qkv_iq4xs", 23, 10240, 2560), ("ssm_out_q8_0", 8, 2560, 6144), ("z_q6k", 14, 6144, 2560),
                ("attn_q_iq4xs", 23, 12288, 2560), ("attn_v_q6k", 14, 512, 2560), ("ab_bf16", 30, 96, 2560),
                ("qkv2048_iq4xs", 23, 8192, 2048), ("ssm_out2048_q8_0", 8, 2048, 4096))

@@ -119,7 +119,7 @@ def test_gemv_hooks_validate_before_device_work(fnlib):
 
 
 def test_gemv_plan_shapes(fnlib):
-    """Plans of the projection shapes around the path (BASELINE hidden 2048 and the reference model's 2560)."""
+    """Plans of the projection shapes around the path (the benchmark configs' hidden 2048 and the reference model's 2560)."""
     for qtype, rows, cols in [(23, 10240, 2560), (8, 2560, 6144), (30, 96, 2560), (14, 512, 2560), (23, 8192, 2048)]:
         gv, waves, ks, rpw, lpr, ntiles, ngroups = fnlib.gemv_plan(qtype, rows, cols)
         assert (gv, waves) == (32, 8) and lpr in (16, 32, 64) and rpw == 8 * 64 // lpr

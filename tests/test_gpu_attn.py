@@ -153,7 +153,7 @@ def test_attn_reference_group_12(fnlib):
 @pytest.mark.parametrize("B,L,nt,pick", [(16, 32768, 1, [0, 7, 15]), (1, 131072, 1, [0]), (16, 32768, 4, [0, 15]),
                                          (1, 32768, 8, [0])])
 def test_attn_full_size_device(fnlib, B, L, nt, pick):
-    """BASELINE config 3 at full size through the device entry point: caches filled in HBM, the oracle run on a
+    """Config 3 at full size through the device entry point: caches filled in HBM, the oracle run on a
     subset of the sequences (they are independent), compared on og and the appended K/V rows.  nt > 1: the last nt
     positions are the new tokens (a verify step at full context)."""
     import fn

@@ -4,7 +4,7 @@ The reference's quant gate (flashnext/test_fn_quants.py:30-37): the GPU decode e
 (error 0), and the GEMV of 8 tokens is within 1e-5 (max|gpu - ref| / max|ref|) of float64 math on the decoded
 weights.  Shapes are those of the projections on the path: the stacked DeltaNet input (qkv), its output (ssm_out),
 the attention q / k / v / o projections and the alpha/beta rows, at the reference model's hidden size 2560 and at
-BASELINE's 2048, plus ragged row counts.  Weights are random bytes with finite fp16 / bf16 scales (the reference's
+the benchmark configs' 2048, plus ragged row counts.  Weights are random bytes with finite fp16 / bf16 scales (the reference's
 real tensors are not in this image).
 
 Every case prints what names it before the GPU call.
@@ -49,7 +49,7 @@ def test_dequant_bit_exact(fnlib, name, rows, cols):
 
 
 # (type, rows, cols): the path's projections in the reference model (engine/faie2fn.cu:2386-2403;
-# flashnext/inspect_fn.txt:77, 95-100, 132-137) and at BASELINE's hidden 2048
+# flashnext/inspect_fn.txt:77, 95-100, 132-137) and at the benchmark configs' hidden 2048
 PATH_SHAPES = [
     ("IQ4_XS", 10240, 2560),   # attn_qkv (DeltaNet in)
     ("Q8_0", 2560, 6144),      # ssm_out / attn_output
@@ -57,8 +57,8 @@ PATH_SHAPES = [
     ("Q6_K", 512, 2560),       # attn_v
     ("IQ4_XS", 512, 2560),     # attn_k
     ("Q6_K", 6144, 2560),      # attn_gate (z) of layer 1
-    ("IQ4_XS", 8192, 2048),    # BASELINE qkv: 8192 mixed channels from hidden 2048
-    ("Q8_0", 2048, 4096),      # BASELINE ssm_out
+    ("IQ4_XS", 8192, 2048),    # config 1/2 qkv: 8192 mixed channels from hidden 2048
+    ("Q8_0", 2048, 4096),      # config 1/2 ssm_out
 ]
 
 
