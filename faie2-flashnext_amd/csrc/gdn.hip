@@ -274,9 +274,14 @@ k_gdn(const GdnArgs a) {
         }
     };
     float ga = 0.0f, gb = 0.0f, dtb = 0.0f, ssa = 0.0f;  // one token's alpha, beta logits; the head's gate params
-    float lbeta = 0.0f, lgamma = 0.0f;                   // multi-token: gates of token u0 + lane
+    float lbeta = 0.0f, lgamma = 0.0f;                   // gates of token u0 + lane (one token: its gates)
     if (FUSED) {
         if (!ONE) lane_logits(0, ga, gb);
+        if (ONE && !xab) {
+            const float *ab0 = a.ab + (size_t) b * a.nt * 2 * a.nvh;
+            ga = ab0[h];
+            gb = ab0[a.nvh + h];
+        }
         dtb = a.dt_bias[h];
         ssa = a.ssm_a[h];
     }
@@ -289,7 +294,9 @@ k_gdn(const GdnArgs a) {
     for (int j = 0; j < CH; ++j)
 #pragma unroll
         for (int r = 0; r < GROWS; ++r) s[j][r] = ld_state(Sb, so + j * DV * 4, r);
-    if (FUSED && !ONE) gdn_gates(ga, gb, dtb, ssa, lbeta, lgamma);  // under the tile's loads
+    // gates under the tile's loads: of the first 64 tokens (lane-parallel), or of the one token (uniform; with the
+    // fused alpha/beta projection they wait for its sums)
+    if (FUSED && (!ONE || !xab)) gdn_gates(ga, gb, dtb, ssa, lbeta, lgamma);
 
     const float scale = 0.08838834764831845f;  // 1/sqrt(128), faie2fn.cu:1352
 
@@ -312,11 +319,6 @@ k_gdn(const GdnArgs a) {
             nz = bld4(buf(a.z + ((size_t) b * a.nt + (u_ - kr)) * a.nvh * DV + (size_t) h * DV, DV * 4), oz, 0); \
     } while (0)
     if (FUSED) {
-        if (ONE && !xab) {
-            const float *ab0 = a.ab + (size_t) b * a.nt * 2 * a.nvh;
-            ga = ab0[h];
-            gb = ab0[a.nvh + h];
-        }
         if (!ONE && ntot > 1) GDN_PREFETCH(1);
     }
 
@@ -398,7 +400,12 @@ k_gdn(const GdnArgs a) {
             }
             float beta, gamma;
             if (FUSED && ONE) {
-                gdn_gates(ga, gb, dtb, ssa, beta, gamma);
+                if (xab) {
+                    gdn_gates(ga, gb, dtb, ssa, beta, gamma);
+                } else {
+                    beta = lbeta;
+                    gamma = lgamma;
+                }
             } else if (FUSED) {
                 beta = readlane(lbeta, u - u0);
                 gamma = readlane(lgamma, u - u0);
