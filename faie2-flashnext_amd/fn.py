@@ -37,7 +37,11 @@ SYMBOLS = (
     "fn_attn_qsa_dev", "fn_attn_qsa_work_bytes", "fn_ix_blocks_dev", "fn_test_attn_qsa",
     "fn_gemv_packed_bytes", "fn_gemv_pack_dev", "fn_dequant_dev", "fn_gemv_work_bytes", "fn_gemv_dev",
     "fn_gdn_verify_dev", "fn_advance_by_dev", "fn_gdn_block_xab_dev",
+    "fn_attn_noalloc_dev",
 )
+
+# bytes of the device array fn_attn_noalloc_dev takes its workspace from (FN_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 # GGUF type ids of the weight formats this library reads (engine/faie2fn.cu:78-81), and (values, bytes) per block
 QTYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ4_XS=23, BF16=30)
@@ -103,6 +107,7 @@ class FN:
         d.fn_gdn_block_xab_dev.argtypes = [i] * 8 + [VP] * 5 + [i] + [VP] * 6 + [C.c_float, VP, VP]
         d.fn_advance_by_dev.argtypes = [VP, VP, i, VP]
         d.fn_attn_dev.argtypes = ([i] * 5 + [C.c_float, C.c_float, i, i] + [VP] * 8 + [i, VP, C.c_size_t, VP, VP])
+        d.fn_attn_noalloc_dev.argtypes = ([i] * 5 + [C.c_float, C.c_float, i, i] + [VP] * 8 + [i, VP, VP])
         d.fn_attn_work_bytes.restype = C.c_size_t
         d.fn_attn_work_bytes.argtypes = [i] * 5
         d.fn_attn_nsplit.argtypes = [i] * 4
@@ -289,6 +294,11 @@ class FN:
                  stream=0, hd=256, nrot=64, theta=1e7, eps=1e-6):
         self.check(self.d.fn_attn_dev(B, nq, nkv, hd, nrot, float(theta), float(eps), nt, max_ctx, pos, qg, k, v, wq,
                                       wk, Kc, Vc, nsplit, work, work_bytes, og, stream))
+
+    def attn_noalloc_dev(self, B, nq, nkv, nt, max_ctx, pos, qg, k, v, wq, wk, Kc, Vc, nsplit, og, stream=0, hd=256,
+                         nrot=64, theta=1e7, eps=1e-6):
+        self.check(self.d.fn_attn_noalloc_dev(B, nq, nkv, hd, nrot, float(theta), float(eps), nt, max_ctx, pos, qg, k,
+                                              v, wq, wk, Kc, Vc, nsplit, og, stream))
 
     def attn_qsa_work_bytes(self, B, nq, nt, nsplit, max_ctx, top=512, hd=256):
         return int(self.d.fn_attn_qsa_work_bytes(B, nq, nt, hd, nsplit, max_ctx, top))

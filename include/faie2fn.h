@@ -163,6 +163,17 @@ size_t fn_attn_work_bytes(int B, int nq, int nt, int hd, int nsplit);
 /* The split count fn_test_attn uses when given 0, for a context of ctx keys. */
 int fn_attn_nsplit(int B, int nkv, int nt, int ctx);
 
+/* GQA decode that allocates nothing.  No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results (bit for bit) as fn_attn_dev, without work / work_bytes: the workspace is a
+ * file-scope device array of FN_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends.  Shapes whose
+ * fn_attn_work_bytes() exceeds it are rejected with an error.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (two streams or threads) race; calls in one stream order do not. */
+#define FN_NOALLOC_SCRATCH_BYTES (32u << 20)
+int fn_attn_noalloc_dev(int B, int nq, int nkv, int hd, int nrot, float theta, float eps, int nt, int max_ctx,
+                        const int32_t *pos, const float *qg, const float *k, const float *v, const float *wq,
+                        const float *wk, float *Kc, float *Vc, int nsplit, float *og, void *stream);
+
 /* pos[b] += nt for b < B, on the stream (the reference's k_advance, faie2fn.cu:1905). */
 int fn_advance_dev(int32_t *pos, int B, int nt, void *stream);
 

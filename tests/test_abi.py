@@ -175,3 +175,18 @@ def test_block_xab_validates_before_device_work(fnlib):
     assert call(hidden=0) == -1 and b"multiple of 4" in d.fn_error()
     assert call(x=a + 4) == -1 and b"16-byte aligned" in d.fn_error()
     assert call(w=a + 8) == -1 and b"16-byte aligned" in d.fn_error()
+
+
+def test_noalloc_attn_rejects_oversize(fnlib):
+    """fn_attn_noalloc_dev refuses shapes whose workspace exceeds its built-in device array, before touching the
+    device; shapes that fit are sized by the same fn_attn_work_bytes as fn_attn_dev."""
+    d = fnlib.d
+    assert len(d.fn_attn_noalloc_dev.argtypes) == 20
+    big = fnlib.attn_work_bytes(64, 16, 8, 64)
+    assert big > fn.NOALLOC_SCRATCH_BYTES
+    assert d.fn_attn_noalloc_dev(64, 16, 2, 256, 64, 1e7, 1e-6, 8, 4096, *([None] * 8), 64, None, None) == -1
+    assert b"workspace" in d.fn_error() and str(fn.NOALLOC_SCRATCH_BYTES).encode() in d.fn_error()
+    assert d.fn_attn_noalloc_dev(1, 16, 2, 256, 64, 1e7, 1e-6, 1, 4096, *([None] * 8), 0, None, None) == -1
+    # the decode shapes of the benchmark fit: B = 16 at 32K and B = 1 at 128K with their automatic split counts
+    for B, L in ((16, 32768), (1, 131072), (1, 4096)):
+        assert fnlib.attn_work_bytes(B, 16, 1, fnlib.attn_nsplit(B, 2, 1, L)) <= fn.NOALLOC_SCRATCH_BYTES
