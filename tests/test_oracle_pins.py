@@ -436,3 +436,63 @@ def test_masked_attention_reduces_to_dense():
         sc = keys @ Q[h] / np.sqrt(hd)
         p = np.exp(sc - sc.max())
         assert np.allclose(tail[0, 0, h], (p @ vals) / p.sum() * gate[h], atol=1e-14)
+
+
+def _ix_case(dots, ixd=128, nblk=3):
+    """Qix [1][1][ixh][ixd], BKc [1][nblk][ixd] with q_h = a_h e_h and block key k_j = sum_h c_jh e_h, so that
+    q_h . k_j = dots[j][h] exactly (one nonzero product per dot)."""
+    dots = np.asarray(dots, np.float64)
+    ixh = dots.shape[1]
+    Q = np.zeros((1, 1, ixh, ixd))
+    K = np.zeros((1, nblk, ixd))
+    for h in range(ixh):
+        Q[0, 0, h, h] = 2.0
+    for j in range(dots.shape[0]):
+        for h in range(ixh):
+            K[0, j, h] = dots[j, h] / 2.0
+    return Q, K
+
+
+def test_ix_score_closed_forms():
+    """orc_ix_score (k_ix_score, faie2fn.cu:1534-1555): score_j = sum_h relu(q_h . k_j) / sqrt(ixd), pinned by closed
+    forms that each plausible misreading fails: one head positive and the rest negative gives that dot / sqrt(128);
+    all heads negative give exactly 0; mixed signs give the sum of the positive dots only (relu of the summed dots
+    would give their difference); the scale is 1/sqrt(128) (not 1/128 or 1); only the (pos + t + 1) / 4 complete
+    blocks are scored."""
+    dots = [[5.0, -1.0, -2.0, -3.0],      # one head positive
+            [-1.0, -2.0, -0.5, -7.0],     # all negative
+            [3.0, -2.0, 4.0, -6.0]]       # mixed: relu per head 7, relu of the sum 0
+    Q, K = _ix_case(dots, nblk=4)
+    # pos 11, nt 1: (11 + 1) / 4 = 3 complete blocks; block 3 is left untouched
+    sc = oracle.ix_score(Q, K, np.array([11]), max_ctx=16)
+    r = np.sqrt(128.0)
+    assert sc[0, 0, 0] == pytest.approx(5.0 / r, rel=1e-15)
+    assert sc[0, 0, 1] == 0.0
+    assert sc[0, 0, 2] == pytest.approx(7.0 / r, rel=1e-15)
+    assert sc[0, 0, 3] == 0.0
+    # a sequence one position shorter has one complete block fewer
+    sc2 = oracle.ix_score(Q, K, np.array([10]), max_ctx=16)
+    assert sc2[0, 0, 2] == 0.0 and sc2[0, 0, 0] == sc[0, 0, 0]
+
+
+def test_ix_score_exact_brute_force():
+    """Exact rational brute force at ixd = 4 (scale 1/2 exactly), 2 heads, 2 tokens, random small integers: the
+    oracle's float64 scores equal sum_h max(0, q_h . k_j) / 2 computed in Fractions (integers make every float64
+    product and sum exact)."""
+    rng = np.random.default_rng(31)
+    B, nt, ixh, ixd, ixr, max_ctx = 2, 2, 2, 4, 4, 32
+    Q = rng.integers(-5, 6, size=(B, nt, ixh, ixd)).astype(np.float64)
+    K = rng.integers(-5, 6, size=(B, max_ctx // ixr, ixd)).astype(np.float64)
+    pos = np.array([9, 22])
+    sc = oracle.ix_score(Q, K, pos, max_ctx, ixr)
+    for b in range(B):
+        for t in range(nt):
+            nb = (pos[b] + t + 1) // ixr
+            for j in range(max_ctx // ixr):
+                want = Fraction(0)
+                if j < nb:
+                    for h in range(ixh):
+                        p = sum(Fraction(int(Q[b, t, h, d])) * Fraction(int(K[b, j, d])) for d in range(ixd))
+                        want += max(Fraction(0), p)
+                    want /= 2
+                assert Fraction(sc[b, t, j]) == want, (b, t, j)
