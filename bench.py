@@ -510,6 +510,12 @@ def main():
     ap.add_argument("--counters", action="store_true",
                     help="counter-collection workload only: 3 plain copies of 1 GiB (the calibration kernel) and one "
                          "eager pass of the config-2 stack (36 dispatches of the fused DeltaNet kernel)")
+    ap.add_argument("--counters-decode", action="store_true",
+                    help="counter-collection workload only: one eager pass of the config-2 stack (36 dispatches of "
+                         "k_gdn<3> at B=64), then 2 eager GQA decode layer-steps at B=16, 32K context "
+                         "(k_attn_split<8, PREP> + k_attn_combine)")
+    ap.add_argument("--attn-only", action="store_true",
+                    help="of the extra legs run only the dense GQA decode ones (config 3, one new token)")
     ap.add_argument("--counters-attn", action="store_true",
                     help="counter-collection workload only: 5 eager multi-token GQA layer-steps at B=16, 32K context, "
                          "nt=8 then 5 at nt=4 (k_attn_split_mt<2>)")
@@ -540,6 +546,18 @@ def main():
                           "flops_nt8": fn_synth.attn_flops(16, 32768, nt=8),
                           "flops_nt4": fn_synth.attn_flops(16, 32768, nt=4)}))
         return
+    if args.counters_decode:
+        st = GdnStack(lib, 64, 36, seed=2)
+        st.launch(stream, advance=False)
+        stream.sync()
+        st.free()
+        at = AttnStack(lib, 16, 32768, 2, seed=3)
+        at.launch(stream)
+        stream.sync()
+        at.free()
+        print(json.dumps({"counters_workload": "fused DeltaNet B=64 x36 (k_gdn<3>), GQA decode B=16 ctx=32768 x2 "
+                                               "(k_attn_split<8, PREP>, k_attn_combine)"}))
+        return
     if args.counters:
         nb = 1 << 30
         a, b = hiprt.Buf(nb), hiprt.Buf(nb)
@@ -569,7 +587,7 @@ def main():
     log(f"[bench] config 2: {ms_step:.3f} ms/step, {ms_kern * 1e3:.2f} us/layer-step, {achieved:.0f} GB/s")
 
     extra = {}
-    if not args.no_extra:
+    if not args.no_extra and not args.attn_only:
         extra["copy_gbs"] = round(copy_yardstick(lib, stream), 1)
         log(f"[bench] streaming copy {extra['copy_gbs']} GB/s")
         # config 0: core, B = 1 (256 layers of 2 MiB state, so the working set is twice the Infinity Cache)
@@ -624,7 +642,8 @@ def main():
         log(f"[bench] config 2 prefill nt=4: {ms * 1e3 / 36:.2f} us/layer-step")
     if not args.no_extra and not args.gdn_only:
         # config 3: GQA decode
-        for Bq, ctx, nl in ((1, 4096, 32), (1, 32768, 8), (1, 131072, 2), (16, 32768, 2)):
+        for Bq, ctx, nl in ((1, 4096, 32), (1, 32768, 8), (1, 131072, 2), (16, 4096, 8), (16, 32768, 2),
+                            (16, 131072, 1)):
             at = AttnStack(lib, Bq, ctx, nl, seed=3)
             ms = time_graph(stream, lambda: at.launch(stream), steps, warmup) / nl
             nsplit = at.nsplit
@@ -633,51 +652,52 @@ def main():
             extra[f"config3_gqa_b{Bq}_ctx{ctx}"] = {"us_per_layer_step": round(ms * 1e3, 2),
                                                    "gbs": round(by / (ms * 1e-3) / 1e9, 1), "nsplit": nsplit}
             log(f"[bench] config 3 B={Bq} ctx={ctx}: {ms * 1e3:.1f} us, {by / (ms * 1e-3) / 1e9:.0f} GB/s")
-        # config 3 multi-token (speculative verify / chunked prefill): nt new tokens per sequence share one K/V pass
-        # on the matrix cores; GB/s counts K/V once, TFLOP/s the fp32 products (peak 157.3)
-        for Bq, ctx, nl, ntq in ((1, 32768, 8, 4), (16, 32768, 2, 4), (16, 32768, 2, 8)):
-            at = AttnStack(lib, Bq, ctx, nl, seed=4, nt=ntq)
-            ms = time_graph(stream, lambda: at.launch(stream), steps, warmup) / nl
-            nsplit = at.nsplit
-            at.free()
-            by, fl = fn_synth.attn_bytes(Bq, ctx, nt=ntq), fn_synth.attn_flops(Bq, ctx, nt=ntq)
-            extra[f"config3_gqa_b{Bq}_ctx{ctx}_nt{ntq}"] = {
-                "us_per_layer_step": round(ms * 1e3, 2), "draft_tokens_per_s": round(Bq * ntq * 1e3 / ms, 1),
-                "gbs": round(by / (ms * 1e-3) / 1e9, 1), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
-                "nsplit": nsplit}
-            log(f"[bench] config 3 B={Bq} ctx={ctx} nt={ntq}: {ms * 1e3:.1f} us, {by / (ms * 1e-3) / 1e9:.0f} GB/s, "
-                f"{fl / (ms * 1e-3) / 1e12:.1f} TFLOP/s")
-        # config 3 through the reference's own attention: QSA indexer active past 2048 keys (top 512 blocks of 4)
-        for Bq, ctx, nl in ((1, 32768, 8), (1, 131072, 4), (16, 32768, 2)):
-            qs = QsaStack(lib, Bq, ctx, nl, seed=5)
-            ms = time_graph(stream, lambda: qs.launch(stream), steps, warmup) / nl
-            qs.free()
-            by = fn_synth.attn_qsa_bytes(Bq, ctx)
-            extra[f"config3_qsa_b{Bq}_ctx{ctx}"] = {"us_per_layer_step": round(ms * 1e3, 2), "algorithmic_bytes": by,
-                                                   "gbs": round(by / (ms * 1e-3) / 1e9, 1)}
-            log(f"[bench] config 3 QSA B={Bq} ctx={ctx}: {ms * 1e3:.1f} us")
-        # the host-array hook on the same layer-step (PCIe-inclusive: state, inputs and outputs cross the bus)
-        lay = fn_synth.BlockLayer(B=64, config=2, layer=0)
-        qkv, ab, z = lay.step()
-        S, conv = lay.S0.copy(), lay.conv0.copy()
-        lib.gdn_block(qkv, lay.conv_w, conv, ab, lay.dt_bias, lay.ssm_a, S, z, lay.norm_w, NKH, NVH)
-        t0 = time.perf_counter()
-        lib.gdn_block(qkv, lay.conv_w, conv, ab, lay.dt_bias, lay.ssm_a, S, z, lay.norm_w, NKH, NVH)
-        hook_ms = (time.perf_counter() - t0) * 1e3
-        extra["config2_host_hook_pcie_inclusive"] = {"ms_per_layer_step": round(hook_ms, 2),
-                                                     "gbs": round(fn_synth.gdn_block_bytes(64) / hook_ms / 1e6, 1)}
-        extra.update(gemv_extras(lib))
-        ms, nbytes = hybrid_config4(lib, steps, warmup)
-        ms_v, by_v = hybrid_verify(lib, stream, steps, warmup)
-        extra["config4_hybrid_verify_b16_ctx32768_nt4_kr2"] = {
-            "ms_per_step": round(ms_v, 4), "draft_tokens_per_s": round(16 * 4 * 1e3 / ms_v, 1),
-            "bytes_per_step": by_v, "gbs": round(by_v / (ms_v * 1e-3) / 1e9, 1)}
-        log(f"[bench] config 4 as a verify step (nt 4, kr 2): {ms_v:.3f} ms/step, "
-            f"{16 * 4 * 1e3 / ms_v:.0f} draft tokens/s")
-        extra["config4_hybrid_b16_ctx32768"] = {"ms_per_step": round(ms, 4), "us_per_token": round(ms * 1e3 / 16, 2),
-                                               "tokens_per_s": round(16 * 1e3 / ms, 1), "bytes_per_step": nbytes,
-                                               "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                                               "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        if not args.attn_only:
+            # config 3 multi-token (speculative verify / chunked prefill): nt new tokens per sequence share one K/V pass
+            # on the matrix cores; GB/s counts K/V once, TFLOP/s the fp32 products (peak 157.3)
+            for Bq, ctx, nl, ntq in ((1, 32768, 8, 4), (16, 32768, 2, 4), (16, 32768, 2, 8)):
+                at = AttnStack(lib, Bq, ctx, nl, seed=4, nt=ntq)
+                ms = time_graph(stream, lambda: at.launch(stream), steps, warmup) / nl
+                nsplit = at.nsplit
+                at.free()
+                by, fl = fn_synth.attn_bytes(Bq, ctx, nt=ntq), fn_synth.attn_flops(Bq, ctx, nt=ntq)
+                extra[f"config3_gqa_b{Bq}_ctx{ctx}_nt{ntq}"] = {
+                    "us_per_layer_step": round(ms * 1e3, 2), "draft_tokens_per_s": round(Bq * ntq * 1e3 / ms, 1),
+                    "gbs": round(by / (ms * 1e-3) / 1e9, 1), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+                    "nsplit": nsplit}
+                log(f"[bench] config 3 B={Bq} ctx={ctx} nt={ntq}: {ms * 1e3:.1f} us, {by / (ms * 1e-3) / 1e9:.0f} GB/s, "
+                    f"{fl / (ms * 1e-3) / 1e12:.1f} TFLOP/s")
+            # config 3 through the reference's own attention: QSA indexer active past 2048 keys (top 512 blocks of 4)
+            for Bq, ctx, nl in ((1, 32768, 8), (1, 131072, 4), (16, 32768, 2)):
+                qs = QsaStack(lib, Bq, ctx, nl, seed=5)
+                ms = time_graph(stream, lambda: qs.launch(stream), steps, warmup) / nl
+                qs.free()
+                by = fn_synth.attn_qsa_bytes(Bq, ctx)
+                extra[f"config3_qsa_b{Bq}_ctx{ctx}"] = {"us_per_layer_step": round(ms * 1e3, 2), "algorithmic_bytes": by,
+                                                       "gbs": round(by / (ms * 1e-3) / 1e9, 1)}
+                log(f"[bench] config 3 QSA B={Bq} ctx={ctx}: {ms * 1e3:.1f} us")
+            # the host-array hook on the same layer-step (PCIe-inclusive: state, inputs and outputs cross the bus)
+            lay = fn_synth.BlockLayer(B=64, config=2, layer=0)
+            qkv, ab, z = lay.step()
+            S, conv = lay.S0.copy(), lay.conv0.copy()
+            lib.gdn_block(qkv, lay.conv_w, conv, ab, lay.dt_bias, lay.ssm_a, S, z, lay.norm_w, NKH, NVH)
+            t0 = time.perf_counter()
+            lib.gdn_block(qkv, lay.conv_w, conv, ab, lay.dt_bias, lay.ssm_a, S, z, lay.norm_w, NKH, NVH)
+            hook_ms = (time.perf_counter() - t0) * 1e3
+            extra["config2_host_hook_pcie_inclusive"] = {"ms_per_layer_step": round(hook_ms, 2),
+                                                         "gbs": round(fn_synth.gdn_block_bytes(64) / hook_ms / 1e6, 1)}
+            extra.update(gemv_extras(lib))
+            ms, nbytes = hybrid_config4(lib, steps, warmup)
+            ms_v, by_v = hybrid_verify(lib, stream, steps, warmup)
+            extra["config4_hybrid_verify_b16_ctx32768_nt4_kr2"] = {
+                "ms_per_step": round(ms_v, 4), "draft_tokens_per_s": round(16 * 4 * 1e3 / ms_v, 1),
+                "bytes_per_step": by_v, "gbs": round(by_v / (ms_v * 1e-3) / 1e9, 1)}
+            log(f"[bench] config 4 as a verify step (nt 4, kr 2): {ms_v:.3f} ms/step, "
+                f"{16 * 4 * 1e3 / ms_v:.0f} draft tokens/s")
+            extra["config4_hybrid_b16_ctx32768"] = {"ms_per_step": round(ms, 4), "us_per_token": round(ms * 1e3 / 16, 2),
+                                                   "tokens_per_s": round(16 * 1e3 / ms, 1), "bytes_per_step": nbytes,
+                                                   "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                                   "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
     for k, v in extra.items():
         log(f"[bench] {k}: {v}")
 

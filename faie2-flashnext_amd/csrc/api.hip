@@ -121,6 +121,12 @@ FN_API int fn_attn_dev(int B, int nq, int nkv, int hd, int nrot, float theta, fl
     return fn::attn_decode_launch(p, (hipStream_t) stream);
 }
 
+FN_API int fn_dev_status(int clear) {
+    unsigned bits = 0;
+    if (fn::status_read(&bits, clear != 0)) return -1;
+    return (int) (bits & 0x7fffffffu);
+}
+
 FN_API int fn_advance_dev(int32_t *pos, int B, int nt, void *stream) {
     return fn::advance_launch(pos, B, nt, (hipStream_t) stream);
 }

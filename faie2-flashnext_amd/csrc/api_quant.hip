@@ -78,14 +78,14 @@ FN_API int fn_gemv_plan(uint32_t type, int rows, int cols, int *out) {
     if (!fn::qlayout(type, rows, cols, L)) return -1;
     if (!out) FN_FAIL("gemv_plan: null pointer");
     const fn::GemvPlan p = fn::gemv_plan(L);
-    const int v[7] = {p.gv, p.waves, p.ks, p.rpw, p.lpr, p.ntiles, p.ngroups};
+    const int v[7] = {p.gv, p.waves, p.ks, p.rpw, p.lpr, p.grid, p.ngroups};
     std::copy(v, v + 7, out);
     return 0;
 }
 
 // the reference's knobs: waves per SM and tile shape belong to its CUDA tiling; split-K is the one that applies
 FN_API void fn_gemv_override(int wpt, int ks, int tb, int warps_per_sm) { fn::gemv_override(wpt, ks, tb, warps_per_sm); }
-FN_API void fn_gemv_waves(int) {}
+FN_API void fn_gemv_waves(int waves) { fn::gemv_persistent(waves); }
 FN_API void fn_bench_hot(int on) { g_bench_hot = on; }
 
 FN_API int fn_bench_gemv(uint32_t type, int rows, int cols, int nt, int iters, float *ms) {

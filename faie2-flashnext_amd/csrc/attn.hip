@@ -48,6 +48,7 @@ struct AttnArgs {
     const int32_t *keys;   // visible-key list per query (QSA) or null (dense)
     const int32_t *nkeys;
     int kstride;           // list stride per query
+    unsigned *status;      // per-device status word: FN_STATUS_POS when a new token falls outside the cache
     float inv_freq[MAXROT / 2];
 };
 
@@ -63,7 +64,10 @@ __global__ void __launch_bounds__(HD) k_attn_prep(const AttnArgs a) {
     __shared__ float red[HD / 64];
     const int bt = blockIdx.x, b = bt / a.nt, t = bt - b * a.nt, j = blockIdx.y, d = threadIdx.x;
     const int P = a.pos[b] + t;
-    if (P < 0 || P >= a.max_ctx) return;  // outside the cache: the host checks positions; never write past it
+    if (P < 0 || P >= a.max_ctx) {  // outside the cache: nothing is written past it; the status word says so
+        if (j == 0 && d == 0) atomicOr(a.status, FN_STATUS_POS);
+        return;
+    }
     const bool isq = j < a.nq;
     const int g = isq ? j / (a.nq / a.nkv) : j - a.nq;
     const float x = isq ? a.qg[((size_t) bt * a.nq + j) * 2 * HD + d] : a.knew[((size_t) bt * a.nkv + g) * HD + d];
@@ -166,6 +170,8 @@ __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
     // the new key is visible (inside the cache) and its slot, the last one (nk - 1 = P for the dense walk, the end of
     // the tail for a key list), falls in this split's tiles
     const bool owner = PREP && P >= 0 && P < a.max_ctx && (nk - 1) / TILE >= tile0 && (nk - 1) / TILE < tile1;
+    // a new token outside the cache is neither appended nor attended past the cache's end; record it once
+    if (PREP && sp_i == 0 && g == 0 && threadIdx.x == 0 && (P < 0 || P >= a.max_ctx)) atomicOr(a.status, FN_STATUS_POS);
 
     if (PREP) {
         if (threadIdx.x < a.nrot / 2) {
@@ -877,6 +883,7 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
     a.B = p.B; a.nq = p.nq; a.nkv = p.nkv; a.nt = p.nt; a.max_ctx = p.max_ctx; a.nsplit = p.nsplit;
     a.nrot = p.nrot; a.eps = p.eps; a.pos = p.pos; a.qg = p.qg; a.knew = p.k; a.vnew = p.v; a.wq = p.wq;
     a.wk = p.wk; a.Kc = p.Kc; a.Vc = p.Vc; a.og = p.og;
+    if (status_word(&a.status)) return -1;
     const size_t bt = (size_t) p.B * p.nt;
     a.Q = p.work;
     a.part_o = a.Q + bt * p.nq * HD;
@@ -940,6 +947,7 @@ int attn_qsa_launch(const AttnDecode &p, const QsaIndexer &ix, hipStream_t st) {
     a.nrot = p.nrot; a.eps = p.eps; a.pos = p.pos; a.qg = p.qg; a.knew = p.k; a.vnew = p.v; a.wq = p.wq;
     a.wk = p.wk; a.Kc = p.Kc; a.Vc = p.Vc; a.og = p.og;
     a.keys = keys; a.nkeys = nkeys; a.kstride = ix.top * 4 + 4;
+    if (status_word(&a.status)) return -1;
     const size_t bt = (size_t) p.B * p.nt;
     a.Q = p.work;
     a.part_o = a.Q + bt * p.nq * HD;

@@ -201,6 +201,23 @@ int path_step(int steps, float *ms) {
     if (!g_eng) FN_FAIL("not loaded");
     Engine &e = *g_eng;
     if (steps < 1) FN_FAIL("path_step: steps must be >= 1");
+    // Positions live in device memory (the caller may write them through FN_BUF_POS), so they are read back before
+    // each call: every step appends one token per sequence to the attention caches, and a sequence whose last
+    // token would land past max_ctx fails the call before anything runs ("context full", the reference's check
+    // on its host counter, faie2fn.cu:2468).
+    if (e.max_ctx > 0) {
+        std::vector<int32_t> ph(e.B);
+        FN_CK(hipMemcpy(ph.data(), e.pos, (size_t) e.B * 4, hipMemcpyDeviceToHost));
+        for (int b = 0; b < e.B; ++b) {
+            if (ph[b] < 0) FN_FAIL("path_step: negative position for sequence " + std::to_string(b));
+            if ((long) ph[b] + steps > e.max_ctx)
+                FN_FAIL("context full: sequence " + std::to_string(b) + " at position " + std::to_string(ph[b]) +
+                        " cannot take " + std::to_string(steps) + " more tokens (max_ctx " +
+                        std::to_string(e.max_ctx) + ")");
+        }
+        unsigned stale = 0;  // bits left by earlier calls outside the engine are not this step's
+        if (status_read(&stale, true)) return -1;
+    }
     if (e.use_graphs && ensure_graph(e)) return -1;
     hipEvent_t a = nullptr, b = nullptr;
     if (ms) {
@@ -221,6 +238,12 @@ int path_step(int steps, float *ms) {
         *ms /= steps;
         (void) hipEventDestroy(a);
         (void) hipEventDestroy(b);
+    }
+    // kernels record what they had to clamp; with the check above nothing should be
+    unsigned bits = 0;
+    if (e.max_ctx > 0) {
+        if (status_read(&bits, true)) return -1;
+        if (bits & FN_STATUS_POS) FN_FAIL("path_step: a token position fell outside the attention cache");
     }
     e.n_past += steps;
     return 0;

@@ -1,6 +1,7 @@
 // Internal launch API of the DeltaNet and attention kernels (device pointers, caller stream).
 #pragma once
 
+#include "../../include/faie2fn.h"
 #include "common.cuh"
 
 #include <algorithm>
@@ -68,6 +69,11 @@ int attn_pick_nsplit(int B, int nkv, int nt, int ctx);
 int attn_decode_launch(const AttnDecode &p, hipStream_t st);
 int advance_launch(int32_t *pos, int B, int nt, hipStream_t st);
 int advance_by_launch(int32_t *pos, const int32_t *kr, int B, hipStream_t st);  // pos[b] += kr[b]
+
+// Per-device status word (FN_STATUS_* bits of include/faie2fn.h): its device address for kernel arguments, and a
+// read (after a device synchronize) that optionally clears it.  Not for use under stream capture.
+int status_word(unsigned **out);
+int status_read(unsigned *bits, bool clear);
 
 int fill_normal_launch(float *p, size_t n, uint64_t seed, float mean, float std, hipStream_t st);
 int copy_launch(void *dst, const void *src, size_t bytes, hipStream_t st);

@@ -101,6 +101,7 @@ struct GdnArgs {
     const float *x;                     // one-token block with the alpha/beta projection fused: x [B][hidden]
     const uint16_t *wab;                //   and the BF16 weight [2 nvh][hidden] (null: ab is given)
     int hidden;
+    unsigned *status;                   // verify: per-device status word (FN_STATUS_KR when kr[b] is clamped)
 };
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
@@ -214,6 +215,7 @@ k_gdn(const GdnArgs a) {
     //    conv weights, ring taps and raw inputs (waves 0-3), z and the norm weight (wave 0)
     // verify: pos is the position of the first new token; the kr replayed tokens sit at pos - kr .. pos - 1
     const int kr = VERIFY ? max(0, min(a.kr[b], a.rnt)) : 0;  // clamped: never past the replay rows
+    if (VERIFY && h == 0 && tid == 0 && kr != a.kr[b]) atomicOr(a.status, FN_STATUS_KR);
     const int ntot = ONE ? 1 : kr + a.nt;
     const int pos = FUSED ? a.pos[b] - kr : 0;  // position of the first token this call processes
     const float *x_b = a.qkv + (size_t) b * a.nt * C;
@@ -608,6 +610,7 @@ int gdn_verify_launch(const GdnVerify &p, hipStream_t st) {
     a.ring_buf = q.conv_ring; a.ab = q.ab; a.dt_bias = q.dt_bias; a.ssm_a = q.ssm_a; a.S = q.S; a.z = q.z;
     a.norm_w = q.norm_w; a.out = q.out;
     a.kr = p.kr; a.rnt = p.rnt; a.rqkv = p.rqkv; a.rab = p.rab;
+    if (status_word(&a.status)) return -1;
     hipLaunchKernelGGL(k_gdn<2>, dim3(q.B * q.nvh), dim3(MT_THREADS), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;

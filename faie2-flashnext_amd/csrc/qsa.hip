@@ -34,6 +34,7 @@ struct IxArgs {
     int32_t *keys;   // [B nt][top * IXR + IXR]
     int32_t *nkeys;  // [B nt]
     int j0, j1;      // block range of k_ix_blocks
+    unsigned *status;  // per-device status word (FN_STATUS_POS)
     float inv_freq[MAXROT / 2];
 };
 
@@ -97,7 +98,10 @@ __global__ void __launch_bounds__(256) k_ix_prep(const IxArgs a) {
     const int pos = a.pos[b];
     for (int t = 0; t < a.nt; ++t) {
         const int P = pos + t;
-        if (P < 0 || P >= a.max_ctx) break;  // past the cache: nothing to append (the host checks positions)
+        if (P < 0 || P >= a.max_ctx) {  // past the cache: nothing to append; the status word says so
+            if (threadIdx.x == 0) atomicOr(a.status, FN_STATUS_POS);
+            break;
+        }
         const size_t bt = (size_t) b * a.nt + t;
         const float *row = a.iqk + bt * (IXH * IXD + IXD);
         const float2 x = reinterpret_cast<const float2 *>(row + wave * IXD)[lane];
@@ -351,6 +355,7 @@ int qsa_select_launch(const QsaIndexer &p, float *work, size_t work_bytes, const
     if (!p.pos || !p.iqk || !p.wqn || !p.wkn || !p.IKc || !p.BKc || !work) FN_FAIL("qsa: null pointer");
     if (work_bytes < qsa_work_bytes(p.B, p.nt, p.max_ctx, p.top)) FN_FAIL("qsa: workspace too small");
     IxArgs a = make_args(p);
+    if (status_word(&a.status)) return -1;
     const size_t bt = (size_t) p.B * p.nt;
     a.Qix = work;
     a.scores = a.Qix + bt * IXH * IXD;

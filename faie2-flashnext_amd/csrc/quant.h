@@ -9,7 +9,7 @@
 namespace fn {
 
 enum : uint32_t {
-    QT_Q8_0 = 8, QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14, QT_IQ4_NL = 20, QT_IQ4_XS = 23, QT_BF16 = 30,
+    QT_Q8_0 = 8, QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14, QT_IQ4_NL = 20, QT_IQ3_S = 21, QT_IQ4_XS = 23, QT_BF16 = 30,
 };
 
 // Packed ("plane") layout of a rows x cols weight.  A GGUF row is a run of blocks, each an array of structs
@@ -45,6 +45,8 @@ struct GemvPlan {
     int lpr = 16;     // lanes per row (16, 32 or 64)
     int ntiles = 0;   // row tiles (workgroups along the rows)
     int ngroups = 0;  // groups per row
+    int grid = 0;     // workgroups along the rows: 0 = the ones resident at once (persistent, sized at launch),
+                      // else one per row tile (ntiles)
 };
 
 GemvPlan gemv_plan(const QLayout &L);
@@ -53,6 +55,9 @@ GemvPlan gemv_plan(const QLayout &L);
 // walk) and the resident waves per CU a persistent grid is sized for; 0 = automatic
 void gemv_override(int lpr, int ks, int kernel, int waves_per_cu);
 size_t gemv_work_bytes(const QLayout &L, int nt);
+// the reference's fn_gemv_waves switch (faie2fn.cu:2041, 2075, 2793): nonzero = persistent grid (default), 0 = one
+// workgroup per row tile
+void gemv_persistent(int on);
 
 // GGUF rows (device) -> packed planes (device); stream-ordered
 int quant_pack_launch(const QLayout &L, const uint8_t *raw, uint8_t *packed, hipStream_t st);

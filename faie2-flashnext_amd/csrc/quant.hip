@@ -64,6 +64,39 @@ template <int SH> __device__ __forceinline__ uint32_t iq4_levels(uint32_t w, con
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// the IQ3_S codebook: 512 grid points of four magnitudes in {1, 3, ..., 15}, one byte each (GGUF's iq3s_grid).  A
+// lane's decode looks up 8 of them per group at data-dependent indices, so the kernels that read IQ3_S copy the
+// table into LDS once per workgroup (tab_fill, before their first barrier) and gather from there.
+__device__ const uint32_t kIq3sGrid[512] = {
+#include "iq3s_grid.inc"
+};
+constexpr int kIq3sLds = 512 * 4;
+
+__device__ __forceinline__ uint32_t *iq3s_lds() {
+    __shared__ uint32_t grid[512];
+    return grid;
+}
+
+struct Iq3Tab {
+    const uint32_t *grid;
+    __device__ __forceinline__ Iq3Tab() : grid(iq3s_lds()) {}
+};
+
+// per-format lookup state held by a decoding lane: the IQ4 levels in registers, or the IQ3_S grid in LDS
+template <uint32_t TY> struct TabOf { using type = Iq4Tab; };
+template <> struct TabOf<QT_IQ3_S> { using type = Iq3Tab; };
+template <uint32_t TY> using TabT = typename TabOf<TY>::type;
+
+// LDS the format's table takes in a GEMV / dequant workgroup, and its fill by the workgroup's nth threads (the
+// caller's next barrier publishes it)
+template <uint32_t TY> constexpr int tab_lds() { return TY == QT_IQ3_S ? kIq3sLds : 0; }
+template <uint32_t TY> __device__ __forceinline__ void tab_fill(int tid, int nth) {
+    if constexpr (TY == QT_IQ3_S) {
+        uint32_t *g = iq3s_lds();
+        for (int i = tid; i < 512; i += nth) g[i] = kIq3sGrid[i];
+    }
+}
+
 __device__ __forceinline__ float sbyte(uint32_t w, int k) { return (float) ((int32_t) (w << (24 - 8 * k)) >> 24); }
 __device__ __forceinline__ float h2f(uint32_t bits) {
     return (float) __builtin_bit_cast(_Float16, (unsigned short) (bits & 0xFFFFu));
@@ -303,9 +336,49 @@ template <> struct Q<QT_Q6_K> {
     }
 };
 
+// IQ3_S: super-blocks of 256 (d fp16, qs[64], qh[8], signs[32], scales[4]); packed as plane 0 = qs, plane 1 = qh,
+// signs and scales (44 bytes), plane 2 = d.  Group ib: db = d * (1 + 2 * (4-bit scale ib)); its 32 values are 8 grid
+// points of 4 magnitudes, point 2l (2l + 1) at index qs[8 ib + 2l (+1)] | bit 2l (2l + 1) of qh[ib] << 8, value
+// 8l + j negated by bit j of signs[4 ib + l] (ggml: y = db * grid[j] * sign)
+template <> struct Q<QT_IQ3_S> {
+    static constexpr int NW = 6;
+    static constexpr int U = prefetch_groups(NW);
+    static constexpr bool MIN = false;
+    __device__ static void load(const RP &R, int g, uint32_t *w) {
+        const int ib = g & 7;
+        ld8(R.b0 + 8 * g, w);                                 // qs of the group
+        const uint8_t *h = R.b1 + 44 * (g >> 3);
+        w[2] = *reinterpret_cast<const uint32_t *>(h + (ib & 4));   // the qh word holding byte ib
+        w[3] = *reinterpret_cast<const uint32_t *>(h + 8 + 4 * ib); // 32 sign bits
+        w[4] = *reinterpret_cast<const uint32_t *>(h + 40);         // the 4 scale bytes
+        w[5] = ld2(R.b2 + 2 * (g >> 3));
+    }
+    // magnitude m with the sign bit sg (0 or 1) of the value: the float's sign bit, exact
+    __device__ static float smag(uint32_t m, uint32_t sg) { return __uint_as_float(__float_as_uint((float) m) | sg << 31); }
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq3Tab &T) {
+        const int ib = g & 7;
+        const uint32_t qh = (w[2] >> (8 * (ib & 3))) & 0xFFu;
+        const uint32_t sc = (w[4] >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xFu;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t qq = l < 2 ? w[0] : w[1];
+            const int s = 16 * (l & 1);
+            const uint32_t g1 = T.grid[((qq >> s) & 255u) | ((qh << (8 - 2 * l)) & 256u)];
+            const uint32_t g2 = T.grid[((qq >> (s + 8)) & 255u) | ((qh << (7 - 2 * l)) & 256u)];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                o.q[8 * l + j] = smag((g1 >> (8 * j)) & 255u, (w[3] >> (8 * l + j)) & 1u);
+                o.q[8 * l + 4 + j] = smag((g2 >> (8 * j)) & 255u, (w[3] >> (8 * l + 4 + j)) & 1u);
+            }
+        }
+        o.s[0] = o.s[1] = h2f(w[5]) * (float) (1 + 2 * (int) sc);
+        o.m[0] = o.m[1] = 0.0f;
+    }
+};
+
 template <uint32_t TY> __device__ __forceinline__ void decode(const PP &P, int row, int g, Grp &o) {
     uint32_t w[Q<TY>::NW];
-    const Iq4Tab T;
+    const TabT<TY> T;
     Q<TY>::load(row_planes(P, row), g, w);
     Q<TY>::unpack(w, g, o, T);
 }
@@ -328,6 +401,10 @@ __global__ void k_pack(QLayout L, const uint8_t *__restrict__ raw, uint8_t *__re
 
 // planes -> float rows, one thread per (row, group of 32), the GGUF value fl(s * q - m) rounded once
 template <uint32_t TY> __global__ void k_dequant(PP P, int rows, int G, int cols, float *__restrict__ out) {
+    if constexpr (tab_lds<TY>() > 0) {
+        tab_fill<TY>(threadIdx.x, blockDim.x);
+        __syncthreads();
+    }
     const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (size_t) rows * G) return;
     const int row = (int) (i / G), g = (int) (i % G);
@@ -359,7 +436,7 @@ template <int LPR> __device__ __forceinline__ float lane_row_sum(float v) {
 // an NT-token call gets the bits a one-token call gets.
 template <uint32_t TY, int NT>
 __device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float4 *xg, float *acc,
-                                           const Iq4Tab &T) {
+                                           const TabT<TY> &T) {
     Grp o;
     Q<TY>::unpack(w, g, o, T);
 #pragma unroll
@@ -444,7 +521,7 @@ __device__ __forceinline__ void load_batch(const PP &P, int rows, int s, int j, 
 
 template <uint32_t TY, int NT, int LPR>
 __device__ __forceinline__ void acc_batch(const uint32_t (&w)[Q<TY>::U][Q<TY>::NW], int j, int lane, int c0, int c1,
-                                          const float4 *xs, float *acc, const Iq4Tab &T) {
+                                          const float4 *xs, float *acc, const TabT<TY> &T) {
     constexpr int U = Q<TY>::U;
     const int gb = c0 + lane % LPR + LPR * U * j;
 #pragma unroll
@@ -520,7 +597,7 @@ __device__ __forceinline__ void gemv_walk_short(const PP &P, int rows, int g0, i
         }
     }
     __syncthreads();
-    const Iq4Tab T;  // (IQ4 formats) the level table in registers, once
+    const TabT<TY> T;  // (IQ4 formats) the level table in registers, once; (IQ3_S) the grid in LDS
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
@@ -555,7 +632,7 @@ __device__ __forceinline__ void gemv_walk_deep(const PP &P, int rows, int g0, in
     const int w0 = blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = w0 < NS ? ((NS - 1 - w0) / nws + 1) * NB : 0;
     uint32_t wa[U][NW], wb[U][NW];
-    const Iq4Tab T;  // (IQ4 formats) the level table in registers, once
+    const TabT<TY> T;  // (IQ4 formats) the level table in registers, once; (IQ3_S) the grid in LDS
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
@@ -608,6 +685,7 @@ __global__ void __launch_bounds__(512) k_gemv(PP P, int rows, int G, int gps, co
     const int NS = (rows + RPW - 1) / RPW, nws = gridDim.x * 8;
     const int NB = (ng + LPR * U - 1) / (LPR * U);
     out += (size_t) blockIdx.y * NT * rows;
+    tab_fill<TY>(threadIdx.x, 512);  // published by the walk's barrier after the x staging
     if constexpr (DEEP) gemv_walk_deep<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs);
     else gemv_walk_short<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs);
 }
@@ -626,7 +704,8 @@ __global__ void __launch_bounds__(512) k_gemv_c(PP P, int rows, int G, int gps, 
     const int s = blockIdx.x * 8 + (tid >> 6);
     const bool live = s < (rows + RPW - 1) / RPW;  // wave-uniform
     out += (size_t) blockIdx.y * NT * rows;
-    const Iq4Tab T;
+    tab_fill<TY>(tid, 512);  // published by the chunk loop's first barrier
+    const TabT<TY> T;
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
@@ -663,6 +742,7 @@ __global__ void k_gemv_reduce(const float *__restrict__ part, int ks, int n, flo
 }
 
 int g_ov_ks = 0, g_ov_lpr = 0, g_ov_kernel = 0, g_ov_wpc = 0;
+int g_persist = 1;  // fn_gemv_waves: 1 = grid of the workgroups resident at once, 0 = one workgroup per row tile
 constexpr int kLdsPerCu = 160 * 1024;  // LDS of a CDNA4 CU (the most one workgroup can take)
 
 
@@ -679,7 +759,8 @@ int gemv_nt(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, f
     const int gps = (pl.ngroups + pl.ks - 1) / pl.ks, ns = (L.rows + 64 / LPR - 1) / (64 / LPR);
     int nwg = (ns + 7) / 8;
     constexpr int XS = xs_stride(NT) * (int) sizeof(float4);  // LDS bytes per group of x
-    if (gps <= kLdsPerCu / XS && g_ov_kernel != 1) {
+    constexpr int LDS = kLdsPerCu - tab_lds<TY>();            // what x may take beside the format's table
+    if (gps <= LDS / XS && g_ov_kernel != 1) {
         static int by_regs = 0;  // workgroups per CU the registers allow (the deep walk's, the larger of the two)
         if (!by_regs) {
             int n = 0;
@@ -687,9 +768,9 @@ int gemv_nt(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, f
             by_regs = std::max(1, n);
         }
         const size_t lds = (size_t) gps * XS;
-        int per_cu = std::min(by_regs, std::max(1, (int) (kLdsPerCu / lds)));
+        int per_cu = std::min(by_regs, std::max(1, (int) (kLdsPerCu / (lds + tab_lds<TY>()))));
         if (g_ov_wpc) per_cu = std::max(1, g_ov_wpc / 8);
-        nwg = std::min(nwg, device_cus() * per_cu);
+        if (g_persist) nwg = std::min(nwg, device_cus() * per_cu);
         // batches of the busiest wave; from 4 on the deep walk's exact waits pay for its surplus loads (measured)
         const int nb = (gps + LPR * Q<TY>::U - 1) / (LPR * Q<TY>::U), per_wave = (ns + 8 * nwg - 1) / (8 * nwg) * nb;
         const bool deep = g_ov_kernel == 3 || (g_ov_kernel != 4 && per_wave >= 4);
@@ -697,7 +778,7 @@ int gemv_nt(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, f
         hipLaunchKernelGGL(kern, dim3((unsigned) nwg, (unsigned) pl.ks), dim3(512), lds, st, P, L.rows, pl.ngroups,
                            gps, x, L.cols, out);
     } else {
-        int kc = g_ov_kernel == 1 ? LPR : std::max(LPR, kLdsPerCu / 2 / XS / LPR * LPR);
+        int kc = g_ov_kernel == 1 ? LPR : std::max(LPR, (kLdsPerCu / 2 - tab_lds<TY>()) / XS / LPR * LPR);
         const int nch = (gps + kc - 1) / kc;
         kc = std::min(kc, ((gps + nch - 1) / nch + LPR - 1) / LPR * LPR);
         const size_t lds = (size_t) kc * XS;
@@ -744,12 +825,13 @@ bool qlayout(uint32_t type, int rows, int cols, QLayout &L) {
         case QT_Q8_0: f = {32, 34, 2, {2, 0, 0}, {32, 2, 0}}; break;
         case QT_IQ4_NL: f = {32, 18, 2, {2, 0, 0}, {16, 2, 0}}; break;
         case QT_IQ4_XS: f = {256, 136, 2, {8, 0, 0}, {128, 8, 0}}; break;
+        case QT_IQ3_S: f = {256, 110, 3, {2, 66, 0}, {64, 44, 2}}; break;
         case QT_Q4_K: f = {256, 144, 2, {16, 0, 0}, {128, 16, 0}}; break;
         case QT_Q5_K: f = {256, 176, 3, {48, 16, 0}, {128, 32, 16}}; break;
         case QT_Q6_K: f = {256, 210, 3, {0, 128, 192}, {128, 64, 18}}; break;
         default:
             set_error("unsupported type " + std::to_string(type) +
-                      " (this library reads BF16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS)");
+                      " (this library reads BF16, Q8_0, Q4_K, Q5_K, Q6_K, IQ3_S, IQ4_NL, IQ4_XS)");
             return false;
     }
     if (rows < 1 || cols < 1 || cols % f.qk) {
@@ -785,6 +867,8 @@ void gemv_override(int lpr, int ks, int kernel, int waves_per_cu) {
     g_ov_wpc = std::max(0, waves_per_cu);
 }
 
+void gemv_persistent(int on) { g_persist = on != 0; }
+
 GemvPlan gemv_plan(const QLayout &L) {
     GemvPlan p;
     p.ngroups = L.cols / 32;
@@ -798,6 +882,7 @@ GemvPlan gemv_plan(const QLayout &L) {
     p.lpr = g_ov_lpr ? g_ov_lpr : lpr;
     p.rpw = 8 * (64 / p.lpr);
     p.ntiles = (L.rows + p.rpw - 1) / p.rpw;
+    p.grid = g_persist ? 0 : p.ntiles;
     p.ks = g_ov_ks ? std::min(g_ov_ks, p.ngroups) : 1;
     const int gps = (p.ngroups + p.ks - 1) / p.ks;
     p.ks = (p.ngroups + gps - 1) / gps;  // every split holds at least one group
@@ -829,6 +914,7 @@ int quant_dequant_launch(const QLayout &L, const uint8_t *packed, float *out, hi
         case QT_Q8_0: hipLaunchKernelGGL(k_dequant<QT_Q8_0>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
         case QT_IQ4_NL: hipLaunchKernelGGL(k_dequant<QT_IQ4_NL>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
         case QT_IQ4_XS: hipLaunchKernelGGL(k_dequant<QT_IQ4_XS>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
+        case QT_IQ3_S: hipLaunchKernelGGL(k_dequant<QT_IQ3_S>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
         case QT_Q4_K: hipLaunchKernelGGL(k_dequant<QT_Q4_K>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
         case QT_Q5_K: hipLaunchKernelGGL(k_dequant<QT_Q5_K>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
         case QT_Q6_K: hipLaunchKernelGGL(k_dequant<QT_Q6_K>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
@@ -857,6 +943,7 @@ int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt,
         case QT_Q8_0: rc = gemv_t<QT_Q8_0>(L, pl, P, x, nt, out, st); break;
         case QT_IQ4_NL: rc = gemv_t<QT_IQ4_NL>(L, pl, P, x, nt, out, st); break;
         case QT_IQ4_XS: rc = gemv_t<QT_IQ4_XS>(L, pl, P, x, nt, out, st); break;
+        case QT_IQ3_S: rc = gemv_t<QT_IQ3_S>(L, pl, P, x, nt, out, st); break;
         case QT_Q4_K: rc = gemv_t<QT_Q4_K>(L, pl, P, x, nt, out, st); break;
         case QT_Q5_K: rc = gemv_t<QT_Q5_K>(L, pl, P, x, nt, out, st); break;
         case QT_Q6_K: rc = gemv_t<QT_Q6_K>(L, pl, P, x, nt, out, st); break;

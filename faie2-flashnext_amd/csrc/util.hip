@@ -1,11 +1,20 @@
-// Device utilities of libfaie2fn: seeded normal fill (synthetic inputs resident in HBM without a host round trip)
-// and a plain streaming copy (the HBM yardstick the path's kernels are compared with, and the known-size kernel
-// that calibrates the FETCH_SIZE / WRITE_SIZE counters).
+// Device utilities of libfaie2fn: seeded normal fill (synthetic inputs resident in HBM without a host round trip),
+// a plain streaming copy (the HBM yardstick the path's kernels are compared with, and the known-size kernel that
+// calibrates the FETCH_SIZE / WRITE_SIZE counters), and the per-device status word in which kernels record misuse
+// they cannot report on the host (positions and counts that live in device memory).
 #include "gdn.h"
+
+#include <mutex>
 
 namespace fn {
 
 namespace {
+
+__device__ __align__(256) unsigned g_status;  // FN_STATUS_* bits, one word per device
+
+constexpr int kMaxDevices = 64;
+unsigned *g_status_addr[kMaxDevices];
+std::mutex g_status_mu;
 
 __device__ __forceinline__ uint64_t mix64(uint64_t z) {  // splitmix64 finaliser
     z += 0x9E3779B97F4A7C15ull;
@@ -48,6 +57,33 @@ int device_cus() {
                 : 256;
     }
     return n;
+}
+
+int status_word(unsigned **out) {
+    int dev = -1;
+    FN_CK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) FN_FAIL("status: device index out of range");
+    std::lock_guard<std::mutex> lk(g_status_mu);
+    if (!g_status_addr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_status));
+        if (e != hipSuccess || !p) FN_FAIL(std::string("status: hipGetSymbolAddress -> ") + hipGetErrorString(e));
+        g_status_addr[dev] = static_cast<unsigned *>(p);
+    }
+    *out = g_status_addr[dev];
+    return 0;
+}
+
+int status_read(unsigned *bits, bool clear) {
+    unsigned *w = nullptr;
+    if (status_word(&w)) return -1;
+    FN_CK(hipDeviceSynchronize());
+    FN_CK(hipMemcpy(bits, w, sizeof(unsigned), hipMemcpyDeviceToHost));
+    if (clear && *bits) {
+        const unsigned zero = 0;
+        FN_CK(hipMemcpy(w, &zero, sizeof(unsigned), hipMemcpyHostToDevice));
+    }
+    return 0;
 }
 
 int fill_normal_launch(float *p, size_t n, uint64_t seed, float mean, float std, hipStream_t st) {

@@ -37,15 +37,19 @@ SYMBOLS = (
     "fn_attn_qsa_dev", "fn_attn_qsa_work_bytes", "fn_ix_blocks_dev", "fn_test_attn_qsa",
     "fn_gemv_packed_bytes", "fn_gemv_pack_dev", "fn_dequant_dev", "fn_gemv_work_bytes", "fn_gemv_dev",
     "fn_gdn_verify_dev", "fn_advance_by_dev", "fn_gdn_block_xab_dev",
-    "fn_attn_noalloc_dev",
+    "fn_attn_noalloc_dev", "fn_dev_status",
 )
+
+# status bits of fn_dev_status (include/faie2fn.h)
+STATUS_POS, STATUS_KR = 1, 2
 
 # bytes of the device array fn_attn_noalloc_dev takes its workspace from (FN_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
 # GGUF type ids of the weight formats this library reads (engine/faie2fn.cu:78-81), and (values, bytes) per block
-QTYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ4_XS=23, BF16=30)
-QBLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18), 23: (256, 136), 30: (1, 2)}
+QTYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ3_S=21, IQ4_XS=23, BF16=30)
+QBLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18), 21: (256, 110), 23: (256, 136),
+          30: (1, 2)}
 
 
 def row_bytes(qtype, cols):
@@ -129,6 +133,8 @@ class FN:
         d.fn_gemv_plan.argtypes = [u32, i, i, I32]
         d.fn_bench_gemv.argtypes = [u32, i, i, i, i, C.POINTER(C.c_float)]
         d.fn_gemv_override.argtypes = [i] * 4
+        d.fn_gemv_waves.argtypes = [i]
+        d.fn_dev_status.argtypes = [i]
         d.fn_bench_hot.argtypes = [i]
         d.fn_gemv_packed_bytes.restype = sz
         d.fn_gemv_packed_bytes.argtypes = [u32, i, i]
@@ -311,6 +317,13 @@ class FN:
 
     def ix_blocks_dev(self, B, max_ctx, j0, j1, IKc, wkn, BKc, stream=0, nrot=64, theta=1e7, eps=1e-6):
         self.check(self.d.fn_ix_blocks_dev(B, max_ctx, j0, j1, IKc, wkn, BKc, nrot, float(theta), float(eps), stream))
+
+    def dev_status(self, clear=True):
+        """FN_STATUS_* bits the kernels recorded on the current device (synchronizes it); cleared unless clear=False."""
+        r = self.d.fn_dev_status(1 if clear else 0)
+        if r < 0:
+            raise RuntimeError(self.d.fn_error().decode())
+        return r
 
     def advance_dev(self, pos, B, nt, stream=0):
         self.check(self.d.fn_advance_dev(pos, B, nt, stream))

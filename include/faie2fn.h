@@ -47,15 +47,19 @@ int fn_test_dequant(uint32_t type, const uint8_t *W, int rows, int cols, float *
  * staged once, 3 / 4 x staged once with the deep / short walk), warps_per_sm = resident waves per CU that a
  * persistent grid is sized for.  Every choice gives the same bits except ks > 1. */
 void fn_gemv_override(int wpt, int ks, int tb, int warps_per_sm);             /* faie2fn.cu:2786 */
+/* The reference's persistent-grid switch: waves != 0 (default) launches the GEMV on the workgroups resident at once,
+ * each walking many row tiles; 0 launches one workgroup per row tile.  Same bits either way; fn_gemv_plan's out[5]
+ * reports the choice for plans made afterwards. */
 void fn_gemv_waves(int waves);                                                /* faie2fn.cu:2793 */
 void fn_pdl(int on);                                                          /* faie2fn.cu:2796 */
 void fn_early(int on);                                                        /* faie2fn.cu:2798 */
 void fn_moe_var(int v);                                                       /* faie2fn.cu:2799 */
 void fn_moe_override(int gu_wpt, int gu_tb, int dn_wpt, int dn_tb);           /* faie2fn.cu:2801 */
 /* Launch plan of a rows x cols weight: out[7] = {values per group (32), waves per workgroup, split-K workgroups
- * per row, rows per workgroup, lanes per row, row tiles, groups per row}.  Same 7-int shape as the reference's
- * {cv, wpt, ks, tb, nbuf, ntiles, nch}, this library's plan in it; like the reference's it depends on the shape
- * only, never on the number of tokens. */
+ * per row, rows per workgroup pass, lanes per row, workgroups along the rows (0 = persistent grid: the workgroups
+ * resident at once, sized at launch; after fn_gemv_waves(0) one per row tile of rows-per-pass rows), groups per
+ * row}.  Same 7-int shape as the reference's {cv, wpt, ks, tb, nbuf, ntiles, nch}, this library's plan in it; like
+ * the reference's it depends on the shape only, never on the number of tokens. */
 int fn_gemv_plan(uint32_t type, int rows, int cols, int *out);                /* faie2fn.cu:2809 */
 void fn_bench_hot(int on);                                                    /* faie2fn.cu:2822 */
 /* ms per GEMV call of nt tokens (1..8) on random bytes of the format, iters calls replayed as one hipGraph, each
@@ -135,7 +139,7 @@ int fn_gdn_block_xab_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, 
  * state, writes S and the ring as the committed state, then runs the nt new tokens on that state in registers
  * only: out [B][nt][nvh dv] gets their outputs, S and the ring never hold them.  One read and one write of S per
  * call, as in plain decode; the new tokens' outputs are bit-identical to decoding them one by one after the
- * committed prefix.  ring >= rnt + 3; kr[b] outside [0, rnt] is clamped into it.  Advance pos by the accepted counts with fn_advance_by_dev before the step
+ * committed prefix.  ring >= rnt + 3; kr[b] outside [0, rnt] is clamped into it and recorded (FN_STATUS_KR, fn_dev_status).  Advance pos by the accepted counts with fn_advance_by_dev before the step
  * (the attention layers of the step then append the new tokens at pos, pos + 1, ... as usual). */
 int fn_gdn_verify_dev(int B, int nkh, int nvh, int dk, int dv, int head_map, int gate_act, int nt, int ring,
                       const int32_t *pos, const int32_t *kr, int rnt, const float *rqkv, const float *rab,
@@ -173,6 +177,17 @@ int fn_attn_nsplit(int B, int nkv, int nt, int ctx);
 int fn_attn_noalloc_dev(int B, int nq, int nkv, int hd, int nrot, float theta, float eps, int nt, int max_ctx,
                         const int32_t *pos, const float *qg, const float *k, const float *v, const float *wq,
                         const float *wk, float *Kc, float *Vc, int nsplit, float *og, void *stream);
+
+/* Misuse the device entry points cannot see on the host, because positions and counts live in device memory (no
+ * counterpart in the reference, whose positions are a host counter checked by forward(), faie2fn.cu:2468).  The
+ * kernels stay in bounds -- a new token outside the cache is neither appended nor attended past the cache's end, a
+ * verify count kr[b] outside [0, rnt] is clamped into it -- and OR a bit into a per-device status word.
+ * fn_dev_status synchronizes the current device, returns the bits (>= 0, -1 on error) and, if clear != 0, zeroes
+ * the word.  Not to be called while a stream is being captured.  The path engine and the host-array hooks check it
+ * themselves and fail with an fn_error() message. */
+#define FN_STATUS_POS 1u  /* attention: a new token's position pos[b] + t outside [0, max_ctx) */
+#define FN_STATUS_KR 2u   /* verify: kr[b] outside [0, rnt] */
+int fn_dev_status(int clear);
 
 /* pos[b] += nt for b < B, on the stream (the reference's k_advance, faie2fn.cu:1905). */
 int fn_advance_dev(int32_t *pos, int B, int nt, void *stream);

@@ -25,6 +25,9 @@
  *   Q4_K [256]   144: d f16 | dmin f16 | scales[12] | qs[128]
  *   Q5_K [256]   176: d f16 | dmin f16 | scales[12] | qh[32] | qs[128]
  *   Q6_K [256]   210: ql[128] | qh[64] | scales int8[16] | d f16
+ *   IQ3_S [256]  110: d f16 | qs[64] | qh[8] | signs[32] | scales[4] (a 4-bit scale per group of 32; each group is
+ *                8 grid points of 4 magnitudes from the format's 512-point codebook, 9-bit index = qs byte + one qh
+ *                bit, signs one bit per value; ggml dequantize_row_iq3_s, reference DQ<T_IQ3_S> faie2fn.cu:565-583)
  */
 #include <math.h>
 #include <stdint.h>
@@ -32,6 +35,11 @@
 #include <string.h>
 
 #define EXPORT __attribute__((visibility("default")))
+
+/* the IQ3_S codebook (GGUF iq3s_grid; the same data file the GPU decode includes) */
+static const uint32_t IQ3S_GRID[512] = {
+#include "../faie2-flashnext_amd/csrc/iq3s_grid.inc"
+};
 
 /* the 16 levels of the IQ4 formats (GGUF kvalues_iq4nl) */
 static const int8_t IQ4_LEVELS[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
@@ -68,6 +76,7 @@ EXPORT int orc_qblock(uint32_t type, int *qk, int *bytes) {
         case 12: *qk = 256; *bytes = 144; return 1;
         case 13: *qk = 256; *bytes = 176; return 1;
         case 14: *qk = 256; *bytes = 210; return 1;
+        case 21: *qk = 256; *bytes = 110; return 1;
         default: return 0;
     }
 }
@@ -140,6 +149,24 @@ static void dq_row(uint32_t type, const uint8_t *r, int cols, float *y) {
                     const int u1 = 1 << (2 * p), u2 = 2 << (2 * p);
                     for (int l = 0; l < 32; ++l) *y++ = fmaf(d1, (float) ((ql[l] & 0xF) + (qh[l] & u1 ? 16 : 0)), -n1);
                     for (int l = 0; l < 32; ++l) *y++ = fmaf(d2, (float) ((ql[l] >> 4) + (qh[l] & u2 ? 16 : 0)), -n2);
+                }
+            }
+            break;
+        case 21: /* IQ3_S: db = d * (1 + 2 * scale), y = db * grid * sign, ggml's order of the products */
+            for (int b = 0; b < cols / 256; ++b, r += 110) {
+                const float d = f16(r);
+                const uint8_t *qs = r + 2, *qh = r + 66, *signs = r + 74, *scales = r + 106;
+                for (int ib = 0; ib < 8; ++ib, y += 32) {
+                    const float db = d * (float) (1 + 2 * ((scales[ib / 2] >> (4 * (ib % 2))) & 0xF));
+                    for (int l = 0; l < 4; ++l) {
+                        const uint32_t g1 = IQ3S_GRID[qs[8 * ib + 2 * l] | ((qh[ib] << (8 - 2 * l)) & 256)];
+                        const uint32_t g2 = IQ3S_GRID[qs[8 * ib + 2 * l + 1] | ((qh[ib] << (7 - 2 * l)) & 256)];
+                        const uint8_t sg = signs[4 * ib + l];
+                        for (int j = 0; j < 4; ++j) {
+                            y[8 * l + j] = db * (float) ((g1 >> (8 * j)) & 255) * ((sg >> j) & 1 ? -1.0f : 1.0f);
+                            y[8 * l + 4 + j] = db * (float) ((g2 >> (8 * j)) & 255) * ((sg >> (j + 4)) & 1 ? -1.0f : 1.0f);
+                        }
+                    }
                 }
             }
             break;

@@ -155,7 +155,19 @@ def ix_score(Qix, BKc, pos, max_ctx, ixr=4):
 # walks ggml's per-row loops; both follow the reference's decoders (engine/faie2fn.cu:441-655).
 
 IQ4_LEVELS = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float32)
-_BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18), 23: (256, 136), 30: (1, 2)}
+_BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18), 21: (256, 110), 23: (256, 136),
+          30: (1, 2)}
+
+
+def iq3s_grid():
+    """The IQ3_S codebook [512] uint32, read from the data file the GPU decode and the C oracle include."""
+    import os
+    import re
+
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "faie2-flashnext_amd", "csrc",
+                        "iq3s_grid.inc")
+    text = re.sub(r"/\*.*?\*/", "", open(path).read(), flags=re.S)
+    return np.array([int(v, 16) for v in re.findall(r"0x[0-9a-fA-F]+", text)], np.uint32)
 
 
 def _f16(b):
@@ -203,6 +215,21 @@ def dequant(qtype, raw, rows, cols):
             qh = blk[:, 16:48].astype(np.int32)
             q = q | (((qh[:, None, :] >> np.arange(8)[None, :, None]) & 1) << 4)
         y = (d * s)[:, :, None] * q.astype(np.float32) - (dmin * m)[:, :, None]
+    elif qtype == 21:
+        # [n][ib][l][pair]: grid point 2l + pair of group ib; its 9-bit index takes bit 2l + pair of qh[ib]
+        d = _f16(blk[:, 0:2])
+        qs = blk[:, 2:66].astype(np.int64).reshape(n, 8, 4, 2)
+        qh = blk[:, 66:74].astype(np.int64)
+        signs = blk[:, 74:106].astype(np.int64).reshape(n, 8, 4)
+        sc = blk[:, 106:110].astype(np.int64)
+        ib = np.arange(8)
+        scale = (sc[:, ib // 2] >> (4 * (ib % 2))) & 15
+        db = d * (1 + 2 * scale).astype(np.float32)                  # [n][8], one float32 product each
+        bit = 2 * np.arange(4)[:, None] + np.arange(2)[None, :]          # [l][pair]
+        idx = qs | (((qh[:, :, None, None] >> bit) & 1) << 8)
+        mag = (iq3s_grid()[idx][..., None] >> (8 * np.arange(4, dtype=np.uint32))) & 255  # [n][8][4][2][4]
+        neg = ((signs[..., None] >> np.arange(8)) & 1).reshape(n, 8, 4, 2, 4)
+        y = (db[:, :, None, None, None] * mag.astype(np.float32)) * np.where(neg == 1, -1.0, 1.0).astype(np.float32)
     elif qtype == 14:
         ql = blk[:, 0:128].reshape(n, 2, 2, 32).astype(np.int32)   # [half][first / second 32 bytes][l]
         qh = blk[:, 128:192].reshape(n, 2, 1, 32).astype(np.int32)

@@ -2,6 +2,7 @@
 reference's model-level entries fail with the reference's -1 + fn_error() convention, and argument validation
 rejects bad calls before any device work."""
 
+import ctypes as C
 import os
 import re
 import subprocess
@@ -105,25 +106,27 @@ def test_gemv_hooks_validate_before_device_work(fnlib):
     2918) before touching a device."""
     z8 = np.zeros(1 << 16, np.uint8)
     x = np.zeros((9, 256), np.float32)
-    with pytest.raises(RuntimeError, match="unsupported type 21"):        # IQ3_S: not read by this library
-        fnlib.dequant(21, z8, 1, 256)
+    with pytest.raises(RuntimeError, match="unsupported type 18"):        # IQ3_XXS: an MoE-expert format
+        fnlib.dequant(18, z8, 1, 256)
     with pytest.raises(RuntimeError, match="unsupported shape"):          # K-quant row not a whole super-block
         fnlib.dequant(12, z8, 1, 288)
     with pytest.raises(RuntimeError, match="nt must be 1..8"):
         fnlib.gemv(8, z8, 1, 256, x)
     with pytest.raises(RuntimeError, match="unsupported type 0"):         # F32 has no block decode
         fnlib.gemv(0, z8, 1, 256, x[:1])
-    assert fnlib.gemv_packed_bytes(21, 4, 256) == 0 and fnlib.gemv_work_bytes(8, 4, 256, 9) == 0
+    assert fnlib.gemv_packed_bytes(18, 4, 256) == 0 and fnlib.gemv_work_bytes(8, 4, 256, 9) == 0
+    assert fnlib.gemv_packed_bytes(21, 4, 256) >= 4 * 110          # IQ3_S is read
     with pytest.raises(RuntimeError, match="unsupported"):
         fnlib.gemv_plan(1, 4, 256)
 
 
 def test_gemv_plan_shapes(fnlib):
     """Plans of the projection shapes around the path (the benchmark configs' hidden 2048 and the reference model's 2560)."""
-    for qtype, rows, cols in [(23, 10240, 2560), (8, 2560, 6144), (30, 96, 2560), (14, 512, 2560), (23, 8192, 2048)]:
-        gv, waves, ks, rpw, lpr, ntiles, ngroups = fnlib.gemv_plan(qtype, rows, cols)
+    for qtype, rows, cols in [(23, 10240, 2560), (8, 2560, 6144), (30, 96, 2560), (14, 512, 2560), (23, 8192, 2048),
+                              (21, 6144, 2560)]:
+        gv, waves, ks, rpw, lpr, grid, ngroups = fnlib.gemv_plan(qtype, rows, cols)
         assert (gv, waves) == (32, 8) and lpr in (16, 32, 64) and rpw == 8 * 64 // lpr
-        assert ntiles == (rows + rpw - 1) // rpw and ngroups == cols // 32
+        assert grid == 0 and ngroups == cols // 32  # persistent grid by default
         assert 1 <= ks <= ngroups
         assert fnlib.gemv_work_bytes(qtype, rows, cols, 3) == (ks * 3 * rows * 4 if ks > 1 else 0)
         assert fnlib.gemv_packed_bytes(qtype, rows, cols) >= rows * fn.row_bytes(qtype, cols)
@@ -141,6 +144,24 @@ def test_gemv_plan_shapes(fnlib):
         assert fnlib.gemv_plan(8, 2560, 6144) == auto
     finally:
         fnlib.gemv_override(0)
+
+
+def test_gemv_waves_switches_the_grid(fnlib):
+    """fn_gemv_waves, the reference's persistent-grid switch (faie2fn.cu:2075, 2793, driven by
+    flashnext/ab_waves_fn.py): 0 gives one workgroup per row tile, any other value the persistent grid again; the plan
+    of the weight reflects it and nothing else in the plan changes."""
+    d = fnlib.d
+    d.fn_gemv_waves.argtypes = [C.c_int]  # as ab_waves_fn.py binds it
+    base = fnlib.gemv_plan(23, 10240, 2560)
+    try:
+        d.fn_gemv_waves(0)
+        flat = fnlib.gemv_plan(23, 10240, 2560)
+        assert flat[5] == (10240 + flat[3] - 1) // flat[3] and flat[:5] + flat[6:] == base[:5] + base[6:]
+        for w in (1, 2, 4):
+            d.fn_gemv_waves(w)
+            assert fnlib.gemv_plan(23, 10240, 2560) == base
+    finally:
+        d.fn_gemv_waves(1)
 
 
 def test_verify_validates_before_device_work(fnlib):

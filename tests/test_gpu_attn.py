@@ -150,11 +150,13 @@ def test_attn_reference_group_12(fnlib):
     _check(fnlib, fn_synth.AttnCase(B=1, L=513, nq=24))
 
 
-@pytest.mark.parametrize("B,L,nt,pick", [(16, 32768, 1, [0, 7, 15]), (1, 131072, 1, [0]), (16, 32768, 4, [0, 15]),
-                                         (1, 32768, 8, [0])])
+@pytest.mark.parametrize("B,L,nt,pick", [(1, 4096, 1, [0]), (1, 32768, 1, [0]), (1, 131072, 1, [0]),
+                                         (16, 4096, 1, [0, 7, 15]), (16, 32768, 1, [0, 7, 15]),
+                                         (16, 131072, 1, [0, 15]), (16, 32768, 4, [0, 15]), (1, 32768, 8, [0])])
 def test_attn_full_size_device(fnlib, B, L, nt, pick):
-    """Config 3 at full size through the device entry point: caches filled in HBM, the oracle run on a
-    subset of the sequences (they are independent), compared on og and the appended K/V rows.  nt > 1: the last nt
+    """Config 3 at every size it names (B = 1 and 16 at 4K, 32K and 128K) through the device entry point: caches
+    filled in HBM, the oracle run on a subset of the sequences (they are independent), compared on og and the
+    appended K/V rows.  nt > 1: the last nt
     positions are the new tokens (a verify step at full context)."""
     import fn
     import hiprt
@@ -192,3 +194,37 @@ def test_attn_full_size_device(fnlib, B, L, nt, pick):
         assert max(e) <= TOL, (b, e)
     for x in (K, V, work, og, *d.values()):
         x.free()
+
+
+def test_attn_position_outside_cache_sets_status(fnlib):
+    """fn_attn_dev with a new token at or past max_ctx: nothing is written past the cache, the result stays finite,
+    and the per-device status word records FN_STATUS_POS until it is cleared (one-token and multi-token paths)."""
+    import fn
+    import hiprt
+
+    B, nq, nkv, hd, max_ctx = 2, 16, 2, 256, 128
+    _say("attn position outside the cache -> status word")
+    fnlib.dev_status()  # start clean
+    rng = np.random.default_rng(3)
+    for nt, pos in ((1, [5, 128]), (3, [126, 7])):
+        K = hiprt.Buf.like(rng.standard_normal(B * nkv * max_ctx * hd).astype(np.float32))
+        V = hiprt.Buf.like(rng.standard_normal(B * nkv * max_ctx * hd).astype(np.float32))
+        k0, v0 = K.download(), V.download()
+        d = {n: hiprt.Buf.like(x) for n, x in (
+            ("qg", rng.standard_normal((B, nt, nq, 2, hd)).astype(np.float32)),
+            ("k", rng.standard_normal((B, nt, nkv, hd)).astype(np.float32)),
+            ("v", rng.standard_normal((B, nt, nkv, hd)).astype(np.float32)),
+            ("wq", np.ones(hd, np.float32)), ("wk", np.ones(hd, np.float32)), ("pos", np.array(pos, np.int32)))}
+        nsplit = fnlib.attn_nsplit(B, nkv, nt, max_ctx)
+        wb = fnlib.attn_work_bytes(B, nq, nt, nsplit)
+        work, og = hiprt.Buf(wb), hiprt.Buf.empty((B, nt, nq, hd))
+        fnlib.attn_dev(B, nq, nkv, nt, max_ctx, d["pos"].ptr, d["qg"].ptr, d["k"].ptr, d["v"].ptr, d["wq"].ptr,
+                       d["wk"].ptr, K.ptr, V.ptr, nsplit, work.ptr, wb, og.ptr, None)
+        assert fnlib.dev_status(clear=False) & fn.STATUS_POS
+        assert fnlib.dev_status() & fn.STATUS_POS
+        assert fnlib.dev_status() == 0
+        assert np.isfinite(og.download()).all()
+        # the other sequence's rows (inside the cache) were appended; nothing else changed size
+        assert K.download().shape == k0.shape and V.download().shape == v0.shape
+        for x in (K, V, work, og, *d.values()):
+            x.free()

@@ -170,3 +170,29 @@ def test_engine_errors(fnlib):
         fnlib.free()
     with pytest.raises(RuntimeError, match="not loaded"):
         fnlib.path_step(1)
+
+
+def test_engine_context_full(fnlib):
+    """Stepping a sequence past the attention cache fails before anything runs ("context full", the reference's
+    forward check, faie2fn.cu:2468): a step that fits runs, the next one is refused, and so is a multi-step call that
+    would cross the end; the positions are left as they were."""
+    _say("engine context full")
+    fnlib.path_init(2, 4, attn_every=4, max_ctx=64)
+    try:
+        pos = fnlib.path_buffer(0, "POS")[0]
+        hiprt.htod(pos, np.array([10, 63], np.int32))
+        fnlib.path_step(1)                       # the token at position 63 takes the last row of the cache
+        with pytest.raises(RuntimeError, match="context full"):
+            fnlib.path_step(1)
+        assert list(hiprt.dtoh(pos, (2,), np.int32)) == [11, 64]
+        hiprt.htod(pos, np.array([10, 61], np.int32))
+        with pytest.raises(RuntimeError, match="context full"):
+            fnlib.path_step(4)                   # 61 + 4 > 64
+        fnlib.path_step(3)                       # 61 + 3 = 64 fits
+        assert list(hiprt.dtoh(pos, (2,), np.int32)) == [13, 64]
+        hiprt.htod(pos, np.array([-1, 0], np.int32))
+        with pytest.raises(RuntimeError, match="negative position"):
+            fnlib.path_step(1)
+        assert fnlib.dev_status() == 0
+    finally:
+        fnlib.free()

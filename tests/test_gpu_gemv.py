@@ -20,7 +20,7 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
-TYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ4_XS=23, BF16=30)
+TYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ3_S=21, IQ4_XS=23, BF16=30)
 RNG = np.random.default_rng(31)
 
 
@@ -32,7 +32,7 @@ def random_finite(qtype, rows, cols, rng):
     qk, bb = oracle.qblock(qtype)
     raw = rng.integers(0, 256, size=rows * (cols // qk) * bb, dtype=np.uint8)
     blk = raw.reshape(-1, bb)
-    for b in {30: [1], 8: [1], 20: [1], 23: [1], 12: [1, 3], 13: [1, 3], 14: [209]}[qtype]:
+    for b in {30: [1], 8: [1], 20: [1], 21: [1], 23: [1], 12: [1, 3], 13: [1, 3], 14: [209]}[qtype]:
         blk[:, b] &= 0xBF
     return raw
 
@@ -57,6 +57,7 @@ PATH_SHAPES = [
     ("Q6_K", 512, 2560),       # attn_v
     ("IQ4_XS", 512, 2560),     # attn_k
     ("Q6_K", 6144, 2560),      # attn_gate (z) of layer 1
+    ("IQ3_S", 6144, 2560),     # attn_gate (z) of layer 0 (inspect_fn.txt:76)
     ("IQ4_XS", 8192, 2048),    # config 1/2 qkv: 8192 mixed channels from hidden 2048
     ("Q8_0", 2048, 4096),      # config 1/2 ssm_out
 ]
@@ -118,6 +119,8 @@ STAGING_CASES = [
     ("IQ4_NL", 3001, 2944, 8),
     ("Q8_0", 700, 4608, 8),     # 148 KB of x in LDS
     ("IQ4_XS", 130, 2560, 5),   # a short weight
+    ("IQ3_S", 1000, 6144, 8),   # the codebook in LDS beside a chunked x
+    ("IQ3_S", 2000, 2560, 2),
 ]
 
 
@@ -143,6 +146,24 @@ def test_gemv_chunked_x_matches_one_stage(fnlib, name, rows, cols, nt, wpc):
         fnlib.gemv_override(0)
     assert np.array_equal(y1, y3) and np.array_equal(y1, y4)
     assert oracle.relerr(y3, oracle.gemv(t, raw, rows, cols, x)) <= TOL
+
+
+@pytest.mark.parametrize("name,rows,cols,nt", STAGING_CASES[:4])
+def test_gemv_waves_switch_same_bits(fnlib, name, rows, cols, nt):
+    """fn_gemv_waves(0) (one workgroup per row tile, the reference's non-persistent grid) and the default persistent
+    grid give the same bits."""
+    t = TYPES[name]
+    _say(f"gemv waves switch {name} {rows}x{cols} nt={nt}")
+    raw = random_finite(t, rows, cols, RNG)
+    x = RNG.standard_normal((nt, cols)).astype(np.float32)
+    y1 = fnlib.gemv(t, raw, rows, cols, x)
+    try:
+        fnlib.d.fn_gemv_waves(0)
+        assert fnlib.gemv_plan(t, rows, cols)[5] > 0
+        y0 = fnlib.gemv(t, raw, rows, cols, x)
+    finally:
+        fnlib.d.fn_gemv_waves(1)
+    assert np.array_equal(y0, y1)
 
 
 @pytest.mark.parametrize("seed", range(16))

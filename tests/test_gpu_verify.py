@@ -170,3 +170,23 @@ def test_verify_argument_checks(fnlib):
     qkv, ab, z = draw(lay, 2)
     with pytest.raises(RuntimeError, match="ring - 3"):   # 2 committed tokens + 3 taps do not fit a ring of 4
         verify(fnlib, st, [1], 2, hiprt.Buf.like(qkv), hiprt.Buf.like(ab), qkv, ab, z)
+
+
+def test_verify_kr_out_of_range_sets_status(fnlib):
+    """kr[b] outside [0, rnt] is clamped into it by the kernel (it never reads past the replay rows) and recorded in the
+    per-device status word as FN_STATUS_KR; an in-range call leaves the word clear."""
+    import fn
+
+    _say("gdn verify kr out of range -> status word")
+    fnlib.dev_status()
+    rng = np.random.default_rng(8)
+    lay = fn_synth.BlockLayer(B=2, config=1, layer=25)
+    st = Seqs(lay, 8, np.array([9, 12]), rng)
+    rq, ra, _ = draw(lay, 4)
+    qkv, ab, z = draw(lay, 2)
+    out, _ = verify(fnlib, st, [2, 3], 4, hiprt.Buf.like(rq), hiprt.Buf.like(ra), qkv, ab, z)
+    assert fnlib.dev_status() == 0
+    out, _ = verify(fnlib, st, [6, 0], 4, hiprt.Buf.like(rq), hiprt.Buf.like(ra), qkv, ab, z)
+    assert np.isfinite(out).all()
+    assert fnlib.dev_status() == fn.STATUS_KR
+    assert fnlib.dev_status() == 0

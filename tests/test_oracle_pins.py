@@ -438,7 +438,7 @@ def test_masked_attention_reduces_to_dense():
         assert np.allclose(tail[0, 0, h], (p @ vals) / p.sum() * gate[h], atol=1e-14)
 
 
-def _ix_case(dots, ixd=128, nblk=3):
+def _ix_dots_case(dots, ixd=128, nblk=3):
     """Qix [1][1][ixh][ixd], BKc [1][nblk][ixd] with q_h = a_h e_h and block key k_j = sum_h c_jh e_h, so that
     q_h . k_j = dots[j][h] exactly (one nonzero product per dot)."""
     dots = np.asarray(dots, np.float64)
@@ -462,7 +462,7 @@ def test_ix_score_closed_forms():
     dots = [[5.0, -1.0, -2.0, -3.0],      # one head positive
             [-1.0, -2.0, -0.5, -7.0],     # all negative
             [3.0, -2.0, 4.0, -6.0]]       # mixed: relu per head 7, relu of the sum 0
-    Q, K = _ix_case(dots, nblk=4)
+    Q, K = _ix_dots_case(dots, nblk=4)
     # pos 11, nt 1: (11 + 1) / 4 = 3 complete blocks; block 3 is left untouched
     sc = oracle.ix_score(Q, K, np.array([11]), max_ctx=16)
     r = np.sqrt(128.0)

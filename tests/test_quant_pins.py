@@ -20,7 +20,7 @@ import oracle
 import oracle.twin as twin
 
 RNG = np.random.default_rng(7)
-TYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ4_XS=23, BF16=30)
+TYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ3_S=21, IQ4_XS=23, BF16=30)
 LEVELS = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
 
 
@@ -40,7 +40,7 @@ def random_finite(qtype, rows, cols, rng):
     qk, bb = oracle.qblock(qtype)
     raw = rng.integers(0, 256, size=rows * (cols // qk) * bb, dtype=np.uint8)
     blk = raw.reshape(-1, bb)
-    hi_bytes = {30: [1], 8: [1], 20: [1], 23: [1], 12: [1, 3], 13: [1, 3], 14: [209]}[qtype]
+    hi_bytes = {30: [1], 8: [1], 20: [1], 21: [1], 23: [1], 12: [1, 3], 13: [1, 3], 14: [209]}[qtype]
     for b in hi_bytes:
         blk[:, b] &= 0xBF
     return raw
@@ -111,6 +111,22 @@ def pack_q6_k(d_bits, sc, c):
         qh[32 * n + l] |= (c[v] >> 4) << (2 * k)
     return np.concatenate([ql, qh, np.asarray(sc, np.int8).view(np.uint8),
                            np.array([d_bits & 255, d_bits >> 8], np.uint8)])
+
+
+def pack_iq3_s(d_bits, sc, idx, neg):
+    """sc [8] 4-bit group scales, idx [64] 9-bit codebook indices (grid point p = values 4p .. 4p + 3), neg [256] sign
+    bits: the 110 bytes d | qs[64] | qh[8] | signs[32] | scales[4].  Point p of group ib = p // 8 is point
+    k = p % 8 of the group: its low 8 index bits go to qs[p], the ninth to bit k of qh[ib]."""
+    idx, neg = np.asarray(idx), np.asarray(neg)
+    qs = (idx & 255).astype(np.uint8)
+    qh = np.zeros(8, np.uint8)
+    for p in range(64):
+        qh[p // 8] |= (idx[p] >> 8) << (p % 8)
+    signs = np.zeros(32, np.uint8)
+    for v in range(256):
+        signs[v // 8] |= neg[v] << (v % 8)
+    scales = np.array([(sc[2 * i] & 15) | ((sc[2 * i + 1] & 15) << 4) for i in range(4)], np.uint8)
+    return np.concatenate([np.array([d_bits & 255, d_bits >> 8], np.uint8), qs, qh, signs, scales])
 
 
 def f32_once(x):
@@ -212,6 +228,48 @@ def test_q6_k_packed_codes():
             want.append(f32_once(float(ds) * (int(c[v]) - 32)))
     got = oracle.dequant(14, np.concatenate(blocks), 1, 768)[0]
     assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_iq3_s_packed_codes():
+    """IQ3_S blocks packed from chosen codebook indices (all 9 bits used), sign bits and scales decode to
+    d * (1 + 2 sc) * magnitude * sign, each magnitude the byte j of its grid point (low byte first); the product
+    d * (1 + 2 sc) is exact (11 x 5 significant bits), so each value is one rounding of an exact float64 product."""
+    grid = twin.iq3s_grid()
+    blocks, want = [], []
+    for _ in range(3):
+        db, d = rand_f16_scale(RNG)
+        sc = RNG.integers(0, 16, size=8)
+        idx = RNG.integers(0, 512, size=64)
+        idx[:2] = [255, 256]            # both sides of the ninth bit
+        neg = RNG.integers(0, 2, size=256)
+        blocks.append(pack_iq3_s(db, sc, idx, neg))
+        for v in range(256):
+            mag = (int(grid[idx[v // 4]]) >> (8 * (v % 4))) & 255
+            want.append(f32_once(d * (1 + 2 * int(sc[v // 32])) * mag * (-1 if neg[v] else 1)))
+    got = oracle.dequant(21, np.concatenate(blocks), 1, 768)[0]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_iq3_s_codebook():
+    """The IQ3_S codebook data: 512 distinct points in ascending order, every magnitude an odd value 1..15 (3 bits
+    of a 4-value lattice point); grid point 0 is (1, 1, 1, 1).  Where the reference tree is present (this container,
+    not the GPU box), the values equal the ggml codebook the reference carries (engine/fn_tables.cuh:513, copied
+    from ggml-common.h), read as text."""
+    import os
+    import re
+
+    g = twin.iq3s_grid()
+    assert g.shape == (512,) and np.all(np.diff(g.astype(np.int64)) > 0) and g[0] == 0x01010101
+    mags = (g[:, None] >> (8 * np.arange(4, dtype=np.uint32))) & 255
+    assert set(np.unique(mags).tolist()) <= set(range(1, 16, 2))
+    ref = "/root/reference/engine/fn_tables.cuh"
+    if not os.path.exists(ref):
+        pytest.skip("reference tree not present (GPU box)")
+    text = open(ref).read()
+    i = text.index("iq3s_grid[512]")
+    body = text[text.index("{", i) + 1:text.index("}", i)]
+    want = np.array([int(v, 16) for v in re.findall(r"0x[0-9a-fA-F]+", body)], np.uint32)
+    assert np.array_equal(g, want)
 
 
 @pytest.mark.parametrize("name", list(TYPES))
