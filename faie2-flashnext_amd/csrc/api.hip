@@ -5,6 +5,7 @@
 // decode-attention path.  Sections 2 and 3 are this path's hooks: host arrays in / out (synchronous, device 0,
 // the reference's unit-test-hook style, faie2fn.cu:2745) and the device-buffer entry points an engine calls.
 #include "engine.h"
+#include "model.h"
 #include "qsa.h"
 #include "hostbuf.h"
 
@@ -31,31 +32,57 @@ using fn::use_device0;
 
 namespace {
 
-const char *kNoModel =
-    "not built: libfaie2fn.so carries the decode-attention path (DeltaNet block, GQA and QSA decode) and the GEMV "
-    "of its projections; model loading, the forward pass, MoE and routing are not part of it";
+const char *kNoRoute =
+    "not built: routing is benchmarked through fn_forward (k_route runs inside the model forward); this library has "
+    "no stand-alone routing benchmark";
 
 // switches the reference exposes for its forward; kept so scripts that set them still run
 int g_pdl = 1, g_early = 1, g_moe_var = 0;
 
 }  // namespace
 
+// The engine entry points act on the loaded model (fn_load) if there is one, else on the path engine (fn_path_init).
 FN_API const char *fn_error(void) { return fn::error_cstr(); }
-FN_API void fn_free(void) { fn::path_free(); }
-FN_API int fn_load(const char *, const char *, int, int) { FN_FAIL(kNoModel); }
-FN_API int fn_split(void) { return fn::path_loaded() ? 0 : -1; }  // one GPU: every layer on device 0
-FN_API double fn_dev_gb(int dv) { return dv == 0 ? fn::path_dev_gb() : -1; }
-FN_API int fn_n_past(void) { return fn::path_n_past(); }
-FN_API double fn_last_ms(void) { return fn::path_last_ms(); }
-FN_API int fn_reset(void) { return fn::path_reset(); }
-FN_API int fn_use_graphs(int on) { return fn::path_use_graphs(on); }
-FN_API int fn_forward(const int32_t *, int, float *, int32_t *) { FN_FAIL("not loaded"); }
-FN_API int fn_debug_layers(float *) { FN_FAIL("not loaded"); }
+FN_API void fn_free(void) {
+    fn::model_free();
+    fn::path_free();
+}
+FN_API int fn_load(const char *shard1, const char *shard2, int max_ctx, int split) {
+    (void) split;  // one GPU: every layer on device 0
+    return fn::model_load(shard1, shard2, max_ctx);
+}
+FN_API int fn_split(void) {
+    if (fn::model_loaded()) return fn::model_layers();  // no layer on a second device
+    return fn::path_loaded() ? 0 : -1;
+}
+FN_API double fn_dev_gb(int dv) {
+    if (fn::model_loaded()) return dv == 0 ? fn::model_dev_gb() : (dv == 1 ? 0.0 : -1.0);
+    return dv == 0 ? fn::path_dev_gb() : -1;
+}
+FN_API int fn_n_past(void) { return fn::model_loaded() ? fn::model_n_past() : fn::path_n_past(); }
+FN_API double fn_last_ms(void) { return fn::model_loaded() ? fn::model_last_ms() : fn::path_last_ms(); }
+FN_API int fn_reset(void) { return fn::model_loaded() ? fn::model_reset() : fn::path_reset(); }
+FN_API int fn_use_graphs(int on) { return fn::model_loaded() ? fn::model_use_graphs(on) : fn::path_use_graphs(on); }
+FN_API int fn_forward(const int32_t *tokens, int nt, float *logits, int32_t *argmax) {
+    return fn::model_forward(tokens, nt, logits, argmax);
+}
+FN_API int fn_debug_layers(float *out) { return fn::model_debug_layers(out); }
 FN_API void fn_pdl(int on) { g_pdl = on != 0; }
 FN_API void fn_early(int on) { g_early = on != 0; }
 FN_API void fn_moe_var(int v) { g_moe_var = v; }
 FN_API void fn_moe_override(int, int, int, int) {}
-FN_API int fn_bench_route(int, int, int, const float *, int, int *, float *, float *) { FN_FAIL(kNoModel); }
+FN_API int fn_bench_route(int, int, int, const float *, int, int *, float *, float *) { FN_FAIL(kNoRoute); }
+
+FN_API int fn_model_dims(const char *path, int *out, int n) {
+    fn::ModelDims d;
+    if (!out || n < 1) FN_FAIL("model_dims: null output");
+    if (fn::model_inspect(path, &d)) return -1;
+    const int v[] = {d.D, d.NL, d.NH, d.NKV, d.HD, d.NROT, d.NE, d.NEU, d.FFE, d.FFS, d.DS, d.NKH, d.NVH, d.DINNER,
+                     d.CONVCH, d.attn_every, d.HC, d.HCR, d.IXH, d.IXD, d.top, d.VOCAB};
+    const int k = (int) (sizeof(v) / sizeof(v[0]));
+    for (int i = 0; i < n; ++i) out[i] = i < k ? v[i] : 0;
+    return k;
+}
 
 // ---------------------------------------------------------------------------------------------
 // 3. device entry points

@@ -9,6 +9,7 @@
 // allocation and by fn_reset (faie2fn.cu:2018-2024, 2703-2717); per-sequence positions live in device memory so
 // a captured step replays unchanged (faie2fn.cu:1447).
 #include "engine.h"
+#include "model.h"
 
 #include <chrono>
 #include <memory>
@@ -120,6 +121,7 @@ int ensure_graph(Engine &e) {
 int path_init(int B, int nl, int attn_every, int nkh, int nvh, int nq, int nkv, int max_ctx, int head_map,
               int gate_act, int nsplit) {
     g_eng.reset();
+    model_free();  // one engine at a time: a path engine replaces a loaded model
     if (B < 1 || nl < 1 || attn_every < 0 || nkh < 1 || nvh < 1 || nvh % nkh) FN_FAIL("path_init: bad DeltaNet shape");
     const bool any_attn = attn_every > 0 && nl >= attn_every;
     if (any_attn && (nq < 1 || nkv < 1 || nq % nkv || max_ctx < 1)) FN_FAIL("path_init: bad attention shape");
@@ -132,6 +134,8 @@ int path_init(int B, int nl, int attn_every, int nkh, int nvh, int nq, int nkv, 
     e->nsplit = any_attn ? (nsplit > 0 ? nsplit : attn_pick_nsplit(B, nkv, 1, e->max_ctx)) : 1;
     FN_CK(hipSetDevice(0));
     FN_CK(hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking));
+    unsigned *sw = nullptr;  // the status word's address, looked up now rather than under a graph capture
+    if (status_word(&sw)) return -1;
     if (e->alloc(&e->pos, B)) return -1;
     if (any_attn) {
         e->work_bytes = attn_work_bytes(B, nq, 1, HD, e->nsplit);

@@ -1,0 +1,669 @@
+// Model engine: fn_load reads a FAIE2-FlashNext GGUF and places it on one GPU; fn_forward runs nt <= 8 tokens of one
+// sequence through the whole model and returns logits and the argmax token.
+//
+// The reference's model forward (engine/faie2fn.cu:1937-2031 Engine, 2370-2490 layer_forward / enqueue / forward,
+// 2524-2696 fn_load) on its two GPUs, rebuilt on one MI355X: every layer on device 0, one stream, one hipGraph per
+// token count.  Per layer (faie2fn.cu:2370-2420):
+//   hyper-connection read  hn = RMSNorm_s(h) (per stream), lr = W_down+inject . hn, t = silu(lr / HC),
+//                          a = W_up . t, x = (1/HC) sum_s sigmoid(a_s) hn_s, inj_s = 2 sigmoid(lr_inject,s / HC)
+//                          (faie2fn.cu:1246-1273, 860-888, 2350-2359)
+//   mixer                  DeltaNet: GEMV qkv / z / alpha-beta, the fused DeltaNet block, GEMV ssm_out;
+//                          attention: GEMV q / k / v / indexer, QSA sparse attention, GEMV o
+//   hyper-connection write h_s += y * inj_s, then hn = RMSNorm_s(h) for the next read (faie2fn.cu:1281-1327)
+//   hyper-connection read  (FFN)
+//   MoE                    router + shared-gate GEMV, softmax top-k routing with the shared expert's SwiGLU
+//                          (faie2fn.cu:1747-1798), routed experts' SwiGLU and down rows, the shared expert's down GEMV
+//   hyper-connection write with y = sum_k w_k down_k + sigmoid(shared gate) shared down (faie2fn.cu:1298-1318)
+// then the final hyper-connection read (no inject), the LM head GEMV and the argmax (lowest index on ties,
+// faie2fn.cu:1910-1934).  Shapes come from the GGUF metadata (the reference fixes them at build time and asserts
+// them at load, faie2fn.cu:2532-2535); the kernels fix head_dim 256, DeltaNet head dim 128, the indexer's 4 x 128 and
+// blocks of 4 keys.  Not built: the per-layer n-gram embedding (PLE, a 27 GB hashed table in the second shard):
+// fn_load rejects a model whose metadata lists PLE layers.
+#include "engine.h"
+#include "gguf.h"
+#include "model.h"
+#include "qsa.h"
+#include "quant.h"
+
+#include <chrono>
+#include <cmath>
+#include <memory>
+#include <vector>
+
+namespace fn {
+
+namespace {
+
+constexpr int MAXT = 8;                      // tokens per forward (faie2fn.cu:67)
+constexpr int HDK = 256, DSK = 128;          // attention head dim, DeltaNet head dim (built sizes)
+constexpr int IXH = 4, IXD = 128, IXR = 4;   // indexer heads, head dim, keys per block (built sizes)
+constexpr int RING = 16;                     // conv ring slots (>= MAXT + 3, a power of two)
+
+__device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// sum over a workgroup of nw waves (wave sums, then wave 0 adds the nw partials in wave order); every thread returns
+// the sum.  red: nw floats of LDS.  Call from uniform control flow.
+__device__ __forceinline__ float block_sum(float v, float *red, int nw) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < nw; ++i) s += red[i];
+    return s;
+}
+
+// RMSNorm of each of the HC streams: out[t][s D + c] = h * rsqrt(mean_c h^2 + eps) * w[s D + c] (faie2fn.cu:1226-1239).
+// grid (nt, HC), 256 threads
+__global__ void __launch_bounds__(256) k_groupnorm(const float *__restrict__ h, const float *__restrict__ w, int D,
+                                                    float eps, float *__restrict__ out) {
+    __shared__ float red[4];
+    const size_t base = ((size_t) blockIdx.x * gridDim.y + blockIdx.y) * D;
+    const float4 *h4 = reinterpret_cast<const float4 *>(h + base);
+    float ss = 0.0f;
+    for (int c = threadIdx.x; c < D / 4; c += 256) {
+        const float4 v = h4[c];
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    const float r = rsqrtf(block_sum(ss, red, 4) / D + eps);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w + (size_t) blockIdx.y * D);
+    float4 *o4 = reinterpret_cast<float4 *>(out + base);
+    for (int c = threadIdx.x; c < D / 4; c += 256) {
+        const float4 v = h4[c], wv = w4[c];
+        o4[c] = make_float4(v.x * r * wv.x, v.y * r * wv.y, v.z * r * wv.z, v.w * r * wv.w);
+    }
+}
+
+// t[t][r] = silu(lr[t][r] / HC) for r < HCR (faie2fn.cu:1266-1273); the inject logits stay in lr.  grid nt, 256 thr
+__global__ void k_hc_lowrank(const float *__restrict__ lr, int ldr, int HCR, int HC, float *__restrict__ t320) {
+    const int t = blockIdx.x;
+    for (int r = threadIdx.x; r < HCR; r += blockDim.x) t320[(size_t) t * HCR + r] = silu(lr[(size_t) t * ldr + r] * (1.0f / HC));
+}
+
+// x[t][c] = (sum_s sigmoid(a[t][s D + c]) hn[t][s D + c]) / HC (streams in order), and, with inject logits,
+// inj[t][s] = 2 sigmoid(lr[t][HCR + s] / HC) (faie2fn.cu:873-888).  grid (nt, ceil(D / 256)), 256 threads
+__global__ void k_hc_mix(const float *__restrict__ a, const float *__restrict__ hn, int D, int HC,
+                         const float *__restrict__ lr, int ldr, int HCR, float *__restrict__ x, float *__restrict__ inj) {
+    const int t = blockIdx.x, c = blockIdx.y * 256 + threadIdx.x;
+    if (c < D) {
+        float s = 0.0f;
+        for (int k = 0; k < HC; ++k) {
+            const size_t i = (size_t) t * HC * D + (size_t) k * D + c;
+            s += sigm(a[i]) * hn[i];
+        }
+        x[(size_t) t * D + c] = s / HC;
+    }
+    if (inj && blockIdx.y == 0 && (int) threadIdx.x < HC)
+        inj[t * HC + threadIdx.x] = 2.0f * sigm(lr[(size_t) t * ldr + HCR + threadIdx.x] / HC);
+}
+
+// hyper-connection write (faie2fn.cu:1281-1327): h[t][s][c] += yv[c] * inj[t][s], where yv = y, or for the MoE
+// yv = sum_k wsel[t][k] dpart[t NEU + k][c] + sigmoid(rsg[t][NE]) y[t][c]; then (norm non-null)
+// hn[t][s][c] = RMSNorm of the new stream s.  grid (nt, HC), 256 threads
+__global__ void __launch_bounds__(256) k_hc_add(float *__restrict__ h, const float *__restrict__ y,
+                                                const float *__restrict__ inj, int D, int HC,
+                                                const float *__restrict__ dpart, const float *__restrict__ wsel,
+                                                int NEU, const float *__restrict__ rsg, int NE,
+                                                const float *__restrict__ norm, float eps, float *__restrict__ hn) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, s = blockIdx.y;
+    float *hp = h + ((size_t) t * HC + s) * D;
+    const float is = inj[t * HC + s];
+    const float sg = dpart ? sigm(rsg[(size_t) t * (NE + 1) + NE]) : 0.0f;
+    float ss = 0.0f;
+    for (int c = threadIdx.x; c < D; c += 256) {
+        float yv = y[(size_t) t * D + c];
+        if (dpart) {
+            float m = 0.0f;
+            for (int k = 0; k < NEU; ++k) m += wsel[t * NEU + k] * dpart[((size_t) t * NEU + k) * D + c];
+            yv = m + sg * yv;
+        }
+        const float v = hp[c] + yv * is;
+        hp[c] = v;
+        ss += v * v;
+    }
+    if (!norm) return;  // (uniform)
+    const float r = rsqrtf(block_sum(ss, red, 4) / D + eps);
+    float *op = hn + ((size_t) t * HC + s) * D;
+    for (int c = threadIdx.x; c < D; c += 256) op[c] = hp[c] * r * norm[(size_t) s * D + c];
+}
+
+// (value, index) maximum over a workgroup: larger value, ties to the lower index; every thread returns the winner
+__device__ __forceinline__ void block_argmax(float &v, int &i, float *bv, int *bi) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(v, o);
+        const int i2 = __shfl_xor(i, o);
+        if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+    }
+    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) { bv[w] = v; bi[w] = i; }
+    __syncthreads();
+    v = bv[0];
+    i = bi[0];
+    for (int k = 1; k < nw; ++k)
+        if (bv[k] > v || (bv[k] == v && bi[k] < i)) { v = bv[k]; i = bi[k]; }
+}
+
+// routing (faie2fn.cu:1747-1798): p = softmax over the NE router logits (rows 0..NE-1 of the router + shared-gate
+// GEMV), the NEU largest in order (probability descending, ties to the lower expert: repeated argmax), weights
+// renormalized over them; and the shared expert's SwiGLU sha[t][r] = silu(shg) * shu.  grid nt, 1024 threads
+__global__ void __launch_bounds__(1024) k_route(const float *__restrict__ rsg, int NE, int NEU,
+                                                const float *__restrict__ shg, const float *__restrict__ shu, int FFS,
+                                                int32_t *__restrict__ sel, float *__restrict__ wsel,
+                                                float *__restrict__ sha) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    __shared__ float topv[32];
+    const int t = blockIdx.x, i = threadIdx.x;
+    for (int r = i; r < FFS; r += blockDim.x)
+        sha[(size_t) t * FFS + r] = silu(shg[(size_t) t * FFS + r]) * shu[(size_t) t * FFS + r];
+    const float l = i < NE ? rsg[(size_t) t * (NE + 1) + i] : -INFINITY;
+    float mv = l;
+    int mi = i;
+    block_argmax(mv, mi, bv, bi);
+    float v = i < NE ? expf(l - mv) : -1.0f;  // probabilities up to the common 1 / sum, in [0, 1]
+    for (int k = 0; k < NEU; ++k) {
+        float bvv = v;
+        int bii = i;
+        block_argmax(bvv, bii, bv, bi);
+        if (i == 0) {
+            topv[k] = bvv;
+            sel[t * NEU + k] = bii;
+        }
+        if (i == bii) v = -1.0f;  // taken
+    }
+    __syncthreads();
+    if (i < NEU) {
+        float s = 0.0f;
+        for (int k = 0; k < NEU; ++k) s += topv[k];
+        wsel[t * NEU + i] = topv[i] / s;
+    }
+}
+
+// argmax of each token's logits, lowest index on ties (faie2fn.cu:1910-1934).  grid nt, 1024 threads
+__global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ logits, int V, int32_t *__restrict__ out) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const float *l = logits + (size_t) blockIdx.x * V;
+    float v = -INFINITY;
+    int idx = 0;
+    for (int i = threadIdx.x; i < V; i += blockDim.x)
+        if (l[i] > v) { v = l[i]; idx = i; }
+    block_argmax(v, idx, bv, bi);
+    if (threadIdx.x == 0) out[blockIdx.x] = idx;
+}
+
+// ------------------------------------------------------------------------------------------------------------
+
+struct QW {
+    QLayout L;
+    uint8_t *p = nullptr;
+};
+
+struct MLayer {
+    bool attn = false;
+    float *hca_norm = nullptr, *hcf_norm = nullptr;
+    QW hca_dinj, hca_up, hcf_dinj, hcf_up;
+    // DeltaNet
+    QW qkv, z, ab, ssm_out;
+    float *conv_w = nullptr, *dt = nullptr, *ssm_a = nullptr, *ssm_norm = nullptr, *S = nullptr, *ring = nullptr;
+    // attention
+    QW q, k, v, o, ixqk;
+    float *qn = nullptr, *kn = nullptr, *ixqn = nullptr, *ixkn = nullptr;
+    float *Kc = nullptr, *Vc = nullptr, *IKc = nullptr, *BKc = nullptr;
+    // FFN
+    QW rsg, sh_gate, sh_up, sh_down, eg, eu, ed;
+};
+
+struct Model {
+    ModelDims d;
+    int max_ctx = 0, nsplit = 1;
+    Gguf g;
+    std::vector<MLayer> L;
+    QW tok, head, out_down, out_up;
+    float *out_norm = nullptr;
+    // activations, MAXT tokens
+    float *h = nullptr, *hn = nullptr, *lr = nullptr, *t320 = nullptr, *a = nullptr, *x = nullptr, *inj = nullptr;
+    float *qkv = nullptr, *zz = nullptr, *abv = nullptr, *on = nullptr, *qg = nullptr, *kk = nullptr, *vv = nullptr;
+    float *iqk = nullptr, *og = nullptr, *y = nullptr, *rsgv = nullptr, *shg = nullptr, *shu = nullptr, *sha = nullptr;
+    float *shd = nullptr, *act = nullptr, *dpart = nullptr, *wsel = nullptr, *logits = nullptr, *work = nullptr;
+    int32_t *ids = nullptr, *sel = nullptr, *pos = nullptr, *am = nullptr;
+    size_t work_bytes = 0;
+    hipStream_t st = nullptr;
+    hipGraphExec_t graph[MAXT + 1] = {};
+    bool use_graphs = true;
+    float *dbg = nullptr;  // host [NL][nt][HC D] when set
+    int n_past = 0;
+    double last_ms = 0;
+    std::vector<void *> allocs;
+    size_t bytes = 0;
+
+    ~Model() {
+        if (st) (void) hipStreamSynchronize(st);
+        for (auto &ge : graph)
+            if (ge) (void) hipGraphExecDestroy(ge);
+        for (void *p : allocs) (void) hipFree(p);
+        if (st) (void) hipStreamDestroy(st);
+    }
+    template <typename T> int alloc(T **p, size_t n) {
+        const size_t nb = std::max<size_t>(n * sizeof(T), 16);
+        const hipError_t e = hipMalloc((void **) p, nb);
+        if (e != hipSuccess) {
+            *p = nullptr;
+            FN_FAIL("load: hipMalloc(" + std::to_string(nb) + " B) -> " + hipGetErrorString(e));
+        }
+        allocs.push_back((void *) *p);
+        bytes += nb;
+        FN_CK(hipMemset(*p, 0, nb));
+        return 0;
+    }
+};
+
+std::unique_ptr<Model> g_model;
+
+// ---- load ----
+
+int need(const Gguf &g, const std::string &name, const GTensor **t) {
+    *t = g.find(name);
+    if (!*t) FN_FAIL("load: tensor " + name + " missing");
+    return 0;
+}
+
+// shape of a 2-D weight (ggml order: ne[0] = columns) or a 3-D expert stack (ne[2] experts of ne[1] rows)
+int check_shape(const std::string &name, const GTensor *t, uint64_t cols, uint64_t rows, uint64_t n3 = 1) {
+    if (t->ne[0] != cols || t->ne[1] * t->ne[2] * t->ne[3] != rows * n3 || (n3 > 1 && t->ne[2] != n3))
+        FN_FAIL("load: tensor " + name + " has shape [" + std::to_string(t->ne[0]) + ", " + std::to_string(t->ne[1]) +
+                ", " + std::to_string(t->ne[2]) + "], expected " + std::to_string(cols) + " columns x " +
+                std::to_string(rows * n3) + " rows");
+    return 0;
+}
+
+// an F32 vector of n values to device memory
+int load_f32(Model &m, const std::string &name, size_t n, float **out) {
+    const GTensor *t;
+    if (need(m.g, name, &t)) return -1;
+    if (t->type != 0) FN_FAIL("load: tensor " + name + " must be F32");
+    if ((size_t) (t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]) != n)
+        FN_FAIL("load: tensor " + name + " has " + std::to_string(t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]) +
+                " values, expected " + std::to_string(n));
+    if (m.alloc(out, n)) return -1;
+    FN_CK(hipMemcpy(*out, t->data, n * 4, hipMemcpyHostToDevice));
+    return 0;
+}
+
+// GGUF rows (one tensor, or several of one type stacked row-wise) -> packed device weight of rows x cols
+int load_qw(Model &m, const std::vector<std::string> &names, const std::vector<uint64_t> &rows, uint64_t cols,
+            QW &w, uint64_t n3 = 1) {
+    uint32_t type = 0;
+    uint64_t total = 0, raw = 0;
+    std::vector<const GTensor *> ts;
+    for (size_t i = 0; i < names.size(); ++i) {
+        const GTensor *t;
+        if (need(m.g, names[i], &t) || check_shape(names[i], t, cols, rows[i], n3)) return -1;
+        if (i && t->type != type) FN_FAIL("load: tensors " + names[0] + " and " + names[i] + " differ in type");
+        type = t->type;
+        total += rows[i] * n3;
+        raw += t->nbytes;
+        ts.push_back(t);
+    }
+    if (total > 0x7fffffffu) FN_FAIL("load: tensor " + names[0] + " has too many rows");
+    if (!qlayout(type, (int) total, (int) cols, w.L)) return -1;  // fn_error says which type / shape
+    uint8_t *stage = nullptr;
+    FN_CK(hipMalloc((void **) &stage, raw));
+    size_t off = 0;
+    hipError_t e = hipSuccess;
+    for (const GTensor *t : ts) {
+        if (e == hipSuccess) e = hipMemcpy(stage + off, t->data, t->nbytes, hipMemcpyHostToDevice);
+        off += t->nbytes;
+    }
+    int rc = e == hipSuccess ? 0 : -1;
+    if (rc) set_error("load: upload of " + names[0] + " -> " + hipGetErrorString(e));
+    if (!rc) rc = m.alloc(&w.p, w.L.bytes);
+    if (!rc) rc = quant_pack_launch(w.L, stage, w.p, nullptr);
+    const hipError_t es = hipDeviceSynchronize();
+    (void) hipFree(stage);
+    if (!rc && es != hipSuccess) FN_FAIL(std::string("load: pack -> ") + hipGetErrorString(es));
+    return rc;
+}
+
+int load_qw1(Model &m, const std::string &name, uint64_t rows, uint64_t cols, QW &w, uint64_t n3 = 1) {
+    return load_qw(m, {name}, {rows}, cols, w, n3);
+}
+
+int read_dims(const Gguf &g, ModelDims &d) {
+    auto it = g.strs.find("general.architecture");
+    if (it == g.strs.end()) FN_FAIL("load: general.architecture missing");
+    const std::string a = it->second + ".";
+    auto num = [&](const char *k, double dflt = -1) { return g.num(a + k, dflt); };
+    d.D = (int) num("embedding_length");
+    d.NL = (int) num("block_count");
+    d.NH = (int) num("attention.head_count");
+    d.NKV = (int) num("attention.head_count_kv");
+    d.HD = (int) num("attention.key_length", 256);
+    d.NROT = (int) num("rope.dimension_count", 64);
+    d.theta = (float) num("rope.freq_base", 1e7);
+    d.eps = (float) num("attention.layer_norm_rms_epsilon", 1e-6);
+    d.NE = (int) num("expert_count");
+    d.NEU = (int) num("expert_used_count");
+    d.FFE = (int) num("expert_feed_forward_length");
+    d.FFS = (int) num("expert_shared_feed_forward_length", d.FFE);
+    d.DS = (int) num("ssm.state_size", 128);
+    d.NKH = (int) num("ssm.group_count");
+    d.NVH = (int) num("ssm.time_step_rank");
+    d.DINNER = (int) num("ssm.inner_size");
+    d.conv = (int) num("ssm.conv_kernel", 4);
+    d.attn_every = (int) num("full_attention_interval", 4);
+    d.HC = (int) num("hyper_connection.count");
+    d.HCR = (int) num("hyper_connection.low_rank");
+    d.IXH = (int) num("attention.indexer.head_count", IXH);
+    d.IXD = (int) num("attention.indexer.key_length", IXD);
+    d.top = (int) num("attention.indexer.top_k", 2048) / IXR;
+    auto ple = g.iarrays.find(a + "ple.layers");
+    d.ple_layers = ple == g.iarrays.end() ? 0 : (int) ple->second.size();
+    const GTensor *te = g.find("token_embd.weight");
+    if (!te) FN_FAIL("load: tensor token_embd.weight missing");
+    d.VOCAB = (int) te->ne[1];
+    d.CONVCH = 2 * d.NKH * d.DS + d.DINNER;
+    auto bad = [](const std::string &what) { FN_FAIL("load: model hyperparameters: " + what); };
+    if (d.D < 32 || d.D % 32 || d.NL < 1 || d.VOCAB < 1) return bad("embedding_length, block_count or vocabulary");
+    if (d.HD != HDK || d.DS != DSK || d.conv != 4) return bad("head dims 256 / 128 and conv kernel 4 are built");
+    if (d.IXH != IXH || d.IXD != IXD || d.top < 1) return bad("the indexer is built for 4 heads of 128");
+    if (d.NKV < 1 || d.NH % d.NKV || (d.NH / d.NKV != 4 && d.NH / d.NKV != 8 && d.NH / d.NKV != 12))
+        return bad("query heads per kv head must be 4, 8 or 12");
+    if (d.NROT < 2 || d.NROT > 128 || d.NROT % 4) return bad("rope dimension count");
+    if (d.NKH < 1 || d.NVH < 1 || d.NVH % d.NKH || d.DINNER != d.NVH * d.DS) return bad("ssm heads");
+    if (d.NE < 1 || d.NE > 1024 || d.NEU < 1 || d.NEU > 32 || d.NEU > d.NE || d.FFE < 32 || d.FFS < 32)
+        return bad("experts (at most 1024, at most 32 used)");
+    if (d.HC < 1 || d.HC > 16 || d.HCR < 1) return bad("hyper-connections");
+    if (d.attn_every < 0) return bad("full_attention_interval");
+    if (d.ple_layers > 0)
+        FN_FAIL("load: the model has per-layer n-gram embedding (PLE) layers, which this library does not build");
+    return 0;
+}
+
+int load_model(Model &m, int max_ctx_req) {
+    const ModelDims &d = m.d;
+    const uint64_t D = d.D, HCD = (uint64_t) d.HC * d.D;
+    m.max_ctx = (std::max(max_ctx_req, 1) + 255) / 256 * 256;
+    FN_CK(hipSetDevice(0));
+    FN_CK(hipStreamCreateWithFlags(&m.st, hipStreamNonBlocking));
+    unsigned *sw = nullptr;  // the status word's address, looked up now rather than under a graph capture
+    if (status_word(&sw)) return -1;
+    if (load_qw1(m, "token_embd.weight", d.VOCAB, D, m.tok) || load_qw1(m, "output.weight", d.VOCAB, D, m.head) ||
+        load_f32(m, "output_hc_norm.weight", HCD, &m.out_norm) ||
+        load_qw1(m, "output_hc_down.weight", d.HCR, HCD, m.out_down) ||
+        load_qw1(m, "output_hc_up.weight", HCD, d.HCR, m.out_up))
+        return -1;
+    m.L.resize(d.NL);
+    for (int il = 0; il < d.NL; ++il) {
+        MLayer &L = m.L[il];
+        L.attn = d.attn_every > 0 && (il + 1) % d.attn_every == 0;
+        const std::string p = "blk." + std::to_string(il) + ".";
+        if (load_f32(m, p + "hc_attn_norm.weight", HCD, &L.hca_norm) ||
+            load_f32(m, p + "hc_ffn_norm.weight", HCD, &L.hcf_norm) ||
+            load_qw(m, {p + "hc_attn_down.weight", p + "hc_attn_inject.weight"}, {(uint64_t) d.HCR, (uint64_t) d.HC},
+                    HCD, L.hca_dinj) ||
+            load_qw1(m, p + "hc_attn_up.weight", HCD, d.HCR, L.hca_up) ||
+            load_qw(m, {p + "hc_ffn_down.weight", p + "hc_ffn_inject.weight"}, {(uint64_t) d.HCR, (uint64_t) d.HC},
+                    HCD, L.hcf_dinj) ||
+            load_qw1(m, p + "hc_ffn_up.weight", HCD, d.HCR, L.hcf_up))
+            return -1;
+        if (!L.attn) {
+            if (load_qw1(m, p + "attn_qkv.weight", d.CONVCH, D, L.qkv) ||
+                load_qw1(m, p + "attn_gate.weight", d.DINNER, D, L.z) ||
+                load_qw(m, {p + "ssm_alpha.weight", p + "ssm_beta.weight"}, {(uint64_t) d.NVH, (uint64_t) d.NVH}, D,
+                        L.ab) ||
+                load_qw1(m, p + "ssm_out.weight", D, d.DINNER, L.ssm_out) ||
+                load_f32(m, p + "ssm_conv1d.weight", (size_t) d.CONVCH * 4, &L.conv_w) ||
+                load_f32(m, p + "ssm_dt.bias", d.NVH, &L.dt) || load_f32(m, p + "ssm_a", d.NVH, &L.ssm_a) ||
+                load_f32(m, p + "ssm_norm.weight", d.DS, &L.ssm_norm) ||
+                m.alloc(&L.S, (size_t) d.NVH * DSK * DSK) || m.alloc(&L.ring, (size_t) RING * d.CONVCH))
+                return -1;
+        } else {
+            const size_t cache = (size_t) d.NKV * m.max_ctx * HDK;
+            if (load_qw1(m, p + "attn_q.weight", (uint64_t) d.NH * 2 * HDK, D, L.q) ||
+                load_qw1(m, p + "attn_k.weight", (uint64_t) d.NKV * HDK, D, L.k) ||
+                load_qw1(m, p + "attn_v.weight", (uint64_t) d.NKV * HDK, D, L.v) ||
+                load_qw1(m, p + "attn_output.weight", D, (uint64_t) d.NH * HDK, L.o) ||
+                load_qw(m, {p + "indexer.q_proj.weight", p + "indexer.k_proj.weight"},
+                        {(uint64_t) IXH * IXD, (uint64_t) IXD}, D, L.ixqk) ||
+                load_f32(m, p + "attn_q_norm.weight", HDK, &L.qn) || load_f32(m, p + "attn_k_norm.weight", HDK, &L.kn) ||
+                load_f32(m, p + "indexer.q_norm.weight", IXD, &L.ixqn) ||
+                load_f32(m, p + "indexer.k_norm.weight", IXD, &L.ixkn) || m.alloc(&L.Kc, cache) ||
+                m.alloc(&L.Vc, cache) || m.alloc(&L.IKc, (size_t) m.max_ctx * IXD) ||
+                m.alloc(&L.BKc, (size_t) m.max_ctx / IXR * IXD))
+                return -1;
+        }
+        if (load_qw(m, {p + "ffn_gate_inp.weight", p + "ffn_gate_inp_shexp.weight"}, {(uint64_t) d.NE, 1}, D, L.rsg) ||
+            load_qw1(m, p + "ffn_gate_shexp.weight", d.FFS, D, L.sh_gate) ||
+            load_qw1(m, p + "ffn_up_shexp.weight", d.FFS, D, L.sh_up) ||
+            load_qw1(m, p + "ffn_down_shexp.weight", D, d.FFS, L.sh_down) ||
+            load_qw1(m, p + "ffn_gate_exps.weight", d.FFE, D, L.eg, d.NE) ||
+            load_qw1(m, p + "ffn_up_exps.weight", d.FFE, D, L.eu, d.NE) ||
+            load_qw1(m, p + "ffn_down_exps.weight", D, d.FFE, L.ed, d.NE))
+            return -1;
+        if (L.eg.L.type != L.eu.L.type) FN_FAIL("load: " + p + " gate and up experts differ in type");
+    }
+    // activations for MAXT tokens
+    const size_t T = MAXT;
+    const int ldr = d.HCR + d.HC;
+    m.nsplit = attn_pick_nsplit(1, d.NKV, MAXT, 4 * d.top + 4);
+    for (int nt = 1; nt <= MAXT; ++nt)
+        m.work_bytes = std::max(m.work_bytes, attn_qsa_work_bytes(1, d.NH, nt, HDK, m.nsplit, m.max_ctx, d.top) + 256);
+    if (m.alloc(&m.h, T * HCD) || m.alloc(&m.hn, T * HCD) || m.alloc(&m.lr, T * ldr) ||
+        m.alloc(&m.t320, T * d.HCR) || m.alloc(&m.a, T * HCD) || m.alloc(&m.x, T * D) || m.alloc(&m.inj, T * d.HC) ||
+        m.alloc(&m.qkv, T * d.CONVCH) || m.alloc(&m.zz, T * d.DINNER) || m.alloc(&m.abv, T * 2 * d.NVH) ||
+        m.alloc(&m.on, T * d.DINNER) || m.alloc(&m.qg, T * d.NH * 2 * HDK) || m.alloc(&m.kk, T * d.NKV * HDK) ||
+        m.alloc(&m.vv, T * d.NKV * HDK) || m.alloc(&m.iqk, T * (IXH * IXD + IXD)) || m.alloc(&m.og, T * d.NH * HDK) ||
+        m.alloc(&m.y, T * D) || m.alloc(&m.rsgv, T * (d.NE + 1)) || m.alloc(&m.shg, T * d.FFS) ||
+        m.alloc(&m.shu, T * d.FFS) || m.alloc(&m.sha, T * d.FFS) || m.alloc(&m.shd, T * D) ||
+        m.alloc(&m.act, T * d.NEU * d.FFE) || m.alloc(&m.dpart, T * d.NEU * D) || m.alloc(&m.wsel, T * d.NEU) ||
+        m.alloc(&m.logits, T * d.VOCAB) || m.alloc(&m.work, m.work_bytes / 4 + 1) || m.alloc(&m.ids, T) ||
+        m.alloc(&m.sel, T * d.NEU) || m.alloc(&m.pos, 1) || m.alloc(&m.am, T))
+        return -1;
+    FN_CK(hipDeviceSynchronize());
+    return 0;
+}
+
+// ---- forward ----
+
+int gemv(const QW &w, const float *x, int nt, float *y, hipStream_t st) {
+    return gemv_launch(w.L, w.p, x, nt, y, nullptr, 0, st);
+}
+
+// hyper-connection read of m.hn (already normalized) through the down(+inject) and up weights into m.x, m.inj
+int hc_read(Model &m, const QW &dinj, const QW &up, int nt) {
+    const ModelDims &d = m.d;
+    const bool inj = dinj.L.rows > d.HCR;
+    const int ldr = dinj.L.rows;
+    if (gemv(dinj, m.hn, nt, m.lr, m.st)) return -1;
+    hipLaunchKernelGGL(k_hc_lowrank, dim3(nt), dim3(256), 0, m.st, m.lr, ldr, d.HCR, d.HC, m.t320);
+    if (gemv(up, m.t320, nt, m.a, m.st)) return -1;
+    hipLaunchKernelGGL(k_hc_mix, dim3(nt, (d.D + 255) / 256), dim3(256), 0, m.st, m.a, m.hn, d.D, d.HC, m.lr, ldr,
+                       d.HCR, m.x, inj ? m.inj : nullptr);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+int mixer(Model &m, MLayer &L, int nt) {
+    const ModelDims &d = m.d;
+    if (!L.attn) {
+        if (gemv(L.qkv, m.x, nt, m.qkv, m.st) || gemv(L.z, m.x, nt, m.zz, m.st) || gemv(L.ab, m.x, nt, m.abv, m.st))
+            return -1;
+        GdnBlock p{1, d.NKH, d.NVH, DSK, DSK, 0, 0, nt, RING, d.eps, m.pos, m.qkv, L.conv_w, L.ring, m.abv, L.dt,
+                   L.ssm_a, L.S, m.zz, L.ssm_norm, m.on};
+        if (gdn_block_launch(p, m.st)) return -1;
+        return gemv(L.ssm_out, m.on, nt, m.y, m.st);
+    }
+    if (gemv(L.q, m.x, nt, m.qg, m.st) || gemv(L.k, m.x, nt, m.kk, m.st) || gemv(L.v, m.x, nt, m.vv, m.st) ||
+        gemv(L.ixqk, m.x, nt, m.iqk, m.st))
+        return -1;
+    AttnDecode p{1, d.NH, d.NKV, HDK, d.NROT, nt, m.max_ctx, m.nsplit, d.theta, d.eps, m.pos, m.qg, m.kk, m.vv, L.qn,
+                 L.kn, L.Kc, L.Vc, m.work, m.work_bytes, m.og};
+    QsaIndexer ix{1, nt, m.max_ctx, d.top, d.NROT, d.theta, d.eps, m.pos, m.iqk, L.ixqn, L.ixkn, L.IKc, L.BKc};
+    if (attn_qsa_launch(p, ix, m.st)) return -1;
+    return gemv(L.o, m.og, nt, m.y, m.st);
+}
+
+int ffn(Model &m, MLayer &L, int nt, const float *next_norm) {
+    const ModelDims &d = m.d;
+    if (gemv(L.rsg, m.x, nt, m.rsgv, m.st) || gemv(L.sh_gate, m.x, nt, m.shg, m.st) ||
+        gemv(L.sh_up, m.x, nt, m.shu, m.st))
+        return -1;
+    hipLaunchKernelGGL(k_route, dim3(nt), dim3(1024), 0, m.st, m.rsgv, d.NE, d.NEU, m.shg, m.shu, d.FFS, m.sel,
+                       m.wsel, m.sha);
+    FN_CK(hipGetLastError());
+    const int np = nt * d.NEU;
+    if (swiglu_launch(L.eg.L, L.eg.p, L.eu.L, L.eu.p, d.FFE, m.sel, np, d.NEU, m.x, m.act, m.st) ||
+        gemv(L.sh_down, m.sha, nt, m.shd, m.st) || rows_launch(L.ed.L, L.ed.p, d.D, m.sel, np, 1, m.act, m.dpart, m.st))
+        return -1;
+    hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, m.shd, m.inj, d.D, d.HC, m.dpart, m.wsel,
+                       d.NEU, m.rsgv, d.NE, next_norm, d.eps, m.hn);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+int enqueue(Model &m, int nt) {
+    const ModelDims &d = m.d;
+    const size_t HCD = (size_t) d.HC * d.D;
+    if (embed_launch(m.tok.L, m.tok.p, m.ids, nt, d.HC, m.h, m.st)) return -1;
+    hipLaunchKernelGGL(k_groupnorm, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, m.L[0].hca_norm, d.D, d.eps, m.hn);
+    for (int il = 0; il < d.NL; ++il) {
+        MLayer &L = m.L[il];
+        if (hc_read(m, L.hca_dinj, L.hca_up, nt) || mixer(m, L, nt)) return -1;
+        hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, m.y, m.inj, d.D, d.HC, nullptr, nullptr, 0,
+                           nullptr, 0, L.hcf_norm, d.eps, m.hn);
+        if (hc_read(m, L.hcf_dinj, L.hcf_up, nt)) return -1;
+        const float *next = il + 1 < d.NL ? m.L[il + 1].hca_norm : m.out_norm;
+        if (ffn(m, L, nt, next)) return -1;
+        if (m.dbg)
+            FN_CK(hipMemcpyAsync(m.dbg + (size_t) il * nt * HCD, m.h, (size_t) nt * HCD * 4, hipMemcpyDeviceToHost,
+                                 m.st));
+    }
+    if (hc_read(m, m.out_down, m.out_up, nt) || gemv(m.head, m.x, nt, m.logits, m.st)) return -1;
+    hipLaunchKernelGGL(k_argmax, dim3(nt), dim3(1024), 0, m.st, m.logits, d.VOCAB, m.am);
+    FN_CK(hipGetLastError());
+    return advance_launch(m.pos, 1, nt, m.st);
+}
+
+int capture(Model &m, int nt) {
+    FN_CK(hipStreamBeginCapture(m.st, hipStreamCaptureModeThreadLocal));
+    const int rc = enqueue(m, nt);
+    hipGraph_t g = nullptr;
+    const hipError_t ec = hipStreamEndCapture(m.st, &g);
+    if (rc) {
+        if (g) (void) hipGraphDestroy(g);
+        return -1;
+    }
+    FN_CK(ec);
+    const hipError_t ei = hipGraphInstantiate(&m.graph[nt], g, nullptr, nullptr, 0);
+    (void) hipGraphDestroy(g);
+    FN_CK(ei);
+    return 0;
+}
+
+int drop_graphs(Model &m) {
+    FN_CK(hipStreamSynchronize(m.st));
+    for (auto &ge : m.graph)
+        if (ge) {
+            FN_CK(hipGraphExecDestroy(ge));
+            ge = nullptr;
+        }
+    return 0;
+}
+
+}  // namespace
+
+int model_load(const char *shard1, const char *shard2, int max_ctx) {
+    g_model.reset();
+    auto m = std::make_unique<Model>();
+    if (gguf_open(m->g, shard1) || read_dims(m->g, m->d)) return -1;
+    if (shard2 && *shard2 && std::string(shard2) != shard1)
+        FN_FAIL("load: a second shard holds only the PLE n-gram table, which this library does not build; pass the "
+                "model in one file");
+    path_free();
+    if (load_model(*m, max_ctx)) return -1;
+    g_model = std::move(m);
+    return 0;
+}
+
+int model_forward(const int32_t *tokens, int nt, float *logits, int32_t *argmax) {
+    if (!g_model) FN_FAIL("not loaded");
+    Model &m = *g_model;
+    if (nt < 1 || nt > MAXT) FN_FAIL("nt out of range");
+    if (!tokens) FN_FAIL("forward: null tokens");
+    if (m.n_past + nt > m.max_ctx) FN_FAIL("context full");
+    for (int t = 0; t < nt; ++t)
+        if (tokens[t] < 0 || tokens[t] >= m.d.VOCAB) FN_FAIL("forward: token id outside the vocabulary");
+    const auto t0 = std::chrono::steady_clock::now();
+    FN_CK(hipMemcpyAsync(m.ids, tokens, (size_t) nt * 4, hipMemcpyHostToDevice, m.st));
+    const bool graphs = m.use_graphs && !m.dbg;
+    if (graphs) {
+        if (!m.graph[nt] && capture(m, nt)) return -1;
+        FN_CK(hipGraphLaunch(m.graph[nt], m.st));
+    } else if (enqueue(m, nt)) {
+        return -1;
+    }
+    if (logits)
+        FN_CK(hipMemcpyAsync(logits, m.logits, (size_t) nt * m.d.VOCAB * 4, hipMemcpyDeviceToHost, m.st));
+    if (argmax) FN_CK(hipMemcpyAsync(argmax, m.am, (size_t) nt * 4, hipMemcpyDeviceToHost, m.st));
+    FN_CK(hipStreamSynchronize(m.st));
+    unsigned bits = 0;
+    if (status_read(&bits, true)) return -1;
+    if (bits) FN_FAIL("forward: a kernel recorded misuse (status bits " + std::to_string(bits) + ")");
+    m.n_past += nt;
+    m.last_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    return 0;
+}
+
+int model_debug_layers(float *out) {
+    if (!g_model) FN_FAIL("not loaded");
+    g_model->dbg = out;
+    return 0;
+}
+
+int model_reset() {
+    if (!g_model) FN_FAIL("not loaded");
+    Model &m = *g_model;
+    FN_CK(hipStreamSynchronize(m.st));
+    for (MLayer &L : m.L)
+        if (!L.attn) {
+            FN_CK(hipMemset(L.S, 0, (size_t) m.d.NVH * DSK * DSK * 4));
+            FN_CK(hipMemset(L.ring, 0, (size_t) RING * m.d.CONVCH * 4));
+        }
+    FN_CK(hipMemset(m.pos, 0, 4));
+    FN_CK(hipDeviceSynchronize());
+    m.n_past = 0;
+    return 0;
+}
+
+int model_use_graphs(int on) {
+    if (!g_model) FN_FAIL("not loaded");
+    if (drop_graphs(*g_model)) return -1;
+    g_model->use_graphs = on != 0;
+    return 0;
+}
+
+bool model_loaded() { return (bool) g_model; }
+void model_free() { g_model.reset(); }
+int model_n_past() { return g_model ? g_model->n_past : -1; }
+double model_dev_gb() { return g_model ? g_model->bytes / 1e9 : -1; }
+double model_last_ms() { return g_model ? g_model->last_ms : -1; }
+int model_layers() { return g_model ? g_model->d.NL : -1; }
+int model_dims(ModelDims *d) {
+    if (!g_model) FN_FAIL("not loaded");
+    *d = g_model->d;
+    return 0;
+}
+
+int model_inspect(const char *path, ModelDims *d) {
+    Gguf g;
+    if (gguf_open(g, path) || read_dims(g, *d)) return -1;
+    return 0;
+}
+
+}  // namespace fn

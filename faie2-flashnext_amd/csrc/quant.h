@@ -67,4 +67,18 @@ int quant_dequant_launch(const QLayout &L, const uint8_t *packed, float *out, hi
 int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, float *y, float *work,
                 size_t work_bytes, hipStream_t st);
 
+// Rows of a packed weight selected on the device (the model forward's embedding and routed experts):
+//   embed_launch: out[t][k * cols + c] = W[ids[t]][c] for k < copies (the GGUF decode, bit for bit);
+//   rows_launch: out[p][r] = W[e_p * R + r] . x[p / xdiv] for r < R, p < npairs, e_p = sel[p] (sel null: e_p = 0),
+//     x rows of cols floats;
+//   swiglu_launch: act[p][r] = silu(Wg[e_p R + r] . x[p / xdiv]) * (Wu[e_p R + r] . x[p / xdiv]).
+// Each row is summed by 16 lanes, lane li taking groups li, li + 16, ... in ascending order (the arithmetic of the
+// GEMV with 16 lanes per row); x and out 16-byte aligned.
+int embed_launch(const QLayout &L, const uint8_t *packed, const int32_t *ids, int nt, int copies, float *out,
+                 hipStream_t st);
+int rows_launch(const QLayout &L, const uint8_t *packed, int R, const int32_t *sel, int npairs, int xdiv,
+                const float *x, float *out, hipStream_t st);
+int swiglu_launch(const QLayout &Lg, const uint8_t *pg, const QLayout &Lu, const uint8_t *pu, int R,
+                  const int32_t *sel, int npairs, int xdiv, const float *x, float *act, hipStream_t st);
+
 }  // namespace fn

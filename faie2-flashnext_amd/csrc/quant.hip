@@ -813,6 +813,77 @@ int gemv_t(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, in
     }
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// rows selected on the device: the model's token embedding and routed experts
+
+// embedding rows: out[t][k cols + c] = decoded W[ids[t]][c], for k < copies.  grid nt, 256 threads
+template <uint32_t TY>
+__global__ void __launch_bounds__(256) k_embed(PP P, int G, int cols, const int32_t *__restrict__ ids, int copies,
+                                               float *__restrict__ out) {
+    if constexpr (tab_lds<TY>() > 0) {
+        tab_fill<TY>(threadIdx.x, blockDim.x);
+        __syncthreads();
+    }
+    const int t = blockIdx.x, row = ids[t];
+    for (int g = threadIdx.x; g < G; g += blockDim.x) {
+        Grp o;
+        decode<TY>(P, row, g, o);
+        float4 v[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int h = c >> 2;
+            float e[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float q = o.q[4 * c + k];
+                e[k] = TY == QT_BF16 ? q : __builtin_fmaf(o.s[h], q, -o.m[h]);
+            }
+            v[c] = make_float4(e[0], e[1], e[2], e[3]);
+        }
+        for (int k = 0; k < copies; ++k) {
+            float4 *dst = reinterpret_cast<float4 *>(out + ((size_t) t * copies + k) * cols + (size_t) g * 32);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) dst[c] = v[c];
+        }
+    }
+}
+
+// row r of expert sel[p] (R rows per expert) against x[p / xdiv]: 16 lanes per row, 4 rows per wave, 16 rows per
+// workgroup; lane li sums its groups li, li + 16, ... in order.  grid (ceil(R / 16), npairs), 256 threads.
+// SWIGLU: the gate row of Wg and the up row of Wu, out = silu(g) * u.
+template <uint32_t TY, bool SWIGLU>
+__global__ void __launch_bounds__(256) k_rows(PP Pg, PP Pu, int R, int nexp, int G, int cols,
+                                              const int32_t *__restrict__ sel, int xdiv, const float *__restrict__ x,
+                                              float *__restrict__ out) {
+    if constexpr (tab_lds<TY>() > 0) {
+        tab_fill<TY>(threadIdx.x, blockDim.x);
+        __syncthreads();
+    }
+    const TabT<TY> T;
+    const int p = blockIdx.y, lane = threadIdx.x & 63, li = lane & 15;
+    const int r = blockIdx.x * 16 + (threadIdx.x >> 6) * 4 + (lane >> 4);
+    const int e = sel ? min(max(sel[p], 0), nexp - 1) : 0;  // an id outside the weight reads its last expert
+    const int row = e * R + min(r, R - 1);
+    const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t) (p / xdiv) * cols);
+    float ag = 0.0f, au = 0.0f;
+    for (int g = li; g < G; g += 16) {
+        uint32_t w[Q<TY>::NW];
+        Q<TY>::load(row_planes(Pg, row), g, w);
+        accumulate<TY, 1>(w, g, xp + 8 * g, &ag, T);
+        if constexpr (SWIGLU) {
+            Q<TY>::load(row_planes(Pu, row), g, w);
+            accumulate<TY, 1>(w, g, xp + 8 * g, &au, T);
+        }
+    }
+    ag = row_sum(ag);
+    if constexpr (SWIGLU) au = row_sum(au);
+    if (li == 0 && r < R) {
+        float v = ag;
+        if constexpr (SWIGLU) v = ag / (1.0f + expf(-ag)) * au;
+        out[(size_t) p * R + r] = v;
+    }
+}
+
 }  // namespace
 
 bool qlayout(uint32_t type, int rows, int cols, QLayout &L) {
@@ -956,6 +1027,81 @@ int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt,
         FN_CK(hipGetLastError());
     }
     return 0;
+}
+
+namespace {
+
+template <uint32_t TY>
+int embed_t(const QLayout &L, const PP &P, const int32_t *ids, int nt, int copies, float *out, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed<TY>, dim3((unsigned) nt), dim3(256), 0, st, P, L.cols / 32, L.cols, ids, copies, out);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+template <uint32_t TY, bool SW>
+int rows_t(const QLayout &L, const PP &Pg, const PP &Pu, int R, const int32_t *sel, int npairs, int xdiv,
+           const float *x, float *out, hipStream_t st) {
+    hipLaunchKernelGGL((k_rows<TY, SW>), dim3((unsigned) ((R + 15) / 16), (unsigned) npairs), dim3(256), 0, st, Pg,
+                       Pu, R, L.rows / R, L.cols / 32, L.cols, sel, xdiv, x, out);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+template <bool SW>
+int rows_any(const QLayout &L, const PP &Pg, const PP &Pu, int R, const int32_t *sel, int npairs, int xdiv,
+             const float *x, float *out, hipStream_t st) {
+    switch (L.type) {
+        case QT_BF16: return rows_t<QT_BF16, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
+        case QT_Q8_0: return rows_t<QT_Q8_0, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
+        case QT_IQ4_NL: return rows_t<QT_IQ4_NL, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
+        case QT_IQ4_XS: return rows_t<QT_IQ4_XS, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
+        case QT_IQ3_S: return rows_t<QT_IQ3_S, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
+        case QT_Q4_K: return rows_t<QT_Q4_K, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
+        case QT_Q5_K: return rows_t<QT_Q5_K, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
+        case QT_Q6_K: return rows_t<QT_Q6_K, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
+        default: FN_FAIL("rows: unsupported type");
+    }
+}
+
+int rows_check(const QLayout &L, int R, int npairs, int xdiv, const float *x, const float *out) {
+    if (R < 1 || L.rows % R || npairs < 1 || npairs > 65535 || xdiv < 1) FN_FAIL("rows: bad shape");
+    if (!x || !out) FN_FAIL("rows: null pointer");
+    if (((uintptr_t) x | (uintptr_t) out) % 16) FN_FAIL("rows: x and out must be 16-byte aligned");
+    return 0;
+}
+
+}  // namespace
+
+int embed_launch(const QLayout &L, const uint8_t *packed, const int32_t *ids, int nt, int copies, float *out,
+                 hipStream_t st) {
+    if (!packed || !ids || !out || nt < 1 || copies < 1) FN_FAIL("embed: bad arguments");
+    if ((uintptr_t) out % 16) FN_FAIL("embed: out must be 16-byte aligned");
+    const PP P = planes(L, packed);
+    switch (L.type) {
+        case QT_BF16: return embed_t<QT_BF16>(L, P, ids, nt, copies, out, st);
+        case QT_Q8_0: return embed_t<QT_Q8_0>(L, P, ids, nt, copies, out, st);
+        case QT_IQ4_NL: return embed_t<QT_IQ4_NL>(L, P, ids, nt, copies, out, st);
+        case QT_IQ4_XS: return embed_t<QT_IQ4_XS>(L, P, ids, nt, copies, out, st);
+        case QT_IQ3_S: return embed_t<QT_IQ3_S>(L, P, ids, nt, copies, out, st);
+        case QT_Q4_K: return embed_t<QT_Q4_K>(L, P, ids, nt, copies, out, st);
+        case QT_Q5_K: return embed_t<QT_Q5_K>(L, P, ids, nt, copies, out, st);
+        case QT_Q6_K: return embed_t<QT_Q6_K>(L, P, ids, nt, copies, out, st);
+        default: FN_FAIL("embed: unsupported type");
+    }
+}
+
+int rows_launch(const QLayout &L, const uint8_t *packed, int R, const int32_t *sel, int npairs, int xdiv,
+                const float *x, float *out, hipStream_t st) {
+    if (!packed || rows_check(L, R, npairs, xdiv, x, out)) return -1;
+    const PP P = planes(L, packed);
+    return rows_any<false>(L, P, P, R, sel, npairs, xdiv, x, out, st);
+}
+
+int swiglu_launch(const QLayout &Lg, const uint8_t *pg, const QLayout &Lu, const uint8_t *pu, int R,
+                  const int32_t *sel, int npairs, int xdiv, const float *x, float *act, hipStream_t st) {
+    if (!pg || !pu || rows_check(Lg, R, npairs, xdiv, x, act)) return -1;
+    if (Lg.type != Lu.type || Lg.rows != Lu.rows || Lg.cols != Lu.cols) FN_FAIL("swiglu: gate and up weights differ");
+    return rows_any<true>(Lg, planes(Lg, pg), planes(Lu, pu), R, sel, npairs, xdiv, x, act, st);
 }
 
 }  // namespace fn

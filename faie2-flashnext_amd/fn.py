@@ -37,8 +37,12 @@ SYMBOLS = (
     "fn_attn_qsa_dev", "fn_attn_qsa_work_bytes", "fn_ix_blocks_dev", "fn_test_attn_qsa",
     "fn_gemv_packed_bytes", "fn_gemv_pack_dev", "fn_dequant_dev", "fn_gemv_work_bytes", "fn_gemv_dev",
     "fn_gdn_verify_dev", "fn_advance_by_dev", "fn_gdn_block_xab_dev",
-    "fn_attn_noalloc_dev", "fn_dev_status",
+    "fn_attn_noalloc_dev", "fn_dev_status", "fn_model_dims",
 )
+
+# the shapes fn_model_dims writes, in order (include/faie2fn.h section 6)
+MODEL_DIMS = ("D", "NL", "NH", "NKV", "HD", "NROT", "NE", "NEU", "FFE", "FFS", "DS", "NKH", "NVH", "DINNER", "CONVCH",
+              "attn_every", "HC", "HCR", "IXH", "IXD", "top", "VOCAB")
 
 # status bits of fn_dev_status (include/faie2fn.h)
 STATUS_POS, STATUS_KR = 1, 2
@@ -134,6 +138,7 @@ class FN:
         d.fn_bench_gemv.argtypes = [u32, i, i, i, i, C.POINTER(C.c_float)]
         d.fn_gemv_override.argtypes = [i] * 4
         d.fn_gemv_waves.argtypes = [i]
+        d.fn_model_dims.argtypes = [C.c_char_p, I32, i]
         d.fn_dev_status.argtypes = [i]
         d.fn_bench_hot.argtypes = [i]
         d.fn_gemv_packed_bytes.restype = sz
@@ -149,8 +154,17 @@ class FN:
             raise RuntimeError(self.d.fn_error().decode())
 
     # ---- the reference's methods (flashnext/fn.py:40-66) ----
-    def load(self, shard1, shard2, max_ctx=32768, split=0):
-        self.check(self.d.fn_load(shard1.encode(), shard2.encode(), max_ctx, split))
+    def load(self, shard1, shard2="", max_ctx=32768, split=0):
+        self.check(self.d.fn_load(shard1.encode(), (shard2 or "").encode(), max_ctx, split))
+        self.vocab = self.model_dims(shard1)["VOCAB"]
+
+    def model_dims(self, path):
+        """The model shapes fn_load reads from a GGUF file (no device work)."""
+        out = np.zeros(32, np.int32)
+        n = self.d.fn_model_dims(path.encode(), out, len(out))
+        if n < 0:
+            raise RuntimeError(self.d.fn_error().decode())
+        return dict(zip(MODEL_DIMS, out[:n].tolist()))
 
     def reset(self):
         self.check(self.d.fn_reset())
@@ -158,7 +172,7 @@ class FN:
     def forward(self, tokens, logits=False):
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         am = np.zeros(len(t), np.int32)
-        lg = np.zeros((len(t), VOCAB), np.float32) if logits else None
+        lg = np.zeros((len(t), getattr(self, "vocab", VOCAB)), np.float32) if logits else None
         self.check(self.d.fn_forward(t, len(t), lg.ctypes.data if logits else None, am.ctypes.data))
         return (am, lg) if logits else am
 

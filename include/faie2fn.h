@@ -23,14 +23,17 @@ extern "C" {
 
 /* ======================================================================================================
  * 1. The reference's C API, same names and C signatures (engine/faie2fn.cu, flashnext/fn.py:26-34), so that
- *    flashnext/fn.py's argtypes bind unchanged.  This library carries the decode-attention path and the GEMV of
- *    its projections: the GEMV hooks (fn_test_dequant, fn_test_gemv, fn_gemv_plan, fn_bench_gemv,
- *    fn_gemv_override, fn_bench_hot) work as in the reference for the formats of section 5; the model-level
- *    entries (GGUF load, forward, MoE, routing) return -1 with an fn_error() message that says so, and the
- *    getters return -1 like the reference's do when no model is loaded.
+ *    flashnext/fn.py's argtypes bind unchanged.  The GEMV hooks (fn_test_dequant, fn_test_gemv, fn_gemv_plan,
+ *    fn_bench_gemv, fn_gemv_override, fn_bench_hot) work as in the reference for the formats of section 5.
+ *    fn_load / fn_forward / fn_debug_layers run the model on one GPU (section 6); fn_bench_route returns -1 (not
+ *    built).  The engine entry points (fn_reset, fn_use_graphs, fn_n_past, fn_dev_gb, fn_last_ms, fn_split,
+ *    fn_free) act on the loaded model, else on the path engine of section 4, and return -1 like the reference's
+ *    when neither is loaded.
  * ====================================================================================================== */
 const char *fn_error(void);                                                   /* faie2fn.cu:2495 */
 void fn_free(void);                                                           /* faie2fn.cu:2497 */
+/* One GPU: the whole model in shard1 (shard2 NULL, "" or the same file; a second shard holds only the PLE n-gram
+ * table, which is not built); split is ignored (every layer on device 0, fn_split() then returns the layer count). */
 int fn_load(const char *shard1, const char *shard2, int max_ctx, int split);  /* faie2fn.cu:2524 */
 int fn_split(void);                                                           /* faie2fn.cu:2698 */
 double fn_dev_gb(int dv);                                                     /* faie2fn.cu:2699 */
@@ -303,6 +306,23 @@ size_t fn_gemv_work_bytes(uint32_t type, int rows, int cols, int nt);
 /* y [nt][rows] = W x, x [nt][cols], nt 1..8, on device buffers; split-K partials (if any) in work. */
 int fn_gemv_dev(uint32_t type, const uint8_t *packed, int rows, int cols, const float *x, int nt, float *y,
                 float *work, size_t work_bytes, void *stream);
+
+/* ======================================================================================================
+ * 6. Model (new beside the reference's fn_load / fn_forward, faie2fn.cu:2524, 2733): what fn_load reads.
+ *    Shapes come from the GGUF metadata (<general.architecture>.* keys: embedding_length, block_count,
+ *    attention.head_count(_kv), expert_count, expert_used_count, expert_(shared_)feed_forward_length, ssm.*,
+ *    hyper_connection.count / low_rank, attention.indexer.*, full_attention_interval, rope.*) and the token
+ *    embedding; head_dim 256, DeltaNet head dim 128, conv kernel 4 and the indexer's 4 x 128 are the built sizes.
+ *    Tensor names are the reference's (token_embd, output, output_hc_*, blk.N.{hc_attn_*, hc_ffn_*, attn_qkv,
+ *    attn_gate, ssm_*, attn_q/k/v/output, attn_q_norm/k_norm, indexer.*, ffn_gate_inp(_shexp), ffn_*_shexp,
+ *    ffn_*_exps}); weights in the formats of section 5, norms and conv weights F32.
+ * ====================================================================================================== */
+
+/* Parse a GGUF file (no device work) and write its model shapes to out[0..n): {D, layers, q heads, kv heads,
+ * head dim, rope dims, experts, experts used, expert ffn, shared ffn, ssm state, ssm groups, ssm value heads,
+ * ssm inner, conv channels, attention interval, hyper-connections, hc low rank, indexer heads, indexer dim,
+ * indexer top blocks, vocabulary}.  Returns the number of values (22) or -1 (fn_error: what is wrong or missing). */
+int fn_model_dims(const char *path, int *out, int n);
 
 #ifdef __cplusplus
 }

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol(fnlib):
 def test_reference_entries_report_not_built(fnlib):
     d = fnlib.d
     assert d.fn_load(b"a.gguf", b"b.gguf", 4096, 0) == -1
-    assert b"not built" in d.fn_error()
+    assert b"cannot open a.gguf" in d.fn_error()
     with pytest.raises(RuntimeError, match="not loaded"):
         fnlib.reset()
     with pytest.raises(RuntimeError, match="not loaded"):

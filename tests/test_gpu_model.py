@@ -1,0 +1,119 @@
+"""GPU parity of the whole model: fn_load of a synthetic GGUF with the reference model's structure (tensor names,
+metadata, weight formats; small dimensions), then fn_forward over a token sequence against the float64 model oracle
+(oracle/model.py): logits of every call and the residual streams after every layer (fn_debug_layers) within 1e-5
+normwise, the argmax token equal wherever the oracle's top two logits are apart.
+
+The sequence runs past the indexer's threshold (top 8 blocks of 4 keys), so the attention layer switches from dense
+to sparse inside it; calls take 1 to 8 tokens.  Every case prints what names it before the GPU calls.
+"""
+
+import numpy as np
+import pytest
+
+import model_synth as ms
+import oracle.model as om
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+CHUNKS = [1, 3, 8, 2, 8, 8, 5, 8, 8, 7, 1, 8, 8, 4]   # 79 tokens
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-300))
+
+
+@pytest.fixture(scope="module")
+def model_file(tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("model") / "tiny.gguf")
+    kv, ts = ms.write_model(path, ms.TINY_DIMS, seed=11)
+    return path, kv, ts
+
+
+def _run(fnlib, ref, ids, debug):
+    """fn_forward over ids in CHUNKS, checked against the oracle after every call; returns the GPU logits."""
+    outs = []
+    i = 0
+    worst = [0.0, 0.0]
+    NL, HCD = ref.NL, ref.HC * ref.D
+    for c, nt in enumerate(CHUNKS):
+        tok = ids[i:i + nt]
+        i += nt
+        buf = np.zeros((NL, nt, HCD), np.float32) if debug else None
+        fnlib.debug_layers(buf)
+        am, lg = fnlib.forward(tok, logits=True)
+        want, want_am, hs, _ = ref.forward(tok)
+        e = _rel(lg, want)
+        worst[0] = max(worst[0], e)
+        assert e <= TOL, (c, nt, e)
+        if debug:
+            for il in range(NL):
+                eh = _rel(buf[il], hs[il])
+                worst[1] = max(worst[1], eh)
+                assert eh <= TOL, (c, il, eh)
+        for t in range(nt):
+            top2 = np.sort(want[t])[-2:]
+            if top2[1] - top2[0] > 1e-4 * abs(top2[1]):
+                assert am[t] == want_am[t], (c, t)
+        outs.append(lg)
+    fnlib.debug_layers(None)
+    _say(f"  worst normwise error: logits {worst[0]:.3e}, residual streams {worst[1]:.3e}")
+    return np.concatenate(outs)
+
+
+def test_model_forward_matches_oracle(fnlib, model_file):
+    path, kv, ts = model_file
+    _say(f"model forward: tiny synthetic model, {sum(CHUNKS)} tokens in calls of {CHUNKS}, per-layer debug")
+    fnlib.load(path, "", max_ctx=256)
+    try:
+        assert fnlib.d.fn_split() == ms.TINY_DIMS["NL"] and fnlib.d.fn_dev_gb(0) > 0
+        ref = om.Model(kv, ts, max_ctx=256)
+        ids = np.random.default_rng(2).integers(0, ms.TINY_DIMS["VOCAB"], size=sum(CHUNKS))
+        _run(fnlib, ref, ids, debug=True)
+        assert fnlib.d.fn_n_past() == sum(CHUNKS)
+    finally:
+        fnlib.free()
+
+
+def test_model_graphs_equal_eager_and_reset(fnlib, model_file):
+    """The same tokens through captured graphs and eagerly give the same bits; fn_reset returns the model to its
+    first state (DeltaNet state, conv rings and the position; the caches are overwritten from position 0)."""
+    path, kv, ts = model_file
+    _say("model forward: graphs vs eager, reset")
+    fnlib.load(path, "", max_ctx=256)
+    try:
+        ids = np.random.default_rng(4).integers(0, ms.TINY_DIMS["VOCAB"], size=20)
+        res = []
+        for graphs in (True, False, True):
+            fnlib.d.fn_use_graphs(1 if graphs else 0)
+            fnlib.reset()
+            out = [fnlib.forward(ids[k:k + 5], logits=True)[1] for k in range(0, 20, 5)]
+            res.append(np.concatenate(out))
+        assert np.array_equal(res[0], res[1]) and np.array_equal(res[0], res[2])
+    finally:
+        fnlib.free()
+
+
+def test_model_errors(fnlib, model_file):
+    path, kv, ts = model_file
+    _say("model forward: argument and context checks")
+    fnlib.load(path, "", max_ctx=256)
+    try:
+        with pytest.raises(RuntimeError, match="nt out of range"):
+            fnlib.forward(np.zeros(9, np.int32))
+        with pytest.raises(RuntimeError, match="vocabulary"):
+            fnlib.forward([ms.TINY_DIMS["VOCAB"]])
+        ids = np.zeros(8, np.int32)
+        for _ in range(32):
+            fnlib.forward(ids)
+        assert fnlib.d.fn_n_past() == 256
+        with pytest.raises(RuntimeError, match="context full"):
+            fnlib.forward([1])
+    finally:
+        fnlib.free()
+    assert fnlib.d.fn_n_past() == -1

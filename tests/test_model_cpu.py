@@ -1,0 +1,184 @@
+"""CPU checks of the model loader's file handling and of the model oracle (no GPU).
+
+* The GGUF writer (model_synth) and the library's reader (fn_model_dims: parse + shapes, no device work) agree on
+  every shape of the synthetic model; malformed files fail with a message that names the problem.
+* The whole-model oracle (oracle/model.py) is pinned piece by piece by closed forms: the hyper-connection read with
+  zero up / inject weights, the routing rule on exact ties, the write with unit inject weights, and one layer's
+  MoE against a hand-assembled sum.
+"""
+
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import fn
+import model_synth as ms
+import oracle.model as om
+
+
+@pytest.fixture(scope="module")
+def tiny(tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("gguf") / "tiny.gguf")
+    kv, ts = ms.write_model(path, ms.TINY_DIMS, seed=3)
+    return path, kv, ts
+
+
+def test_reader_reads_the_written_shapes(fnlib, tiny):
+    path, kv, ts = tiny
+    d = fnlib.model_dims(path)
+    T = ms.TINY_DIMS
+    assert (d["D"], d["NL"], d["NH"], d["NKV"], d["NE"], d["NEU"], d["FFE"], d["FFS"]) == \
+        (T["D"], T["NL"], T["NH"], T["NKV"], T["NE"], T["NEU"], T["FFE"], T["FFS"])
+    assert (d["NKH"], d["NVH"], d["HC"], d["HCR"], d["VOCAB"], d["attn_every"]) == \
+        (T["NKH"], T["NVH"], T["HC"], T["HCR"], T["VOCAB"], T["attn_every"])
+    assert (d["HD"], d["DS"], d["NROT"], d["IXH"], d["IXD"], d["top"]) == (256, 128, 64, 4, 128, T["top_k"] // 4)
+    assert d["DINNER"] == T["NVH"] * 128 and d["CONVCH"] == 2 * T["NKH"] * 128 + T["NVH"] * 128
+
+
+def test_reader_alignment_and_version(fnlib, tmp_path):
+    """A GGUF v2 file and one with general.alignment = 64 parse to the same shapes."""
+    kv, ts = ms.model_tensors(ms.TINY_DIMS, seed=1)
+    a, b = str(tmp_path / "a.gguf"), str(tmp_path / "b.gguf")
+    ms.write_gguf(a, kv, ts, alignment=64, version=2)
+    ms.write_gguf(b, kv, ts)
+    assert fnlib.model_dims(a) == fnlib.model_dims(b)
+
+
+def _err(fnlib, path):
+    with pytest.raises(RuntimeError) as e:
+        fnlib.model_dims(path)
+    return str(e.value)
+
+
+def test_reader_rejects_malformed_files(fnlib, tmp_path, tiny):
+    path, kv, ts = tiny
+    raw = open(path, "rb").read()
+    p = str(tmp_path / "x.gguf")
+    open(p, "wb").write(b"GGUX" + raw[4:])
+    assert "bad magic" in _err(fnlib, p)
+    open(p, "wb").write(raw[:4] + struct.pack("<I", 9) + raw[8:])
+    assert "version 9" in _err(fnlib, p)
+    open(p, "wb").write(raw[:200])
+    assert "truncated" in _err(fnlib, p)
+    open(p, "wb").write(raw[: len(raw) - 1000])
+    assert "outside the file" in _err(fnlib, p)
+    assert "cannot open" in _err(fnlib, str(tmp_path / "missing.gguf"))
+
+
+def test_reader_rejects_unbuilt_shapes(fnlib, tmp_path):
+    p = str(tmp_path / "y.gguf")
+    kv, ts = ms.model_tensors(ms.TINY_DIMS, seed=2)
+    k2 = dict(kv)
+    k2["qwen4exp.attention.key_length"] = 128
+    ms.write_gguf(p, k2, ts)
+    assert "head dims" in _err(fnlib, p)
+    k2 = dict(kv)
+    k2["qwen4exp.attention.head_count"] = 6           # 3 query heads per kv head
+    ms.write_gguf(p, k2, ts)
+    assert "4, 8 or 12" in _err(fnlib, p)
+    k2 = dict(kv)
+    k2["qwen4exp.ple.layers"] = [1]
+    ms.write_gguf(p, k2, ts)
+    assert "PLE" in _err(fnlib, p)
+    k2 = dict(kv)
+    del k2["general.architecture"]
+    ms.write_gguf(p, k2, ts)
+    assert "architecture" in _err(fnlib, p)
+
+
+def test_load_before_device_checks_the_file(fnlib, tmp_path):
+    """fn_load reports file problems with the reference's -1 + fn_error() convention (faie2fn.cu:2531-2535)."""
+    d = fnlib.d
+    assert d.fn_load(str(tmp_path / "none.gguf").encode(), b"", 4096, 0) == -1
+    assert b"cannot open" in d.fn_error()
+    with pytest.raises(RuntimeError, match="not loaded"):
+        fnlib.forward([1, 2])
+
+
+# ---- oracle pins ----
+
+
+@pytest.fixture(scope="module")
+def oracle_model(tiny):
+    path, kv, ts = tiny
+    return om.Model(kv, ts, max_ctx=256)
+
+
+def test_hc_read_closed_forms(oracle_model):
+    """With the up weight zero, sigmoid(0) = 1/2 for every stream, so x = mean_s(hn_s) / 2; with the inject rows
+    zero, inj = 2 sigmoid(0) = 1 for every stream (tile_mix, faie2fn.cu:873-888)."""
+    m = oracle_model
+    rng = np.random.default_rng(5)
+    hn = rng.standard_normal((3, m.HC * m.D))
+    name_d, name_u, name_i = "output_hc_down.weight", "blk.0.hc_attn_up.weight", "blk.0.hc_attn_inject.weight"
+    saved = dict(m._w)
+    try:
+        m._w[(name_u,)] = np.zeros((m.HC * m.D, m.HCR))
+        m._w[(name_d, name_i)] = np.concatenate([m.w(name_d), np.zeros((m.HC, m.HC * m.D))])
+        x, inj = m.hc_read(hn, name_d, name_u, name_i)
+    finally:
+        m._w = saved
+    assert np.allclose(x, hn.reshape(3, m.HC, m.D).mean(1) / 2, rtol=1e-14, atol=0)
+    assert np.array_equal(inj, np.ones((3, m.HC)))
+
+
+def test_groupnorm_closed_form(oracle_model):
+    """A stream of constant c normalizes to sign(c) * w / sqrt(1 + eps / c^2)."""
+    m = oracle_model
+    h = np.full((1, m.HC * m.D), 3.0)
+    w = np.arange(m.HC * m.D, dtype=np.float64)
+    out = m.groupnorm(h, w)
+    assert np.allclose(out, w / np.sqrt(1 + m.eps / 9.0), rtol=1e-15)
+
+
+def test_route_ties_and_weights(oracle_model):
+    """Equal logits: the lowest expert indices win (repeated argmax, faie2fn.cu:1749-1751); weights are the
+    renormalized softmax of the chosen ones, so equal logits give equal weights 1 / NEU."""
+    m = oracle_model
+    l = np.zeros((2, m.NE))
+    l[1, 5] = 1.0
+    sel, w = m.route(l)
+    assert list(sel[0]) == list(range(m.NEU)) and np.allclose(w[0], 1.0 / m.NEU)
+    assert sel[1][0] == 5 and list(sel[1][1:]) == [i for i in range(m.NE) if i != 5][: m.NEU - 1]
+    e = np.exp(1.0)
+    assert np.allclose(w[1], np.array([e] + [1.0] * (m.NEU - 1)) / (e + m.NEU - 1))
+
+
+def test_moe_layer_hand_sum(oracle_model):
+    """One token through blk.0's MoE equals the hand-assembled sum over its routed experts plus the gated shared
+    expert, each expert SwiGLU(gate, up) then down (k_tmoe_gu / k_tmoe_down / k_hc_add, faie2fn.cu:1047-1183,
+    1298-1318)."""
+    m = oracle_model
+    p = "blk.0."
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((1, m.D))
+    y, sel = m.ffn(0, x)
+    rl = (x @ m.w(p + "ffn_gate_inp.weight").T)[0]
+    pr = np.exp(rl - rl.max())
+    top = np.argsort(-pr, kind="stable")[: m.NEU]
+    assert list(top) == list(sel[0])
+    want = np.zeros(m.D)
+    for e in top:
+        g = m.w(p + "ffn_gate_exps.weight")[e * m.FFE:(e + 1) * m.FFE] @ x[0]
+        u = m.w(p + "ffn_up_exps.weight")[e * m.FFE:(e + 1) * m.FFE] @ x[0]
+        a = g / (1 + np.exp(-g)) * u
+        want += pr[e] / pr[top].sum() * (m.w(p + "ffn_down_exps.weight")[e * m.D:(e + 1) * m.D] @ a)
+    sg = (x @ m.w(p + "ffn_gate_shexp.weight").T)[0]
+    su = (x @ m.w(p + "ffn_up_shexp.weight").T)[0]
+    sd = m.w(p + "ffn_down_shexp.weight") @ (sg / (1 + np.exp(-sg)) * su)
+    gate = (x @ m.w(p + "ffn_gate_inp_shexp.weight").T)[0, 0]
+    want += sd / (1 + np.exp(-gate))
+    assert np.allclose(y[0], want, rtol=1e-12, atol=1e-12)
+
+
+def test_oracle_forward_runs_and_is_deterministic(oracle_model):
+    m = oracle_model
+    m.reset()
+    l1, a1, h1, _ = m.forward([3, 17, 250])
+    m.reset()
+    l2, a2, h2, _ = m.forward([3, 17, 250])
+    assert np.array_equal(l1, l2) and np.array_equal(a1, a2) and np.isfinite(l1).all()
+    assert h1.shape == (m.NL, 3, m.HC * m.D)
+    m.reset()
