@@ -9,7 +9,8 @@
 namespace fn {
 
 enum : uint32_t {
-    QT_Q8_0 = 8, QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14, QT_IQ4_NL = 20, QT_IQ3_S = 21, QT_IQ4_XS = 23, QT_BF16 = 30,
+    QT_Q8_0 = 8, QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14, QT_IQ2_XXS = 16, QT_IQ2_XS = 17, QT_IQ3_XXS = 18,
+    QT_IQ4_NL = 20, QT_IQ3_S = 21, QT_IQ2_S = 22, QT_IQ4_XS = 23, QT_BF16 = 30, QT_Q2_0 = 42,
 };
 
 // Packed ("plane") layout of a rows x cols weight.  A GGUF row is a run of blocks, each an array of structs

@@ -1,4 +1,5 @@
-// GGUF weight formats and the GEMV of the projections around the decode path, for gfx950.
+// GGUF weight formats and the GEMV of the projections around the decode path, for gfx950: layouts, plans and the
+// dispatch to the per-format instantiations (quant_impl.cuh, quant_t*.hip).
 //
 // The reference decodes its weights with ggml's arithmetic (engine/faie2fn.cu:343-689) and runs them through a
 // tiled, split-K GEMV (faie2fn.cu:690-1042, 2033-2116) whose test hooks are fn_test_dequant / fn_test_gemv
@@ -14,377 +15,14 @@
 //     sum is a 16-lane DPP reduction.  Short rows split K over workgroups whose partials a second pass adds in a
 //     fixed order, so results do not depend on timing.  For formats without an offset the scale multiplies the
 //     16-value dot product instead of each weight.
-#include "quant.h"
-
-#include <algorithm>
+#include "quant_impl.cuh"
 
 namespace fn {
 
+int g_ov_ks = 0, g_ov_lpr = 0, g_ov_kernel = 0, g_ov_wpc = 0;
+int g_persist = 1;  // fn_gemv_waves: 1 = grid of the workgroups resident at once, 0 = one workgroup per row tile
+
 namespace {
-
-constexpr int MAXNT = 8;
-
-// ------------------------------------------------------------------------------------------------------------
-// the IQ4 codebook (the GGUF format's 16 non-uniform levels), and its signed bytes packed four to a word for
-// byte-permute lookups: word k holds entries 4k..4k+3, entry 4k in the low byte
-
-constexpr int kIq4Levels[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
-
-constexpr uint32_t pack4(int k) {
-    return (uint32_t) (uint8_t) kIq4Levels[4 * k] | (uint32_t) (uint8_t) kIq4Levels[4 * k + 1] << 8 |
-           (uint32_t) (uint8_t) kIq4Levels[4 * k + 2] << 16 | (uint32_t) (uint8_t) kIq4Levels[4 * k + 3] << 24;
-}
-constexpr uint32_t KV0 = pack4(0), KV1 = pack4(1), KV2 = pack4(2), KV3 = pack4(3);
-static_assert(KV0 == 0xBFAD9881u && KV3 == 0x71594535u, "IQ4 level packing");
-
-// a constant held in a VGPR the compiler cannot see through: gfx9 VOP3 encodings take no literal, so a VOP3 op
-// such as v_and_or_b32 with two 32-bit constants is only emitted when they sit in registers
-__device__ __forceinline__ uint32_t vconst(uint32_t c) {
-    uint32_t r;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
-    return r;
-}
-
-struct Iq4Tab {
-    uint32_t kv0, kv1, kv2, kv3, m7, m4, sel0;
-    __device__ __forceinline__ Iq4Tab()
-        : kv0(vconst(KV0)), kv1(vconst(KV1)), kv2(vconst(KV2)), kv3(vconst(KV3)), m7(vconst(0x07070707u)),
-          m4(vconst(0x04040404u)), sel0(vconst(0x03020100u)) {}
-};
-
-// four nibble indices -> their four signed levels as bytes.  v_perm_b32 picks bytes out of an 8-byte pair by
-// selector 0..7, so levels 0..7 and 8..15 are looked up separately with the low 3 bits and the index's bit 3 then
-// chooses between the two results byte by byte.  The indices are the nibbles of w at bit offset SH (0: low nibbles,
-// 4: high nibbles): 3 perms, 2 shifts and 2 and-ors per four levels.
-template <int SH> __device__ __forceinline__ uint32_t iq4_levels(uint32_t w, const Iq4Tab &T) {
-    const uint32_t s = (w >> SH) & T.m7;
-    const uint32_t lo = __builtin_amdgcn_perm(T.kv1, T.kv0, s);
-    const uint32_t hi = __builtin_amdgcn_perm(T.kv3, T.kv2, s);
-    const uint32_t sel = ((w >> (SH + 1)) & T.m4) | T.sel0;
-    return __builtin_amdgcn_perm(hi, lo, sel);
-}
-
-// the IQ3_S codebook: 512 grid points of four magnitudes in {1, 3, ..., 15}, one byte each (GGUF's iq3s_grid).  A
-// lane's decode looks up 8 of them per group at data-dependent indices, so the kernels that read IQ3_S copy the
-// table into LDS once per workgroup (tab_fill, before their first barrier) and gather from there.
-__device__ const uint32_t kIq3sGrid[512] = {
-#include "iq3s_grid.inc"
-};
-constexpr int kIq3sLds = 512 * 4;
-
-__device__ __forceinline__ uint32_t *iq3s_lds() {
-    __shared__ uint32_t grid[512];
-    return grid;
-}
-
-struct Iq3Tab {
-    const uint32_t *grid;
-    __device__ __forceinline__ Iq3Tab() : grid(iq3s_lds()) {}
-};
-
-// per-format lookup state held by a decoding lane: the IQ4 levels in registers, or the IQ3_S grid in LDS
-template <uint32_t TY> struct TabOf { using type = Iq4Tab; };
-template <> struct TabOf<QT_IQ3_S> { using type = Iq3Tab; };
-template <uint32_t TY> using TabT = typename TabOf<TY>::type;
-
-// LDS the format's table takes in a GEMV / dequant workgroup, and its fill by the workgroup's nth threads (the
-// caller's next barrier publishes it)
-template <uint32_t TY> constexpr int tab_lds() { return TY == QT_IQ3_S ? kIq3sLds : 0; }
-template <uint32_t TY> __device__ __forceinline__ void tab_fill(int tid, int nth) {
-    if constexpr (TY == QT_IQ3_S) {
-        uint32_t *g = iq3s_lds();
-        for (int i = tid; i < 512; i += nth) g[i] = kIq3sGrid[i];
-    }
-}
-
-__device__ __forceinline__ float sbyte(uint32_t w, int k) { return (float) ((int32_t) (w << (24 - 8 * k)) >> 24); }
-__device__ __forceinline__ float h2f(uint32_t bits) {
-    return (float) __builtin_bit_cast(_Float16, (unsigned short) (bits & 0xFFFFu));
-}
-// byte k (0..11) of the 12 bytes w0 w1 w2
-__device__ __forceinline__ uint32_t byte12(uint32_t w0, uint32_t w1, uint32_t w2, int k) {
-    const uint32_t w = k < 4 ? w0 : (k < 8 ? w1 : w2);
-    return (w >> (8 * (k & 3))) & 0xFFu;
-}
-
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-typedef unsigned int v2u __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ void ld16(const uint8_t *p, uint32_t *w) {
-    const v4u v = *reinterpret_cast<const v4u *>(p);
-    w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
-}
-__device__ __forceinline__ void ld8(const uint8_t *p, uint32_t *w) {
-    const v2u v = *reinterpret_cast<const v2u *>(p);
-    w[0] = v.x, w[1] = v.y;
-}
-__device__ __forceinline__ uint32_t ld2(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
-
-// planes of a packed weight as the kernels see them
-struct PP {
-    const uint8_t *p0, *p1, *p2;
-    size_t rs0, rs1, rs2;
-};
-
-// the three planes of one row
-struct RP {
-    const uint8_t *b0, *b1, *b2;
-};
-__device__ __forceinline__ RP row_planes(const PP &P, int row) {
-    return RP{P.p0 + (size_t) row * P.rs0, P.p1 + (size_t) row * P.rs1, P.p2 + (size_t) row * P.rs2};
-}
-
-// one decoded group: GGUF value j = fl(s[j / 16] * q[j] - m[j / 16])
-struct Grp {
-    float q[32];
-    float s[2], m[2];
-};
-
-template <uint32_t TY> struct Q;
-
-// groups a GEMV lane keeps in flight per batch for a format of nw raw words per group (two batches live at once)
-constexpr int prefetch_groups(int nw) { return nw <= 8 ? 4 : (nw <= 12 ? 2 : 1); }
-
-// BF16: a group is 32 consecutive values (64 bytes); q holds the values themselves, s = 1
-template <> struct Q<QT_BF16> {
-    static constexpr int NW = 16;
-    static constexpr int U = prefetch_groups(NW);
-    static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
-        const uint8_t *p = R.b0 + 64 * g;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ld16(p + 16 * i, w + 4 * i);
-    }
-    __device__ static void unpack(const uint32_t *w, int, Grp &o, const Iq4Tab &T) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            o.q[2 * i] = __uint_as_float(w[i] << 16);
-            o.q[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-        }
-        o.s[0] = o.s[1] = 1.0f;
-        o.m[0] = o.m[1] = 0.0f;
-    }
-};
-
-// Q8_0: 32 int8 quants, one fp16 scale (ggml: y = d * q)
-template <> struct Q<QT_Q8_0> {
-    static constexpr int NW = 9;
-    static constexpr int U = prefetch_groups(NW);
-    static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
-        const uint8_t *q = R.b0 + 32 * g;
-        ld16(q, w);
-        ld16(q + 16, w + 4);
-        w[8] = ld2(R.b1 + 2 * g);
-    }
-    __device__ static void unpack(const uint32_t *w, int, Grp &o, const Iq4Tab &T) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) o.q[4 * i + k] = sbyte(w[i], k);
-        o.s[0] = o.s[1] = h2f(w[8]);
-        o.m[0] = o.m[1] = 0.0f;
-    }
-};
-
-// IQ4_NL: 16 bytes of nibble indices (byte b: low nibble = value b, high nibble = value b + 16), fp16 scale
-// (ggml: y = d * level)
-template <> struct Q<QT_IQ4_NL> {
-    static constexpr int NW = 5;
-    static constexpr int U = prefetch_groups(NW);
-    static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
-        ld16(R.b0 + 16 * g, w);
-        w[4] = ld2(R.b1 + 2 * g);
-    }
-    __device__ static void levels(const uint32_t *w, Grp &o, const Iq4Tab &T) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = iq4_levels<0>(w[i], T), hi = iq4_levels<4>(w[i], T);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                o.q[4 * i + k] = sbyte(lo, k);
-                o.q[16 + 4 * i + k] = sbyte(hi, k);
-            }
-        }
-    }
-    __device__ static void unpack(const uint32_t *w, int, Grp &o, const Iq4Tab &T) {
-        levels(w, o, T);
-        o.s[0] = o.s[1] = h2f(w[4]);
-        o.m[0] = o.m[1] = 0.0f;
-    }
-};
-
-// IQ4_XS: super-blocks of 256 (d fp16, scales_h u16, scales_l[4], qs[128]); group ib has a 6-bit scale ls and
-// the IQ4_NL nibble layout (ggml: dl = d * (ls - 32), y = dl * level)
-template <> struct Q<QT_IQ4_XS> {
-    static constexpr int NW = 6;
-    static constexpr int U = prefetch_groups(NW);
-    static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
-        ld16(R.b0 + 16 * g, w);  // super-block g / 8 at 128 (g / 8), group g % 8 at 16 (g % 8) inside it
-        ld8(R.b1 + 8 * (g >> 3), w + 4);
-    }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
-        const int ib = g & 7;
-        Q<QT_IQ4_NL>::levels(w, o, T);
-        const uint32_t sl = (w[5] >> (8 * (ib >> 1))) >> (4 * (ib & 1)) & 0xFu;
-        const uint32_t sh = (w[4] >> (16 + 2 * ib)) & 3u;
-        const float dl = h2f(w[4]) * (float) ((int) (sl | sh << 4) - 32);
-        o.s[0] = o.s[1] = dl;
-        o.m[0] = o.m[1] = 0.0f;
-    }
-};
-
-// 6-bit scale and min of group ib from the 12 packed scale bytes of Q4_K / Q5_K (ggml get_scale_min_k4)
-__device__ __forceinline__ void scale_min_k(const uint32_t *h, int ib, float &sc, float &mn) {
-    const uint32_t b_ib = byte12(h[0], h[1], h[2], ib), b_4 = byte12(h[0], h[1], h[2], ib + 4);
-    if (ib < 4) {
-        sc = (float) (b_ib & 63u);
-        mn = (float) (b_4 & 63u);
-    } else {
-        const uint32_t b_m4 = byte12(h[0], h[1], h[2], ib - 4);
-        sc = (float) ((b_4 & 0xFu) | (b_m4 >> 6) << 4);
-        mn = (float) ((b_4 >> 4) | (b_ib >> 6) << 4);
-    }
-}
-
-// Q4_K: super-blocks of 256 (d, dmin fp16, 12 scale bytes, qs[128]); group ib reads the low (even ib) or high
-// (odd ib) nibbles of qs[32 (ib/2) .. +31] (ggml: y = d*sc * q - dmin*m)
-template <> struct Q<QT_Q4_K> {
-    static constexpr int NW = 12;
-    static constexpr int U = prefetch_groups(NW);
-    static constexpr bool MIN = true;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
-        const uint8_t *q = R.b0 + 16 * (g & ~1);  // the 32 bytes of groups 2k and 2k + 1
-        ld16(q, w);
-        ld16(q + 16, w + 4);
-        ld16(R.b1 + 16 * (g >> 3), w + 8);
-    }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
-        const int ib = g & 7, sh = 4 * (ib & 1);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) o.q[4 * i + k] = (float) ((w[i] >> (8 * k + sh)) & 0xFu);
-        float sc, mn;
-        scale_min_k(w + 9, ib, sc, mn);
-        o.s[0] = o.s[1] = h2f(w[8]) * sc;
-        o.m[0] = o.m[1] = h2f(w[8] >> 16) * mn;
-    }
-};
-
-// Q5_K: Q4_K plus a fifth bit per value: bit ib of qh[j] (ggml: q = nibble + 16 * bit)
-template <> struct Q<QT_Q5_K> {
-    static constexpr int NW = 20;
-    static constexpr int U = prefetch_groups(NW);
-    static constexpr bool MIN = true;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
-        const uint8_t *q = R.b0 + 16 * (g & ~1);
-        ld16(q, w);
-        ld16(q + 16, w + 4);
-        const uint8_t *h = R.b1 + 32 * (g >> 3);
-        ld16(h, w + 8);
-        ld16(h + 16, w + 12);
-        ld16(R.b2 + 16 * (g >> 3), w + 16);
-    }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
-        const int ib = g & 7, sh = 4 * (ib & 1);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                o.q[4 * i + k] = (float) (((w[i] >> (8 * k + sh)) & 0xFu) | ((w[8 + i] >> (8 * k + ib)) & 1u) << 4);
-        float sc, mn;
-        scale_min_k(w + 17, ib, sc, mn);
-        o.s[0] = o.s[1] = h2f(w[16]) * sc;
-        o.m[0] = o.m[1] = h2f(w[16] >> 16) * mn;
-    }
-};
-
-// Q6_K: super-blocks of 256 (ql[128], qh[64], int8 scales[16], d fp16).  Value 128 n + 32 qu + l (n < 2, qu < 4,
-// l < 32): low 4 bits from nibble (qu >> 1) of ql[64 n + 32 (qu & 1) + l], high 2 bits from bits 2 qu of
-// qh[32 n + l], scale scales[8 n + 2 qu + l / 16] (ggml: y = d * sc * (q - 32))
-template <> struct Q<QT_Q6_K> {
-    static constexpr int NW = 18;
-    static constexpr int U = prefetch_groups(NW);
-    static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
-        const int ib = g & 7, n = ib >> 2, qu = ib & 3, sb = g >> 3;
-        const uint8_t *l = R.b0 + 128 * sb + 64 * n + 32 * (qu & 1);
-        ld16(l, w);
-        ld16(l + 16, w + 4);
-        const uint8_t *h = R.b1 + 64 * sb + 32 * n;
-        ld16(h, w + 8);
-        ld16(h + 16, w + 12);
-        const uint8_t *t = R.b2 + 18 * sb;
-        w[16] = ld2(t + 8 * n + 2 * qu);
-        w[17] = ld2(t + 16);
-    }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
-        const int qu = g & 3, lsh = 4 * (qu >> 1), hsh = 2 * qu;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                o.q[4 * i + k] =
-                    (float) ((int) (((w[i] >> (8 * k + lsh)) & 0xFu) | ((w[8 + i] >> (8 * k + hsh)) & 3u) << 4) - 32);
-        const float d = h2f(w[17]);
-        o.s[0] = d * sbyte(w[16], 0);
-        o.s[1] = d * sbyte(w[16], 1);
-        o.m[0] = o.m[1] = 0.0f;
-    }
-};
-
-// IQ3_S: super-blocks of 256 (d fp16, qs[64], qh[8], signs[32], scales[4]); packed as plane 0 = qs, plane 1 = qh,
-// signs and scales (44 bytes), plane 2 = d.  Group ib: db = d * (1 + 2 * (4-bit scale ib)); its 32 values are 8 grid
-// points of 4 magnitudes, point 2l (2l + 1) at index qs[8 ib + 2l (+1)] | bit 2l (2l + 1) of qh[ib] << 8, value
-// 8l + j negated by bit j of signs[4 ib + l] (ggml: y = db * grid[j] * sign)
-template <> struct Q<QT_IQ3_S> {
-    static constexpr int NW = 6;
-    static constexpr int U = prefetch_groups(NW);
-    static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
-        const int ib = g & 7;
-        ld8(R.b0 + 8 * g, w);                                 // qs of the group
-        const uint8_t *h = R.b1 + 44 * (g >> 3);
-        w[2] = *reinterpret_cast<const uint32_t *>(h + (ib & 4));   // the qh word holding byte ib
-        w[3] = *reinterpret_cast<const uint32_t *>(h + 8 + 4 * ib); // 32 sign bits
-        w[4] = *reinterpret_cast<const uint32_t *>(h + 40);         // the 4 scale bytes
-        w[5] = ld2(R.b2 + 2 * (g >> 3));
-    }
-    // magnitude m with the sign bit sg (0 or 1) of the value: the float's sign bit, exact
-    __device__ static float smag(uint32_t m, uint32_t sg) { return __uint_as_float(__float_as_uint((float) m) | sg << 31); }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq3Tab &T) {
-        const int ib = g & 7;
-        const uint32_t qh = (w[2] >> (8 * (ib & 3))) & 0xFFu;
-        const uint32_t sc = (w[4] >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xFu;
-#pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            const uint32_t qq = l < 2 ? w[0] : w[1];
-            const int s = 16 * (l & 1);
-            const uint32_t g1 = T.grid[((qq >> s) & 255u) | ((qh << (8 - 2 * l)) & 256u)];
-            const uint32_t g2 = T.grid[((qq >> (s + 8)) & 255u) | ((qh << (7 - 2 * l)) & 256u)];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                o.q[8 * l + j] = smag((g1 >> (8 * j)) & 255u, (w[3] >> (8 * l + j)) & 1u);
-                o.q[8 * l + 4 + j] = smag((g2 >> (8 * j)) & 255u, (w[3] >> (8 * l + 4 + j)) & 1u);
-            }
-        }
-        o.s[0] = o.s[1] = h2f(w[5]) * (float) (1 + 2 * (int) sc);
-        o.m[0] = o.m[1] = 0.0f;
-    }
-};
-
-template <uint32_t TY> __device__ __forceinline__ void decode(const PP &P, int row, int g, Grp &o) {
-    uint32_t w[Q<TY>::NW];
-    const TabT<TY> T;
-    Q<TY>::load(row_planes(P, row), g, w);
-    Q<TY>::unpack(w, g, o, T);
-}
-
-// ------------------------------------------------------------------------------------------------------------
-// kernels
 
 // GGUF rows -> planes: one thread per (row, block), plain byte copies (load-time work)
 __global__ void k_pack(QLayout L, const uint8_t *__restrict__ raw, uint8_t *__restrict__ out) {
@@ -399,339 +37,6 @@ __global__ void k_pack(QLayout L, const uint8_t *__restrict__ raw, uint8_t *__re
     }
 }
 
-// planes -> float rows, one thread per (row, group of 32), the GGUF value fl(s * q - m) rounded once
-template <uint32_t TY> __global__ void k_dequant(PP P, int rows, int G, int cols, float *__restrict__ out) {
-    if constexpr (tab_lds<TY>() > 0) {
-        tab_fill<TY>(threadIdx.x, blockDim.x);
-        __syncthreads();
-    }
-    const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t) rows * G) return;
-    const int row = (int) (i / G), g = (int) (i % G);
-    Grp o;
-    decode<TY>(P, row, g, o);
-    float4 *dst = reinterpret_cast<float4 *>(out + (size_t) row * cols + (size_t) g * 32);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const int h = c >> 2;
-        float v[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float q = o.q[4 * c + k];
-            v[k] = TY == QT_BF16 ? q : __builtin_fmaf(o.s[h], q, -o.m[h]);
-        }
-        dst[c] = make_float4(v[0], v[1], v[2], v[3]);
-    }
-}
-
-// sum over the LPR lanes of a row (16: one DPP row, 32: half a wave, 64: the wave); every lane of the row gets it
-template <int LPR> __device__ __forceinline__ float lane_row_sum(float v) {
-    if constexpr (LPR == 16) return row_sum(v);
-    else if constexpr (LPR == 32) return half_sum(v);
-    else return wave_sum(v);
-}
-
-// one group's contribution to the NT accumulators; xg points at the group's x in LDS: float4 c of token t at
-// xg[t * 8 + c] (offsets known at compile time).  The arithmetic (and its order) does not depend on NT: token t of
-// an NT-token call gets the bits a one-token call gets.
-template <uint32_t TY, int NT>
-__device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float4 *xg, float *acc,
-                                           const TabT<TY> &T) {
-    Grp o;
-    Q<TY>::unpack(w, g, o, T);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        if constexpr (Q<TY>::MIN) {
-            float wv[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) wv[j] = __builtin_fmaf(o.s[h], o.q[16 * h + j], -o.m[h]);
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                float a = acc[t];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const float4 xv = xg[t * 8 + 4 * h + c];
-                    a = __builtin_fmaf(wv[4 * c], xv.x, a);
-                    a = __builtin_fmaf(wv[4 * c + 1], xv.y, a);
-                    a = __builtin_fmaf(wv[4 * c + 2], xv.z, a);
-                    a = __builtin_fmaf(wv[4 * c + 3], xv.w, a);
-                }
-                acc[t] = a;
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                float d0 = 0.0f, d1 = 0.0f;
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const float4 xv = xg[t * 8 + 4 * h + c];
-                    d0 = __builtin_fmaf(o.q[16 * h + 4 * c], xv.x, d0);
-                    d1 = __builtin_fmaf(o.q[16 * h + 4 * c + 1], xv.y, d1);
-                    d0 = __builtin_fmaf(o.q[16 * h + 4 * c + 2], xv.z, d0);
-                    d1 = __builtin_fmaf(o.q[16 * h + 4 * c + 3], xv.w, d1);
-                }
-                acc[t] = __builtin_fmaf(o.s[h], d0 + d1, acc[t]);
-            }
-        }
-    }
-}
-
-// x of tokens [0, NT) and groups [c0, c0 + nch) -> LDS, group-major: float4 c of token t of group c0 + gr at
-// xs[gr * xs_stride(NT) + t * 8 + c].  The stride is odd (in float4), so the lanes of a row, which read consecutive
-// groups, hit distinct bank quads, and every read's offset inside a group is an immediate.  One pass moves XB float4
-// per thread; its loads are clamped to the last element, so the pass's array stays in registers.
-constexpr int xs_stride(int nt) { return nt * 8 + 1; }
-
-template <int NT, int XB> struct XPass {
-    float4 r[XB];
-    __device__ __forceinline__ void load(const float *__restrict__ x, int cols, int c0, int nch, int e0, int tid,
-                                         int nth) {
-        const int nx = NT * 8 * nch;
-#pragma unroll
-        for (int k = 0; k < XB; ++k) {
-            const int e = min(e0 + tid + nth * k, nx - 1), tg = e >> 3, t = tg / nch, gr = tg - t * nch;
-            r[k] = *reinterpret_cast<const float4 *>(x + (size_t) t * cols + (size_t) (c0 + gr) * 32 + 4 * (e & 7));
-        }
-    }
-    __device__ __forceinline__ void store(float4 *xs, int nch, int e0, int tid, int nth) const {
-        const int nx = NT * 8 * nch;
-#pragma unroll
-        for (int k = 0; k < XB; ++k) {
-            const int e = e0 + tid + nth * k;
-            if (e < nx) {
-                const int tg = e >> 3, t = tg / nch, gr = tg - t * nch;
-                xs[gr * xs_stride(NT) + t * 8 + (e & 7)] = r[k];
-            }
-        }
-    }
-};
-
-// batch j of row-set s over the groups [c0, c1): groups c0 + li + LPR (U j + u), u < U, of row s RPW + lane / LPR.
-// Row and group are clamped into the weight: a lane past the last row or group loads a valid address whose value
-// it never uses.
-template <uint32_t TY, int LPR>
-__device__ __forceinline__ void load_batch(const PP &P, int rows, int s, int j, int lane, int c0, int c1,
-                                           uint32_t (&w)[Q<TY>::U][Q<TY>::NW]) {
-    constexpr int U = Q<TY>::U;
-    const RP R = row_planes(P, min(s * (64 / LPR) + lane / LPR, rows - 1));
-    const int gb = c0 + lane % LPR + LPR * U * j;
-#pragma unroll
-    for (int u = 0; u < U; ++u) Q<TY>::load(R, min(gb + LPR * u, c1 - 1), w[u]);
-}
-
-template <uint32_t TY, int NT, int LPR>
-__device__ __forceinline__ void acc_batch(const uint32_t (&w)[Q<TY>::U][Q<TY>::NW], int j, int lane, int c0, int c1,
-                                          const float4 *xs, float *acc, const TabT<TY> &T) {
-    constexpr int U = Q<TY>::U;
-    const int gb = c0 + lane % LPR + LPR * U * j;
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-        if (gb + LPR * u < c1)
-            accumulate<TY, NT>(w[u], gb + LPR * u, xs + (gb + LPR * u - c0) * xs_stride(NT), acc, T);
-}
-
-// end of a row-set: the row sums (every lane of a row gets them) stored by the row's first lane; accumulators reset
-template <int NT, int LPR>
-__device__ __forceinline__ void flush_rows(int s, int lane, int rows, float *acc, float *__restrict__ out) {
-    const int row = s * (64 / LPR) + lane / LPR;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = lane_row_sum<LPR>(acc[t]);
-    if (lane % LPR == 0 && row < rows) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) out[(size_t) t * rows + row] = acc[t];
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
-}
-
-// GEMV of one split (blockIdx.y) of the groups: [g0, g1), g0 = blockIdx.y * gps.  A wave works on row-sets of
-// 64 / LPR rows, LPR lanes per row; lane li of a row sums its groups li, li + LPR, ... in ascending order into one
-// accumulator per token, then the row's LPR lanes are summed.  That arithmetic is the same in both kernels below,
-// for every launch shape and token count, so token t of an nt-token call gets the bits of a one-token call on x[t].
-//
-// k_gemv, for a split whose x fits the LDS: the workgroup stages x once, then each wave walks its own row-sets
-// s = global wave id, + waves in the grid, ..., in batches of U groups per lane, with the next batch's loads (the
-// next row-set's, at the end of one) in flight while it sums the current one.  The host sizes the grid to the
-// workgroups resident at once, so no workgroup waits for another to finish.  Two walks, picked by the host from the
-// batches per wave (same bits):
-
-// short walk (a wave has a few batches): a batch is loaded only when the wave has it.  The compiler's wait counts
-// then merge the paths with and without the load and wait as if nothing newer were in flight, which costs nothing
-// at this depth and saves the surplus loads of the deep walk
-template <uint32_t TY, int NT, int LPR>
-__device__ __forceinline__ void gemv_walk_short(const PP &P, int rows, int g0, int g1, int ng, int NS, int nws,
-                                                int NB, const float *__restrict__ x, int cols,
-                                                float *__restrict__ out, float4 *xs) {
-    constexpr int NW = Q<TY>::NW, U = Q<TY>::U, XB = NT <= 2 ? 4 : 8;
-    const int tid = threadIdx.x, lane = tid & 63;
-    // the wave's batches in order: (s, j), then (s1, j1) = next(s, j), ...; wave-uniform, so the row reductions run
-    // on whole waves
-    int s = blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(tid >> 6), j = 0, s1, j1;
-    const auto next = [NB, nws](int s_, int j_, int &sn, int &jn) {
-        sn = j_ + 1 == NB ? s_ + nws : s_;
-        jn = j_ + 1 == NB ? 0 : j_ + 1;
-    };
-    next(s, j, s1, j1);
-    uint32_t wa[U][NW], wb[U][NW];
-    // x [NT][cols] -> xs (the layout of XPass).  The first part of x is requested before the first two weight
-    // batches, so that its LDS writes wait for x alone.
-    const int nx = NT * 8 * ng;
-    for (int e0 = 0; e0 < nx; e0 += 512 * XB) {
-        float4 xr[XB];  // loads clamped to the last element (unconditional: the array stays in registers)
-#pragma unroll
-        for (int k = 0; k < XB; ++k) {
-            const int e = min(e0 + tid + 512 * k, nx - 1), tg = e >> 3, t = tg / ng, gr = tg - t * ng;
-            xr[k] = *reinterpret_cast<const float4 *>(x + (size_t) t * cols + (size_t) (g0 + gr) * 32 + 4 * (e & 7));
-        }
-        if (e0 == 0) {
-            if (s < NS) load_batch<TY, LPR>(P, rows, s, j, lane, g0, g1, wa);
-            if (s1 < NS) load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wb);
-        }
-#pragma unroll
-        for (int k = 0; k < XB; ++k) {
-            const int e = e0 + tid + 512 * k;
-            if (e < nx) {
-                const int tg = e >> 3, t = tg / ng, gr = tg - t * ng;
-                xs[gr * xs_stride(NT) + t * 8 + (e & 7)] = xr[k];
-            }
-        }
-    }
-    __syncthreads();
-    const TabT<TY> T;  // (IQ4 formats) the level table in registers, once; (IQ3_S) the grid in LDS
-    float acc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
-    // two batches in flight: while one is summed, the other (and then the one after it) is loading
-    while (s < NS) {
-        acc_batch<TY, NT, LPR>(wa, j, lane, g0, g1, xs, acc, T);
-        if (j == NB - 1) flush_rows<NT, LPR>(s, lane, rows, acc, out);
-        s = s1;
-        j = j1;
-        next(s, j, s1, j1);
-        if (s >= NS) break;
-        if (s1 < NS) load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wa);
-        acc_batch<TY, NT, LPR>(wb, j, lane, g0, g1, xs, acc, T);
-        if (j == NB - 1) flush_rows<NT, LPR>(s, lane, rows, acc, out);
-        s = s1;
-        j = j1;
-        next(s, j, s1, j1);
-        if (s >= NS) break;
-        if (s1 < NS) load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wb);
-    }
-}
-
-// deep walk (many batches per wave): a steady-state pipeline whose wait counts stay exact
-template <uint32_t TY, int NT, int LPR>
-__device__ __forceinline__ void gemv_walk_deep(const PP &P, int rows, int g0, int g1, int ng, int NS, int nws, int NB,
-                                               const float *__restrict__ x, int cols, float *__restrict__ out,
-                                               float4 *xs) {
-    constexpr int NW = Q<TY>::NW, U = Q<TY>::U, XB = NT <= 2 ? 4 : 8;
-    const int tid = threadIdx.x, lane = tid & 63;
-    // The wave's batches: b = 0 .. n-1, batch b = groups batch b % NB of row-set w0 + (b / NB) * nws.  Everything
-    // here is wave-uniform; readfirstlane makes that visible to the compiler, so the loops branch on scalars.
-    const int w0 = blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n = w0 < NS ? ((NS - 1 - w0) / nws + 1) * NB : 0;
-    uint32_t wa[U][NW], wb[U][NW];
-    const TabT<TY> T;  // (IQ4 formats) the level table in registers, once; (IQ3_S) the grid in LDS
-    float acc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
-    // x [NT][cols] -> xs (the layout of XPass).  The first part of x is requested before the wave's first one or two
-    // weight batches, so that its LDS writes wait for x alone.  A wave with one batch or none takes a short path
-    // with no prefetch; every wave passes the one barrier either way.
-    XPass<NT, XB> xp;
-    for (int e0 = 0; e0 < NT * 8 * ng; e0 += 512 * XB) {
-        xp.load(x, cols, g0, ng, e0, tid, 512);
-        if (e0 == 0) {
-            const int b1 = n > 1 ? 1 : 0;
-            load_batch<TY, LPR>(P, rows, w0, 0, lane, g0, g1, wa);
-            load_batch<TY, LPR>(P, rows, w0 + (b1 / NB) * nws, b1 % NB, lane, g0, g1, wb);
-        }
-        xp.store(xs, ng, e0, tid, 512);
-    }
-    __syncthreads();
-#define FN_GEMV_LOAD(W, B) load_batch<TY, LPR>(P, rows, w0 + ((B) / NB) * nws, (B) % NB, lane, g0, g1, W)
-#define FN_GEMV_SUM(W, B)                                                                      \
-    do {                                                                                       \
-        acc_batch<TY, NT, LPR>(W, (B) % NB, lane, g0, g1, xs, acc, T);                         \
-        if ((B) % NB == NB - 1) flush_rows<NT, LPR>(w0 + ((B) / NB) * nws, lane, rows, acc, out); \
-    } while (0)
-    // Steady state: two batches in flight while one is summed.  Every pass issues the same loads and the loop leaves
-    // only at its test, so the compiler's wait counts stay exact (a path that skips a load makes them assume nothing
-    // newer is in flight, and each wait would then drain the prefetched batch too).  The last two or three batches
-    // go after the loop.
-    int b = 0;
-    for (; b + 3 < n; b += 2) {
-        FN_GEMV_SUM(wa, b);
-        FN_GEMV_LOAD(wa, b + 2);
-        FN_GEMV_SUM(wb, b + 1);
-        FN_GEMV_LOAD(wb, b + 3);
-    }
-    if (b < n) FN_GEMV_SUM(wa, b);
-    if (b + 2 < n) FN_GEMV_LOAD(wa, b + 2);
-    if (b + 1 < n) FN_GEMV_SUM(wb, b + 1);
-    if (b + 2 < n) FN_GEMV_SUM(wa, b + 2);
-#undef FN_GEMV_SUM
-#undef FN_GEMV_LOAD
-}
-
-template <uint32_t TY, int NT, int LPR, bool DEEP>
-__global__ void __launch_bounds__(512) k_gemv(PP P, int rows, int G, int gps, const float *__restrict__ x, int cols,
-                                                float *__restrict__ out) {
-    extern __shared__ float4 xs[];
-    constexpr int U = Q<TY>::U, RPW = 64 / LPR;
-    const int g0 = blockIdx.y * gps, g1 = min(G, g0 + gps), ng = g1 - g0;
-    if (ng <= 0) return;  // (the plan gives every split a group; whole workgroup, before any barrier)
-    const int NS = (rows + RPW - 1) / RPW, nws = gridDim.x * 8;
-    const int NB = (ng + LPR * U - 1) / (LPR * U);
-    out += (size_t) blockIdx.y * NT * rows;
-    tab_fill<TY>(threadIdx.x, 512);  // published by the walk's barrier after the x staging
-    if constexpr (DEEP) gemv_walk_deep<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs);
-    else gemv_walk_short<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs);
-}
-
-// k_gemv_c, for an x too large for the LDS: x goes through it in chunks of kc groups (a multiple of LPR, so a
-// group's lane does not depend on the chunking); the workgroup's 8 waves take one row-set each and walk the chunks
-// together.  Grid: one workgroup per 8 row-sets.
-template <uint32_t TY, int NT, int LPR>
-__global__ void __launch_bounds__(512) k_gemv_c(PP P, int rows, int G, int gps, int kc, const float *__restrict__ x,
-                                                  int cols, float *__restrict__ out) {
-    extern __shared__ float4 xs[];
-    constexpr int NW = Q<TY>::NW, U = Q<TY>::U, RPW = 64 / LPR, XB = NT <= 2 ? 4 : 8;
-    const int g0 = blockIdx.y * gps, g1 = min(G, g0 + gps);
-    if (g1 <= g0) return;  // (the plan gives every split a group; whole workgroup, before any barrier)
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int s = blockIdx.x * 8 + (tid >> 6);
-    const bool live = s < (rows + RPW - 1) / RPW;  // wave-uniform
-    out += (size_t) blockIdx.y * NT * rows;
-    tab_fill<TY>(tid, 512);  // published by the chunk loop's first barrier
-    const TabT<TY> T;
-    float acc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
-    uint32_t wa[U][NW], wb[U][NW];
-    XPass<NT, XB> xp;
-    for (int c0 = g0; c0 < g1; c0 += kc) {
-        const int c1 = min(g1, c0 + kc), nch = c1 - c0, NB = (nch + LPR * U - 1) / (LPR * U);
-        __syncthreads();  // every wave is done reading the previous chunk
-        for (int e0 = 0; e0 < NT * 8 * nch; e0 += 512 * XB) {
-            xp.load(x, cols, c0, nch, e0, tid, 512);
-            if (e0 == 0 && live) load_batch<TY, LPR>(P, rows, s, 0, lane, c0, c1, wa);
-            xp.store(xs, nch, e0, tid, 512);
-        }
-        __syncthreads();
-        if (!live) continue;
-        for (int j = 0; j < NB; j += 2) {
-            if (j + 1 < NB) load_batch<TY, LPR>(P, rows, s, j + 1, lane, c0, c1, wb);
-            acc_batch<TY, NT, LPR>(wa, j, lane, c0, c1, xs, acc, T);
-            if (j + 1 >= NB) break;
-            if (j + 2 < NB) load_batch<TY, LPR>(P, rows, s, j + 2, lane, c0, c1, wa);
-            acc_batch<TY, NT, LPR>(wb, j + 1, lane, c0, c1, xs, acc, T);
-        }
-    }
-    if (live) flush_rows<NT, LPR>(s, lane, rows, acc, out);
-}
-
 // y[i] = sum over splits s = 0..ks-1 of part[s][i], in that order
 __global__ void k_gemv_reduce(const float *__restrict__ part, int ks, int n, float *__restrict__ y) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -741,148 +46,19 @@ __global__ void k_gemv_reduce(const float *__restrict__ part, int ks, int n, flo
     y[i] = s;
 }
 
-int g_ov_ks = 0, g_ov_lpr = 0, g_ov_kernel = 0, g_ov_wpc = 0;
-int g_persist = 1;  // fn_gemv_waves: 1 = grid of the workgroups resident at once, 0 = one workgroup per row tile
-constexpr int kLdsPerCu = 160 * 1024;  // LDS of a CDNA4 CU (the most one workgroup can take)
-
-
-PP planes(const QLayout &L, const uint8_t *packed) {
-    PP P{packed + L.off[0], packed + L.off[1], packed + L.off[2], L.rs[0], L.rs[1], L.rs[2]};
-    return P;
+const QOps *ops(uint32_t type) {
+    for (auto f : {qops_group1, qops_group2, qops_group3, qops_group4, qops_group5})
+        if (const void *o = f(type)) return static_cast<const QOps *>(o);
+    return nullptr;
 }
 
-// One GEMV launch.  x of the split in the LDS at once when it fits the CU's 160 KB: k_gemv on a grid of the
-// workgroups resident at once.  Else k_gemv_c with chunks of the largest multiple of LPR groups whose x fits 80 KB
-// (two workgroups per CU), evened out.
-template <uint32_t TY, int NT, int LPR>
-int gemv_nt(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, float *out, hipStream_t st) {
-    const int gps = (pl.ngroups + pl.ks - 1) / pl.ks, ns = (L.rows + 64 / LPR - 1) / (64 / LPR);
-    int nwg = (ns + 7) / 8;
-    constexpr int XS = xs_stride(NT) * (int) sizeof(float4);  // LDS bytes per group of x
-    constexpr int LDS = kLdsPerCu - tab_lds<TY>();            // what x may take beside the format's table
-    if (gps <= LDS / XS && g_ov_kernel != 1) {
-        static int by_regs = 0;  // workgroups per CU the registers allow (the deep walk's, the larger of the two)
-        if (!by_regs) {
-            int n = 0;
-            FN_CK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv<TY, NT, LPR, true>, 512, 0));
-            by_regs = std::max(1, n);
-        }
-        const size_t lds = (size_t) gps * XS;
-        int per_cu = std::min(by_regs, std::max(1, (int) (kLdsPerCu / (lds + tab_lds<TY>()))));
-        if (g_ov_wpc) per_cu = std::max(1, g_ov_wpc / 8);
-        if (g_persist) nwg = std::min(nwg, device_cus() * per_cu);
-        // batches of the busiest wave; from 4 on the deep walk's exact waits pay for its surplus loads (measured)
-        const int nb = (gps + LPR * Q<TY>::U - 1) / (LPR * Q<TY>::U), per_wave = (ns + 8 * nwg - 1) / (8 * nwg) * nb;
-        const bool deep = g_ov_kernel == 3 || (g_ov_kernel != 4 && per_wave >= 4);
-        const auto kern = deep ? k_gemv<TY, NT, LPR, true> : k_gemv<TY, NT, LPR, false>;
-        hipLaunchKernelGGL(kern, dim3((unsigned) nwg, (unsigned) pl.ks), dim3(512), lds, st, P, L.rows, pl.ngroups,
-                           gps, x, L.cols, out);
-    } else {
-        int kc = g_ov_kernel == 1 ? LPR : std::max(LPR, (kLdsPerCu / 2 - tab_lds<TY>()) / XS / LPR * LPR);
-        const int nch = (gps + kc - 1) / kc;
-        kc = std::min(kc, ((gps + nch - 1) / nch + LPR - 1) / LPR * LPR);
-        const size_t lds = (size_t) kc * XS;
-        hipLaunchKernelGGL((k_gemv_c<TY, NT, LPR>), dim3((unsigned) nwg, (unsigned) pl.ks), dim3(512), lds, st, P,
-                           L.rows, pl.ngroups, gps, kc, x, L.cols, out);
-    }
-    FN_CK(hipGetLastError());
+int rows_check(const QLayout &L, int R, int npairs, int xdiv, const float *x, const float *out) {
+    if (R < 1 || L.rows % R || npairs < 1 || npairs > 65535 || xdiv < 1) FN_FAIL("rows: bad shape");
+    if (!x || !out) FN_FAIL("rows: null pointer");
+    if (((uintptr_t) x | (uintptr_t) out) % 16) FN_FAIL("rows: x and out must be 16-byte aligned");
     return 0;
 }
 
-template <uint32_t TY, int LPR>
-int gemv_tl(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, int nt, float *out, hipStream_t st) {
-    switch (nt) {
-        case 1: return gemv_nt<TY, 1, LPR>(L, pl, P, x, out, st);
-        case 2: return gemv_nt<TY, 2, LPR>(L, pl, P, x, out, st);
-        case 3: return gemv_nt<TY, 3, LPR>(L, pl, P, x, out, st);
-        case 4: return gemv_nt<TY, 4, LPR>(L, pl, P, x, out, st);
-        case 5: return gemv_nt<TY, 5, LPR>(L, pl, P, x, out, st);
-        case 6: return gemv_nt<TY, 6, LPR>(L, pl, P, x, out, st);
-        case 7: return gemv_nt<TY, 7, LPR>(L, pl, P, x, out, st);
-        case 8: return gemv_nt<TY, 8, LPR>(L, pl, P, x, out, st);
-        default: FN_FAIL("gemv: nt must be 1..8");
-    }
-}
-
-template <uint32_t TY>
-int gemv_t(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, int nt, float *out, hipStream_t st) {
-    switch (pl.lpr) {
-        case 16: return gemv_tl<TY, 16>(L, pl, P, x, nt, out, st);
-        case 32: return gemv_tl<TY, 32>(L, pl, P, x, nt, out, st);
-        default: return gemv_tl<TY, 64>(L, pl, P, x, nt, out, st);
-    }
-}
-
-// ------------------------------------------------------------------------------------------------------------
-// rows selected on the device: the model's token embedding and routed experts
-
-// embedding rows: out[t][k cols + c] = decoded W[ids[t]][c], for k < copies.  grid nt, 256 threads
-template <uint32_t TY>
-__global__ void __launch_bounds__(256) k_embed(PP P, int G, int cols, const int32_t *__restrict__ ids, int copies,
-                                               float *__restrict__ out) {
-    if constexpr (tab_lds<TY>() > 0) {
-        tab_fill<TY>(threadIdx.x, blockDim.x);
-        __syncthreads();
-    }
-    const int t = blockIdx.x, row = ids[t];
-    for (int g = threadIdx.x; g < G; g += blockDim.x) {
-        Grp o;
-        decode<TY>(P, row, g, o);
-        float4 v[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const int h = c >> 2;
-            float e[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float q = o.q[4 * c + k];
-                e[k] = TY == QT_BF16 ? q : __builtin_fmaf(o.s[h], q, -o.m[h]);
-            }
-            v[c] = make_float4(e[0], e[1], e[2], e[3]);
-        }
-        for (int k = 0; k < copies; ++k) {
-            float4 *dst = reinterpret_cast<float4 *>(out + ((size_t) t * copies + k) * cols + (size_t) g * 32);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) dst[c] = v[c];
-        }
-    }
-}
-
-// row r of expert sel[p] (R rows per expert) against x[p / xdiv]: 16 lanes per row, 4 rows per wave, 16 rows per
-// workgroup; lane li sums its groups li, li + 16, ... in order.  grid (ceil(R / 16), npairs), 256 threads.
-// SWIGLU: the gate row of Wg and the up row of Wu, out = silu(g) * u.
-template <uint32_t TY, bool SWIGLU>
-__global__ void __launch_bounds__(256) k_rows(PP Pg, PP Pu, int R, int nexp, int G, int cols,
-                                              const int32_t *__restrict__ sel, int xdiv, const float *__restrict__ x,
-                                              float *__restrict__ out) {
-    if constexpr (tab_lds<TY>() > 0) {
-        tab_fill<TY>(threadIdx.x, blockDim.x);
-        __syncthreads();
-    }
-    const TabT<TY> T;
-    const int p = blockIdx.y, lane = threadIdx.x & 63, li = lane & 15;
-    const int r = blockIdx.x * 16 + (threadIdx.x >> 6) * 4 + (lane >> 4);
-    const int e = sel ? min(max(sel[p], 0), nexp - 1) : 0;  // an id outside the weight reads its last expert
-    const int row = e * R + min(r, R - 1);
-    const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t) (p / xdiv) * cols);
-    float ag = 0.0f, au = 0.0f;
-    for (int g = li; g < G; g += 16) {
-        uint32_t w[Q<TY>::NW];
-        Q<TY>::load(row_planes(Pg, row), g, w);
-        accumulate<TY, 1>(w, g, xp + 8 * g, &ag, T);
-        if constexpr (SWIGLU) {
-            Q<TY>::load(row_planes(Pu, row), g, w);
-            accumulate<TY, 1>(w, g, xp + 8 * g, &au, T);
-        }
-    }
-    ag = row_sum(ag);
-    if constexpr (SWIGLU) au = row_sum(au);
-    if (li == 0 && r < R) {
-        float v = ag;
-        if constexpr (SWIGLU) v = ag / (1.0f + expf(-ag)) * au;
-        out[(size_t) p * R + r] = v;
-    }
-}
 
 }  // namespace
 
@@ -897,12 +73,18 @@ bool qlayout(uint32_t type, int rows, int cols, QLayout &L) {
         case QT_IQ4_NL: f = {32, 18, 2, {2, 0, 0}, {16, 2, 0}}; break;
         case QT_IQ4_XS: f = {256, 136, 2, {8, 0, 0}, {128, 8, 0}}; break;
         case QT_IQ3_S: f = {256, 110, 3, {2, 66, 0}, {64, 44, 2}}; break;
+        case QT_IQ2_XXS: f = {256, 66, 2, {2, 0, 0}, {64, 2, 0}}; break;
+        case QT_IQ2_XS: f = {256, 74, 3, {2, 66, 0}, {64, 8, 2}}; break;
+        case QT_IQ2_S: f = {256, 82, 3, {2, 66, 0}, {64, 16, 2}}; break;
+        case QT_IQ3_XXS: f = {256, 98, 2, {2, 0, 0}, {96, 2, 0}}; break;
+        case QT_Q2_0: f = {64, 18, 2, {2, 0, 0}, {16, 2, 0}}; break;
         case QT_Q4_K: f = {256, 144, 2, {16, 0, 0}, {128, 16, 0}}; break;
         case QT_Q5_K: f = {256, 176, 3, {48, 16, 0}, {128, 32, 16}}; break;
         case QT_Q6_K: f = {256, 210, 3, {0, 128, 192}, {128, 64, 18}}; break;
         default:
             set_error("unsupported type " + std::to_string(type) +
-                      " (this library reads BF16, Q8_0, Q4_K, Q5_K, Q6_K, IQ3_S, IQ4_NL, IQ4_XS)");
+                      " (this library reads BF16, Q8_0, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ4_NL, "
+                      "IQ4_XS, Q2_0)");
             return false;
     }
     if (rows < 1 || cols < 1 || cols % f.qk) {
@@ -976,23 +158,9 @@ int quant_pack_launch(const QLayout &L, const uint8_t *raw, uint8_t *packed, hip
 int quant_dequant_launch(const QLayout &L, const uint8_t *packed, float *out, hipStream_t st) {
     if (!packed || !out) FN_FAIL("dequant: null pointer");
     if ((uintptr_t) out % 16 || (uintptr_t) packed % 16) FN_FAIL("dequant: pointers must be 16-byte aligned");
-    const PP P = planes(L, packed);
-    const int G = L.cols / 32;
-    const size_t n = (size_t) L.rows * G;
-    const dim3 grid((unsigned) ((n + 255) / 256)), block(256);
-    switch (L.type) {
-        case QT_BF16: hipLaunchKernelGGL(k_dequant<QT_BF16>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
-        case QT_Q8_0: hipLaunchKernelGGL(k_dequant<QT_Q8_0>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
-        case QT_IQ4_NL: hipLaunchKernelGGL(k_dequant<QT_IQ4_NL>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
-        case QT_IQ4_XS: hipLaunchKernelGGL(k_dequant<QT_IQ4_XS>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
-        case QT_IQ3_S: hipLaunchKernelGGL(k_dequant<QT_IQ3_S>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
-        case QT_Q4_K: hipLaunchKernelGGL(k_dequant<QT_Q4_K>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
-        case QT_Q5_K: hipLaunchKernelGGL(k_dequant<QT_Q5_K>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
-        case QT_Q6_K: hipLaunchKernelGGL(k_dequant<QT_Q6_K>, grid, block, 0, st, P, L.rows, G, L.cols, out); break;
-        default: FN_FAIL("dequant: unsupported type");
-    }
-    FN_CK(hipGetLastError());
-    return 0;
+    const QOps *o = ops(L.type);
+    if (!o) FN_FAIL("dequant: unsupported type");
+    return o->dequant(L, planes(L, packed), out, st);
 }
 
 int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, float *y, float *work,
@@ -1007,19 +175,9 @@ int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt,
         if (!work || work_bytes < need) FN_FAIL("gemv: work buffer smaller than fn_gemv_work_bytes()");
         out = work;
     }
-    const PP P = planes(L, packed);
-    int rc = 0;
-    switch (L.type) {
-        case QT_BF16: rc = gemv_t<QT_BF16>(L, pl, P, x, nt, out, st); break;
-        case QT_Q8_0: rc = gemv_t<QT_Q8_0>(L, pl, P, x, nt, out, st); break;
-        case QT_IQ4_NL: rc = gemv_t<QT_IQ4_NL>(L, pl, P, x, nt, out, st); break;
-        case QT_IQ4_XS: rc = gemv_t<QT_IQ4_XS>(L, pl, P, x, nt, out, st); break;
-        case QT_IQ3_S: rc = gemv_t<QT_IQ3_S>(L, pl, P, x, nt, out, st); break;
-        case QT_Q4_K: rc = gemv_t<QT_Q4_K>(L, pl, P, x, nt, out, st); break;
-        case QT_Q5_K: rc = gemv_t<QT_Q5_K>(L, pl, P, x, nt, out, st); break;
-        case QT_Q6_K: rc = gemv_t<QT_Q6_K>(L, pl, P, x, nt, out, st); break;
-        default: FN_FAIL("gemv: unsupported type");
-    }
+    const QOps *o = ops(L.type);
+    if (!o) FN_FAIL("gemv: unsupported type");
+    const int rc = o->gemv(L, pl, planes(L, packed), x, nt, out, st);
     if (rc) return rc;
     if (pl.ks > 1) {
         const int n = nt * L.rows;
@@ -1029,79 +187,32 @@ int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt,
     return 0;
 }
 
-namespace {
-
-template <uint32_t TY>
-int embed_t(const QLayout &L, const PP &P, const int32_t *ids, int nt, int copies, float *out, hipStream_t st) {
-    hipLaunchKernelGGL(k_embed<TY>, dim3((unsigned) nt), dim3(256), 0, st, P, L.cols / 32, L.cols, ids, copies, out);
-    FN_CK(hipGetLastError());
-    return 0;
-}
-
-template <uint32_t TY, bool SW>
-int rows_t(const QLayout &L, const PP &Pg, const PP &Pu, int R, const int32_t *sel, int npairs, int xdiv,
-           const float *x, float *out, hipStream_t st) {
-    hipLaunchKernelGGL((k_rows<TY, SW>), dim3((unsigned) ((R + 15) / 16), (unsigned) npairs), dim3(256), 0, st, Pg,
-                       Pu, R, L.rows / R, L.cols / 32, L.cols, sel, xdiv, x, out);
-    FN_CK(hipGetLastError());
-    return 0;
-}
-
-template <bool SW>
-int rows_any(const QLayout &L, const PP &Pg, const PP &Pu, int R, const int32_t *sel, int npairs, int xdiv,
-             const float *x, float *out, hipStream_t st) {
-    switch (L.type) {
-        case QT_BF16: return rows_t<QT_BF16, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
-        case QT_Q8_0: return rows_t<QT_Q8_0, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
-        case QT_IQ4_NL: return rows_t<QT_IQ4_NL, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
-        case QT_IQ4_XS: return rows_t<QT_IQ4_XS, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
-        case QT_IQ3_S: return rows_t<QT_IQ3_S, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
-        case QT_Q4_K: return rows_t<QT_Q4_K, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
-        case QT_Q5_K: return rows_t<QT_Q5_K, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
-        case QT_Q6_K: return rows_t<QT_Q6_K, SW>(L, Pg, Pu, R, sel, npairs, xdiv, x, out, st);
-        default: FN_FAIL("rows: unsupported type");
-    }
-}
-
-int rows_check(const QLayout &L, int R, int npairs, int xdiv, const float *x, const float *out) {
-    if (R < 1 || L.rows % R || npairs < 1 || npairs > 65535 || xdiv < 1) FN_FAIL("rows: bad shape");
-    if (!x || !out) FN_FAIL("rows: null pointer");
-    if (((uintptr_t) x | (uintptr_t) out) % 16) FN_FAIL("rows: x and out must be 16-byte aligned");
-    return 0;
-}
-
-}  // namespace
 
 int embed_launch(const QLayout &L, const uint8_t *packed, const int32_t *ids, int nt, int copies, float *out,
                  hipStream_t st) {
     if (!packed || !ids || !out || nt < 1 || copies < 1) FN_FAIL("embed: bad arguments");
     if ((uintptr_t) out % 16) FN_FAIL("embed: out must be 16-byte aligned");
-    const PP P = planes(L, packed);
-    switch (L.type) {
-        case QT_BF16: return embed_t<QT_BF16>(L, P, ids, nt, copies, out, st);
-        case QT_Q8_0: return embed_t<QT_Q8_0>(L, P, ids, nt, copies, out, st);
-        case QT_IQ4_NL: return embed_t<QT_IQ4_NL>(L, P, ids, nt, copies, out, st);
-        case QT_IQ4_XS: return embed_t<QT_IQ4_XS>(L, P, ids, nt, copies, out, st);
-        case QT_IQ3_S: return embed_t<QT_IQ3_S>(L, P, ids, nt, copies, out, st);
-        case QT_Q4_K: return embed_t<QT_Q4_K>(L, P, ids, nt, copies, out, st);
-        case QT_Q5_K: return embed_t<QT_Q5_K>(L, P, ids, nt, copies, out, st);
-        case QT_Q6_K: return embed_t<QT_Q6_K>(L, P, ids, nt, copies, out, st);
-        default: FN_FAIL("embed: unsupported type");
-    }
+    const QOps *o = ops(L.type);
+    if (!o) FN_FAIL("embed: unsupported type");
+    return o->embed(L, planes(L, packed), ids, nt, copies, out, st);
 }
 
 int rows_launch(const QLayout &L, const uint8_t *packed, int R, const int32_t *sel, int npairs, int xdiv,
                 const float *x, float *out, hipStream_t st) {
     if (!packed || rows_check(L, R, npairs, xdiv, x, out)) return -1;
+    const QOps *o = ops(L.type);
+    if (!o) FN_FAIL("rows: unsupported type");
     const PP P = planes(L, packed);
-    return rows_any<false>(L, P, P, R, sel, npairs, xdiv, x, out, st);
+    return o->rows(L, P, P, R, sel, npairs, xdiv, x, out, st);
 }
 
 int swiglu_launch(const QLayout &Lg, const uint8_t *pg, const QLayout &Lu, const uint8_t *pu, int R,
                   const int32_t *sel, int npairs, int xdiv, const float *x, float *act, hipStream_t st) {
     if (!pg || !pu || rows_check(Lg, R, npairs, xdiv, x, act)) return -1;
     if (Lg.type != Lu.type || Lg.rows != Lu.rows || Lg.cols != Lu.cols) FN_FAIL("swiglu: gate and up weights differ");
-    return rows_any<true>(Lg, planes(Lg, pg), planes(Lu, pu), R, sel, npairs, xdiv, x, act, st);
+    const QOps *o = ops(Lg.type);
+    if (!o) FN_FAIL("swiglu: unsupported type");
+    return o->swiglu(Lg, planes(Lg, pg), planes(Lu, pu), R, sel, npairs, xdiv, x, act, st);
 }
 
 }  // namespace fn

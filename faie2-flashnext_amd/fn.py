@@ -51,9 +51,10 @@ STATUS_POS, STATUS_KR = 1, 2
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
 # GGUF type ids of the weight formats this library reads (engine/faie2fn.cu:78-81), and (values, bytes) per block
-QTYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ3_S=21, IQ4_XS=23, BF16=30)
-QBLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18), 21: (256, 110), 23: (256, 136),
-          30: (1, 2)}
+QTYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ2_XXS=16, IQ2_XS=17, IQ3_XXS=18, IQ4_NL=20, IQ3_S=21, IQ2_S=22,
+              IQ4_XS=23, BF16=30, Q2_0=42)
+QBLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 16: (256, 66), 17: (256, 74), 18: (256, 98),
+          20: (32, 18), 21: (256, 110), 22: (256, 82), 23: (256, 136), 30: (1, 2), 42: (64, 18)}
 
 
 def row_bytes(qtype, cols):

@@ -15,10 +15,13 @@ import numpy as np
 _U32, _I32, _F32, _BOOL, _STR, _ARR, _U64, _I64 = 4, 5, 6, 7, 8, 9, 10, 11
 # ggml type ids and (values, bytes) per block
 F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ3_S, IQ4_XS, BF16 = 0, 1, 8, 12, 13, 14, 20, 21, 23, 30
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ2_S, Q2_0 = 16, 17, 18, 22, 42
 BLOCK = {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210),
-         IQ4_NL: (32, 18), IQ3_S: (256, 110), IQ4_XS: (256, 136), BF16: (1, 2)}
+         IQ4_NL: (32, 18), IQ3_S: (256, 110), IQ4_XS: (256, 136), BF16: (1, 2), IQ2_XXS: (256, 66), IQ2_XS: (256, 74),
+         IQ3_XXS: (256, 98), IQ2_S: (256, 82), Q2_0: (64, 18)}
 # byte offsets of the fp16 scale fields inside a block (d, and dmin for the K formats with a minimum)
-SCALES = {Q8_0: [0], Q4_K: [0, 2], Q5_K: [0, 2], Q6_K: [208], IQ4_NL: [0], IQ3_S: [0], IQ4_XS: [0]}
+SCALES = {Q8_0: [0], Q4_K: [0, 2], Q5_K: [0, 2], Q6_K: [208], IQ4_NL: [0], IQ3_S: [0], IQ4_XS: [0], IQ2_XXS: [0],
+          IQ2_XS: [0], IQ3_XXS: [0], IQ2_S: [0], Q2_0: [0]}
 
 
 def _s(x):
@@ -81,7 +84,7 @@ def _f16_bits(x):
 # (code ranges: Q8_0 int8; IQ4 levels x (ls - 32) for IQ4_XS; IQ3_S (1 + 2 sc) x grid magnitudes; Q6_K int8 scale x
 # (q - 32); Q4_K / Q5_K 6-bit scale x 4 / 5-bit code)
 _RMS = {Q8_0: 73.9, IQ4_NL: 67.4, IQ4_XS: 67.4 * 18.5, IQ3_S: 18.5 * 7.6, Q6_K: 73.9 * 18.5, Q4_K: 36.5 * 8.8,
-        Q5_K: 36.5 * 18.0}
+        Q5_K: 36.5 * 18.0, IQ2_XXS: 53.4, IQ2_XS: 55.8, IQ2_S: 56.7, IQ3_XXS: 141.4, Q2_0: 1.225}
 
 
 def random_weight(ty, rows, cols, rng, std=None):
@@ -113,11 +116,17 @@ REFERENCE_DIMS = dict(D=2560, NL=48, NH=24, NKV=2, NE=512, NEU=10, FFE=640, FFS=
 TINY_DIMS = dict(D=256, NL=4, NH=8, NKV=2, NE=8, NEU=2, FFE=64, FFS=64, NKH=2, NVH=4, HC=4, HCR=32, top_k=32, VOCAB=320,
                  attn_every=4)
 
-# weight formats of the reference model by tensor (flashnext/inspect_fn.txt), with the routed experts in formats this
-# library reads (the reference's are IQ2_XXS / IQ2_XS / IQ2_S / IQ3_XXS gate/up and Q2_0 / IQ4_NL down)
-TYPES = dict(token_embd=IQ3_S, output=Q6_K, hc=BF16, attn_qkv=IQ4_XS, attn_gate=(IQ3_S, Q6_K), ssm_ab=BF16,
+# weight formats of the reference model by tensor (flashnext/inspect_fn.txt:75-157): layer-dependent formats as
+# tuples cycled over the layers (routed experts: IQ2_XS / IQ2_XXS / IQ2_S / IQ3_XXS gate and up, IQ4_NL / Q2_0 down)
+TYPES = dict(token_embd=IQ3_S, output=Q5_K, hc=BF16, attn_qkv=IQ4_XS, attn_gate=(IQ3_S, Q6_K), ssm_ab=BF16,
              ssm_out=Q8_0, attn_q=IQ4_XS, attn_k=IQ4_XS, attn_v=Q6_K, attn_output=Q8_0, indexer=BF16, router=BF16,
-             shexp_gate=IQ4_XS, shexp_up=IQ3_S, shexp_down=Q8_0, exps_gate=IQ3_S, exps_up=IQ3_S, exps_down=IQ4_NL)
+             shexp_gate=IQ4_XS, shexp_up=IQ3_S, shexp_down=Q8_0, exps_gate=(IQ2_XS, IQ2_XXS, IQ2_S, IQ3_XXS),
+             exps_up=(IQ2_XS, IQ2_XXS, IQ2_S, IQ3_XXS), exps_down=(IQ4_NL, Q2_0))
+
+
+def pick(ty, il):
+    """the format of layer il: a tuple of formats cycles over the layers"""
+    return ty[il % len(ty)] if isinstance(ty, tuple) else ty
 
 
 def model_tensors(dims, seed=0, types=None):
@@ -167,8 +176,7 @@ def model_tensors(dims, seed=0, types=None):
             W(p + f"hc_{part}_up.weight", T["hc"], HCD, HCR)
         if not attn:
             W(p + "attn_qkv.weight", T["attn_qkv"], CONV, D)
-            gate = T["attn_gate"]
-            W(p + "attn_gate.weight", gate[il % len(gate)] if isinstance(gate, tuple) else gate, DINNER, D)
+            W(p + "attn_gate.weight", pick(T["attn_gate"], il), DINNER, D)
             W(p + "ssm_alpha.weight", T["ssm_ab"], NVH, D)
             W(p + "ssm_beta.weight", T["ssm_ab"], NVH, D)
             W(p + "ssm_out.weight", T["ssm_out"], D, DINNER)
@@ -193,9 +201,9 @@ def model_tensors(dims, seed=0, types=None):
         W(p + "ffn_gate_shexp.weight", T["shexp_gate"], FFS, D)
         W(p + "ffn_up_shexp.weight", T["shexp_up"], FFS, D)
         W(p + "ffn_down_shexp.weight", T["shexp_down"], D, FFS)
-        W(p + "ffn_gate_exps.weight", T["exps_gate"], FFE, D, NE)
-        W(p + "ffn_up_exps.weight", T["exps_up"], FFE, D, NE)
-        W(p + "ffn_down_exps.weight", T["exps_down"], D, FFE, NE)
+        W(p + "ffn_gate_exps.weight", pick(T["exps_gate"], il), FFE, D, NE)
+        W(p + "ffn_up_exps.weight", pick(T["exps_up"], il), FFE, D, NE)
+        W(p + "ffn_down_exps.weight", pick(T["exps_down"], il), D, FFE, NE)
     return kv, ts
 
 

@@ -28,6 +28,18 @@
  *   IQ3_S [256]  110: d f16 | qs[64] | qh[8] | signs[32] | scales[4] (a 4-bit scale per group of 32; each group is
  *                8 grid points of 4 magnitudes from the format's 512-point codebook, 9-bit index = qs byte + one qh
  *                bit, signs one bit per value; ggml dequantize_row_iq3_s, reference DQ<T_IQ3_S> faie2fn.cu:565-583)
+ *   IQ2_XXS [256] 66: d f16 | qs u16[32] (per group of 32: 4 grid bytes, then a word of 4 x 7-bit sign indices and
+ *                a 4-bit scale in bits 28-31; faie2fn.cu:495-509)
+ *   IQ2_XS [256] 74: d f16 | qs u16[32] (9-bit grid index, 7-bit sign index) | scales[8] (two 4-bit scales per group,
+ *                one per half; :511-527)
+ *   IQ2_S [256]  82: d f16 | qs[32] grid low bytes | signs[32] | qh[8] (2 high index bits per 8 values) | scales[8]
+ *                (:529-546)
+ *   IQ3_XXS [256] 98: d f16 | qs[64] grid bytes | scales_and_signs u32[8] (4 x 7-bit sign indices, 4-bit scale in bits
+ *                28-31; :548-563)
+ *   Q2_0 [64]    18: d f16 | qs[16] (2-bit codes, value v in bits 2 (v % 4) of byte v / 4): y = d * (q - 1) (the
+ *                reference fork's type 42, :470-485)
+ * The IQ2 / IQ3_XXS sign indices select a sign byte ksign(i) = i | parity(i) << 7 (GGUF's ksigns_iq2xs), bit j negating
+ * value j of a run of 8.
  */
 #include <math.h>
 #include <stdint.h>
@@ -40,6 +52,28 @@
 static const uint32_t IQ3S_GRID[512] = {
 #include "../faie2-flashnext_amd/csrc/iq3s_grid.inc"
 };
+
+/* the IQ2 / IQ3_XXS codebooks (GGUF iq2xxs_grid, iq2xs_grid, iq2s_grid as low-word / high-word pairs; iq3xxs_grid) */
+static const uint32_t IQ2XXS_GRID[512] = {
+#include "../faie2-flashnext_amd/csrc/iq2xxs_grid.inc"
+};
+static const uint32_t IQ2XS_GRID[1024] = {
+#include "../faie2-flashnext_amd/csrc/iq2xs_grid.inc"
+};
+static const uint32_t IQ2S_GRID[2048] = {
+#include "../faie2-flashnext_amd/csrc/iq2s_grid.inc"
+};
+static const uint32_t IQ3XXS_GRID[256] = {
+#include "../faie2-flashnext_amd/csrc/iq3xxs_grid.inc"
+};
+
+/* the sign byte of a 7-bit sign index: the index with its parity as bit 7 (an even count of negated values) */
+static unsigned ksign(unsigned i) { return i | (unsigned) (__builtin_popcount(i) & 1) << 7; }
+
+/* magnitude j (0..7) of entry e of a codebook of 8-byte entries stored as two words */
+static float mag8(const uint32_t *grid, unsigned e, int j) {
+    return (float) ((grid[2 * e + (j >> 2)] >> (8 * (j & 3))) & 255);
+}
 
 /* the 16 levels of the IQ4 formats (GGUF kvalues_iq4nl) */
 static const int8_t IQ4_LEVELS[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
@@ -77,6 +111,11 @@ EXPORT int orc_qblock(uint32_t type, int *qk, int *bytes) {
         case 13: *qk = 256; *bytes = 176; return 1;
         case 14: *qk = 256; *bytes = 210; return 1;
         case 21: *qk = 256; *bytes = 110; return 1;
+        case 16: *qk = 256; *bytes = 66; return 1;
+        case 17: *qk = 256; *bytes = 74; return 1;
+        case 22: *qk = 256; *bytes = 82; return 1;
+        case 18: *qk = 256; *bytes = 98; return 1;
+        case 42: *qk = 64; *bytes = 18; return 1;
         default: return 0;
     }
 }
@@ -168,6 +207,77 @@ static void dq_row(uint32_t type, const uint8_t *r, int cols, float *y) {
                         }
                     }
                 }
+            }
+            break;
+        case 16: /* IQ2_XXS: db = d * (0.5 + s) * 0.25, y = db * grid * sign */
+            for (int b = 0; b < cols / 256; ++b, r += 66) {
+                const float d = f16(r);
+                for (int ib = 0; ib < 8; ++ib) {
+                    const uint8_t *q = r + 2 + 8 * ib;
+                    const uint32_t a1 = (uint32_t) q[4] | (uint32_t) q[5] << 8 | (uint32_t) q[6] << 16 | (uint32_t) q[7] << 24;
+                    const float db = d * (0.5f + (float) (a1 >> 28)) * 0.25f;
+                    for (int l = 0; l < 4; ++l, y += 8) {
+                        const unsigned sg = ksign((a1 >> (7 * l)) & 127);
+                        for (int j = 0; j < 8; ++j) y[j] = db * mag8(IQ2XXS_GRID, q[l], j) * ((sg >> j) & 1 ? -1.0f : 1.0f);
+                    }
+                }
+            }
+            break;
+        case 17: /* IQ2_XS: db = d * (0.5 + s_half) * 0.25 */
+            for (int b = 0; b < cols / 256; ++b, r += 74) {
+                const float d = f16(r);
+                const uint8_t *sc = r + 66;
+                for (int ib = 0; ib < 8; ++ib) {
+                    const float db0 = d * (0.5f + (float) (sc[ib] & 0xF)) * 0.25f;
+                    const float db1 = d * (0.5f + (float) (sc[ib] >> 4)) * 0.25f;
+                    for (int l = 0; l < 4; ++l, y += 8) {
+                        const unsigned q = (unsigned) r[2 + 2 * (4 * ib + l)] | (unsigned) r[3 + 2 * (4 * ib + l)] << 8;
+                        const unsigned sg = ksign(q >> 9);
+                        for (int j = 0; j < 8; ++j)
+                            y[j] = (l < 2 ? db0 : db1) * mag8(IQ2XS_GRID, q & 511, j) * ((sg >> j) & 1 ? -1.0f : 1.0f);
+                    }
+                }
+            }
+            break;
+        case 22: /* IQ2_S: 10-bit grid index (qs byte + 2 bits of qh), a full sign byte per 8 values */
+            for (int b = 0; b < cols / 256; ++b, r += 82) {
+                const float d = f16(r);
+                const uint8_t *qs = r + 2, *signs = r + 34, *qh = r + 66, *sc = r + 74;
+                for (int ib = 0; ib < 8; ++ib) {
+                    const float db0 = d * (0.5f + (float) (sc[ib] & 0xF)) * 0.25f;
+                    const float db1 = d * (0.5f + (float) (sc[ib] >> 4)) * 0.25f;
+                    for (int l = 0; l < 4; ++l, y += 8) {
+                        const unsigned e = qs[4 * ib + l] | ((qh[ib] << (8 - 2 * l)) & 0x300);
+                        const unsigned sg = signs[4 * ib + l];
+                        for (int j = 0; j < 8; ++j)
+                            y[j] = (l < 2 ? db0 : db1) * mag8(IQ2S_GRID, e, j) * ((sg >> j) & 1 ? -1.0f : 1.0f);
+                    }
+                }
+            }
+            break;
+        case 18: /* IQ3_XXS: db = d * (0.5 + s) * 0.5, 4-magnitude grid points in pairs */
+            for (int b = 0; b < cols / 256; ++b, r += 98) {
+                const float d = f16(r);
+                const uint8_t *qs = r + 2, *ss = r + 66;
+                for (int ib = 0; ib < 8; ++ib) {
+                    const uint32_t aux = (uint32_t) ss[4 * ib] | (uint32_t) ss[4 * ib + 1] << 8 |
+                                         (uint32_t) ss[4 * ib + 2] << 16 | (uint32_t) ss[4 * ib + 3] << 24;
+                    const float db = d * (0.5f + (float) (aux >> 28)) * 0.5f;
+                    for (int l = 0; l < 4; ++l, y += 8) {
+                        const unsigned sg = ksign((aux >> (7 * l)) & 127);
+                        const uint32_t g1 = IQ3XXS_GRID[qs[8 * ib + 2 * l]], g2 = IQ3XXS_GRID[qs[8 * ib + 2 * l + 1]];
+                        for (int j = 0; j < 4; ++j) {
+                            y[j] = db * (float) ((g1 >> (8 * j)) & 255) * ((sg >> j) & 1 ? -1.0f : 1.0f);
+                            y[j + 4] = db * (float) ((g2 >> (8 * j)) & 255) * ((sg >> (j + 4)) & 1 ? -1.0f : 1.0f);
+                        }
+                    }
+                }
+            }
+            break;
+        case 42: /* Q2_0: y = d * (q - 1) */
+            for (int b = 0; b < cols / 64; ++b, r += 18, y += 64) {
+                const float d = f16(r);
+                for (int v = 0; v < 64; ++v) y[v] = d * (float) ((int) ((r[2 + v / 4] >> (2 * (v % 4))) & 3) - 1);
             }
             break;
         case 14: /* Q6_K: y = d * sc * (q - 32) */

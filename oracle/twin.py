@@ -156,18 +156,45 @@ def ix_score(Qix, BKc, pos, max_ctx, ixr=4):
 
 IQ4_LEVELS = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float32)
 _BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18), 21: (256, 110), 23: (256, 136),
-          30: (1, 2)}
+          30: (1, 2), 16: (256, 66), 17: (256, 74), 22: (256, 82), 18: (256, 98), 42: (64, 18)}
 
 
-def iq3s_grid():
-    """The IQ3_S codebook [512] uint32, read from the data file the GPU decode and the C oracle include."""
+def grid_words(name):
+    """A codebook data file (csrc/<name>.inc, the one the GPU decode and the C oracle include) as uint32 words."""
     import os
     import re
 
     path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "faie2-flashnext_amd", "csrc",
-                        "iq3s_grid.inc")
+                        name + ".inc")
     text = re.sub(r"/\*.*?\*/", "", open(path).read(), flags=re.S)
     return np.array([int(v, 16) for v in re.findall(r"0x[0-9a-fA-F]+", text)], np.uint32)
+
+
+def iq3s_grid():
+    """The IQ3_S codebook [512] uint32."""
+    return grid_words("iq3s_grid")
+
+
+def grid_mags(name, per):
+    """Magnitudes [entries][per] of a codebook of `per` bytes per entry."""
+    w = grid_words(name)
+    b = ((w[:, None] >> (8 * np.arange(4, dtype=np.uint32))) & 255).reshape(-1)
+    return b.reshape(-1, per).astype(np.float32)
+
+
+def ksigns(idx):
+    """sign bits [..., 8] of 7-bit sign indices: the index with its parity as bit 7"""
+    idx = np.asarray(idx, np.int64)
+    par = np.zeros_like(idx)
+    for k in range(7):
+        par ^= (idx >> k) & 1
+    byte = idx | (par << 7)
+    return (byte[..., None] >> np.arange(8)) & 1
+
+
+def _le32(b):
+    b = b.astype(np.uint32)
+    return b[..., 0] | (b[..., 1] << 8) | (b[..., 2] << 16) | (b[..., 3] << 24)
 
 
 def _f16(b):
@@ -230,6 +257,48 @@ def dequant(qtype, raw, rows, cols):
         mag = (iq3s_grid()[idx][..., None] >> (8 * np.arange(4, dtype=np.uint32))) & 255  # [n][8][4][2][4]
         neg = ((signs[..., None] >> np.arange(8)) & 1).reshape(n, 8, 4, 2, 4)
         y = (db[:, :, None, None, None] * mag.astype(np.float32)) * np.where(neg == 1, -1.0, 1.0).astype(np.float32)
+    elif qtype in (16, 17, 22, 18):
+        d = _f16(blk[:, 0:2]).reshape(n)                                   # [n]
+        f = np.float32
+        if qtype == 16:   # IQ2_XXS: 4 grid bytes and a word of signs + scale per group
+            q = blk[:, 2:66].reshape(n, 8, 8)
+            a1 = _le32(q[:, :, 4:8])
+            db = d[:, None] * (f(0.5) + (a1 >> 28).astype(f)) * f(0.25)    # [n][8]
+            mags = grid_mags("iq2xxs_grid", 8)[q[:, :, 0:4].astype(np.int64)]  # [n][8][4][8]
+            neg = ksigns((a1[:, :, None] >> (7 * np.arange(4))) & 127)     # [n][8][4][8]
+            dbl = np.repeat(db[:, :, None], 4, axis=2)
+        elif qtype == 17:  # IQ2_XS: 9-bit grid index + 7-bit sign index per 8 values, a 4-bit scale per half
+            q = np.ascontiguousarray(blk[:, 2:66]).view(np.uint16).reshape(n, 8, 4).astype(np.int64)
+            sc = blk[:, 66:74].astype(np.int64)
+            db0 = d[:, None] * (f(0.5) + (sc & 15).astype(f)) * f(0.25)
+            db1 = d[:, None] * (f(0.5) + (sc >> 4).astype(f)) * f(0.25)
+            dbl = np.stack([db0, db0, db1, db1], axis=2)                   # [n][8][4]
+            mags = grid_mags("iq2xs_grid", 8)[q & 511]
+            neg = ksigns(q >> 9)
+        elif qtype == 22:  # IQ2_S: grid low byte + 2 bits of qh, a sign byte per 8 values
+            qs = blk[:, 2:34].reshape(n, 8, 4).astype(np.int64)
+            sg = blk[:, 34:66].reshape(n, 8, 4).astype(np.int64)
+            qh = blk[:, 66:74].astype(np.int64)
+            sc = blk[:, 74:82].astype(np.int64)
+            db0 = d[:, None] * (f(0.5) + (sc & 15).astype(f)) * f(0.25)
+            db1 = d[:, None] * (f(0.5) + (sc >> 4).astype(f)) * f(0.25)
+            dbl = np.stack([db0, db0, db1, db1], axis=2)
+            e = qs | ((qh[:, :, None] << (8 - 2 * np.arange(4))) & 0x300)
+            mags = grid_mags("iq2s_grid", 8)[e]
+            neg = (sg[..., None] >> np.arange(8)) & 1
+        else:              # IQ3_XXS: pairs of 4-magnitude grid points, a word of signs + scale per group
+            qs = blk[:, 2:66].reshape(n, 8, 4, 2).astype(np.int64)
+            aux = _le32(blk[:, 66:98].reshape(n, 8, 4))
+            db = d[:, None] * (f(0.5) + (aux >> 28).astype(f)) * f(0.5)
+            dbl = np.repeat(db[:, :, None], 4, axis=2)
+            g4 = grid_mags("iq3xxs_grid", 4)
+            mags = np.concatenate([g4[qs[..., 0]], g4[qs[..., 1]]], axis=-1)   # [n][8][4][8]
+            neg = ksigns((aux[:, :, None] >> (7 * np.arange(4))) & 127)
+        y = (dbl[..., None] * mags) * np.where(neg == 1, f(-1.0), f(1.0))
+    elif qtype == 42:  # Q2_0: y = d * (q - 1)
+        d = _f16(blk[:, 0:2]).reshape(n)
+        q = (blk[:, 2:18, None].astype(np.int64) >> (2 * np.arange(4))) & 3   # [n][16][4] -> value 4 byte + k
+        y = d[:, None] * (q.reshape(n, 64) - 1).astype(np.float32)
     elif qtype == 14:
         ql = blk[:, 0:128].reshape(n, 2, 2, 32).astype(np.int32)   # [half][first / second 32 bytes][l]
         qh = blk[:, 128:192].reshape(n, 2, 1, 32).astype(np.int32)

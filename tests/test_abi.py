@@ -106,15 +106,15 @@ def test_gemv_hooks_validate_before_device_work(fnlib):
     2918) before touching a device."""
     z8 = np.zeros(1 << 16, np.uint8)
     x = np.zeros((9, 256), np.float32)
-    with pytest.raises(RuntimeError, match="unsupported type 18"):        # IQ3_XXS: an MoE-expert format
-        fnlib.dequant(18, z8, 1, 256)
+    with pytest.raises(RuntimeError, match="unsupported type 19"):        # IQ1_S: not a format of the model
+        fnlib.dequant(19, z8, 1, 256)
     with pytest.raises(RuntimeError, match="unsupported shape"):          # K-quant row not a whole super-block
         fnlib.dequant(12, z8, 1, 288)
     with pytest.raises(RuntimeError, match="nt must be 1..8"):
         fnlib.gemv(8, z8, 1, 256, x)
     with pytest.raises(RuntimeError, match="unsupported type 0"):         # F32 has no block decode
         fnlib.gemv(0, z8, 1, 256, x[:1])
-    assert fnlib.gemv_packed_bytes(18, 4, 256) == 0 and fnlib.gemv_work_bytes(8, 4, 256, 9) == 0
+    assert fnlib.gemv_packed_bytes(19, 4, 256) == 0 and fnlib.gemv_work_bytes(8, 4, 256, 9) == 0
     assert fnlib.gemv_packed_bytes(21, 4, 256) >= 4 * 110          # IQ3_S is read
     with pytest.raises(RuntimeError, match="unsupported"):
         fnlib.gemv_plan(1, 4, 256)

@@ -20,7 +20,8 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
-TYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ3_S=21, IQ4_XS=23, BF16=30)
+TYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ3_S=21, IQ4_XS=23, BF16=30, IQ2_XXS=16, IQ2_XS=17,
+             IQ2_S=22, IQ3_XXS=18, Q2_0=42)
 RNG = np.random.default_rng(31)
 
 
@@ -32,7 +33,8 @@ def random_finite(qtype, rows, cols, rng):
     qk, bb = oracle.qblock(qtype)
     raw = rng.integers(0, 256, size=rows * (cols // qk) * bb, dtype=np.uint8)
     blk = raw.reshape(-1, bb)
-    for b in {30: [1], 8: [1], 20: [1], 21: [1], 23: [1], 12: [1, 3], 13: [1, 3], 14: [209]}[qtype]:
+    for b in {30: [1], 8: [1], 20: [1], 21: [1], 23: [1], 12: [1, 3], 13: [1, 3], 14: [209], 16: [1], 17: [1], 22: [1],
+              18: [1], 42: [1]}[qtype]:
         blk[:, b] &= 0xBF
     return raw
 
@@ -58,6 +60,11 @@ PATH_SHAPES = [
     ("IQ4_XS", 512, 2560),     # attn_k
     ("Q6_K", 6144, 2560),      # attn_gate (z) of layer 1
     ("IQ3_S", 6144, 2560),     # attn_gate (z) of layer 0 (inspect_fn.txt:76)
+    ("IQ2_XS", 640, 2560),     # one routed expert's gate / up rows (blk.0.ffn_gate_exps, inspect_fn.txt:80)
+    ("IQ2_XXS", 640, 2560),    # blk.1.ffn_gate_exps
+    ("IQ2_S", 640, 2560),
+    ("IQ3_XXS", 640, 2560),
+    ("Q2_0", 2560, 640),       # one routed expert's down rows (blk.1.ffn_down_exps)
     ("IQ4_XS", 8192, 2048),    # config 1/2 qkv: 8192 mixed channels from hidden 2048
     ("Q8_0", 2048, 4096),      # config 1/2 ssm_out
 ]

@@ -20,7 +20,8 @@ import oracle
 import oracle.twin as twin
 
 RNG = np.random.default_rng(7)
-TYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ3_S=21, IQ4_XS=23, BF16=30)
+TYPES = dict(Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14, IQ4_NL=20, IQ3_S=21, IQ4_XS=23, BF16=30, IQ2_XXS=16, IQ2_XS=17,
+             IQ2_S=22, IQ3_XXS=18, Q2_0=42)
 LEVELS = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
 
 
@@ -40,7 +41,8 @@ def random_finite(qtype, rows, cols, rng):
     qk, bb = oracle.qblock(qtype)
     raw = rng.integers(0, 256, size=rows * (cols // qk) * bb, dtype=np.uint8)
     blk = raw.reshape(-1, bb)
-    hi_bytes = {30: [1], 8: [1], 20: [1], 21: [1], 23: [1], 12: [1, 3], 13: [1, 3], 14: [209]}[qtype]
+    hi_bytes = {30: [1], 8: [1], 20: [1], 21: [1], 23: [1], 12: [1, 3], 13: [1, 3], 14: [209], 16: [1], 17: [1], 22: [1],
+                18: [1], 42: [1]}[qtype]
     for b in hi_bytes:
         blk[:, b] &= 0xBF
     return raw
@@ -270,6 +272,148 @@ def test_iq3_s_codebook():
     body = text[text.index("{", i) + 1:text.index("}", i)]
     want = np.array([int(v, 16) for v in re.findall(r"0x[0-9a-fA-F]+", body)], np.uint32)
     assert np.array_equal(g, want)
+
+
+def ksign_bits(i):
+    """sign bits of a 7-bit sign index: the index and, as bit 7, its parity (GGUF ksigns_iq2xs)"""
+    b = i | ((bin(i).count("1") & 1) << 7)
+    return [(b >> j) & 1 for j in range(8)]
+
+
+def mags(name, per, e):
+    w = twin.grid_words(name)
+    words = per // 4
+    return [(int(w[words * e + j // 4]) >> (8 * (j % 4))) & 255 for j in range(per)]
+
+
+def test_iq2_xxs_packed_codes():
+    """IQ2_XXS from chosen codes: per group 4 grid indices (bytes), 4 seven-bit sign indices and a 4-bit scale in one
+    word; value = d (0.5 + s) / 4 x grid magnitude x sign (all products exact)."""
+    blocks, want = [], []
+    for _ in range(2):
+        db_, d = rand_f16_scale(RNG)
+        out = [db_ & 255, db_ >> 8]
+        for ib in range(8):
+            idx = RNG.integers(0, 256, size=4)
+            sidx = RNG.integers(0, 128, size=4)
+            sc = int(RNG.integers(0, 16))
+            w = int(sidx[0]) | int(sidx[1]) << 7 | int(sidx[2]) << 14 | int(sidx[3]) << 21 | sc << 28
+            out += [int(v) for v in idx] + [(w >> (8 * k)) & 255 for k in range(4)]
+            dl = d * (0.5 + sc) * 0.25
+            for l in range(4):
+                m, sg = mags("iq2xxs_grid", 8, int(idx[l])), ksign_bits(int(sidx[l]))
+                want += [f32_once(dl * m[j] * (-1 if sg[j] else 1)) for j in range(8)]
+        blocks.append(np.array(out, np.uint8))
+    got = oracle.dequant(16, np.concatenate(blocks), 1, 512)[0]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_iq2_xs_packed_codes():
+    """IQ2_XS: 16-bit codes of a 9-bit grid index and a 7-bit sign index, two 4-bit scales per group (first and
+    second half)."""
+    blocks, want = [], []
+    for _ in range(2):
+        db_, d = rand_f16_scale(RNG)
+        qs, sc = [], []
+        vals = []
+        for ib in range(8):
+            s0, s1 = int(RNG.integers(0, 16)), int(RNG.integers(0, 16))
+            sc.append(s0 | s1 << 4)
+            for l in range(4):
+                e, si = int(RNG.integers(0, 512)), int(RNG.integers(0, 128))
+                qs.append(e | si << 9)
+                dl = d * (0.5 + (s0 if l < 2 else s1)) * 0.25
+                m, sg = mags("iq2xs_grid", 8, e), ksign_bits(si)
+                vals += [f32_once(dl * m[j] * (-1 if sg[j] else 1)) for j in range(8)]
+        blocks.append(np.concatenate([np.array([db_ & 255, db_ >> 8], np.uint8),
+                                      np.array(qs, np.uint16).view(np.uint8), np.array(sc, np.uint8)]))
+        want += vals
+    got = oracle.dequant(17, np.concatenate(blocks), 1, 512)[0]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_iq2_s_packed_codes():
+    """IQ2_S: a 10-bit grid index (byte of qs, two bits of qh[ib] at 2l), a full sign byte per 8 values, two 4-bit
+    scales per group."""
+    db_, d = rand_f16_scale(RNG)
+    qs, signs, qh, sc, want = [], [], [], [], []
+    for ib in range(8):
+        s0, s1 = int(RNG.integers(0, 16)), int(RNG.integers(0, 16))
+        sc.append(s0 | s1 << 4)
+        h = 0
+        for l in range(4):
+            e, sb = int(RNG.integers(0, 1024)), int(RNG.integers(0, 256))
+            qs.append(e & 255)
+            h |= (e >> 8) << (2 * l)
+            signs.append(sb)
+            dl = d * (0.5 + (s0 if l < 2 else s1)) * 0.25
+            m = mags("iq2s_grid", 8, e)
+            want += [f32_once(dl * m[j] * (-1 if (sb >> j) & 1 else 1)) for j in range(8)]
+        qh.append(h)
+    blk = np.array([db_ & 255, db_ >> 8] + qs + signs + qh + sc, np.uint8)
+    got = oracle.dequant(22, blk, 1, 256)[0]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_iq3_xxs_packed_codes():
+    """IQ3_XXS: per group 8 grid bytes (pairs of 4-magnitude points) and a word of 4 sign indices + a 4-bit scale;
+    value = d (0.5 + s) / 2 x magnitude x sign."""
+    db_, d = rand_f16_scale(RNG)
+    qs, ss, want = [], [], []
+    for ib in range(8):
+        idx = [int(v) for v in RNG.integers(0, 256, size=8)]
+        sidx = [int(v) for v in RNG.integers(0, 128, size=4)]
+        s = int(RNG.integers(0, 16))
+        qs += idx
+        w = sidx[0] | sidx[1] << 7 | sidx[2] << 14 | sidx[3] << 21 | s << 28
+        ss += [(w >> (8 * k)) & 255 for k in range(4)]
+        dl = d * (0.5 + s) * 0.5
+        for l in range(4):
+            m = mags("iq3xxs_grid", 4, idx[2 * l]) + mags("iq3xxs_grid", 4, idx[2 * l + 1])
+            sg = ksign_bits(sidx[l])
+            want += [f32_once(dl * m[j] * (-1 if sg[j] else 1)) for j in range(8)]
+    blk = np.array([db_ & 255, db_ >> 8] + qs + ss, np.uint8)
+    got = oracle.dequant(18, blk, 1, 256)[0]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_q2_0_packed_codes():
+    """Q2_0 (the reference fork's type 42, faie2fn.cu:470-485): value v of a 64-value block is d (q - 1) with q the
+    2-bit code at bits 2 (v % 4) of byte v / 4."""
+    blocks, want = [], []
+    for _ in range(4):
+        db_, d = rand_f16_scale(RNG)
+        q = RNG.integers(0, 4, size=64)
+        by = [int(q[4 * k] | q[4 * k + 1] << 2 | q[4 * k + 2] << 4 | q[4 * k + 3] << 6) for k in range(16)]
+        blocks.append(np.array([db_ & 255, db_ >> 8] + by, np.uint8))
+        want += [f32_once(d * (int(v) - 1)) for v in q]
+    got = oracle.dequant(42, np.concatenate(blocks), 1, 256)[0]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+@pytest.mark.parametrize("name,entries,per,levels", [("iq2xxs_grid", 256, 8, {8, 25, 43}),
+                                                     ("iq2xs_grid", 512, 8, {8, 25, 43}),
+                                                     ("iq2s_grid", 1024, 8, {8, 25, 43}),
+                                                     ("iq3xxs_grid", 256, 4, {4, 12, 20, 28, 36, 44, 52, 62})])
+def test_iq2_iq3xxs_codebooks(name, entries, per, levels):
+    """The codebook data files: entry count, distinct entries in ascending order, magnitudes from the format's level
+    set; where the reference tree is present, equal to the copy it carries (engine/fn_tables.cuh:21, 88, 219, 478)."""
+    import os
+    import re
+
+    w = twin.grid_words(name).astype(np.uint64)
+    vals = w if per == 4 else w[0::2] | (w[1::2] << np.uint64(32))
+    assert len(vals) == entries and np.all(vals[1:] > vals[:-1])
+    m = twin.grid_mags(name, per)
+    assert set(np.unique(m).astype(int).tolist()) <= levels
+    ref = "/root/reference/engine/fn_tables.cuh"
+    if not os.path.exists(ref):
+        pytest.skip("reference tree not present (GPU box)")
+    text = open(ref).read()
+    i = text.index(name + "[")
+    body = text[text.index("{", i) + 1:text.index("}", i)]
+    want = np.array([int(v, 16) for v in re.findall(r"0x[0-9a-fA-F]+", body)], np.uint64)
+    assert np.array_equal(vals, want)
 
 
 @pytest.mark.parametrize("name", list(TYPES))
