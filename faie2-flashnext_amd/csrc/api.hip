@@ -78,7 +78,8 @@ FN_API int fn_model_dims(const char *path, int *out, int n) {
     if (!out || n < 1) FN_FAIL("model_dims: null output");
     if (fn::model_inspect(path, &d)) return -1;
     const int v[] = {d.D, d.NL, d.NH, d.NKV, d.HD, d.NROT, d.NE, d.NEU, d.FFE, d.FFS, d.DS, d.NKH, d.NVH, d.DINNER,
-                     d.CONVCH, d.attn_every, d.HC, d.HCR, d.IXH, d.IXD, d.top, d.VOCAB};
+                     d.CONVCH, d.attn_every, d.HC, d.HCR, d.IXH, d.IXD, d.top, d.VOCAB, d.ple_layers, d.ple_heads,
+                     d.ple_hd};
     const int k = (int) (sizeof(v) / sizeof(v[0]));
     for (int i = 0; i < n; ++i) out[i] = i < k ? v[i] : 0;
     return k;

@@ -3,6 +3,7 @@
 #pragma once
 
 #include <cstdint>
+#include <vector>
 
 namespace fn {
 
@@ -10,7 +11,10 @@ namespace fn {
 struct ModelDims {
     int D = 0, NL = 0, NH = 0, NKV = 0, HD = 0, NROT = 0, NE = 0, NEU = 0, FFE = 0, FFS = 0, DS = 0, NKH = 0, NVH = 0;
     int DINNER = 0, CONVCH = 0, conv = 0, attn_every = 0, HC = 0, HCR = 0, IXH = 0, IXD = 0, top = 0, VOCAB = 0;
-    int ple_layers = 0;
+    // per-layer n-gram embedding (PLE): the layers that have one, and its hashing and shapes
+    std::vector<int> ple;
+    int ple_layers = 0, ple_heads = 0, ple_hd = 0, ple_eos = -1;
+    std::vector<int64_t> ple_mult, ple_off, ple_size;
     float theta = 0, eps = 0;
 };
 

@@ -15,10 +15,13 @@
 //                          (faie2fn.cu:1747-1798), routed experts' SwiGLU and down rows, the shared expert's down GEMV
 //   hyper-connection write with y = sum_k w_k down_k + sigmoid(shared gate) shared down (faie2fn.cu:1298-1318)
 // then the final hyper-connection read (no inject), the LM head GEMV and the argmax (lowest index on ties,
-// faie2fn.cu:1910-1934).  Shapes come from the GGUF metadata (the reference fixes them at build time and asserts
-// them at load, faie2fn.cu:2532-2535); the kernels fix head_dim 256, DeltaNet head dim 128, the indexer's 4 x 128 and
-// blocks of 4 keys.  Not built: the per-layer n-gram embedding (PLE, a 27 GB hashed table in the second shard):
-// fn_load rejects a model whose metadata lists PLE layers.
+// faie2fn.cu:1910-1934).  The layers listed in <arch>.ple.layers first add the per-layer n-gram embedding
+// (faie2fn.cu:1805-1896, 2373-2381): the bigram and trigram contexts of each position hash into rows of a table of
+// IQ4_NL rows (per_layer_token_embd, 27 GB in the reference model's second shard, kept here in HBM where the
+// reference maps it from pinned host memory); key and value GEMVs of the gathered row, a per-stream signed-sqrt
+// gate, and a dilated causal conv (kernel 4, dilation 3) of the gated value feed the residual streams.  Shapes come
+// from the GGUF metadata (the reference fixes them at build time and asserts them at load, faie2fn.cu:2532-2535); the
+// kernels fix head_dim 256, DeltaNet head dim 128, the indexer's 4 x 128 and blocks of 4 keys.
 #include "engine.h"
 #include "gguf.h"
 #include "model.h"
@@ -38,6 +41,8 @@ constexpr int MAXT = 8;                      // tokens per forward (faie2fn.cu:6
 constexpr int HDK = 256, DSK = 128;          // attention head dim, DeltaNet head dim (built sizes)
 constexpr int IXH = 4, IXD = 128, IXR = 4;   // indexer heads, head dim, keys per block (built sizes)
 constexpr int RING = 16;                     // conv ring slots (>= MAXT + 3, a power of two)
+constexpr int PLE_HIST = 9;                  // PLE conv history: (kernel 4 - 1) x dilation 3 (faie2fn.cu:66)
+constexpr int PLE_MAXH = 64;                 // n-gram heads the hashing kernel takes
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
@@ -197,6 +202,89 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ logit
     if (threadIdx.x == 0) out[blockIdx.x] = idx;
 }
 
+// tok_all[pos + t] = ids[t]: the token history the n-gram hashing reads (faie2fn.cu:1899-1903).  1 block
+__global__ void k_store_tokens(const int32_t *__restrict__ ids, int32_t *__restrict__ tok_all,
+                               const int32_t *__restrict__ pos, int nt, int max_ctx) {
+    const int t = threadIdx.x, p = *pos + t;
+    if (t < nt && p >= 0 && p < max_ctx) tok_all[p] = ids[t];
+}
+
+struct PleHash {
+    unsigned long long mult[3], size[PLE_MAXH], off[PLE_MAXH];
+};
+
+// table rows of the n-gram heads of position pos + t (faie2fn.cu:1810-1823): head hd hashes the bigram (token,
+// previous) and, for the second half of the heads, the trigram; contexts do not reach back across an EOS.
+// grid nt, 64 threads
+__global__ void k_ple_ids(const int32_t *__restrict__ tok_all, const int32_t *__restrict__ pos, int nheads, int eos,
+                          const PleHash hsh, int32_t *__restrict__ rows) {
+    const int t = blockIdx.x, hd = threadIdx.x;
+    if (hd >= nheads) return;
+    const int p = *pos + t;
+    // ids widen to 64 bits with their sign, products wrap modulo 2^64 (the reference's unsigned long long arithmetic)
+    const unsigned long long t0 = (unsigned long long) (long long) tok_all[p];
+    const int p1 = p >= 1 ? tok_all[p - 1] : eos;
+    const int p2 = (p >= 2 && p1 != eos) ? tok_all[p - 2] : eos;
+    unsigned long long mixed = (t0 * hsh.mult[0]) ^ ((unsigned long long) (long long) p1 * hsh.mult[1]);
+    if (hd >= nheads / 2) mixed ^= (unsigned long long) (long long) p2 * hsh.mult[2];
+    rows[t * nheads + hd] = (int32_t) (mixed % hsh.size[hd] + hsh.off[hd]);
+}
+
+// per stream s (faie2fn.cu:1843-1875): gate = <RMSNorm(key_s) wk, RMSNorm(h_s) wq> / sqrt(D), signed square root
+// (magnitude floored at 1e-6); gv = sigmoid(gate) * val; gvn = RMSNorm(gv) wc.  grid (nt, HC), 256 threads
+__global__ void __launch_bounds__(256) k_ple_gate(const float *__restrict__ key, const float *__restrict__ val,
+                                                  const float *__restrict__ h, const float *__restrict__ wk,
+                                                  const float *__restrict__ wq, const float *__restrict__ wc, int D,
+                                                  float eps, float *__restrict__ gv, float *__restrict__ gvn) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, s = blockIdx.y, HC = gridDim.y;
+    const size_t base = ((size_t) t * HC + s) * D;
+    const float *kt = key + base, *ht = h + base, *vt = val + (size_t) t * D;
+    float sk = 0.0f, sq = 0.0f;
+    for (int c = threadIdx.x; c < D; c += 256) {
+        sk += kt[c] * kt[c];
+        sq += ht[c] * ht[c];
+    }
+    sk = block_sum(sk, red, 4);
+    sq = block_sum(sq, red, 4);
+    const float rk = rsqrtf(sk / D + eps), rq = rsqrtf(sq / D + eps);
+    float dot = 0.0f;
+    for (int c = threadIdx.x; c < D; c += 256)
+        dot += (kt[c] * rk * wk[(size_t) s * D + c]) * (ht[c] * rq * wq[(size_t) s * D + c]);
+    dot = block_sum(dot, red, 4);
+    float gate = dot / sqrtf((float) D);
+    gate = gate == 0.0f ? 0.0f : copysignf(sqrtf(fmaxf(fabsf(gate), 1e-6f)), gate);
+    const float sg = sigm(gate);
+    float sv = 0.0f;
+    for (int c = threadIdx.x; c < D; c += 256) {
+        const float x = sg * vt[c];
+        gv[base + c] = x;
+        sv += x * x;
+    }
+    sv = block_sum(sv, red, 4);
+    const float rv = rsqrtf(sv / D + eps);
+    for (int c = threadIdx.x; c < D; c += 256) gvn[base + c] = gv[base + c] * rv * wc[(size_t) s * D + c];
+}
+
+// dilated causal depthwise conv (kernel 4, dilation 3) over gvn with its history, SiLU, then h += gv + conv; the
+// history keeps the last 9 gvn of every channel (faie2fn.cu:1878-1896).  grid ceil(n / 256), 256 threads
+__global__ void k_ple_conv(float *__restrict__ h, const float *__restrict__ gv, const float *__restrict__ gvn,
+                           float *__restrict__ hist, const float *__restrict__ w, int n, int nt) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= n) return;
+    float x[PLE_HIST + MAXT];
+#pragma unroll
+    for (int i = 0; i < PLE_HIST; ++i) x[i] = hist[(size_t) i * n + c];
+    for (int t = 0; t < nt; ++t) x[PLE_HIST + t] = gvn[(size_t) t * n + c];
+    const float w0 = w[c * 4 + 0], w1 = w[c * 4 + 1], w2 = w[c * 4 + 2], w3 = w[c * 4 + 3];
+    for (int t = 0; t < nt; ++t) {
+        const int i = PLE_HIST + t;
+        const float sv = w0 * x[i - 9] + w1 * x[i - 6] + w2 * x[i - 3] + w3 * x[i];
+        h[(size_t) t * n + c] += gv[(size_t) t * n + c] + silu(sv);
+    }
+    for (int i = 0; i < PLE_HIST; ++i) hist[(size_t) i * n + c] = x[nt + i];
+}
+
 // ------------------------------------------------------------------------------------------------------------
 
 struct QW {
@@ -217,12 +305,20 @@ struct MLayer {
     float *Kc = nullptr, *Vc = nullptr, *IKc = nullptr, *BKc = nullptr;
     // FFN
     QW rsg, sh_gate, sh_up, sh_down, eg, eu, ed;
+    // per-layer n-gram embedding
+    bool ple = false;
+    QW ple_key, ple_val;
+    float *ple_nk = nullptr, *ple_nq = nullptr, *ple_nc = nullptr, *ple_conv = nullptr, *ple_hist = nullptr;
 };
 
 struct Model {
     ModelDims d;
     int max_ctx = 0, nsplit = 1;
-    Gguf g;
+    Gguf g, g2;  // the model, and the optional second shard (the n-gram table)
+    QW ple_table;
+    PleHash hsh{};
+    int32_t *tok_all = nullptr, *ple_rows = nullptr;
+    float *ple_emb = nullptr, *ple_k = nullptr, *ple_v = nullptr, *ple_gv = nullptr, *ple_gvn = nullptr;
     std::vector<MLayer> L;
     QW tok, head, out_down, out_up;
     float *out_norm = nullptr;
@@ -267,8 +363,9 @@ std::unique_ptr<Model> g_model;
 
 // ---- load ----
 
-int need(const Gguf &g, const std::string &name, const GTensor **t) {
-    *t = g.find(name);
+int need(const Model &m, const std::string &name, const GTensor **t) {
+    *t = m.g.find(name);
+    if (!*t && m.g2.base) *t = m.g2.find(name);
     if (!*t) FN_FAIL("load: tensor " + name + " missing");
     return 0;
 }
@@ -285,13 +382,24 @@ int check_shape(const std::string &name, const GTensor *t, uint64_t cols, uint64
 // an F32 vector of n values to device memory
 int load_f32(Model &m, const std::string &name, size_t n, float **out) {
     const GTensor *t;
-    if (need(m.g, name, &t)) return -1;
-    if (t->type != 0) FN_FAIL("load: tensor " + name + " must be F32");
+    if (need(m, name, &t)) return -1;
+    if (t->type != 0 && t->type != 1) FN_FAIL("load: tensor " + name + " must be F32 or F16");
     if ((size_t) (t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]) != n)
         FN_FAIL("load: tensor " + name + " has " + std::to_string(t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]) +
                 " values, expected " + std::to_string(n));
     if (m.alloc(out, n)) return -1;
-    FN_CK(hipMemcpy(*out, t->data, n * 4, hipMemcpyHostToDevice));
+    if (t->type == 0) {
+        FN_CK(hipMemcpy(*out, t->data, n * 4, hipMemcpyHostToDevice));
+        return 0;
+    }
+    std::vector<float> hf(n);  // F16 -> F32 exactly (the reference's load_f32, faie2fn.cu:2173-2184)
+    const uint16_t *hb = reinterpret_cast<const uint16_t *>(t->data);
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t b = hb[i], sgn = (b >> 15) & 1, e = (b >> 10) & 31, f = b & 1023;
+        float v = e == 0 ? std::ldexp((float) f, -24) : (e == 31 ? (f ? NAN : INFINITY) : std::ldexp((float) (1024 + f), (int) e - 25));
+        hf[i] = sgn ? -v : v;
+    }
+    FN_CK(hipMemcpy(*out, hf.data(), n * 4, hipMemcpyHostToDevice));
     return 0;
 }
 
@@ -303,7 +411,7 @@ int load_qw(Model &m, const std::vector<std::string> &names, const std::vector<u
     std::vector<const GTensor *> ts;
     for (size_t i = 0; i < names.size(); ++i) {
         const GTensor *t;
-        if (need(m.g, names[i], &t) || check_shape(names[i], t, cols, rows[i], n3)) return -1;
+        if (need(m, names[i], &t) || check_shape(names[i], t, cols, rows[i], n3)) return -1;
         if (i && t->type != type) FN_FAIL("load: tensors " + names[0] + " and " + names[i] + " differ in type");
         type = t->type;
         total += rows[i] * n3;
@@ -362,8 +470,20 @@ int read_dims(const Gguf &g, ModelDims &d) {
     d.IXH = (int) num("attention.indexer.head_count", IXH);
     d.IXD = (int) num("attention.indexer.key_length", IXD);
     d.top = (int) num("attention.indexer.top_k", 2048) / IXR;
-    auto ple = g.iarrays.find(a + "ple.layers");
-    d.ple_layers = ple == g.iarrays.end() ? 0 : (int) ple->second.size();
+    auto arr = [&](const char *k) {
+        auto it2 = g.iarrays.find(a + k);
+        return it2 == g.iarrays.end() ? std::vector<int64_t>{} : it2->second;
+    };
+    for (int64_t v : arr("ple.layers")) d.ple.push_back((int) v);
+    d.ple_layers = (int) d.ple.size();
+    if (d.ple_layers) {
+        d.ple_heads = 2 * (int) num("ple.heads_per_ngram", 8);
+        d.ple_hd = (int) num("embedding_length_per_layer_input", 160);
+        d.ple_eos = (int) num("ple.eos_token_id", -1);
+        d.ple_mult = arr("ple.layer_multipliers");
+        d.ple_off = arr("ple.head_offsets");
+        d.ple_size = arr("ple.head_vocab_sizes");
+    }
     const GTensor *te = g.find("token_embd.weight");
     if (!te) FN_FAIL("load: tensor token_embd.weight missing");
     d.VOCAB = (int) te->ne[1];
@@ -380,9 +500,59 @@ int read_dims(const Gguf &g, ModelDims &d) {
         return bad("experts (at most 1024, at most 32 used)");
     if (d.HC < 1 || d.HC > 16 || d.HCR < 1) return bad("hyper-connections");
     if (d.attn_every < 0) return bad("full_attention_interval");
-    if (d.ple_layers > 0)
-        FN_FAIL("load: the model has per-layer n-gram embedding (PLE) layers, which this library does not build");
+    if (d.ple_layers) {
+        if ((int) num("ple.ngram_size", 3) != 3 || (int) num("ple.conv_kernel", 4) != 4)
+            return bad("PLE: n-grams of 3 and conv kernel 4 are built");
+        if (d.ple_heads < 2 || d.ple_heads > PLE_MAXH || d.ple_hd < 32 || d.ple_hd % 32 || d.ple_heads * d.ple_hd != d.D)
+            return bad("PLE: heads x values per head must be the embedding length, values per head a multiple of 32");
+        if (d.ple_mult.size() != 3 || (int) d.ple_off.size() != d.ple_heads || (int) d.ple_size.size() != d.ple_heads)
+            return bad("PLE: multipliers, head offsets and head sizes");
+        for (int i = 0; i < d.ple_heads; ++i)
+            if (d.ple_size[i] < 1 || d.ple_off[i] < 0 || d.ple_off[i] + d.ple_size[i] > 0x7fffffffLL)
+                return bad("PLE: head table ranges");
+        for (int il : d.ple)
+            if (il < 0 || il >= d.NL) return bad("PLE: layer index");
+    }
     return 0;
+}
+
+// the per-layer n-gram embedding: the hashed table (packed whole into HBM), each PLE layer's key / value weights,
+// norms and conv, the hash constants, and the buffers of MAXT tokens (faie2fn.cu:2598-2603, 2661-2687)
+int load_ple(Model &m) {
+    const ModelDims &d = m.d;
+    const uint64_t D = d.D, HCD = (uint64_t) d.HC * d.D;
+    const GTensor *t;
+    if (need(m, "per_layer_token_embd.weight", &t)) return -1;
+    if (t->nd != 2 || t->ne[0] != (uint64_t) d.ple_hd)
+        FN_FAIL("load: per_layer_token_embd.weight must be [" + std::to_string(d.ple_hd) + "] x rows");
+    int64_t need_rows = 0;
+    for (int i = 0; i < d.ple_heads; ++i) need_rows = std::max(need_rows, d.ple_off[i] + d.ple_size[i]);
+    if ((int64_t) t->ne[1] < need_rows)
+        FN_FAIL("load: per_layer_token_embd.weight has " + std::to_string(t->ne[1]) + " rows, the n-gram heads reach " +
+                std::to_string(need_rows));
+    if (load_qw1(m, "per_layer_token_embd.weight", t->ne[1], d.ple_hd, m.ple_table)) return -1;
+    for (int il : d.ple) {
+        MLayer &L = m.L[il];
+        L.ple = true;
+        const std::string p = "blk." + std::to_string(il) + ".";
+        if (load_qw1(m, p + "ple_key.weight", HCD, D, L.ple_key) || load_qw1(m, p + "ple_value.weight", D, D, L.ple_val) ||
+            load_f32(m, p + "ple_norm_key.weight", HCD, &L.ple_nk) ||
+            load_f32(m, p + "ple_norm_query.weight", HCD, &L.ple_nq) ||
+            load_f32(m, p + "ple_norm_conv.weight", HCD, &L.ple_nc) ||
+            load_f32(m, p + "ple_conv1d.weight", HCD * 4, &L.ple_conv) ||
+            m.alloc(&L.ple_hist, (size_t) PLE_HIST * HCD))
+            return -1;
+    }
+    for (int i = 0; i < 3; ++i) m.hsh.mult[i] = (unsigned long long) d.ple_mult[i];
+    for (int i = 0; i < d.ple_heads; ++i) {
+        m.hsh.size[i] = (unsigned long long) d.ple_size[i];
+        m.hsh.off[i] = (unsigned long long) d.ple_off[i];
+    }
+    const size_t T = MAXT;
+    return m.alloc(&m.ple_rows, T * d.ple_heads) || m.alloc(&m.ple_emb, T * D) || m.alloc(&m.ple_k, T * HCD) ||
+                   m.alloc(&m.ple_v, T * D) || m.alloc(&m.ple_gv, T * HCD) || m.alloc(&m.ple_gvn, T * HCD)
+               ? -1
+               : 0;
 }
 
 int load_model(Model &m, int max_ctx_req) {
@@ -448,6 +618,7 @@ int load_model(Model &m, int max_ctx_req) {
             return -1;
         if (L.eg.L.type != L.eu.L.type) FN_FAIL("load: " + p + " gate and up experts differ in type");
     }
+    if (d.ple_layers && load_ple(m)) return -1;
     // activations for MAXT tokens
     const size_t T = MAXT;
     const int ldr = d.HCR + d.HC;
@@ -463,7 +634,7 @@ int load_model(Model &m, int max_ctx_req) {
         m.alloc(&m.shu, T * d.FFS) || m.alloc(&m.sha, T * d.FFS) || m.alloc(&m.shd, T * D) ||
         m.alloc(&m.act, T * d.NEU * d.FFE) || m.alloc(&m.dpart, T * d.NEU * D) || m.alloc(&m.wsel, T * d.NEU) ||
         m.alloc(&m.logits, T * d.VOCAB) || m.alloc(&m.work, m.work_bytes / 4 + 1) || m.alloc(&m.ids, T) ||
-        m.alloc(&m.sel, T * d.NEU) || m.alloc(&m.pos, 1) || m.alloc(&m.am, T))
+        m.alloc(&m.sel, T * d.NEU) || m.alloc(&m.pos, 1) || m.alloc(&m.am, T) || m.alloc(&m.tok_all, m.max_ctx))
         return -1;
     FN_CK(hipDeviceSynchronize());
     return 0;
@@ -527,18 +698,44 @@ int ffn(Model &m, MLayer &L, int nt, const float *next_norm) {
     return 0;
 }
 
+// the n-gram embedding of a PLE layer added to the residual streams m.h (faie2fn.cu:2374-2381)
+int ple(Model &m, MLayer &L, int nt) {
+    const ModelDims &d = m.d;
+    const int HCD = d.HC * d.D;
+    hipLaunchKernelGGL(k_ple_ids, dim3(nt), dim3(64), 0, m.st, m.tok_all, m.pos, d.ple_heads, d.ple_eos, m.hsh,
+                       m.ple_rows);
+    FN_CK(hipGetLastError());
+    // ple_emb[t][hd * ple_hd + c] = table[row(t, hd)][c]: the gather is the embedding lookup of nt * heads rows
+    if (embed_launch(m.ple_table.L, m.ple_table.p, m.ple_rows, nt * d.ple_heads, 1, m.ple_emb, m.st) ||
+        gemv(L.ple_key, m.ple_emb, nt, m.ple_k, m.st) || gemv(L.ple_val, m.ple_emb, nt, m.ple_v, m.st))
+        return -1;
+    hipLaunchKernelGGL(k_ple_gate, dim3(nt, d.HC), dim3(256), 0, m.st, m.ple_k, m.ple_v, m.h, L.ple_nk, L.ple_nq,
+                       L.ple_nc, d.D, d.eps, m.ple_gv, m.ple_gvn);
+    hipLaunchKernelGGL(k_ple_conv, dim3((HCD + 255) / 256), dim3(256), 0, m.st, m.h, m.ple_gv, m.ple_gvn, L.ple_hist,
+                       L.ple_conv, HCD, nt);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
 int enqueue(Model &m, int nt) {
     const ModelDims &d = m.d;
     const size_t HCD = (size_t) d.HC * d.D;
+    if (d.ple_layers) {
+        hipLaunchKernelGGL(k_store_tokens, dim3(1), dim3(MAXT), 0, m.st, m.ids, m.tok_all, m.pos, nt, m.max_ctx);
+        FN_CK(hipGetLastError());
+    }
     if (embed_launch(m.tok.L, m.tok.p, m.ids, nt, d.HC, m.h, m.st)) return -1;
-    hipLaunchKernelGGL(k_groupnorm, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, m.L[0].hca_norm, d.D, d.eps, m.hn);
     for (int il = 0; il < d.NL; ++il) {
         MLayer &L = m.L[il];
+        if (L.ple && ple(m, L, nt)) return -1;
+        // layer 0 and a PLE layer normalize the streams for themselves; otherwise the previous write left m.hn
+        if (il == 0 || L.ple)
+            hipLaunchKernelGGL(k_groupnorm, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, L.hca_norm, d.D, d.eps, m.hn);
         if (hc_read(m, L.hca_dinj, L.hca_up, nt) || mixer(m, L, nt)) return -1;
         hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, m.y, m.inj, d.D, d.HC, nullptr, nullptr, 0,
                            nullptr, 0, L.hcf_norm, d.eps, m.hn);
         if (hc_read(m, L.hcf_dinj, L.hcf_up, nt)) return -1;
-        const float *next = il + 1 < d.NL ? m.L[il + 1].hca_norm : m.out_norm;
+        const float *next = il + 1 == d.NL ? m.out_norm : m.L[il + 1].ple ? nullptr : m.L[il + 1].hca_norm;
         if (ffn(m, L, nt, next)) return -1;
         if (m.dbg)
             FN_CK(hipMemcpyAsync(m.dbg + (size_t) il * nt * HCD, m.h, (size_t) nt * HCD * 4, hipMemcpyDeviceToHost,
@@ -582,9 +779,8 @@ int model_load(const char *shard1, const char *shard2, int max_ctx) {
     g_model.reset();
     auto m = std::make_unique<Model>();
     if (gguf_open(m->g, shard1) || read_dims(m->g, m->d)) return -1;
-    if (shard2 && *shard2 && std::string(shard2) != shard1)
-        FN_FAIL("load: a second shard holds only the PLE n-gram table, which this library does not build; pass the "
-                "model in one file");
+    // the second shard (the reference model keeps the n-gram table there): its tensors join the first's
+    if (shard2 && *shard2 && std::string(shard2) != shard1 && gguf_open(m->g2, shard2)) return -1;
     path_free();
     if (load_model(*m, max_ctx)) return -1;
     g_model = std::move(m);
@@ -635,6 +831,8 @@ int model_reset() {
             FN_CK(hipMemset(L.S, 0, (size_t) m.d.NVH * DSK * DSK * 4));
             FN_CK(hipMemset(L.ring, 0, (size_t) RING * m.d.CONVCH * 4));
         }
+    for (MLayer &L : m.L)
+        if (L.ple) FN_CK(hipMemset(L.ple_hist, 0, (size_t) PLE_HIST * m.d.HC * m.d.D * 4));
     FN_CK(hipMemset(m.pos, 0, 4));
     FN_CK(hipDeviceSynchronize());
     m.n_past = 0;

@@ -42,7 +42,7 @@ SYMBOLS = (
 
 # the shapes fn_model_dims writes, in order (include/faie2fn.h section 6)
 MODEL_DIMS = ("D", "NL", "NH", "NKV", "HD", "NROT", "NE", "NEU", "FFE", "FFS", "DS", "NKH", "NVH", "DINNER", "CONVCH",
-              "attn_every", "HC", "HCR", "IXH", "IXD", "top", "VOCAB")
+              "attn_every", "HC", "HCR", "IXH", "IXD", "top", "VOCAB", "PLE_LAYERS", "PLE_HEADS", "PLE_HD")
 
 # status bits of fn_dev_status (include/faie2fn.h)
 STATUS_POS, STATUS_KR = 1, 2

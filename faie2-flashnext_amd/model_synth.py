@@ -111,17 +111,26 @@ def random_weight(ty, rows, cols, rng, std=None):
 
 
 # the reference model's shapes (flashnext/inspect_fn.txt), and a small model of the same structure for tests
+# (PLE: the per-layer n-gram embedding of the layers in ple_layers; its hash constants and head sizes are the
+# reference model's, flashnext/inspect_fn.txt:37-45)
 REFERENCE_DIMS = dict(D=2560, NL=48, NH=24, NKV=2, NE=512, NEU=10, FFE=640, FFS=640, NKH=16, NVH=48, HC=4, HCR=320,
-                      top_k=2048, VOCAB=248320, attn_every=4)
+                      top_k=2048, VOCAB=248320, attn_every=4, ple_layers=[1], ple_heads_per_ngram=8, ple_hd=160,
+                      ple_eos=248044, ple_mult=[23703573157769, 20109073645365, 8052911324071],
+                      ple_sizes=[20000003, 20000023, 20000033, 20000047, 20000059, 20000063, 20000069, 20000077,
+                                 20000081, 20000093, 20000107, 20000147, 20000153, 20000159, 20000161, 20000171])
+# the tiny model's multipliers are large enough that the hash products wrap modulo 2^64, and its EOS is an ordinary
+# token id, so short random sequences cross it
 TINY_DIMS = dict(D=256, NL=4, NH=8, NKV=2, NE=8, NEU=2, FFE=64, FFS=64, NKH=2, NVH=4, HC=4, HCR=32, top_k=32, VOCAB=320,
-                 attn_every=4)
+                 attn_every=4, ple_layers=[1], ple_heads_per_ngram=4, ple_hd=32, ple_eos=7,
+                 ple_mult=[0x7F4A7C159E3779B9, 0x5851F42D4C957F2D, 0x14057B7EF767814F],
+                 ple_sizes=[97, 101, 103, 107, 109, 113, 127, 131])
 
-# weight formats of the reference model by tensor (flashnext/inspect_fn.txt:75-157): layer-dependent formats as
+# weight formats of the reference model by tensor (flashnext/inspect_fn.txt:75-164): layer-dependent formats as
 # tuples cycled over the layers (routed experts: IQ2_XS / IQ2_XXS / IQ2_S / IQ3_XXS gate and up, IQ4_NL / Q2_0 down)
 TYPES = dict(token_embd=IQ3_S, output=Q5_K, hc=BF16, attn_qkv=IQ4_XS, attn_gate=(IQ3_S, Q6_K), ssm_ab=BF16,
              ssm_out=Q8_0, attn_q=IQ4_XS, attn_k=IQ4_XS, attn_v=Q6_K, attn_output=Q8_0, indexer=BF16, router=BF16,
              shexp_gate=IQ4_XS, shexp_up=IQ3_S, shexp_down=Q8_0, exps_gate=(IQ2_XS, IQ2_XXS, IQ2_S, IQ3_XXS),
-             exps_up=(IQ2_XS, IQ2_XXS, IQ2_S, IQ3_XXS), exps_down=(IQ4_NL, Q2_0))
+             exps_up=(IQ2_XS, IQ2_XXS, IQ2_S, IQ3_XXS), exps_down=(IQ4_NL, Q2_0), ple=BF16, ple_table=IQ4_NL)
 
 
 def pick(ty, il):
@@ -151,6 +160,14 @@ def model_tensors(dims, seed=0, types=None):
           a + "hyper_connection.count": HC, a + "hyper_connection.low_rank": HCR,
           a + "attention.indexer.head_count": IXH, a + "attention.indexer.key_length": IXD,
           a + "attention.indexer.top_k": d["top_k"]}
+    ple = list(d.get("ple_layers", []))
+    if ple:
+        sizes = list(d["ple_sizes"])
+        offs = [int(v) for v in np.concatenate([[0], np.cumsum(sizes)[:-1]])]
+        kv.update({a + "ple.layers": ple, a + "ple.ngram_size": 3, a + "ple.heads_per_ngram": d["ple_heads_per_ngram"],
+                   a + "ple.conv_kernel": 4, a + "ple.eos_token_id": d["ple_eos"],
+                   a + "embedding_length_per_layer_input": d["ple_hd"], a + "ple.layer_multipliers": list(d["ple_mult"]),
+                   a + "ple.head_offsets": offs, a + "ple.head_vocab_sizes": sizes})
     ts = []
 
     def W(name, ty, rows, cols, n3=1, std=None):
@@ -195,6 +212,13 @@ def model_tensors(dims, seed=0, types=None):
             W(p + "indexer.k_proj.weight", T["indexer"], IXD, D)
             V_(p + "indexer.q_norm.weight", IXD, 1.0, 0.1)
             V_(p + "indexer.k_norm.weight", IXD, 1.0, 0.1)
+        if il in ple:
+            W(p + "ple_key.weight", T["ple"], HCD, D)
+            W(p + "ple_value.weight", T["ple"], D, D)
+            for nm in ("key", "query", "conv"):
+                V_(p + f"ple_norm_{nm}.weight", HCD, 1.0, 0.1)
+            ts.append((p + "ple_conv1d.weight", F16, [4, HCD],
+                       rng.normal(0.0, 0.3, HCD * 4).astype(np.float16).tobytes()))
         W(p + "ffn_gate_inp.weight", T["router"], NE, D, std=2.0 / np.sqrt(D))
         ts.append((p + "ffn_gate_inp_shexp.weight", T["router"], [D],
                    random_weight(T["router"], 1, D, rng)))
@@ -204,11 +228,19 @@ def model_tensors(dims, seed=0, types=None):
         W(p + "ffn_gate_exps.weight", pick(T["exps_gate"], il), FFE, D, NE)
         W(p + "ffn_up_exps.weight", pick(T["exps_up"], il), FFE, D, NE)
         W(p + "ffn_down_exps.weight", pick(T["exps_down"], il), D, FFE, NE)
+    if ple:
+        W("per_layer_token_embd.weight", T["ple_table"], sum(d["ple_sizes"]), d["ple_hd"], std=1.0)
     return kv, ts
 
 
-def write_model(path, dims=None, seed=0, types=None):
-    """Write a synthetic model GGUF; returns (metadata, tensors) as written."""
+def write_model(path, dims=None, seed=0, types=None, shard2=None):
+    """Write a synthetic model GGUF; returns (metadata, tensors) as written.  With shard2, the n-gram table goes to
+    that second file instead (as in the reference model's two shards)."""
     kv, ts = model_tensors(dims or TINY_DIMS, seed, types)
-    write_gguf(path, kv, ts)
+    if shard2:
+        table = [t for t in ts if t[0] == "per_layer_token_embd.weight"]
+        write_gguf(path, kv, [t for t in ts if t[0] != "per_layer_token_embd.weight"])
+        write_gguf(shard2, {"general.architecture": kv["general.architecture"]}, table)
+    else:
+        write_gguf(path, kv, ts)
     return kv, ts

@@ -32,8 +32,9 @@ extern "C" {
  * ====================================================================================================== */
 const char *fn_error(void);                                                   /* faie2fn.cu:2495 */
 void fn_free(void);                                                           /* faie2fn.cu:2497 */
-/* One GPU: the whole model in shard1 (shard2 NULL, "" or the same file; a second shard holds only the PLE n-gram
- * table, which is not built); split is ignored (every layer on device 0, fn_split() then returns the layer count). */
+/* One GPU: the model in shard1, and shard2 (NULL, "" or the same file when there is none) whose tensors join
+ * shard1's (the reference model keeps the PLE n-gram table there); split is ignored (every layer on device 0,
+ * fn_split() then returns the layer count). */
 int fn_load(const char *shard1, const char *shard2, int max_ctx, int split);  /* faie2fn.cu:2524 */
 int fn_split(void);                                                           /* faie2fn.cu:2698 */
 double fn_dev_gb(int dv);                                                     /* faie2fn.cu:2699 */
@@ -315,13 +316,18 @@ int fn_gemv_dev(uint32_t type, const uint8_t *packed, int rows, int cols, const 
  *    embedding; head_dim 256, DeltaNet head dim 128, conv kernel 4 and the indexer's 4 x 128 are the built sizes.
  *    Tensor names are the reference's (token_embd, output, output_hc_*, blk.N.{hc_attn_*, hc_ffn_*, attn_qkv,
  *    attn_gate, ssm_*, attn_q/k/v/output, attn_q_norm/k_norm, indexer.*, ffn_gate_inp(_shexp), ffn_*_shexp,
- *    ffn_*_exps}); weights in the formats of section 5, norms and conv weights F32.
+ *    ffn_*_exps}); weights in the formats of section 5, norms and conv weights F32 or F16.  The layers listed in
+ *    <arch>.ple.layers add the per-layer n-gram embedding first: blk.N.{ple_key, ple_value, ple_norm_key,
+ *    ple_norm_query, ple_norm_conv, ple_conv1d} and the table per_layer_token_embd ([ple values per head] x rows,
+ *    packed whole into HBM), hashed by ple.{heads_per_ngram, eos_token_id, layer_multipliers, head_offsets,
+ *    head_vocab_sizes} and embedding_length_per_layer_input; n-grams of 3 and conv kernel 4 are the built sizes.
  * ====================================================================================================== */
 
 /* Parse a GGUF file (no device work) and write its model shapes to out[0..n): {D, layers, q heads, kv heads,
  * head dim, rope dims, experts, experts used, expert ffn, shared ffn, ssm state, ssm groups, ssm value heads,
  * ssm inner, conv channels, attention interval, hyper-connections, hc low rank, indexer heads, indexer dim,
- * indexer top blocks, vocabulary}.  Returns the number of values (22) or -1 (fn_error: what is wrong or missing). */
+ * indexer top blocks, vocabulary, PLE layers, PLE heads, PLE values per head}.  Returns the number of values (25)
+ * or -1 (fn_error: what is wrong or missing). */
 int fn_model_dims(const char *path, int *out, int n);
 
 #ifdef __cplusplus

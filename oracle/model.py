@@ -15,7 +15,11 @@ the reference kernel it restates:
   renormalized over them; the shared expert's SwiGLU (k_route, :1747-1798);
 * routed experts: silu(gate_e . x) * (up_e . x) (k_tmoe_gu, :1047-1079), down_e . act (k_tmoe_down, :1159-1183);
 * final read without inject, LM head, argmax with ties to the lowest index (enqueue_dev1, :2441-2447; k_argmax,
-  :1910-1934).
+  :1910-1934);
+* per-layer n-gram embedding of the layers in ple.layers, before their first read (layer_forward, :2374-2381): the
+  table rows of each head from the 64-bit hash of the bigram / trigram context (k_ple_ids, :1810-1823, contexts cut
+  at EOS), the key and value products of the gathered rows, the per-stream gate (k_ple_gate, :1843-1875) and the
+  dilated causal conv with its 9-deep history (k_ple_conv, :1878-1896); such a layer normalizes its streams itself.
 
 Arithmetic is float64 throughout; the path kernels' inputs pass through float32 where the GPU's do (their oracle
 functions take float32 arrays), which keeps every comparison on the GPU's own input precision.
@@ -57,6 +61,11 @@ class Model:
         self.t = {name: (ty, dims, raw) for name, ty, dims, raw in tensors}
         self.VOCAB = self.t["token_embd.weight"][1][1]
         self.C = 2 * self.NKH * DS + self.NVH * DS
+        self.ple_layers = list(g("ple.layers", []))
+        if self.ple_layers:
+            self.ple_heads, self.ple_hd = 2 * g("ple.heads_per_ngram"), g("embedding_length_per_layer_input")
+            self.ple_eos, self.ple_mult = g("ple.eos_token_id"), list(g("ple.layer_multipliers"))
+            self.ple_off, self.ple_size = list(g("ple.head_offsets")), list(g("ple.head_vocab_sizes"))
         self._w = {}
         self.reset()
 
@@ -84,6 +93,8 @@ class Model:
     # ---- state ----
     def reset(self):
         self.pos = 0
+        self.toks = []
+        self.ple_hist = {il: np.zeros((9, self.HC * self.D)) for il in self.ple_layers}
         self.S, self.conv, self.K, self.V, self.IK, self.BK = {}, {}, {}, {}, {}, {}
         for il in range(self.NL):
             if self.is_attn(il):
@@ -178,16 +189,80 @@ class Model:
         y += _sig(rsg[:, self.NE:self.NE + 1]) * shd
         return y, sel
 
+    # ---- per-layer n-gram embedding ----
+    def ple_rows(self, p):
+        """table rows of the n-gram heads at position p: mixed = t0 m0 ^ p1 m1 (^ p2 m2 for the trigram half), every
+        product of the ids widened with their sign and taken modulo 2^64; row = mixed mod size + offset"""
+        M = (1 << 64) - 1
+        tok, eos = self.toks, self.ple_eos
+        t0 = tok[p]
+        p1 = tok[p - 1] if p >= 1 else eos
+        p2 = tok[p - 2] if (p >= 2 and p1 != eos) else eos
+        m0, m1, m2 = self.ple_mult
+        rows = []
+        for hd in range(self.ple_heads):
+            mixed = ((t0 * m0) & M) ^ ((p1 * m1) & M)
+            if hd >= self.ple_heads // 2:
+                mixed ^= (p2 * m2) & M
+            rows.append(mixed % self.ple_size[hd] + self.ple_off[hd])
+        return rows
+
+    def ple_gate(self, key, val, h, wk, wq, wc):
+        """(gv, gvn) [nt][HC D] from key [nt][HC D], val [nt][D] and the streams h [nt][HC D]"""
+        nt, HC, D = h.shape[0], self.HC, self.D
+        rms = lambda x: x / np.sqrt((x * x).mean(-1, keepdims=True) + self.eps)  # noqa: E731
+        kn = rms(key.reshape(nt, HC, D)) * wk.reshape(HC, D)
+        qn = rms(h.reshape(nt, HC, D)) * wq.reshape(HC, D)
+        gate = (kn * qn).sum(-1) / np.sqrt(D)                                       # [nt][HC]
+        gate = np.where(gate == 0.0, 0.0, np.sign(gate) * np.sqrt(np.maximum(np.abs(gate), 1e-6)))
+        gv = _sig(gate)[:, :, None] * val[:, None, :]
+        gvn = rms(gv) * wc.reshape(HC, D)
+        return gv.reshape(nt, -1), gvn.reshape(nt, -1)
+
+    def ple_conv(self, il, gv, gvn, w):
+        """h increment gv + silu(w0 x[t-9] + w1 x[t-6] + w2 x[t-3] + w3 x[t]) over x = history ++ gvn; w [HC D][4]"""
+        nt = gv.shape[0]
+        x = np.concatenate([self.ple_hist[il], gvn])
+        out = np.zeros_like(gv)
+        for t in range(nt):
+            i = 9 + t
+            sv = w[:, 0] * x[i - 9] + w[:, 1] * x[i - 6] + w[:, 2] * x[i - 3] + w[:, 3] * x[i]
+            out[t] = gv[t] + _silu(sv)
+        self.ple_hist[il] = x[nt:nt + 9].copy()
+        return out
+
+    def ple(self, il, h, nt):
+        p = f"blk.{il}."
+        rows = [self.ple_rows(self.pos + t) for t in range(nt)]
+        table = self.ple_table()
+        emb = np.stack([np.concatenate([table[r] for r in rr]) for rr in rows])      # [nt][D]
+        key = emb @ self.w(p + "ple_key.weight").T
+        val = emb @ self.w(p + "ple_value.weight").T
+        gv, gvn = self.ple_gate(key, val, h, self.f32(p + "ple_norm_key.weight"), self.f32(p + "ple_norm_query.weight"),
+                                self.f32(p + "ple_norm_conv.weight"))
+        w = self.f16(p + "ple_conv1d.weight").reshape(self.HC * self.D, 4)
+        return h + self.ple_conv(il, gv, gvn, w)
+
+    def ple_table(self):
+        return self.w("per_layer_token_embd.weight")
+
+    def f16(self, name):
+        ty, _, raw = self.t[name]
+        return (np.frombuffer(raw, np.float16) if ty == 1 else np.frombuffer(raw, np.float32)).astype(np.float64)
+
     # ---- forward ----
     def forward(self, ids):
         """logits [nt][VOCAB] float64, argmax [nt], h after every layer [NL][nt][HC D], routed experts per layer"""
         ids = np.asarray(ids)
         nt = len(ids)
+        self.toks[self.pos:self.pos + nt] = [int(i) for i in ids]
         emb = self.w("token_embd.weight")[ids]
         h = np.tile(emb, (1, self.HC))
         hs, sels = [], []
         for il in range(self.NL):
             p = f"blk.{il}."
+            if il in self.ple_layers:
+                h = self.ple(il, h, nt)
             hn = self.groupnorm(h, self.f32(p + "hc_attn_norm.weight"))
             x, inj = self.hc_read(hn, p + "hc_attn_down.weight", p + "hc_attn_up.weight", p + "hc_attn_inject.weight")
             y = self.mixer(il, x)

@@ -4,7 +4,9 @@ metadata, weight formats; small dimensions), then fn_forward over a token sequen
 normwise, the argmax token equal wherever the oracle's top two logits are apart.
 
 The sequence runs past the indexer's threshold (top 8 blocks of 4 keys), so the attention layer switches from dense
-to sparse inside it; calls take 1 to 8 tokens.  Every case prints what names it before the GPU calls.
+to sparse inside it; calls take 1 to 8 tokens.  Layer 1 carries the per-layer n-gram embedding (as in the reference
+model), and the sequence holds EOS tokens, which cut the n-gram contexts.  Every case prints what names it before
+the GPU calls.
 """
 
 import numpy as np
@@ -74,6 +76,7 @@ def test_model_forward_matches_oracle(fnlib, model_file):
         assert fnlib.d.fn_split() == ms.TINY_DIMS["NL"] and fnlib.d.fn_dev_gb(0) > 0
         ref = om.Model(kv, ts, max_ctx=256)
         ids = np.random.default_rng(2).integers(0, ms.TINY_DIMS["VOCAB"], size=sum(CHUNKS))
+        ids[[0, 9, 10, 33, 60]] = ms.TINY_DIMS["ple_eos"]
         _run(fnlib, ref, ids, debug=True)
         assert fnlib.d.fn_n_past() == sum(CHUNKS)
     finally:
@@ -116,4 +119,39 @@ def test_model_errors(fnlib, model_file):
             fnlib.forward([1])
     finally:
         fnlib.free()
+    assert fnlib.d.fn_n_past() == -1
+
+
+def test_model_two_shards_equal_one_file(fnlib, model_file, tmp_path):
+    """The n-gram table in a second file (the reference model's layout) gives the same bits as one file."""
+    path, kv, ts = model_file
+    s1, s2 = str(tmp_path / "s1.gguf"), str(tmp_path / "s2.gguf")
+    ms.write_model(s1, ms.TINY_DIMS, seed=11, shard2=s2)
+    ids = np.random.default_rng(5).integers(0, ms.TINY_DIMS["VOCAB"], size=16)
+    out = []
+    for a, b in ((path, ""), (s1, s2)):
+        _say(f"model forward: shards {a!r} {b!r}")
+        fnlib.load(a, b, max_ctx=256)
+        try:
+            out.append(np.concatenate([fnlib.forward(ids[k:k + 4], logits=True)[1] for k in range(0, 16, 4)]))
+        finally:
+            fnlib.free()
+    assert np.array_equal(out[0], out[1])
+
+
+def test_model_ple_load_checks(fnlib, tmp_path):
+    """A table with fewer rows than the n-gram heads address, and a second shard that is missing, fail the load."""
+    kv, ts = ms.model_tensors(ms.TINY_DIMS, seed=3)
+    T = ms.TINY_DIMS
+    short = sum(T["ple_sizes"]) - 1
+    ts2 = [t if t[0] != "per_layer_token_embd.weight" else
+           (t[0], t[1], [T["ple_hd"], short], t[3][: short * T["ple_hd"] // 32 * 18]) for t in ts]
+    p = str(tmp_path / "short.gguf")
+    ms.write_gguf(p, kv, ts2)
+    _say("model load: short n-gram table")
+    with pytest.raises(RuntimeError, match="n-gram heads reach"):
+        fnlib.load(p, "", max_ctx=256)
+    _say("model load: missing second shard")
+    with pytest.raises(RuntimeError, match="cannot open"):
+        fnlib.load(p, str(tmp_path / "absent.gguf"), max_ctx=256)
     assert fnlib.d.fn_n_past() == -1

@@ -37,6 +37,20 @@ def test_reader_reads_the_written_shapes(fnlib, tiny):
     assert d["DINNER"] == T["NVH"] * 128 and d["CONVCH"] == 2 * T["NKH"] * 128 + T["NVH"] * 128
 
 
+def test_reader_reads_ple_and_two_shards(fnlib, tmp_path):
+    """The PLE shapes come from the metadata; a model whose table sits in a second file reads the same from the
+    first (the reference model's shard layout)."""
+    a, b, c = str(tmp_path / "one.gguf"), str(tmp_path / "s1.gguf"), str(tmp_path / "s2.gguf")
+    ms.write_model(a, ms.TINY_DIMS, seed=1)
+    ms.write_model(b, ms.TINY_DIMS, seed=1, shard2=c)
+    d = fnlib.model_dims(a)
+    T = ms.TINY_DIMS
+    assert (d["PLE_LAYERS"], d["PLE_HEADS"], d["PLE_HD"]) == (1, 2 * T["ple_heads_per_ngram"], T["ple_hd"])
+    assert fnlib.model_dims(b) == d
+    r = ms.REFERENCE_DIMS
+    assert 2 * r["ple_heads_per_ngram"] * r["ple_hd"] == r["D"] and len(r["ple_sizes"]) == 2 * r["ple_heads_per_ngram"]
+
+
 def test_reader_alignment_and_version(fnlib, tmp_path):
     """A GGUF v2 file and one with general.alignment = 64 parse to the same shapes."""
     kv, ts = ms.model_tensors(ms.TINY_DIMS, seed=1)
@@ -79,7 +93,15 @@ def test_reader_rejects_unbuilt_shapes(fnlib, tmp_path):
     ms.write_gguf(p, k2, ts)
     assert "4, 8 or 12" in _err(fnlib, p)
     k2 = dict(kv)
-    k2["qwen4exp.ple.layers"] = [1]
+    k2["qwen4exp.ple.head_vocab_sizes"] = [97] * 7                 # one size short of the 8 heads
+    ms.write_gguf(p, k2, ts)
+    assert "PLE" in _err(fnlib, p)
+    k2 = dict(kv)
+    k2["qwen4exp.embedding_length_per_layer_input"] = 48           # 8 heads x 48 != D
+    ms.write_gguf(p, k2, ts)
+    assert "PLE" in _err(fnlib, p)
+    k2 = dict(kv)
+    k2["qwen4exp.ple.layers"] = [4]                                # layer outside the model
     ms.write_gguf(p, k2, ts)
     assert "PLE" in _err(fnlib, p)
     k2 = dict(kv)
@@ -181,4 +203,99 @@ def test_oracle_forward_runs_and_is_deterministic(oracle_model):
     l2, a2, h2, _ = m.forward([3, 17, 250])
     assert np.array_equal(l1, l2) and np.array_equal(a1, a2) and np.isfinite(l1).all()
     assert h1.shape == (m.NL, 3, m.HC * m.D)
+    m.reset()
+
+
+# ---- per-layer n-gram embedding pins ----
+
+
+def test_ple_hash_matches_uint64_arithmetic(oracle_model):
+    """The rows of every head equal the hash in numpy's wrapping uint64 arithmetic (ids widened with their sign),
+    an independent statement of the reference's unsigned long long products (k_ple_ids, faie2fn.cu:1810-1823); the
+    tiny model's multipliers make every product wrap."""
+    m = oracle_model
+    m.reset()
+    rng = np.random.default_rng(8)
+    m.toks = [int(v) for v in rng.integers(0, m.VOCAB, 40)]
+    m.toks[10] = m.ple_eos
+    mult = np.array(m.ple_mult, np.uint64)
+    assert all(int(v) * 300 >= 1 << 64 for v in m.ple_mult)
+    H = m.ple_heads
+    with np.errstate(over="ignore"):
+        for p in range(40):
+            tok = np.array(m.toks, np.int64).view(np.uint64)
+            eos = np.array([m.ple_eos], np.int64).view(np.uint64)[0]
+            p1 = tok[p - 1] if p >= 1 else eos
+            p2 = tok[p - 2] if p >= 2 and p1 != eos else eos
+            big = (tok[p] * mult[0]) ^ (p1 * mult[1])
+            tri = big ^ (p2 * mult[2])
+            want = [int((big if hd < H // 2 else tri) % np.uint64(m.ple_size[hd])) + m.ple_off[hd] for hd in range(H)]
+            assert m.ple_rows(p) == want, p
+    m.reset()
+
+
+def test_ple_hash_context_rules(oracle_model):
+    """Bigram heads never see the token two back; trigram heads see it unless the previous token is EOS; the first
+    position's context is EOS (k_ple_ids, faie2fn.cu:1817-1821)."""
+    m = oracle_model
+    H = m.ple_heads
+    m.toks = [5, 9, 11]
+    r = m.ple_rows(2)
+    m.toks = [6, 9, 11]
+    r2 = m.ple_rows(2)
+    assert r[: H // 2] == r2[: H // 2] and r[H // 2:] != r2[H // 2:]
+    m.toks = [5, m.ple_eos, 11]
+    r = m.ple_rows(2)
+    m.toks = [6, m.ple_eos, 11]
+    assert m.ple_rows(2) == r
+    m.toks = [m.ple_eos, m.ple_eos, 11]
+    assert m.ple_rows(2) == r                    # the cut context reads EOS, whatever sits before it
+    m.toks = [11]
+    assert m.ple_rows(0) == r                    # position 0: previous token and the one before are EOS
+    m.reset()
+
+
+def test_ple_gate_closed_forms(oracle_model):
+    """key = h with unit norm weights: gate = sqrt(sqrt(D) ms / (ms + eps)) per stream (ms the stream's mean
+    square); key = -h gives the negative root; key = 0 gives gate 0, sigmoid 1/2; gvn = RMSNorm of the scaled value
+    (k_ple_gate, faie2fn.cu:1843-1875)."""
+    m = oracle_model
+    HC, D = m.HC, m.D
+    rng = np.random.default_rng(9)
+    h = rng.standard_normal((2, HC * D)) * np.repeat(np.array([0.5, 1.0, 2.0, 3.0]), D)
+    val = rng.standard_normal((2, D))
+    one = np.ones(HC * D)
+    ms_ = (h.reshape(2, HC, D) ** 2).mean(-1)
+    for sgn in (1.0, -1.0):
+        gv, gvn = m.ple_gate(sgn * h, val, h, one, one, one)
+        gate = sgn * np.sqrt(np.sqrt(D) * ms_ / (ms_ + m.eps))
+        sg = 1 / (1 + np.exp(-gate))
+        want = sg[:, :, None] * val[:, None, :]
+        assert np.allclose(gv.reshape(2, HC, D), want, rtol=1e-13, atol=0)
+        msv = (want ** 2).mean(-1, keepdims=True)
+        assert np.allclose(gvn.reshape(2, HC, D), want / np.sqrt(msv + m.eps), rtol=1e-13, atol=0)
+    gv, _ = m.ple_gate(np.zeros_like(h), val, h, one, one, one)
+    assert np.array_equal(gv.reshape(2, HC, D), np.broadcast_to(0.5 * val[:, None, :], (2, HC, D)))
+
+
+def test_ple_conv_taps_and_history(oracle_model):
+    """Weights (0,0,0,1) read the current value, (1,0,0,0) the value 9 steps back, (0,1,0,0) 6 back, (0,0,1,0)
+    3 back; the history afterwards is the last 9 inputs (k_ple_conv, faie2fn.cu:1878-1896)."""
+    m = oracle_model
+    n = m.HC * m.D
+    il = m.ple_layers[0]
+    rng = np.random.default_rng(10)
+    hist = rng.standard_normal((9, n))
+    gvn = rng.standard_normal((5, n))
+    gv = rng.standard_normal((5, n))
+    x = np.concatenate([hist, gvn])
+    silu = lambda v: v / (1 + np.exp(-v))  # noqa: E731
+    for tap, back in ((3, 0), (2, 3), (1, 6), (0, 9)):
+        w = np.zeros((n, 4))
+        w[:, tap] = 1.0
+        m.ple_hist[il] = hist.copy()
+        out = m.ple_conv(il, gv, gvn, w)
+        want = gv + silu(np.stack([x[9 + t - back] for t in range(5)]))
+        assert np.allclose(out, want, rtol=1e-14, atol=1e-15), tap
+        assert np.array_equal(m.ple_hist[il], x[5:14])
     m.reset()
