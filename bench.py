@@ -418,6 +418,61 @@ def hybrid_verify(lib, stream, steps, warmup, B=16, ctx=32768, nt=4, kr=2, nl=48
     return ms, nbytes
 
 
+def model_decode(lib, nl=8, ctx=4096, tokens=64, seed=0):
+    """fn_load + fn_forward on a synthetic model of the reference model's dimensions and weight formats with nl layers
+    (PLE at layer 1; the n-gram table's head sizes 1/100 of the reference's, which changes only the table's size:
+    16 rows are gathered per token either way).  Greedy-decode latency per fn_forward call (tokens in, argmax out,
+    host-synchronous, as the reference's 5.70 ms per forward is quoted) at nt = 1 and nt = 8, after a warm-up."""
+    import model_synth as ms
+    dims = dict(ms.REFERENCE_DIMS, NL=nl, ple_sizes=[v // 100 for v in ms.REFERENCE_DIMS["ple_sizes"]])
+    d = "/dev/shm" if os.path.isdir("/dev/shm") else os.environ.get("TMPDIR", "/tmp")
+    path = os.path.join(d, f"fn_bench_model_{os.getpid()}.gguf")
+    t0 = time.perf_counter()
+    kv, ts = ms.model_tensors(dims, seed, fast=True)
+    log(f"[bench] model: {nl} layers generated in {time.perf_counter() - t0:.1f} s")
+    ms.write_gguf(path, kv, ts)
+    sizes = {name: len(raw) for name, _, _, raw in ts}
+    del ts
+    log(f"[bench] model: written ({os.path.getsize(path) / 1e9:.2f} GB) in {time.perf_counter() - t0:.1f} s")
+    try:
+        t1 = time.perf_counter()
+        lib.load(path, "", max_ctx=ctx)
+        log(f"[bench] model: loaded in {time.perf_counter() - t1:.1f} s, {lib.d.fn_dev_gb(0):.2f} GB on the device")
+    finally:
+        os.remove(path)
+    # bytes one token reads: every weight but the routed experts, the embedding and the table (one row each); the
+    # routed experts NEU / NE of theirs; the DeltaNet states read and written
+    R = ms.REFERENCE_DIMS
+    exps = sum(v for k, v in sizes.items() if "_exps." in k)
+    dense = sum(v for k, v in sizes.items() if "_exps." not in k and k not in
+                ("token_embd.weight", "per_layer_token_embd.weight"))
+    n_dn = sum(1 for il in range(nl) if (il + 1) % R["attn_every"])
+    state = n_dn * 2 * R["NVH"] * 128 * 128 * 4
+    per_token = dense + exps * R["NEU"] // R["NE"] + state
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(0, R["VOCAB"], size=tokens + 8 * tokens).astype(np.int32)
+    out = {"layers": nl, "ctx": ctx, "weight_gb_on_device": round(lib.d.fn_dev_gb(0), 2),
+           "bytes_per_token_nt1": per_token}
+    try:
+        for nt in (1, 8):
+            lib.reset()
+            for i in range(4):                                     # warm-up: captures the graph for nt
+                lib.forward(ids[i * nt:(i + 1) * nt])
+            lib.reset()
+            t1 = time.perf_counter()
+            for i in range(tokens // nt if nt > 1 else tokens):
+                lib.forward(ids[i * nt:(i + 1) * nt])
+            calls = tokens // nt if nt > 1 else tokens
+            ms_call = (time.perf_counter() - t1) * 1e3 / calls
+            out[f"nt{nt}"] = {"ms_per_forward": round(ms_call, 4), "tokens_per_s": round(nt * 1e3 / ms_call, 1),
+                              "us_per_layer": round(ms_call * 1e3 / nl, 2)}
+            log(f"[bench] model nt={nt}: {ms_call:.3f} ms per forward, {nt * 1e3 / ms_call:.1f} tokens/s")
+        out["nt1"]["gbs"] = round(per_token / (out["nt1"]["ms_per_forward"] * 1e-3) / 1e9, 1)
+    finally:
+        lib.free()
+    return out
+
+
 def time_graph(stream, fn_launch, steps, warmup):
     """Capture fn_launch into a hipGraph, replay warmup times, then time `steps` replays with HIP events recorded
     on the same stream.  Returns ms per replay."""
@@ -516,6 +571,9 @@ def main():
                          "(k_attn_split<8, PREP> + k_attn_combine)")
     ap.add_argument("--attn-only", action="store_true",
                     help="of the extra legs run only the dense GQA decode ones (config 3, one new token)")
+    ap.add_argument("--model", type=int, default=0, metavar="LAYERS",
+                    help="only the whole-model leg: fn_load + fn_forward greedy decode of a synthetic model of the "
+                         "reference's dimensions and formats with LAYERS layers")
     ap.add_argument("--counters-attn", action="store_true",
                     help="counter-collection workload only: 5 eager multi-token GQA layer-steps at B=16, 32K context, "
                          "nt=8 then 5 at nt=4 (k_attn_split_mt<2>)")
@@ -529,6 +587,10 @@ def main():
         raise RuntimeError("no HIP device visible")
     stream = hiprt.Stream()
     steps, warmup = max(1, args.steps), max(0, args.warmup)
+    if args.model:
+        res = model_decode(lib, nl=args.model)
+        print(json.dumps({"model_decode": res}), flush=True)
+        return
     if args.gemv:
         res = gemv_extras(lib)
         for k, v in res.items():

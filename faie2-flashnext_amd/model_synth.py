@@ -87,7 +87,21 @@ _RMS = {Q8_0: 73.9, IQ4_NL: 67.4, IQ4_XS: 67.4 * 18.5, IQ3_S: 18.5 * 7.6, Q6_K: 
         Q5_K: 36.5 * 18.0, IQ2_XXS: 53.4, IQ2_XS: 55.8, IQ2_S: 56.7, IQ3_XXS: 141.4, Q2_0: 1.225}
 
 
-def random_weight(ty, rows, cols, rng, std=None):
+def _code_bytes(n, rng, pool):
+    """n uniformly random bytes, or (with a pool) n bytes of the pool repeated from a random start: as random-looking
+    to a decoder and written at copy speed, for benchmark models of tens of GB"""
+    if pool is None:
+        return rng.integers(0, 256, size=n, dtype=np.uint8)
+    out = np.empty(n, np.uint8)
+    i, pos = 0, int(rng.integers(0, len(pool)))
+    while i < n:
+        k = min(n - i, len(pool) - pos)
+        out[i:i + k] = pool[pos:pos + k]
+        i, pos = i + k, 0
+    return out
+
+
+def random_weight(ty, rows, cols, rng, std=None, pool=None):
     """Raw GGUF bytes of a rows x cols weight of type ty with values of spread ~ std (default 1 / sqrt(cols)): normal
     values for the float types; for the block formats random code bytes with every fp16 scale field set to the one
     value that gives that spread."""
@@ -101,13 +115,13 @@ def random_weight(ty, rows, cols, rng, std=None):
         u = v.view(np.uint32).astype(np.uint64)
         return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16).tobytes()
     qk, bb = BLOCK[ty]
-    raw = rng.integers(0, 256, size=rows * (cols // qk) * bb, dtype=np.uint8)
+    raw = _code_bytes(rows * (cols // qk) * bb, rng, pool)
     blk = raw.reshape(-1, bb)
     bits = np.frombuffer(_f16_bits(std / _RMS[ty]).tobytes(), np.uint8)
     for o in SCALES[ty]:
         blk[:, o] = bits[0]
         blk[:, o + 1] = bits[1]
-    return raw.tobytes()
+    return raw if pool is not None else raw.tobytes()  # (a uint8 array serves the writer as well as bytes)
 
 
 # the reference model's shapes (flashnext/inspect_fn.txt), and a small model of the same structure for tests
@@ -138,10 +152,12 @@ def pick(ty, il):
     return ty[il % len(ty)] if isinstance(ty, tuple) else ty
 
 
-def model_tensors(dims, seed=0, types=None):
-    """(metadata, tensors) of a synthetic model with the reference's tensor names and layouts."""
+def model_tensors(dims, seed=0, types=None, fast=False):
+    """(metadata, tensors) of a synthetic model with the reference's tensor names and layouts.  fast: block-format
+    code bytes come from a repeated 64 MiB random pool (benchmark models)."""
     T = dict(TYPES, **(types or {}))
     rng = np.random.default_rng(seed)
+    pool = rng.integers(0, 256, size=64 << 20, dtype=np.uint8) if fast else None
     d = dict(dims)
     D, NL, NH, NKV, NE, NEU = d["D"], d["NL"], d["NH"], d["NKV"], d["NE"], d["NEU"]
     FFE, FFS, NKH, NVH, HC, HCR, V = d["FFE"], d["FFS"], d["NKH"], d["NVH"], d["HC"], d["HCR"], d["VOCAB"]
@@ -171,7 +187,7 @@ def model_tensors(dims, seed=0, types=None):
     ts = []
 
     def W(name, ty, rows, cols, n3=1, std=None):
-        raw = random_weight(ty, rows * n3, cols, rng, std)
+        raw = random_weight(ty, rows * n3, cols, rng, std, pool)
         dims_ = [cols, rows] + ([n3] if n3 > 1 else [])
         ts.append((name, ty, dims_, raw))
 
@@ -233,10 +249,10 @@ def model_tensors(dims, seed=0, types=None):
     return kv, ts
 
 
-def write_model(path, dims=None, seed=0, types=None, shard2=None):
+def write_model(path, dims=None, seed=0, types=None, shard2=None, fast=False):
     """Write a synthetic model GGUF; returns (metadata, tensors) as written.  With shard2, the n-gram table goes to
     that second file instead (as in the reference model's two shards)."""
-    kv, ts = model_tensors(dims or TINY_DIMS, seed, types)
+    kv, ts = model_tensors(dims or TINY_DIMS, seed, types, fast)
     if shard2:
         table = [t for t in ts if t[0] == "per_layer_token_embd.weight"]
         write_gguf(path, kv, [t for t in ts if t[0] != "per_layer_token_embd.weight"])
