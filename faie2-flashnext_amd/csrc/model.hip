@@ -43,6 +43,7 @@ constexpr int IXH = 4, IXD = 128, IXR = 4;   // indexer heads, head dim, keys pe
 constexpr int RING = 16;                     // conv ring slots (>= MAXT + 3, a power of two)
 constexpr int PLE_HIST = 9;                  // PLE conv history: (kernel 4 - 1) x dilation 3 (faie2fn.cu:66)
 constexpr int PLE_MAXH = 64;                 // n-gram heads the hashing kernel takes
+constexpr int HC_KS = 8;                     // split of the hyper-connection down product along its rows
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
@@ -81,16 +82,27 @@ __global__ void __launch_bounds__(256) k_groupnorm(const float *__restrict__ h, 
     }
 }
 
-// t[t][r] = silu(lr[t][r] / HC) for r < HCR (faie2fn.cu:1266-1273); the inject logits stay in lr.  grid nt, 256 thr
-__global__ void k_hc_lowrank(const float *__restrict__ lr, int ldr, int HCR, int HC, float *__restrict__ t320) {
+// sum of the ks split-K partials of the down (+ inject) product, in split order: part[k][t][r], ldr values a token
+__device__ __forceinline__ float lr_sum(const float *__restrict__ part, int ks, int nt, int ldr, int t, int r) {
+    float v = part[(size_t) t * ldr + r];
+    for (int k = 1; k < ks; ++k) v += part[((size_t) k * nt + t) * ldr + r];
+    return v;
+}
+
+// t[t][r] = silu(lr[t][r] / HC) for r < HCR (faie2fn.cu:1266-1273), lr the sum of the ks partials; the inject
+// logits stay in the partials.  grid nt, 256 threads
+__global__ void k_hc_lowrank(const float *__restrict__ lr, int ks, int nt, int ldr, int HCR, int HC,
+                             float *__restrict__ t320) {
     const int t = blockIdx.x;
-    for (int r = threadIdx.x; r < HCR; r += blockDim.x) t320[(size_t) t * HCR + r] = silu(lr[(size_t) t * ldr + r] * (1.0f / HC));
+    for (int r = threadIdx.x; r < HCR; r += blockDim.x)
+        t320[(size_t) t * HCR + r] = silu(lr_sum(lr, ks, nt, ldr, t, r) * (1.0f / HC));
 }
 
 // x[t][c] = (sum_s sigmoid(a[t][s D + c]) hn[t][s D + c]) / HC (streams in order), and, with inject logits,
 // inj[t][s] = 2 sigmoid(lr[t][HCR + s] / HC) (faie2fn.cu:873-888).  grid (nt, ceil(D / 256)), 256 threads
 __global__ void k_hc_mix(const float *__restrict__ a, const float *__restrict__ hn, int D, int HC,
-                         const float *__restrict__ lr, int ldr, int HCR, float *__restrict__ x, float *__restrict__ inj) {
+                         const float *__restrict__ lr, int ks, int nt, int ldr, int HCR, float *__restrict__ x,
+                         float *__restrict__ inj) {
     const int t = blockIdx.x, c = blockIdx.y * 256 + threadIdx.x;
     if (c < D) {
         float s = 0.0f;
@@ -101,105 +113,238 @@ __global__ void k_hc_mix(const float *__restrict__ a, const float *__restrict__ 
         x[(size_t) t * D + c] = s / HC;
     }
     if (inj && blockIdx.y == 0 && (int) threadIdx.x < HC)
-        inj[t * HC + threadIdx.x] = 2.0f * sigm(lr[(size_t) t * ldr + HCR + threadIdx.x] / HC);
+        inj[t * HC + threadIdx.x] = 2.0f * sigm(lr_sum(lr, ks, nt, ldr, t, HCR + threadIdx.x) / HC);
+}
+
+// The up product and the mix in one pass, for a BF16 up weight U [HC D][HCR] (the reference model's): the
+// low-rank activation tt[t][r] = silu(lr[t][r] / HC) goes to the LDS, each row of U is summed by 8 lanes (lane li
+// takes the 8-value chunks li, li + 8, ... in order, then a 3-step xor tree), and the workgroup's 32 rows are the
+// HC streams of 32 / HC columns, so it finishes x for them: x[t][c] = (sum_s sigmoid(U[s D + c] . tt[t]) hn[t][s D
+// + c]) / HC, streams in order; workgroup 0 also writes inj.  Replaces k_hc_lowrank + the up GEMV + k_hc_mix
+// (faie2fn.cu:1266-1273, 873-888).  grid ceil(D HC / 32), 256 threads, LDS nt HCR + 8 x 32 floats
+__global__ void __launch_bounds__(256) k_hc_upmix(const uint8_t *__restrict__ U, size_t urs, const float *__restrict__ lr,
+                                                  int ks, int nt, int ldr, int HCR, int HC, int D,
+                                                  const float *__restrict__ hn, float *__restrict__ x,
+                                                  float *__restrict__ inj) {
+    extern __shared__ float sm[];
+    float *tt = sm, *as = sm + nt * HCR;  // tt [nt][HCR], as [nt][32]
+    const int tid = threadIdx.x, cpb = 32 / HC, c0 = blockIdx.x * cpb;
+    for (int i = tid; i < nt * HCR; i += 256) {
+        const int t = i / HCR, r = i - t * HCR;
+        tt[i] = silu(lr_sum(lr, ks, nt, ldr, t, r) * (1.0f / HC));
+    }
+    __syncthreads();
+    const int ri = tid >> 3, li = tid & 7, cc = ri / HC, s = ri - cc * HC, c = c0 + cc;
+    const int nq = HCR / 8;
+    float acc[MAXT];
+#pragma unroll
+    for (int t = 0; t < MAXT; ++t) acc[t] = 0.0f;
+    if (c < D) {
+        const uint4 *row = reinterpret_cast<const uint4 *>(U + ((size_t) s * D + c) * urs);
+        for (int j = li; j < nq; j += 8) {
+            const uint4 w = row[j];
+            const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+            float wf[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                wf[2 * e] = __uint_as_float(wv[e] << 16);
+                wf[2 * e + 1] = __uint_as_float(wv[e] & 0xFFFF0000u);
+            }
+#pragma unroll
+            for (int t = 0; t < MAXT; ++t) {
+                if (t < nt) {
+                    const float4 x0 = *reinterpret_cast<const float4 *>(tt + t * HCR + 8 * j);
+                    const float4 x1 = *reinterpret_cast<const float4 *>(tt + t * HCR + 8 * j + 4);
+                    float a = acc[t];
+                    a = __builtin_fmaf(wf[0], x0.x, a);
+                    a = __builtin_fmaf(wf[1], x0.y, a);
+                    a = __builtin_fmaf(wf[2], x0.z, a);
+                    a = __builtin_fmaf(wf[3], x0.w, a);
+                    a = __builtin_fmaf(wf[4], x1.x, a);
+                    a = __builtin_fmaf(wf[5], x1.y, a);
+                    a = __builtin_fmaf(wf[6], x1.z, a);
+                    a = __builtin_fmaf(wf[7], x1.w, a);
+                    acc[t] = a;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < MAXT; ++t) {
+        if (t < nt) {
+            float v = acc[t];
+            v += __shfl_xor(v, 4);
+            v += __shfl_xor(v, 2);
+            v += __shfl_xor(v, 1);
+            if (li == 0) as[t * 32 + ri] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < cpb * nt) {
+        const int t = tid / cpb, cx = tid - t * cpb, cg = c0 + cx;
+        if (cg < D) {
+            float sum = 0.0f;
+            for (int k = 0; k < HC; ++k) sum += sigm(as[t * 32 + cx * HC + k]) * hn[(size_t) t * HC * D + (size_t) k * D + cg];
+            x[(size_t) t * D + cg] = sum / HC;
+        }
+    }
+    if (inj && blockIdx.x == 0 && tid < nt * HC) {
+        const int t = tid / HC, k = tid - t * HC;
+        inj[t * HC + k] = 2.0f * sigm(lr_sum(lr, ks, nt, ldr, t, HCR + k) / HC);
+    }
 }
 
 // hyper-connection write (faie2fn.cu:1281-1327): h[t][s][c] += yv[c] * inj[t][s], where yv = y, or for the MoE
 // yv = sum_k wsel[t][k] dpart[t NEU + k][c] + sigmoid(rsg[t][NE]) y[t][c]; then (norm non-null)
-// hn[t][s][c] = RMSNorm of the new stream s.  grid (nt, HC), 256 threads
-__global__ void __launch_bounds__(256) k_hc_add(float *__restrict__ h, const float *__restrict__ y,
-                                                const float *__restrict__ inj, int D, int HC,
-                                                const float *__restrict__ dpart, const float *__restrict__ wsel,
-                                                int NEU, const float *__restrict__ rsg, int NE,
-                                                const float *__restrict__ norm, float eps, float *__restrict__ hn) {
-    __shared__ float red[4];
-    const int t = blockIdx.x, s = blockIdx.y;
-    float *hp = h + ((size_t) t * HC + s) * D;
+// hn[t][s][c] = RMSNorm of the new stream s.  One thread per 4 columns (all loads of a thread issued together).
+// grid (nt, HC), min(1024, D / 4 rounded up to 64) threads
+__global__ void __launch_bounds__(1024) k_hc_add(float *__restrict__ h, const float *__restrict__ y,
+                                                 const float *__restrict__ inj, int D, int HC,
+                                                 const float *__restrict__ dpart, const float *__restrict__ wsel,
+                                                 int NEU, const float *__restrict__ rsg, int NE,
+                                                 const float *__restrict__ norm, float eps, float *__restrict__ hn) {
+    __shared__ float red[16];
+    const int t = blockIdx.x, s = blockIdx.y, D4 = D / 4;
+    float4 *hp = reinterpret_cast<float4 *>(h + ((size_t) t * HC + s) * D);
+    const float4 *y4 = reinterpret_cast<const float4 *>(y + (size_t) t * D);
     const float is = inj[t * HC + s];
     const float sg = dpart ? sigm(rsg[(size_t) t * (NE + 1) + NE]) : 0.0f;
     float ss = 0.0f;
-    for (int c = threadIdx.x; c < D; c += 256) {
-        float yv = y[(size_t) t * D + c];
+    for (int c = threadIdx.x; c < D4; c += blockDim.x) {
+        float4 yv = y4[c];
         if (dpart) {
-            float m = 0.0f;
-            for (int k = 0; k < NEU; ++k) m += wsel[t * NEU + k] * dpart[((size_t) t * NEU + k) * D + c];
-            yv = m + sg * yv;
+            float4 m = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 *dp = reinterpret_cast<const float4 *>(dpart + (size_t) t * NEU * D) + c;
+            for (int k = 0; k < NEU; ++k) {
+                const float wk = wsel[t * NEU + k];
+                const float4 d = dp[(size_t) k * D4];
+                m.x += wk * d.x;
+                m.y += wk * d.y;
+                m.z += wk * d.z;
+                m.w += wk * d.w;
+            }
+            yv = make_float4(m.x + sg * yv.x, m.y + sg * yv.y, m.z + sg * yv.z, m.w + sg * yv.w);
         }
-        const float v = hp[c] + yv * is;
+        float4 v = hp[c];
+        v = make_float4(v.x + yv.x * is, v.y + yv.y * is, v.z + yv.z * is, v.w + yv.w * is);
         hp[c] = v;
-        ss += v * v;
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     }
     if (!norm) return;  // (uniform)
-    const float r = rsqrtf(block_sum(ss, red, 4) / D + eps);
-    float *op = hn + ((size_t) t * HC + s) * D;
-    for (int c = threadIdx.x; c < D; c += 256) op[c] = hp[c] * r * norm[(size_t) s * D + c];
+    const float r = rsqrtf(block_sum(ss, red, blockDim.x >> 6) / D + eps);
+    float4 *op = reinterpret_cast<float4 *>(hn + ((size_t) t * HC + s) * D);
+    const float4 *w4 = reinterpret_cast<const float4 *>(norm + (size_t) s * D);
+    for (int c = threadIdx.x; c < D4; c += blockDim.x) {
+        const float4 v = hp[c], w = w4[c];
+        op[c] = make_float4(v.x * r * w.x, v.y * r * w.y, v.z * r * w.z, v.w * r * w.w);
+    }
 }
 
-// (value, index) maximum over a workgroup: larger value, ties to the lower index; every thread returns the winner
-__device__ __forceinline__ void block_argmax(float &v, int &i, float *bv, int *bi) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float v2 = __shfl_xor(v, o);
-        const int i2 = __shfl_xor(i, o);
-        if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+// (value, index) of the better of two: larger value, ties to the lower index
+__device__ __forceinline__ void vi_max(float &v, int &i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
     }
-    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) { bv[w] = v; bi[w] = i; }
-    __syncthreads();
-    v = bv[0];
-    i = bi[0];
-    for (int k = 1; k < nw; ++k)
-        if (bv[k] > v || (bv[k] == v && bi[k] < i)) { v = bv[k]; i = bi[k]; }
+}
+
+__device__ __forceinline__ void wave_argmax(float &v, int &i) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) vi_max(v, i, __shfl_xor(v, o), __shfl_xor(i, o));
 }
 
 // routing (faie2fn.cu:1747-1798): p = softmax over the NE router logits (rows 0..NE-1 of the router + shared-gate
 // GEMV), the NEU largest in order (probability descending, ties to the lower expert: repeated argmax), weights
-// renormalized over them; and the shared expert's SwiGLU sha[t][r] = silu(shg) * shu.  grid nt, 1024 threads
-__global__ void __launch_bounds__(1024) k_route(const float *__restrict__ rsg, int NE, int NEU,
-                                                const float *__restrict__ shg, const float *__restrict__ shu, int FFS,
-                                                int32_t *__restrict__ sel, float *__restrict__ wsel,
-                                                float *__restrict__ sha) {
-    __shared__ float bv[16];
-    __shared__ int bi[16];
-    __shared__ float topv[32];
-    const int t = blockIdx.x, i = threadIdx.x;
-    for (int r = i; r < FFS; r += blockDim.x)
-        sha[(size_t) t * FFS + r] = silu(shg[(size_t) t * FFS + r]) * shu[(size_t) t * FFS + r];
-    const float l = i < NE ? rsg[(size_t) t * (NE + 1) + i] : -INFINITY;
-    float mv = l;
-    int mi = i;
-    block_argmax(mv, mi, bv, bi);
-    float v = i < NE ? expf(l - mv) : -1.0f;  // probabilities up to the common 1 / sum, in [0, 1]
+// renormalized over them; and the shared expert's SwiGLU sha[t][r] = silu(shg) * shu.  Wave 0 routes with the NE
+// probabilities in registers (expert lane + 64 j in slot j), one wave argmax per pick and no barrier; the other
+// waves do the SwiGLU.  grid nt, 256 threads
+constexpr int ROUTE_PER = 16;  // experts per lane (NE <= 1024)
+__global__ void __launch_bounds__(256) k_route(const float *__restrict__ rsg, int NE, int NEU,
+                                               const float *__restrict__ shg, const float *__restrict__ shu, int FFS,
+                                               int32_t *__restrict__ sel, float *__restrict__ wsel,
+                                               float *__restrict__ sha) {
+    const int t = blockIdx.x, tid = threadIdx.x;
+    if (tid >= 64) {
+        for (int r = tid - 64; r < FFS; r += 192)
+            sha[(size_t) t * FFS + r] = silu(shg[(size_t) t * FFS + r]) * shu[(size_t) t * FFS + r];
+        return;
+    }
+    const float *l = rsg + (size_t) t * (NE + 1);
+    float v[ROUTE_PER];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < ROUTE_PER; ++j) {
+        const int e = tid + 64 * j;
+        v[j] = e < NE ? l[e] : -INFINITY;
+        mx = fmaxf(mx, v[j]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+#pragma unroll
+    for (int j = 0; j < ROUTE_PER; ++j) v[j] = tid + 64 * j < NE ? expf(v[j] - mx) : -1.0f;  // in [0, 1]; -1 = none
+    float mine = 0.0f;  // lane k keeps the k-th pick's probability
     for (int k = 0; k < NEU; ++k) {
-        float bvv = v;
-        int bii = i;
-        block_argmax(bvv, bii, bv, bi);
-        if (i == 0) {
-            topv[k] = bvv;
-            sel[t * NEU + k] = bii;
+        float bv = v[0];
+        int bi = tid;
+#pragma unroll
+        for (int j = 1; j < ROUTE_PER; ++j)
+            if (v[j] > bv) {  // strict: the lane's lower expert wins a tie
+                bv = v[j];
+                bi = tid + 64 * j;
+            }
+        wave_argmax(bv, bi);
+#pragma unroll
+        for (int j = 0; j < ROUTE_PER; ++j)
+            if (tid + 64 * j == bi) v[j] = -1.0f;  // taken
+        if (tid == k) mine = bv;
+        if (tid == 0) sel[t * NEU + k] = bi;
+    }
+    float sum = 0.0f;
+    for (int k = 0; k < NEU; ++k) sum += __shfl(mine, k);
+    if (tid < NEU) wsel[t * NEU + tid] = mine / sum;
+}
+
+// argmax of each token's logits, lowest index on ties (faie2fn.cu:1910-1934), in two passes: AM_CH chunks per
+// token each leave their (value, index) (index V when no logit in the chunk beats -inf), then one wave merges them
+constexpr int AM_CH = 128;
+// grid (nt, AM_CH), 256 threads
+__global__ void __launch_bounds__(256) k_argmax_part(const float *__restrict__ logits, int V, float *__restrict__ pv,
+                                                     int32_t *__restrict__ pi) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const int t = blockIdx.x, ch = blockIdx.y, per = (V + AM_CH - 1) / AM_CH;
+    const int lo = ch * per, hi = min(V, lo + per);
+    const float *l = logits + (size_t) t * V;
+    float v = -INFINITY;
+    int idx = V;
+    for (int i = lo + threadIdx.x; i < hi; i += 256)
+        if (l[i] > v) {
+            v = l[i];
+            idx = i;
         }
-        if (i == bii) v = -1.0f;  // taken
+    wave_argmax(v, idx);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        bv[w] = v;
+        bi[w] = idx;
     }
     __syncthreads();
-    if (i < NEU) {
-        float s = 0.0f;
-        for (int k = 0; k < NEU; ++k) s += topv[k];
-        wsel[t * NEU + i] = topv[i] / s;
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; ++k) vi_max(v, idx, bv[k], bi[k]);
+        pv[t * AM_CH + ch] = v;
+        pi[t * AM_CH + ch] = idx;
     }
 }
 
-// argmax of each token's logits, lowest index on ties (faie2fn.cu:1910-1934).  grid nt, 1024 threads
-__global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ logits, int V, int32_t *__restrict__ out) {
-    __shared__ float bv[16];
-    __shared__ int bi[16];
-    const float *l = logits + (size_t) blockIdx.x * V;
+// grid nt, 64 threads
+__global__ void k_argmax_merge(const float *__restrict__ pv, const int32_t *__restrict__ pi, int V,
+                               int32_t *__restrict__ out) {
+    const int t = blockIdx.x;
     float v = -INFINITY;
-    int idx = 0;
-    for (int i = threadIdx.x; i < V; i += blockDim.x)
-        if (l[i] > v) { v = l[i]; idx = i; }
-    block_argmax(v, idx, bv, bi);
-    if (threadIdx.x == 0) out[blockIdx.x] = idx;
+    int idx = V;
+    for (int k = threadIdx.x; k < AM_CH; k += 64) vi_max(v, idx, pv[t * AM_CH + k], pi[t * AM_CH + k]);
+    wave_argmax(v, idx);
+    if (threadIdx.x == 0) out[t] = idx == V ? 0 : idx;
 }
 
 // tok_all[pos + t] = ids[t]: the token history the n-gram hashing reads (faie2fn.cu:1899-1903).  1 block
@@ -327,7 +472,8 @@ struct Model {
     float *qkv = nullptr, *zz = nullptr, *abv = nullptr, *on = nullptr, *qg = nullptr, *kk = nullptr, *vv = nullptr;
     float *iqk = nullptr, *og = nullptr, *y = nullptr, *rsgv = nullptr, *shg = nullptr, *shu = nullptr, *sha = nullptr;
     float *shd = nullptr, *act = nullptr, *dpart = nullptr, *wsel = nullptr, *logits = nullptr, *work = nullptr;
-    int32_t *ids = nullptr, *sel = nullptr, *pos = nullptr, *am = nullptr;
+    float *amv = nullptr;
+    int32_t *ids = nullptr, *sel = nullptr, *pos = nullptr, *am = nullptr, *ami = nullptr;
     size_t work_bytes = 0;
     hipStream_t st = nullptr;
     hipGraphExec_t graph[MAXT + 1] = {};
@@ -625,7 +771,8 @@ int load_model(Model &m, int max_ctx_req) {
     m.nsplit = attn_pick_nsplit(1, d.NKV, MAXT, 4 * d.top + 4);
     for (int nt = 1; nt <= MAXT; ++nt)
         m.work_bytes = std::max(m.work_bytes, attn_qsa_work_bytes(1, d.NH, nt, HDK, m.nsplit, m.max_ctx, d.top) + 256);
-    if (m.alloc(&m.h, T * HCD) || m.alloc(&m.hn, T * HCD) || m.alloc(&m.lr, T * ldr) ||
+    if (m.alloc(&m.h, T * HCD) || m.alloc(&m.hn, T * HCD) || m.alloc(&m.lr, HC_KS * T * ldr) ||
+        m.alloc(&m.amv, T * AM_CH) || m.alloc(&m.ami, T * AM_CH) ||
         m.alloc(&m.t320, T * d.HCR) || m.alloc(&m.a, T * HCD) || m.alloc(&m.x, T * D) || m.alloc(&m.inj, T * d.HC) ||
         m.alloc(&m.qkv, T * d.CONVCH) || m.alloc(&m.zz, T * d.DINNER) || m.alloc(&m.abv, T * 2 * d.NVH) ||
         m.alloc(&m.on, T * d.DINNER) || m.alloc(&m.qg, T * d.NH * 2 * HDK) || m.alloc(&m.kk, T * d.NKV * HDK) ||
@@ -646,19 +793,32 @@ int gemv(const QW &w, const float *x, int nt, float *y, hipStream_t st) {
     return gemv_launch(w.L, w.p, x, nt, y, nullptr, 0, st);
 }
 
-// hyper-connection read of m.hn (already normalized) through the down(+inject) and up weights into m.x, m.inj
+// hyper-connection read of m.hn (already normalized) through the down(+inject) and up weights into m.x, m.inj.
+// The down product (a few hundred rows of HC D columns) runs split along its rows, HC_KS ways, and its consumers sum
+// the partials; with a BF16 up weight (the reference model's) the up product and the mix are one kernel.
 int hc_read(Model &m, const QW &dinj, const QW &up, int nt) {
     const ModelDims &d = m.d;
     const bool inj = dinj.L.rows > d.HCR;
     const int ldr = dinj.L.rows;
-    if (gemv(dinj, m.hn, nt, m.lr, m.st)) return -1;
-    hipLaunchKernelGGL(k_hc_lowrank, dim3(nt), dim3(256), 0, m.st, m.lr, ldr, d.HCR, d.HC, m.t320);
+    int ks = 1;
+    if (gemv_split_launch(dinj.L, dinj.p, m.hn, nt, HC_KS, m.lr, &ks, m.st)) return -1;
+    if (up.L.type == QT_BF16 && 32 % d.HC == 0 && d.HCR % 8 == 0) {
+        const int cpb = 32 / d.HC;
+        const size_t lds = ((size_t) nt * d.HCR + 8 * 32) * 4;
+        hipLaunchKernelGGL(k_hc_upmix, dim3((d.D + cpb - 1) / cpb), dim3(256), lds, m.st, up.p + up.L.off[0],
+                           up.L.rs[0], m.lr, ks, nt, ldr, d.HCR, d.HC, d.D, m.hn, m.x, inj ? m.inj : nullptr);
+        FN_CK(hipGetLastError());
+        return 0;
+    }
+    hipLaunchKernelGGL(k_hc_lowrank, dim3(nt), dim3(256), 0, m.st, m.lr, ks, nt, ldr, d.HCR, d.HC, m.t320);
     if (gemv(up, m.t320, nt, m.a, m.st)) return -1;
-    hipLaunchKernelGGL(k_hc_mix, dim3(nt, (d.D + 255) / 256), dim3(256), 0, m.st, m.a, m.hn, d.D, d.HC, m.lr, ldr,
-                       d.HCR, m.x, inj ? m.inj : nullptr);
+    hipLaunchKernelGGL(k_hc_mix, dim3(nt, (d.D + 255) / 256), dim3(256), 0, m.st, m.a, m.hn, d.D, d.HC, m.lr, ks, nt,
+                       ldr, d.HCR, m.x, inj ? m.inj : nullptr);
     FN_CK(hipGetLastError());
     return 0;
 }
+
+unsigned hc_add_threads(int D) { return (unsigned) std::min(1024, (D / 4 + 63) / 64 * 64); }
 
 int mixer(Model &m, MLayer &L, int nt) {
     const ModelDims &d = m.d;
@@ -685,14 +845,15 @@ int ffn(Model &m, MLayer &L, int nt, const float *next_norm) {
     if (gemv(L.rsg, m.x, nt, m.rsgv, m.st) || gemv(L.sh_gate, m.x, nt, m.shg, m.st) ||
         gemv(L.sh_up, m.x, nt, m.shu, m.st))
         return -1;
-    hipLaunchKernelGGL(k_route, dim3(nt), dim3(1024), 0, m.st, m.rsgv, d.NE, d.NEU, m.shg, m.shu, d.FFS, m.sel,
+    hipLaunchKernelGGL(k_route, dim3(nt), dim3(256), 0, m.st, m.rsgv, d.NE, d.NEU, m.shg, m.shu, d.FFS, m.sel,
                        m.wsel, m.sha);
     FN_CK(hipGetLastError());
     const int np = nt * d.NEU;
     if (swiglu_launch(L.eg.L, L.eg.p, L.eu.L, L.eu.p, d.FFE, m.sel, np, d.NEU, m.x, m.act, m.st) ||
         gemv(L.sh_down, m.sha, nt, m.shd, m.st) || rows_launch(L.ed.L, L.ed.p, d.D, m.sel, np, 1, m.act, m.dpart, m.st))
         return -1;
-    hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, m.shd, m.inj, d.D, d.HC, m.dpart, m.wsel,
+    hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(hc_add_threads(d.D)), 0, m.st, m.h, m.shd, m.inj, d.D, d.HC,
+                       m.dpart, m.wsel,
                        d.NEU, m.rsgv, d.NE, next_norm, d.eps, m.hn);
     FN_CK(hipGetLastError());
     return 0;
@@ -732,8 +893,8 @@ int enqueue(Model &m, int nt) {
         if (il == 0 || L.ple)
             hipLaunchKernelGGL(k_groupnorm, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, L.hca_norm, d.D, d.eps, m.hn);
         if (hc_read(m, L.hca_dinj, L.hca_up, nt) || mixer(m, L, nt)) return -1;
-        hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, m.y, m.inj, d.D, d.HC, nullptr, nullptr, 0,
-                           nullptr, 0, L.hcf_norm, d.eps, m.hn);
+        hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(hc_add_threads(d.D)), 0, m.st, m.h, m.y, m.inj, d.D, d.HC,
+                           nullptr, nullptr, 0, nullptr, 0, L.hcf_norm, d.eps, m.hn);
         if (hc_read(m, L.hcf_dinj, L.hcf_up, nt)) return -1;
         const float *next = il + 1 == d.NL ? m.out_norm : m.L[il + 1].ple ? nullptr : m.L[il + 1].hca_norm;
         if (ffn(m, L, nt, next)) return -1;
@@ -742,7 +903,8 @@ int enqueue(Model &m, int nt) {
                                  m.st));
     }
     if (hc_read(m, m.out_down, m.out_up, nt) || gemv(m.head, m.x, nt, m.logits, m.st)) return -1;
-    hipLaunchKernelGGL(k_argmax, dim3(nt), dim3(1024), 0, m.st, m.logits, d.VOCAB, m.am);
+    hipLaunchKernelGGL(k_argmax_part, dim3(nt, AM_CH), dim3(256), 0, m.st, m.logits, d.VOCAB, m.amv, m.ami);
+    hipLaunchKernelGGL(k_argmax_merge, dim3(nt), dim3(64), 0, m.st, m.amv, m.ami, d.VOCAB, m.am);
     FN_CK(hipGetLastError());
     return advance_launch(m.pos, 1, nt, m.st);
 }

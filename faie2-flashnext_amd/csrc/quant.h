@@ -50,7 +50,8 @@ struct GemvPlan {
                       // else one per row tile (ntiles)
 };
 
-GemvPlan gemv_plan(const QLayout &L);
+// ks_force > 0: that many splits along the row (capped so that every split holds a group), whatever the override
+GemvPlan gemv_plan(const QLayout &L, int ks_force = 0);
 // benchmarking and tests: force lanes per row (16 / 32 / 64), split-K, the kernel (1 = x staged in chunks of lpr
 // groups, the path of an x too large for the LDS; 2 = x staged once; 3 / 4 = x staged once with the deep / short
 // walk) and the resident waves per CU a persistent grid is sized for; 0 = automatic
@@ -67,6 +68,12 @@ int quant_dequant_launch(const QLayout &L, const uint8_t *packed, float *out, hi
 // y[t][r] = sum_c W[r][c] x[t][c] for t < nt (1..8); x [nt][cols], y [nt][rows]; work: gemv_work_bytes() bytes
 int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, float *y, float *work,
                 size_t work_bytes, hipStream_t st);
+
+// the GEMV with ks splits along the row and no reduce pass: part[k][t][r] = sum over split k's groups, k < *ks_out
+// (ks capped so that every split holds a group); the consumer sums the partials in split order.  The split is fixed
+// by the call, never by nt, so token t keeps the bits of a one-token call
+int gemv_split_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, int ks, float *part,
+                      int *ks_out, hipStream_t st);
 
 // Rows of a packed weight selected on the device (the model forward's embedding and routed experts):
 //   embed_launch: out[t][k * cols + c] = W[ids[t]][c] for k < copies (the GGUF decode, bit for bit);

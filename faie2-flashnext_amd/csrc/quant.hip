@@ -122,21 +122,23 @@ void gemv_override(int lpr, int ks, int kernel, int waves_per_cu) {
 
 void gemv_persistent(int on) { g_persist = on != 0; }
 
-GemvPlan gemv_plan(const QLayout &L) {
+GemvPlan gemv_plan(const QLayout &L, int ks_force) {
     GemvPlan p;
     p.ngroups = L.cols / 32;
     // lanes per row (measured on the projection shapes, nt 1 and 8): a few groups per lane, fewer lanes per row for
     // very tall weights (more row-sets per wave to stream through), and enough lanes in all (rows * lpr / 64 waves)
     // to spread a short weight over the CUs
-    const int G = p.ngroups;
+    // (a forced split: the same rule on the groups of one split and the rows times the splits)
+    const int kf = ks_force > 0 ? std::min(ks_force, p.ngroups) : 1;
+    const int G = (p.ngroups + kf - 1) / kf;
     const bool q6 = L.type == QT_Q6_K;  // one group in flight per lane and batch: more groups per lane pay off
     int lpr = G >= 160 ? 32 : (G >= 128 ? 64 : (G >= 48 ? (L.rows >= 32768 || (q6 && L.rows >= 4096) ? 16 : 32) : 16));
-    while (lpr < 64 && G > lpr && (size_t) L.rows * lpr / 64 < 1024) lpr *= 2;
+    while (lpr < 64 && G > lpr && (size_t) L.rows * kf * lpr / 64 < 1024) lpr *= 2;
     p.lpr = g_ov_lpr ? g_ov_lpr : lpr;
     p.rpw = 8 * (64 / p.lpr);
     p.ntiles = (L.rows + p.rpw - 1) / p.rpw;
     p.grid = g_persist ? 0 : p.ntiles;
-    p.ks = g_ov_ks ? std::min(g_ov_ks, p.ngroups) : 1;
+    p.ks = std::min(ks_force > 0 ? ks_force : g_ov_ks ? g_ov_ks : 1, p.ngroups);
     const int gps = (p.ngroups + p.ks - 1) / p.ks;
     p.ks = (p.ngroups + gps - 1) / gps;  // every split holds at least one group
     return p;
@@ -187,6 +189,17 @@ int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt,
     return 0;
 }
 
+int gemv_split_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, int ks, float *part,
+                      int *ks_out, hipStream_t st) {
+    if (nt < 1 || nt > MAXNT) FN_FAIL("gemv: nt must be 1..8");
+    if (!packed || !x || !part || ks < 1) FN_FAIL("gemv: bad arguments");
+    if ((uintptr_t) packed % 16 || (uintptr_t) x % 16) FN_FAIL("gemv: weight and x must be 16-byte aligned");
+    const GemvPlan pl = gemv_plan(L, ks);
+    const QOps *o = ops(L.type);
+    if (!o) FN_FAIL("gemv: unsupported type");
+    if (ks_out) *ks_out = pl.ks;
+    return o->gemv(L, pl, planes(L, packed), x, nt, part, st);
+}
 
 int embed_launch(const QLayout &L, const uint8_t *packed, const int32_t *ids, int nt, int copies, float *out,
                  hipStream_t st) {

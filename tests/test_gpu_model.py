@@ -155,3 +155,21 @@ def test_model_ple_load_checks(fnlib, tmp_path):
     with pytest.raises(RuntimeError, match="cannot open"):
         fnlib.load(p, str(tmp_path / "absent.gguf"), max_ctx=256)
     assert fnlib.d.fn_n_past() == -1
+
+
+def test_model_quantized_hyper_connections(fnlib, tmp_path):
+    """Hyper-connection weights in a block format take the general path (low-rank kernel, up GEMV, mix kernel) in
+    place of the fused BF16 up-and-mix kernel; both match the oracle."""
+    p = str(tmp_path / "hcq.gguf")
+    kv, ts = ms.write_model(p, ms.TINY_DIMS, seed=12, types={"hc": ms.Q8_0})
+    _say("model forward: Q8_0 hyper-connection weights, 20 tokens")
+    fnlib.load(p, "", max_ctx=256)
+    try:
+        ref = om.Model(kv, ts, max_ctx=256)
+        ids = np.random.default_rng(3).integers(0, ms.TINY_DIMS["VOCAB"], size=20)
+        for k, nt in ((0, 1), (1, 8), (9, 3), (12, 8)):
+            am, lg = fnlib.forward(ids[k:k + nt], logits=True)
+            want, _, _, _ = ref.forward(ids[k:k + nt])
+            assert _rel(lg, want) <= TOL, (k, nt, _rel(lg, want))
+    finally:
+        fnlib.free()
