@@ -418,7 +418,7 @@ def hybrid_verify(lib, stream, steps, warmup, B=16, ctx=32768, nt=4, kr=2, nl=48
     return ms, nbytes
 
 
-def model_decode(lib, nl=8, ctx=4096, tokens=64, seed=0):
+def model_decode(lib, nl=8, ctx=4096, tokens=64, seed=0, nts=(1, 8)):
     """fn_load + fn_forward on a synthetic model of the reference model's dimensions and weight formats with nl layers
     (PLE at layer 1; the n-gram table's head sizes 1/100 of the reference's, which changes only the table's size:
     16 rows are gathered per token either way).  Greedy-decode latency per fn_forward call (tokens in, argmax out,
@@ -454,7 +454,7 @@ def model_decode(lib, nl=8, ctx=4096, tokens=64, seed=0):
     out = {"layers": nl, "ctx": ctx, "weight_gb_on_device": round(lib.d.fn_dev_gb(0), 2),
            "bytes_per_token_nt1": per_token}
     try:
-        for nt in (1, 8):
+        for nt in nts:
             lib.reset()
             for i in range(4):                                     # warm-up: captures the graph for nt
                 lib.forward(ids[i * nt:(i + 1) * nt])
@@ -467,7 +467,8 @@ def model_decode(lib, nl=8, ctx=4096, tokens=64, seed=0):
             out[f"nt{nt}"] = {"ms_per_forward": round(ms_call, 4), "tokens_per_s": round(nt * 1e3 / ms_call, 1),
                               "us_per_layer": round(ms_call * 1e3 / nl, 2)}
             log(f"[bench] model nt={nt}: {ms_call:.3f} ms per forward, {nt * 1e3 / ms_call:.1f} tokens/s")
-        out["nt1"]["gbs"] = round(per_token / (out["nt1"]["ms_per_forward"] * 1e-3) / 1e9, 1)
+        if "nt1" in out:
+            out["nt1"]["gbs"] = round(per_token / (out["nt1"]["ms_per_forward"] * 1e-3) / 1e9, 1)
     finally:
         lib.free()
     return out
@@ -574,6 +575,8 @@ def main():
     ap.add_argument("--model", type=int, default=0, metavar="LAYERS",
                     help="only the whole-model leg: fn_load + fn_forward greedy decode of a synthetic model of the "
                          "reference's dimensions and formats with LAYERS layers")
+    ap.add_argument("--model-nt", type=int, default=0, choices=(0, 1, 8),
+                    help="with --model: time only calls of this many tokens (0: both 1 and 8)")
     ap.add_argument("--counters-attn", action="store_true",
                     help="counter-collection workload only: 5 eager multi-token GQA layer-steps at B=16, 32K context, "
                          "nt=8 then 5 at nt=4 (k_attn_split_mt<2>)")
@@ -588,7 +591,7 @@ def main():
     stream = hiprt.Stream()
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     if args.model:
-        res = model_decode(lib, nl=args.model)
+        res = model_decode(lib, nl=args.model, nts=(args.model_nt,) if args.model_nt else (1, 8))
         print(json.dumps({"model_decode": res}), flush=True)
         return
     if args.gemv:

@@ -44,6 +44,7 @@ constexpr int RING = 16;                     // conv ring slots (>= MAXT + 3, a 
 constexpr int PLE_HIST = 9;                  // PLE conv history: (kernel 4 - 1) x dilation 3 (faie2fn.cu:66)
 constexpr int PLE_MAXH = 64;                 // n-gram heads the hashing kernel takes
 constexpr int HC_KS = 8;                     // split of the hyper-connection down product along its rows
+constexpr int UPMIX_U = 8;                   // 8-value chunks per lane of the fused up-and-mix kernel (HCR <= 512)
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
@@ -129,20 +130,30 @@ __global__ void __launch_bounds__(256) k_hc_upmix(const uint8_t *__restrict__ U,
     extern __shared__ float sm[];
     float *tt = sm, *as = sm + nt * HCR;  // tt [nt][HCR], as [nt][32]
     const int tid = threadIdx.x, cpb = 32 / HC, c0 = blockIdx.x * cpb;
+    const int ri = tid >> 3, li = tid & 7, cc = ri / HC, s = ri - cc * HC, c = c0 + cc;
+    const int nq = HCR / 8;
+    // the lane's weight chunks li + 8 u, u < UPMIX_U, requested first: they do not depend on the activation
+    const bool live = c < D;
+    uint4 wq[UPMIX_U];
+    if (live) {
+        const uint4 *row = reinterpret_cast<const uint4 *>(U + ((size_t) s * D + c) * urs);
+#pragma unroll
+        for (int u = 0; u < UPMIX_U; ++u) wq[u] = row[min(li + 8 * u, nq - 1)];
+    }
     for (int i = tid; i < nt * HCR; i += 256) {
         const int t = i / HCR, r = i - t * HCR;
         tt[i] = silu(lr_sum(lr, ks, nt, ldr, t, r) * (1.0f / HC));
     }
     __syncthreads();
-    const int ri = tid >> 3, li = tid & 7, cc = ri / HC, s = ri - cc * HC, c = c0 + cc;
-    const int nq = HCR / 8;
     float acc[MAXT];
 #pragma unroll
     for (int t = 0; t < MAXT; ++t) acc[t] = 0.0f;
-    if (c < D) {
-        const uint4 *row = reinterpret_cast<const uint4 *>(U + ((size_t) s * D + c) * urs);
-        for (int j = li; j < nq; j += 8) {
-            const uint4 w = row[j];
+    if (live) {
+#pragma unroll
+        for (int u = 0; u < UPMIX_U; ++u) {
+            const int j = li + 8 * u;
+            if (j >= nq) break;
+            const uint4 w = wq[u];
             const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
             float wf[8];
 #pragma unroll
@@ -172,10 +183,14 @@ __global__ void __launch_bounds__(256) k_hc_upmix(const uint8_t *__restrict__ U,
 #pragma unroll
     for (int t = 0; t < MAXT; ++t) {
         if (t < nt) {
+            // the 8 lanes of a row: quad sums by DPP quad_perm (xor 1, xor 2), then lane 0 of the row adds lane 4's
             float v = acc[t];
-            v += __shfl_xor(v, 4);
-            v += __shfl_xor(v, 2);
-            v += __shfl_xor(v, 1);
+            v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xf, 0xf,
+                                                                       false));
+            v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xf, 0xf,
+                                                                       false));
+            v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf,
+                                                                       false));
             if (li == 0) as[t * 32 + ri] = v;
         }
     }
@@ -248,9 +263,23 @@ __device__ __forceinline__ void vi_max(float &v, int &i, float v2, int i2) {
     }
 }
 
+// minimum over the 64 lanes (DPP inside rows, a swizzle across the row pair, readlanes across the halves),
+// wave-uniform; call from wave-uniform control flow
+__device__ __forceinline__ int wave_min_i(int v) {
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false));  // row_ror 8
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false));  // row_ror 4
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x122, 0xf, 0xf, false));  // row_ror 2
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x121, 0xf, 0xf, false));  // row_ror 1
+    v = min(v, __builtin_amdgcn_ds_swizzle(v, 0x401f));                     // lane ^ 16
+    return min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 32));
+}
+
+// (value, index) maximum over the wave, ties to the lower index, wave-uniform: the largest value, then the least
+// index among the lanes that hold it (two cross-lane reductions, no LDS traffic)
 __device__ __forceinline__ void wave_argmax(float &v, int &i) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) vi_max(v, i, __shfl_xor(v, o), __shfl_xor(i, o));
+    const float m = wave_max(v);
+    i = wave_min_i(v == m ? i : INT_MAX);
+    v = m;
 }
 
 // routing (faie2fn.cu:1747-1798): p = softmax over the NE router logits (rows 0..NE-1 of the router + shared-gate
@@ -802,7 +831,7 @@ int hc_read(Model &m, const QW &dinj, const QW &up, int nt) {
     const int ldr = dinj.L.rows;
     int ks = 1;
     if (gemv_split_launch(dinj.L, dinj.p, m.hn, nt, HC_KS, m.lr, &ks, m.st)) return -1;
-    if (up.L.type == QT_BF16 && 32 % d.HC == 0 && d.HCR % 8 == 0) {
+    if (up.L.type == QT_BF16 && 32 % d.HC == 0 && d.HCR % 8 == 0 && d.HCR <= 64 * UPMIX_U) {
         const int cpb = 32 / d.HC;
         const size_t lds = ((size_t) nt * d.HCR + 8 * 32) * 4;
         hipLaunchKernelGGL(k_hc_upmix, dim3((d.D + cpb - 1) / cpb), dim3(256), lds, m.st, up.p + up.L.off[0],
