@@ -989,28 +989,49 @@ __global__ void __launch_bounds__(256) k_embed(PP P, int G, int cols, const int3
 // row r of expert sel[p] (R rows per expert) against x[p / xdiv]: 16 lanes per row, 4 rows per wave, 16 rows per
 // workgroup; lane li sums its groups li, li + 16, ... in order.  grid (ceil(R / 16), npairs), 256 threads.
 // SWIGLU: the gate row of Wg and the up row of Wu, out = silu(g) * u.
+// One memory round trip before the arithmetic: the lane's first ROWS_PRE groups of weight words, the x row (into
+// LDS, group-major with an odd float4 stride so that a row's 16 lanes read distinct bank quads) and the format's
+// codebook are all requested before the one barrier.  LDS: 9 float4 per group of x.
+constexpr int ROWS_PRE = 5;
 template <uint32_t TY, bool SWIGLU>
 __global__ void __launch_bounds__(256) k_rows(PP Pg, PP Pu, int R, int nexp, int G, int cols,
                                               const int32_t *__restrict__ sel, int xdiv, const float *__restrict__ x,
                                               float *__restrict__ out) {
-    if constexpr (tab_lds<TY>() > 0) {
-        tab_fill<TY>(threadIdx.x, blockDim.x);
-        __syncthreads();
-    }
-    const TabT<TY> T;
+    extern __shared__ float4 xs[];  // [G][9]
+    constexpr int NW = Q<TY>::NW;
     const int p = blockIdx.y, lane = threadIdx.x & 63, li = lane & 15;
     const int r = blockIdx.x * 16 + (threadIdx.x >> 6) * 4 + (lane >> 4);
     const int e = sel ? min(max(sel[p], 0), nexp - 1) : 0;  // an id outside the weight reads its last expert
     const int row = e * R + min(r, R - 1);
+    const RP rg = row_planes(Pg, row), ru = row_planes(Pu, row);
+    uint32_t wg[ROWS_PRE][NW], wu[ROWS_PRE][NW];
+#pragma unroll
+    for (int k = 0; k < ROWS_PRE; ++k) {
+        const int g = min(li + 16 * k, G - 1);  // (clamped: a valid address, its value unused past G)
+        Q<TY>::load(rg, g, wg[k]);
+        if constexpr (SWIGLU) Q<TY>::load(ru, g, wu[k]);
+    }
     const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t) (p / xdiv) * cols);
+    for (int i = threadIdx.x; i < G * 8; i += 256) xs[(i >> 3) * 9 + (i & 7)] = xp[i];
+    tab_fill<TY>(threadIdx.x, blockDim.x);
+    __syncthreads();
+    const TabT<TY> T;
     float ag = 0.0f, au = 0.0f;
-    for (int g = li; g < G; g += 16) {
-        uint32_t w[Q<TY>::NW];
-        Q<TY>::load(row_planes(Pg, row), g, w);
-        accumulate<TY, 1>(w, g, xp + 8 * g, &ag, T);
+#pragma unroll
+    for (int k = 0; k < ROWS_PRE; ++k) {
+        const int g = li + 16 * k;
+        if (g < G) {
+            accumulate<TY, 1>(wg[k], g, xs + 9 * g, &ag, T);
+            if constexpr (SWIGLU) accumulate<TY, 1>(wu[k], g, xs + 9 * g, &au, T);
+        }
+    }
+    for (int g = li + 16 * ROWS_PRE; g < G; g += 16) {  // rows longer than 80 groups
+        uint32_t w[NW];
+        Q<TY>::load(rg, g, w);
+        accumulate<TY, 1>(w, g, xs + 9 * g, &ag, T);
         if constexpr (SWIGLU) {
-            Q<TY>::load(row_planes(Pu, row), g, w);
-            accumulate<TY, 1>(w, g, xp + 8 * g, &au, T);
+            Q<TY>::load(ru, g, w);
+            accumulate<TY, 1>(w, g, xs + 9 * g, &au, T);
         }
     }
     ag = row_sum(ag);
@@ -1034,7 +1055,9 @@ int embed_t(const QLayout &L, const PP &P, const int32_t *ids, int nt, int copie
 template <uint32_t TY, bool SW>
 int rows_t(const QLayout &L, const PP &Pg, const PP &Pu, int R, const int32_t *sel, int npairs, int xdiv,
            const float *x, float *out, hipStream_t st) {
-    hipLaunchKernelGGL((k_rows<TY, SW>), dim3((unsigned) ((R + 15) / 16), (unsigned) npairs), dim3(256), 0, st, Pg,
+    const size_t lds = (size_t) (L.cols / 32) * 9 * sizeof(float4);
+    if (lds + tab_lds<TY>() > (size_t) kLdsPerCu) FN_FAIL("rows: x row too long for the LDS");
+    hipLaunchKernelGGL((k_rows<TY, SW>), dim3((unsigned) ((R + 15) / 16), (unsigned) npairs), dim3(256), lds, st, Pg,
                        Pu, R, L.rows / R, L.cols / 32, L.cols, sel, xdiv, x, out);
     FN_CK(hipGetLastError());
     return 0;
