@@ -1,6 +1,8 @@
 // Shared device helpers and host error plumbing for libfaie2fn (gfx950 / CDNA4, wave64).
 #pragma once
 
+#include <climits>
+
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -83,6 +85,86 @@ __device__ __forceinline__ float wave_max(float v) {
     v = row_max(v);
     v = fmaxf(v, swz_xor16(v));
     return fmaxf(readlane(v, 0), readlane(v, 32));
+}
+
+// minimum over the 64 lanes (DPP inside rows, a swizzle across the row pair, readlanes across the halves),
+// wave-uniform; call from wave-uniform control flow
+__device__ __forceinline__ int wave_min_i(int v) {
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false));  // row_ror 8
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false));  // row_ror 4
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x122, 0xf, 0xf, false));  // row_ror 2
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x121, 0xf, 0xf, false));  // row_ror 1
+    v = min(v, __builtin_amdgcn_ds_swizzle(v, 0x401f));                     // lane ^ 16
+    return min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 32));
+}
+
+// (value, index) of the better of two: larger value, ties to the lower index
+__device__ __forceinline__ void vi_max(float &v, int &i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+// (value, index) maximum over the wave, ties to the lower index, wave-uniform: the largest value, then the least
+// index among the lanes that hold it (two cross-lane reductions, no LDS traffic)
+__device__ __forceinline__ void wave_argmax(float &v, int &i) {
+    const float m = wave_max(v);
+    i = wave_min_i(v == m ? i : INT_MAX);
+    v = m;
+}
+
+// MoE routing of one token by one whole wave (faie2fn.cu:1747-1798): p = softmax of the NE <= 1024 router logits
+// l[0..NE), picked in order probability descending with ties to the lower expert (repeated argmax), npick picks.
+// Returns pick `want`'s expert to every lane; with sel / wsel non-null (npick = NEU) it also writes the NEU picks
+// and their weights renormalized over them, sel[k] and wsel[k].  The probabilities ride in registers (expert
+// lane + 64 j in slot j), one wave argmax per pick.
+// PER: experts per lane, 8 (NE <= 512) or 16 (NE <= 1024).
+constexpr int ROUTE_PER = 16;
+template <int PER>
+__device__ __forceinline__ int route_wave(const float *__restrict__ l, int NE, int npick, int want,
+                                          int32_t *__restrict__ sel, float *__restrict__ wsel) {
+    const int lane = threadIdx.x & 63;
+    float v[PER];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < NE ? l[e] : -INFINITY;
+        mx = fmaxf(mx, v[j]);
+    }
+    mx = wave_max(mx);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) v[j] = lane + 64 * j < NE ? expf(v[j] - mx) : -1.0f;  // in [0, 1]; -1 none
+    float mine = 0.0f;  // lane k keeps the k-th pick's probability
+    int got = 0;
+    for (int k = 0; k < npick; ++k) {
+        float bv = v[0];
+        int bi = lane;
+#pragma unroll
+        for (int j = 1; j < PER; ++j)
+            if (v[j] > bv) {  // strict: the lane's lower expert wins a tie
+                bv = v[j];
+                bi = lane + 64 * j;
+            }
+        wave_argmax(bv, bi);
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            if (lane + 64 * j == bi) v[j] = -1.0f;  // taken
+        if (lane == k) mine = bv;
+        if (sel && lane == 0) sel[k] = bi;
+        if (k == want) got = bi;
+    }
+    if (wsel) {
+        float sum = 0.0f;
+        for (int k = 0; k < npick; ++k) sum += __shfl(mine, k);
+        if (lane < npick) wsel[lane] = mine / sum;
+    }
+    return got;
+}
+__device__ __forceinline__ int route_pick(const float *__restrict__ l, int NE, int npick, int want,
+                                          int32_t *__restrict__ sel, float *__restrict__ wsel) {
+    return NE <= 512 ? route_wave<8>(l, NE, npick, want, sel, wsel) : route_wave<16>(l, NE, npick, want, sel, wsel);
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }

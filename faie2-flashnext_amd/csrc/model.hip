@@ -11,8 +11,9 @@
 //                          attention: GEMV q / k / v / indexer, QSA sparse attention, GEMV o
 //   hyper-connection write h_s += y * inj_s, then hn = RMSNorm_s(h) for the next read (faie2fn.cu:1281-1327)
 //   hyper-connection read  (FFN)
-//   MoE                    router + shared-gate GEMV, softmax top-k routing with the shared expert's SwiGLU
-//                          (faie2fn.cu:1747-1798), routed experts' SwiGLU and down rows, the shared expert's down GEMV
+//   MoE                    router + shared-gate GEMV; the routed experts' SwiGLU rows, whose kernel also does the
+//                          softmax top-k routing and the shared expert's SwiGLU (faie2fn.cu:1747-1798); down rows,
+//                          the shared expert's down GEMV
 //   hyper-connection write with y = sum_k w_k down_k + sigmoid(shared gate) shared down (faie2fn.cu:1298-1318)
 // then the final hyper-connection read (no inject), the LM head GEMV and the argmax (lowest index on ties,
 // faie2fn.cu:1910-1934).  The layers listed in <arch>.ple.layers first add the per-layer n-gram embedding
@@ -45,6 +46,7 @@ constexpr int PLE_HIST = 9;                  // PLE conv history: (kernel 4 - 1)
 constexpr int PLE_MAXH = 64;                 // n-gram heads the hashing kernel takes
 constexpr int HC_KS = 8;                     // split of the hyper-connection down product along its rows
 constexpr int UPMIX_U = 8;                   // 8-value chunks per lane of the fused up-and-mix kernel (HCR <= 512)
+constexpr int UPMIX_HC = 8;                  // streams the fused up-and-mix kernel takes (HC <= 8)
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
@@ -140,6 +142,14 @@ __global__ void __launch_bounds__(256) k_hc_upmix(const uint8_t *__restrict__ U,
 #pragma unroll
         for (int u = 0; u < UPMIX_U; ++u) wq[u] = row[min(li + 8 * u, nq - 1)];
     }
+    // the mix's normalised streams, requested now as well (thread tid < cpb nt finishes column c0 + tid % cpb of
+    // token tid / cpb)
+    float hv[UPMIX_HC];
+    const int mt = tid / cpb, mc = c0 + (tid - mt * cpb);
+    const bool mixer = tid < cpb * nt && mc < D;
+#pragma unroll
+    for (int k = 0; k < UPMIX_HC; ++k)
+        hv[k] = mixer && k < HC ? hn[(size_t) mt * HC * D + (size_t) k * D + mc] : 0.0f;
     for (int i = tid; i < nt * HCR; i += 256) {
         const int t = i / HCR, r = i - t * HCR;
         tt[i] = silu(lr_sum(lr, ks, nt, ldr, t, r) * (1.0f / HC));
@@ -195,13 +205,13 @@ __global__ void __launch_bounds__(256) k_hc_upmix(const uint8_t *__restrict__ U,
         }
     }
     __syncthreads();
-    if (tid < cpb * nt) {
-        const int t = tid / cpb, cx = tid - t * cpb, cg = c0 + cx;
-        if (cg < D) {
-            float sum = 0.0f;
-            for (int k = 0; k < HC; ++k) sum += sigm(as[t * 32 + cx * HC + k]) * hn[(size_t) t * HC * D + (size_t) k * D + cg];
-            x[(size_t) t * D + cg] = sum / HC;
-        }
+    if (mixer) {
+        const int cx = mc - c0;
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < UPMIX_HC; ++k)
+            if (k < HC) sum += sigm(as[mt * 32 + cx * HC + k]) * hv[k];
+        x[(size_t) mt * D + mc] = sum / HC;
     }
     if (inj && blockIdx.x == 0 && tid < nt * HC) {
         const int t = tid / HC, k = tid - t * HC;
@@ -255,82 +265,22 @@ __global__ void __launch_bounds__(1024) k_hc_add(float *__restrict__ h, const fl
     }
 }
 
-// (value, index) of the better of two: larger value, ties to the lower index
-__device__ __forceinline__ void vi_max(float &v, int &i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) {
-        v = v2;
-        i = i2;
-    }
-}
-
-// minimum over the 64 lanes (DPP inside rows, a swizzle across the row pair, readlanes across the halves),
-// wave-uniform; call from wave-uniform control flow
-__device__ __forceinline__ int wave_min_i(int v) {
-    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false));  // row_ror 8
-    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false));  // row_ror 4
-    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x122, 0xf, 0xf, false));  // row_ror 2
-    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x121, 0xf, 0xf, false));  // row_ror 1
-    v = min(v, __builtin_amdgcn_ds_swizzle(v, 0x401f));                     // lane ^ 16
-    return min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 32));
-}
-
-// (value, index) maximum over the wave, ties to the lower index, wave-uniform: the largest value, then the least
-// index among the lanes that hold it (two cross-lane reductions, no LDS traffic)
-__device__ __forceinline__ void wave_argmax(float &v, int &i) {
-    const float m = wave_max(v);
-    i = wave_min_i(v == m ? i : INT_MAX);
-    v = m;
-}
-
-// routing (faie2fn.cu:1747-1798): p = softmax over the NE router logits (rows 0..NE-1 of the router + shared-gate
-// GEMV), the NEU largest in order (probability descending, ties to the lower expert: repeated argmax), weights
-// renormalized over them; and the shared expert's SwiGLU sha[t][r] = silu(shg) * shu.  Wave 0 routes with the NE
-// probabilities in registers (expert lane + 64 j in slot j), one wave argmax per pick and no barrier; the other
-// waves do the SwiGLU.  grid nt, 256 threads
-constexpr int ROUTE_PER = 16;  // experts per lane (NE <= 1024)
+// routing for calls of several tokens (one call of one token routes inside the experts' gate/up kernel; both use
+// route_pick, so the picks and weights are the same bits) and the shared expert's SwiGLU sha[t][r] = silu(shg) shu.
+// grid nt, 256 threads (wave 0 routes, the other waves do the SwiGLU)
 __global__ void __launch_bounds__(256) k_route(const float *__restrict__ rsg, int NE, int NEU,
                                                const float *__restrict__ shg, const float *__restrict__ shu, int FFS,
                                                int32_t *__restrict__ sel, float *__restrict__ wsel,
                                                float *__restrict__ sha) {
     const int t = blockIdx.x, tid = threadIdx.x;
     if (tid >= 64) {
-        for (int r = tid - 64; r < FFS; r += 192)
-            sha[(size_t) t * FFS + r] = silu(shg[(size_t) t * FFS + r]) * shu[(size_t) t * FFS + r];
+        for (int r = tid - 64; r < FFS; r += 192) {
+            const float g = shg[(size_t) t * FFS + r];
+            sha[(size_t) t * FFS + r] = g / (1.0f + expf(-g)) * shu[(size_t) t * FFS + r];
+        }
         return;
     }
-    const float *l = rsg + (size_t) t * (NE + 1);
-    float v[ROUTE_PER];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < ROUTE_PER; ++j) {
-        const int e = tid + 64 * j;
-        v[j] = e < NE ? l[e] : -INFINITY;
-        mx = fmaxf(mx, v[j]);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-#pragma unroll
-    for (int j = 0; j < ROUTE_PER; ++j) v[j] = tid + 64 * j < NE ? expf(v[j] - mx) : -1.0f;  // in [0, 1]; -1 = none
-    float mine = 0.0f;  // lane k keeps the k-th pick's probability
-    for (int k = 0; k < NEU; ++k) {
-        float bv = v[0];
-        int bi = tid;
-#pragma unroll
-        for (int j = 1; j < ROUTE_PER; ++j)
-            if (v[j] > bv) {  // strict: the lane's lower expert wins a tie
-                bv = v[j];
-                bi = tid + 64 * j;
-            }
-        wave_argmax(bv, bi);
-#pragma unroll
-        for (int j = 0; j < ROUTE_PER; ++j)
-            if (tid + 64 * j == bi) v[j] = -1.0f;  // taken
-        if (tid == k) mine = bv;
-        if (tid == 0) sel[t * NEU + k] = bi;
-    }
-    float sum = 0.0f;
-    for (int k = 0; k < NEU; ++k) sum += __shfl(mine, k);
-    if (tid < NEU) wsel[t * NEU + tid] = mine / sum;
+    route_pick(rsg + (size_t) t * (NE + 1), NE, NEU, 0, sel + t * NEU, wsel + t * NEU);
 }
 
 // argmax of each token's logits, lowest index on ties (faie2fn.cu:1910-1934), in two passes: AM_CH chunks per
@@ -831,7 +781,7 @@ int hc_read(Model &m, const QW &dinj, const QW &up, int nt) {
     const int ldr = dinj.L.rows;
     int ks = 1;
     if (gemv_split_launch(dinj.L, dinj.p, m.hn, nt, HC_KS, m.lr, &ks, m.st)) return -1;
-    if (up.L.type == QT_BF16 && 32 % d.HC == 0 && d.HCR % 8 == 0 && d.HCR <= 64 * UPMIX_U) {
+    if (up.L.type == QT_BF16 && 32 % d.HC == 0 && d.HC <= UPMIX_HC && d.HCR % 8 == 0 && d.HCR <= 64 * UPMIX_U) {
         const int cpb = 32 / d.HC;
         const size_t lds = ((size_t) nt * d.HCR + 8 * 32) * 4;
         hipLaunchKernelGGL(k_hc_upmix, dim3((d.D + cpb - 1) / cpb), dim3(256), lds, m.st, up.p + up.L.off[0],
@@ -874,11 +824,26 @@ int ffn(Model &m, MLayer &L, int nt, const float *next_norm) {
     if (gemv(L.rsg, m.x, nt, m.rsgv, m.st) || gemv(L.sh_gate, m.x, nt, m.shg, m.st) ||
         gemv(L.sh_up, m.x, nt, m.shu, m.st))
         return -1;
-    hipLaunchKernelGGL(k_route, dim3(nt), dim3(256), 0, m.st, m.rsgv, d.NE, d.NEU, m.shg, m.shu, d.FFS, m.sel,
-                       m.wsel, m.sha);
-    FN_CK(hipGetLastError());
+    // routing (softmax top-k of the router logits, faie2fn.cu:1747-1798): for one token inside the experts' gate/up
+    // kernel, which then also writes the picks, their weights and the shared expert's SwiGLU (one kernel fewer); for
+    // several tokens in its own kernel (each of their gate/up workgroups would route again)
+    if (nt > 1) {
+        hipLaunchKernelGGL(k_route, dim3(nt), dim3(256), 0, m.st, m.rsgv, d.NE, d.NEU, m.shg, m.shu, d.FFS, m.sel,
+                           m.wsel, m.sha);
+        FN_CK(hipGetLastError());
+    }
+    RouteIn rt;
+    rt.rsg = m.rsgv;
+    rt.NE = d.NE;
+    rt.NEU = d.NEU;
+    rt.FFS = d.FFS;
+    rt.sel = m.sel;
+    rt.wsel = m.wsel;
+    rt.shg = m.shg;
+    rt.shu = m.shu;
+    rt.sha = m.sha;
     const int np = nt * d.NEU;
-    if (swiglu_launch(L.eg.L, L.eg.p, L.eu.L, L.eu.p, d.FFE, m.sel, np, d.NEU, m.x, m.act, m.st) ||
+    if (swiglu_launch(L.eg.L, L.eg.p, L.eu.L, L.eu.p, d.FFE, m.sel, np, d.NEU, m.x, m.act, m.st, nt > 1 ? nullptr : &rt) ||
         gemv(L.sh_down, m.sha, nt, m.shd, m.st) || rows_launch(L.ed.L, L.ed.p, d.D, m.sel, np, 1, m.act, m.dpart, m.st))
         return -1;
     hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(hc_add_threads(d.D)), 0, m.st, m.h, m.shd, m.inj, d.D, d.HC,

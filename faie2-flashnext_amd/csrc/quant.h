@@ -86,7 +86,20 @@ int embed_launch(const QLayout &L, const uint8_t *packed, const int32_t *ids, in
                  hipStream_t st);
 int rows_launch(const QLayout &L, const uint8_t *packed, int R, const int32_t *sel, int npairs, int xdiv,
                 const float *x, float *out, hipStream_t st);
+// The routing done inside the expert gate/up kernel (the model forward, one kernel fewer): pair p = t NEU + k
+// takes the k-th pick of token t (route_wave over the router logits rsg[t][0 .. NE), row stride NE + 1); the
+// workgroups of pair t NEU, row tile 0, write sel[t][..] and wsel[t][..] and the shared expert's SwiGLU
+// sha[t][r] = silu(shg[t][r]) * shu[t][r], r < FFS.
+struct RouteIn {
+    const float *rsg = nullptr;
+    int NE = 0, NEU = 0, FFS = 0;
+    int32_t *sel = nullptr;
+    float *wsel = nullptr;
+    const float *shg = nullptr, *shu = nullptr;
+    float *sha = nullptr;
+};
 int swiglu_launch(const QLayout &Lg, const uint8_t *pg, const QLayout &Lu, const uint8_t *pu, int R,
-                  const int32_t *sel, int npairs, int xdiv, const float *x, float *act, hipStream_t st);
+                  const int32_t *sel, int npairs, int xdiv, const float *x, float *act, hipStream_t st,
+                  const RouteIn *route = nullptr);
 
 }  // namespace fn

@@ -216,16 +216,24 @@ int rows_launch(const QLayout &L, const uint8_t *packed, int R, const int32_t *s
     const QOps *o = ops(L.type);
     if (!o) FN_FAIL("rows: unsupported type");
     const PP P = planes(L, packed);
-    return o->rows(L, P, P, R, sel, npairs, xdiv, x, out, st);
+    return o->rows(L, P, P, R, sel, npairs, xdiv, x, out, st, RouteIn{});
 }
 
 int swiglu_launch(const QLayout &Lg, const uint8_t *pg, const QLayout &Lu, const uint8_t *pu, int R,
-                  const int32_t *sel, int npairs, int xdiv, const float *x, float *act, hipStream_t st) {
+                  const int32_t *sel, int npairs, int xdiv, const float *x, float *act, hipStream_t st,
+                  const RouteIn *route) {
     if (!pg || !pu || rows_check(Lg, R, npairs, xdiv, x, act)) return -1;
     if (Lg.type != Lu.type || Lg.rows != Lu.rows || Lg.cols != Lu.cols) FN_FAIL("swiglu: gate and up weights differ");
     const QOps *o = ops(Lg.type);
     if (!o) FN_FAIL("swiglu: unsupported type");
-    return o->swiglu(Lg, planes(Lg, pg), planes(Lu, pu), R, sel, npairs, xdiv, x, act, st);
+    RouteIn rt{};
+    if (route) {
+        rt = *route;
+        if (!rt.rsg || !rt.sel || !rt.wsel || !rt.shg || !rt.shu || !rt.sha || rt.NE < 1 || rt.NE > 64 * ROUTE_PER ||
+            rt.NEU < 1 || rt.NEU > 64 || rt.NEU > rt.NE || xdiv != rt.NEU || npairs % rt.NEU)
+            FN_FAIL("swiglu: bad routing arguments");
+    }
+    return o->swiglu(Lg, planes(Lg, pg), planes(Lu, pu), R, sel, npairs, xdiv, x, act, st, rt);
 }
 
 }  // namespace fn

@@ -996,25 +996,46 @@ constexpr int ROWS_PRE = 5;
 template <uint32_t TY, bool SWIGLU>
 __global__ void __launch_bounds__(256) k_rows(PP Pg, PP Pu, int R, int nexp, int G, int cols,
                                               const int32_t *__restrict__ sel, int xdiv, const float *__restrict__ x,
-                                              float *__restrict__ out) {
+                                              float *__restrict__ out, RouteIn rt) {
     extern __shared__ float4 xs[];  // [G][9]
+    __shared__ int e_sh;
     constexpr int NW = Q<TY>::NW;
-    const int p = blockIdx.y, lane = threadIdx.x & 63, li = lane & 15;
-    const int r = blockIdx.x * 16 + (threadIdx.x >> 6) * 4 + (lane >> 4);
-    const int e = sel ? min(max(sel[p], 0), nexp - 1) : 0;  // an id outside the weight reads its last expert
-    const int row = e * R + min(r, R - 1);
-    const RP rg = row_planes(Pg, row), ru = row_planes(Pu, row);
+    const int p = blockIdx.y, tid = threadIdx.x, lane = tid & 63, li = lane & 15;
+    const int r = blockIdx.x * 16 + (tid >> 6) * 4 + (lane >> 4);
+    const bool routed = SWIGLU && rt.rsg != nullptr;
     uint32_t wg[ROWS_PRE][NW], wu[ROWS_PRE][NW];
+    RP rg, ru;
+    const auto load_pre = [&](int e) {  // an id outside the weight reads its last expert
+        const int row = min(max(e, 0), nexp - 1) * R + min(r, R - 1);
+        rg = row_planes(Pg, row);
+        ru = row_planes(Pu, row);
 #pragma unroll
-    for (int k = 0; k < ROWS_PRE; ++k) {
-        const int g = min(li + 16 * k, G - 1);  // (clamped: a valid address, its value unused past G)
-        Q<TY>::load(rg, g, wg[k]);
-        if constexpr (SWIGLU) Q<TY>::load(ru, g, wu[k]);
-    }
+        for (int k = 0; k < ROWS_PRE; ++k) {
+            const int g = min(li + 16 * k, G - 1);  // (clamped: a valid address, its value unused past G)
+            Q<TY>::load(rg, g, wg[k]);
+            if constexpr (SWIGLU) Q<TY>::load(ru, g, wu[k]);
+        }
+    };
+    if (!routed) load_pre(sel ? sel[p] : 0);
     const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t) (p / xdiv) * cols);
-    for (int i = threadIdx.x; i < G * 8; i += 256) xs[(i >> 3) * 9 + (i & 7)] = xp[i];
-    tab_fill<TY>(threadIdx.x, blockDim.x);
+    for (int i = tid; i < G * 8; i += 256) xs[(i >> 3) * 9 + (i & 7)] = xp[i];
+    tab_fill<TY>(tid, blockDim.x);
+    if (routed) {
+        const int t = p / rt.NEU, k = p - t * rt.NEU;
+        const bool writer = k == 0 && blockIdx.x == 0;
+        if (tid < 64) {
+            const int e = route_pick(rt.rsg + (size_t) t * (rt.NE + 1), rt.NE, writer ? rt.NEU : k + 1, k,
+                                     writer ? rt.sel + t * rt.NEU : nullptr, writer ? rt.wsel + t * rt.NEU : nullptr);
+            if (tid == 0) e_sh = e;
+        } else if (writer) {
+            for (int i = tid - 64; i < rt.FFS; i += 192) {
+                const float g = rt.shg[(size_t) t * rt.FFS + i];
+                rt.sha[(size_t) t * rt.FFS + i] = g / (1.0f + expf(-g)) * rt.shu[(size_t) t * rt.FFS + i];
+            }
+        }
+    }
     __syncthreads();
+    if (routed) load_pre(e_sh);
     const TabT<TY> T;
     float ag = 0.0f, au = 0.0f;
 #pragma unroll
@@ -1054,11 +1075,11 @@ int embed_t(const QLayout &L, const PP &P, const int32_t *ids, int nt, int copie
 
 template <uint32_t TY, bool SW>
 int rows_t(const QLayout &L, const PP &Pg, const PP &Pu, int R, const int32_t *sel, int npairs, int xdiv,
-           const float *x, float *out, hipStream_t st) {
+           const float *x, float *out, hipStream_t st, const RouteIn &rt) {
     const size_t lds = (size_t) (L.cols / 32) * 9 * sizeof(float4);
     if (lds + tab_lds<TY>() > (size_t) kLdsPerCu) FN_FAIL("rows: x row too long for the LDS");
     hipLaunchKernelGGL((k_rows<TY, SW>), dim3((unsigned) ((R + 15) / 16), (unsigned) npairs), dim3(256), lds, st, Pg,
-                       Pu, R, L.rows / R, L.cols / 32, L.cols, sel, xdiv, x, out);
+                       Pu, R, L.rows / R, L.cols / 32, L.cols, sel, xdiv, x, out, rt);
     FN_CK(hipGetLastError());
     return 0;
 }
@@ -1070,9 +1091,9 @@ struct QOps {
     int (*dequant)(const QLayout &, const PP &, float *, hipStream_t);
     int (*embed)(const QLayout &, const PP &, const int32_t *, int, int, float *, hipStream_t);
     int (*rows)(const QLayout &, const PP &, const PP &, int, const int32_t *, int, int, const float *, float *,
-                hipStream_t);
+                hipStream_t, const RouteIn &);
     int (*swiglu)(const QLayout &, const PP &, const PP &, int, const int32_t *, int, int, const float *, float *,
-                  hipStream_t);
+                  hipStream_t, const RouteIn &);
 };
 
 template <uint32_t TY> int dequant_t(const QLayout &L, const PP &P, float *out, hipStream_t st) {
