@@ -355,39 +355,53 @@ __global__ void k_ple_ids(const int32_t *__restrict__ tok_all, const int32_t *__
 }
 
 // per stream s (faie2fn.cu:1843-1875): gate = <RMSNorm(key_s) wk, RMSNorm(h_s) wq> / sqrt(D), signed square root
-// (magnitude floored at 1e-6); gv = sigmoid(gate) * val; gvn = RMSNorm(gv) wc.  grid (nt, HC), 256 threads
-__global__ void __launch_bounds__(256) k_ple_gate(const float *__restrict__ key, const float *__restrict__ val,
-                                                  const float *__restrict__ h, const float *__restrict__ wk,
-                                                  const float *__restrict__ wq, const float *__restrict__ wc, int D,
-                                                  float eps, float *__restrict__ gv, float *__restrict__ gvn) {
-    __shared__ float red[4];
-    const int t = blockIdx.x, s = blockIdx.y, HC = gridDim.y;
+// (magnitude floored at 1e-6); gv = sigmoid(gate) * val; gvn = RMSNorm(gv) wc.  One thread per 4 columns, every
+// input requested at the start.  grid (nt, HC), min(1024, D / 4 rounded up to 64) threads
+__global__ void __launch_bounds__(1024) k_ple_gate(const float *__restrict__ key, const float *__restrict__ val,
+                                                   const float *__restrict__ h, const float *__restrict__ wk,
+                                                   const float *__restrict__ wq, const float *__restrict__ wc, int D,
+                                                   float eps, float *__restrict__ gv, float *__restrict__ gvn) {
+    __shared__ float red[16];
+    const int t = blockIdx.x, s = blockIdx.y, HC = gridDim.y, D4 = D / 4, nw = blockDim.x >> 6;
     const size_t base = ((size_t) t * HC + s) * D;
-    const float *kt = key + base, *ht = h + base, *vt = val + (size_t) t * D;
+    const float4 *kt = reinterpret_cast<const float4 *>(key + base), *ht = reinterpret_cast<const float4 *>(h + base);
+    const float4 *vt = reinterpret_cast<const float4 *>(val + (size_t) t * D);
+    const float4 *wk4 = reinterpret_cast<const float4 *>(wk + (size_t) s * D);
+    const float4 *wq4 = reinterpret_cast<const float4 *>(wq + (size_t) s * D);
+    const float4 *wc4 = reinterpret_cast<const float4 *>(wc + (size_t) s * D);
+    float4 *gv4 = reinterpret_cast<float4 *>(gv + base), *gvn4 = reinterpret_cast<float4 *>(gvn + base);
     float sk = 0.0f, sq = 0.0f;
-    for (int c = threadIdx.x; c < D; c += 256) {
-        sk += kt[c] * kt[c];
-        sq += ht[c] * ht[c];
+    for (int c = threadIdx.x; c < D4; c += blockDim.x) {
+        const float4 k = kt[c], x = ht[c];
+        sk += k.x * k.x + k.y * k.y + k.z * k.z + k.w * k.w;
+        sq += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
     }
-    sk = block_sum(sk, red, 4);
-    sq = block_sum(sq, red, 4);
+    sk = block_sum(sk, red, nw);
+    sq = block_sum(sq, red, nw);
     const float rk = rsqrtf(sk / D + eps), rq = rsqrtf(sq / D + eps);
     float dot = 0.0f;
-    for (int c = threadIdx.x; c < D; c += 256)
-        dot += (kt[c] * rk * wk[(size_t) s * D + c]) * (ht[c] * rq * wq[(size_t) s * D + c]);
-    dot = block_sum(dot, red, 4);
+    for (int c = threadIdx.x; c < D4; c += blockDim.x) {
+        const float4 k = kt[c], x = ht[c], a = wk4[c], b = wq4[c];
+        dot += (k.x * rk * a.x) * (x.x * rq * b.x) + (k.y * rk * a.y) * (x.y * rq * b.y) +
+               (k.z * rk * a.z) * (x.z * rq * b.z) + (k.w * rk * a.w) * (x.w * rq * b.w);
+    }
+    dot = block_sum(dot, red, nw);
     float gate = dot / sqrtf((float) D);
     gate = gate == 0.0f ? 0.0f : copysignf(sqrtf(fmaxf(fabsf(gate), 1e-6f)), gate);
     const float sg = sigm(gate);
     float sv = 0.0f;
-    for (int c = threadIdx.x; c < D; c += 256) {
-        const float x = sg * vt[c];
-        gv[base + c] = x;
-        sv += x * x;
+    for (int c = threadIdx.x; c < D4; c += blockDim.x) {
+        const float4 v = vt[c];
+        const float4 x = make_float4(sg * v.x, sg * v.y, sg * v.z, sg * v.w);
+        gv4[c] = x;
+        sv += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
     }
-    sv = block_sum(sv, red, 4);
+    sv = block_sum(sv, red, nw);
     const float rv = rsqrtf(sv / D + eps);
-    for (int c = threadIdx.x; c < D; c += 256) gvn[base + c] = gv[base + c] * rv * wc[(size_t) s * D + c];
+    for (int c = threadIdx.x; c < D4; c += blockDim.x) {
+        const float4 x = gv4[c], w = wc4[c];
+        gvn4[c] = make_float4(x.x * rv * w.x, x.y * rv * w.y, x.z * rv * w.z, x.w * rv * w.w);
+    }
 }
 
 // dilated causal depthwise conv (kernel 4, dilation 3) over gvn with its history, SiLU, then h += gv + conv; the
@@ -864,7 +878,7 @@ int ple(Model &m, MLayer &L, int nt) {
     if (embed_launch(m.ple_table.L, m.ple_table.p, m.ple_rows, nt * d.ple_heads, 1, m.ple_emb, m.st) ||
         gemv(L.ple_key, m.ple_emb, nt, m.ple_k, m.st) || gemv(L.ple_val, m.ple_emb, nt, m.ple_v, m.st))
         return -1;
-    hipLaunchKernelGGL(k_ple_gate, dim3(nt, d.HC), dim3(256), 0, m.st, m.ple_k, m.ple_v, m.h, L.ple_nk, L.ple_nq,
+    hipLaunchKernelGGL(k_ple_gate, dim3(nt, d.HC), dim3(hc_add_threads(d.D)), 0, m.st, m.ple_k, m.ple_v, m.h, L.ple_nk, L.ple_nq,
                        L.ple_nc, d.D, d.eps, m.ple_gv, m.ple_gvn);
     hipLaunchKernelGGL(k_ple_conv, dim3((HCD + 255) / 256), dim3(256), 0, m.st, m.h, m.ple_gv, m.ple_gvn, L.ple_hist,
                        L.ple_conv, HCD, nt);

@@ -293,9 +293,11 @@ template <> struct Q<QT_Q4_K> {
     __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
         const int ib = g & 7, sh = 4 * (ib & 1);
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t q = (w[i] >> sh) & 0x0F0F0F0Fu;  // the group's 4 nibbles of word i, one per byte
 #pragma unroll
-            for (int k = 0; k < 4; ++k) o.q[4 * i + k] = (float) ((w[i] >> (8 * k + sh)) & 0xFu);
+            for (int k = 0; k < 4; ++k) o.q[4 * i + k] = (float) ((q >> (8 * k)) & 0xFFu);
+        }
         float sc, mn;
         scale_min_k(w + 9, ib, sc, mn);
         o.s[0] = o.s[1] = h2f(w[8]) * sc;
@@ -320,10 +322,12 @@ template <> struct Q<QT_Q5_K> {
     __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
         const int ib = g & 7, sh = 4 * (ib & 1);
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < 8; ++i) {
+            // 4 values per 32-bit operation: the nibbles, then bit ib of each qh byte moved to bit 4 of its byte
+            const uint32_t q = (((w[8 + i] >> ib) << 4) & 0x10101010u) | ((w[i] >> sh) & 0x0F0F0F0Fu);
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                o.q[4 * i + k] = (float) (((w[i] >> (8 * k + sh)) & 0xFu) | ((w[8 + i] >> (8 * k + ib)) & 1u) << 4);
+            for (int k = 0; k < 4; ++k) o.q[4 * i + k] = (float) ((q >> (8 * k)) & 0xFFu);
+        }
         float sc, mn;
         scale_min_k(w + 17, ib, sc, mn);
         o.s[0] = o.s[1] = h2f(w[16]) * sc;
@@ -353,11 +357,12 @@ template <> struct Q<QT_Q6_K> {
     __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
         const int qu = g & 3, lsh = 4 * (qu >> 1), hsh = 2 * qu;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < 8; ++i) {
+            // 4 six-bit codes per 32-bit operation (low nibble, then 2 high bits at bits 4-5 of each byte)
+            const uint32_t q = (((w[8 + i] >> hsh) & 0x03030303u) << 4) | ((w[i] >> lsh) & 0x0F0F0F0Fu);
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                o.q[4 * i + k] =
-                    (float) ((int) (((w[i] >> (8 * k + lsh)) & 0xFu) | ((w[8 + i] >> (8 * k + hsh)) & 3u) << 4) - 32);
+            for (int k = 0; k < 4; ++k) o.q[4 * i + k] = (float) ((q >> (8 * k)) & 0xFFu) - 32.0f;
+        }
         const float d = h2f(w[17]);
         o.s[0] = d * sbyte(w[16], 0);
         o.s[1] = d * sbyte(w[16], 1);
