@@ -380,21 +380,26 @@ __device__ __forceinline__ float sum_x16_x32(float x) {
 }
 
 // K of the 16-key block starting at key kb: lane l takes 16-byte chunk 4u + l/16 of key kb + l%16 (keys past nkmax
-// are clamped: finite values, masked later)
+// are clamped: finite values, masked later).  KEEP: an ordinary load, whose lines stay in the L2 for the other row
+// group of the workgroup, which reads the same block (with the nontemporal hint the second read went back to HBM:
+// 1.26x the K/V bytes at 8 new tokens); else nontemporal (each byte is read once).
+template <bool KEEP> __device__ __forceinline__ float4 mt_ld(const float4 *p) { return KEEP ? *p : ld_nt(p); }
+template <bool KEEP>
 __device__ __forceinline__ void mt_load_k(float4 (&k)[16], const float4 *Kb, int kb, int nkmax, int lane) {
     const int key = min(kb + (lane & 15), nkmax - 1);
     const float4 *kt = Kb + (size_t) (key / TILE) * (TILE * HD / 4) + (key % TILE);
 #pragma unroll
-    for (int u = 0; u < 16; ++u) k[u] = ld_nt(kt + (4 * u + (lane >> 4)) * TILE);
+    for (int u = 0; u < 16; ++u) k[u] = mt_ld<KEEP>(kt + (4 * u + (lane >> 4)) * TILE);
 }
 // V of the block: v[4s + c] = dims 64c + 4(l%16) .. +3 of key kb + 4(l/16) + s
+template <bool KEEP>
 __device__ __forceinline__ void mt_load_v(float4 (&v)[16], const float4 *Vb, int kb, int nkmax, int lane) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         const int row = min(kb + 4 * (lane >> 4) + s, nkmax - 1);
         const float4 *vr = Vb + (size_t) row * (HD / 4) + (lane & 15);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[4 * s + c] = ld_nt(vr + 16 * c);
+        for (int c = 0; c < 4; ++c) v[4 * s + c] = mt_ld<KEEP>(vr + 16 * c);
     }
 }
 
@@ -595,8 +600,9 @@ __device__ __forceinline__ void mt_block(const float4 (&k)[16], const float4 (&v
     mt_pv<NRW>(v, p, o);
 }
 
-// grid (nsplit, nkv, B), RW * KW <= 4 waves; dynamic LDS: max(RW * NRW * 16 KiB of Q, RW * KW * 16 * MT_OS * 4 B)
-template <int NRW>
+// grid (nsplit, nkv, B), RW * KW <= 4 waves; dynamic LDS: max(RW * NRW * 16 KiB of Q, RW * KW * 16 * MT_OS * 4 B);
+// KEEP = RW > 1 (row groups share each block through the L2)
+template <int NRW, bool KEEP>
 __global__ void __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 k_attn_split_mt(const AttnArgs a, int grp, int RW, int KW) {
     extern __shared__ float4 mt_lds[];
@@ -648,19 +654,19 @@ k_attn_split_mt(const AttnArgs a, int grp, int RW, int KW) {
         // while B's 32 are still in flight)
         const int npair = (nw + 1) / 2;
         float4 ka[16], va[16], kb2[16], vb2[16];
-        mt_load_k(ka, Kb, k0 + kw * 16, nkmax, lane);
-        mt_load_v(va, Vb, k0 + kw * 16, nkmax, lane);
-        mt_load_k(kb2, Kb, k0 + (kw + KW) * 16, nkmax, lane);
-        mt_load_v(vb2, Vb, k0 + (kw + KW) * 16, nkmax, lane);
+        mt_load_k<KEEP>(ka, Kb, k0 + kw * 16, nkmax, lane);
+        mt_load_v<KEEP>(va, Vb, k0 + kw * 16, nkmax, lane);
+        mt_load_k<KEEP>(kb2, Kb, k0 + (kw + KW) * 16, nkmax, lane);
+        mt_load_v<KEEP>(vb2, Vb, k0 + (kw + KW) * 16, nkmax, lane);
         int pr = 0;
         for (; pr + 1 < npair; ++pr) {
             const int kb = k0 + (kw + 2 * pr * KW) * 16;
             mt_block<NRW>(ka, va, kb, qs, o, m, l, lim, lane);
-            mt_load_k(ka, Kb, kb + 2 * KW * 16, nkmax, lane);
-            mt_load_v(va, Vb, kb + 2 * KW * 16, nkmax, lane);
+            mt_load_k<KEEP>(ka, Kb, kb + 2 * KW * 16, nkmax, lane);
+            mt_load_v<KEEP>(va, Vb, kb + 2 * KW * 16, nkmax, lane);
             mt_block<NRW>(kb2, vb2, kb + KW * 16, qs, o, m, l, lim, lane);
-            mt_load_k(kb2, Kb, kb + 3 * KW * 16, nkmax, lane);
-            mt_load_v(vb2, Vb, kb + 3 * KW * 16, nkmax, lane);
+            mt_load_k<KEEP>(kb2, Kb, kb + 3 * KW * 16, nkmax, lane);
+            mt_load_v<KEEP>(vb2, Vb, kb + 3 * KW * 16, nkmax, lane);
         }
         const int kb = k0 + (kw + 2 * pr * KW) * 16;
         mt_block<NRW>(ka, va, kb, qs, o, m, l, lim, lane);
@@ -674,11 +680,11 @@ k_attn_split_mt(const AttnArgs a, int grp, int RW, int KW) {
         float4 kf[16], vf[16];
         v4f S[NRW];
         auto kbl = [&](int i) { return k0 + (kw + i * KW) * 16; };  // first key of this wave's block i
-        mt_load_k(kf, Kb, kbl(0), nkmax, lane);
-        mt_load_v(vf, Vb, kbl(0), nkmax, lane);
+        mt_load_k<KEEP>(kf, Kb, kbl(0), nkmax, lane);
+        mt_load_v<KEEP>(vf, Vb, kbl(0), nkmax, lane);
         mt_qk<NRW>(kf, qs, lane, kbl(0), S);
         __builtin_amdgcn_sched_barrier(0);
-        mt_load_k(kf, Kb, kbl(1), nkmax, lane);  // past the wave's last block when nw = 1: in bounds, unused
+        mt_load_k<KEEP>(kf, Kb, kbl(1), nkmax, lane);  // past the wave's last block when nw = 1: in bounds, unused
         __builtin_amdgcn_sched_barrier(0);
         int i = 0;
         for (; i + 1 < nw; ++i) {
@@ -689,12 +695,12 @@ k_attn_split_mt(const AttnArgs a, int grp, int RW, int KW) {
 #pragma unroll
             for (int j = 0; j < NRW; ++j) S[j] = Sn[j];
             __builtin_amdgcn_sched_barrier(0);
-            mt_load_k(kf, Kb, kbl(i + 2), nkmax, lane);
+            mt_load_k<KEEP>(kf, Kb, kbl(i + 2), nkmax, lane);
             __builtin_amdgcn_sched_barrier(0);
             mt_rescale<NRW>(o, corr);
             mt_pv<NRW>(vf, p, o);
             __builtin_amdgcn_sched_barrier(0);
-            mt_load_v(vf, Vb, kbl(i + 1), nkmax, lane);
+            mt_load_v<KEEP>(vf, Vb, kbl(i + 1), nkmax, lane);
             __builtin_amdgcn_sched_barrier(0);
         }
         v4f p[NRW];
@@ -908,8 +914,9 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
         const int nrw = nr == 1 ? 1 : 2, rw = (nr + nrw - 1) / nrw, kw = std::max(1, WAVES / rw);
         const size_t lds = std::max((size_t) rw * nrw * 16 * HD * 4, (size_t) rw * kw * 16 * MT_OS * 4);
         const dim3 mg(p.nsplit, p.nkv, p.B), mb(rw * kw * 64);
-        if (nrw == 1) hipLaunchKernelGGL(k_attn_split_mt<1>, mg, mb, lds, st, a, grp, rw, kw);
-        else hipLaunchKernelGGL(k_attn_split_mt<2>, mg, mb, lds, st, a, grp, rw, kw);
+        if (nrw == 1) hipLaunchKernelGGL((k_attn_split_mt<1, false>), mg, mb, lds, st, a, grp, rw, kw);
+        else if (rw == 1) hipLaunchKernelGGL((k_attn_split_mt<2, false>), mg, mb, lds, st, a, grp, rw, kw);
+        else hipLaunchKernelGGL((k_attn_split_mt<2, true>), mg, mb, lds, st, a, grp, rw, kw);
     } else {
         if (grp == 8) hipLaunchKernelGGL((k_attn_split<8, false>), sg, sb, 0, st, a);
         else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, false>), sg, sb, 0, st, a);
