@@ -33,6 +33,7 @@ import fn_synth  # noqa: E402
 import hiprt  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0
+MT_LEGS = ((1, 32768, 8, 4), (16, 32768, 2, 4), (16, 32768, 2, 8))  # multi-token legs: B, context, layers, nt
 METRIC = "µs per layer-step + achieved HBM GB/s (% of peak), DeltaNet & GQA decode, B=1/64"
 NKH, NVH, DK = 16, 32, 128
 C = 2 * NKH * DK + NVH * DK
@@ -577,6 +578,8 @@ def main():
                          "reference's dimensions and formats with LAYERS layers")
     ap.add_argument("--model-nt", type=int, default=0, choices=(0, 1, 8),
                     help="with --model: time only calls of this many tokens (0: both 1 and 8)")
+    ap.add_argument("--mt-only", action="store_true",
+                    help="only the multi-token GQA legs (config 3 shapes, nt = 4 and 8, hipGraph replays)")
     ap.add_argument("--counters-attn", action="store_true",
                     help="counter-collection workload only: 5 eager multi-token GQA layer-steps at B=16, 32K context, "
                          "nt=8 then 5 at nt=4 (k_attn_split_mt<2>)")
@@ -593,6 +596,19 @@ def main():
     if args.model:
         res = model_decode(lib, nl=args.model, nts=(args.model_nt,) if args.model_nt else (1, 8))
         print(json.dumps({"model_decode": res}), flush=True)
+        return
+    if args.mt_only:
+        res = {}
+        for Bq, ctx, nl, ntq in MT_LEGS:
+            at = AttnStack(lib, Bq, ctx, nl, seed=4, nt=ntq)
+            ms = time_graph(stream, lambda: at.launch(stream), steps, warmup) / nl
+            at.free()
+            by, fl = fn_synth.attn_bytes(Bq, ctx, nt=ntq), fn_synth.attn_flops(Bq, ctx, nt=ntq)
+            res[f"config3_gqa_b{Bq}_ctx{ctx}_nt{ntq}"] = {"us_per_layer_step": round(ms * 1e3, 2),
+                                                         "gbs": round(by / (ms * 1e-3) / 1e9, 1),
+                                                         "tflops": round(fl / (ms * 1e-3) / 1e12, 1)}
+            log(f"[bench] config 3 B={Bq} ctx={ctx} nt={ntq}: {ms * 1e3:.1f} us")
+        print(json.dumps({"multi_token": res}), flush=True)
         return
     if args.gemv:
         res = gemv_extras(lib)
@@ -720,7 +736,7 @@ def main():
         if not args.attn_only:
             # config 3 multi-token (speculative verify / chunked prefill): nt new tokens per sequence share one K/V pass
             # on the matrix cores; GB/s counts K/V once, TFLOP/s the fp32 products (peak 157.3)
-            for Bq, ctx, nl, ntq in ((1, 32768, 8, 4), (16, 32768, 2, 4), (16, 32768, 2, 8)):
+            for Bq, ctx, nl, ntq in MT_LEGS:
                 at = AttnStack(lib, Bq, ctx, nl, seed=4, nt=ntq)
                 ms = time_graph(stream, lambda: at.launch(stream), steps, warmup) / nl
                 nsplit = at.nsplit
