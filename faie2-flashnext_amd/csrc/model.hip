@@ -44,7 +44,7 @@ constexpr int IXH = 4, IXD = 128, IXR = 4;   // indexer heads, head dim, keys pe
 constexpr int RING = 16;                     // conv ring slots (>= MAXT + 3, a power of two)
 constexpr int PLE_HIST = 9;                  // PLE conv history: (kernel 4 - 1) x dilation 3 (faie2fn.cu:66)
 constexpr int PLE_MAXH = 64;                 // n-gram heads the hashing kernel takes
-constexpr int HC_KS = 8;                     // split of the hyper-connection down product along its rows
+constexpr int HC_KS = 4;                     // split of the hyper-connection down product along its rows
 constexpr int UPMIX_U = 8;                   // 8-value chunks per lane of the fused up-and-mix kernel (HCR <= 512)
 constexpr int UPMIX_HC = 8;                  // streams the fused up-and-mix kernel takes (HC <= 8)
 

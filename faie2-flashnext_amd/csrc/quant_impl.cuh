@@ -912,6 +912,16 @@ int gemv_nt(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, f
         }
         const size_t lds = (size_t) gps * XS;
         int per_cu = std::min(by_regs, std::max(1, (int) (kLdsPerCu / (lds + tab_lds<TY>()))));
+        // one token through a tall weight (each wave would walk 32 or more batches): one workgroup per CU more than
+        // fit at once (measured: the Q5_K LM head, 248320 x 2560, 143-156 -> 114-117 us; the launch shape never
+        // changes the bits)
+        {
+            const int nb1 = (gps + LPR * Q<TY>::U - 1) / (LPR * Q<TY>::U);
+            const int nwg1 = std::min(nwg, device_cus() * per_cu);
+            if (NT == 1 && (ns + 8 * nwg1 - 1) / (8 * nwg1) * nb1 >= 32 &&
+                (size_t) (per_cu + 1) * (lds + tab_lds<TY>()) <= (size_t) kLdsPerCu)
+                ++per_cu;
+        }
         if (g_ov_wpc) per_cu = std::max(1, g_ov_wpc / 8);
         if (g_persist) nwg = std::min(nwg, device_cus() * per_cu);
         // batches of the busiest wave; from 4 on the deep walk's exact waits pay for its surplus loads (measured)
