@@ -31,6 +31,7 @@
 
 #include <chrono>
 #include <cmath>
+#include <cstring>
 #include <memory>
 #include <vector>
 
@@ -469,6 +470,11 @@ struct Model {
     int32_t *ids = nullptr, *sel = nullptr, *pos = nullptr, *am = nullptr, *ami = nullptr;
     size_t work_bytes = 0;
     hipStream_t st = nullptr;
+    // pinned host staging of one call's token ids, argmax ids and the status word (an asynchronous copy from or to
+    // pageable memory is a blocking one), and the status word's device address
+    int32_t *h_ids = nullptr, *h_am = nullptr;
+    unsigned *h_status = nullptr, *status = nullptr;
+    void *host = nullptr;
     hipGraphExec_t graph[MAXT + 1] = {};
     bool use_graphs = true;
     float *dbg = nullptr;  // host [NL][nt][HC D] when set
@@ -482,6 +488,7 @@ struct Model {
         for (auto &ge : graph)
             if (ge) (void) hipGraphExecDestroy(ge);
         for (void *p : allocs) (void) hipFree(p);
+        if (host) (void) hipHostFree(host);
         if (st) (void) hipStreamDestroy(st);
     }
     template <typename T> int alloc(T **p, size_t n) {
@@ -700,8 +707,12 @@ int load_model(Model &m, int max_ctx_req) {
     m.max_ctx = (std::max(max_ctx_req, 1) + 255) / 256 * 256;
     FN_CK(hipSetDevice(0));
     FN_CK(hipStreamCreateWithFlags(&m.st, hipStreamNonBlocking));
-    unsigned *sw = nullptr;  // the status word's address, looked up now rather than under a graph capture
-    if (status_word(&sw)) return -1;
+    // the status word's address, looked up now rather than under a graph capture
+    if (status_word(&m.status)) return -1;
+    FN_CK(hipHostMalloc(&m.host, 2 * MAXT * sizeof(int32_t) + 64, hipHostMallocDefault));
+    m.h_ids = static_cast<int32_t *>(m.host);
+    m.h_am = m.h_ids + MAXT;
+    m.h_status = reinterpret_cast<unsigned *>(m.h_am + MAXT);
     if (load_qw1(m, "token_embd.weight", d.VOCAB, D, m.tok) || load_qw1(m, "output.weight", d.VOCAB, D, m.head) ||
         load_f32(m, "output_hc_norm.weight", HCD, &m.out_norm) ||
         load_qw1(m, "output_hc_down.weight", d.HCR, HCD, m.out_down) ||
@@ -966,7 +977,8 @@ int model_forward(const int32_t *tokens, int nt, float *logits, int32_t *argmax)
     for (int t = 0; t < nt; ++t)
         if (tokens[t] < 0 || tokens[t] >= m.d.VOCAB) FN_FAIL("forward: token id outside the vocabulary");
     const auto t0 = std::chrono::steady_clock::now();
-    FN_CK(hipMemcpyAsync(m.ids, tokens, (size_t) nt * 4, hipMemcpyHostToDevice, m.st));
+    std::memcpy(m.h_ids, tokens, (size_t) nt * 4);
+    FN_CK(hipMemcpyAsync(m.ids, m.h_ids, (size_t) nt * 4, hipMemcpyHostToDevice, m.st));
     const bool graphs = m.use_graphs && !m.dbg;
     if (graphs) {
         if (!m.graph[nt] && capture(m, nt)) return -1;
@@ -976,11 +988,15 @@ int model_forward(const int32_t *tokens, int nt, float *logits, int32_t *argmax)
     }
     if (logits)
         FN_CK(hipMemcpyAsync(logits, m.logits, (size_t) nt * m.d.VOCAB * 4, hipMemcpyDeviceToHost, m.st));
-    if (argmax) FN_CK(hipMemcpyAsync(argmax, m.am, (size_t) nt * 4, hipMemcpyDeviceToHost, m.st));
+    FN_CK(hipMemcpyAsync(m.h_am, m.am, (size_t) nt * 4, hipMemcpyDeviceToHost, m.st));
+    FN_CK(hipMemcpyAsync(m.h_status, m.status, sizeof(unsigned), hipMemcpyDeviceToHost, m.st));
     FN_CK(hipStreamSynchronize(m.st));
-    unsigned bits = 0;
-    if (status_read(&bits, true)) return -1;
-    if (bits) FN_FAIL("forward: a kernel recorded misuse (status bits " + std::to_string(bits) + ")");
+    if (const unsigned bits = *m.h_status) {
+        unsigned cleared = 0;
+        if (status_read(&cleared, true)) return -1;
+        FN_FAIL("forward: a kernel recorded misuse (status bits " + std::to_string(bits) + ")");
+    }
+    if (argmax) std::memcpy(argmax, m.h_am, (size_t) nt * 4);
     m.n_past += nt;
     m.last_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     return 0;
