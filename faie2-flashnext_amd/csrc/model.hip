@@ -48,6 +48,7 @@ constexpr int PLE_MAXH = 64;                 // n-gram heads the hashing kernel 
 constexpr int HC_KS = 4;                     // split of the hyper-connection down product along its rows
 constexpr int UPMIX_U = 8;                   // 8-value chunks per lane of the fused up-and-mix kernel (HCR <= 512)
 constexpr int UPMIX_HC = 8;                  // streams the fused up-and-mix kernel takes (HC <= 8)
+constexpr int UPMIX_ROWS = 64;               // rows of the up weight per workgroup of the fused up-and-mix kernel
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
@@ -122,17 +123,17 @@ __global__ void k_hc_mix(const float *__restrict__ a, const float *__restrict__ 
 
 // The up product and the mix in one pass, for a BF16 up weight U [HC D][HCR] (the reference model's): the
 // low-rank activation tt[t][r] = silu(lr[t][r] / HC) goes to the LDS, each row of U is summed by 8 lanes (lane li
-// takes the 8-value chunks li, li + 8, ... in order, then a 3-step xor tree), and the workgroup's 32 rows are the
-// HC streams of 32 / HC columns, so it finishes x for them: x[t][c] = (sum_s sigmoid(U[s D + c] . tt[t]) hn[t][s D
-// + c]) / HC, streams in order; workgroup 0 also writes inj.  Replaces k_hc_lowrank + the up GEMV + k_hc_mix
-// (faie2fn.cu:1266-1273, 873-888).  grid ceil(D HC / 32), 256 threads, LDS nt HCR + 8 x 32 floats
-__global__ void __launch_bounds__(256) k_hc_upmix(const uint8_t *__restrict__ U, size_t urs, const float *__restrict__ lr,
-                                                  int ks, int nt, int ldr, int HCR, int HC, int D,
-                                                  const float *__restrict__ hn, float *__restrict__ x,
-                                                  float *__restrict__ inj) {
+// takes the 8-value chunks li, li + 8, ... in order, then a 3-step xor tree), and the workgroup's UPMIX_ROWS rows
+// are the HC streams of UPMIX_ROWS / HC columns, so it finishes x for them:
+// x[t][c] = (sum_s sigmoid(U[s D + c] . tt[t]) hn[t][s D + c]) / HC, streams in order; workgroup 0 also writes
+// inj.  Replaces k_hc_lowrank + the up GEMV + k_hc_mix (faie2fn.cu:1266-1273, 873-888).
+// grid ceil(D HC / UPMIX_ROWS), 8 UPMIX_ROWS threads, LDS nt HCR + 8 UPMIX_ROWS floats
+__global__ void __launch_bounds__(UPMIX_ROWS * 8)
+    k_hc_upmix(const uint8_t *__restrict__ U, size_t urs, const float *__restrict__ lr, int ks, int nt, int ldr,
+               int HCR, int HC, int D, const float *__restrict__ hn, float *__restrict__ x, float *__restrict__ inj) {
     extern __shared__ float sm[];
-    float *tt = sm, *as = sm + nt * HCR;  // tt [nt][HCR], as [nt][32]
-    const int tid = threadIdx.x, cpb = 32 / HC, c0 = blockIdx.x * cpb;
+    float *tt = sm, *as = sm + nt * HCR;  // tt [nt][HCR], as [nt][UPMIX_ROWS]
+    const int tid = threadIdx.x, cpb = UPMIX_ROWS / HC, c0 = blockIdx.x * cpb;
     const int ri = tid >> 3, li = tid & 7, cc = ri / HC, s = ri - cc * HC, c = c0 + cc;
     const int nq = HCR / 8;
     // the lane's weight chunks li + 8 u, u < UPMIX_U, requested first: they do not depend on the activation
@@ -151,7 +152,7 @@ __global__ void __launch_bounds__(256) k_hc_upmix(const uint8_t *__restrict__ U,
 #pragma unroll
     for (int k = 0; k < UPMIX_HC; ++k)
         hv[k] = mixer && k < HC ? hn[(size_t) mt * HC * D + (size_t) k * D + mc] : 0.0f;
-    for (int i = tid; i < nt * HCR; i += 256) {
+    for (int i = tid; i < nt * HCR; i += UPMIX_ROWS * 8) {
         const int t = i / HCR, r = i - t * HCR;
         tt[i] = silu(lr_sum(lr, ks, nt, ldr, t, r) * (1.0f / HC));
     }
@@ -202,7 +203,7 @@ __global__ void __launch_bounds__(256) k_hc_upmix(const uint8_t *__restrict__ U,
                                                                        false));
             v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf,
                                                                        false));
-            if (li == 0) as[t * 32 + ri] = v;
+            if (li == 0) as[t * UPMIX_ROWS + ri] = v;
         }
     }
     __syncthreads();
@@ -211,7 +212,7 @@ __global__ void __launch_bounds__(256) k_hc_upmix(const uint8_t *__restrict__ U,
         float sum = 0.0f;
 #pragma unroll
         for (int k = 0; k < UPMIX_HC; ++k)
-            if (k < HC) sum += sigm(as[mt * 32 + cx * HC + k]) * hv[k];
+            if (k < HC) sum += sigm(as[mt * UPMIX_ROWS + cx * HC + k]) * hv[k];
         x[(size_t) mt * D + mc] = sum / HC;
     }
     if (inj && blockIdx.x == 0 && tid < nt * HC) {
@@ -542,7 +543,9 @@ int load_f32(Model &m, const std::string &name, size_t n, float **out) {
     const uint16_t *hb = reinterpret_cast<const uint16_t *>(t->data);
     for (size_t i = 0; i < n; ++i) {
         const uint32_t b = hb[i], sgn = (b >> 15) & 1, e = (b >> 10) & 31, f = b & 1023;
-        float v = e == 0 ? std::ldexp((float) f, -24) : (e == 31 ? (f ? NAN : INFINITY) : std::ldexp((float) (1024 + f), (int) e - 25));
+        const float v = e == 0    ? std::ldexp((float) f, -24)
+                        : e == 31 ? (f ? NAN : INFINITY)
+                                  : std::ldexp((float) (1024 + f), (int) e - 25);
         hf[i] = sgn ? -v : v;
     }
     FN_CK(hipMemcpy(*out, hf.data(), n * 4, hipMemcpyHostToDevice));
@@ -649,7 +652,8 @@ int read_dims(const Gguf &g, ModelDims &d) {
     if (d.ple_layers) {
         if ((int) num("ple.ngram_size", 3) != 3 || (int) num("ple.conv_kernel", 4) != 4)
             return bad("PLE: n-grams of 3 and conv kernel 4 are built");
-        if (d.ple_heads < 2 || d.ple_heads > PLE_MAXH || d.ple_hd < 32 || d.ple_hd % 32 || d.ple_heads * d.ple_hd != d.D)
+        if (d.ple_heads < 2 || d.ple_heads > PLE_MAXH || d.ple_hd < 32 || d.ple_hd % 32 ||
+            d.ple_heads * d.ple_hd != d.D)
             return bad("PLE: heads x values per head must be the embedding length, values per head a multiple of 32");
         if (d.ple_mult.size() != 3 || (int) d.ple_off.size() != d.ple_heads || (int) d.ple_size.size() != d.ple_heads)
             return bad("PLE: multipliers, head offsets and head sizes");
@@ -681,7 +685,8 @@ int load_ple(Model &m) {
         MLayer &L = m.L[il];
         L.ple = true;
         const std::string p = "blk." + std::to_string(il) + ".";
-        if (load_qw1(m, p + "ple_key.weight", HCD, D, L.ple_key) || load_qw1(m, p + "ple_value.weight", D, D, L.ple_val) ||
+        if (load_qw1(m, p + "ple_key.weight", HCD, D, L.ple_key) ||
+            load_qw1(m, p + "ple_value.weight", D, D, L.ple_val) ||
             load_f32(m, p + "ple_norm_key.weight", HCD, &L.ple_nk) ||
             load_f32(m, p + "ple_norm_query.weight", HCD, &L.ple_nq) ||
             load_f32(m, p + "ple_norm_conv.weight", HCD, &L.ple_nc) ||
@@ -751,7 +756,8 @@ int load_model(Model &m, int max_ctx_req) {
                 load_qw1(m, p + "attn_output.weight", D, (uint64_t) d.NH * HDK, L.o) ||
                 load_qw(m, {p + "indexer.q_proj.weight", p + "indexer.k_proj.weight"},
                         {(uint64_t) IXH * IXD, (uint64_t) IXD}, D, L.ixqk) ||
-                load_f32(m, p + "attn_q_norm.weight", HDK, &L.qn) || load_f32(m, p + "attn_k_norm.weight", HDK, &L.kn) ||
+                load_f32(m, p + "attn_q_norm.weight", HDK, &L.qn) ||
+                load_f32(m, p + "attn_k_norm.weight", HDK, &L.kn) ||
                 load_f32(m, p + "indexer.q_norm.weight", IXD, &L.ixqn) ||
                 load_f32(m, p + "indexer.k_norm.weight", IXD, &L.ixkn) || m.alloc(&L.Kc, cache) ||
                 m.alloc(&L.Vc, cache) || m.alloc(&L.IKc, (size_t) m.max_ctx * IXD) ||
@@ -806,10 +812,11 @@ int hc_read(Model &m, const QW &dinj, const QW &up, int nt) {
     const int ldr = dinj.L.rows;
     int ks = 1;
     if (gemv_split_launch(dinj.L, dinj.p, m.hn, nt, HC_KS, m.lr, &ks, m.st)) return -1;
-    if (up.L.type == QT_BF16 && 32 % d.HC == 0 && d.HC <= UPMIX_HC && d.HCR % 8 == 0 && d.HCR <= 64 * UPMIX_U) {
-        const int cpb = 32 / d.HC;
-        const size_t lds = ((size_t) nt * d.HCR + 8 * 32) * 4;
-        hipLaunchKernelGGL(k_hc_upmix, dim3((d.D + cpb - 1) / cpb), dim3(256), lds, m.st, up.p + up.L.off[0],
+    if (up.L.type == QT_BF16 && UPMIX_ROWS % d.HC == 0 && d.HC <= UPMIX_HC && d.HCR % 8 == 0 &&
+        d.HCR <= 64 * UPMIX_U) {
+        const int cpb = UPMIX_ROWS / d.HC;
+        const size_t lds = ((size_t) nt * d.HCR + 8 * UPMIX_ROWS) * 4;
+        hipLaunchKernelGGL(k_hc_upmix, dim3((d.D + cpb - 1) / cpb), dim3(UPMIX_ROWS * 8), lds, m.st, up.p + up.L.off[0],
                            up.L.rs[0], m.lr, ks, nt, ldr, d.HCR, d.HC, d.D, m.hn, m.x, inj ? m.inj : nullptr);
         FN_CK(hipGetLastError());
         return 0;
@@ -868,7 +875,8 @@ int ffn(Model &m, MLayer &L, int nt, const float *next_norm) {
     rt.shu = m.shu;
     rt.sha = m.sha;
     const int np = nt * d.NEU;
-    if (swiglu_launch(L.eg.L, L.eg.p, L.eu.L, L.eu.p, d.FFE, m.sel, np, d.NEU, m.x, m.act, m.st, nt > 1 ? nullptr : &rt) ||
+    if (swiglu_launch(L.eg.L, L.eg.p, L.eu.L, L.eu.p, d.FFE, m.sel, np, d.NEU, m.x, m.act, m.st,
+                      nt > 1 ? nullptr : &rt) ||
         gemv(L.sh_down, m.sha, nt, m.shd, m.st) || rows_launch(L.ed.L, L.ed.p, d.D, m.sel, np, 1, m.act, m.dpart, m.st))
         return -1;
     hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(hc_add_threads(d.D)), 0, m.st, m.h, m.shd, m.inj, d.D, d.HC,
@@ -889,8 +897,8 @@ int ple(Model &m, MLayer &L, int nt) {
     if (embed_launch(m.ple_table.L, m.ple_table.p, m.ple_rows, nt * d.ple_heads, 1, m.ple_emb, m.st) ||
         gemv(L.ple_key, m.ple_emb, nt, m.ple_k, m.st) || gemv(L.ple_val, m.ple_emb, nt, m.ple_v, m.st))
         return -1;
-    hipLaunchKernelGGL(k_ple_gate, dim3(nt, d.HC), dim3(hc_add_threads(d.D)), 0, m.st, m.ple_k, m.ple_v, m.h, L.ple_nk, L.ple_nq,
-                       L.ple_nc, d.D, d.eps, m.ple_gv, m.ple_gvn);
+    hipLaunchKernelGGL(k_ple_gate, dim3(nt, d.HC), dim3(hc_add_threads(d.D)), 0, m.st, m.ple_k, m.ple_v, m.h,
+                       L.ple_nk, L.ple_nq, L.ple_nc, d.D, d.eps, m.ple_gv, m.ple_gvn);
     hipLaunchKernelGGL(k_ple_conv, dim3((HCD + 255) / 256), dim3(256), 0, m.st, m.h, m.ple_gv, m.ple_gvn, L.ple_hist,
                        L.ple_conv, HCD, nt);
     FN_CK(hipGetLastError());
