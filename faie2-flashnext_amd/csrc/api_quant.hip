@@ -168,3 +168,15 @@ FN_API int fn_gemv_dev(uint32_t type, const uint8_t *packed, int rows, int cols,
     if (!fn::qlayout(type, rows, cols, L)) return -1;
     return fn::gemv_launch(L, packed, x, nt, y, work, work_bytes, (hipStream_t) stream);
 }
+
+FN_API int fn_gemv_group_dev(int n, const uint32_t *types, const int *rows, int cols, const uint8_t *const *packed,
+                             const float *x, int nt, float *const *y, void *stream) {
+    if (n < 1 || n > 4 || !types || !rows || !packed || !y) FN_FAIL("gemv group: 1 to 4 parts");
+    QLayout L[4];
+    fn::GemvPart g[4];
+    for (int i = 0; i < n; ++i) {
+        if (!fn::qlayout(types[i], rows[i], cols, L[i])) return -1;
+        g[i] = fn::GemvPart{&L[i], packed[i], y[i]};
+    }
+    return fn::gemv_group_launch(g, n, x, nt, (hipStream_t) stream);
+}

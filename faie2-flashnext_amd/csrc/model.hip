@@ -834,16 +834,16 @@ unsigned hc_add_threads(int D) { return (unsigned) std::min(1024, (D / 4 + 63) /
 int mixer(Model &m, MLayer &L, int nt) {
     const ModelDims &d = m.d;
     if (!L.attn) {
-        if (gemv(L.qkv, m.x, nt, m.qkv, m.st) || gemv(L.z, m.x, nt, m.zz, m.st) || gemv(L.ab, m.x, nt, m.abv, m.st))
-            return -1;
+        const GemvPart g[3] = {{&L.qkv.L, L.qkv.p, m.qkv}, {&L.z.L, L.z.p, m.zz}, {&L.ab.L, L.ab.p, m.abv}};
+        if (gemv_group_launch(g, 3, m.x, nt, m.st)) return -1;
         GdnBlock p{1, d.NKH, d.NVH, DSK, DSK, 0, 0, nt, RING, d.eps, m.pos, m.qkv, L.conv_w, L.ring, m.abv, L.dt,
                    L.ssm_a, L.S, m.zz, L.ssm_norm, m.on};
         if (gdn_block_launch(p, m.st)) return -1;
         return gemv(L.ssm_out, m.on, nt, m.y, m.st);
     }
-    if (gemv(L.q, m.x, nt, m.qg, m.st) || gemv(L.k, m.x, nt, m.kk, m.st) || gemv(L.v, m.x, nt, m.vv, m.st) ||
-        gemv(L.ixqk, m.x, nt, m.iqk, m.st))
-        return -1;
+    const GemvPart g[4] = {{&L.q.L, L.q.p, m.qg}, {&L.k.L, L.k.p, m.kk}, {&L.v.L, L.v.p, m.vv},
+                           {&L.ixqk.L, L.ixqk.p, m.iqk}};
+    if (gemv_group_launch(g, 4, m.x, nt, m.st)) return -1;
     AttnDecode p{1, d.NH, d.NKV, HDK, d.NROT, nt, m.max_ctx, m.nsplit, d.theta, d.eps, m.pos, m.qg, m.kk, m.vv, L.qn,
                  L.kn, L.Kc, L.Vc, m.work, m.work_bytes, m.og};
     QsaIndexer ix{1, nt, m.max_ctx, d.top, d.NROT, d.theta, d.eps, m.pos, m.iqk, L.ixqn, L.ixkn, L.IKc, L.BKc};
@@ -853,9 +853,9 @@ int mixer(Model &m, MLayer &L, int nt) {
 
 int ffn(Model &m, MLayer &L, int nt, const float *next_norm) {
     const ModelDims &d = m.d;
-    if (gemv(L.rsg, m.x, nt, m.rsgv, m.st) || gemv(L.sh_gate, m.x, nt, m.shg, m.st) ||
-        gemv(L.sh_up, m.x, nt, m.shu, m.st))
-        return -1;
+    const GemvPart g[3] = {{&L.rsg.L, L.rsg.p, m.rsgv}, {&L.sh_gate.L, L.sh_gate.p, m.shg},
+                           {&L.sh_up.L, L.sh_up.p, m.shu}};
+    if (gemv_group_launch(g, 3, m.x, nt, m.st)) return -1;
     // routing (softmax top-k of the router logits, faie2fn.cu:1747-1798): for one token inside the experts' gate/up
     // kernel, which then also writes the picks, their weights and the shared expert's SwiGLU (one kernel fewer); for
     // several tokens in its own kernel (each of their gate/up workgroups would route again)

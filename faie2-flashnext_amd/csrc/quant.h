@@ -75,6 +75,18 @@ int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt,
 int gemv_split_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, int ks, float *part,
                       int *ks_out, hipStream_t st);
 
+// Several weights with the same cols over one x (y_i[t][r] = W_i[r] . x[t]): one launch when their formats form one
+// of the sets built as a group (quant_grp.hip) and x of nt tokens fits the LDS, else one GEMV launch per weight.
+// A grouped launch sums every row with the group's lanes per row (the GEMV's arithmetic with that lpr), so a
+// weight's results may differ in the last bits from its own GEMV's; which path runs depends on the shapes and
+// formats only, never on nt.
+struct GemvPart {
+    const QLayout *L;
+    const uint8_t *packed;
+    float *y;
+};
+int gemv_group_launch(const GemvPart *parts, int n, const float *x, int nt, hipStream_t st);
+
 // Rows of a packed weight selected on the device (the model forward's embedding and routed experts):
 //   embed_launch: out[t][k * cols + c] = W[ids[t]][c] for k < copies (the GGUF decode, bit for bit);
 //   rows_launch: out[p][r] = W[e_p * R + r] . x[p / xdiv] for r < R, p < npairs, e_p = sel[p] (sel null: e_p = 0),

@@ -714,12 +714,12 @@ __device__ __forceinline__ void flush_rows(int s, int lane, int rows, float *acc
 template <uint32_t TY, int NT, int LPR>
 __device__ __forceinline__ void gemv_walk_short(const PP &P, int rows, int g0, int g1, int ng, int NS, int nws,
                                                 int NB, const float *__restrict__ x, int cols,
-                                                float *__restrict__ out, float4 *xs) {
+                                                float *__restrict__ out, float4 *xs, int blk) {
     constexpr int NW = Q<TY>::NW, U = Q<TY>::U, XB = NT <= 2 ? 4 : 8;
     const int tid = threadIdx.x, lane = tid & 63;
     // the wave's batches in order: (s, j), then (s1, j1) = next(s, j), ...; wave-uniform, so the row reductions run
     // on whole waves
-    int s = blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(tid >> 6), j = 0, s1, j1;
+    int s = blk * 8 + __builtin_amdgcn_readfirstlane(tid >> 6), j = 0, s1, j1;
     const auto next = [NB, nws](int s_, int j_, int &sn, int &jn) {
         sn = j_ + 1 == NB ? s_ + nws : s_;
         jn = j_ + 1 == NB ? 0 : j_ + 1;
@@ -840,7 +840,7 @@ __global__ void __launch_bounds__(512) k_gemv(PP P, int rows, int G, int gps, co
     out += (size_t) blockIdx.y * NT * rows;
     tab_fill<TY>(threadIdx.x, 512);  // published by the walk's barrier after the x staging
     if constexpr (DEEP) gemv_walk_deep<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs);
-    else gemv_walk_short<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs);
+    else gemv_walk_short<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs, blockIdx.x);
 }
 
 // k_gemv_c, for an x too large for the LDS: x goes through it in chunks of kc groups (a multiple of LPR, so a
@@ -940,6 +940,96 @@ int gemv_nt(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, f
     }
     FN_CK(hipGetLastError());
     return 0;
+}
+
+// Grouped GEMV: weights of different formats and the same cols over one x, in one launch.  Workgroups
+// [0, nwg_0) walk part 0, the next nwg_1 part 1, and so on; each stages x itself and walks its part's row-sets
+// (wave w of the part's workgroups: row-sets w, w + 8 nwg, ...) with the short walk, LPR lanes per row for every
+// part.  A row's arithmetic is the GEMV's with that LPR, whatever the grid's split among the parts.
+struct GPart {
+    PP P;
+    int rows, nwg;
+    float *out;
+};
+template <int N> struct GParts {
+    GPart p[N];
+};
+
+template <int NT, int LPR, int I, int N, uint32_t TY, uint32_t... R>
+__device__ __forceinline__ void grp_walk(const GParts<N> &ps, int blk, int G, const float *__restrict__ x, int cols,
+                                         float4 *xs) {
+    if (blk < ps.p[I].nwg) {
+        constexpr int U = Q<TY>::U, RPW = 64 / LPR;
+        const GPart &p = ps.p[I];
+        tab_fill<TY>(threadIdx.x, 512);  // published by the walk's barrier after the x staging
+        gemv_walk_short<TY, NT, LPR>(p.P, p.rows, 0, G, G, (p.rows + RPW - 1) / RPW, p.nwg * 8,
+                                     (G + LPR * U - 1) / (LPR * U), x, cols, p.out, xs, blk);
+    } else if constexpr (sizeof...(R) > 0) {
+        grp_walk<NT, LPR, I + 1, N, R...>(ps, blk - ps.p[I].nwg, G, x, cols, xs);
+    }
+}
+
+template <int NT, int LPR, uint32_t... TS>
+__global__ void __launch_bounds__(512) k_gemv_grp(GParts<sizeof...(TS)> ps, int G, const float *__restrict__ x,
+                                                    int cols) {
+    extern __shared__ float4 xs[];
+    grp_walk<NT, LPR, 0, sizeof...(TS), TS...>(ps, blockIdx.x, G, x, cols, xs);
+}
+
+// parts in the order of TS; the caller has checked that x of NT tokens fits the LDS beside the formats' tables.
+// The grid is the workgroups resident at once (or fewer: one row-set per wave at most), shared among the parts by
+// their packed bytes, at least one workgroup each.
+template <int NT, int LPR, uint32_t... TS>
+int gemv_grp_nt(const QLayout *const *L, const PP *P, float *const *y, const float *x, hipStream_t st) {
+    constexpr int N = sizeof...(TS), RPW = 64 / LPR;
+    const int G = L[0]->cols / 32;
+    const size_t lds = (size_t) G * xs_stride(NT) * sizeof(float4), tabs = (size_t) (tab_lds<TS>() + ...);
+    static int by_regs = 0;
+    if (!by_regs) {
+        int n = 0;
+        FN_CK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv_grp<NT, LPR, TS...>, 512, 0));
+        by_regs = std::max(1, n);
+    }
+    const int per_cu = std::min(by_regs, std::max(1, (int) (kLdsPerCu / (lds + tabs))));
+    const int budget = device_cus() * per_cu;
+    GParts<N> ps;
+    int need[N], sum_need = 0;
+    double bytes = 0;
+    for (int i = 0; i < N; ++i) {
+        need[i] = ((L[i]->rows + RPW - 1) / RPW + 7) / 8;
+        sum_need += need[i];
+        bytes += (double) L[i]->bytes;
+    }
+    int nwg = 0;
+    for (int i = 0; i < N; ++i) {
+        int w = need[i];
+        if (sum_need > budget) w = std::min(need[i], std::max(1, (int) (budget * (double) L[i]->bytes / bytes)));
+        ps.p[i] = GPart{P[i], L[i]->rows, w, y[i]};
+        nwg += w;
+    }
+    hipLaunchKernelGGL((k_gemv_grp<NT, LPR, TS...>), dim3((unsigned) nwg), dim3(512), lds, st, ps, G, x, L[0]->cols);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
+template <int LPR, uint32_t... TS>
+int gemv_grp_l(const QLayout *const *L, const PP *P, float *const *y, const float *x, int nt, hipStream_t st) {
+    switch (nt) {
+        case 1: return gemv_grp_nt<1, LPR, TS...>(L, P, y, x, st);
+        case 2: return gemv_grp_nt<2, LPR, TS...>(L, P, y, x, st);
+        case 3: return gemv_grp_nt<3, LPR, TS...>(L, P, y, x, st);
+        case 4: return gemv_grp_nt<4, LPR, TS...>(L, P, y, x, st);
+        case 5: return gemv_grp_nt<5, LPR, TS...>(L, P, y, x, st);
+        case 6: return gemv_grp_nt<6, LPR, TS...>(L, P, y, x, st);
+        case 7: return gemv_grp_nt<7, LPR, TS...>(L, P, y, x, st);
+        case 8: return gemv_grp_nt<8, LPR, TS...>(L, P, y, x, st);
+        default: FN_FAIL("gemv: nt must be 1..8");
+    }
+}
+
+template <uint32_t... TS>
+int gemv_grp(const QLayout *const *L, const PP *P, float *const *y, const float *x, int nt, int lpr, hipStream_t st) {
+    return lpr == 32 ? gemv_grp_l<32, TS...>(L, P, y, x, nt, st) : gemv_grp_l<64, TS...>(L, P, y, x, nt, st);
 }
 
 template <uint32_t TY, int LPR>

@@ -37,7 +37,7 @@ SYMBOLS = (
     "fn_attn_qsa_dev", "fn_attn_qsa_work_bytes", "fn_ix_blocks_dev", "fn_test_attn_qsa",
     "fn_gemv_packed_bytes", "fn_gemv_pack_dev", "fn_dequant_dev", "fn_gemv_work_bytes", "fn_gemv_dev",
     "fn_gdn_verify_dev", "fn_advance_by_dev", "fn_gdn_block_xab_dev",
-    "fn_attn_noalloc_dev", "fn_dev_status", "fn_model_dims",
+    "fn_attn_noalloc_dev", "fn_dev_status", "fn_model_dims", "fn_gemv_group_dev",
 )
 
 # the shapes fn_model_dims writes, in order (include/faie2fn.h section 6)
@@ -149,6 +149,7 @@ class FN:
         d.fn_gemv_work_bytes.restype = sz
         d.fn_gemv_work_bytes.argtypes = [u32, i, i, i]
         d.fn_gemv_dev.argtypes = [u32, VP, i, i, VP, i, VP, VP, sz, VP]
+        d.fn_gemv_group_dev.argtypes = [i, VP, VP, i, VP, VP, i, VP, VP]
 
     def check(self, rc):
         if rc != 0:
@@ -363,6 +364,14 @@ class FN:
 
     def gemv_dev(self, qtype, packed, rows, cols, x, nt, y, work, work_bytes, stream=0):
         self.check(self.d.fn_gemv_dev(int(qtype), packed, rows, cols, x, nt, y, work, work_bytes, stream))
+
+    def gemv_group_dev(self, types, rows, cols, packed, x, nt, ys, stream=0):
+        n = len(types)
+        ty = (C.c_uint32 * n)(*[int(t) for t in types])
+        rw = (C.c_int * n)(*[int(r) for r in rows])
+        pk = (VP * n)(*packed)
+        yp = (VP * n)(*ys)
+        self.check(self.d.fn_gemv_group_dev(n, ty, rw, cols, pk, x, nt, yp, stream))
 
     # ---- path engine ----
     def path_init(self, B, nl, attn_every=4, nkh=16, nvh=32, nq=16, nkv=2, max_ctx=4096, head_map=0, gate_act=0,

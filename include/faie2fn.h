@@ -308,6 +308,16 @@ size_t fn_gemv_work_bytes(uint32_t type, int rows, int cols, int nt);
 int fn_gemv_dev(uint32_t type, const uint8_t *packed, int rows, int cols, const float *x, int nt, float *y,
                 float *work, size_t work_bytes, void *stream);
 
+/* Several packed weights of the same cols over one x (new; the reference runs the projections that read one
+ * activation row as separate GEMVs, faie2fn.cu:2386-2403): y[i] [nt][rows[i]] = W_i x for i < n (1..4).  One
+ * launch, x staged once per workgroup, when the formats form one of the built sets ({IQ4_XS, IQ3_S, BF16},
+ * {IQ4_XS, Q6_K, BF16}, {IQ4_XS, IQ4_XS, Q6_K, BF16}, in any order) and x of nt tokens fits the LDS; otherwise one
+ * fn_gemv_dev-like launch per weight.  A grouped launch sums each row over at least 32 lanes, so a weight whose own
+ * plan takes 16 lanes per row may differ from fn_gemv_dev in the last bits; the path taken depends on the formats
+ * and shapes only, never on nt (token t gets the bits of a one-token call).  No work buffer. */
+int fn_gemv_group_dev(int n, const uint32_t *types, const int *rows, int cols, const uint8_t *const *packed,
+                      const float *x, int nt, float *const *y, void *stream);
+
 /* ======================================================================================================
  * 6. Model (new beside the reference's fn_load / fn_forward, faie2fn.cu:2524, 2733): what fn_load reads.
  *    Shapes come from the GGUF metadata (<general.architecture>.* keys: embedding_length, block_count,

@@ -211,3 +211,26 @@ def test_noalloc_attn_rejects_oversize(fnlib):
     # the decode shapes of the benchmark fit: B = 16 at 32K and B = 1 at 128K with their automatic split counts
     for B, L in ((16, 32768), (1, 131072), (1, 4096)):
         assert fnlib.attn_work_bytes(B, 16, 1, fnlib.attn_nsplit(B, 2, 1, L)) <= fn.NOALLOC_SCRATCH_BYTES
+
+
+def test_gemv_group_refuses_bad_arguments(fnlib):
+    """fn_gemv_group_dev checks its parts before any launch: 1 to 4 of them, formats and shapes the library reads,
+    no null weight, output or x."""
+    d = fnlib.d
+    assert d.fn_gemv_group_dev(0, None, None, 2560, None, None, 1, None, None) == -1
+    assert d.fn_gemv_group_dev(5, None, None, 2560, None, None, 1, None, None) == -1
+    assert b"1 to 4 parts" in d.fn_error()
+    ty = (C.c_uint32 * 2)(23, 30)
+    rows = (C.c_int * 2)(64, 8)
+    fake = (C.c_void_p * 2)(4096, 8192)
+    assert d.fn_gemv_group_dev(2, ty, rows, 2560, fake, None, 1, fake, None) == -1  # x null
+    assert d.fn_gemv_group_dev(2, ty, rows, 2500, fake, 4096, 1, fake, None) == -1  # 2500: not whole blocks
+    assert b"unsupported shape" in d.fn_error()
+    bad = (C.c_uint32 * 2)(23, 99)
+    assert d.fn_gemv_group_dev(2, bad, rows, 2560, fake, 4096, 1, fake, None) == -1
+    assert b"unsupported type" in d.fn_error()
+    nul = (C.c_void_p * 2)(4096, None)
+    assert d.fn_gemv_group_dev(2, ty, rows, 2560, nul, 4096, 1, fake, None) == -1
+    assert b"null part" in d.fn_error()
+    assert d.fn_gemv_group_dev(2, ty, rows, 2560, fake, 4096, 9, fake, None) == -1
+    assert b"nt must be" in d.fn_error()

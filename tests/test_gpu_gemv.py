@@ -239,3 +239,69 @@ def test_bench_gemv_runs(fnlib):
     ms = fnlib.bench_gemv(23, 10240, 2560, nt=1, iters=8)
     assert 0.0 < ms < 5.0
 
+
+
+# Grouped launches (fn_gemv_group_dev): the model's projections that read one activation row, at the reference
+# model's width (DeltaNet qkv / z / alpha-beta with z in either format, attention q / k / v / indexer, the FFN's
+# router / shared gate / shared up), at the benchmark configs' 2048, at a small width, and a set that is not built
+# (one launch per weight).
+GROUPS = [
+    ("deltanet, z IQ3_S", [("IQ4_XS", 10240), ("IQ3_S", 6144), ("BF16", 96)], 2560),
+    ("deltanet, z Q6_K", [("IQ4_XS", 10240), ("Q6_K", 6144), ("BF16", 96)], 2560),
+    ("attention", [("IQ4_XS", 12288), ("IQ4_XS", 512), ("Q6_K", 512), ("BF16", 640)], 2560),
+    ("ffn", [("BF16", 513), ("IQ4_XS", 640), ("IQ3_S", 640)], 2560),
+    ("width 2048", [("BF16", 64), ("IQ4_XS", 8192), ("Q6_K", 4096)], 2048),
+    ("width 256", [("IQ4_XS", 40), ("IQ3_S", 24), ("BF16", 8)], 256),
+    ("not built", [("Q8_0", 300), ("BF16", 77)], 2560),
+]
+
+
+def _group_run(fnlib, types, rows, raws, cols, x):
+    nt = x.shape[0]
+    packs = []
+    for t, r, raw in zip(types, rows, raws):
+        draw = hiprt.Buf.like(raw)
+        p = hiprt.Buf(fnlib.gemv_packed_bytes(t, r, cols), np.uint8)
+        fnlib.gemv_pack_dev(t, draw.ptr, r, cols, p.ptr)
+        packs.append(p)
+    dx = hiprt.Buf.like(x)
+    ys = [hiprt.Buf.empty((nt, r)) for r in rows]
+    fnlib.gemv_group_dev(types, rows, cols, [p.ptr for p in packs], dx.ptr, nt, [y.ptr for y in ys])
+    hiprt.sync()
+    return [y.download() for y in ys]
+
+
+@pytest.mark.parametrize("name,parts,cols", GROUPS)
+@pytest.mark.parametrize("nt", [1, 3, 8])
+def test_gemv_group(fnlib, name, parts, cols, nt):
+    """Every weight of a group within 1e-5 of float64 math; a weight whose own plan sums a row over as many lanes as
+    the group (at least 32, the fewest of the parts' plans) gets its own GEMV's bits, and so does every weight of a
+    set that is not built."""
+    types = [TYPES[n] for n, _ in parts]
+    rows = [r for _, r in parts]
+    _say(f"gemv group {name}: {parts} cols={cols} nt={nt}")
+    raws = [random_finite(t, r, cols, RNG) for t, r in zip(types, rows)]
+    x = RNG.standard_normal((nt, cols)).astype(np.float32)
+    ys = _group_run(fnlib, types, rows, raws, cols, x)
+    lprs = [fnlib.gemv_plan(t, r, cols)[4] for t, r in zip(types, rows)]
+    glpr = min(max(32, v) for v in lprs)
+    for t, r, raw, y, lpr in zip(types, rows, raws, ys, lprs):
+        assert oracle.relerr(y, oracle.gemv(t, raw, r, cols, x)) <= TOL, (t, r)
+        if lpr == glpr or name == "not built":
+            assert np.array_equal(y, fnlib.gemv(t, raw, r, cols, x)), (t, r)
+
+
+def test_gemv_group_tokens_independent(fnlib):
+    """Token t of an 8-token grouped call equals a one-token grouped call on x[t]."""
+    name, parts, cols = GROUPS[2]
+    types = [TYPES[n] for n, _ in parts]
+    rows = [r for _, r in parts]
+    _say(f"gemv group {name}: nt=8 vs 8 x nt=1")
+    raws = [random_finite(t, r, cols, RNG) for t, r in zip(types, rows)]
+    x = RNG.standard_normal((8, cols)).astype(np.float32)
+    ys = _group_run(fnlib, types, rows, raws, cols, x)
+    for i in range(8):
+        one = _group_run(fnlib, types, rows, raws, cols, x[i:i + 1])
+        for y, y1 in zip(ys, one):
+            assert np.array_equal(y[i], y1[0])
+
