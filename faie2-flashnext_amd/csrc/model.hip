@@ -196,12 +196,14 @@ __global__ void __launch_bounds__(UPMIX_ROWS * 8)
     for (int t = 0; t < MAXT; ++t) {
         if (t < nt) {
             // the 8 lanes of a row: quad sums by DPP quad_perm (xor 1, xor 2), then lane 0 of the row adds lane 4's
+            // (row_ror by n reads lane l - n of the 16-lane DPP row, so ror 12 reads l + 4: lane 0 gets lane 4,
+            // lane 8 gets lane 12, each from its own 8-lane row)
             float v = acc[t];
             v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xf, 0xf,
                                                                        false));
             v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xf, 0xf,
                                                                        false));
-            v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf,
+            v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x12C, 0xf, 0xf,
                                                                        false));
             if (li == 0) as[t * UPMIX_ROWS + ri] = v;
         }

@@ -84,7 +84,19 @@ class Model:
                 else:
                     m = oracle.dequant(ty, np.frombuffer(raw, np.uint8), rows, cols)
                 mats.append(m.astype(np.float64))
-            self._w[key] = np.concatenate(mats, axis=0)
+            self._w[key] = mats[0] if len(mats) == 1 else np.concatenate(mats, axis=0)
+        return self._w[key]
+
+    def rows(self, name, e, R):
+        """float64 rows [e R, (e + 1) R) of a tensor (one expert of a stacked expert tensor), decoded from those rows'
+        bytes alone (GGUF rows are whole blocks, so a row range is a byte range)"""
+        key = (name, e)
+        if key not in self._w:
+            ty, dims, raw = self.t[name]
+            cols = dims[0]
+            rb = len(raw) // int(np.prod(dims[1:]))
+            part = np.frombuffer(raw, np.uint8)[e * R * rb:(e + 1) * R * rb]
+            self._w[key] = oracle.dequant(ty, part, R, cols).astype(np.float64)
         return self._w[key]
 
     def f32(self, name):
@@ -177,15 +189,13 @@ class Model:
         sha = _silu(x @ self.w(p + "ffn_gate_shexp.weight").T) * (x @ self.w(p + "ffn_up_shexp.weight").T)
         shd = sha @ self.w(p + "ffn_down_shexp.weight").T
         sel, wsel = self.route(rsg[:, : self.NE])
-        Wg, Wu, Wd = self.w(p + "ffn_gate_exps.weight"), self.w(p + "ffn_up_exps.weight"), \
-            self.w(p + "ffn_down_exps.weight")
         y = np.zeros((nt, self.D))
         for t in range(nt):
             for k in range(self.NEU):
                 e = sel[t, k]
-                g = Wg[e * self.FFE:(e + 1) * self.FFE] @ x[t]
-                u = Wu[e * self.FFE:(e + 1) * self.FFE] @ x[t]
-                y[t] += wsel[t, k] * (Wd[e * self.D:(e + 1) * self.D] @ (_silu(g) * u))
+                g = self.rows(p + "ffn_gate_exps.weight", e, self.FFE) @ x[t]
+                u = self.rows(p + "ffn_up_exps.weight", e, self.FFE) @ x[t]
+                y[t] += wsel[t, k] * (self.rows(p + "ffn_down_exps.weight", e, self.D) @ (_silu(g) * u))
         y += _sig(rsg[:, self.NE:self.NE + 1]) * shd
         return y, sel
 

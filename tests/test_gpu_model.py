@@ -173,3 +173,38 @@ def test_model_quantized_hyper_connections(fnlib, tmp_path):
             assert _rel(lg, want) <= TOL, (k, nt, _rel(lg, want))
     finally:
         fnlib.free()
+
+
+# the reference model's widths in two layers (a DeltaNet layer, then an attention layer that carries the n-gram
+# embedding): hidden 2560, 16 / 48 DeltaNet heads, 24 / 2 attention heads, hyper-connections 4 of rank 320, experts
+# and the shared expert of 640; fewer experts and a small vocabulary keep the float64 oracle quick
+MEDIUM_DIMS = dict(ms.TINY_DIMS, D=2560, NL=2, attn_every=2, NH=24, NKV=2, NE=8, NEU=2, FFE=640, FFS=640, NKH=16,
+                   NVH=48, HC=4, HCR=320, VOCAB=4096, ple_hd=320, ple_heads_per_ngram=4)
+
+
+def test_model_reference_widths(fnlib, tmp_path):
+    """Every kernel of the forward at the reference model's row lengths and projection shapes (the grouped
+    projections at 10240 / 6144 / 96 and 12288 / 512 / 512 / 640 rows, 80-group rows in the GEMVs and expert rows,
+    the up-and-mix kernel at rank 320), one- and several-token calls, within 1e-5 of the oracle."""
+    p = str(tmp_path / "medium.gguf")
+    kv, ts = ms.write_model(p, MEDIUM_DIMS, seed=21)
+    _say("model forward: reference widths, 2 layers, 20 tokens in calls of 1, 8, 3, 8")
+    fnlib.load(p, "", max_ctx=256)
+    try:
+        ref = om.Model(kv, ts, max_ctx=256)
+        ids = np.random.default_rng(6).integers(0, MEDIUM_DIMS["VOCAB"], size=20)
+        ids[[4, 13]] = MEDIUM_DIMS["ple_eos"]
+        i = 0
+        for nt in (1, 8, 3, 8):
+            am, lg = fnlib.forward(ids[i:i + nt], logits=True)
+            want, want_am, _, _ = ref.forward(ids[i:i + nt])
+            e = _rel(lg, want)
+            _say(f"  nt={nt}: logits error {e:.3e}")
+            assert e <= TOL, (i, nt, e)
+            for t in range(nt):
+                top2 = np.sort(want[t])[-2:]
+                if top2[1] - top2[0] > 1e-4 * abs(top2[1]):
+                    assert am[t] == want_am[t], (i, t)
+            i += nt
+    finally:
+        fnlib.free()
