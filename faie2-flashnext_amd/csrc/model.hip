@@ -878,12 +878,21 @@ int ffn(Model &m, MLayer &L, int nt, const float *next_norm) {
     rt.sha = m.sha;
     const int np = nt * d.NEU;
     if (swiglu_launch(L.eg.L, L.eg.p, L.eu.L, L.eu.p, d.FFE, m.sel, np, d.NEU, m.x, m.act, m.st,
-                      nt > 1 ? nullptr : &rt) ||
-        gemv(L.sh_down, m.sha, nt, m.shd, m.st) || rows_launch(L.ed.L, L.ed.p, d.D, m.sel, np, 1, m.act, m.dpart, m.st))
+                      nt > 1 ? nullptr : &rt))
         return -1;
+    // the experts' down rows, the shared expert's down row and their weighted sum in one kernel where it is built
+    // for the formats (the reference model's are), else the rows, a GEMV, and the sum inside the stream write
+    const bool fused = moe_down_supported(L.ed.L, L.sh_down.L, d.D);
+    if (fused) {
+        if (moe_down_launch(L.ed.L, L.ed.p, L.sh_down.L, L.sh_down.p, d.D, m.sel, m.wsel, d.NEU, m.act, m.sha, m.rsgv,
+                            d.NE, nt, m.shd, m.st))
+            return -1;
+    } else if (gemv(L.sh_down, m.sha, nt, m.shd, m.st) ||
+               rows_launch(L.ed.L, L.ed.p, d.D, m.sel, np, 1, m.act, m.dpart, m.st)) {
+        return -1;
+    }
     hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(hc_add_threads(d.D)), 0, m.st, m.h, m.shd, m.inj, d.D, d.HC,
-                       m.dpart, m.wsel,
-                       d.NEU, m.rsgv, d.NE, next_norm, d.eps, m.hn);
+                       fused ? nullptr : m.dpart, m.wsel, d.NEU, m.rsgv, d.NE, next_norm, d.eps, m.hn);
     FN_CK(hipGetLastError());
     return 0;
 }

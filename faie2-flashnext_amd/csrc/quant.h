@@ -114,4 +114,13 @@ int swiglu_launch(const QLayout &Lg, const uint8_t *pg, const QLayout &Lu, const
                   const int32_t *sel, int npairs, int xdiv, const float *x, float *act, hipStream_t st,
                   const RouteIn *route = nullptr);
 
+// The MoE output of nt tokens in one launch: y[t][r] = sigmoid(rsg[t][NE]) (Ws[r] . sha[t]) + the sum over k < NEU,
+// in order, of wsel[t][k] (We[sel[t][k] R + r] . act[t NEU + k]), r < R; We the stacked experts' down weights
+// (rows of cols = FFE values), Ws the shared expert's (R x cols, Q8_0), each dot product with the arithmetic of
+// rows_launch.  moe_down_supported: the formats and shapes this kernel is built for (else: rows_launch and a GEMV).
+bool moe_down_supported(const QLayout &Le, const QLayout &Ls, int R);
+int moe_down_launch(const QLayout &Le, const uint8_t *pe, const QLayout &Ls, const uint8_t *ps, int R,
+                    const int32_t *sel, const float *wsel, int NEU, const float *act, const float *sha, const float *rsg,
+                    int NE, int nt, float *y, hipStream_t st);
+
 }  // namespace fn

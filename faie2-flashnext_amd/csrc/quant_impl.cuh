@@ -1091,13 +1091,16 @@ __global__ void __launch_bounds__(256) k_embed(PP P, int G, int cols, const int3
     }
 }
 
-// row r of expert sel[p] (R rows per expert) against x[p / xdiv]: 16 lanes per row, 4 rows per wave, 16 rows per
-// workgroup; lane li sums its groups li, li + 16, ... in order.  grid (ceil(R / 16), npairs), 256 threads.
-// SWIGLU: the gate row of Wg and the up row of Wu, out = silu(g) * u.
+// row r of expert sel[p] (R rows per expert) against x[p / xdiv]: 16 lanes per row; lane li sums its groups li,
+// li + 16, ... in order, then the 16 lanes are summed.  Plain rows: 4 rows per wave, 16 per workgroup.
+// SWIGLU: the gate row of Wg and the up row of Wu, out = silu(g) * u; lanes 0-15 of each 32-lane half of a wave
+// take the gate row and lanes 16-31 the up row (2 rows per wave, 8 per workgroup), and the up sum crosses over by a
+// swizzle, so every lane decodes one weight.  grid (ceil(R / rows per workgroup), npairs), 256 threads.
 // One memory round trip before the arithmetic: the lane's first ROWS_PRE groups of weight words, the x row (into
 // LDS, group-major with an odd float4 stride so that a row's 16 lanes read distinct bank quads) and the format's
 // codebook are all requested before the one barrier.  LDS: 9 float4 per group of x.
 constexpr int ROWS_PRE = 5;
+template <bool SWIGLU> constexpr int rows_per_wg() { return SWIGLU ? 8 : 16; }
 template <uint32_t TY, bool SWIGLU>
 __global__ void __launch_bounds__(256) k_rows(PP Pg, PP Pu, int R, int nexp, int G, int cols,
                                               const int32_t *__restrict__ sel, int xdiv, const float *__restrict__ x,
@@ -1106,20 +1109,17 @@ __global__ void __launch_bounds__(256) k_rows(PP Pg, PP Pu, int R, int nexp, int
     __shared__ int e_sh;
     constexpr int NW = Q<TY>::NW;
     const int p = blockIdx.y, tid = threadIdx.x, lane = tid & 63, li = lane & 15;
-    const int r = blockIdx.x * 16 + (tid >> 6) * 4 + (lane >> 4);
+    const bool up = SWIGLU && (lane & 16);  // (SWIGLU) this lane sums the up row
+    const int r = SWIGLU ? blockIdx.x * 8 + (tid >> 6) * 2 + (lane >> 5)
+                         : blockIdx.x * 16 + (tid >> 6) * 4 + (lane >> 4);
     const bool routed = SWIGLU && rt.rsg != nullptr;
-    uint32_t wg[ROWS_PRE][NW], wu[ROWS_PRE][NW];
-    RP rg, ru;
+    uint32_t w[ROWS_PRE][NW];
+    RP rw;
     const auto load_pre = [&](int e) {  // an id outside the weight reads its last expert
         const int row = min(max(e, 0), nexp - 1) * R + min(r, R - 1);
-        rg = row_planes(Pg, row);
-        ru = row_planes(Pu, row);
+        rw = row_planes(up ? Pu : Pg, row);
 #pragma unroll
-        for (int k = 0; k < ROWS_PRE; ++k) {
-            const int g = min(li + 16 * k, G - 1);  // (clamped: a valid address, its value unused past G)
-            Q<TY>::load(rg, g, wg[k]);
-            if constexpr (SWIGLU) Q<TY>::load(ru, g, wu[k]);
-        }
+        for (int k = 0; k < ROWS_PRE; ++k) Q<TY>::load(rw, min(li + 16 * k, G - 1), w[k]);  // (clamped: valid address)
     };
     if (!routed) load_pre(sel ? sel[p] : 0);
     const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t) (p / xdiv) * cols);
@@ -1142,30 +1142,23 @@ __global__ void __launch_bounds__(256) k_rows(PP Pg, PP Pu, int R, int nexp, int
     __syncthreads();
     if (routed) load_pre(e_sh);
     const TabT<TY> T;
-    float ag = 0.0f, au = 0.0f;
+    float a = 0.0f;
 #pragma unroll
     for (int k = 0; k < ROWS_PRE; ++k) {
         const int g = li + 16 * k;
-        if (g < G) {
-            accumulate<TY, 1>(wg[k], g, xs + 9 * g, &ag, T);
-            if constexpr (SWIGLU) accumulate<TY, 1>(wu[k], g, xs + 9 * g, &au, T);
-        }
+        if (g < G) accumulate<TY, 1>(w[k], g, xs + 9 * g, &a, T);
     }
     for (int g = li + 16 * ROWS_PRE; g < G; g += 16) {  // rows longer than 80 groups
-        uint32_t w[NW];
-        Q<TY>::load(rg, g, w);
-        accumulate<TY, 1>(w, g, xs + 9 * g, &ag, T);
-        if constexpr (SWIGLU) {
-            Q<TY>::load(ru, g, w);
-            accumulate<TY, 1>(w, g, xs + 9 * g, &au, T);
-        }
+        uint32_t wn[NW];
+        Q<TY>::load(rw, g, wn);
+        accumulate<TY, 1>(wn, g, xs + 9 * g, &a, T);
     }
-    ag = row_sum(ag);
-    if constexpr (SWIGLU) au = row_sum(au);
-    if (li == 0 && r < R) {
-        float v = ag;
-        if constexpr (SWIGLU) v = ag / (1.0f + expf(-ag)) * au;
-        out[(size_t) p * R + r] = v;
+    a = row_sum(a);
+    if constexpr (SWIGLU) {
+        const float u = swz_xor16(a);  // the up row's sum, at the gate row's lanes
+        if (!up && li == 0 && r < R) out[(size_t) p * R + r] = a / (1.0f + expf(-a)) * u;
+    } else {
+        if (li == 0 && r < R) out[(size_t) p * R + r] = a;
     }
 }
 
@@ -1183,7 +1176,8 @@ int rows_t(const QLayout &L, const PP &Pg, const PP &Pu, int R, const int32_t *s
            const float *x, float *out, hipStream_t st, const RouteIn &rt) {
     const size_t lds = (size_t) (L.cols / 32) * 9 * sizeof(float4);
     if (lds + tab_lds<TY>() > (size_t) kLdsPerCu) FN_FAIL("rows: x row too long for the LDS");
-    hipLaunchKernelGGL((k_rows<TY, SW>), dim3((unsigned) ((R + 15) / 16), (unsigned) npairs), dim3(256), lds, st, Pg,
+    constexpr int RW = rows_per_wg<SW>();
+    hipLaunchKernelGGL((k_rows<TY, SW>), dim3((unsigned) ((R + RW - 1) / RW), (unsigned) npairs), dim3(256), lds, st, Pg,
                        Pu, R, L.rows / R, L.cols / 32, L.cols, sel, xdiv, x, out, rt);
     FN_CK(hipGetLastError());
     return 0;

@@ -208,3 +208,28 @@ def test_model_reference_widths(fnlib, tmp_path):
             i += nt
     finally:
         fnlib.free()
+
+
+def test_model_token_count_invariance(fnlib, tmp_path):
+    """Token t of an 8-token call gets the bits of one-token calls in a model without attention layers (every
+    DeltaNet, hyper-connection, projection and expert kernel sums per token in a fixed order, whatever the launch
+    shape); with attention layers, whose several-token kernel runs on the matrix cores, within 1e-6."""
+    out = {}
+    for name, dims in (("no attention", dict(ms.TINY_DIMS, attn_every=0)), ("hybrid", ms.TINY_DIMS)):
+        p = str(tmp_path / "inv.gguf")
+        ms.write_model(p, dims, seed=11)
+        _say(f"model forward: 8-token calls vs one-token calls, {name}")
+        fnlib.load(p, "", max_ctx=256)
+        try:
+            ids = np.random.default_rng(3).integers(0, dims["VOCAB"], size=24)
+            fnlib.reset()
+            a = np.concatenate([fnlib.forward(ids[k:k + 8], logits=True)[1] for k in range(0, 24, 8)])
+            fnlib.reset()
+            b = np.concatenate([fnlib.forward(ids[k:k + 1], logits=True)[1] for k in range(24)])
+            out[name] = (a, b)
+        finally:
+            fnlib.free()
+    a, b = out["no attention"]
+    assert np.array_equal(a, b)
+    a, b = out["hybrid"]
+    assert _rel(a, b) <= 1e-6
