@@ -168,6 +168,20 @@ __device__ __forceinline__ int route_pick(const float *__restrict__ l, int NE, i
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// x.x^2 + x.y^2 + x.z^2 + x.w^2 as one fixed chain (a product, then three fmas), so that every kernel that sums
+// squares of a stream gets the same bits whatever the compiler would contract
+__device__ __forceinline__ float sumsq4(float4 v) {
+    float q = v.x * v.x;
+    q = __builtin_fmaf(v.y, v.y, q);
+    q = __builtin_fmaf(v.z, v.z, q);
+    return __builtin_fmaf(v.w, v.w, q);
+}
+// h + y s, one fma per component
+__device__ __forceinline__ float4 add_scaled(float4 h, float4 y, float s) {
+    return make_float4(__builtin_fmaf(y.x, s, h.x), __builtin_fmaf(y.y, s, h.y), __builtin_fmaf(y.z, s, h.z),
+                       __builtin_fmaf(y.w, s, h.w));
+}
 __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }
 
 __device__ __forceinline__ float4 f4(float a) { return make_float4(a, a, a, a); }

@@ -67,17 +67,16 @@ __device__ __forceinline__ float block_sum(float v, float *red, int nw) {
 }
 
 // RMSNorm of each of the HC streams: out[t][s D + c] = h * rsqrt(mean_c h^2 + eps) * w[s D + c] (faie2fn.cu:1226-1239).
-// grid (nt, HC), 256 threads
+// grid (nt, HC), 256 threads.  The sum of squares has the order of k_hc_add's and of the fused write + norm + down
+// kernel's (thread tid: float4 tid, tid + 256, ... in order, sumsq4 each; then the wave sums in wave order), so
+// every path gives the same bits.
 __global__ void __launch_bounds__(256) k_groupnorm(const float *__restrict__ h, const float *__restrict__ w, int D,
                                                     float eps, float *__restrict__ out) {
     __shared__ float red[4];
     const size_t base = ((size_t) blockIdx.x * gridDim.y + blockIdx.y) * D;
     const float4 *h4 = reinterpret_cast<const float4 *>(h + base);
     float ss = 0.0f;
-    for (int c = threadIdx.x; c < D / 4; c += 256) {
-        const float4 v = h4[c];
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
+    for (int c = threadIdx.x; c < D / 4; c += 256) ss += sumsq4(h4[c]);
     const float r = rsqrtf(block_sum(ss, red, 4) / D + eps);
     const float4 *w4 = reinterpret_cast<const float4 *>(w + (size_t) blockIdx.y * D);
     float4 *o4 = reinterpret_cast<float4 *>(out + base);
@@ -225,14 +224,14 @@ __global__ void __launch_bounds__(UPMIX_ROWS * 8)
 
 // hyper-connection write (faie2fn.cu:1281-1327): h[t][s][c] += yv[c] * inj[t][s], where yv = y, or for the MoE
 // yv = sum_k wsel[t][k] dpart[t NEU + k][c] + sigmoid(rsg[t][NE]) y[t][c]; then (norm non-null)
-// hn[t][s][c] = RMSNorm of the new stream s.  One thread per 4 columns (all loads of a thread issued together).
-// grid (nt, HC), min(1024, D / 4 rounded up to 64) threads
-__global__ void __launch_bounds__(1024) k_hc_add(float *__restrict__ h, const float *__restrict__ y,
+// hn[t][s][c] = RMSNorm of the new stream s (the sum of squares in k_groupnorm's order).  grid (nt, HC), 256
+// threads
+__global__ void __launch_bounds__(256) k_hc_add(float *__restrict__ h, const float *__restrict__ y,
                                                  const float *__restrict__ inj, int D, int HC,
                                                  const float *__restrict__ dpart, const float *__restrict__ wsel,
                                                  int NEU, const float *__restrict__ rsg, int NE,
                                                  const float *__restrict__ norm, float eps, float *__restrict__ hn) {
-    __shared__ float red[16];
+    __shared__ float red[4];
     const int t = blockIdx.x, s = blockIdx.y, D4 = D / 4;
     float4 *hp = reinterpret_cast<float4 *>(h + ((size_t) t * HC + s) * D);
     const float4 *y4 = reinterpret_cast<const float4 *>(y + (size_t) t * D);
@@ -254,10 +253,9 @@ __global__ void __launch_bounds__(1024) k_hc_add(float *__restrict__ h, const fl
             }
             yv = make_float4(m.x + sg * yv.x, m.y + sg * yv.y, m.z + sg * yv.z, m.w + sg * yv.w);
         }
-        float4 v = hp[c];
-        v = make_float4(v.x + yv.x * is, v.y + yv.y * is, v.z + yv.z * is, v.w + yv.w * is);
+        const float4 v = add_scaled(hp[c], yv, is);
         hp[c] = v;
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        ss += sumsq4(v);
     }
     if (!norm) return;  // (uniform)
     const float r = rsqrtf(block_sum(ss, red, blockDim.x >> 6) / D + eps);
@@ -465,7 +463,9 @@ struct Model {
     QW tok, head, out_down, out_up;
     float *out_norm = nullptr;
     // activations, MAXT tokens
-    float *h = nullptr, *hn = nullptr, *lr = nullptr, *t320 = nullptr, *a = nullptr, *x = nullptr, *inj = nullptr;
+    // h: the residual streams; h2: the other buffer of the pair a fused write moves them to
+    float *h = nullptr, *h2 = nullptr, *hb[2] = {}, *hn = nullptr, *lr = nullptr, *t320 = nullptr, *a = nullptr;
+    float *x = nullptr, *inj = nullptr;
     float *qkv = nullptr, *zz = nullptr, *abv = nullptr, *on = nullptr, *qg = nullptr, *kk = nullptr, *vv = nullptr;
     float *iqk = nullptr, *og = nullptr, *y = nullptr, *rsgv = nullptr, *shg = nullptr, *shu = nullptr, *sha = nullptr;
     float *shd = nullptr, *act = nullptr, *dpart = nullptr, *wsel = nullptr, *logits = nullptr, *work = nullptr;
@@ -783,7 +783,8 @@ int load_model(Model &m, int max_ctx_req) {
     m.nsplit = attn_pick_nsplit(1, d.NKV, MAXT, 4 * d.top + 4);
     for (int nt = 1; nt <= MAXT; ++nt)
         m.work_bytes = std::max(m.work_bytes, attn_qsa_work_bytes(1, d.NH, nt, HDK, m.nsplit, m.max_ctx, d.top) + 256);
-    if (m.alloc(&m.h, T * HCD) || m.alloc(&m.hn, T * HCD) || m.alloc(&m.lr, HC_KS * T * ldr) ||
+    if (m.alloc(&m.hb[0], T * HCD) || m.alloc(&m.hb[1], T * HCD) || m.alloc(&m.hn, T * HCD) ||
+        m.alloc(&m.lr, (size_t) std::max(HC_KS, d.HC) * T * ldr) ||
         m.alloc(&m.amv, T * AM_CH) || m.alloc(&m.ami, T * AM_CH) ||
         m.alloc(&m.t320, T * d.HCR) || m.alloc(&m.a, T * HCD) || m.alloc(&m.x, T * D) || m.alloc(&m.inj, T * d.HC) ||
         m.alloc(&m.qkv, T * d.CONVCH) || m.alloc(&m.zz, T * d.DINNER) || m.alloc(&m.abv, T * 2 * d.NVH) ||
@@ -805,15 +806,13 @@ int gemv(const QW &w, const float *x, int nt, float *y, hipStream_t st) {
     return gemv_launch(w.L, w.p, x, nt, y, nullptr, 0, st);
 }
 
-// hyper-connection read of m.hn (already normalized) through the down(+inject) and up weights into m.x, m.inj.
-// The down product (a few hundred rows of HC D columns) runs split along its rows, HC_KS ways, and its consumers sum
-// the partials; with a BF16 up weight (the reference model's) the up product and the mix are one kernel.
-int hc_read(Model &m, const QW &dinj, const QW &up, int nt) {
+// the rest of a hyper-connection read once the down (+ inject) product's ks partials are in m.lr: with a BF16 up
+// weight (the reference model's) the low-rank SiLU, the up product and the mix are one kernel, else three; into
+// m.x and (with inject rows) m.inj
+int hc_up(Model &m, const QW &dinj, const QW &up, int nt, int ks) {
     const ModelDims &d = m.d;
     const bool inj = dinj.L.rows > d.HCR;
     const int ldr = dinj.L.rows;
-    int ks = 1;
-    if (gemv_split_launch(dinj.L, dinj.p, m.hn, nt, HC_KS, m.lr, &ks, m.st)) return -1;
     if (up.L.type == QT_BF16 && UPMIX_ROWS % d.HC == 0 && d.HC <= UPMIX_HC && d.HCR % 8 == 0 &&
         d.HCR <= 64 * UPMIX_U) {
         const int cpb = UPMIX_ROWS / d.HC;
@@ -829,6 +828,35 @@ int hc_read(Model &m, const QW &dinj, const QW &up, int nt) {
                        ldr, d.HCR, m.x, inj ? m.inj : nullptr);
     FN_CK(hipGetLastError());
     return 0;
+}
+
+// One hyper-connection stage: with y, the write of y into the streams (y[t] inj[t][s] into stream s, inj the
+// previous read's inject weights) ahead of the read; then the read: each stream's RMSNorm with weight norm into
+// m.hn, the down (+ inject) product (a few hundred rows of HC D columns, split by stream, its consumers summing the
+// partials) and hc_up.  With a BF16 down weight (the reference model's) the write, the norm and the down product
+// are one kernel for a one-token call, and the streams move to the other buffer of the pair; else k_hc_add (or
+// k_groupnorm without y) and the split down GEMV (faster for several tokens: the fused kernel's every workgroup
+// would norm all of them).  Both give the same bits: the same sums of squares in the same order, and the split
+// GEMV sums each row with 64 lanes as the fused kernel does.  dpart: y is the shared expert's part of an MoE output whose routed rows wait in m.dpart
+// (expert formats without the MoE output kernel).
+int hc_stage(Model &m, const float *y, bool dpart, const float *norm, const QW &dinj, const QW &up, int nt) {
+    const ModelDims &d = m.d;
+    if (!dpart && nt == 1 && hc_down_supported(dinj.L, d.D, d.HC)) {
+        if (hc_down_launch(m.h, y, m.inj, norm, d.D, d.HC, d.eps, dinj.L, dinj.p, nt, y ? m.h2 : nullptr, m.hn, m.lr,
+                           m.st))
+            return -1;
+        if (y) std::swap(m.h, m.h2);
+        return hc_up(m, dinj, up, nt, d.HC);
+    }
+    if (y)
+        hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, y, m.inj, d.D, d.HC,
+                           dpart ? m.dpart : nullptr, m.wsel, d.NEU, m.rsgv, d.NE, norm, d.eps, m.hn);
+    else
+        hipLaunchKernelGGL(k_groupnorm, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, norm, d.D, d.eps, m.hn);
+    FN_CK(hipGetLastError());
+    int ks = 1;
+    if (gemv_split_launch(dinj.L, dinj.p, m.hn, nt, HC_KS, m.lr, &ks, m.st)) return -1;
+    return hc_up(m, dinj, up, nt, ks);
 }
 
 unsigned hc_add_threads(int D) { return (unsigned) std::min(1024, (D / 4 + 63) / 64 * 64); }
@@ -853,7 +881,8 @@ int mixer(Model &m, MLayer &L, int nt) {
     return gemv(L.o, m.og, nt, m.y, m.st);
 }
 
-int ffn(Model &m, MLayer &L, int nt, const float *next_norm) {
+// the FFN of x into m.shd: the MoE output when *whole, else the shared expert's part (the routed rows in m.dpart)
+int ffn(Model &m, MLayer &L, int nt, bool *whole) {
     const ModelDims &d = m.d;
     const GemvPart g[3] = {{&L.rsg.L, L.rsg.p, m.rsgv}, {&L.sh_gate.L, L.sh_gate.p, m.shg},
                            {&L.sh_up.L, L.sh_up.p, m.shu}};
@@ -891,9 +920,7 @@ int ffn(Model &m, MLayer &L, int nt, const float *next_norm) {
                rows_launch(L.ed.L, L.ed.p, d.D, m.sel, np, 1, m.act, m.dpart, m.st)) {
         return -1;
     }
-    hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(hc_add_threads(d.D)), 0, m.st, m.h, m.shd, m.inj, d.D, d.HC,
-                       fused ? nullptr : m.dpart, m.wsel, d.NEU, m.rsgv, d.NE, next_norm, d.eps, m.hn);
-    FN_CK(hipGetLastError());
+    *whole = fused;
     return 0;
 }
 
@@ -923,24 +950,45 @@ int enqueue(Model &m, int nt) {
         hipLaunchKernelGGL(k_store_tokens, dim3(1), dim3(MAXT), 0, m.st, m.ids, m.tok_all, m.pos, nt, m.max_ctx);
         FN_CK(hipGetLastError());
     }
+    m.h = m.hb[0];  // every call (and every captured graph) starts from the same buffer of the pair
+    m.h2 = m.hb[1];
     if (embed_launch(m.tok.L, m.tok.p, m.ids, nt, d.HC, m.h, m.st)) return -1;
-    for (int il = 0; il < d.NL; ++il) {
-        MLayer &L = m.L[il];
-        if (L.ple && ple(m, L, nt)) return -1;
-        // layer 0 and a PLE layer normalize the streams for themselves; otherwise the previous write left m.hn
-        if (il == 0 || L.ple)
-            hipLaunchKernelGGL(k_groupnorm, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, L.hca_norm, d.D, d.eps, m.hn);
-        if (hc_read(m, L.hca_dinj, L.hca_up, nt) || mixer(m, L, nt)) return -1;
-        hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(hc_add_threads(d.D)), 0, m.st, m.h, m.y, m.inj, d.D, d.HC,
-                           nullptr, nullptr, 0, nullptr, 0, L.hcf_norm, d.eps, m.hn);
-        if (hc_read(m, L.hcf_dinj, L.hcf_up, nt)) return -1;
-        const float *next = il + 1 == d.NL ? m.out_norm : m.L[il + 1].ple ? nullptr : m.L[il + 1].hca_norm;
-        if (ffn(m, L, nt, next)) return -1;
+    // the FFN output of a layer is written into the streams by the next stage (its write and the next read's norm
+    // and down product are one kernel); pend is that output, pend_dp whether its routed rows wait in m.dpart
+    const float *pend = nullptr;
+    bool pend_dp = false;
+    const auto dbg_copy = [&](int il) -> int {
         if (m.dbg)
             FN_CK(hipMemcpyAsync(m.dbg + (size_t) il * nt * HCD, m.h, (size_t) nt * HCD * 4, hipMemcpyDeviceToHost,
                                  m.st));
+        return 0;
+    };
+    for (int il = 0; il < d.NL; ++il) {
+        MLayer &L = m.L[il];
+        if (L.ple) {
+            // the n-gram embedding reads and writes the streams themselves: the pending write goes first, alone
+            if (pend) {
+                hipLaunchKernelGGL(k_hc_add, dim3(nt, d.HC), dim3(256), 0, m.st, m.h, pend, m.inj,
+                                   d.D, d.HC, pend_dp ? m.dpart : nullptr, m.wsel, d.NEU, m.rsgv, d.NE, nullptr,
+                                   d.eps, m.hn);
+                FN_CK(hipGetLastError());
+                pend = nullptr;
+            }
+            if ((il > 0 && dbg_copy(il - 1)) || ple(m, L, nt) ||
+                hc_stage(m, nullptr, false, L.hca_norm, L.hca_dinj, L.hca_up, nt))
+                return -1;
+        } else if (hc_stage(m, pend, pend_dp, L.hca_norm, L.hca_dinj, L.hca_up, nt) || (il > 0 && dbg_copy(il - 1))) {
+            return -1;
+        }
+        bool whole = true;
+        if (mixer(m, L, nt) || hc_stage(m, m.y, false, L.hcf_norm, L.hcf_dinj, L.hcf_up, nt) ||
+            ffn(m, L, nt, &whole))
+            return -1;
+        pend = m.shd;
+        pend_dp = !whole;
     }
-    if (hc_read(m, m.out_down, m.out_up, nt) || gemv(m.head, m.x, nt, m.logits, m.st)) return -1;
+    if (hc_stage(m, pend, pend_dp, m.out_norm, m.out_down, m.out_up, nt) || dbg_copy(d.NL - 1)) return -1;
+    if (gemv(m.head, m.x, nt, m.logits, m.st)) return -1;
     hipLaunchKernelGGL(k_argmax_part, dim3(nt, AM_CH), dim3(256), 0, m.st, m.logits, d.VOCAB, m.amv, m.ami);
     hipLaunchKernelGGL(k_argmax_merge, dim3(nt), dim3(64), 0, m.st, m.amv, m.ami, d.VOCAB, m.am);
     FN_CK(hipGetLastError());

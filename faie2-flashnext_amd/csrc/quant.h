@@ -114,6 +114,15 @@ int swiglu_launch(const QLayout &Lg, const uint8_t *pg, const QLayout &Lu, const
                   const int32_t *sel, int npairs, int xdiv, const float *x, float *act, hipStream_t st,
                   const RouteIn *route = nullptr);
 
+// Hyper-connection write + the next read's per-stream RMSNorm + its down (+ inject) product, one launch (hc.hip):
+// v[t][k] = h[t][k] + y[t] inj[t][k] (v = h when y is null; written to hout), hn[t][k] = RMSNorm(v[t][k]) w[k],
+// part[k][t][r] = W[r][k D .. (k + 1) D) . hn[t][k] for the R rows of W (HC D columns, BF16).  hc_down_supported:
+// the weights and widths it is built for.
+bool hc_down_supported(const QLayout &L, int D, int HC);
+int hc_down_launch(const float *h, const float *y, const float *inj, const float *w, int D, int HC, float eps,
+                   const QLayout &L, const uint8_t *packed, int nt, float *hout, float *hn, float *part,
+                   hipStream_t st);
+
 // The MoE output of nt tokens in one launch: y[t][r] = sigmoid(rsg[t][NE]) (Ws[r] . sha[t]) + the sum over k < NEU,
 // in order, of wsel[t][k] (We[sel[t][k] R + r] . act[t NEU + k]), r < R; We the stacked experts' down weights
 // (rows of cols = FFE values), Ws the shared expert's (R x cols, Q8_0), each dot product with the arithmetic of
