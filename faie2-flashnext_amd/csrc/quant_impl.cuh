@@ -97,9 +97,33 @@ template <uint32_t TY> __device__ __forceinline__ uint32_t *grid_lds() {
     return grid;
 }
 
+// Byte masks of a sign byte: entry s is two words whose byte j is 0xFF where bit j (first word) or bit 4 + j
+// (second word) of s is set.  The grid formats' magnitudes are bytes 1..127, so a word of four of them takes its
+// signs as (g ^ m) + (m & 0x01010101): every flagged byte negated in two's complement with no carry between bytes,
+// ready for the signed-byte conversion (two operations per four values instead of a bit test and an or per value).
+constexpr uint32_t sign_mask4(uint32_t s) {
+    return (s & 1u ? 0xFFu : 0u) | (s & 2u ? 0xFF00u : 0u) | (s & 4u ? 0xFF0000u : 0u) | (s & 8u ? 0xFF000000u : 0u);
+}
+struct SignTab {
+    uint32_t w[512];
+    constexpr SignTab() : w() {
+        for (uint32_t s = 0; s < 256; ++s) {
+            w[2 * s] = sign_mask4(s & 15u);
+            w[2 * s + 1] = sign_mask4(s >> 4);
+        }
+    }
+};
+__device__ const SignTab kSignTab{};
+static_assert(SignTab().w[2 * 0x81] == 0xFFu && SignTab().w[2 * 0x81 + 1] == 0xFF000000u, "sign byte masks");
+__device__ __forceinline__ uint32_t *sign_lds() {
+    __shared__ uint32_t sgn[512];
+    return sgn;
+}
+__device__ __forceinline__ uint32_t neg_bytes(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
+
 template <uint32_t TY> struct GridTab {
-    const uint32_t *grid;
-    __device__ __forceinline__ GridTab() : grid(grid_lds<TY>()) {}
+    const uint32_t *grid, *sgn;
+    __device__ __forceinline__ GridTab() : grid(grid_lds<TY>()), sgn(sign_lds()) {}
 };
 
 // per-format lookup state held by a decoding lane: the IQ4 levels in registers, or the grid codebook in LDS
@@ -109,22 +133,19 @@ template <uint32_t TY> using TabT = typename TabOf<TY>::type;
 
 // LDS the format's table takes in a GEMV / dequant workgroup, and its fill by the workgroup's nth threads (the
 // caller's next barrier publishes it)
-template <uint32_t TY> constexpr int tab_lds() { return GridOf<TY>::words * 4; }
+template <uint32_t TY> constexpr int tab_lds() { return GridOf<TY>::words > 0 ? GridOf<TY>::words * 4 + 2048 : 0; }
 template <uint32_t TY> __device__ __forceinline__ void tab_fill(int tid, int nth) {
     if constexpr (GridOf<TY>::words > 0) {
-        uint32_t *g = grid_lds<TY>();
+        uint32_t *g = grid_lds<TY>(), *sg = sign_lds();
         const uint32_t *src = grid_src<TY>();
         for (int i = tid; i < GridOf<TY>::words; i += nth) g[i] = src[i];
+        for (int i = tid; i < 512; i += nth) sg[i] = kSignTab.w[i];
     }
 }
 
 // the sign byte of a 7-bit sign index of the IQ2 / IQ3_XXS formats: the index with its parity as bit 7 (an even
 // count of negated values; GGUF's ksigns_iq2xs)
 __device__ __forceinline__ uint32_t ksign(uint32_t i) { return i | (uint32_t) (__builtin_popcount(i) & 1) << 7; }
-// magnitude m carrying sign bit sg (0 or 1) of the value: the float's sign bit, exact
-__device__ __forceinline__ float smag(uint32_t m, uint32_t sg) {
-    return __uint_as_float(__float_as_uint((float) m) | sg << 31);
-}
 
 __device__ __forceinline__ float sbyte(uint32_t w, int k) { return (float) ((int32_t) (w << (24 - 8 * k)) >> 24); }
 __device__ __forceinline__ float h2f(uint32_t bits) {
@@ -395,12 +416,14 @@ template <> struct Q<QT_IQ3_S> {
         for (int l = 0; l < 4; ++l) {
             const uint32_t qq = l < 2 ? w[0] : w[1];
             const int s = 16 * (l & 1);
-            const uint32_t g1 = T.grid[((qq >> s) & 255u) | ((qh << (8 - 2 * l)) & 256u)];
-            const uint32_t g2 = T.grid[((qq >> (s + 8)) & 255u) | ((qh << (7 - 2 * l)) & 256u)];
+            const uint32_t sb = (w[3] >> (8 * l)) & 255u;  // the signs of values 8 l .. 8 l + 7
+            const uint32_t g1 = neg_bytes(T.grid[((qq >> s) & 255u) | ((qh << (8 - 2 * l)) & 256u)], T.sgn[2 * sb]);
+            const uint32_t g2 =
+                neg_bytes(T.grid[((qq >> (s + 8)) & 255u) | ((qh << (7 - 2 * l)) & 256u)], T.sgn[2 * sb + 1]);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                o.q[8 * l + j] = smag((g1 >> (8 * j)) & 255u, (w[3] >> (8 * l + j)) & 1u);
-                o.q[8 * l + 4 + j] = smag((g2 >> (8 * j)) & 255u, (w[3] >> (8 * l + 4 + j)) & 1u);
+                o.q[8 * l + j] = sbyte(g1, j);
+                o.q[8 * l + 4 + j] = sbyte(g2, j);
             }
         }
         o.s[0] = o.s[1] = h2f(w[5]) * (float) (1 + 2 * (int) sc);
@@ -409,12 +432,13 @@ template <> struct Q<QT_IQ3_S> {
 };
 
 // 8 magnitudes of an 8-byte grid entry e (two words at 2e) with the signs of sign byte sg into q[8l .. 8l + 7]
-__device__ __forceinline__ void grid8(float *q, const uint32_t *grid, uint32_t e, uint32_t sg) {
-    const uint32_t g0 = grid[2 * e], g1 = grid[2 * e + 1];
+template <uint32_t TY>
+__device__ __forceinline__ void grid8(float *q, const GridTab<TY> &T, uint32_t e, uint32_t sg) {
+    const uint32_t g0 = neg_bytes(T.grid[2 * e], T.sgn[2 * sg]), g1 = neg_bytes(T.grid[2 * e + 1], T.sgn[2 * sg + 1]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        q[j] = smag((g0 >> (8 * j)) & 255u, (sg >> j) & 1u);
-        q[4 + j] = smag((g1 >> (8 * j)) & 255u, (sg >> (4 + j)) & 1u);
+        q[j] = sbyte(g0, j);
+        q[4 + j] = sbyte(g1, j);
     }
 }
 
@@ -431,7 +455,7 @@ template <> struct Q<QT_IQ2_XXS> {
     }
     __device__ static void unpack(const uint32_t *w, int g, Grp &o, const GridTab<QT_IQ2_XXS> &T) {
 #pragma unroll
-        for (int l = 0; l < 4; ++l) grid8(o.q + 8 * l, T.grid, (w[0] >> (8 * l)) & 255u, ksign((w[1] >> (7 * l)) & 127u));
+        for (int l = 0; l < 4; ++l) grid8(o.q + 8 * l, T, (w[0] >> (8 * l)) & 255u, ksign((w[1] >> (7 * l)) & 127u));
         o.s[0] = o.s[1] = h2f(w[2]) * (0.5f + (float) (w[1] >> 28)) * 0.25f;
         o.m[0] = o.m[1] = 0.0f;
     }
@@ -455,7 +479,7 @@ template <> struct Q<QT_IQ2_XS> {
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             const uint32_t c = (w[l >> 1] >> (16 * (l & 1))) & 0xFFFFu;
-            grid8(o.q + 8 * l, T.grid, c & 511u, ksign(c >> 9));
+            grid8(o.q + 8 * l, T, c & 511u, ksign(c >> 9));
         }
         const uint32_t sc = (w[2] >> (8 * (ib & 3))) & 0xFFu;
         const float d = h2f(w[3]);
@@ -486,7 +510,7 @@ template <> struct Q<QT_IQ2_S> {
         const uint32_t qh = (w[2] >> (8 * (ib & 3))) & 0xFFu, sc = (w[3] >> (8 * (ib & 3))) & 0xFFu;
 #pragma unroll
         for (int l = 0; l < 4; ++l)
-            grid8(o.q + 8 * l, T.grid, ((w[0] >> (8 * l)) & 255u) | ((qh << (8 - 2 * l)) & 0x300u), (w[1] >> (8 * l)) & 255u);
+            grid8(o.q + 8 * l, T, ((w[0] >> (8 * l)) & 255u) | ((qh << (8 - 2 * l)) & 0x300u), (w[1] >> (8 * l)) & 255u);
         const float d = h2f(w[4]);
         o.s[0] = d * (0.5f + (float) (sc & 15u)) * 0.25f;
         o.s[1] = d * (0.5f + (float) (sc >> 4)) * 0.25f;
@@ -512,11 +536,12 @@ template <> struct Q<QT_IQ3_XXS> {
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             const uint32_t qq = w[l >> 1], s = 16 * (l & 1), sg = ksign((w[2] >> (7 * l)) & 127u);
-            const uint32_t g1 = T.grid[(qq >> s) & 255u], g2 = T.grid[(qq >> (s + 8)) & 255u];
+            const uint32_t g1 = neg_bytes(T.grid[(qq >> s) & 255u], T.sgn[2 * sg]);
+            const uint32_t g2 = neg_bytes(T.grid[(qq >> (s + 8)) & 255u], T.sgn[2 * sg + 1]);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                o.q[8 * l + j] = smag((g1 >> (8 * j)) & 255u, (sg >> j) & 1u);
-                o.q[8 * l + 4 + j] = smag((g2 >> (8 * j)) & 255u, (sg >> (4 + j)) & 1u);
+                o.q[8 * l + j] = sbyte(g1, j);
+                o.q[8 * l + 4 + j] = sbyte(g2, j);
             }
         }
         o.s[0] = o.s[1] = h2f(w[3]) * (0.5f + (float) (w[2] >> 28)) * 0.5f;
