@@ -233,3 +233,25 @@ def test_model_token_count_invariance(fnlib, tmp_path):
     assert np.array_equal(a, b)
     a, b = out["hybrid"]
     assert _rel(a, b) <= 1e-6
+
+
+@pytest.mark.parametrize("ne,neu", [(24, 10), (40, 17)])
+def test_model_expert_counts(fnlib, tmp_path, ne, neu):
+    """The reference model's 10 experts a token, and 17 (the MoE output kernel then takes its items in two passes a
+    wave for one token, and the several-token kernel three chunks of weight words), against the oracle."""
+    dims = dict(ms.TINY_DIMS, NE=ne, NEU=neu)
+    p = str(tmp_path / "experts.gguf")
+    kv, ts = ms.write_model(p, dims, seed=13)
+    _say(f"model forward: {ne} experts, {neu} a token, 12 tokens in calls of 1, 8, 3")
+    fnlib.load(p, "", max_ctx=256)
+    try:
+        ref = om.Model(kv, ts, max_ctx=256)
+        ids = np.random.default_rng(7).integers(0, dims["VOCAB"], size=12)
+        i = 0
+        for nt in (1, 8, 3):
+            _, lg = fnlib.forward(ids[i:i + nt], logits=True)
+            want, _, _, _ = ref.forward(ids[i:i + nt])
+            assert _rel(lg, want) <= TOL, (ne, neu, i, nt, _rel(lg, want))
+            i += nt
+    finally:
+        fnlib.free()
