@@ -578,6 +578,8 @@ def main():
                          "reference's dimensions and formats with LAYERS layers")
     ap.add_argument("--model-nt", type=int, default=0, choices=(0, 1, 8),
                     help="with --model: time only calls of this many tokens (0: both 1 and 8)")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the whole-model leg of the extra legs (48 layers, ~47 GB written to /dev/shm and loaded)")
     ap.add_argument("--mt-only", action="store_true",
                     help="only the multi-token GQA legs (config 3 shapes, nt = 4 and 8, hipGraph replays)")
     ap.add_argument("--counters-attn", action="store_true",
@@ -779,6 +781,9 @@ def main():
                                                    "tokens_per_s": round(16 * 1e3 / ms, 1), "bytes_per_step": nbytes,
                                                    "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                                                    "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    if not args.no_extra and not args.gdn_only and not args.attn_only and not args.no_model:
+        # the whole model at the reference's 48 layers, one-token greedy decode (the reference's 5.70 ms per forward)
+        extra["model_decode_48_layers"] = model_decode(lib, nl=48, nts=(1,))
     for k, v in extra.items():
         log(f"[bench] {k}: {v}")
 
