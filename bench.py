@@ -527,6 +527,50 @@ def gemv_extras(lib, iters=50, nts=(1, 8)):
     return out
 
 
+# the model's projections that read one x, as one grouped launch (fn_gemv_group_dev): (name, [(type, rows)], cols)
+GROUP_SHAPES = (("deltanet_qkv_z_ab", ((23, 10240), (21, 6144), (30, 96)), 2560),
+                ("attention_q_k_v_ix", ((23, 12288), (23, 512), (14, 512), (30, 640)), 2560),
+                ("ffn_router_shgate_shup", ((30, 513), (23, 640), (21, 640)), 2560))
+
+
+def group_extras(lib, stream, iters=40, nts=(1, 8)):
+    """µs per grouped call and GB/s (every weight once, x once, the outputs once) of the model's projection groups,
+    weights cold (the calls cycle through copies that together exceed 1 GiB), calls replayed as one hipGraph; beside
+    it the sum of the weights' own GEMVs (fn_bench_gemv, cold)."""
+    out = {}
+    lib.bench_hot(False)
+    for name, parts, cols in GROUP_SHAPES:
+        types, rows = [t for t, _ in parts], [r for _, r in parts]
+        nbytes = [lib.gemv_packed_bytes(t, r, cols) for t, r in parts]
+        copies = max(2, min(iters, (1 << 30) // sum(nbytes) + 1))
+        bufs = [[hiprt.Buf(nb, np.uint8) for nb in nbytes] for _ in range(copies)]
+        for i, cp in enumerate(bufs):
+            for j, (bb, nb) in enumerate(zip(cp, nbytes)):
+                lib.fill_normal_dev(bb.ptr, nb // 4, 1000 + 16 * i + j)
+        for nt in nts:
+            x = hiprt.Buf(nt * cols * 4)
+            lib.fill_normal_dev(x.ptr, nt * cols, 7)
+            ys = [hiprt.Buf(nt * r * 4) for r in rows]
+
+            def launch():
+                for i in range(iters):
+                    lib.gemv_group_dev(types, rows, cols, [b.ptr for b in bufs[i % copies]], x.ptr, nt,
+                                       [y.ptr for y in ys], stream.handle)
+            ms = time_graph(stream, launch, 3, 1) / iters
+            by = sum(r * fn.row_bytes(t, cols) + 4 * nt * r for t, r in parts) + 4 * nt * cols
+            sep = sum(lib.bench_gemv(t, r, cols, nt=nt, iters=iters) for t, r in parts)
+            out[f"gemv_group_{name}_nt{nt}"] = {"us": round(ms * 1e3, 2), "bytes": by,
+                                                "gbs": round(by / (ms * 1e-3) / 1e9, 1),
+                                                "separate_launches_us": round(sep * 1e3, 2)}
+            x.free()
+            for y in ys:
+                y.free()
+        for cp in bufs:
+            for bb in cp:
+                bb.free()
+    return out
+
+
 def cpu_baseline(budget_s=12.0):
     """The float64 C oracle (OpenMP over all host cores) on a bounded sample of the headline workload: B = 64
     sequences of one layer, decode steps repeated until about budget_s seconds of CPU work.  Same unit as value."""
@@ -614,6 +658,7 @@ def main():
         return
     if args.gemv:
         res = gemv_extras(lib)
+        res.update(group_extras(lib, stream))
         for k, v in res.items():
             log(f"[bench] {k}: {v}")
         print(json.dumps({"gemv": res}), flush=True)
@@ -770,6 +815,7 @@ def main():
             extra["config2_host_hook_pcie_inclusive"] = {"ms_per_layer_step": round(hook_ms, 2),
                                                          "gbs": round(fn_synth.gdn_block_bytes(64) / hook_ms / 1e6, 1)}
             extra.update(gemv_extras(lib))
+            extra.update(group_extras(lib, stream))
             ms, nbytes = hybrid_config4(lib, steps, warmup)
             ms_v, by_v = hybrid_verify(lib, stream, steps, warmup)
             extra["config4_hybrid_verify_b16_ctx32768_nt4_kr2"] = {
