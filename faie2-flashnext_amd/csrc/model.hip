@@ -911,7 +911,7 @@ int ffn(Model &m, MLayer &L, int nt, bool *whole) {
         return -1;
     // the experts' down rows, the shared expert's down row and their weighted sum in one kernel where it is built
     // for the formats (the reference model's are), else the rows, a GEMV, and the sum inside the stream write
-    const bool fused = moe_down_supported(L.ed.L, L.sh_down.L, d.D);
+    const bool fused = moe_down_supported(L.ed.L, L.sh_down.L, d.D, d.NEU);
     if (fused) {
         if (moe_down_launch(L.ed.L, L.ed.p, L.sh_down.L, L.sh_down.p, d.D, m.sel, m.wsel, d.NEU, m.act, m.sha, m.rsgv,
                             d.NE, nt, m.shd, m.st))

@@ -126,8 +126,9 @@ int hc_down_launch(const float *h, const float *y, const float *inj, const float
 // The MoE output of nt tokens in one launch: y[t][r] = sigmoid(rsg[t][NE]) (Ws[r] . sha[t]) + the sum over k < NEU,
 // in order, of wsel[t][k] (We[sel[t][k] R + r] . act[t NEU + k]), r < R; We the stacked experts' down weights
 // (rows of cols = FFE values), Ws the shared expert's (R x cols, Q8_0), each dot product with the arithmetic of
-// rows_launch.  moe_down_supported: the formats and shapes this kernel is built for (else: rows_launch and a GEMV).
-bool moe_down_supported(const QLayout &Le, const QLayout &Ls, int R);
+// rows_launch.  moe_down_supported: the formats, shapes and expert counts this kernel is built for (its LDS holds a
+// token's NEU + 1 x rows), else rows_launch and a GEMV.
+bool moe_down_supported(const QLayout &Le, const QLayout &Ls, int R, int NEU);
 int moe_down_launch(const QLayout &Le, const uint8_t *pe, const QLayout &Ls, const uint8_t *ps, int R,
                     const int32_t *sel, const float *wsel, int NEU, const float *act, const float *sha, const float *rsg,
                     int NE, int nt, float *y, hipStream_t st);

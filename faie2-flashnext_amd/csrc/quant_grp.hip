@@ -52,9 +52,9 @@ int gemv_group_launch(const GemvPart *parts, int n, const float *x, int nt, hipS
         }
         if (ok) kind = k;
     }
-    // x of nt tokens in the LDS beside the codebooks (IQ3_S: 2 KiB)
+    // x of nt tokens in the LDS beside the codebooks (IQ3_S: its grid and the sign masks, 4 KiB)
     const size_t xlds = (size_t) (parts[0].L->cols / 32) * xs_stride(nt) * sizeof(float4);
-    if (kind < 0 || xlds + 2048 > (size_t) kLdsPerCu) {
+    if (kind < 0 || xlds + (size_t) tab_lds<QT_IQ3_S>() > (size_t) kLdsPerCu) {
         for (int i = 0; i < n; ++i)
             if (gemv_launch(*parts[i].L, parts[i].packed, x, nt, parts[i].y, nullptr, 0, st)) return -1;
         return 0;

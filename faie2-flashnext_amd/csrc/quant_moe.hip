@@ -204,9 +204,13 @@ int moe_down_t(const QLayout &Le, const PP &Pe, const QLayout &Ls, const PP &Ps,
 
 }  // namespace
 
-bool moe_down_supported(const QLayout &Le, const QLayout &Ls, int R) {
+bool moe_down_supported(const QLayout &Le, const QLayout &Ls, int R, int NEU) {
     const int G = Le.cols / 32;
     if (Ls.type != QT_Q8_0 || Ls.cols != Le.cols || Ls.rows != R || G < 1 || G > 16 * MOE_GPL) return false;
+    // the x rows of a token's NEU + 1 items, their dot products and factors in the LDS beside a grid format's tables
+    const size_t lds = (size_t) (NEU + 1) * G * 9 * sizeof(float4) + (size_t) (NEU + 1) * 5 * sizeof(float) +
+                       (size_t) tab_lds<QT_IQ2_S>();  // (the largest codebook and sign masks of any format)
+    if (NEU < 1 || NEU > 64 || lds > (size_t) kLdsPerCu) return false;
     switch (Le.type) {
         case QT_BF16: case QT_Q8_0: case QT_IQ4_NL: case QT_IQ4_XS: case QT_IQ3_S: case QT_IQ2_XXS: case QT_IQ2_XS:
         case QT_IQ2_S: case QT_IQ3_XXS: case QT_Q2_0: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: return true;
@@ -217,7 +221,7 @@ bool moe_down_supported(const QLayout &Le, const QLayout &Ls, int R) {
 int moe_down_launch(const QLayout &Le, const uint8_t *pe, const QLayout &Ls, const uint8_t *ps, int R,
                     const int32_t *sel, const float *wsel, int NEU, const float *act, const float *sha, const float *rsg,
                     int NE, int nt, float *y, hipStream_t st) {
-    if (!moe_down_supported(Le, Ls, R)) FN_FAIL("moe down: formats or shapes not built");
+    if (!moe_down_supported(Le, Ls, R, NEU)) FN_FAIL("moe down: formats or shapes not built");
     if (!pe || !ps || !sel || !wsel || !act || !sha || !rsg || !y || nt < 1 || NEU < 1 || NEU > 64 || R < 1 ||
         Le.rows % R)
         FN_FAIL("moe down: bad arguments");
