@@ -580,6 +580,18 @@ def group_extras(lib, stream, iters=40, nts=(1, 8)):
     return out
 
 
+def route_extras(lib, iters=200):
+    """µs per MoE routing call (fn_bench_route: 512 router logits summed from 5 split-K partials, top 10), one token
+    and eight, both variants, calls replayed as one hipGraph (flashnext/route_fn.py's timing)."""
+    part = np.random.default_rng(1).standard_normal((5, 8, 528)).astype(np.float32)
+    out = {}
+    for v, name in ((0, "rank"), (1, "wave")):
+        for nt in (1, 8):
+            ms = min(lib.bench_route(v, part, nt, iters)[2] for _ in range(3))
+            out[f"route_{name}_nt{nt}"] = {"us": round(ms * 1e3, 2)}
+    return out
+
+
 def cpu_baseline(budget_s=12.0):
     """The float64 C oracle (OpenMP over all host cores) on a bounded sample of the headline workload: B = 64
     sequences of one layer, decode steps repeated until about budget_s seconds of CPU work.  Same unit as value."""
@@ -668,6 +680,7 @@ def main():
     if args.gemv:
         res = gemv_extras(lib)
         res.update(group_extras(lib, stream))
+        res.update(route_extras(lib))
         for k, v in res.items():
             log(f"[bench] {k}: {v}")
         print(json.dumps({"gemv": res}), flush=True)
@@ -825,6 +838,7 @@ def main():
                                                          "gbs": round(fn_synth.gdn_block_bytes(64) / hook_ms / 1e6, 1)}
             extra.update(gemv_extras(lib))
             extra.update(group_extras(lib, stream))
+            extra.update(route_extras(lib))
             ms, nbytes = hybrid_config4(lib, steps, warmup)
             ms_v, by_v = hybrid_verify(lib, stream, steps, warmup)
             extra["config4_hybrid_verify_b16_ctx32768_nt4_kr2"] = {

@@ -1,8 +1,8 @@
 // C ABI of libfaie2fn.so (declared in include/faie2fn.h).
 //
 // Section 1 keeps the reference's fn_* names and signatures (engine/faie2fn.cu:2492-2935) so its ctypes layer
-// (flashnext/fn.py) binds unchanged; the model-level ones report that this library carries only the
-// decode-attention path.  Sections 2 and 3 are this path's hooks: host arrays in / out (synchronous, device 0,
+// (flashnext/fn.py) binds unchanged; fn_load / fn_forward run the model on one GPU (model.hip), fn_bench_route is
+// in route.hip.  Sections 2 and 3 are this path's hooks: host arrays in / out (synchronous, device 0,
 // the reference's unit-test-hook style, faie2fn.cu:2745) and the device-buffer entry points an engine calls.
 #include "engine.h"
 #include "model.h"
@@ -31,10 +31,6 @@ using fn::use_device0;
 // 1. reference API
 
 namespace {
-
-const char *kNoRoute =
-    "not built: routing is benchmarked through fn_forward (k_route runs inside the model forward); this library has "
-    "no stand-alone routing benchmark";
 
 // switches the reference exposes for its forward; kept so scripts that set them still run
 int g_pdl = 1, g_early = 1, g_moe_var = 0;
@@ -71,7 +67,6 @@ FN_API void fn_pdl(int on) { g_pdl = on != 0; }
 FN_API void fn_early(int on) { g_early = on != 0; }
 FN_API void fn_moe_var(int v) { g_moe_var = v; }
 FN_API void fn_moe_override(int, int, int, int) {}
-FN_API int fn_bench_route(int, int, int, const float *, int, int *, float *, float *) { FN_FAIL(kNoRoute); }
 
 FN_API int fn_model_dims(const char *path, int *out, int n) {
     fn::ModelDims d;

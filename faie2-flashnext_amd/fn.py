@@ -137,6 +137,7 @@ class FN:
         u32, sz = C.c_uint32, C.c_size_t
         d.fn_gemv_plan.argtypes = [u32, i, i, I32]
         d.fn_bench_gemv.argtypes = [u32, i, i, i, i, C.POINTER(C.c_float)]
+        d.fn_bench_route.argtypes = [i, i, i, VP, i, VP, VP, VP]
         d.fn_gemv_override.argtypes = [i] * 4
         d.fn_gemv_waves.argtypes = [i]
         d.fn_model_dims.argtypes = [C.c_char_p, I32, i]
@@ -206,6 +207,19 @@ class FN:
         ms = C.c_float(0.0)
         self.check(self.d.fn_bench_gemv(int(qtype), rows, cols, nt, iters, C.byref(ms)))
         return ms.value
+
+    def bench_route(self, variant, part, nt, iters=1):
+        """MoE routing of nt tokens on router partials part [ks][8][528]: (sel [nt][10], weights [nt][10], ms per
+        call); variant 0 ranks every expert, 1 is the model's one-wave routing."""
+        part = np.ascontiguousarray(part, dtype=np.float32)
+        if part.ndim != 3 or part.shape[1:] != (8, 528):
+            raise ValueError("part must be [ks][8][528] float32")
+        sel = np.zeros((nt, 10), np.int32)
+        w = np.zeros((nt, 10), np.float32)
+        ms = np.zeros(1, np.float32)
+        self.check(self.d.fn_bench_route(variant, nt, part.shape[0], part.ctypes.data, iters, sel.ctypes.data,
+                                         w.ctypes.data, ms.ctypes.data))
+        return sel, w, float(ms[0])
 
     def gemv_override(self, ks=0, lpr=0, kernel=0, waves_per_cu=0):
         """Force the GEMV plan (0 = automatic): split-K, lanes per row, kernel (1 x in chunks, 2 x staged once, 3 / 4

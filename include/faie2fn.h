@@ -25,8 +25,8 @@ extern "C" {
  * 1. The reference's C API, same names and C signatures (engine/faie2fn.cu, flashnext/fn.py:26-34), so that
  *    flashnext/fn.py's argtypes bind unchanged.  The GEMV hooks (fn_test_dequant, fn_test_gemv, fn_gemv_plan,
  *    fn_bench_gemv, fn_gemv_override, fn_bench_hot) work as in the reference for the formats of section 5.
- *    fn_load / fn_forward / fn_debug_layers run the model on one GPU (section 6); fn_bench_route returns -1 (not
- *    built).  The engine entry points (fn_reset, fn_use_graphs, fn_n_past, fn_dev_gb, fn_last_ms, fn_split,
+ *    fn_load / fn_forward / fn_debug_layers run the model on one GPU (section 6); fn_bench_route times the
+ *    model's MoE routing.  The engine entry points (fn_reset, fn_use_graphs, fn_n_past, fn_dev_gb, fn_last_ms, fn_split,
  *    fn_free) act on the loaded model, else on the path engine of section 4, and return -1 like the reference's
  *    when neither is loaded.
  * ====================================================================================================== */
@@ -70,6 +70,10 @@ void fn_bench_hot(int on);                                                    /*
  * reading its own copy of the weight (copies beyond the 256 MB Infinity Cache, 512 MiB written before the timed
  * replay) unless fn_bench_hot(1). */
 int fn_bench_gemv(uint32_t type, int rows, int cols, int nt, int iters, float *ms);  /* faie2fn.cu:2823 */
+/* MoE routing (softmax top-10 of 512 router logits, ties to the lower expert, weights renormalized over the picks)
+ * of nt tokens 1..8, the logits summed from part [ks][8][528] (ks 1..64 split-K partials, the reference's layout),
+ * iters calls replayed as one hipGraph: ms per call, sel / wsel [nt][10].  variant 0 ranks every expert, variant 1
+ * is the model forward's one-wave routing; both give the same bits. */
 int fn_bench_route(int variant, int nt, int ks, const float *part, int iters, int *sel, float *wsel,
                    float *ms);                                                /* faie2fn.cu:2875 */
 /* y [nt][rows] = W x for GGUF rows W and x [nt][cols], nt 1..8 (packed, then the GEMV of section 5). */

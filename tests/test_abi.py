@@ -42,8 +42,6 @@ def test_reference_entries_report_not_built(fnlib):
         fnlib.reset()
     with pytest.raises(RuntimeError, match="not loaded"):
         fnlib.forward([1, 2, 3])
-    assert d.fn_bench_route(0, 1, 1, None, 1, None, None, None) == -1
-    assert b"not built" in d.fn_error()
     assert d.fn_split() == -1 and d.fn_n_past() == -1
     assert d.fn_dev_gb(0) == -1.0 and d.fn_last_ms() == -1.0
     d.fn_pdl(0), d.fn_early(0), d.fn_moe_var(1), d.fn_bench_hot(1), d.fn_free()
@@ -234,3 +232,26 @@ def test_gemv_group_refuses_bad_arguments(fnlib):
     assert b"null part" in d.fn_error()
     assert d.fn_gemv_group_dev(2, ty, rows, 2560, fake, 4096, 9, fake, None) == -1
     assert b"nt must be" in d.fn_error()
+
+
+def test_bench_route_refuses_bad_arguments(fnlib):
+    """fn_bench_route checks its arguments before any device work (engine/faie2fn.cu:2875's arguments)."""
+    d = fnlib.d
+    part = np.zeros((1, 8, 528), np.float32)
+    sel = np.zeros(80, np.int32)
+    w = np.zeros(80, np.float32)
+    ms = np.zeros(1, np.float32)
+    args = lambda v, nt, ks, it: (v, nt, ks, part.ctypes.data, it, sel.ctypes.data, w.ctypes.data,  # noqa: E731
+                                  ms.ctypes.data)
+    assert d.fn_bench_route(*args(2, 1, 1, 1)) == -1
+    assert b"variant" in d.fn_error()
+    assert d.fn_bench_route(*args(0, 9, 1, 1)) == -1
+    assert b"nt must be" in d.fn_error()
+    assert d.fn_bench_route(*args(1, 1, 0, 1)) == -1
+    assert b"ks must be" in d.fn_error()
+    assert d.fn_bench_route(*args(1, 1, 1, 0)) == -1
+    assert b"iters" in d.fn_error()
+    assert d.fn_bench_route(0, 1, 1, None, 1, None, None, None) == -1
+    assert b"null pointer" in d.fn_error()
+    with pytest.raises(ValueError):
+        fnlib.bench_route(0, np.zeros((1, 8, 500), np.float32), 1)
