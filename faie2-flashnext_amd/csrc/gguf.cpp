@@ -216,9 +216,16 @@ int gguf_open(Gguf &g, const char *path) {
             set_error("gguf: tensor " + kv.first + ": rows are not whole blocks of its type");
             return -1;
         }
-        const uint64_t rows = t.ne[1] * t.ne[2] * t.ne[3];
-        t.nbytes = t.ne[0] / (uint64_t) qk * (uint64_t) bb * rows;
-        if (t.offset % g.alignment || data0 + t.offset > g.size || t.nbytes > g.size - data0 - t.offset) {
+        // the byte count in 64 bits without wrapping (a header can claim any sizes)
+        uint64_t rows = 0, row_bytes = 0;
+        if (__builtin_mul_overflow(t.ne[1], t.ne[2], &rows) || __builtin_mul_overflow(rows, t.ne[3], &rows) ||
+            __builtin_mul_overflow(t.ne[0] / (uint64_t) qk, (uint64_t) bb, &row_bytes) ||
+            __builtin_mul_overflow(row_bytes, rows, &t.nbytes)) {
+            set_error("gguf: tensor " + kv.first + " has implausible dimensions");
+            return -1;
+        }
+        if (t.offset % g.alignment || data0 > g.size || t.offset > g.size - data0 ||
+            t.nbytes > g.size - data0 - t.offset) {
             set_error("gguf: tensor " + kv.first + " lies outside the file or is misaligned");
             return -1;
         }

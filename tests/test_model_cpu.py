@@ -79,6 +79,10 @@ def test_reader_rejects_malformed_files(fnlib, tmp_path, tiny):
     open(p, "wb").write(raw[: len(raw) - 1000])
     assert "outside the file" in _err(fnlib, p)
     assert "cannot open" in _err(fnlib, str(tmp_path / "missing.gguf"))
+    # dimensions whose byte count wraps 64 bits (2^33 rows x 2^32 x 2^32) are refused, not wrapped into range
+    name, ty, dims, data = ts[0]
+    ms.write_gguf(p, kv, [(name, ty, [dims[0], 1 << 33, 1 << 32, 1 << 32], data)] + list(ts[1:]))
+    assert "implausible dimensions" in _err(fnlib, p)
 
 
 def test_reader_rejects_unbuilt_shapes(fnlib, tmp_path):
