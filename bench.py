@@ -592,6 +592,19 @@ def route_extras(lib, iters=200):
     return out
 
 
+def cpu_model():
+    """The host CPU's model name (Linux /proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(budget_s=12.0):
     """The float64 C oracle (OpenMP over all host cores) on a bounded sample of the headline workload: B = 64
     sequences of one layer, decode steps repeated until about budget_s seconds of CPU work.  Same unit as value."""
@@ -614,7 +627,7 @@ def cpu_baseline(budget_s=12.0):
             break
     per = el / n
     return {"value": round(fn_synth.gdn_block_bytes(64) / per / 1e9, 4), "unit": "GB/s",
-            "us_per_layer_step": round(per * 1e6, 1), "cores": cores, "kind": "port",
+            "us_per_layer_step": round(per * 1e6, 1), "cores": cores, "cpu": cpu_model(), "kind": "port",
             "sample": f"float64 C oracle (oracle/fn_oracle.c, OpenMP {cores} threads), fused DeltaNet block, B=64, "
                       f"1 layer x {n} decode steps ({el:.1f} s)"}
 
