@@ -235,10 +235,11 @@ def test_model_token_count_invariance(fnlib, tmp_path):
     assert _rel(a, b) <= 1e-6
 
 
-@pytest.mark.parametrize("ne,neu", [(24, 10), (40, 17)])
+@pytest.mark.parametrize("ne,neu", [(24, 10), (40, 17), (600, 10)])
 def test_model_expert_counts(fnlib, tmp_path, ne, neu):
     """The reference model's 10 experts a token, and 17 (the MoE output kernel then takes its items in two passes a
-    wave for one token, and the several-token kernel three chunks of weight words), against the oracle."""
+    wave for one token, and the several-token kernel three chunks of weight words), and 600 experts (more than 512:
+    the routing holds 16 logits a lane instead of 8), against the oracle."""
     dims = dict(ms.TINY_DIMS, NE=ne, NEU=neu)
     p = str(tmp_path / "experts.gguf")
     kv, ts = ms.write_model(p, dims, seed=13)
