@@ -8,7 +8,8 @@ namespace fn {
 
 namespace {
 
-constexpr int HC_DR = 8;  // rows of the down weight a workgroup sums (2 per wave)
+constexpr int HC_RW = 1;          // rows of the down weight a wave sums (one: 4 rows a workgroup, the most workgroups)
+constexpr int HC_DR = 4 * HC_RW;  // rows a workgroup sums
 constexpr int HC_CH = 4;  // float4s of a stream a thread takes (D <= 4096)
 
 // grid (ceil(R / HC_DR), HC), 256 threads; stream k = blockIdx.y.  Every workgroup of stream k computes, for t < NT,
@@ -27,11 +28,11 @@ __global__ void __launch_bounds__(256) k_hc_down(const float *__restrict__ h, co
     constexpr int NWB = Q<QT_BF16>::NW, GPL = 2;  // groups per lane per row (G <= 128)
     const int k = blockIdx.y, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, G = D / 32, D4 = D / 4;
     const bool writer = blockIdx.x == 0;
-    // the wave's two rows' weight words first: they do not depend on the streams
-    uint32_t wr[2][GPL][NWB];
-    const int r0 = blockIdx.x * HC_DR + wv * 2;
+    // the wave's rows' weight words first: they do not depend on the streams
+    uint32_t wr[HC_RW][GPL][NWB];
+    const int r0 = blockIdx.x * HC_DR + wv * HC_RW;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < HC_RW; ++j) {
         RP rp = row_planes(W, min(r0 + j, R - 1));
         rp.b0 += (size_t) k * D * 2;  // stream k's columns
 #pragma unroll
@@ -97,7 +98,7 @@ __global__ void __launch_bounds__(256) k_hc_down(const float *__restrict__ h, co
     __syncthreads();
     const Iq4Tab T;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < HC_RW; ++j) {
         const int r = r0 + j;
         float acc[NT];
 #pragma unroll
