@@ -114,6 +114,31 @@ __device__ __forceinline__ void wave_argmax(float &v, int &i) {
     v = m;
 }
 
+// maximum of a 64-bit key over the wave, wave-uniform, through DPP alone (no LDS crossbar): row_shr 1, 2, 4, 8 leave
+// each row's maximum in its lane 15, row_bcast 15 and row_bcast 31 join the rows, lane 63 holds the result.  Lanes
+// without a DPP source read 0, the identity of an unsigned maximum.  Call from wave-uniform control flow.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+    uint32_t hi = (uint32_t) (k >> 32), lo = (uint32_t) k;
+#define FN_KEY_STEP(CTRL, ROWS)                                                                                \
+    do {                                                                                                      \
+        const uint32_t h2 = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) hi, CTRL, ROWS, 0xf, true);       \
+        const uint32_t l2 = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) lo, CTRL, ROWS, 0xf, true);       \
+        if ((((uint64_t) h2 << 32) | l2) > (((uint64_t) hi << 32) | lo)) {                                    \
+            hi = h2;                                                                                          \
+            lo = l2;                                                                                          \
+        }                                                                                                     \
+    } while (0)
+    FN_KEY_STEP(0x111, 0xf);  // row_shr 1
+    FN_KEY_STEP(0x112, 0xf);  // row_shr 2
+    FN_KEY_STEP(0x114, 0xf);  // row_shr 4
+    FN_KEY_STEP(0x118, 0xf);  // row_shr 8
+    FN_KEY_STEP(0x142, 0xa);  // row_bcast 15: lane 15 of rows 0 and 2 into rows 1 and 3
+    FN_KEY_STEP(0x143, 0xc);  // row_bcast 31: lane 31 into rows 2 and 3
+#undef FN_KEY_STEP
+    return ((uint64_t) (uint32_t) __builtin_amdgcn_readlane((int) hi, 63) << 32) |
+           (uint32_t) __builtin_amdgcn_readlane((int) lo, 63);
+}
+
 // MoE routing of one token by one whole wave (faie2fn.cu:1747-1798): p = softmax of the NE <= 1024 router logits
 // l[0..NE), picked in order probability descending with ties to the lower expert (repeated argmax), npick picks.
 // Returns pick `want`'s expert to every lane; with sel / wsel non-null (npick = NEU) it also writes the NEU picks
@@ -147,7 +172,14 @@ __device__ __forceinline__ int route_wave(const float *__restrict__ l, int NE, i
                 bv = v[j];
                 bi = lane + 64 * j;
             }
-        wave_argmax(bv, bi);
+        // one reduction of (value, index) as a 64-bit key: a probability's bits order like the probability (it is
+        // >= 0), the complemented index puts the lower expert first on a tie, and 0 is no candidate
+        {
+            const uint64_t key = bv >= 0.0f ? ((uint64_t) __float_as_uint(bv) << 32) | (uint32_t) ~bi : 0;
+            const uint64_t best = wave_max_key(key);
+            bv = __uint_as_float((uint32_t) (best >> 32));
+            bi = (int) ~(uint32_t) best;
+        }
 #pragma unroll
         for (int j = 0; j < PER; ++j)
             if (lane + 64 * j == bi) v[j] = -1.0f;  // taken
@@ -157,7 +189,7 @@ __device__ __forceinline__ int route_wave(const float *__restrict__ l, int NE, i
     }
     if (wsel) {
         float sum = 0.0f;
-        for (int k = 0; k < npick; ++k) sum += __shfl(mine, k);
+        for (int k = 0; k < npick; ++k) sum += readlane(mine, k);  // in pick order
         if (lane < npick) wsel[lane] = mine / sum;
     }
     return got;

@@ -1147,9 +1147,14 @@ __global__ void __launch_bounds__(256) k_rows(PP Pg, PP Pu, int R, int nexp, int
         for (int k = 0; k < ROWS_PRE; ++k) Q<TY>::load(rw, min(li + 16 * k, G - 1), w[k]);  // (clamped: valid address)
     };
     if (!routed) load_pre(sel ? sel[p] : 0);
-    const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t) (p / xdiv) * cols);
-    for (int i = tid; i < G * 8; i += 256) xs[(i >> 3) * 9 + (i & 7)] = xp[i];
-    tab_fill<TY>(tid, blockDim.x);
+    // x and the codebook into the LDS; a routed call leaves wave 0 out, so that its router logits, the first thing
+    // it loads, wait behind nothing
+    const int s0 = routed ? 64 : 0;
+    if (tid >= s0) {
+        const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t) (p / xdiv) * cols);
+        for (int i = tid - s0; i < G * 8; i += 256 - s0) xs[(i >> 3) * 9 + (i & 7)] = xp[i];
+        tab_fill<TY>(tid - s0, 256 - s0);
+    }
     if (routed) {
         const int t = p / rt.NEU, k = p - t * rt.NEU;
         const bool writer = k == 0 && blockIdx.x == 0;
