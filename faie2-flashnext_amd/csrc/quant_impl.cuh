@@ -1082,6 +1082,36 @@ int gemv_t(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, in
 }
 
 // ------------------------------------------------------------------------------------------------------------
+// n float4 into the LDS with nth threads (thread tid takes elements tid, tid + nth, ...), in rounds of XR per thread:
+// a round's loads are all issued (unconditionally, clamped to the last element) before any of its stores, so it costs
+// one memory round trip -- a loop of load-then-store, or loads under a branch, waits for each load before the next.
+// Loads complete in issue order, so a caller issues the first round's loads (load), then other loads the LDS rows
+// are not waiting for, then the stores (store), then the further rounds (stage_rest, for n > XR nth).
+// src(e) returns element e, dst(e, v) stores it.
+template <int XR> struct LdsStage {
+    float4 r[XR];
+    template <typename Src> __device__ __forceinline__ void load(int n, int e0, int tid, int nth, const Src &src) {
+#pragma unroll
+        for (int k = 0; k < XR; ++k) r[k] = src(min(e0 + tid + nth * k, n - 1));
+    }
+    template <typename Dst>
+    __device__ __forceinline__ void store(int n, int e0, int tid, int nth, const Dst &dst) const {
+#pragma unroll
+        for (int k = 0; k < XR; ++k) {
+            const int e = e0 + tid + nth * k;
+            if (e < n) dst(e, r[k]);
+        }
+    }
+};
+template <int XR, typename Src, typename Dst>
+__device__ __forceinline__ void stage_rest(int n, int tid, int nth, const Src &src, const Dst &dst) {
+    for (int e0 = nth * XR; e0 < n; e0 += nth * XR) {
+        LdsStage<XR> st;
+        st.load(n, e0, tid, nth, src);
+        st.store(n, e0, tid, nth, dst);
+    }
+}
+
 // rows selected on the device: the model's token embedding and routed experts
 
 // embedding rows: out[t][k cols + c] = decoded W[ids[t]][c], for k < copies.  grid nt, 256 threads
@@ -1146,13 +1176,19 @@ __global__ void __launch_bounds__(256) k_rows(PP Pg, PP Pu, int R, int nexp, int
 #pragma unroll
         for (int k = 0; k < ROWS_PRE; ++k) Q<TY>::load(rw, min(li + 16 * k, G - 1), w[k]);  // (clamped: valid address)
     };
-    if (!routed) load_pre(sel ? sel[p] : 0);
     // x and the codebook into the LDS; a routed call leaves wave 0 out, so that its router logits, the first thing
-    // it loads, wait behind nothing
+    // it loads, wait behind nothing.  The x rows are requested before the weight words, whose arrival the LDS stores
+    // then do not wait for.
     const int s0 = routed ? 64 : 0;
+    const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t) (p / xdiv) * cols);
+    const auto xsrc = [&](int i) { return xp[i]; };
+    const auto xdst = [&](int i, float4 v) { xs[(i >> 3) * 9 + (i & 7)] = v; };
+    LdsStage<4> xst;
+    if (tid >= s0) xst.load(G * 8, 0, tid - s0, 256 - s0, xsrc);
+    if (!routed) load_pre(sel ? sel[p] : 0);
     if (tid >= s0) {
-        const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t) (p / xdiv) * cols);
-        for (int i = tid - s0; i < G * 8; i += 256 - s0) xs[(i >> 3) * 9 + (i & 7)] = xp[i];
+        xst.store(G * 8, 0, tid - s0, 256 - s0, xdst);
+        stage_rest<4>(G * 8, tid - s0, 256 - s0, xsrc, xdst);
         tab_fill<TY>(tid - s0, 256 - s0);
     }
     if (routed) {

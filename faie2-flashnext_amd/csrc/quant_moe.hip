@@ -29,7 +29,10 @@ __global__ void __launch_bounds__(256) k_moe_down4(PP Pe, PP Ps, int R, int nexp
                                                    int NE, float *__restrict__ y) {
     extern __shared__ float4 xs[];  // [NEU + 1][G][9], then (floats) the dot products [NEU + 1][4] and factors
     constexpr int NW = Q<TY>::NW, NWS = Q<TS>::NW;
-    const int t = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63, li = lane & 15, q = lane >> 4;
+    // (the wave index made visibly uniform: the items' expert ids are then scalar loads, which do not wait behind the
+    // weight words already requested the way a vector load would)
+    const int t = blockIdx.y, tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63,
+              li = lane & 15, q = lane >> 4;
     const int r = blockIdx.x * 4 + q, rr = min(r, R - 1), NI = NEU + 1, G8 = G * 8;
     float *dsum = reinterpret_cast<float *>(xs + (size_t) NI * G * 9), *wl = dsum + NI * 4;
     const int32_t *es = sel + (size_t) t * NEU;
@@ -39,35 +42,45 @@ __global__ void __launch_bounds__(256) k_moe_down4(PP Pe, PP Ps, int R, int nexp
         wl[k] = k < NEU ? wsel[(size_t) t * NEU + k] : sigmoidf_(rsg[(size_t) t * (NE + 1) + NE]);
     for (int p0 = 0; p0 < NI; p0 += 4 * MOE_IPW) {  // (the same count in every wave)
         const int i0 = p0 + w;
+        // the pass's x rows (items p0 .. p0 + 4 MOE_IPW - 1), by the whole workgroup: requested first
+        const int ni = min(NI - p0, 4 * MOE_IPW), nx = ni * G8;
+        const auto xsrc = [&](int e) {
+            const int i = p0 + e / G8, j = e - (i - p0) * G8;
+            return reinterpret_cast<const float4 *>(i < NEU ? act + ((size_t) t * NEU + i) * cols
+                                                            : sha + (size_t) t * cols)[j];
+        };
+        const auto xdst = [&](int e, float4 v) {
+            const int i = p0 + e / G8, j = e - (i - p0) * G8;
+            xs[(i * G + (j >> 3)) * 9 + (j & 7)] = v;
+        };
+        LdsStage<8> xst;
+        xst.load(nx, 0, tid, 256, xsrc);
         uint32_t we[MOE_IPW][MOE_GPL][NW], ws[MOE_GPL][NWS];
-        bool has_s = false;
-        // weight words of the wave's items i0 + 4 j (groups li + 16 u, clamped to valid addresses)
+        const bool has_s = (NEU - i0) % 4 == 0 && NEU >= i0 && NEU < i0 + 4 * MOE_IPW;  // the shared item is ours
+        // weight words of the wave's items i0 + 4 j (groups li + 16 u, clamped to valid addresses).  Every load is
+        // issued, unconditionally: a slot past the experts re-requests the wave's last expert row (already on its
+        // way, so no new traffic), and every wave requests the shared row.  (Loads under a branch were merged into
+        // the array after the branch by register copies, each waiting for the load: one round trip per item.)
+        const int ilast = w < NEU ? w + 4 * ((NEU - 1 - w) / 4) : 0;
 #pragma unroll
         for (int j = 0; j < MOE_IPW; ++j) {
-            const int i = i0 + 4 * j;
-            if (i < NEU) {
-                const RP rp = row_planes(Pe, min(max(es[i], 0), nexp - 1) * R + rr);
+            const int i = i0 + 4 * j, ie = i < NEU ? i : ilast;
+            const RP rp = row_planes(Pe, min(max(es[ie], 0), nexp - 1) * R + rr);
 #pragma unroll
-                for (int u = 0; u < MOE_GPL; ++u) Q<TY>::load(rp, min(li + 16 * u, G - 1), we[j][u]);
-            } else if (i == NEU) {
-                has_s = true;
-                const RP rp = row_planes(Ps, rr);
+            for (int u = 0; u < MOE_GPL; ++u) Q<TY>::load(rp, min(li + 16 * u, G - 1), we[j][u]);
+        }
+        {
+            const RP rp = row_planes(Ps, rr);
 #pragma unroll
-                for (int u = 0; u < MOE_GPL; ++u) Q<TS>::load(rp, min(li + 16 * u, G - 1), ws[u]);
-            }
+            for (int u = 0; u < MOE_GPL; ++u) Q<TS>::load(rp, min(li + 16 * u, G - 1), ws[u]);
         }
         if (p0 == 0) {
             tab_fill<TY>(tid, 256);
             tab_fill<TS>(tid, 256);
         }
         // the pass's x rows (items p0 .. p0 + 4 MOE_IPW - 1) -> LDS, by the whole workgroup
-        const int ni = min(NI - p0, 4 * MOE_IPW);
-        for (int e = tid; e < ni * G8; e += 256) {
-            const int i = p0 + e / G8, j = e - (i - p0) * G8;
-            const float4 *src = reinterpret_cast<const float4 *>(i < NEU ? act + ((size_t) t * NEU + i) * cols
-                                                                         : sha + (size_t) t * cols);
-            xs[(i * G + (j >> 3)) * 9 + (j & 7)] = src[j];
-        }
+        xst.store(nx, 0, tid, 256, xdst);
+        stage_rest<8>(nx, tid, 256, xsrc, xdst);
         __syncthreads();
         const TabT<TY> T;
 #pragma unroll
@@ -131,6 +144,19 @@ __global__ void __launch_bounds__(256) k_moe_down16(PP Pe, PP Ps, int R, int nex
             for (int u = 0; u < MOE_GPL; ++u) Q<TY>::load(rp, min(li + 16 * u, G - 1), w[j][u]);
         }
     };
+    // the token's x rows requested first, then the weight words
+    const int G8 = G * 8, nx = (NEU + 1) * G8;
+    const auto xsrc = [&](int i) {
+        const int k = i / G8, j = i - k * G8;
+        return reinterpret_cast<const float4 *>(k < NEU ? act + ((size_t) t * NEU + k) * cols
+                                                        : sha + (size_t) t * cols)[j];
+    };
+    const auto xdst = [&](int i, float4 v) {
+        const int k = i / G8, j = i - k * G8;
+        xs[(k * G + (j >> 3)) * 9 + (j & 7)] = v;
+    };
+    LdsStage<8> xst;
+    xst.load(nx, 0, tid, 256, xsrc);
     load(0, wa);
     {
         const RP rp = row_planes(Ps, rr);
@@ -138,13 +164,8 @@ __global__ void __launch_bounds__(256) k_moe_down16(PP Pe, PP Ps, int R, int nex
         for (int u = 0; u < MOE_GPL; ++u) Q<TS>::load(rp, min(li + 16 * u, G - 1), ws[u]);
     }
     if (KC < NEU) load(KC, wb);
-    const int G8 = G * 8;
-    for (int i = tid; i < (NEU + 1) * G8; i += 256) {
-        const int k = i / G8, j = i - k * G8;
-        const float4 *src = reinterpret_cast<const float4 *>(k < NEU ? act + ((size_t) t * NEU + k) * cols
-                                                                     : sha + (size_t) t * cols);
-        xs[(k * G + (j >> 3)) * 9 + (j & 7)] = src[j];
-    }
+    xst.store(nx, 0, tid, 256, xdst);
+    stage_rest<8>(nx, tid, 256, xsrc, xdst);
     tab_fill<TY>(tid, 256);
     tab_fill<TS>(tid, 256);
     __syncthreads();
