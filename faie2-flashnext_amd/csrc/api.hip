@@ -30,13 +30,6 @@ using fn::use_device0;
 // ---------------------------------------------------------------------------------------------
 // 1. reference API
 
-namespace {
-
-// switches the reference exposes for its forward; kept so scripts that set them still run
-int g_pdl = 1, g_early = 1, g_moe_var = 0;
-
-}  // namespace
-
 // The engine entry points act on the loaded model (fn_load) if there is one, else on the path engine (fn_path_init).
 FN_API const char *fn_error(void) { return fn::error_cstr(); }
 FN_API void fn_free(void) {
@@ -63,9 +56,14 @@ FN_API int fn_forward(const int32_t *tokens, int nt, float *logits, int32_t *arg
     return fn::model_forward(tokens, nt, logits, argmax);
 }
 FN_API int fn_debug_layers(float *out) { return fn::model_debug_layers(out); }
-FN_API void fn_pdl(int on) { g_pdl = on != 0; }
-FN_API void fn_early(int on) { g_early = on != 0; }
-FN_API void fn_moe_var(int v) { g_moe_var = v; }
+// The reference's A/B switches for its CUDA forward, accepted so that its scripts bind and run; none changes what
+// this library launches.  fn_pdl / fn_early: programmatic dependent launch, and GEMVs started beside the kernel
+// before them under it, have no HIP counterpart (the forward is one hipGraph on one stream; graph branches for the
+// independent GEMVs measured slower).  fn_moe_var / fn_moe_override: tile shapes of the reference's expert kernels;
+// the expert kernels here have one shape each.
+FN_API void fn_pdl(int) {}
+FN_API void fn_early(int) {}
+FN_API void fn_moe_var(int) {}
 FN_API void fn_moe_override(int, int, int, int) {}
 
 FN_API int fn_model_dims(const char *path, int *out, int n) {

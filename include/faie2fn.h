@@ -55,6 +55,9 @@ void fn_gemv_override(int wpt, int ks, int tb, int warps_per_sm);             /*
  * each walking many row tiles; 0 launches one workgroup per row tile.  Same bits either way; fn_gemv_plan's out[5]
  * reports the choice for plans made afterwards. */
 void fn_gemv_waves(int waves);                                                /* faie2fn.cu:2793 */
+/* The reference's A/B switches for its CUDA forward (programmatic dependent launch, GEMVs started early under it,
+ * the expert kernels' tile shapes): accepted so that its scripts bind and run, no effect here (no HIP counterpart;
+ * one hipGraph per token count on one stream; one shape per expert kernel). */
 void fn_pdl(int on);                                                          /* faie2fn.cu:2796 */
 void fn_early(int on);                                                        /* faie2fn.cu:2798 */
 void fn_moe_var(int v);                                                       /* faie2fn.cu:2799 */
