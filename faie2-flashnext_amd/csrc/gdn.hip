@@ -80,8 +80,13 @@ constexpr int NG = 16, GROWS = DK / NG;
 __device__ __forceinline__ float4 ld_state(brsrc S, uint32_t so, int r) {
     return bld4<GDN_NT ? 2 : 0>(S, so, (uint32_t) r * NG * DV * 4);
 }
-__device__ __forceinline__ void st_state(brsrc S, uint32_t so, int r, float4 v) {
-    bst4<GDN_NT_ST ? 2 : 0>(S, so, (uint32_t) r * NG * DV * 4, v);
+// Cache policy of the state tile's stores: nontemporal (2), or nontemporal at system scope (2 | 16) for one-token
+// calls whose grid holds more workgroups than are resident at once, where the stores of one round of heads share
+// the memory with the loads of the next (B = 64: 49.2 -> 48.9 us per launch; at B = 1, one round, 5.21 -> 5.37 us,
+// so those keep the plain hint).  The policy changes no value.
+constexpr int ST_NT = GDN_NT_ST ? 2 : 0, ST_NT_SYS = ST_NT | 16;
+template <int AUX = ST_NT> __device__ __forceinline__ void st_state(brsrc S, uint32_t so, int r, float4 v) {
+    bst4<AUX>(S, so, (uint32_t) r * NG * DV * 4, v);
 }
 
 struct GdnArgs {
@@ -183,7 +188,7 @@ __device__ __forceinline__ void conv_store_hist(const ConvChan &cc, const GdnArg
     if (n >= 3) bst(ring, oc, slot_off(a, C, end - 3), cc.hist[0]);
 }
 
-template <int MODE, int NTH = (MODE == 1 || MODE == 2) ? MT_THREADS : THREADS>
+template <int MODE, int NTH = (MODE == 1 || MODE == 2) ? MT_THREADS : THREADS, int SAUX = ST_NT>
 __global__ void __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu((MODE == 1 || MODE == 2) ? GDN_VERIFY_WPE : GDN_WPE, 8)))
 k_gdn(const GdnArgs a) {
     constexpr int WAVES = NTH / 64;
@@ -355,7 +360,7 @@ k_gdn(const GdnArgs a) {
 #pragma unroll
                 for (int j = 0; j < CH; ++j)
 #pragma unroll
-                    for (int r = 0; r < GROWS; ++r) st_state(Sb, so + j * DV * 4, r, s[j][r]);
+                    for (int r = 0; r < GROWS; ++r) st_state<SAUX>(Sb, so + j * DV * 4, r, s[j][r]);
                 if (qk_thr) {
                     if (primary) {
                         conv_store_hist(c0, a, ring, C, o0, pos + kr, kr);
@@ -530,7 +535,7 @@ k_gdn(const GdnArgs a) {
 #pragma unroll
     for (int j = 0; j < CH; ++j)
 #pragma unroll
-        for (int r = 0; r < GROWS; ++r) st_state(Sb, so + j * DV * 4, r, s[j][r]);
+        for (int r = 0; r < GROWS; ++r) st_state<SAUX>(Sb, so + j * DV * 4, r, s[j][r]);
     if (FUSED) {
         if (qk_thr) {
             if (primary) {
@@ -574,8 +579,12 @@ int gdn_block_launch(const GdnBlock &p, hipStream_t st) {
     a.gate_act = p.gate_act; a.eps = p.eps; a.pos = p.pos; a.qkv = p.qkv; a.conv_w = p.conv_w;
     a.ring_buf = p.conv_ring; a.ab = p.ab; a.dt_bias = p.dt_bias; a.ssm_a = p.ssm_a; a.S = p.S; a.z = p.z;
     a.norm_w = p.norm_w; a.out = p.out; a.x = p.x; a.wab = p.wab; a.hidden = p.hidden;
-    if (p.nt == 1) hipLaunchKernelGGL(k_gdn<3>, dim3(p.B * p.nvh), dim3(THREADS), GDN_ONE_LDS_PAD, st, a);
-    else hipLaunchKernelGGL(k_gdn<1>, dim3(p.B * p.nvh), dim3(MT_THREADS), 0, st, a);
+    if (p.nt == 1 && p.B * p.nvh > 2 * device_cus())  // more heads than one round of resident workgroups (two a CU)
+        hipLaunchKernelGGL((k_gdn<3, THREADS, ST_NT_SYS>), dim3(p.B * p.nvh), dim3(THREADS), GDN_ONE_LDS_PAD, st, a);
+    else if (p.nt == 1)
+        hipLaunchKernelGGL(k_gdn<3>, dim3(p.B * p.nvh), dim3(THREADS), GDN_ONE_LDS_PAD, st, a);
+    else
+        hipLaunchKernelGGL(k_gdn<1>, dim3(p.B * p.nvh), dim3(MT_THREADS), 0, st, a);
     FN_CK(hipGetLastError());
     return 0;
 }
