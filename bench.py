@@ -340,8 +340,8 @@ class QsaStack:
             self.layers.append(d)
         hiprt.sync()
 
-    def launch(self, stream):
-        for d in self.layers:
+    def launch(self, stream, layers=None):
+        for d in (self.layers if layers is None else layers):
             self.lib.attn_qsa_dev(self.B, self.nq, self.nkv, 1, self.max_ctx, self.pos.ptr, d["qg"].ptr, d["k"].ptr,
                                   d["v"].ptr, d["wq"].ptr, d["wk"].ptr, d["K"].ptr, d["V"].ptr, d["iqk"].ptr,
                                   d["wqn"].ptr, d["wkn"].ptr, d["IK"].ptr, d["BK"].ptr, self.top, self.nsplit,
@@ -353,6 +353,55 @@ class QsaStack:
                 b.free()
         self.pos.free()
         self.work.free()
+
+
+def stage_split(lib, stream, stack, names, reps=24):
+    """Per-kernel µs of one attention layer-step of `stack` (its kernels in launch order, `names`), from HIP events
+    the library records after each launch (fn_stage_events): eager launches queued behind ~1 ms of copies, so the
+    device runs them back to back; the median over reps layer-steps (layers in turn).  The events add a marker
+    between kernels, so the sum runs a little above the graph-replayed layer-step."""
+    big = [hiprt.Buf(1 << 30), hiprt.Buf(1 << 30)]
+    evs = [[hiprt.Event() for _ in range(len(names) + 1)] for _ in range(reps)]
+    try:
+        stack.launch(stream)
+        stream.sync()
+        for _ in range(3):
+            lib.copy_dev(big[1].ptr, big[0].ptr, 1 << 30, stream.handle)
+        for r in range(reps):
+            evs[r][0].record(stream)
+            lib.stage_events([e.handle for e in evs[r][1:]])
+            stack.launch(stream, layers=[stack.layers[r % len(stack.layers)]])
+        lib.stage_events([])
+        stream.sync()
+        per = np.array([[evs[r][i + 1].ms_since(evs[r][i]) * 1e3 for i in range(len(names))] for r in range(reps)])
+    finally:
+        lib.stage_events([])
+        for b in big:
+            b.free()
+    med = np.median(per, axis=0)
+    out = {n: round(float(v), 2) for n, v in zip(names, med)}
+    out["sum"] = round(float(med.sum()), 2)
+    return out
+
+
+QSA_STAGES = ("k_ix_prep", "k_ix_score", "k_ix_select", "k_attn_split_list", "k_attn_combine")
+DENSE_STAGES = ("k_attn_split", "k_attn_combine")
+
+
+def stage_extras(lib, stream):
+    """The per-kernel split of the sparse (QSA) attention chain and of dense GQA decode at the config-3 shapes."""
+    res = {}
+    for Bq, ctx, nl in ((1, 32768, 8), (1, 131072, 4), (16, 32768, 2)):
+        qs = QsaStack(lib, Bq, ctx, nl, seed=5)
+        res[f"qsa_b{Bq}_ctx{ctx}"] = stage_split(lib, stream, qs, QSA_STAGES)
+        qs.free()
+        log(f"[bench] QSA B={Bq} ctx={ctx} per kernel: {res[f'qsa_b{Bq}_ctx{ctx}']}")
+    for Bq, ctx, nl in ((1, 4096, 32), (16, 4096, 8), (1, 32768, 8)):
+        at = AttnStack(lib, Bq, ctx, nl, seed=3)
+        res[f"gqa_b{Bq}_ctx{ctx}"] = stage_split(lib, stream, at, DENSE_STAGES)
+        at.free()
+        log(f"[bench] GQA B={Bq} ctx={ctx} per kernel: {res[f'gqa_b{Bq}_ctx{ctx}']}")
+    return res
 
 
 def hybrid_config4(lib, steps, warmup, B=16, ctx=32768, nl=48):
@@ -386,7 +435,8 @@ def hybrid_config4(lib, steps, warmup, B=16, ctx=32768, nl=48):
         ms = lib.path_step(steps, timed=True)
     finally:
         lib.free()
-    nbytes = 36 * fn_synth.gdn_block_bytes(B) + 12 * fn_synth.attn_bytes(B, ctx)
+    n_attn = nl // 4
+    nbytes = (nl - n_attn) * fn_synth.gdn_block_bytes(B) + n_attn * fn_synth.attn_bytes(B, ctx)
     return ms, nbytes
 
 
@@ -418,6 +468,45 @@ def hybrid_verify(lib, stream, steps, warmup, B=16, ctx=32768, nt=4, kr=2, nl=48
         at.free()
     nbytes = (nl - nl // 4) * fn_synth.gdn_verify_bytes(B, nt, kr) + (nl // 4) * fn_synth.attn_bytes(B, ctx, nt=nt)
     return ms, nbytes
+
+
+# config 3's GQA decode legs (B, context, distinct layers: enough that the caches exceed the 256 MB Infinity Cache)
+GQA_LEGS = ((1, 4096, 32), (1, 32768, 8), (1, 131072, 2), (16, 4096, 8), (16, 32768, 2), (16, 131072, 1))
+# the north star's batch of 64 (GQA decode and the fused hybrid step)
+GQA_LEGS_B64 = ((64, 4096, 2), (64, 32768, 1))
+HYBRID_B64_CTX = (4096, 32768)
+
+
+def gqa_leg(lib, stream, steps, warmup, Bq, ctx, nl):
+    """One config-3 GQA decode leg: µs per layer-step over nl distinct layers, GB/s and fraction of the 8 TB/s peak."""
+    at = AttnStack(lib, Bq, ctx, nl, seed=3)
+    ms = time_graph(stream, lambda: at.launch(stream), steps, warmup) / nl
+    nsplit = at.nsplit
+    at.free()
+    by = fn_synth.attn_bytes(Bq, ctx)
+    gbs = by / (ms * 1e-3) / 1e9
+    log(f"[bench] config 3 B={Bq} ctx={ctx}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s")
+    return {"us_per_layer_step": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "nsplit": nsplit}
+
+
+def hybrid_leg(lib, steps, warmup, B, ctx):
+    """The hybrid 48-layer step (config 4's stack) at batch B and context ctx through the path engine."""
+    ms, nbytes = hybrid_config4(lib, steps, warmup, B=B, ctx=ctx)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] config 4 stack B={B} ctx={ctx}: {ms:.3f} ms/step, {gbs:.0f} GB/s")
+    return {"ms_per_step": round(ms, 4), "us_per_token": round(ms * 1e3 / B, 2), "tokens_per_s": round(B * 1e3 / ms, 1),
+            "bytes_per_step": nbytes, "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+
+
+def b64_extras(lib, stream, steps, warmup):
+    """GQA decode and the fused DeltaNet + GQA hybrid step at the north star's batch of 64."""
+    res = {}
+    for Bq, ctx, nl in GQA_LEGS_B64:
+        res[f"config3_gqa_b{Bq}_ctx{ctx}"] = gqa_leg(lib, stream, steps, warmup, Bq, ctx, nl)
+    for ctx in HYBRID_B64_CTX:
+        res[f"config4_hybrid_b64_ctx{ctx}"] = hybrid_leg(lib, steps, warmup, 64, ctx)
+    return res
 
 
 def model_decode(lib, nl=8, ctx=4096, tokens=64, seed=0, nts=(1, 8)):
@@ -660,6 +749,12 @@ def main():
                     help="skip the whole-model leg of the extra legs (48 layers, ~47 GB written to /dev/shm and loaded)")
     ap.add_argument("--mt-only", action="store_true",
                     help="only the multi-token GQA legs (config 3 shapes, nt = 4 and 8, hipGraph replays)")
+    ap.add_argument("--stages", action="store_true",
+                    help="only the per-kernel split of the QSA chain and of dense GQA decode (HIP events after each "
+                         "launch, no profiler)")
+    ap.add_argument("--b64-only", action="store_true",
+                    help="only the batch-64 legs: GQA decode at 4K and 32K context and the 48-layer hybrid step at "
+                         "4K and 32K (hipGraph replays)")
     ap.add_argument("--counters-attn", action="store_true",
                     help="counter-collection workload only: 5 eager multi-token GQA layer-steps at B=16, 32K context, "
                          "nt=8 then 5 at nt=4 (k_attn_split_mt<2>)")
@@ -676,6 +771,14 @@ def main():
     if args.model:
         res = model_decode(lib, nl=args.model, nts=(args.model_nt,) if args.model_nt else (1, 8))
         print(json.dumps({"model_decode": res}), flush=True)
+        return
+    if args.stages:
+        res = stage_extras(lib, stream)
+        print(json.dumps({"stages": res}), flush=True)
+        return
+    if args.b64_only:
+        res = b64_extras(lib, stream, steps, warmup)
+        print(json.dumps({"b64": res}), flush=True)
         return
     if args.mt_only:
         res = {}
@@ -805,16 +908,8 @@ def main():
         log(f"[bench] config 2 prefill nt=4: {ms * 1e3 / 36:.2f} us/layer-step")
     if not args.no_extra and not args.gdn_only:
         # config 3: GQA decode
-        for Bq, ctx, nl in ((1, 4096, 32), (1, 32768, 8), (1, 131072, 2), (16, 4096, 8), (16, 32768, 2),
-                            (16, 131072, 1)):
-            at = AttnStack(lib, Bq, ctx, nl, seed=3)
-            ms = time_graph(stream, lambda: at.launch(stream), steps, warmup) / nl
-            nsplit = at.nsplit
-            at.free()
-            by = fn_synth.attn_bytes(Bq, ctx)
-            extra[f"config3_gqa_b{Bq}_ctx{ctx}"] = {"us_per_layer_step": round(ms * 1e3, 2),
-                                                   "gbs": round(by / (ms * 1e-3) / 1e9, 1), "nsplit": nsplit}
-            log(f"[bench] config 3 B={Bq} ctx={ctx}: {ms * 1e3:.1f} us, {by / (ms * 1e-3) / 1e9:.0f} GB/s")
+        for Bq, ctx, nl in GQA_LEGS:
+            extra[f"config3_gqa_b{Bq}_ctx{ctx}"] = gqa_leg(lib, stream, steps, warmup, Bq, ctx, nl)
         if not args.attn_only:
             # config 3 multi-token (speculative verify / chunked prefill): nt new tokens per sequence share one K/V pass
             # on the matrix cores; GB/s counts K/V once, TFLOP/s the fp32 products (peak 157.3)
@@ -855,6 +950,7 @@ def main():
             extra.update(gemv_extras(lib))
             extra.update(group_extras(lib, stream))
             extra.update(route_extras(lib))
+            extra["kernel_split_us"] = stage_extras(lib, stream)
             ms, nbytes = hybrid_config4(lib, steps, warmup)
             ms_v, by_v = hybrid_verify(lib, stream, steps, warmup)
             extra["config4_hybrid_verify_b16_ctx32768_nt4_kr2"] = {
@@ -866,6 +962,8 @@ def main():
                                                    "tokens_per_s": round(16 * 1e3 / ms, 1), "bytes_per_step": nbytes,
                                                    "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                                                    "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+            # the north star's batch of 64: GQA decode legs and the hybrid step
+            extra.update(b64_extras(lib, stream, steps, warmup))
     if not args.no_extra and not args.gdn_only and not args.attn_only and not args.no_model:
         # the whole model at the reference's 48 layers, one-token greedy decode (the reference's 5.70 ms per forward);
         # a box without the room for its 47 GB file (or the device memory) reports why instead of failing the run

@@ -160,6 +160,8 @@ FN_API int fn_copy_dev(void *dst, const void *src, size_t bytes, void *stream) {
     return fn::copy_launch(dst, src, bytes, (hipStream_t) stream);
 }
 
+FN_API int fn_stage_events(void **events, int n) { return fn::stage_events(events, n); }
+
 FN_API size_t fn_attn_qsa_work_bytes(int B, int nq, int nt, int hd, int nsplit, int max_ctx, int top) {
     if (B < 1 || nq < 1 || nt < 1 || hd < 1 || nsplit < 1 || max_ctx < 1 || top < 1) return 0;
     return fn::attn_qsa_work_bytes(B, nq, nt, hd, nsplit, max_ctx, top) + 256;

@@ -903,7 +903,10 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
     // one new token per sequence: the split kernel does the norm/RoPE/append itself (one launch fewer); several
     // tokens see each other's new keys, so they go through k_attn_prep first
     const bool fused = p.nt == 1;
-    if (!fused) hipLaunchKernelGGL(k_attn_prep, dim3((unsigned) bt, p.nq + p.nkv), dim3(HD), 0, st, a);
+    if (!fused) {
+        hipLaunchKernelGGL(k_attn_prep, dim3((unsigned) bt, p.nq + p.nkv), dim3(HD), 0, st, a);
+        stage_mark(st);
+    }
     const int nr = (p.nt * grp + 15) / 16;  // 16-row blocks of the multi-token query matrix
     if (fused) {
         if (grp == 8) hipLaunchKernelGGL((k_attn_split<8, true>), sg, sb, 0, st, a);
@@ -922,7 +925,9 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
         else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, false>), sg, sb, 0, st, a);
         else hipLaunchKernelGGL((k_attn_split<4, false>), sg, sb, 0, st, a);
     }
+    stage_mark(st);
     hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(combine_waves(p.nsplit) * 64), 0, st, a);
+    stage_mark(st);
     FN_CK(hipGetLastError());
     return 0;
 }
@@ -968,11 +973,14 @@ int attn_qsa_launch(const AttnDecode &p, const QsaIndexer &ix, hipStream_t st) {
         else hipLaunchKernelGGL((k_attn_split<4, true, true>), sg, sb, 0, st, a);
     } else {
         hipLaunchKernelGGL(k_attn_prep, dim3((unsigned) bt, p.nq + p.nkv), dim3(HD), 0, st, a);
+        stage_mark(st);
         if (grp == 8) hipLaunchKernelGGL((k_attn_split<8, false, true>), sg, sb, 0, st, a);
         else if (grp == 12) hipLaunchKernelGGL((k_attn_split<12, false, true>), sg, sb, 0, st, a);
         else hipLaunchKernelGGL((k_attn_split<4, false, true>), sg, sb, 0, st, a);
     }
+    stage_mark(st);
     hipLaunchKernelGGL(k_attn_combine, dim3(p.nq, (unsigned) bt), dim3(combine_waves(p.nsplit) * 64), 0, st, a);
+    stage_mark(st);
     FN_CK(hipGetLastError());
     return 0;
 }

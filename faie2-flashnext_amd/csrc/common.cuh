@@ -34,6 +34,11 @@ const char *error_cstr();
 // compute units of the current device (queried once; 256, MI355X, if the query fails)
 int device_cus();
 
+// Per-kernel timing without a profiler: while a list of events is set (fn_stage_events), the attention paths
+// record the next event of the list on the call's stream after each of their launches; stage_mark does nothing
+// when no list is set or the list is used up.  Not for graph capture.
+void stage_mark(hipStream_t st);
+
 // ---------------------------------------------------------------------------------------------
 // wave64 cross-lane primitives.  Rotations inside a row of 16 lanes go through DPP (row_ror), the exchange
 // between the two rows of each 32-lane half through ds_swizzle (bit mode, xor 16), and the two halves of the

@@ -77,5 +77,6 @@ int status_read(unsigned *bits, bool clear);
 
 int fill_normal_launch(float *p, size_t n, uint64_t seed, float mean, float std, hipStream_t st);
 int copy_launch(void *dst, const void *src, size_t bytes, hipStream_t st);
+int stage_events(void **ev, int n);
 
 }  // namespace fn

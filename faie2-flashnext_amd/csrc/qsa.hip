@@ -368,13 +368,16 @@ int qsa_select_launch(const QsaIndexer &p, float *work, size_t work_bytes, const
     const int G = (int) std::max<size_t>(1, std::min<size_t>(tiles, (1024 + bt - 1) / bt));
     const int nbmax = p.max_ctx / IXR;
     hipLaunchKernelGGL(k_ix_prep, dim3(p.B), dim3(256), 0, st, a);
+    stage_mark(st);
     hipLaunchKernelGGL(k_ix_score, dim3((unsigned) bt, G), dim3(256), 0, st, a);
+    stage_mark(st);
     if (nbmax <= 1024 * 8)
         hipLaunchKernelGGL(k_ix_select<8>, dim3((unsigned) bt), dim3(1024), 0, st, a);
     else if (nbmax <= 1024 * 32)
         hipLaunchKernelGGL(k_ix_select<32>, dim3((unsigned) bt), dim3(1024), 0, st, a);
     else
         hipLaunchKernelGGL(k_ix_select<0>, dim3((unsigned) bt), dim3(1024), 0, st, a);
+    stage_mark(st);
     FN_CK(hipGetLastError());
     return 0;
 }

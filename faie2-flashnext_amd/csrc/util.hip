@@ -5,6 +5,7 @@
 #include "gdn.h"
 
 #include <mutex>
+#include <vector>
 
 namespace fn {
 
@@ -84,6 +85,22 @@ int status_read(unsigned *bits, bool clear) {
         FN_CK(hipMemcpy(w, &zero, sizeof(unsigned), hipMemcpyHostToDevice));
     }
     return 0;
+}
+
+namespace {
+std::vector<hipEvent_t> g_stage_ev;
+size_t g_stage_next = 0;
+}  // namespace
+
+int stage_events(void **ev, int n) {
+    if (n < 0 || n > 64 || (n && !ev)) FN_FAIL("stage_events: 0..64 events");
+    g_stage_ev.assign(reinterpret_cast<hipEvent_t *>(ev), reinterpret_cast<hipEvent_t *>(ev) + n);
+    g_stage_next = 0;
+    return 0;
+}
+
+void stage_mark(hipStream_t st) {
+    if (g_stage_next < g_stage_ev.size()) (void) hipEventRecord(g_stage_ev[g_stage_next++], st);
 }
 
 int fill_normal_launch(float *p, size_t n, uint64_t seed, float mean, float std, hipStream_t st) {

@@ -37,7 +37,7 @@ SYMBOLS = (
     "fn_attn_qsa_dev", "fn_attn_qsa_work_bytes", "fn_ix_blocks_dev", "fn_test_attn_qsa",
     "fn_gemv_packed_bytes", "fn_gemv_pack_dev", "fn_dequant_dev", "fn_gemv_work_bytes", "fn_gemv_dev",
     "fn_gdn_verify_dev", "fn_advance_by_dev", "fn_gdn_block_xab_dev",
-    "fn_attn_noalloc_dev", "fn_dev_status", "fn_model_dims", "fn_gemv_group_dev",
+    "fn_attn_noalloc_dev", "fn_dev_status", "fn_model_dims", "fn_gemv_group_dev", "fn_stage_events",
 )
 
 # the shapes fn_model_dims writes, in order (include/faie2fn.h section 6)
@@ -123,6 +123,7 @@ class FN:
         d.fn_advance_dev.argtypes = [VP, i, i, VP]
         d.fn_fill_normal_dev.argtypes = [VP, C.c_size_t, C.c_uint64, C.c_float, C.c_float, VP]
         d.fn_copy_dev.argtypes = [VP, VP, C.c_size_t, VP]
+        d.fn_stage_events.argtypes = [C.POINTER(VP), C.c_int]
         d.fn_path_init.argtypes = [i] * 11
         d.fn_path_buffer.argtypes = [i, i, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]
         d.fn_path_step.argtypes = [i, C.POINTER(C.c_float)]
@@ -363,6 +364,12 @@ class FN:
 
     def copy_dev(self, dst, src, nbytes, stream=0):
         self.check(self.d.fn_copy_dev(dst, src, nbytes, stream))
+
+    def stage_events(self, handles):
+        """Record handles[0], handles[1], ... after each kernel launch of the attention entry points (an empty list
+        clears); handles are hipEvent_t values (hiprt.Event.handle)."""
+        arr = (VP * max(1, len(handles)))(*handles)
+        self.check(self.d.fn_stage_events(arr, len(handles)))
 
     def gemv_packed_bytes(self, qtype, rows, cols):
         return int(self.d.fn_gemv_packed_bytes(int(qtype), rows, cols))

@@ -210,6 +210,13 @@ int fn_advance_dev(int32_t *pos, int B, int nt, void *stream);
 int fn_fill_normal_dev(float *p, size_t n, uint64_t seed, float mean, float std, void *stream);
 int fn_copy_dev(void *dst, const void *src, size_t bytes, void *stream);
 
+/* Per-kernel timing without a profiler (no counterpart in the reference, which times kernels under nsys): with
+ * n > 0 hipEvent_t handles set, the GQA decode and sparse attention entry points (fn_attn_dev, fn_attn_qsa_dev and
+ * the path engine's attention layers) record events[0], events[1], ... on their stream after each of their kernel
+ * launches, in launch order, until the list is used up; n = 0 clears the list.  The events must not be recorded
+ * while a stream is being captured.  0 or -1 (n outside 0..64). */
+int fn_stage_events(void **events, int n);
+
 /* ======================================================================================================
  * 3b. QSA sparse attention (new): the reference's attention layer with its indexer (faie2fn.cu:1480-1607, the
  *     masked k_attn_split :1628-1636, launch order :2396-2402).  Indexer shapes are the reference's: 4 query heads

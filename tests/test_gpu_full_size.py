@@ -1,10 +1,11 @@
 """GPU parity at the benchmark configurations' own workloads (not reduced copies of them), through the device entry
 points and the path engine, against the float64 oracle per tensor per step (normwise <= 1e-5).
 
-* config 1: one fused DeltaNet layer at B = 1 over all 512 decode steps;
+* config 1: one fused DeltaNet layer at B = 1 over all 512 decode steps, with the sigmoid and the SiLU output gate;
 * config 2: the B = 64 layer over all 128 steps, the oracle on three sequences (sequences are independent);
-* config 4: the 48-layer hybrid engine (36 DeltaNet + 12 attention layers) at B = 16 with 32768 keys of context,
-  three decode steps that end exactly at the cache's end, every layer checked every step on sequences 0 and 15.
+* config 4: the 48-layer hybrid engine (36 DeltaNet + 12 attention layers) at B = 16 with 32768 keys of context
+  and at B = 64 with 4096 keys, three decode steps that end exactly at the cache's end, every layer checked every
+  step on the first, a middle and the last sequence.
 
 Config 3's sizes are in test_gpu_attn.py (test_attn_full_size_device).  Every case prints what names it.
 """
@@ -63,7 +64,7 @@ def _ring_taps(ring_seq, p):
     return np.stack([ring_seq[(p - 3 + j) & 3] for j in range(3)])
 
 
-@pytest.mark.parametrize("gate_act", [0])
+@pytest.mark.parametrize("gate_act", [0, 1])
 def test_config1_layer_512_steps(fnlib, gate_act):
     """Config 1's decode length: one layer, B = 1, 512 steps on the device path, out, S and the conv taps against
     the oracle after every step (errors do not accumulate past the bar over the whole run)."""
@@ -125,12 +126,13 @@ def _k_row(K, b, g, p, max_ctx):
     return t[:, p % 64, :].reshape(HD)
 
 
-def test_config4_hybrid_engine_full_context(fnlib):
-    """Config 4 as the engine runs it: 48 layers in the reference's hybrid order, B = 16, 32768 keys of context
-    (caches filled in HBM), 3 decode steps ending at the last row of the cache.  Every layer is checked every step
-    on sequences 0 and 15: DeltaNet out, S and conv taps; attention og and the appended K/V rows."""
-    B, nl, L, steps = 16, 48, 32768, 3
-    pick = [0, 15]
+@pytest.mark.parametrize("B, L, pick", [(16, 32768, [0, 15]), (64, 4096, [0, 31, 63])])
+def test_config4_hybrid_engine_full_context(fnlib, B, L, pick):
+    """Config 4 as the engine runs it: 48 layers in the reference's hybrid order, B = 16 with 32768 keys of context
+    (caches filled in HBM), and the north star's batch of 64 with 4096 keys, 3 decode steps ending at the last row of
+    the cache.  Every layer is checked every step on the picked sequences (first, middle, last): DeltaNet out, S and
+    conv taps; attention og and the appended K/V rows."""
+    nl, steps = 48, 3
     pos0 = L - steps
     _say(f"full size: config 4 engine, B={B}, {nl} layers, context {L}, {steps} steps, oracle on sequences {pick}")
     rng = np.random.default_rng(4004)
