@@ -66,8 +66,9 @@ int quant_pack_launch(const QLayout &L, const uint8_t *raw, uint8_t *packed, hip
 // packed planes -> float rows [rows][cols], bit for bit the GGUF decode of the format
 int quant_dequant_launch(const QLayout &L, const uint8_t *packed, float *out, hipStream_t st);
 // y[t][r] = sum_c W[r][c] x[t][c] for t < nt (1..8); x [nt][cols], y [nt][rows]; work: gemv_work_bytes() bytes
+// ks_force: as gemv_plan's (1: no split-K whatever fn_gemv_override asks, for callers without a work buffer)
 int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, float *y, float *work,
-                size_t work_bytes, hipStream_t st);
+                size_t work_bytes, hipStream_t st, int ks_force = 0);
 
 // the GEMV with ks splits along the row and no reduce pass: part[k][t][r] = sum over split k's groups, k < *ks_out
 // (ks capped so that every split holds a group); the consumer sums the partials in split order.  The split is fixed
@@ -96,6 +97,23 @@ int gemv_group_launch(const GemvPart *parts, int n, const float *x, int nt, hipS
 // GEMV with 16 lanes per row); x and out 16-byte aligned.
 int embed_launch(const QLayout &L, const uint8_t *packed, const int32_t *ids, int nt, int copies, float *out,
                  hipStream_t st);
+
+// The n-gram rows of the per-layer embedding: token t of a call (position p = *pos + t) reads, for each of `heads`
+// hash heads, the table row its n-gram context hashes to, decoded into out[t][head cols + c] (cols = the table's
+// row length).  The hash of head h: key = XOR over k < order of (uint64) c[k] * mult[k], modulo 2^64, where c[0]
+// is the token, c[k] the token k positions back (EOS before the sequence starts and after an EOS), order 2 for the
+// first half of the heads and 3 for the second; row = first[h] + key mod size[h].  The call's ids go into the
+// token ring (the id of position p at p & ring_mask) that later calls read their context from.
+struct NgramGather {
+    const int32_t *ids = nullptr;   // the call's token ids [nt]
+    const int32_t *pos = nullptr;   // position of the call's first token (device)
+    int32_t *ring = nullptr;        // token ring (device), ring_mask + 1 >= nt + 2 entries
+    int ring_mask = 0;
+    const uint64_t *tab = nullptr;  // device: mult[3], then size[heads], then first[heads]
+    int heads = 0, eos = -1;
+};
+int ngram_gather_launch(const QLayout &L, const uint8_t *packed, const NgramGather &g, int nt, float *out,
+                        hipStream_t st);
 int rows_launch(const QLayout &L, const uint8_t *packed, int R, const int32_t *sel, int npairs, int xdiv,
                 const float *x, float *out, hipStream_t st);
 // The routing done inside the expert gate/up kernel (the model forward, one kernel fewer): pair p = t NEU + k

@@ -166,11 +166,11 @@ int quant_dequant_launch(const QLayout &L, const uint8_t *packed, float *out, hi
 }
 
 int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, float *y, float *work,
-                size_t work_bytes, hipStream_t st) {
+                size_t work_bytes, hipStream_t st, int ks_force) {
     if (nt < 1 || nt > MAXNT) FN_FAIL("gemv: nt must be 1..8");
     if (!packed || !x || !y) FN_FAIL("gemv: null pointer");
     if ((uintptr_t) packed % 16 || (uintptr_t) x % 16) FN_FAIL("gemv: weight and x must be 16-byte aligned");
-    const GemvPlan pl = gemv_plan(L);
+    const GemvPlan pl = gemv_plan(L, ks_force);
     float *out = y;
     if (pl.ks > 1) {
         const size_t need = (size_t) pl.ks * nt * L.rows * 4;
@@ -208,6 +208,17 @@ int embed_launch(const QLayout &L, const uint8_t *packed, const int32_t *ids, in
     const QOps *o = ops(L.type);
     if (!o) FN_FAIL("embed: unsupported type");
     return o->embed(L, planes(L, packed), ids, nt, copies, out, st);
+}
+
+int ngram_gather_launch(const QLayout &L, const uint8_t *packed, const NgramGather &g, int nt, float *out,
+                        hipStream_t st) {
+    if (!packed || !out || !g.ids || !g.pos || !g.ring || !g.tab || nt < 1 || g.heads < 2)
+        FN_FAIL("ngram: bad arguments");
+    if (g.ring_mask < nt + 1 || (g.ring_mask & (g.ring_mask + 1))) FN_FAIL("ngram: token ring too short");
+    if ((uintptr_t) out % 16) FN_FAIL("ngram: out must be 16-byte aligned");
+    const QOps *o = ops(L.type);
+    if (!o) FN_FAIL("ngram: unsupported type");
+    return o->ngram(L, planes(L, packed), g, nt, out, st);
 }
 
 int rows_launch(const QLayout &L, const uint8_t *packed, int R, const int32_t *sel, int npairs, int xdiv,

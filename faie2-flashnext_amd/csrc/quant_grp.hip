@@ -52,11 +52,13 @@ int gemv_group_launch(const GemvPart *parts, int n, const float *x, int nt, hipS
         }
         if (ok) kind = k;
     }
-    // x of nt tokens in the LDS beside the codebooks (IQ3_S: its grid and the sign masks, 4 KiB)
-    const size_t xlds = (size_t) (parts[0].L->cols / 32) * xs_stride(nt) * sizeof(float4);
+    // x of MAXNT tokens in the LDS beside the codebooks (IQ3_S: its grid and the sign masks, 4 KiB): sized for the
+    // largest call, so that whether the parts share a launch never depends on nt (token t of an nt-token call keeps
+    // the bits of a one-token call); the separate launches take no split-K, like the grouped one
+    const size_t xlds = (size_t) (parts[0].L->cols / 32) * xs_stride(MAXNT) * sizeof(float4);
     if (kind < 0 || xlds + (size_t) tab_lds<QT_IQ3_S>() > (size_t) kLdsPerCu) {
         for (int i = 0; i < n; ++i)
-            if (gemv_launch(*parts[i].L, parts[i].packed, x, nt, parts[i].y, nullptr, 0, st)) return -1;
+            if (gemv_launch(*parts[i].L, parts[i].packed, x, nt, parts[i].y, nullptr, 0, st, 1)) return -1;
         return 0;
     }
     // lanes per row: the fewest any part's own plan takes, at least 32 (the group is built for 32 and 64)

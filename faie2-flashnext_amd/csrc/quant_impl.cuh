@@ -1146,6 +1146,49 @@ __global__ void __launch_bounds__(256) k_embed(PP P, int G, int cols, const int3
     }
 }
 
+// n-gram rows (NgramGather): workgroup t hashes the context of token t once per thread, then decodes its
+// (head, group) items; the context's earlier positions come from the token ring and this call's own from ids, and
+// thread 0 writes token t's ring slot, which no workgroup of the call reads.  grid nt, 256 threads
+template <uint32_t TY>
+__global__ void __launch_bounds__(256) k_ngram_rows(PP P, int G, int cols, NgramGather ng, float *__restrict__ out) {
+    if constexpr (tab_lds<TY>() > 0) {
+        tab_fill<TY>(threadIdx.x, blockDim.x);
+        __syncthreads();
+    }
+    const int t = blockIdx.x, p0 = *ng.pos, p = p0 + t;
+    long long c[3];
+    c[0] = ng.ids[t];
+    bool open = true;
+#pragma unroll
+    for (int k = 1; k < 3; ++k) {
+        open = open && p - k >= 0;
+        const int q = p - k;
+        c[k] = open ? (q >= p0 ? ng.ids[q - p0] : ng.ring[q & ng.ring_mask]) : ng.eos;
+        open = open && c[k] != ng.eos;
+    }
+    if (threadIdx.x == 0) ng.ring[p & ng.ring_mask] = ng.ids[t];
+    const uint64_t *mult = ng.tab, *size = ng.tab + 3, *first = ng.tab + 3 + ng.heads;
+    for (int i = threadIdx.x; i < ng.heads * G; i += blockDim.x) {
+        const int hd = i / G, g = i - hd * G;
+        uint64_t key = (uint64_t) c[0] * mult[0] ^ (uint64_t) c[1] * mult[1];
+        if (2 * hd >= ng.heads) key ^= (uint64_t) c[2] * mult[2];
+        const int row = (int) (first[hd] + key % size[hd]);
+        Grp o;
+        decode<TY>(P, row, g, o);
+        float4 *dst = reinterpret_cast<float4 *>(out + ((size_t) t * ng.heads + hd) * cols + (size_t) g * 32);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            float e[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float q = o.q[4 * v + k];
+                e[k] = TY == QT_BF16 ? q : __builtin_fmaf(o.s[v >> 2], q, -o.m[v >> 2]);
+            }
+            dst[v] = make_float4(e[0], e[1], e[2], e[3]);
+        }
+    }
+}
+
 // row r of expert sel[p] (R rows per expert) against x[p / xdiv]: 16 lanes per row; lane li sums its groups li,
 // li + 16, ... in order, then the 16 lanes are summed.  Plain rows: 4 rows per wave, 16 per workgroup.
 // SWIGLU: the gate row of Wg and the up row of Wu, out = silu(g) * u; lanes 0-15 of each 32-lane half of a wave
@@ -1237,6 +1280,13 @@ int embed_t(const QLayout &L, const PP &P, const int32_t *ids, int nt, int copie
     return 0;
 }
 
+template <uint32_t TY>
+int ngram_t(const QLayout &L, const PP &P, const NgramGather &g, int nt, float *out, hipStream_t st) {
+    hipLaunchKernelGGL(k_ngram_rows<TY>, dim3((unsigned) nt), dim3(256), 0, st, P, L.cols / 32, L.cols, g, out);
+    FN_CK(hipGetLastError());
+    return 0;
+}
+
 template <uint32_t TY, bool SW>
 int rows_t(const QLayout &L, const PP &Pg, const PP &Pu, int R, const int32_t *sel, int npairs, int xdiv,
            const float *x, float *out, hipStream_t st, const RouteIn &rt) {
@@ -1255,6 +1305,7 @@ struct QOps {
     int (*gemv)(const QLayout &, const GemvPlan &, const PP &, const float *, int, float *, hipStream_t);
     int (*dequant)(const QLayout &, const PP &, float *, hipStream_t);
     int (*embed)(const QLayout &, const PP &, const int32_t *, int, int, float *, hipStream_t);
+    int (*ngram)(const QLayout &, const PP &, const NgramGather &, int, float *, hipStream_t);
     int (*rows)(const QLayout &, const PP &, const PP &, int, const int32_t *, int, int, const float *, float *,
                 hipStream_t, const RouteIn &);
     int (*swiglu)(const QLayout &, const PP &, const PP &, int, const int32_t *, int, int, const float *, float *,
@@ -1270,7 +1321,8 @@ template <uint32_t TY> int dequant_t(const QLayout &L, const PP &P, float *out, 
 }
 
 template <uint32_t TY> const QOps *qops_of() {
-    static const QOps o{&gemv_t<TY>, &dequant_t<TY>, &embed_t<TY>, &rows_t<TY, false>, &rows_t<TY, true>};
+    static const QOps o{&gemv_t<TY>, &dequant_t<TY>, &embed_t<TY>, &ngram_t<TY>, &rows_t<TY, false>,
+                        &rows_t<TY, true>};
     return &o;
 }
 

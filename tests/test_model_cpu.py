@@ -123,6 +123,32 @@ def test_load_before_device_checks_the_file(fnlib, tmp_path):
         fnlib.forward([1, 2])
 
 
+def test_load_plans_every_tensor_before_the_device(fnlib, tmp_path):
+    """fn_load walks its tensor table over the file before it touches the device: a missing tensor, a tensor of
+    another shape and an n-gram table shorter than its heads address fail with a message naming the tensor (here,
+    without a GPU), and leave no model loaded."""
+    kv, ts = ms.model_tensors(ms.TINY_DIMS, seed=3)
+    T = ms.TINY_DIMS
+    p = str(tmp_path / "bad.gguf")
+    ms.write_gguf(p, kv, [t for t in ts if t[0] != "blk.2.ssm_out.weight"])
+    with pytest.raises(RuntimeError, match=r"blk\.2\.ssm_out\.weight missing"):
+        fnlib.load(p, "", max_ctx=256)
+    # one row fewer in a BF16 weight (rows of D values, 2 bytes each)
+    row = T["D"] * 2
+    ts2 = [t if t[0] != "blk.1.ssm_alpha.weight" else (t[0], t[1], [T["D"], T["NVH"] - 1], t[3][: (T["NVH"] - 1) * row])
+           for t in ts]
+    ms.write_gguf(p, kv, ts2)
+    with pytest.raises(RuntimeError, match=r"blk\.1\.ssm_alpha\.weight has shape \[256, 3, 1\], expected 256 columns x 4"):
+        fnlib.load(p, "", max_ctx=256)
+    short = sum(T["ple_sizes"]) - 1
+    ts3 = [t if t[0] != "per_layer_token_embd.weight" else
+           (t[0], t[1], [T["ple_hd"], short], t[3][: short * T["ple_hd"] // 32 * 18]) for t in ts]
+    ms.write_gguf(p, kv, ts3)
+    with pytest.raises(RuntimeError, match="n-gram heads reach"):
+        fnlib.load(p, "", max_ctx=256)
+    assert fnlib.d.fn_n_past() == -1
+
+
 # ---- oracle pins ----
 
 
