@@ -78,13 +78,19 @@ FN_API int fn_gemv_plan(uint32_t type, int rows, int cols, int *out) {
     if (!fn::qlayout(type, rows, cols, L)) return -1;
     if (!out) FN_FAIL("gemv_plan: null pointer");
     const fn::GemvPlan p = fn::gemv_plan(L);
-    const int v[7] = {p.gv, p.waves, p.ks, p.rpw, p.lpr, p.grid, p.ngroups};
+    // the reference's slots {cv, wpt, ks, tb, nbuf, ntiles, nch}: wpt is the split of a row's columns, here the
+    // 16-lane groups that sum a row (lanes per row / 16); tb and nbuf hold this plan's rows per workgroup pass and
+    // waves per workgroup
+    const int v[7] = {p.gv, p.lpr / 16, p.ks, p.rpw, p.waves, p.grid, p.ngroups};
     std::copy(v, v + 7, out);
     return 0;
 }
 
-// the reference's knobs: waves per SM and tile shape belong to its CUDA tiling; split-K is the one that applies
-FN_API void fn_gemv_override(int wpt, int ks, int tb, int warps_per_sm) { fn::gemv_override(wpt, ks, tb, warps_per_sm); }
+// wpt: 16-lane groups per row (1, 2 or 4; anything else: automatic), as fn_gemv_plan reports it; ks: split-K;
+// tb: this library's kernel choice; warps_per_sm: resident waves per CU a persistent grid is sized for
+FN_API void fn_gemv_override(int wpt, int ks, int tb, int warps_per_sm) {
+    fn::gemv_override(wpt == 1 || wpt == 2 || wpt == 4 ? 16 * wpt : 0, ks, tb, warps_per_sm);
+}
 FN_API void fn_gemv_waves(int waves) { fn::gemv_persistent(waves); }
 FN_API void fn_bench_hot(int on) { g_bench_hot = on; }
 

@@ -197,8 +197,8 @@ class FN:
         return y
 
     def gemv_plan(self, qtype, rows, cols):
-        """{values per group, waves per workgroup, split-K, rows per workgroup, groups in flight, row tiles,
-        groups per row} of a weight."""
+        """{values per group, 16-lane groups per row (wpt), split-K, rows per workgroup pass, waves per workgroup,
+        workgroups along the rows (0: persistent), groups per row} of a weight."""
         out = np.zeros(7, np.int32)
         self.check(self.d.fn_gemv_plan(int(qtype), rows, cols, out))
         return [int(v) for v in out]
@@ -223,9 +223,11 @@ class FN:
         return sel, w, float(ms[0])
 
     def gemv_override(self, ks=0, lpr=0, kernel=0, waves_per_cu=0):
-        """Force the GEMV plan (0 = automatic): split-K, lanes per row, kernel (1 x in chunks, 2 x staged once, 3 / 4
-        x staged once with the deep / short walk) and the resident waves per CU the persistent grid is sized for."""
-        self.d.fn_gemv_override(int(lpr), int(ks), int(kernel), int(waves_per_cu))
+        """Force the GEMV plan (0 = automatic): split-K, lanes per row (16, 32, 64; passed as the reference's wpt,
+        16-lane groups per row), kernel (1 x in chunks, 2 x staged once, 3 / 4 x staged once with the deep / short
+        walk) and the resident waves per CU the persistent grid is sized for."""
+        wpt = int(lpr) // 16 if int(lpr) in (16, 32, 64) else (5 if lpr else 0)  # 5: an invalid split (ignored)
+        self.d.fn_gemv_override(wpt, int(ks), int(kernel), int(waves_per_cu))
 
     def bench_hot(self, on):
         self.d.fn_bench_hot(1 if on else 0)

@@ -46,10 +46,14 @@ int fn_forward(const int32_t *tokens, int nt, float *logits, int32_t *argmax);  
 int fn_debug_layers(float *out);                                              /* faie2fn.cu:2739 */
 /* GGUF rows W (rows x cols of `type`, the file's bytes) -> out [rows][cols] float32, bit for bit ggml's decode. */
 int fn_test_dequant(uint32_t type, const uint8_t *W, int rows, int cols, float *out);  /* faie2fn.cu:2751 */
-/* Force the plan of GEMVs launched from now on, 0 = automatic (the reference's arguments, this library's meaning):
- * wpt = lanes per row (16, 32 or 64), ks = split-K workgroups per row, tb = kernel (1 x staged in chunks, 2 x
- * staged once, 3 / 4 x staged once with the deep / short walk), warps_per_sm = resident waves per CU that a
- * persistent grid is sized for.  Every choice gives the same bits except ks > 1. */
+/* Force the plan of GEMVs launched from now on, 0 = automatic.  wpt: the reference's split of a row's columns
+ * (its warps per 16-row tile); here the 16-lane groups that sum one row, 1, 2 or 4 (16, 32 or 64 lanes per row;
+ * other values: automatic), the quantity fn_gemv_plan reports in out[1], so a forced plan reads back as forced.
+ * ks: split-K workgroups per row, as the reference's (out[2]).  tb: not the reference's tiles per block (the
+ * workgroups here are fixed at 8 waves) but this library's kernel choice (1 x staged in chunks, 2 x staged once,
+ * 3 / 4 x staged once with the deep / short walk).  warps_per_sm: the resident waves per CU a persistent grid is
+ * sized for (the reference's target warps per SM).  Lanes per row and ks > 1 change the summation order, the other
+ * choices give the same bits.  The model forward's GEMVs take no split-K whatever ks asks (no work buffer). */
 void fn_gemv_override(int wpt, int ks, int tb, int warps_per_sm);             /* faie2fn.cu:2786 */
 /* The reference's persistent-grid switch: waves != 0 (default) launches the GEMV on the workgroups resident at once,
  * each walking many row tiles; 0 launches one workgroup per row tile.  Same bits either way; fn_gemv_plan's out[5]
@@ -62,11 +66,11 @@ void fn_pdl(int on);                                                          /*
 void fn_early(int on);                                                        /* faie2fn.cu:2798 */
 void fn_moe_var(int v);                                                       /* faie2fn.cu:2799 */
 void fn_moe_override(int gu_wpt, int gu_tb, int dn_wpt, int dn_tb);           /* faie2fn.cu:2801 */
-/* Launch plan of a rows x cols weight: out[7] = {values per group (32), waves per workgroup, split-K workgroups
- * per row, rows per workgroup pass, lanes per row, workgroups along the rows (0 = persistent grid: the workgroups
- * resident at once, sized at launch; after fn_gemv_waves(0) one per row tile of rows-per-pass rows), groups per
- * row}.  Same 7-int shape as the reference's {cv, wpt, ks, tb, nbuf, ntiles, nch}, this library's plan in it; like
- * the reference's it depends on the shape only, never on the number of tokens. */
+/* Launch plan of a rows x cols weight in the reference's 7 slots {cv, wpt, ks, tb, nbuf, ntiles, nch}:
+ * out = {values per group (32), 16-lane groups per row (wpt, as fn_gemv_override takes it), split-K workgroups per
+ * row, rows per workgroup pass, waves per workgroup (8), workgroups along the rows (0 = persistent grid: the
+ * workgroups resident at once, sized at launch; after fn_gemv_waves(0) one per row tile of rows-per-pass rows),
+ * groups per row}.  Like the reference's it depends on the shape only, never on the number of tokens. */
 int fn_gemv_plan(uint32_t type, int rows, int cols, int *out);                /* faie2fn.cu:2809 */
 void fn_bench_hot(int on);                                                    /* faie2fn.cu:2822 */
 /* ms per GEMV call of nt tokens (1..8) on random bytes of the format, iters calls replayed as one hipGraph, each

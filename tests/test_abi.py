@@ -122,7 +122,8 @@ def test_gemv_plan_shapes(fnlib):
     """Plans of the projection shapes around the path (the benchmark configs' hidden 2048 and the reference model's 2560)."""
     for qtype, rows, cols in [(23, 10240, 2560), (8, 2560, 6144), (30, 96, 2560), (14, 512, 2560), (23, 8192, 2048),
                               (21, 6144, 2560)]:
-        gv, waves, ks, rpw, lpr, grid, ngroups = fnlib.gemv_plan(qtype, rows, cols)
+        gv, wpt, ks, rpw, waves, grid, ngroups = fnlib.gemv_plan(qtype, rows, cols)
+        lpr = 16 * wpt
         assert (gv, waves) == (32, 8) and lpr in (16, 32, 64) and rpw == 8 * 64 // lpr
         assert grid == 0 and ngroups == cols // 32  # persistent grid by default
         assert 1 <= ks <= ngroups
@@ -137,11 +138,39 @@ def test_gemv_plan_shapes(fnlib):
     auto = fnlib.gemv_plan(8, 2560, 6144)
     fnlib.gemv_override(lpr=16)                                  # forced lanes per row; an invalid value is ignored
     try:
-        assert fnlib.gemv_plan(23, 10240, 2560)[1::3] == [8, 16]
+        assert fnlib.gemv_plan(23, 10240, 2560)[1::3] == [1, 8]
         fnlib.gemv_override(lpr=48)
         assert fnlib.gemv_plan(8, 2560, 6144) == auto
     finally:
         fnlib.gemv_override(0)
+
+
+def test_forced_gemv_plan_reads_back(fnlib):
+    """flashnext/sweep_gemv_fn.py's forced loop: fn_gemv_override(wpt, ks, 0, 16) then fn_gemv_plan, keeping the
+    plans whose out[1] == wpt and out[2] == ks.  Every wpt this library builds (1, 2, 4 sixteen-lane groups per row)
+    and every ks reads back as forced; wpt 8 and 16 (no such split here) read back as the automatic choice, so the
+    script's filter skips them instead of mislabelling them."""
+    d = fnlib.d
+    auto = fnlib.gemv_plan(23, 10240, 2560)
+    saved = d.fn_gemv_override.argtypes, d.fn_gemv_plan.argtypes
+    d.fn_gemv_override.argtypes = [C.c_int] * 4       # as the sweep binds them
+    d.fn_gemv_plan.argtypes = [C.c_uint32, C.c_int, C.c_int, C.POINTER(C.c_int)]
+    kept = []
+    try:
+        for wpt in (1, 2, 4, 8, 16):
+            for ks in (1, 2, 4, 8, 16):
+                d.fn_gemv_override(wpt, ks, 0, 16)
+                plan = (C.c_int * 7)()
+                assert d.fn_gemv_plan(23, 10240, 2560, plan) == 0
+                if plan[1] == wpt and plan[2] == ks:
+                    kept.append((wpt, ks))
+                else:
+                    assert wpt in (8, 16) and plan[1] == auto[1] and plan[2] == ks
+    finally:
+        d.fn_gemv_override(0, 0, 0, 0)
+        d.fn_gemv_override.argtypes, d.fn_gemv_plan.argtypes = saved
+    assert kept == [(w, k) for w in (1, 2, 4) for k in (1, 2, 4, 8, 16)]
+    assert fnlib.gemv_plan(23, 10240, 2560) == auto
 
 
 def test_gemv_waves_switches_the_grid(fnlib):

@@ -283,7 +283,7 @@ def test_gemv_group(fnlib, name, parts, cols, nt):
     raws = [random_finite(t, r, cols, RNG) for t, r in zip(types, rows)]
     x = RNG.standard_normal((nt, cols)).astype(np.float32)
     ys = _group_run(fnlib, types, rows, raws, cols, x)
-    lprs = [fnlib.gemv_plan(t, r, cols)[4] for t, r in zip(types, rows)]
+    lprs = [16 * fnlib.gemv_plan(t, r, cols)[1] for t, r in zip(types, rows)]
     glpr = min(max(32, v) for v in lprs)
     for t, r, raw, y, lpr in zip(types, rows, raws, ys, lprs):
         assert oracle.relerr(y, oracle.gemv(t, raw, r, cols, x)) <= TOL, (t, r)
@@ -304,4 +304,22 @@ def test_gemv_group_tokens_independent(fnlib):
         one = _group_run(fnlib, types, rows, raws, cols, x[i:i + 1])
         for y, y1 in zip(ys, one):
             assert np.array_equal(y[i], y1[0])
+
+
+def test_gemv_group_path_independent_of_nt(fnlib):
+    """At 5120 columns the x of 8 tokens does not fit the LDS beside the codebooks while the x of one token does;
+    the path (grouped or one launch per weight) is chosen for the largest call, so a one-token call takes the same
+    path as an 8-token one: every weight keeps its own GEMV's bits at nt 1 and 8, and token t of the 8-token call
+    equals the one-token call on x[t]."""
+    types = [TYPES["IQ4_XS"], TYPES["IQ3_S"], TYPES["BF16"]]
+    rows, cols = [512, 256, 64], 5120
+    _say(f"gemv group at cols={cols}: nt=8 vs nt=1, own-GEMV bits")
+    raws = [random_finite(t, r, cols, RNG) for t, r in zip(types, rows)]
+    x = RNG.standard_normal((8, cols)).astype(np.float32)
+    ys = _group_run(fnlib, types, rows, raws, cols, x)
+    for i in (0, 5):
+        one = _group_run(fnlib, types, rows, raws, cols, x[i:i + 1])
+        for t, r, raw, y, y1 in zip(types, rows, raws, ys, one):
+            assert np.array_equal(y[i], y1[0]), (t, i)
+            assert np.array_equal(y1, fnlib.gemv(t, raw, r, cols, x[i:i + 1])), (t, i)
 

@@ -122,6 +122,55 @@ def test_model_errors(fnlib, model_file):
     assert fnlib.d.fn_n_past() == -1
 
 
+def _stale_status_bit(fnlib):
+    """Leave FN_STATUS_POS in the device's status word: a GQA decode call whose new token lies past its cache."""
+    import hiprt
+
+    B, nq, nkv, hd, max_ctx = 1, 16, 2, 256, 64
+    rng = np.random.default_rng(1)
+    bufs = [hiprt.Buf.like(rng.standard_normal(n).astype(np.float32)) for n in
+            (B * nkv * max_ctx * hd, B * nkv * max_ctx * hd, B * nq * 2 * hd, B * nkv * hd, B * nkv * hd, hd, hd)]
+    K, V, qg, k, v, wq, wk = bufs
+    pos = hiprt.Buf.like(np.array([max_ctx], np.int32))
+    nsplit = fnlib.attn_nsplit(B, nkv, 1, max_ctx)
+    wb = fnlib.attn_work_bytes(B, nq, 1, nsplit)
+    work, og = hiprt.Buf(wb), hiprt.Buf.empty((B, 1, nq, hd))
+    fnlib.attn_dev(B, nq, nkv, 1, max_ctx, pos.ptr, qg.ptr, k.ptr, v.ptr, wq.ptr, wk.ptr, K.ptr, V.ptr, nsplit,
+                   work.ptr, wb, og.ptr, None)
+    hiprt.sync()
+    for b in (*bufs, pos, work, og):
+        b.free()
+
+
+def test_model_forward_after_split_override_and_stale_status(fnlib, model_file):
+    """The forward holds no work buffer for a split-K GEMV: after fn_gemv_override asks for 3 splits its GEMVs keep
+    their own plan (same bits as without the override).  A status bit another entry point left behind is not the
+    forward's: the call clears it first and succeeds."""
+    import fn
+
+    path, kv, ts = model_file
+    ids = np.random.default_rng(6).integers(0, ms.TINY_DIMS["VOCAB"], size=12)
+    _say("model forward: after fn_gemv_override(ks=3) and with a stale FN_STATUS_POS bit")
+    fnlib.load(path, "", max_ctx=256)
+    try:
+        base = np.concatenate([fnlib.forward(ids[k:k + 4], logits=True)[1] for k in range(0, 12, 4)])
+        fnlib.reset()
+        fnlib.gemv_override(ks=3)
+        try:
+            over = np.concatenate([fnlib.forward(ids[k:k + 4], logits=True)[1] for k in range(0, 12, 4)])
+        finally:
+            fnlib.gemv_override()
+        assert np.array_equal(base, over)
+        fnlib.reset()
+        _stale_status_bit(fnlib)
+        assert fnlib.dev_status(clear=False) & fn.STATUS_POS
+        again = np.concatenate([fnlib.forward(ids[k:k + 4], logits=True)[1] for k in range(0, 12, 4)])
+        assert np.array_equal(base, again)
+        assert fnlib.dev_status() == 0
+    finally:
+        fnlib.free()
+
+
 def test_model_two_shards_equal_one_file(fnlib, model_file, tmp_path):
     """The n-gram table in a second file (the reference model's layout) gives the same bits as one file."""
     path, kv, ts = model_file
