@@ -38,6 +38,7 @@ SYMBOLS = (
     "fn_gemv_packed_bytes", "fn_gemv_pack_dev", "fn_dequant_dev", "fn_gemv_work_bytes", "fn_gemv_dev",
     "fn_gdn_verify_dev", "fn_advance_by_dev", "fn_gdn_block_xab_dev",
     "fn_attn_noalloc_dev", "fn_dev_status", "fn_model_dims", "fn_gemv_group_dev", "fn_stage_events",
+    "fn_bench_gdn", "fn_bench_attn",
 )
 
 # the shapes fn_model_dims writes, in order (include/faie2fn.h section 6)
@@ -124,6 +125,8 @@ class FN:
         d.fn_fill_normal_dev.argtypes = [VP, C.c_size_t, C.c_uint64, C.c_float, C.c_float, VP]
         d.fn_copy_dev.argtypes = [VP, VP, C.c_size_t, VP]
         d.fn_stage_events.argtypes = [C.POINTER(VP), C.c_int]
+        d.fn_bench_gdn.argtypes = [C.c_int] * 5 + [C.POINTER(C.c_float)]
+        d.fn_bench_attn.argtypes = [C.c_int] * 6 + [C.POINTER(C.c_float)]
         d.fn_path_init.argtypes = [i] * 11
         d.fn_path_buffer.argtypes = [i, i, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]
         d.fn_path_step.argtypes = [i, C.POINTER(C.c_float)]
@@ -366,6 +369,18 @@ class FN:
 
     def copy_dev(self, dst, src, nbytes, stream=0):
         self.check(self.d.fn_copy_dev(dst, src, nbytes, stream))
+
+    def bench_gdn(self, B, nkh=16, nvh=32, nt=1, iters=20):
+        """µs per layer-step of the fused DeltaNet block, cold state, graph-replayed (fn_bench_gdn)."""
+        us = C.c_float(0.0)
+        self.check(self.d.fn_bench_gdn(B, nkh, nvh, nt, iters, C.byref(us)))
+        return us.value
+
+    def bench_attn(self, B, ctx, nq=16, nkv=2, nt=1, iters=20):
+        """µs per layer-step of GQA decode at context ctx, cold caches, graph-replayed (fn_bench_attn)."""
+        us = C.c_float(0.0)
+        self.check(self.d.fn_bench_attn(B, nq, nkv, ctx, nt, iters, C.byref(us)))
+        return us.value
 
     def stage_events(self, handles):
         """Record handles[0], handles[1], ... after each kernel launch of the attention entry points (an empty list

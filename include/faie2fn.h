@@ -214,6 +214,16 @@ int fn_advance_dev(int32_t *pos, int B, int nt, void *stream);
 int fn_fill_normal_dev(float *p, size_t n, uint64_t seed, float mean, float std, void *stream);
 int fn_copy_dev(void *dst, const void *src, size_t bytes, void *stream);
 
+/* Timing hooks of the path (SURVEY's path hooks; the reference's style of fn_bench_gemv, faie2fn.cu:2823): inputs
+ * filled in HBM (seeded normal values), enough distinct layers that state or caches are cold (>= 1 GiB), one pass
+ * over the layers captured as a hipGraph, `iters` replays timed with HIP events; *us = microseconds per layer-step.
+ *   fn_bench_gdn: the fused DeltaNet block (dk = dv = 128, conv k = 4) of B sequences, nt tokens each;
+ *   fn_bench_attn: GQA decode (head dim 256, RoPE on 64 dims) of B sequences with nt new tokens at positions
+ *   ctx - nt .. ctx - 1 (query heads per kv head 4, 8 or 12).
+ * Shapes are checked before any device work. */
+int fn_bench_gdn(int B, int nkh, int nvh, int nt, int iters, float *us);
+int fn_bench_attn(int B, int nq, int nkv, int ctx, int nt, int iters, float *us);
+
 /* Per-kernel timing without a profiler (no counterpart in the reference, which times kernels under nsys): with
  * n > 0 hipEvent_t handles set, the GQA decode and sparse attention entry points (fn_attn_dev, fn_attn_qsa_dev and
  * the path engine's attention layers) record events[0], events[1], ... on their stream after each of their kernel

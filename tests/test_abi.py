@@ -284,3 +284,17 @@ def test_bench_route_refuses_bad_arguments(fnlib):
     assert b"null pointer" in d.fn_error()
     with pytest.raises(ValueError):
         fnlib.bench_route(0, np.zeros((1, 8, 500), np.float32), 1)
+
+
+def test_bench_hooks_check_shapes_before_the_device(fnlib):
+    """fn_bench_gdn / fn_bench_attn reject shapes they cannot time before touching a device (these run without a
+    GPU)."""
+    for args, msg in (((0, 16, 32, 1, 20), "B >= 1"), ((1, 16, 30, 1, 20), "multiple of nkh"),
+                      ((1, 16, 32, 9, 20), "nt 1..8"), ((1, 16, 32, 1, 0), "iters")):
+        with pytest.raises(RuntimeError, match=msg):
+            fnlib.bench_gdn(*args[:1], nkh=args[1], nvh=args[2], nt=args[3], iters=args[4])
+    with pytest.raises(RuntimeError, match="4, 8 or 12"):
+        fnlib.bench_attn(1, 4096, nq=16, nkv=8)
+    with pytest.raises(RuntimeError, match="ctx >= nt"):
+        fnlib.bench_attn(1, 2, nt=4)
+
