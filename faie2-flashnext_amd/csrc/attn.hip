@@ -889,7 +889,8 @@ int attn_decode_launch(const AttnDecode &p, hipStream_t st) {
     a.B = p.B; a.nq = p.nq; a.nkv = p.nkv; a.nt = p.nt; a.max_ctx = p.max_ctx; a.nsplit = p.nsplit;
     a.nrot = p.nrot; a.eps = p.eps; a.pos = p.pos; a.qg = p.qg; a.knew = p.k; a.vnew = p.v; a.wq = p.wq;
     a.wk = p.wk; a.Kc = p.Kc; a.Vc = p.Vc; a.og = p.og;
-    if (status_word(&a.status)) return -1;
+    if (p.status) a.status = p.status;
+    else if (status_word(&a.status)) return -1;
     const size_t bt = (size_t) p.B * p.nt;
     a.Q = p.work;
     a.part_o = a.Q + bt * p.nq * HD;
@@ -959,7 +960,8 @@ int attn_qsa_launch(const AttnDecode &p, const QsaIndexer &ix, hipStream_t st) {
     a.nrot = p.nrot; a.eps = p.eps; a.pos = p.pos; a.qg = p.qg; a.knew = p.k; a.vnew = p.v; a.wq = p.wq;
     a.wk = p.wk; a.Kc = p.Kc; a.Vc = p.Vc; a.og = p.og;
     a.keys = keys; a.nkeys = nkeys; a.kstride = ix.top * 4 + 4;
-    if (status_word(&a.status)) return -1;
+    if (p.status) a.status = p.status;
+    else if (status_word(&a.status)) return -1;
     const size_t bt = (size_t) p.B * p.nt;
     a.Q = p.work;
     a.part_o = a.Q + bt * p.nq * HD;

@@ -62,6 +62,7 @@ struct AttnDecode {
     float *work;                        // attn_work_bytes()
     size_t work_bytes;
     float *og;                          // [B][nt][nq][hd]
+    unsigned *status = nullptr;         // where kernels record misuse (FN_STATUS_*); null: the device's status word
 };
 
 size_t attn_work_bytes(int B, int nq, int nt, int hd, int nsplit);

@@ -397,9 +397,10 @@ int mixer(Model &m, const Layer &L, int nt) {
     const GemvPart g[4] = {{&qg.L, qg.p, a.qg}, {&k.L, k.p, a.kk}, {&v.L, v.p, a.vv}, {&ix.L, ix.p, a.iqk}};
     if (gemv_group_launch(g, 4, a.x, nt, m.st)) return -1;
     AttnDecode p{1, d.NH, d.NKV, HDK, d.NROT, nt, m.max_ctx, m.nsplit, d.theta, d.eps, a.pos, a.qg, a.kk, a.vv,
-                 L.f(AT_QNORM), L.f(AT_KNORM), L.f(AT_KCACHE), L.f(AT_VCACHE), a.work, m.work_bytes, a.og};
+                 L.f(AT_QNORM), L.f(AT_KNORM), L.f(AT_KCACHE), L.f(AT_VCACHE), a.work, m.work_bytes, a.og,
+                 a.status};
     QsaIndexer qix{1, nt, m.max_ctx, d.top, d.NROT, d.theta, d.eps, a.pos, a.iqk, L.f(AT_IXQNORM), L.f(AT_IXKNORM),
-                   L.f(AT_IXKEYS), L.f(AT_IXBLOCKS)};
+                   L.f(AT_IXKEYS), L.f(AT_IXBLOCKS), a.status};
     if (attn_qsa_launch(p, qix, m.st)) return -1;
     return gemv(L.q(AT_O), a.og, nt, a.y, m.st);
 }
@@ -592,12 +593,8 @@ int model_load(const char *shard1, const char *shard2, int max_ctx) {
     path_free();
     FN_CK(hipSetDevice(0));
     FN_CK(hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking));
-    // the status word's address, looked up now rather than under a graph capture
-    if (status_word(&m->status)) return -1;
-    FN_CK(hipHostMalloc(&m->host, 2 * MAXT * sizeof(int32_t) + 64, hipHostMallocDefault));
-    m->h_ids = static_cast<int32_t *>(m->host);
-    m->h_am = m->h_ids + MAXT;
-    m->h_status = reinterpret_cast<unsigned *>(m->h_am + MAXT);
+    FN_CK(hipHostMalloc(&m->host, IO_WORDS * sizeof(int32_t), hipHostMallocDefault));
+    m->h_io = static_cast<int32_t *>(m->host);
     if (commit_weights(*m)) return -1;
     g_model = std::move(m);
     return 0;
@@ -613,11 +610,10 @@ int model_forward(const int32_t *tokens, int nt, float *logits, int32_t *argmax)
     for (int t = 0; t < nt; ++t)
         if (tokens[t] < 0 || tokens[t] >= m.d.VOCAB) FN_FAIL("forward: token id outside the vocabulary");
     const auto t0 = std::chrono::steady_clock::now();
-    std::memcpy(m.h_ids, tokens, (size_t) nt * 4);
-    // bits another entry point left in the status word are not this call's: cleared on the stream first
-    *m.h_status = 0;
-    FN_CK(hipMemcpyAsync(m.status, m.h_status, sizeof(unsigned), hipMemcpyHostToDevice, m.st));
-    FN_CK(hipMemcpyAsync(m.a.ids, m.h_ids, (size_t) nt * 4, hipMemcpyHostToDevice, m.st));
+    // the call's ids and a cleared status word in, one copy; the status word and the argmax ids out, one copy
+    std::memcpy(m.h_io, tokens, (size_t) nt * 4);
+    m.h_io[MAXT] = 0;
+    FN_CK(hipMemcpyAsync(m.a.io, m.h_io, (MAXT + 1) * sizeof(int32_t), hipMemcpyHostToDevice, m.st));
     const bool graphs = m.use_graphs && !m.dbg;
     if (graphs) {
         if (!m.graph[nt] && capture(m, nt)) return -1;
@@ -627,18 +623,15 @@ int model_forward(const int32_t *tokens, int nt, float *logits, int32_t *argmax)
     }
     if (logits)
         FN_CK(hipMemcpyAsync(logits, m.a.logits, (size_t) nt * m.d.VOCAB * 4, hipMemcpyDeviceToHost, m.st));
-    FN_CK(hipMemcpyAsync(m.h_am, m.a.am, (size_t) nt * 4, hipMemcpyDeviceToHost, m.st));
-    FN_CK(hipMemcpyAsync(m.h_status, m.status, sizeof(unsigned), hipMemcpyDeviceToHost, m.st));
+    FN_CK(hipMemcpyAsync(m.h_io + MAXT, m.a.io + MAXT, (size_t) (nt + 1) * 4, hipMemcpyDeviceToHost, m.st));
     FN_CK(hipStreamSynchronize(m.st));
-    if (const unsigned bits = *m.h_status) {
+    if (const unsigned bits = (unsigned) m.h_io[MAXT]) {
         // the device advanced its position and wrote state for tokens the host does not count: refuse further
         // calls until fn_reset
         m.failed = true;
-        unsigned cleared = 0;
-        if (status_read(&cleared, true)) return -1;
         FN_FAIL("forward: a kernel recorded misuse (status bits " + std::to_string(bits) + "); fn_reset to continue");
     }
-    if (argmax) std::memcpy(argmax, m.h_am, (size_t) nt * 4);
+    if (argmax) std::memcpy(argmax, m.h_io + MAXT + 1, (size_t) nt * 4);
     m.n_past += nt;
     m.last_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     return 0;

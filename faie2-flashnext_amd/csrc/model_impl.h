@@ -89,11 +89,16 @@ struct Acts {
     float *sha = nullptr, *shd = nullptr, *act = nullptr, *dpart = nullptr, *wsel = nullptr, *logits = nullptr;
     float *amv = nullptr, *work = nullptr;
     float *ng_emb = nullptr, *ng_key = nullptr, *ng_val = nullptr;
-    int32_t *ids = nullptr, *sel = nullptr, *pos = nullptr, *am = nullptr, *ami = nullptr, *ng_tok = nullptr;
+    int32_t *sel = nullptr, *pos = nullptr, *ami = nullptr, *ng_tok = nullptr;
     uint64_t *ng_tab = nullptr;  // n-gram hash: multipliers [3], then per head its table size, then its first row
+    // one call's exchange with the host, one block so that a call needs one copy in and one out:
+    // io = [MAXT token ids][status word][MAXT argmax ids]
+    int32_t *io = nullptr, *ids = nullptr, *am = nullptr;
+    unsigned *status = nullptr;  // the model's own misuse word (FN_STATUS_* bits of its attention kernels)
 };
 
 constexpr int AM_CH = 128;  // chunks of the two-pass argmax
+constexpr int IO_WORDS = 2 * MAXT + 1;  // Acts::io
 constexpr int HC_KS = 4;    // split of the hyper-connection down product along its rows (several-token calls)
 
 struct Model {
@@ -106,10 +111,8 @@ struct Model {
     hipStream_t st = nullptr;
     // the residual streams of the current stage and the other buffer of the pair a fused write moves them to
     float *h = nullptr, *h2 = nullptr;
-    // pinned host staging of one call's token ids, argmax ids and the status word (an asynchronous copy from or to
-    // pageable memory is a blocking one), and the status word's device address
-    int32_t *h_ids = nullptr, *h_am = nullptr;
-    unsigned *h_status = nullptr, *status = nullptr;
+    // pinned host staging of Acts::io (an asynchronous copy from or to pageable memory is a blocking one)
+    int32_t *h_io = nullptr;
     void *host = nullptr;
     hipGraphExec_t graph[MAXT + 1] = {};
     bool use_graphs = true;

@@ -322,8 +322,8 @@ int carve_acts(Model &m) {
         {(void **) &a.shg, T * d.FFS * F}, {(void **) &a.shu, T * d.FFS * F}, {(void **) &a.sha, T * d.FFS * F},
         {(void **) &a.shd, T * d.D * F}, {(void **) &a.act, T * d.NEU * d.FFE * F},
         {(void **) &a.dpart, T * d.NEU * d.D * F}, {(void **) &a.wsel, T * d.NEU * F},
-        {(void **) &a.logits, T * d.VOCAB * F}, {(void **) &a.work, m.work_bytes}, {(void **) &a.ids, T * 4},
-        {(void **) &a.sel, T * d.NEU * 4}, {(void **) &a.pos, 4}, {(void **) &a.am, T * 4},
+        {(void **) &a.logits, T * d.VOCAB * F}, {(void **) &a.work, m.work_bytes}, {(void **) &a.io, IO_WORDS * 4},
+        {(void **) &a.sel, T * d.NEU * 4}, {(void **) &a.pos, 4},
     };
     if (d.ple_layers) {
         cuts.push_back({(void **) &a.ng_emb, T * d.D * F});
@@ -346,6 +346,9 @@ int carve_acts(Model &m) {
         *c.p = base + off;
         off += (std::max<size_t>(c.bytes, 16) + 255) / 256 * 256;
     }
+    a.ids = a.io;
+    a.status = reinterpret_cast<unsigned *>(a.io + MAXT);
+    a.am = a.io + MAXT + 1;
     return 0;
 }
 

@@ -13,6 +13,7 @@ struct QsaIndexer {
     const float *wqn, *wkn; // [128]
     float *IKc;             // [B][max_ctx][128] raw index keys
     float *BKc;             // [B][max_ctx / 4 / 64][32][64][4] block keys
+    unsigned *status = nullptr;  // where kernels record misuse (FN_STATUS_*); null: the device's status word
 };
 
 size_t qsa_work_bytes(int B, int nt, int max_ctx, int top);

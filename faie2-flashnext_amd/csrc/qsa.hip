@@ -355,7 +355,8 @@ int qsa_select_launch(const QsaIndexer &p, float *work, size_t work_bytes, const
     if (!p.pos || !p.iqk || !p.wqn || !p.wkn || !p.IKc || !p.BKc || !work) FN_FAIL("qsa: null pointer");
     if (work_bytes < qsa_work_bytes(p.B, p.nt, p.max_ctx, p.top)) FN_FAIL("qsa: workspace too small");
     IxArgs a = make_args(p);
-    if (status_word(&a.status)) return -1;
+    if (p.status) a.status = p.status;
+    else if (status_word(&a.status)) return -1;
     const size_t bt = (size_t) p.B * p.nt;
     a.Qix = work;
     a.scores = a.Qix + bt * IXH * IXD;
