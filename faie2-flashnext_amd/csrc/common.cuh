@@ -103,6 +103,19 @@ __device__ __forceinline__ int wave_min_i(int v) {
     return min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 32));
 }
 
+// inclusive prefix sum over the wave in lane order through DPP alone (no LDS crossbar): row_shr 1, 2, 4, 8 scan each
+// row of 16 lanes (lanes without a source read 0), row_bcast 15 carries row 0's total into row 1 and row 2's into
+// row 3, row_bcast 31 carries lane 31's into rows 2 and 3.  Call from wave-uniform control flow.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);   // row_shr 1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);   // row_shr 2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);   // row_shr 4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);   // row_shr 8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast 15 into rows 1 and 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast 31 into rows 2 and 3
+    return x;
+}
+
 // (value, index) of the better of two: larger value, ties to the lower index
 __device__ __forceinline__ void vi_max(float &v, int &i, float v2, int i2) {
     if (v2 > v || (v2 == v && i2 < i)) {

@@ -181,18 +181,11 @@ __global__ void __launch_bounds__(256) k_ix_score(const IxArgs a) {
     }
 }
 
-// exclusive prefix sums of x and y over the 1024 threads in thread order, and their totals (wsum: 32 ints of LDS)
+// exclusive prefix sums of x and y over the 1024 threads in thread order, and their totals (wsum: 32 ints of LDS);
+// the wave scans are DPP (a shuffle-based scan, an LDS-crossbar permute per step, took ~1.8 us of this kernel)
 __device__ __forceinline__ int2 block_excl_scan2(int x, int y, int2 *wsum, int2 &total) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    int ix = x, iy = y;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int vx = __shfl_up(ix, off), vy = __shfl_up(iy, off);
-        if (lane >= off) {
-            ix += vx;
-            iy += vy;
-        }
-    }
+    const int ix = wave_incl_scan(x), iy = wave_incl_scan(y);
     __syncthreads();  // wsum free
     if (lane == 63) wsum[wave] = make_int2(ix, iy);
     __syncthreads();
@@ -213,11 +206,16 @@ __device__ __forceinline__ int2 block_excl_scan2(int x, int y, int2 *wsum, int2 
 
 // grid B nt, 1024 threads.  Thread t owns the contiguous blocks t*per .. t*per+per-1, per = ceil(nb / 1024) rounded
 // up to a multiple of 4 so that they load as float4; with PER > 0 the scores stay in registers (nb <= 1024 PER), with
-// PER == 0 every pass re-reads them (L2-resident).  Radix select on the score bits (scores are >= +0, so their bits
-// order like the values): 11-bit digits [30:20], [19:9] and 9-bit [8:0], each pass a 2048-bin LDS histogram of the
-// entries that match the digits fixed so far, then a block scan (descending) for the digit at which the count from
-// the top reaches `need`.  The histogram has 8 copies, by lane % 8, in different banks: lanes of one atomic
-// instruction that share a digit mostly hit different words.
+// PER == 0 every pass re-reads them (L2-resident).  Scores are >= +0, so their bits order like the values.
+// With the scores in registers (PER > 0) the selection first tries one pass: a 16384-bin LDS histogram of bits
+// [30:17] (the exponent and 6 mantissa bits, bins 1/64 of an octave wide), one block scan (descending) for the bin
+// where the count from the top reaches `top`; every block above that bin is kept, and the bin's own blocks (a few
+// dozen for the scores of real queries) are ranked exactly among themselves in the LDS (higher score first, equal
+// scores lower index first) and the first `need` of them kept.  A bin of more than 1024 blocks (mass ties) falls
+// through to the radix select: 11-bit digits [30:20], [19:9] and 9-bit [8:0], each pass a 2048-bin LDS histogram of
+// the entries that match the digits fixed so far, then a block scan for the digit at which the count from the top
+// reaches `need`.  Its histogram has 8 copies, by lane % 8, in different banks: lanes of one atomic instruction that
+// share a digit mostly hit different words.
 template <int PER>
 __global__ void __launch_bounds__(1024) k_ix_select(const IxArgs a) {
     constexpr int NBIN = 2048, NC = 8, HS = NBIN + 1, MAXPER = PER > 0 ? PER : 4;
@@ -245,6 +243,104 @@ __global__ void __launch_bounds__(1024) k_ix_select(const IxArgs a) {
             if (j0 + i < jn) u = *reinterpret_cast<const uint4 *>(s + j0 + i);
             v[i] = u.x; v[i + 1] = u.y; v[i + 2] = u.z; v[i + 3] = u.w;
         }
+    }
+    // the incomplete tail block is always visible (faie2fn.cu:1630)
+    const auto tail = [&]() {
+        const int tail0 = nb * IXR;
+        if (tid <= P - tail0) keys[a.top * IXR + tid] = tail0 + tid;
+        if (tid == 0) a.nkeys[bt] = a.top * IXR + (P + 1 - tail0);
+    };
+    int4 *kv = reinterpret_cast<int4 *>(keys);
+    if constexpr (PER > 0) {
+        constexpr int FS = 17, NF = 1 << (31 - FS), BPT = NF / 1024, CMAX = 1024;
+        static_assert(NF <= NC * HS, "the one-pass histogram shares the radix histogram's LDS");
+        static_assert(PER <= 32, "a thread's kept blocks are one 32-bit mask");
+        __shared__ uint2 cand[CMAX];               // (score bits, block) of the threshold bin
+        __shared__ unsigned kept[PER * 1024 / 32];  // bitmap of the threshold bin's kept blocks
+        __shared__ int sh_bin, sh_bneed, sh_bcnt, sh_slot;
+        int4 *h4 = reinterpret_cast<int4 *>(hist);
+        for (int i = tid; i < NF / 4; i += 1024) h4[i] = make_int4(0, 0, 0, 0);
+        for (int i = tid; i < PER * 32; i += 1024) kept[i] = 0u;
+        if (tid == 0) sh_slot = 0;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (j0 + i < jn) atomicAdd(&hist[v[i] >> FS], 1);
+        __syncthreads();
+        // thread t holds bins NF - BPT (t + 1) .. NF - 1 - BPT t: the scan in thread order runs over them descending
+        const int lo = NF - BPT * (tid + 1);
+        int c[BPT], sum = 0;
+#pragma unroll
+        for (int q = 0; q < BPT / 4; ++q) {
+            const int4 h = h4[lo / 4 + q];
+            c[4 * q] = h.x; c[4 * q + 1] = h.y; c[4 * q + 2] = h.z; c[4 * q + 3] = h.w;
+        }
+#pragma unroll
+        for (int k = 0; k < BPT; ++k) sum += c[k];
+        int2 tot;
+        const int excl = block_excl_scan2(sum, 0, wsum, tot).x;
+        if (excl < a.top && excl + sum >= a.top) {  // exactly one thread: counts >= 0, total = nb > top
+            int run = excl;
+#pragma unroll
+            for (int k = BPT - 1; k >= 0; --k) {
+                if (run < a.top && run + c[k] >= a.top) {
+                    sh_bin = lo + k;
+                    sh_bneed = a.top - run;  // blocks still to take from this bin
+                    sh_bcnt = c[k];
+                }
+                run += c[k];
+            }
+        }
+        __syncthreads();
+        const unsigned bin = (unsigned) sh_bin;
+        const int bneed = sh_bneed, bcnt = sh_bcnt;
+        if (bcnt <= CMAX) {  // (uniform)
+#pragma unroll
+            for (int i = 0; i < PER; ++i)
+                if (j0 + i < jn && (v[i] >> FS) == bin) cand[atomicAdd(&sh_slot, 1)] = make_uint2(v[i], (unsigned) (j0 + i));
+            __syncthreads();
+            if (bcnt <= 64) {  // (uniform) one wave, the other candidates read across lanes
+                if (tid < 64) {
+                    const uint2 me = tid < bcnt ? cand[tid] : make_uint2(0u, 0u);
+                    int rank = 0;
+                    for (int k = 0; k < bcnt; ++k) {
+                        const unsigned ox = (unsigned) __builtin_amdgcn_readlane((int) me.x, k);
+                        const unsigned oj = (unsigned) __builtin_amdgcn_readlane((int) me.y, k);
+                        rank += ox > me.x || (ox == me.x && oj < me.y);
+                    }
+                    if (tid < bcnt && rank < bneed) atomicOr(&kept[me.y >> 5], 1u << (me.y & 31));
+                }
+            } else if (tid < bcnt) {
+                const uint2 me = cand[tid];
+                int rank = 0;
+                for (int k = 0; k < bcnt; ++k) {
+                    const uint2 o = cand[k];
+                    rank += o.x > me.x || (o.x == me.x && o.y < me.y);
+                }
+                if (rank < bneed) atomicOr(&kept[me.y >> 5], 1u << (me.y & 31));
+            }
+            __syncthreads();
+            // every block above the bin, and the bin's kept ones (the thread's run spans at most two bitmap words,
+            // read once), as a bit mask; then one scan gives each thread its list slot
+            const int w0 = j0 >> 5;
+            const unsigned kw0 = kept[w0], kw1 = w0 + 1 < PER * 32 ? kept[w0 + 1] : 0u;
+            unsigned keep = 0u;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int j = j0 + i;
+                const unsigned d = v[i] >> FS, kw = (j >> 5) == w0 ? kw0 : kw1;
+                keep |= (unsigned) (j < jn && (d > bin || (d == bin && ((kw >> (j & 31)) & 1u)))) << i;
+            }
+            int slot = block_excl_scan2(__builtin_popcount(keep), 0, wsum, tot).x;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int j = j0 + i;
+                if ((keep >> i) & 1u) kv[slot++] = make_int4(j * IXR, j * IXR + 1, j * IXR + 2, j * IXR + 3);
+            }
+            tail();
+            return;
+        }
+        __syncthreads();  // the radix passes reuse the histogram's LDS
     }
     int *hl = hist + (tid & (NC - 1)) * HS;
     unsigned prefix = 0, pmask = 0;
@@ -306,7 +402,6 @@ __global__ void __launch_bounds__(1024) k_ix_select(const IxArgs a) {
     int2 tot;
     const int2 before = block_excl_scan2(gt, eq, wsum, tot);
     int slot = before.x + min(before.y, need), eq_rank = before.y;
-    int4 *kv = reinterpret_cast<int4 *>(keys);
     auto emit = [&](int j, unsigned u) {
         const bool keep = u > thr || (u == thr && eq_rank < need);
         eq_rank += u == thr;
@@ -319,10 +414,7 @@ __global__ void __launch_bounds__(1024) k_ix_select(const IxArgs a) {
     } else {
         for (int j = j0; j < jn; ++j) emit(j, s[j]);
     }
-    // the incomplete tail block is always visible (faie2fn.cu:1630)
-    const int tail0 = nb * IXR;
-    if (tid <= P - tail0) keys[a.top * IXR + tid] = tail0 + tid;
-    if (tid == 0) a.nkeys[bt] = a.top * IXR + (P + 1 - tail0);
+    tail();
 }
 
 IxArgs make_args(const QsaIndexer &p) {

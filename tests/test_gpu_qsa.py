@@ -126,6 +126,24 @@ def test_qsa_ties_keep_lowest_index(fnlib):
     assert mask[0, 0, :32].all() and not mask[0, 0, 32:].any()
 
 
+@pytest.mark.parametrize("nb", [600, 2000, 7000])
+def test_qsa_mass_ties_fall_back_to_radix(fnlib, nb):
+    """All-zero scores (zero index queries) put every complete block in one histogram bin: 600 blocks are ranked in
+    the LDS by index; 2000 and 7000 exceed the 1024 the one-pass selection ranks and take the radix passes.  Either
+    way the first `top` blocks are kept."""
+    top = 512
+    pos = nb * 4 + 1
+    max_ctx = (pos + 256) // 256 * 256
+    _say(f"qsa mass ties nb={nb} top={top}")
+    c = make_case(1, 1, max_ctx, [pos], seed=6)
+    c["iqk"][:, :, :512] = 0
+    Kc, Vc, IKc = c["Kc"].copy(), c["Vc"].copy(), c["IKc"].copy()
+    og, sc, mask = fnlib.attn_qsa(c["qg"], c["k"], c["v"], c["wq"], c["wk"], Kc, Vc, c["iqk"], c["wqn"], c["wkn"], IKc,
+                                  c["pos"], top=top)
+    assert not sc[0, 0, :nb].any()
+    assert mask[0, 0, :top].all() and not mask[0, 0, top:nb].any()
+
+
 @pytest.mark.parametrize("max_ctx,pos,top", [(16384, 12001, 512), (33024, 30001, 700), (131328, 9999, 512)])
 def test_qsa_select_storage_paths(fnlib, max_ctx, pos, top):
     """The selection keeps each thread's scores in registers up to 8 blocks a thread (here 3), up to 32 (here 8, for a
