@@ -660,29 +660,44 @@ __device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float
 // per thread; its loads are clamped to the last element, so the pass's array stays in registers.
 constexpr int xs_stride(int nt) { return nt * 8 + 1; }
 
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// The x of a pass is held as native 4-float vectors: a float4 (a struct) loaded and stored unchanged becomes a
+// 16-byte global-to-LDS memcpy, which the compiler places (load and store) at the store, behind the weight loads
+// requested in between, so that the store waited for them all (vmcnt counts loads in issue order).
 template <int NT, int XB> struct XPass {
-    float4 r[XB];
+    f4v r[XB];
     __device__ __forceinline__ void load(const float *__restrict__ x, int cols, int c0, int nch, int e0, int tid,
                                          int nth) {
         const int nx = NT * 8 * nch;
 #pragma unroll
         for (int k = 0; k < XB; ++k) {
             const int e = min(e0 + tid + nth * k, nx - 1), tg = e >> 3, t = tg / nch, gr = tg - t * nch;
-            r[k] = *reinterpret_cast<const float4 *>(x + (size_t) t * cols + (size_t) (c0 + gr) * 32 + 4 * (e & 7));
+            r[k] = *reinterpret_cast<const f4v *>(x + (size_t) t * cols + (size_t) (c0 + gr) * 32 + 4 * (e & 7));
         }
     }
+    // stores clamped like the loads (a lane past the end writes the last element's value to its place again), so
+    // that the loads and stores of a pass sit in one basic block
     __device__ __forceinline__ void store(float4 *xs, int nch, int e0, int tid, int nth) const {
         const int nx = NT * 8 * nch;
 #pragma unroll
         for (int k = 0; k < XB; ++k) {
-            const int e = e0 + tid + nth * k;
-            if (e < nx) {
-                const int tg = e >> 3, t = tg / nch, gr = tg - t * nch;
-                xs[gr * xs_stride(NT) + t * 8 + (e & 7)] = r[k];
-            }
+            const int e = min(e0 + tid + nth * k, nx - 1), tg = e >> 3, t = tg / nch, gr = tg - t * nch;
+            *reinterpret_cast<f4v *>(xs + gr * xs_stride(NT) + t * 8 + (e & 7)) = r[k];
         }
     }
 };
+
+// the passes of x after the first (x of many tokens): loaded and stored here, before the caller requests weights
+template <int NT, int XB>
+__device__ __forceinline__ void stage_x_rest(const float *__restrict__ x, int cols, int c0, int nch, float4 *xs,
+                                             int tid) {
+    for (int e0 = 512 * XB; e0 < NT * 8 * nch; e0 += 512 * XB) {
+        XPass<NT, XB> q;
+        q.load(x, cols, c0, nch, e0, tid, 512);
+        q.store(xs, nch, e0, tid, 512);
+    }
+}
 
 // batch j of row-set s over the groups [c0, c1): groups c0 + li + LPR (U j + u), u < U, of row s RPW + lane / LPR.
 // Row and group are clamped into the weight: a lane past the last row or group loads a valid address whose value
@@ -751,29 +766,20 @@ __device__ __forceinline__ void gemv_walk_short(const PP &P, int rows, int g0, i
     };
     next(s, j, s1, j1);
     uint32_t wa[U][NW], wb[U][NW];
-    // x [NT][cols] -> xs (the layout of XPass).  The first part of x is requested before the first two weight
-    // batches, so that its LDS writes wait for x alone.
-    const int nx = NT * 8 * ng;
-    for (int e0 = 0; e0 < nx; e0 += 512 * XB) {
-        float4 xr[XB];  // loads clamped to the last element (unconditional: the array stays in registers)
-#pragma unroll
-        for (int k = 0; k < XB; ++k) {
-            const int e = min(e0 + tid + 512 * k, nx - 1), tg = e >> 3, t = tg / ng, gr = tg - t * ng;
-            xr[k] = *reinterpret_cast<const float4 *>(x + (size_t) t * cols + (size_t) (g0 + gr) * 32 + 4 * (e & 7));
-        }
-        if (e0 == 0) {
-            if (s < NS) load_batch<TY, LPR>(P, rows, s, j, lane, g0, g1, wa);
-            if (s1 < NS) load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wb);
-        }
-#pragma unroll
-        for (int k = 0; k < XB; ++k) {
-            const int e = e0 + tid + 512 * k;
-            if (e < nx) {
-                const int tg = e >> 3, t = tg / ng, gr = tg - t * ng;
-                xs[gr * xs_stride(NT) + t * 8 + (e & 7)] = xr[k];
-            }
-        }
-    }
+    // x [NT][cols] -> xs (the layout of XPass).  The first pass of x is requested before the first two weight
+    // batches, so that its LDS writes wait for x alone (vmcnt counts loads in issue order); scheduling fences keep
+    // the compiler from moving the weight loads ahead of it.  Further passes (x of many tokens) go before the
+    // weight loads too, so that no path with a different count of loads in flight joins the walk.
+    XPass<NT, XB> xp;
+    xp.load(x, cols, g0, ng, 0, tid, 512);
+    stage_x_rest<NT, XB>(x, cols, g0, ng, xs, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    // unconditional (load_batch clamps the row: a wave past the last row-set loads a row it never sums), so that
+    // this is one basic block with the x pass
+    load_batch<TY, LPR>(P, rows, s, j, lane, g0, g1, wa);
+    load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wb);
+    __builtin_amdgcn_sched_barrier(0);
+    xp.store(xs, ng, 0, tid, 512);
     __syncthreads();
     const TabT<TY> T;  // (IQ4 formats) the level table in registers, once; (IQ3_S) the grid in LDS
     float acc[NT];
@@ -818,14 +824,15 @@ __device__ __forceinline__ void gemv_walk_deep(const PP &P, int rows, int g0, in
     // weight batches, so that its LDS writes wait for x alone.  A wave with one batch or none takes a short path
     // with no prefetch; every wave passes the one barrier either way.
     XPass<NT, XB> xp;
-    for (int e0 = 0; e0 < NT * 8 * ng; e0 += 512 * XB) {
-        xp.load(x, cols, g0, ng, e0, tid, 512);
-        if (e0 == 0) {
-            const int b1 = n > 1 ? 1 : 0;
-            load_batch<TY, LPR>(P, rows, w0, 0, lane, g0, g1, wa);
-            load_batch<TY, LPR>(P, rows, w0 + (b1 / NB) * nws, b1 % NB, lane, g0, g1, wb);
-        }
-        xp.store(xs, ng, e0, tid, 512);
+    {
+        const int b1 = n > 1 ? 1 : 0;
+        xp.load(x, cols, g0, ng, 0, tid, 512);
+        stage_x_rest<NT, XB>(x, cols, g0, ng, xs, tid);
+        __builtin_amdgcn_sched_barrier(0);  // (as in the short walk) x, then the weights, then x's LDS writes
+        load_batch<TY, LPR>(P, rows, w0, 0, lane, g0, g1, wa);
+        load_batch<TY, LPR>(P, rows, w0 + (b1 / NB) * nws, b1 % NB, lane, g0, g1, wb);
+        __builtin_amdgcn_sched_barrier(0);
+        xp.store(xs, ng, 0, tid, 512);
     }
     __syncthreads();
 #define FN_GEMV_LOAD(W, B) load_batch<TY, LPR>(P, rows, w0 + ((B) / NB) * nws, (B) % NB, lane, g0, g1, W)
@@ -892,11 +899,12 @@ __global__ void __launch_bounds__(512) k_gemv_c(PP P, int rows, int G, int gps, 
     for (int c0 = g0; c0 < g1; c0 += kc) {
         const int c1 = min(g1, c0 + kc), nch = c1 - c0, NB = (nch + LPR * U - 1) / (LPR * U);
         __syncthreads();  // every wave is done reading the previous chunk
-        for (int e0 = 0; e0 < NT * 8 * nch; e0 += 512 * XB) {
-            xp.load(x, cols, c0, nch, e0, tid, 512);
-            if (e0 == 0 && live) load_batch<TY, LPR>(P, rows, s, 0, lane, c0, c1, wa);
-            xp.store(xs, nch, e0, tid, 512);
-        }
+        xp.load(x, cols, c0, nch, 0, tid, 512);
+        stage_x_rest<NT, XB>(x, cols, c0, nch, xs, tid);
+        __builtin_amdgcn_sched_barrier(0);  // (as in k_gemv's walks) x, then the weights, then x's LDS writes
+        load_batch<TY, LPR>(P, rows, s, 0, lane, c0, c1, wa);  // (row clamped: a dead wave's loads go unused)
+        __builtin_amdgcn_sched_barrier(0);
+        xp.store(xs, nch, 0, tid, 512);
         __syncthreads();
         if (!live) continue;
         for (int j = 0; j < NB; j += 2) {
