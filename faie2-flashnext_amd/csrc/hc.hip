@@ -26,9 +26,32 @@ __global__ void __launch_bounds__(256) k_hc_down(const float *__restrict__ h, co
     extern __shared__ float4 xs[];  // [G][xs_stride(NT)]
     __shared__ float red[NT][4];
     constexpr int NWB = Q<QT_BF16>::NW, GPL = 2;  // groups per lane per row (G <= 128)
+    constexpr bool PRE = NT <= 2;  // the streams of every token requested up front (8 float4 registers a token)
     const int k = blockIdx.y, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, G = D / 32, D4 = D / 4;
     const bool writer = blockIdx.x == 0;
-    // the wave's rows' weight words first: they do not depend on the streams
+    // Requests in the order their values are needed, since a value waits for everything requested before it (vmcnt
+    // counts loads in issue order): the streams (h, and y when given; the y slot reads h again without one, unused)
+    // and the norm weight, then the wave's rows' weight words, which only the dot product after the norm uses.
+    // Every load is unconditional (indices clamped), so that all of them issue before the first wait.
+    float4 hv[PRE ? NT : 1][HC_CH], yv[PRE ? NT : 1][HC_CH];
+    if constexpr (PRE) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float4 *h4 = reinterpret_cast<const float4 *>(h + ((size_t) t * HC + k) * D);
+            const float4 *y4 = reinterpret_cast<const float4 *>(y ? y + (size_t) t * D : h);
+#pragma unroll
+            for (int j = 0; j < HC_CH; ++j) {
+                const int c = min(tid + 256 * j, D4 - 1);
+                hv[t][j] = h4[c];
+                yv[t][j] = y4[c];
+            }
+        }
+    }
+    // the norm weight of the thread's float4s (tid, tid + 256, ... < D / 4; at most HC_CH of them)
+    const float4 *w4 = reinterpret_cast<const float4 *>(w + (size_t) k * D);
+    float4 wc[HC_CH];
+#pragma unroll
+    for (int j = 0; j < HC_CH; ++j) wc[j] = w4[min(tid + 256 * j, D4 - 1)];
     uint32_t wr[HC_RW][GPL][NWB];
     const int r0 = blockIdx.x * HC_DR + wv * HC_RW;
 #pragma unroll
@@ -38,13 +61,7 @@ __global__ void __launch_bounds__(256) k_hc_down(const float *__restrict__ h, co
 #pragma unroll
         for (int u = 0; u < GPL; ++u) Q<QT_BF16>::load(rp, min(lane + 64 * u, G - 1), wr[j][u]);
     }
-    // the norm weight of the thread's float4s (tid, tid + 256, ... < D / 4; at most HC_CH of them)
-    const float4 *w4 = reinterpret_cast<const float4 *>(w + (size_t) k * D);
-    float4 wc[HC_CH];
-#pragma unroll
-    for (int j = 0; j < HC_CH; ++j) wc[j] = tid + 256 * j < D4 ? w4[tid + 256 * j] : make_float4(0, 0, 0, 0);
-    // v and its sum of squares, the thread's float4s in order for each token; unrolled, so that the loads of later
-    // float4s and tokens are in flight before the LDS stores wait for the first
+    // v and its sum of squares, the thread's float4s in order for each token
     float ss[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -56,9 +73,12 @@ __global__ void __launch_bounds__(256) k_hc_down(const float *__restrict__ h, co
         for (int j = 0; j < HC_CH; ++j) {
             const int c = tid + 256 * j;
             if (c < D4) {
-                float4 v = h4[c];
+                float4 v;
+                if constexpr (PRE) v = hv[t][j];
+                else v = h4[c];
                 if (y) {
-                    v = add_scaled(v, y4[c], is);
+                    if constexpr (PRE) v = add_scaled(v, yv[t][j], is);
+                    else v = add_scaled(v, y4[c], is);
                     if (writer) reinterpret_cast<float4 *>(hout + ((size_t) t * HC + k) * D)[c] = v;
                 }
                 ss[t] += sumsq4(v);
@@ -72,7 +92,8 @@ __global__ void __launch_bounds__(256) k_hc_down(const float *__restrict__ h, co
 #pragma unroll
         for (int t = 0; t < NT; ++t) red[t][wv] = ss[t];
     }
-    __syncthreads();
+    // LDS-only barriers: the waves exchange through the LDS alone, and the weight words stay in flight across them
+    lds_barrier();
     // hn = v r w, in place in the LDS (each thread rescales the float4s it wrote)
     float r[NT];
 #pragma unroll
@@ -95,7 +116,7 @@ __global__ void __launch_bounds__(256) k_hc_down(const float *__restrict__ h, co
             if (writer) reinterpret_cast<float4 *>(hn + ((size_t) t * HC + k) * D)[c] = o;
         }
     }
-    __syncthreads();
+    lds_barrier();
     const Iq4Tab T;
 #pragma unroll
     for (int j = 0; j < HC_RW; ++j) {

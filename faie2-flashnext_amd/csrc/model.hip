@@ -126,27 +126,47 @@ __global__ void __launch_bounds__(UPMIX_ROWS * 8)
     const int tid = threadIdx.x, cpb = UPMIX_ROWS / HC, c0 = blockIdx.x * cpb;
     const int ri = tid >> 3, li = tid & 7, cc = ri / HC, s = ri - cc * HC, c = c0 + cc;
     const int nq = HCR / 8;
-    // the lane's weight chunks li + 8 u, u < UPMIX_U, requested first: they do not depend on the activation
+    // Requests in the order their values are needed (a value waits for everything requested before it: vmcnt
+    // counts loads in issue order), each unconditional with clamped indices so that all issue before the first
+    // wait: the low-rank partials of the thread's first activation entry (ks <= UPMIX_HC of them), then the lane's
+    // weight chunks li + 8 u, u < UPMIX_U, then the mix's normalised streams (thread tid < cpb nt finishes column
+    // c0 + tid % cpb of token tid / cpb).
+    const int i0 = min(tid, nt * HCR - 1), t0 = i0 / HCR, rr0 = i0 - t0 * HCR;
+    float lp[UPMIX_HC];
+#pragma unroll
+    for (int k = 0; k < UPMIX_HC; ++k) lp[k] = lr[((size_t) min(k, ks - 1) * nt + t0) * ldr + rr0];
+    __builtin_amdgcn_sched_barrier(0);
     const bool live = c < D;
     uint4 wq[UPMIX_U];
-    if (live) {
-        const uint4 *row = reinterpret_cast<const uint4 *>(U + ((size_t) s * D + c) * urs);
+    {
+        const uint4 *row = reinterpret_cast<const uint4 *>(U + ((size_t) s * D + min(c, D - 1)) * urs);
 #pragma unroll
         for (int u = 0; u < UPMIX_U; ++u) wq[u] = row[min(li + 8 * u, nq - 1)];
     }
-    // the mix's normalised streams, requested now as well (thread tid < cpb nt finishes column c0 + tid % cpb of
-    // token tid / cpb)
     float hv[UPMIX_HC];
     const int mt = tid / cpb, mc = c0 + (tid - mt * cpb);
     const bool mixer = tid < cpb * nt && mc < D;
+    {
+        const float *hm = hn + (size_t) min(mt, nt - 1) * HC * D + min(mc, D - 1);
 #pragma unroll
-    for (int k = 0; k < UPMIX_HC; ++k)
-        hv[k] = mixer && k < HC ? hn[(size_t) mt * HC * D + (size_t) k * D + mc] : 0.0f;
-    for (int i = tid; i < nt * HCR; i += UPMIX_ROWS * 8) {
+        for (int k = 0; k < UPMIX_HC; ++k) hv[k] = hm[(size_t) min(k, HC - 1) * D];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the activation: silu of the partials' sum in split order (lr_sum's), the first entry from the registers.
+    // Unconditional (a thread past the entries writes the last entry's value to it again), so that the compiler
+    // does not move the partials' loads under a branch, behind the weight chunks.
+    {
+        float v = lp[0];
+#pragma unroll
+        for (int k = 1; k < UPMIX_HC; ++k)
+            if (k < ks) v += lp[k];
+        tt[i0] = silu(v * (1.0f / HC));
+    }
+    for (int i = tid + UPMIX_ROWS * 8; i < nt * HCR; i += UPMIX_ROWS * 8) {
         const int t = i / HCR, r = i - t * HCR;
         tt[i] = silu(lr_sum(lr, ks, nt, ldr, t, r) * (1.0f / HC));
     }
-    __syncthreads();
+    lds_barrier();  // (the exchange is through the LDS alone; the weight chunks stay in flight)
     float acc[MAXT];
 #pragma unroll
     for (int t = 0; t < MAXT; ++t) acc[t] = 0.0f;
@@ -334,7 +354,7 @@ int hc_up(Model &m, const QW &dinj, const QW &up, int nt, int ks) {
     Acts &a = m.a;
     const bool inj = dinj.L.rows > d.HCR;
     const int ldr = dinj.L.rows;
-    if (up.L.type == QT_BF16 && UPMIX_ROWS % d.HC == 0 && d.HC <= UPMIX_HC && d.HCR % 8 == 0 &&
+    if (up.L.type == QT_BF16 && UPMIX_ROWS % d.HC == 0 && d.HC <= UPMIX_HC && ks <= UPMIX_HC && d.HCR % 8 == 0 &&
         d.HCR <= 64 * UPMIX_U) {
         const int cpb = UPMIX_ROWS / d.HC;
         const size_t lds = ((size_t) nt * d.HCR + 8 * UPMIX_ROWS) * 4;
