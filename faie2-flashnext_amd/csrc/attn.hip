@@ -160,6 +160,24 @@ __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
 
     const int sp_i = blockIdx.x, g = blockIdx.y, bt = blockIdx.z, b = bt / a.nt, t = bt - b * a.nt;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // (one new token) Every load of the prologue is requested first, before the position is waited for and before
+    // any of them is used (none depends on the position): the RoPE frequency, the wave's query rows and their norm
+    // weight, the new key row, its norm weight and the new value row; the sines and cosines then overlap their round
+    // trip.  The key row is normalised and the key and value rows go to the LDS by every wave (the same values),
+    // unconditionally, so that the compiler does not move their loads under the owner's branch, behind the others.
+    float fr = 0.0f;
+    float4 wq, xq[HPW], xk, wkv, xv;
+    if constexpr (PREP) {
+        fr = a.inv_freq[min((int) threadIdx.x, MAXROT / 2 - 1)];
+        wq = reinterpret_cast<const float4 *>(a.wq)[lane];
+#pragma unroll
+        for (int i = 0; i < HPW; ++i)
+            xq[i] = reinterpret_cast<const float4 *>(a.qg + ((size_t) bt * a.nq + g * GRP + wave * HPW + i) * 2 * HD)[lane];
+        const size_t kv = ((size_t) bt * a.nkv + g) * HD;
+        xk = reinterpret_cast<const float4 *>(a.knew + kv)[lane];
+        wkv = reinterpret_cast<const float4 *>(a.wk)[lane];
+        xv = reinterpret_cast<const float4 *>(a.vnew + kv)[lane];
+    }
     const int P = a.pos[b] + t;
     const int32_t *klist = LIST ? a.keys + (size_t) bt * a.kstride : nullptr;
     const int nk = LIST ? a.nkeys[bt] : min(P + 1, a.max_ctx);  // slots 0 .. nk-1 hold visible keys
@@ -175,23 +193,14 @@ __global__ void __launch_bounds__(WAVES * 64) k_attn_split(const AttnArgs a) {
 
     if (PREP) {
         if (threadIdx.x < a.nrot / 2) {
-            const float ang = (float) P * a.inv_freq[threadIdx.x];  // fp32 angle (faie2fn.cu:1440)
+            const float ang = (float) P * fr;  // fp32 angle (faie2fn.cu:1440)
             rcs[threadIdx.x] = cosf(ang);
             rsn[threadIdx.x] = sinf(ang);
         }
-        const float4 wq = reinterpret_cast<const float4 *>(a.wq)[lane];
 #pragma unroll
-        for (int i = 0; i < HPW; ++i) {
-            const int hh = wave * HPW + i;
-            const float4 x = reinterpret_cast<const float4 *>(a.qg + ((size_t) bt * a.nq + g * GRP + hh) * 2 * HD)[lane];
-            qs[lane * GRP + hh] = rms_row(x, wq, a.eps);
-        }
-        if (owner && wave == 0) {
-            const size_t kv = ((size_t) bt * a.nkv + g) * HD;
-            kn4[lane] = rms_row(reinterpret_cast<const float4 *>(a.knew + kv)[lane],
-                                reinterpret_cast<const float4 *>(a.wk)[lane], a.eps);
-            vn4[lane] = reinterpret_cast<const float4 *>(a.vnew + kv)[lane];
-        }
+        for (int i = 0; i < HPW; ++i) qs[lane * GRP + wave * HPW + i] = rms_row(xq[i], wq, a.eps);
+        kn4[lane] = rms_row(xk, wkv, a.eps);
+        vn4[lane] = xv;
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < HPW; ++i) rope_row_lds(qs + wave * HPW + i, GRP, lane, a.nrot, rcs, rsn);

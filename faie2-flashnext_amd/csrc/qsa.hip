@@ -237,10 +237,11 @@ __global__ void __launch_bounds__(1024) k_ix_select(const IxArgs a) {
     const int per = ((nb + 1023) / 1024 + 3) & ~3, j0 = min(tid * per, nb), jn = min(j0 + per, nb);
     unsigned v[MAXPER];
     if (PER > 0) {
+        // every float4 requested before the first is used: unconditional loads (a float4 past the thread's run reads
+        // the row's first one instead; every use below checks j < jn), so that none sits under a branch with a wait
 #pragma unroll
         for (int i = 0; i < MAXPER; i += 4) {
-            uint4 u = make_uint4(0u, 0u, 0u, 0u);
-            if (j0 + i < jn) u = *reinterpret_cast<const uint4 *>(s + j0 + i);
+            const uint4 u = *reinterpret_cast<const uint4 *>(s + (j0 + i < jn ? j0 + i : 0));
             v[i] = u.x; v[i + 1] = u.y; v[i + 2] = u.z; v[i + 3] = u.w;
         }
     }
