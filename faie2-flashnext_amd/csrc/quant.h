@@ -67,6 +67,9 @@ int quant_pack_launch(const QLayout &L, const uint8_t *raw, uint8_t *packed, hip
 int quant_dequant_launch(const QLayout &L, const uint8_t *packed, float *out, hipStream_t st);
 // y[t][r] = sum_c W[r][c] x[t][c] for t < nt (1..8); x [nt][cols], y [nt][rows]; work: gemv_work_bytes() bytes
 // ks_force: as gemv_plan's (1: no split-K whatever fn_gemv_override asks, for callers without a work buffer)
+// whether every plane of the packed weight is addressable with 32-bit offsets (the GEMV kernels' form)
+bool gemv_planes_fit(const QLayout &L);
+
 int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, float *y, float *work,
                 size_t work_bytes, hipStream_t st, int ks_force = 0);
 

@@ -165,10 +165,18 @@ int quant_dequant_launch(const QLayout &L, const uint8_t *packed, float *out, hi
     return o->dequant(L, planes(L, packed), out, st);
 }
 
+// the GEMV kernels address each plane of a weight with 32-bit offsets from its base
+bool gemv_planes_fit(const QLayout &L) {
+    for (int i = 0; i < 3; ++i)
+        if (L.rs[i] * (size_t) L.rows > ((size_t) 1 << 32)) return false;
+    return true;
+}
+
 int gemv_launch(const QLayout &L, const uint8_t *packed, const float *x, int nt, float *y, float *work,
                 size_t work_bytes, hipStream_t st, int ks_force) {
     if (nt < 1 || nt > MAXNT) FN_FAIL("gemv: nt must be 1..8");
     if (!packed || !x || !y) FN_FAIL("gemv: null pointer");
+    if (!gemv_planes_fit(L)) FN_FAIL("gemv: a plane of the packed weight exceeds 4 GiB");
     if ((uintptr_t) packed % 16 || (uintptr_t) x % 16) FN_FAIL("gemv: weight and x must be 16-byte aligned");
     const GemvPlan pl = gemv_plan(L, ks_force);
     float *out = y;
@@ -193,6 +201,7 @@ int gemv_split_launch(const QLayout &L, const uint8_t *packed, const float *x, i
                       int *ks_out, hipStream_t st) {
     if (nt < 1 || nt > MAXNT) FN_FAIL("gemv: nt must be 1..8");
     if (!packed || !x || !part || ks < 1) FN_FAIL("gemv: bad arguments");
+    if (!gemv_planes_fit(L)) FN_FAIL("gemv: a plane of the packed weight exceeds 4 GiB");
     if ((uintptr_t) packed % 16 || (uintptr_t) x % 16) FN_FAIL("gemv: weight and x must be 16-byte aligned");
     const GemvPlan pl = gemv_plan(L, ks);
     const QOps *o = ops(L.type);

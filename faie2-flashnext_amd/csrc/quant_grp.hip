@@ -35,6 +35,7 @@ int gemv_group_launch(const GemvPart *parts, int n, const float *x, int nt, hipS
         const GemvPart &g = parts[i];
         if (!g.L || !g.packed || !g.y) FN_FAIL("gemv group: null part");
         if (g.L->cols != parts[0].L->cols) FN_FAIL("gemv group: parts differ in cols");
+        if (!gemv_planes_fit(*g.L)) FN_FAIL("gemv: a plane of the packed weight exceeds 4 GiB");
     }
     // a matching format set: every slot takes the first unused part of its format
     int kind = -1, slot_of[4] = {0, 0, 0, 0};

@@ -183,6 +183,21 @@ struct RP {
 __device__ __forceinline__ RP row_planes(const PP &P, int row) {
     return RP{P.p0 + (size_t) row * P.rs0, P.p1 + (size_t) row * P.rs1, P.p2 + (size_t) row * P.rs2};
 }
+// The same for the GEMV's weight loads: a plane is its base (wave-uniform, in SGPRs) and the row's 32-bit byte
+// offset, so that a load's address is the base plus one 32-bit VGPR (the load's scalar-base form) instead of a
+// 64-bit multiply-add per plane per batch.  Needs planes under 4 GiB (gemv_launch checks).
+struct Plane32 {
+    const uint8_t *base;
+    uint32_t off;
+    __device__ __forceinline__ const uint8_t *operator+(uint32_t x) const { return base + (off + x); }
+};
+struct RP32 {
+    Plane32 b0, b1, b2;
+};
+__device__ __forceinline__ RP32 row_planes32(const PP &P, int row) {
+    const uint32_t r = (uint32_t) row;
+    return RP32{{P.p0, r * (uint32_t) P.rs0}, {P.p1, r * (uint32_t) P.rs1}, {P.p2, r * (uint32_t) P.rs2}};
+}
 
 // one decoded group: GGUF value j = fl(s[j / 16] * q[j] - m[j / 16])
 struct Grp {
@@ -200,7 +215,7 @@ template <> struct Q<QT_BF16> {
     static constexpr int NW = 16;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         const uint8_t *p = R.b0 + 64 * g;
 #pragma unroll
         for (int i = 0; i < 4; ++i) ld16(p + 16 * i, w + 4 * i);
@@ -221,7 +236,7 @@ template <> struct Q<QT_Q8_0> {
     static constexpr int NW = 9;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         const uint8_t *q = R.b0 + 32 * g;
         ld16(q, w);
         ld16(q + 16, w + 4);
@@ -243,7 +258,7 @@ template <> struct Q<QT_IQ4_NL> {
     static constexpr int NW = 5;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         ld16(R.b0 + 16 * g, w);
         w[4] = ld2(R.b1 + 2 * g);
     }
@@ -271,7 +286,7 @@ template <> struct Q<QT_IQ4_XS> {
     static constexpr int NW = 6;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         ld16(R.b0 + 16 * g, w);  // super-block g / 8 at 128 (g / 8), group g % 8 at 16 (g % 8) inside it
         ld8(R.b1 + 8 * (g >> 3), w + 4);
     }
@@ -305,7 +320,7 @@ template <> struct Q<QT_Q4_K> {
     static constexpr int NW = 12;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = true;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         const uint8_t *q = R.b0 + 16 * (g & ~1);  // the 32 bytes of groups 2k and 2k + 1
         ld16(q, w);
         ld16(q + 16, w + 4);
@@ -331,7 +346,7 @@ template <> struct Q<QT_Q5_K> {
     static constexpr int NW = 20;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = true;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         const uint8_t *q = R.b0 + 16 * (g & ~1);
         ld16(q, w);
         ld16(q + 16, w + 4);
@@ -342,10 +357,12 @@ template <> struct Q<QT_Q5_K> {
     }
     __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
         const int ib = g & 7, sh = 4 * (ib & 1);
+        const uint32_t rot = (uint32_t) (ib + 28) & 31u;  // a right rotation by ib - 4 takes bit 8k + ib to 8k + 4
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             // 4 values per 32-bit operation: the nibbles, then bit ib of each qh byte moved to bit 4 of its byte
-            const uint32_t q = (((w[8 + i] >> ib) << 4) & 0x10101010u) | ((w[i] >> sh) & 0x0F0F0F0Fu);
+            const uint32_t hb = __builtin_amdgcn_alignbit(w[8 + i], w[8 + i], rot);
+            const uint32_t q = (hb & 0x10101010u) | ((w[i] >> sh) & 0x0F0F0F0Fu);
 #pragma unroll
             for (int k = 0; k < 4; ++k) o.q[4 * i + k] = (float) ((q >> (8 * k)) & 0xFFu);
         }
@@ -363,7 +380,7 @@ template <> struct Q<QT_Q6_K> {
     static constexpr int NW = 18;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         const int ib = g & 7, n = ib >> 2, qu = ib & 3, sb = g >> 3;
         const uint8_t *l = R.b0 + 128 * sb + 64 * n + 32 * (qu & 1);
         ld16(l, w);
@@ -399,7 +416,7 @@ template <> struct Q<QT_IQ3_S> {
     static constexpr int NW = 6;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         const int ib = g & 7;
         ld8(R.b0 + 8 * g, w);                                 // qs of the group
         const uint8_t *h = R.b1 + 44 * (g >> 3);
@@ -449,7 +466,7 @@ template <> struct Q<QT_IQ2_XXS> {
     static constexpr int NW = 3;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         ld8(R.b0 + 8 * g, w);
         w[2] = ld2(R.b1 + 2 * (g >> 3));
     }
@@ -468,7 +485,7 @@ template <> struct Q<QT_IQ2_XS> {
     static constexpr int NW = 4;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         const int ib = g & 7;
         ld8(R.b0 + 8 * g, w);
         w[2] = *reinterpret_cast<const uint32_t *>(R.b1 + 8 * (g >> 3) + (ib & 4));
@@ -496,7 +513,7 @@ template <> struct Q<QT_IQ2_S> {
     static constexpr int NW = 5;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         const int ib = g & 7;
         const uint8_t *a = R.b0 + 64 * (g >> 3), *h = R.b1 + 16 * (g >> 3);
         w[0] = *reinterpret_cast<const uint32_t *>(a + 4 * ib);
@@ -525,7 +542,7 @@ template <> struct Q<QT_IQ3_XXS> {
     static constexpr int NW = 4;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         const int ib = g & 7;
         const uint8_t *a = R.b0 + 96 * (g >> 3);
         ld8(a + 8 * ib, w);
@@ -555,7 +572,7 @@ template <> struct Q<QT_Q2_0> {
     static constexpr int NW = 3;
     static constexpr int U = prefetch_groups(NW);
     static constexpr bool MIN = false;
-    __device__ static void load(const RP &R, int g, uint32_t *w) {
+    template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         ld8(R.b0 + 8 * g, w);
         w[2] = ld2(R.b1 + 2 * (g >> 1));
     }
@@ -612,14 +629,18 @@ template <int LPR> __device__ __forceinline__ float lane_row_sum(float v) {
 // one group's contribution to the NT accumulators; xg points at the group's x in LDS: float4 c of token t at
 // xg[t * 8 + c] (offsets known at compile time).  The arithmetic (and its order) does not depend on NT: token t of
 // an NT-token call gets the bits a one-token call gets.
-template <uint32_t TY, int NT>
+// FAC (formats with a minimum, Q4_K / Q5_K): sum_j (s q_j - m) x_j is taken as s (sum_j q_j x_j) - m (sum_j x_j),
+// with the half-group sums of x from xsm[2 t + h] (x_half_sums), which every row of the call shares: the dequantised
+// value is never formed, one multiply-add per value fewer.  Without FAC each value is dequantised to fl(s q - m)
+// first (the GGUF value, as k_dequant writes it).
+template <uint32_t TY, int NT, bool FAC = false>
 __device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float4 *xg, float *acc,
-                                           const TabT<TY> &T) {
+                                           const TabT<TY> &T, const float *xsm = nullptr) {
     Grp o;
     Q<TY>::unpack(w, g, o, T);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        if constexpr (Q<TY>::MIN) {
+        if constexpr (Q<TY>::MIN && !FAC) {
             float wv[16];
 #pragma unroll
             for (int j = 0; j < 16; ++j) wv[j] = __builtin_fmaf(o.s[h], o.q[16 * h + j], -o.m[h]);
@@ -635,6 +656,21 @@ __device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float
                     a = __builtin_fmaf(wv[4 * c + 3], xv.w, a);
                 }
                 acc[t] = a;
+            }
+        } else if constexpr (Q<TY>::MIN) {
+            // one chain per half and token: s (q . x) - m (sum x), three operations a token beyond the products
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                float d = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const float4 xv = xg[t * 8 + 4 * h + c];
+                    d = __builtin_fmaf(o.q[16 * h + 4 * c], xv.x, d);
+                    d = __builtin_fmaf(o.q[16 * h + 4 * c + 1], xv.y, d);
+                    d = __builtin_fmaf(o.q[16 * h + 4 * c + 2], xv.z, d);
+                    d = __builtin_fmaf(o.q[16 * h + 4 * c + 3], xv.w, d);
+                }
+                acc[t] = __builtin_fmaf(-o.m[h], xsm[2 * t + h], __builtin_fmaf(o.s[h], d, acc[t]));
             }
         } else {
 #pragma unroll
@@ -654,11 +690,41 @@ __device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float
     }
 }
 
+
 // x of tokens [0, NT) and groups [c0, c0 + nch) -> LDS, group-major: float4 c of token t of group c0 + gr at
 // xs[gr * xs_stride(NT) + t * 8 + c].  The stride is odd (in float4), so the lanes of a row, which read consecutive
 // groups, hit distinct bank quads, and every read's offset inside a group is an immediate.  One pass moves XB float4
 // per thread; its loads are clamped to the last element, so the pass's array stays in registers.
 constexpr int xs_stride(int nt) { return nt * 8 + 1; }
+
+// formats whose GEMV takes the factored minimum (accumulate<FAC>) and so stages the half-group sums of x
+template <uint32_t TY> constexpr bool gemv_fac() { return Q<TY>::MIN; }
+// LDS bytes per group of x in the GEMV kernels: the x float4s (xs_stride(nt) of them) and, for gemv_fac formats,
+// the nt x 2 half-group sums
+template <uint32_t TY> constexpr int xs_group_bytes(int nt) {
+    return (nt * 8 + 1) * (int) sizeof(float4) + (gemv_fac<TY>() ? nt * 2 * (int) sizeof(float) : 0);
+}
+
+// the half-group sums of the staged x (groups [0, nch) of the LDS layout below): xsm[(gr NT + t) 2 + h] = the 16
+// values x[t][32 gr + 16 h + j], j = 0..15, added in order, so that every launch shape and token count gets the
+// same sums.  nth threads; the caller publishes them with a barrier.
+template <int NT>
+__device__ __forceinline__ void x_half_sums(const float4 *xs, int nch, float *xsm, int tid, int nth) {
+    for (int i = tid; i < nch * NT * 2; i += nth) {
+        const int h = i & 1, tg = i >> 1, gr = tg / NT, t = tg - gr * NT;
+        const float4 *p = xs + gr * xs_stride(NT) + t * 8 + 4 * h;
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float4 v = p[c];
+            s += v.x;
+            s += v.y;
+            s += v.z;
+            s += v.w;
+        }
+        xsm[i] = s;
+    }
+}
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
@@ -706,7 +772,7 @@ template <uint32_t TY, int LPR>
 __device__ __forceinline__ void load_batch(const PP &P, int rows, int s, int j, int lane, int c0, int c1,
                                            uint32_t (&w)[Q<TY>::U][Q<TY>::NW]) {
     constexpr int U = Q<TY>::U;
-    const RP R = row_planes(P, min(s * (64 / LPR) + lane / LPR, rows - 1));
+    const RP32 R = row_planes32(P, min(s * (64 / LPR) + lane / LPR, rows - 1));
     const int gb = c0 + lane % LPR + LPR * U * j;
 #pragma unroll
     for (int u = 0; u < U; ++u) Q<TY>::load(R, min(gb + LPR * u, c1 - 1), w[u]);
@@ -714,13 +780,18 @@ __device__ __forceinline__ void load_batch(const PP &P, int rows, int s, int j, 
 
 template <uint32_t TY, int NT, int LPR>
 __device__ __forceinline__ void acc_batch(const uint32_t (&w)[Q<TY>::U][Q<TY>::NW], int j, int lane, int c0, int c1,
-                                          const float4 *xs, float *acc, const TabT<TY> &T) {
+                                          const float4 *xs, const float *xsm, float *acc, const TabT<TY> &T) {
     constexpr int U = Q<TY>::U;
     const int gb = c0 + lane % LPR + LPR * U * j;
 #pragma unroll
     for (int u = 0; u < U; ++u)
-        if (gb + LPR * u < c1)
-            accumulate<TY, NT>(w[u], gb + LPR * u, xs + (gb + LPR * u - c0) * xs_stride(NT), acc, T);
+        if (gb + LPR * u < c1) {
+            const int gr = gb + LPR * u - c0;
+            if constexpr (gemv_fac<TY>())
+                accumulate<TY, NT, true>(w[u], gb + LPR * u, xs + gr * xs_stride(NT), acc, T, xsm + gr * NT * 2);
+            else
+                accumulate<TY, NT>(w[u], gb + LPR * u, xs + gr * xs_stride(NT), acc, T);
+        }
 }
 
 // end of a row-set: the row sums (every lane of a row gets them) stored by the row's first lane; accumulators reset
@@ -754,7 +825,7 @@ __device__ __forceinline__ void flush_rows(int s, int lane, int rows, float *acc
 template <uint32_t TY, int NT, int LPR>
 __device__ __forceinline__ void gemv_walk_short(const PP &P, int rows, int g0, int g1, int ng, int NS, int nws,
                                                 int NB, const float *__restrict__ x, int cols,
-                                                float *__restrict__ out, float4 *xs, int blk) {
+                                                float *__restrict__ out, float4 *xs, float *xsm, int blk) {
     constexpr int NW = Q<TY>::NW, U = Q<TY>::U, XB = NT <= 2 ? 4 : 8;
     const int tid = threadIdx.x, lane = tid & 63;
     // the wave's batches in order: (s, j), then (s1, j1) = next(s, j), ...; wave-uniform, so the row reductions run
@@ -781,20 +852,24 @@ __device__ __forceinline__ void gemv_walk_short(const PP &P, int rows, int g0, i
     __builtin_amdgcn_sched_barrier(0);
     xp.store(xs, ng, 0, tid, 512);
     __syncthreads();
+    if constexpr (gemv_fac<TY>()) {
+        x_half_sums<NT>(xs, ng, xsm, tid, 512);
+        lds_barrier();
+    }
     const TabT<TY> T;  // (IQ4 formats) the level table in registers, once; (IQ3_S) the grid in LDS
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
     // two batches in flight: while one is summed, the other (and then the one after it) is loading
     while (s < NS) {
-        acc_batch<TY, NT, LPR>(wa, j, lane, g0, g1, xs, acc, T);
+        acc_batch<TY, NT, LPR>(wa, j, lane, g0, g1, xs, xsm, acc, T);
         if (j == NB - 1) flush_rows<NT, LPR>(s, lane, rows, acc, out);
         s = s1;
         j = j1;
         next(s, j, s1, j1);
         if (s >= NS) break;
         if (s1 < NS) load_batch<TY, LPR>(P, rows, s1, j1, lane, g0, g1, wa);
-        acc_batch<TY, NT, LPR>(wb, j, lane, g0, g1, xs, acc, T);
+        acc_batch<TY, NT, LPR>(wb, j, lane, g0, g1, xs, xsm, acc, T);
         if (j == NB - 1) flush_rows<NT, LPR>(s, lane, rows, acc, out);
         s = s1;
         j = j1;
@@ -808,7 +883,7 @@ __device__ __forceinline__ void gemv_walk_short(const PP &P, int rows, int g0, i
 template <uint32_t TY, int NT, int LPR>
 __device__ __forceinline__ void gemv_walk_deep(const PP &P, int rows, int g0, int g1, int ng, int NS, int nws, int NB,
                                                const float *__restrict__ x, int cols, float *__restrict__ out,
-                                               float4 *xs) {
+                                               float4 *xs, float *xsm) {
     constexpr int NW = Q<TY>::NW, U = Q<TY>::U, XB = NT <= 2 ? 4 : 8;
     const int tid = threadIdx.x, lane = tid & 63;
     // The wave's batches: b = 0 .. n-1, batch b = groups batch b % NB of row-set w0 + (b / NB) * nws.  Everything
@@ -835,10 +910,14 @@ __device__ __forceinline__ void gemv_walk_deep(const PP &P, int rows, int g0, in
         xp.store(xs, ng, 0, tid, 512);
     }
     __syncthreads();
+    if constexpr (gemv_fac<TY>()) {
+        x_half_sums<NT>(xs, ng, xsm, tid, 512);
+        lds_barrier();
+    }
 #define FN_GEMV_LOAD(W, B) load_batch<TY, LPR>(P, rows, w0 + ((B) / NB) * nws, (B) % NB, lane, g0, g1, W)
 #define FN_GEMV_SUM(W, B)                                                                      \
     do {                                                                                       \
-        acc_batch<TY, NT, LPR>(W, (B) % NB, lane, g0, g1, xs, acc, T);                         \
+        acc_batch<TY, NT, LPR>(W, (B) % NB, lane, g0, g1, xs, xsm, acc, T);                    \
         if ((B) % NB == NB - 1) flush_rows<NT, LPR>(w0 + ((B) / NB) * nws, lane, rows, acc, out); \
     } while (0)
     // Steady state: two batches in flight while one is summed.  Every pass issues the same loads and the loop leaves
@@ -871,8 +950,9 @@ __global__ void __launch_bounds__(512) k_gemv(PP P, int rows, int G, int gps, co
     const int NB = (ng + LPR * U - 1) / (LPR * U);
     out += (size_t) blockIdx.y * NT * rows;
     tab_fill<TY>(threadIdx.x, 512);  // published by the walk's barrier after the x staging
-    if constexpr (DEEP) gemv_walk_deep<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs);
-    else gemv_walk_short<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs, blockIdx.x);
+    float *xsm = reinterpret_cast<float *>(xs + gps * xs_stride(NT));  // (gemv_fac formats) the x sums, after x
+    if constexpr (DEEP) gemv_walk_deep<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs, xsm);
+    else gemv_walk_short<TY, NT, LPR>(P, rows, g0, g1, ng, NS, nws, NB, x, cols, out, xs, xsm, blockIdx.x);
 }
 
 // k_gemv_c, for an x too large for the LDS: x goes through it in chunks of kc groups (a multiple of LPR, so a
@@ -890,6 +970,7 @@ __global__ void __launch_bounds__(512) k_gemv_c(PP P, int rows, int G, int gps, 
     const bool live = s < (rows + RPW - 1) / RPW;  // wave-uniform
     out += (size_t) blockIdx.y * NT * rows;
     tab_fill<TY>(tid, 512);  // published by the chunk loop's first barrier
+    float *xsm = reinterpret_cast<float *>(xs + kc * xs_stride(NT));  // (gemv_fac formats) the chunk's x sums
     const TabT<TY> T;
     float acc[NT];
 #pragma unroll
@@ -906,13 +987,17 @@ __global__ void __launch_bounds__(512) k_gemv_c(PP P, int rows, int G, int gps, 
         __builtin_amdgcn_sched_barrier(0);
         xp.store(xs, nch, 0, tid, 512);
         __syncthreads();
+        if constexpr (gemv_fac<TY>()) {
+            x_half_sums<NT>(xs, nch, xsm, tid, 512);
+            lds_barrier();
+        }
         if (!live) continue;
         for (int j = 0; j < NB; j += 2) {
             if (j + 1 < NB) load_batch<TY, LPR>(P, rows, s, j + 1, lane, c0, c1, wb);
-            acc_batch<TY, NT, LPR>(wa, j, lane, c0, c1, xs, acc, T);
+            acc_batch<TY, NT, LPR>(wa, j, lane, c0, c1, xs, xsm, acc, T);
             if (j + 1 >= NB) break;
             if (j + 2 < NB) load_batch<TY, LPR>(P, rows, s, j + 2, lane, c0, c1, wa);
-            acc_batch<TY, NT, LPR>(wb, j + 1, lane, c0, c1, xs, acc, T);
+            acc_batch<TY, NT, LPR>(wb, j + 1, lane, c0, c1, xs, xsm, acc, T);
         }
     }
     if (live) flush_rows<NT, LPR>(s, lane, rows, acc, out);
@@ -934,7 +1019,7 @@ template <uint32_t TY, int NT, int LPR>
 int gemv_nt(const QLayout &L, const GemvPlan &pl, const PP &P, const float *x, float *out, hipStream_t st) {
     const int gps = (pl.ngroups + pl.ks - 1) / pl.ks, ns = (L.rows + 64 / LPR - 1) / (64 / LPR);
     int nwg = (ns + 7) / 8;
-    constexpr int XS = xs_stride(NT) * (int) sizeof(float4);  // LDS bytes per group of x
+    constexpr int XS = xs_group_bytes<TY>(NT);  // LDS bytes per group of x (and its sums)
     constexpr int LDS = kLdsPerCu - tab_lds<TY>();            // what x may take beside the format's table
     if (gps <= LDS / XS && g_ov_kernel != 1) {
         static int by_regs = 0;  // workgroups per CU the registers allow (the deep walk's, the larger of the two)
@@ -993,10 +1078,11 @@ __device__ __forceinline__ void grp_walk(const GParts<N> &ps, int blk, int G, co
                                          float4 *xs) {
     if (blk < ps.p[I].nwg) {
         constexpr int U = Q<TY>::U, RPW = 64 / LPR;
+        static_assert(!gemv_fac<TY>(), "the grouped kernel stages no x sums");
         const GPart &p = ps.p[I];
         tab_fill<TY>(threadIdx.x, 512);  // published by the walk's barrier after the x staging
         gemv_walk_short<TY, NT, LPR>(p.P, p.rows, 0, G, G, (p.rows + RPW - 1) / RPW, p.nwg * 8,
-                                     (G + LPR * U - 1) / (LPR * U), x, cols, p.out, xs, blk);
+                                     (G + LPR * U - 1) / (LPR * U), x, cols, p.out, xs, nullptr, blk);
     } else if constexpr (sizeof...(R) > 0) {
         grp_walk<NT, LPR, I + 1, N, R...>(ps, blk - ps.p[I].nwg, G, x, cols, xs);
     }
