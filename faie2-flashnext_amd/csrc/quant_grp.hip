@@ -56,7 +56,12 @@ int gemv_group_launch(const GemvPart *parts, int n, const float *x, int nt, hipS
     // x of MAXNT tokens in the LDS beside the codebooks (IQ3_S: its grid and the sign masks, 4 KiB): sized for the
     // largest call, so that whether the parts share a launch never depends on nt (token t of an nt-token call keeps
     // the bits of a one-token call); the separate launches take no split-K, like the grouped one
-    const size_t xlds = (size_t) (parts[0].L->cols / 32) * xs_stride(MAXNT) * sizeof(float4);
+    // (and the half sums of x when a part's format has a minimum: Q6_K in kinds 1 and 2)
+    bool fac = false;
+    for (int s = 0; kind >= 0 && s < kKindN[kind]; ++s)
+        fac = fac || kKind[kind][s] == QT_Q4_K || kKind[kind][s] == QT_Q5_K || kKind[kind][s] == QT_Q6_K;
+    const size_t xlds = (size_t) (parts[0].L->cols / 32) *
+                        (xs_stride(MAXNT) * sizeof(float4) + (fac ? MAXNT * 2 * sizeof(float) : 0));
     if (kind < 0 || xlds + (size_t) tab_lds<QT_IQ3_S>() > (size_t) kLdsPerCu) {
         for (int i = 0; i < n; ++i)
             if (gemv_launch(*parts[i].L, parts[i].packed, x, nt, parts[i].y, nullptr, 0, st, 1)) return -1;

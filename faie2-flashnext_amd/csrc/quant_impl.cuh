@@ -375,11 +375,13 @@ template <> struct Q<QT_Q5_K> {
 
 // Q6_K: super-blocks of 256 (ql[128], qh[64], int8 scales[16], d fp16).  Value 128 n + 32 qu + l (n < 2, qu < 4,
 // l < 32): low 4 bits from nibble (qu >> 1) of ql[64 n + 32 (qu & 1) + l], high 2 bits from bits 2 qu of
-// qh[32 n + l], scale scales[8 n + 2 qu + l / 16] (ggml: y = d * sc * (q - 32))
+// qh[32 n + l], scale scales[8 n + 2 qu + l / 16] (ggml: y = d * sc * (q - 32)).  Decoded as q with the minimum
+// m = 32 s, so that the GEMV takes the factored form s (q.x) - 32 s (sum x) like the other formats with a minimum;
+// the GGUF value itself is s (q - 32) (gguf_value).
 template <> struct Q<QT_Q6_K> {
     static constexpr int NW = 18;
     static constexpr int U = prefetch_groups(NW);
-    static constexpr bool MIN = false;
+    static constexpr bool MIN = true;
     template <class R_> __device__ static void load(const R_ &R, int g, uint32_t *w) {
         const int ib = g & 7, n = ib >> 2, qu = ib & 3, sb = g >> 3;
         const uint8_t *l = R.b0 + 128 * sb + 64 * n + 32 * (qu & 1);
@@ -393,18 +395,21 @@ template <> struct Q<QT_Q6_K> {
         w[17] = ld2(t + 16);
     }
     __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
-        const int qu = g & 3, lsh = 4 * (qu >> 1), hsh = 2 * qu;
+        const int qu = g & 3, lsh = 4 * (qu >> 1);
+        const uint32_t rot = (uint32_t) (2 * qu + 28) & 31u;  // a right rotation by 2 qu - 4: bits 8k + 2qu, + 1 to 8k + 4, 5
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             // 4 six-bit codes per 32-bit operation (low nibble, then 2 high bits at bits 4-5 of each byte)
-            const uint32_t q = (((w[8 + i] >> hsh) & 0x03030303u) << 4) | ((w[i] >> lsh) & 0x0F0F0F0Fu);
+            const uint32_t hb = __builtin_amdgcn_alignbit(w[8 + i], w[8 + i], rot);
+            const uint32_t q = (hb & 0x30303030u) | ((w[i] >> lsh) & 0x0F0F0F0Fu);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) o.q[4 * i + k] = (float) ((q >> (8 * k)) & 0xFFu) - 32.0f;
+            for (int k = 0; k < 4; ++k) o.q[4 * i + k] = (float) ((q >> (8 * k)) & 0xFFu);
         }
         const float d = h2f(w[17]);
         o.s[0] = d * sbyte(w[16], 0);
         o.s[1] = d * sbyte(w[16], 1);
-        o.m[0] = o.m[1] = 0.0f;
+        o.m[0] = 32.0f * o.s[0];
+        o.m[1] = 32.0f * o.s[1];
     }
 };
 
@@ -584,6 +589,14 @@ template <> struct Q<QT_Q2_0> {
     }
 };
 
+// the GGUF value of code q (a decoded group's entry) in half h, rounded once as ggml's dequantisers round it:
+// fl(s q - m), or for Q6_K, whose minimum is 32 s, fl(s (q - 32)) (the same value, and the sign of a zero kept)
+template <uint32_t TY> __device__ __forceinline__ float gguf_value(const Grp &o, int h, float q) {
+    if constexpr (TY == QT_BF16) return q;
+    else if constexpr (TY == QT_Q6_K) return o.s[h] * (q - 32.0f);
+    else return __builtin_fmaf(o.s[h], q, -o.m[h]);
+}
+
 template <uint32_t TY> __device__ __forceinline__ void decode(const PP &P, int row, int g, Grp &o) {
     uint32_t w[Q<TY>::NW];
     const TabT<TY> T;
@@ -613,7 +626,7 @@ template <uint32_t TY> __global__ void k_dequant(PP P, int rows, int G, int cols
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const float q = o.q[4 * c + k];
-            v[k] = TY == QT_BF16 ? q : __builtin_fmaf(o.s[h], q, -o.m[h]);
+            v[k] = gguf_value<TY>(o, h, q);
         }
         dst[c] = make_float4(v[0], v[1], v[2], v[3]);
     }
@@ -643,7 +656,7 @@ __device__ __forceinline__ void accumulate(const uint32_t *w, int g, const float
         if constexpr (Q<TY>::MIN && !FAC) {
             float wv[16];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) wv[j] = __builtin_fmaf(o.s[h], o.q[16 * h + j], -o.m[h]);
+            for (int j = 0; j < 16; ++j) wv[j] = gguf_value<TY>(o, h, o.q[16 * h + j]);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 float a = acc[t];
@@ -1078,11 +1091,12 @@ __device__ __forceinline__ void grp_walk(const GParts<N> &ps, int blk, int G, co
                                          float4 *xs) {
     if (blk < ps.p[I].nwg) {
         constexpr int U = Q<TY>::U, RPW = 64 / LPR;
-        static_assert(!gemv_fac<TY>(), "the grouped kernel stages no x sums");
         const GPart &p = ps.p[I];
         tab_fill<TY>(threadIdx.x, 512);  // published by the walk's barrier after the x staging
+        // (gemv_fac formats) the x sums after the x groups; the launch sizes the LDS for them when a part needs them
+        float *xsm = reinterpret_cast<float *>(xs + G * xs_stride(NT));
         gemv_walk_short<TY, NT, LPR>(p.P, p.rows, 0, G, G, (p.rows + RPW - 1) / RPW, p.nwg * 8,
-                                     (G + LPR * U - 1) / (LPR * U), x, cols, p.out, xs, nullptr, blk);
+                                     (G + LPR * U - 1) / (LPR * U), x, cols, p.out, xs, xsm, blk);
     } else if constexpr (sizeof...(R) > 0) {
         grp_walk<NT, LPR, I + 1, N, R...>(ps, blk - ps.p[I].nwg, G, x, cols, xs);
     }
@@ -1102,7 +1116,9 @@ template <int NT, int LPR, uint32_t... TS>
 int gemv_grp_nt(const QLayout *const *L, const PP *P, float *const *y, const float *x, hipStream_t st) {
     constexpr int N = sizeof...(TS), RPW = 64 / LPR;
     const int G = L[0]->cols / 32;
-    const size_t lds = (size_t) G * xs_stride(NT) * sizeof(float4), tabs = (size_t) (tab_lds<TS>() + ...);
+    constexpr bool FAC = (gemv_fac<TS>() || ...);
+    const size_t lds = (size_t) G * (xs_stride(NT) * sizeof(float4) + (FAC ? NT * 2 * sizeof(float) : 0)),
+                 tabs = (size_t) (tab_lds<TS>() + ...);
     static int by_regs = 0;
     if (!by_regs) {
         int n = 0;
@@ -1228,7 +1244,7 @@ __global__ void __launch_bounds__(256) k_embed(PP P, int G, int cols, const int3
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const float q = o.q[4 * c + k];
-                e[k] = TY == QT_BF16 ? q : __builtin_fmaf(o.s[h], q, -o.m[h]);
+                e[k] = gguf_value<TY>(o, h, q);
             }
             v[c] = make_float4(e[0], e[1], e[2], e[3]);
         }
@@ -1276,7 +1292,7 @@ __global__ void __launch_bounds__(256) k_ngram_rows(PP P, int G, int cols, Ngram
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const float q = o.q[4 * v + k];
-                e[k] = TY == QT_BF16 ? q : __builtin_fmaf(o.s[v >> 2], q, -o.m[v >> 2]);
+                e[k] = gguf_value<TY>(o, v >> 2, q);
             }
             dst[v] = make_float4(e[0], e[1], e[2], e[3]);
         }
