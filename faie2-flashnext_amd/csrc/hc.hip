@@ -117,7 +117,7 @@ __global__ void __launch_bounds__(256) k_hc_down(const float *__restrict__ h, co
         }
     }
     lds_barrier();
-    const Iq4Tab T;
+    const NoTab T;
 #pragma unroll
     for (int j = 0; j < HC_RW; ++j) {
         const int r = r0 + j;

@@ -7,6 +7,7 @@
 #include "quant.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace fn {
 
@@ -30,31 +31,36 @@ constexpr uint32_t pack4(int k) {
 constexpr uint32_t KV0 = pack4(0), KV1 = pack4(1), KV2 = pack4(2), KV3 = pack4(3);
 static_assert(KV0 == 0xBFAD9881u && KV3 == 0x71594535u, "IQ4 level packing");
 
-// a constant held in a VGPR the compiler cannot see through: gfx9 VOP3 encodings take no literal, so a VOP3 op
-// such as v_and_or_b32 with two 32-bit constants is only emitted when they sit in registers
-__device__ __forceinline__ uint32_t vconst(uint32_t c) {
-    uint32_t r;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
-    return r;
+// the lookup state of the formats that decode without a table
+struct NoTab {};
+
+// The IQ4 levels (IQ4_NL, IQ4_XS) as 16 floats in LDS, copied once per workgroup (tab_fill): a value's lookup is one
+// LDS read at its index's byte offset, with no conversion after it.  The 16 words sit in 16 distinct banks, so the
+// lanes of a read never conflict (equal indices are broadcast).  (Before: three v_perm_b32 lookups in the signed
+// level bytes held in registers, two shifts, two and-ors per four values, then a signed-byte conversion each.)
+__device__ __forceinline__ float *iq4_lds() {
+    __shared__ float lev[16];
+    return lev;
 }
-
-struct Iq4Tab {
-    uint32_t kv0, kv1, kv2, kv3, m7, m4, sel0;
-    __device__ __forceinline__ Iq4Tab()
-        : kv0(vconst(KV0)), kv1(vconst(KV1)), kv2(vconst(KV2)), kv3(vconst(KV3)), m7(vconst(0x07070707u)),
-          m4(vconst(0x04040404u)), sel0(vconst(0x03020100u)) {}
+struct Iq4LdsTab {
+    const float *lev;
+    __device__ __forceinline__ Iq4LdsTab() : lev(iq4_lds()) {}
+    // the level of the index held at byte offset off (4 x index) of the table
+    __device__ __forceinline__ float at(uint32_t off) const {
+        return *reinterpret_cast<const float *>(reinterpret_cast<const char *>(lev) + off);
+    }
 };
-
-// four nibble indices -> their four signed levels as bytes.  v_perm_b32 picks bytes out of an 8-byte pair by
-// selector 0..7, so levels 0..7 and 8..15 are looked up separately with the low 3 bits and the index's bit 3 then
-// chooses between the two results byte by byte.  The indices are the nibbles of w at bit offset SH (0: low nibbles,
-// 4: high nibbles): 3 perms, 2 shifts and 2 and-ors per four levels.
-template <int SH> __device__ __forceinline__ uint32_t iq4_levels(uint32_t w, const Iq4Tab &T) {
-    const uint32_t s = (w >> SH) & T.m7;
-    const uint32_t lo = __builtin_amdgcn_perm(T.kv1, T.kv0, s);
-    const uint32_t hi = __builtin_amdgcn_perm(T.kv3, T.kv2, s);
-    const uint32_t sel = ((w >> (SH + 1)) & T.m4) | T.sel0;
-    return __builtin_amdgcn_perm(hi, lo, sel);
+template <uint32_t TY> constexpr bool iq4_fmt() { return TY == QT_IQ4_NL || TY == QT_IQ4_XS; }
+// byte K of x, zero-extended, in one instruction (the compiler splits a constant-mask field extract into a shift and
+// an and; bytes 1 and 2 go through v_bfe_u32 as written)
+template <int K> __device__ __forceinline__ uint32_t byte_of(uint32_t x) {
+    if constexpr (K == 0) return x & 0xFFu;
+    else if constexpr (K == 3) return x >> 24;
+    else {
+        uint32_t r;
+        asm("v_bfe_u32 %0, %1, %2, 8" : "=v"(r) : "v"(x), "i"(8 * K));
+        return r;
+    }
 }
 
 // Codebooks of the grid formats (GGUF's iq3s_grid, iq3xxs_grid, iq2xxs_grid, iq2xs_grid, iq2s_grid; 8-byte entries as
@@ -126,16 +132,26 @@ template <uint32_t TY> struct GridTab {
     __device__ __forceinline__ GridTab() : grid(grid_lds<TY>()), sgn(sign_lds()) {}
 };
 
-// per-format lookup state held by a decoding lane: the IQ4 levels in registers, or the grid codebook in LDS
-template <uint32_t TY, bool G = (GridOf<TY>::words > 0)> struct TabOf { using type = Iq4Tab; };
+// per-format lookup state held by a decoding lane: the IQ4 levels or the grid codebook in LDS (none for the other
+// formats)
+template <uint32_t TY, bool G = (GridOf<TY>::words > 0)> struct TabOf {
+    using type = typename std::conditional<iq4_fmt<TY>(), Iq4LdsTab, NoTab>::type;
+};
 template <uint32_t TY> struct TabOf<TY, true> { using type = GridTab<TY>; };
 template <uint32_t TY> using TabT = typename TabOf<TY>::type;
 
 // LDS the format's table takes in a GEMV / dequant workgroup, and its fill by the workgroup's nth threads (the
 // caller's next barrier publishes it)
-template <uint32_t TY> constexpr int tab_lds() { return GridOf<TY>::words > 0 ? GridOf<TY>::words * 4 + 2048 : 0; }
+template <uint32_t TY> constexpr int tab_lds() {
+    return GridOf<TY>::words > 0 ? GridOf<TY>::words * 4 + 2048 : (iq4_fmt<TY>() ? 64 : 0);
+}
 template <uint32_t TY> __device__ __forceinline__ void tab_fill(int tid, int nth) {
-    if constexpr (GridOf<TY>::words > 0) {
+    if constexpr (iq4_fmt<TY>()) {
+        if (tid < 16) {
+            const uint32_t kw = tid < 4 ? KV0 : (tid < 8 ? KV1 : (tid < 12 ? KV2 : KV3));
+            iq4_lds()[tid] = (float) (int8_t) (kw >> (8 * (tid & 3)));
+        }
+    } else if constexpr (GridOf<TY>::words > 0) {
         uint32_t *g = grid_lds<TY>(), *sg = sign_lds();
         const uint32_t *src = grid_src<TY>();
         for (int i = tid; i < GridOf<TY>::words; i += nth) g[i] = src[i];
@@ -220,7 +236,7 @@ template <> struct Q<QT_BF16> {
 #pragma unroll
         for (int i = 0; i < 4; ++i) ld16(p + 16 * i, w + 4 * i);
     }
-    __device__ static void unpack(const uint32_t *w, int, Grp &o, const Iq4Tab &T) {
+    __device__ static void unpack(const uint32_t *w, int, Grp &o, const NoTab &T) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             o.q[2 * i] = __uint_as_float(w[i] << 16);
@@ -242,7 +258,7 @@ template <> struct Q<QT_Q8_0> {
         ld16(q + 16, w + 4);
         w[8] = ld2(R.b1 + 2 * g);
     }
-    __device__ static void unpack(const uint32_t *w, int, Grp &o, const Iq4Tab &T) {
+    __device__ static void unpack(const uint32_t *w, int, Grp &o, const NoTab &T) {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -262,18 +278,22 @@ template <> struct Q<QT_IQ4_NL> {
         ld16(R.b0 + 16 * g, w);
         w[4] = ld2(R.b1 + 2 * g);
     }
-    __device__ static void levels(const uint32_t *w, Grp &o, const Iq4Tab &T) {
+    __device__ static void levels(const uint32_t *w, Grp &o, const Iq4LdsTab &T) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = iq4_levels<0>(w[i], T), hi = iq4_levels<4>(w[i], T);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                o.q[4 * i + k] = sbyte(lo, k);
-                o.q[16 + 4 * i + k] = sbyte(hi, k);
-            }
+            // 4 x the index of each value in its byte (low nibbles, then high): a byte is the table offset
+            const uint32_t lo = (w[i] << 2) & 0x3C3C3C3Cu, hi = (w[i] >> 2) & 0x3C3C3C3Cu;
+            o.q[4 * i] = T.at(byte_of<0>(lo));
+            o.q[4 * i + 1] = T.at(byte_of<1>(lo));
+            o.q[4 * i + 2] = T.at(byte_of<2>(lo));
+            o.q[4 * i + 3] = T.at(byte_of<3>(lo));
+            o.q[16 + 4 * i] = T.at(byte_of<0>(hi));
+            o.q[16 + 4 * i + 1] = T.at(byte_of<1>(hi));
+            o.q[16 + 4 * i + 2] = T.at(byte_of<2>(hi));
+            o.q[16 + 4 * i + 3] = T.at(byte_of<3>(hi));
         }
     }
-    __device__ static void unpack(const uint32_t *w, int, Grp &o, const Iq4Tab &T) {
+    __device__ static void unpack(const uint32_t *w, int, Grp &o, const Iq4LdsTab &T) {
         levels(w, o, T);
         o.s[0] = o.s[1] = h2f(w[4]);
         o.m[0] = o.m[1] = 0.0f;
@@ -290,7 +310,7 @@ template <> struct Q<QT_IQ4_XS> {
         ld16(R.b0 + 16 * g, w);  // super-block g / 8 at 128 (g / 8), group g % 8 at 16 (g % 8) inside it
         ld8(R.b1 + 8 * (g >> 3), w + 4);
     }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4LdsTab &T) {
         const int ib = g & 7;
         Q<QT_IQ4_NL>::levels(w, o, T);
         const uint32_t sl = (w[5] >> (8 * (ib >> 1))) >> (4 * (ib & 1)) & 0xFu;
@@ -326,7 +346,7 @@ template <> struct Q<QT_Q4_K> {
         ld16(q + 16, w + 4);
         ld16(R.b1 + 16 * (g >> 3), w + 8);
     }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const NoTab &T) {
         const int ib = g & 7, sh = 4 * (ib & 1);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -355,7 +375,7 @@ template <> struct Q<QT_Q5_K> {
         ld16(h + 16, w + 12);
         ld16(R.b2 + 16 * (g >> 3), w + 16);
     }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const NoTab &T) {
         const int ib = g & 7, sh = 4 * (ib & 1);
         const uint32_t rot = (uint32_t) (ib + 28) & 31u;  // a right rotation by ib - 4 takes bit 8k + ib to 8k + 4
 #pragma unroll
@@ -394,7 +414,7 @@ template <> struct Q<QT_Q6_K> {
         w[16] = ld2(t + 8 * n + 2 * qu);
         w[17] = ld2(t + 16);
     }
-    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const Iq4Tab &T) {
+    __device__ static void unpack(const uint32_t *w, int g, Grp &o, const NoTab &T) {
         const int qu = g & 3, lsh = 4 * (qu >> 1);
         const uint32_t rot = (uint32_t) (2 * qu + 28) & 31u;  // a right rotation by 2 qu - 4: bits 8k + 2qu, + 1 to 8k + 4, 5
 #pragma unroll
@@ -581,7 +601,7 @@ template <> struct Q<QT_Q2_0> {
         ld8(R.b0 + 8 * g, w);
         w[2] = ld2(R.b1 + 2 * (g >> 1));
     }
-    __device__ static void unpack(const uint32_t *w, int, Grp &o, const Iq4Tab &T) {
+    __device__ static void unpack(const uint32_t *w, int, Grp &o, const NoTab &T) {
 #pragma unroll
         for (int v = 0; v < 32; ++v) o.q[v] = (float) ((int) ((w[v >> 4] >> (2 * (v & 15))) & 3u) - 1);
         o.s[0] = o.s[1] = h2f(w[2]);
@@ -869,7 +889,7 @@ __device__ __forceinline__ void gemv_walk_short(const PP &P, int rows, int g0, i
         x_half_sums<NT>(xs, ng, xsm, tid, 512);
         lds_barrier();
     }
-    const TabT<TY> T;  // (IQ4 formats) the level table in registers, once; (IQ3_S) the grid in LDS
+    const TabT<TY> T;  // (IQ4 formats) the level table, (grid formats) the codebook, both in LDS
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
@@ -904,7 +924,7 @@ __device__ __forceinline__ void gemv_walk_deep(const PP &P, int rows, int g0, in
     const int w0 = blockIdx.x * 8 + __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = w0 < NS ? ((NS - 1 - w0) / nws + 1) * NB : 0;
     uint32_t wa[U][NW], wb[U][NW];
-    const TabT<TY> T;  // (IQ4 formats) the level table in registers, once; (IQ3_S) the grid in LDS
+    const TabT<TY> T;  // (IQ4 formats) the level table, (grid formats) the codebook, both in LDS
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
