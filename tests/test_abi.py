@@ -261,6 +261,18 @@ def test_gemv_group_refuses_bad_arguments(fnlib):
     assert b"null part" in d.fn_error()
     assert d.fn_gemv_group_dev(2, ty, rows, 2560, fake, 4096, 9, fake, None) == -1
     assert b"nt must be" in d.fn_error()
+    # a plane past 4 GiB (the GEMV kernels address planes with 32-bit offsets) is refused before any launch
+    big = (C.c_int * 2)(64, 1100000)  # BF16, 4096 bytes a row: 4.5 GB
+    assert d.fn_gemv_group_dev(2, ty, big, 2048, fake, 4096, 1, fake, None) == -1
+    assert b"exceeds 4 GiB" in d.fn_error()
+
+
+def test_gemv_refuses_planes_past_4gib(fnlib):
+    """fn_gemv_dev refuses a weight with a plane over 4 GiB before any launch (the GEMV kernels address each plane
+    with 32-bit offsets)."""
+    d = fnlib.d
+    assert d.fn_gemv_dev(30, 4096, 1100000, 2048, 4096, 1, 8192, None, 0, None) == -1  # BF16 rows of 4096 B: 4.5 GB
+    assert b"exceeds 4 GiB" in d.fn_error()
 
 
 def test_bench_route_refuses_bad_arguments(fnlib):
