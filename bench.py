@@ -509,11 +509,13 @@ def b64_extras(lib, stream, steps, warmup):
     return res
 
 
-def model_decode(lib, nl=8, ctx=4096, tokens=64, seed=0, nts=(1, 8)):
+def model_decode(lib, nl=8, ctx=4096, tokens=64, seed=0, nts=(1, 8), moe_sweep=()):
     """fn_load + fn_forward on a synthetic model of the reference model's dimensions and weight formats with nl layers
     (PLE at layer 1; the n-gram table's head sizes 1/100 of the reference's, which changes only the table's size:
     16 rows are gathered per token either way).  Greedy-decode latency per fn_forward call (tokens in, argmax out,
-    host-synchronous, as the reference's 5.70 ms per forward is quoted) at nt = 1 and nt = 8, after a warm-up."""
+    host-synchronous, as the reference's 5.70 ms per forward is quoted) at nt = 1 and nt = 8, after a warm-up.
+    moe_sweep: dn_wpt values of fn_moe_override to time afterwards (1 = the 16-row MoE output kernel, 4 = the
+    4-row one), each checked for the same argmax tokens."""
     import model_synth as ms
     dims = dict(ms.REFERENCE_DIMS, NL=nl, ple_sizes=[v // 100 for v in ms.REFERENCE_DIMS["ple_sizes"]])
     d = "/dev/shm" if os.path.isdir("/dev/shm") else os.environ.get("TMPDIR", "/tmp")
@@ -552,23 +554,39 @@ def model_decode(lib, nl=8, ctx=4096, tokens=64, seed=0, nts=(1, 8)):
     ids = rng.integers(0, R["VOCAB"], size=tokens + 8 * tokens).astype(np.int32)
     out = {"layers": nl, "ctx": ctx, "weight_gb_on_device": round(lib.d.fn_dev_gb(0), 2),
            "bytes_per_token_nt1": per_token}
+    def timed(nt, tag=""):
+        lib.reset()
+        for i in range(4):                                     # warm-up: captures the graph for nt
+            lib.forward(ids[i * nt:(i + 1) * nt])
+        lib.reset()
+        calls = tokens // nt if nt > 1 else tokens
+        am = []
+        t1 = time.perf_counter()
+        for i in range(calls):
+            am.append(lib.forward(ids[i * nt:(i + 1) * nt]))
+        ms_call = (time.perf_counter() - t1) * 1e3 / calls
+        log(f"[bench] model{tag} nt={nt}: {ms_call:.3f} ms per forward, {nt * 1e3 / ms_call:.1f} tokens/s")
+        return {"ms_per_forward": round(ms_call, 4), "tokens_per_s": round(nt * 1e3 / ms_call, 1),
+                "us_per_layer": round(ms_call * 1e3 / nl, 2)}, np.concatenate(am)
+
     try:
+        base = {}
         for nt in nts:
-            lib.reset()
-            for i in range(4):                                     # warm-up: captures the graph for nt
-                lib.forward(ids[i * nt:(i + 1) * nt])
-            lib.reset()
-            t1 = time.perf_counter()
-            for i in range(tokens // nt if nt > 1 else tokens):
-                lib.forward(ids[i * nt:(i + 1) * nt])
-            calls = tokens // nt if nt > 1 else tokens
-            ms_call = (time.perf_counter() - t1) * 1e3 / calls
-            out[f"nt{nt}"] = {"ms_per_forward": round(ms_call, 4), "tokens_per_s": round(nt * 1e3 / ms_call, 1),
-                              "us_per_layer": round(ms_call * 1e3 / nl, 2)}
-            log(f"[bench] model nt={nt}: {ms_call:.3f} ms per forward, {nt * 1e3 / ms_call:.1f} tokens/s")
+            out[f"nt{nt}"], base[nt] = timed(nt)
         if "nt1" in out:
             out["nt1"]["gbs"] = round(per_token / (out["nt1"]["ms_per_forward"] * 1e-3) / 1e9, 1)
+        # the MoE output kernel forced either way (fn_moe_override's dn_wpt, as the reference's tune_moe_fn.py
+        # sweeps it): the same argmax tokens are required
+        for w in moe_sweep:
+            lib.moe_override(w)
+            lib.use_graphs(True)
+            for nt in nts:
+                res, am = timed(nt, f" dn_wpt={w}")
+                res["same_tokens"] = bool(np.array_equal(am, base[nt]))
+                out.setdefault(f"moe_dn_wpt{w}", {})[f"nt{nt}"] = res
     finally:
+        if moe_sweep:
+            lib.moe_override(-1)
         lib.free()
     return out
 
@@ -745,6 +763,9 @@ def main():
                          "reference's dimensions and formats with LAYERS layers")
     ap.add_argument("--model-nt", type=int, default=0, choices=(0, 1, 8),
                     help="with --model: time only calls of this many tokens (0: both 1 and 8)")
+    ap.add_argument("--model-moe", action="store_true",
+                    help="with --model: also time the forward with the MoE output kernel forced to 16 and to 4 rows a "
+                         "workgroup (fn_moe_override's dn_wpt 1 and 4) and check the argmax tokens are the same")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the whole-model leg of the extra legs (48 layers, ~47 GB written to /dev/shm and loaded)")
     ap.add_argument("--mt-only", action="store_true",
@@ -769,7 +790,8 @@ def main():
     stream = hiprt.Stream()
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     if args.model:
-        res = model_decode(lib, nl=args.model, nts=(args.model_nt,) if args.model_nt else (1, 8))
+        res = model_decode(lib, nl=args.model, nts=(args.model_nt,) if args.model_nt else (1, 8),
+                           moe_sweep=(1, 4) if args.model_moe else ())
         print(json.dumps({"model_decode": res}), flush=True)
         return
     if args.stages:

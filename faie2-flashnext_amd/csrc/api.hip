@@ -6,6 +6,7 @@
 // the reference's unit-test-hook style, faie2fn.cu:2745) and the device-buffer entry points an engine calls.
 #include "engine.h"
 #include "model.h"
+#include "quant.h"
 #include "qsa.h"
 #include "hostbuf.h"
 
@@ -56,15 +57,21 @@ FN_API int fn_forward(const int32_t *tokens, int nt, float *logits, int32_t *arg
     return fn::model_forward(tokens, nt, logits, argmax);
 }
 FN_API int fn_debug_layers(float *out) { return fn::model_debug_layers(out); }
-// The reference's A/B switches for its CUDA forward, accepted so that its scripts bind and run; none changes what
-// this library launches.  fn_pdl / fn_early: programmatic dependent launch, and GEMVs started beside the kernel
-// before them under it, have no HIP counterpart (the forward is one hipGraph on one stream; graph branches for the
-// independent GEMVs measured slower).  fn_moe_var / fn_moe_override: tile shapes of the reference's expert kernels;
-// the expert kernels here have one shape each.
+// The reference's A/B switches for its CUDA forward, accepted so that its scripts bind and run; these three change
+// nothing here.  fn_pdl / fn_early: programmatic dependent launch, and GEMVs started beside the kernel before them
+// under it, have no HIP counterpart (the forward is one hipGraph on one stream; graph branches for the independent
+// GEMVs measured slower).  fn_moe_var: the variant of the reference's expert gate/up tiles; the gate/up kernel here
+// has one shape (16 lanes a row, 8 rows a workgroup).
 FN_API void fn_pdl(int) {}
 FN_API void fn_early(int) {}
 FN_API void fn_moe_var(int) {}
-FN_API void fn_moe_override(int, int, int, int) {}
+// The reference's expert launch shapes (gate/up and down: warps splitting a tile's columns, tiles a block).  dn_wpt
+// picks the MoE output kernel by the waves that share one output row: 1 = the 16-row kernel (one wave sums whole
+// rows), 2 or more = the 4-row kernel (four waves split each row's items); 0 leaves it, as in the reference, and a
+// negative value returns to the automatic choice (not in the reference, which ignores it).  Either kernel gives
+// the same bits; a graph captured before keeps its kernel (fn_use_graphs drops the graphs).  gu_wpt, gu_tb, dn_tb:
+// no effect (one gate/up shape; rows a workgroup follow from the kernel).
+FN_API void fn_moe_override(int, int, int dn_wpt, int) { fn::moe_down_override(dn_wpt); }
 
 FN_API int fn_model_dims(const char *path, int *out, int n) {
     fn::ModelDims d;

@@ -153,5 +153,10 @@ bool moe_down_supported(const QLayout &Le, const QLayout &Ls, int R, int NEU);
 int moe_down_launch(const QLayout &Le, const uint8_t *pe, const QLayout &Ls, const uint8_t *ps, int R,
                     const int32_t *sel, const float *wsel, int NEU, const float *act, const float *sha, const float *rsg,
                     int NE, int nt, float *y, hipStream_t st);
+// benchmarking: the waves that share one output row of moe_down_launch.  1: the 16-row kernel (a wave takes 4 rows
+// and every item of the token); 2 or more: the 4-row kernel (4 waves split the items of each row); 0: unchanged;
+// negative: automatic (4 rows a workgroup for one token, 16 for several).  Either kernel gives the same bits.
+// Launches read it when they are made (a captured graph keeps the kernel it was captured with).
+void moe_down_override(int waves_per_row);
 
 }  // namespace fn

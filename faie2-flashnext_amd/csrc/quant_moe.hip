@@ -206,14 +206,17 @@ __global__ void __launch_bounds__(256) k_moe_down16(PP Pe, PP Ps, int R, int nex
         y[(size_t) t * R + r] = __builtin_fmaf(sigmoidf_(rsg[(size_t) t * (NE + 1) + NE]), d, m);
 }
 
+// the kernel forced by moe_down_override: 0 automatic, 1 the 16-row kernel, 4 the 4-row kernel
+int g_moe_down_waves = 0;
+
 template <uint32_t TY, uint32_t TS>
 int moe_down_t(const QLayout &Le, const PP &Pe, const QLayout &Ls, const PP &Ps, int R, const int32_t *sel,
                const float *wsel, int NEU, const float *act, const float *sha, const float *rsg, int NE, int nt,
                float *y, hipStream_t st) {
     const int G = Le.cols / 32;
     const size_t xl = (size_t) (NEU + 1) * G * 9 * sizeof(float4);
-    if (nt == 1)
-        hipLaunchKernelGGL((k_moe_down4<TY, TS>), dim3((unsigned) ((R + 3) / 4), 1u), dim3(256),
+    if (g_moe_down_waves == 4 || (g_moe_down_waves == 0 && nt == 1))
+        hipLaunchKernelGGL((k_moe_down4<TY, TS>), dim3((unsigned) ((R + 3) / 4), (unsigned) nt), dim3(256),
                            xl + (size_t) (NEU + 1) * 5 * sizeof(float), st, Pe, Ps, R, Le.rows / R, G, Le.cols, sel,
                            wsel, NEU, act, sha, rsg, NE, y);
     else
@@ -224,6 +227,10 @@ int moe_down_t(const QLayout &Le, const PP &Pe, const QLayout &Ls, const PP &Ps,
 }
 
 }  // namespace
+
+void moe_down_override(int waves_per_row) {
+    g_moe_down_waves = waves_per_row < 0 ? 0 : (waves_per_row == 1 ? 1 : (waves_per_row > 1 ? 4 : g_moe_down_waves));
+}
 
 bool moe_down_supported(const QLayout &Le, const QLayout &Ls, int R, int NEU) {
     const int G = Le.cols / 32;

@@ -232,6 +232,12 @@ class FN:
         wpt = int(lpr) // 16 if int(lpr) in (16, 32, 64) else (5 if lpr else 0)  # 5: an invalid split (ignored)
         self.d.fn_gemv_override(wpt, int(ks), int(kernel), int(waves_per_cu))
 
+    def moe_override(self, waves_per_row=-1):
+        """Force the MoE output kernel by the waves that share one output row (the reference's dn_wpt): 1 = 16 rows
+        a workgroup, 2 or more = 4 rows a workgroup; negative = automatic.  Graphs captured before keep their kernel
+        (use_graphs drops them)."""
+        self.d.fn_moe_override(0, 0, int(waves_per_row), 0)
+
     def bench_hot(self, on):
         self.d.fn_bench_hot(1 if on else 0)
 

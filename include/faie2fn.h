@@ -60,11 +60,15 @@ void fn_gemv_override(int wpt, int ks, int tb, int warps_per_sm);             /*
  * reports the choice for plans made afterwards. */
 void fn_gemv_waves(int waves);                                                /* faie2fn.cu:2793 */
 /* The reference's A/B switches for its CUDA forward (programmatic dependent launch, GEMVs started early under it,
- * the expert kernels' tile shapes): accepted so that its scripts bind and run, no effect here (no HIP counterpart;
- * one hipGraph per token count on one stream; one shape per expert kernel). */
+ * the gate/up tile variant): accepted so that its scripts bind and run, no effect here (no HIP counterpart; one
+ * hipGraph per token count on one stream; one gate/up shape). */
 void fn_pdl(int on);                                                          /* faie2fn.cu:2796 */
 void fn_early(int on);                                                        /* faie2fn.cu:2798 */
 void fn_moe_var(int v);                                                       /* faie2fn.cu:2799 */
+/* The expert launch shapes.  dn_wpt picks the MoE output kernel by the waves that share one output row: 1 = 16 rows
+ * a workgroup (one wave sums whole rows), 2 or more = 4 rows a workgroup (four waves split each row's items), 0 =
+ * unchanged, negative = automatic (4 rows for one token, 16 for several; an extension: the reference ignores values
+ * <= 0).  Same bits either way; graphs captured before keep their kernel.  gu_wpt, gu_tb, dn_tb: no effect. */
 void fn_moe_override(int gu_wpt, int gu_tb, int dn_wpt, int dn_tb);           /* faie2fn.cu:2801 */
 /* Launch plan of a rows x cols weight in the reference's 7 slots {cv, wpt, ks, tb, nbuf, ntiles, nch}:
  * out = {values per group (32), 16-lane groups per row (wpt, as fn_gemv_override takes it), split-K workgroups per

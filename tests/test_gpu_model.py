@@ -307,3 +307,35 @@ def test_model_expert_counts(fnlib, tmp_path, ne, neu):
             i += nt
     finally:
         fnlib.free()
+
+
+@pytest.mark.parametrize("ne,neu", [(24, 10), (40, 17)])
+def test_model_moe_override_same_bits(fnlib, tmp_path, ne, neu):
+    """fn_moe_override's dn_wpt picks the MoE output kernel: 1 runs the 16-row kernel for one-token calls too, 4 the
+    4-row kernel for several-token calls too (grid rows x tokens).  Both give the automatic choice's bits, through
+    the graphs captured after the override (fn_use_graphs drops the earlier ones) and eagerly; 17 experts a token
+    take the 4-row kernel's items in two passes."""
+    dims = dict(ms.TINY_DIMS, NE=ne, NEU=neu)
+    p = str(tmp_path / "moe.gguf")
+    ms.write_model(p, dims, seed=17)
+    ids = np.random.default_rng(8).integers(0, dims["VOCAB"], size=12)
+
+    def run():
+        fnlib.reset()
+        out, i = [], 0
+        for nt in (1, 8, 3):
+            out.append(fnlib.forward(ids[i:i + nt], logits=True)[1])
+            i += nt
+        return np.concatenate(out)
+
+    fnlib.load(p, "", max_ctx=256)
+    try:
+        base = run()
+        for w, graphs in ((1, True), (4, True), (1, False), (4, False)):
+            _say(f"model forward: {neu} experts a token, fn_moe_override dn_wpt={w}, graphs {graphs}")
+            fnlib.moe_override(w)
+            fnlib.use_graphs(graphs)
+            assert np.array_equal(run(), base), (neu, w, graphs)
+    finally:
+        fnlib.moe_override(-1)
+        fnlib.free()
