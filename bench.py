@@ -384,7 +384,8 @@ def stage_split(lib, stream, stack, names, reps=24):
     return out
 
 
-QSA_STAGES = ("k_ix_prep", "k_ix_score", "k_ix_select", "k_attn_split_list", "k_attn_combine")
+# (one-token calls: the index query prep runs inside the scoring launch)
+QSA_STAGES = ("k_ix_score_prep", "k_ix_select", "k_attn_split_list", "k_attn_combine")
 DENSE_STAGES = ("k_attn_split", "k_attn_combine")
 
 

@@ -4,7 +4,8 @@
 //                call completes get their block key rope(rmsnorm(mean of 4 raw keys) * wkn) at the block start
 //   k_ix_blocks  the same block keys over a range of blocks (prefill / rebuilding a cache)
 //   k_ix_score   score(block j) = sum over the 4 heads of relu(q_h . BK_j) / sqrt(128); lane = block over a
-//                block-tiled key store, so each wave load is one coalesced 1 KiB row of 64 blocks
+//                block-tiled key store, so each wave load is one coalesced 1 KiB row of 64 blocks.  For one-token
+//                calls k_ix_prep's work runs inside it (k_ix_score<true>), one dependent launch fewer
 //   k_ix_select  the top `top` blocks by score, ties at the threshold kept lowest index first, by a 3-pass radix
 //                select on the score bits in LDS histograms (the reference binary-searches 32 bit-passes); it emits
 //                the sorted list of visible keys (kept blocks, then the incomplete tail) that the attention split
@@ -127,30 +128,94 @@ __global__ void __launch_bounds__(256) k_ix_blocks(const IxArgs a) {
 // grid (B nt, G), 256 threads.  Workgroup y takes tiles y, y + G, ... of 64 blocks; lane = block, and wave w loads
 // dims 32w .. 32w+31 of the tile (8 coalesced 1 KiB rows), so one tile is 4 waves' loads in flight at once.  The
 // four waves' partial head dots meet in LDS; wave 0 applies the relu per head and stores the tile's 64 scores.
+// PREP (one-token calls, nt = 1): k_ix_prep's work rides in this launch.  Every workgroup of a query normalises and
+// ropes the 4 index q heads itself (wave h = head h, as k_ix_prep), with its first tile's loads already in flight;
+// workgroup 0 appends the raw index key; when the new key completes block jn, the workgroup owning jn's tile
+// (y = (jn / 64) % G) builds the block key from the 3 cached raw keys and the new one (the same arithmetic as
+// block_key), stores it, and scores block jn from its own copy: no workgroup reads a block key this launch writes.
+// Both happen before the dense test, so a dense query's caches are kept up to date.  Same bits as k_ix_prep followed
+// by the plain kernel.
+template <bool PREP>
 __global__ void __launch_bounds__(256) k_ix_score(const IxArgs a) {
     constexpr int CW = IXD / 4 / 4;  // float4 chunks per wave
     __shared__ float4 qs[IXD / 4][IXH];
     __shared__ float part[2][4][IXH][BT];
+    __shared__ float buf[PREP ? 4 : 1][IXD];  // PREP: the waves' RoPE rows; row 0 then holds the new block key
     const int bt = blockIdx.x, b = bt / a.nt, t = bt - b * a.nt;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nb = min(a.pos[b] + t + 1, a.max_ctx) / IXR;
-    if (nb <= a.top) return;  // dense: nothing to select
+    const int P = a.pos[b] + t;
+    const int nb = min(P + 1, a.max_ctx) / IXR;
     const int ntiles = (nb + BT - 1) / BT;
     int tile = blockIdx.y;
-    if (tile >= ntiles) return;
+    const bool live = nb > a.top && tile < ntiles;  // sparse query, and this workgroup has tiles
+    // PREP: the head's query row, the new raw key and the 3 cached raw keys of the block the new key would complete
+    // requested first (unconditional, clamped), so that the query's norm and RoPE wait for them and not for the tile
+    float2 x, nk, rk[IXR - 1];
+    if constexpr (PREP) {
+        const float *row = a.iqk + (size_t) bt * (IXH * IXD + IXD);
+        x = reinterpret_cast<const float2 *>(row + wave * IXD)[lane];
+        nk = reinterpret_cast<const float2 *>(row + IXH * IXD)[lane];
+        const int pc = min(max(P, 0), a.max_ctx - 1);
+        const float *k = a.IKc + ((size_t) b * a.max_ctx + (size_t) (pc / IXR) * IXR) * IXD;
+#pragma unroll
+        for (int e = 0; e < IXR - 1; ++e) rk[e] = reinterpret_cast<const float2 *>(k + e * IXD)[lane];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     const float4 *Bb = reinterpret_cast<const float4 *>(a.BKc) +
                        ((size_t) b * (a.max_ctx / IXR / BT) * (IXD / 4) + wave * CW) * BT + lane;
     float4 kf[CW];
+    if (live) {
 #pragma unroll
-    for (int c = 0; c < CW; ++c) kf[c] = ld_nt(&Bb[((size_t) tile * (IXD / 4) + c) * BT]);
-    for (int i = threadIdx.x; i < IXH * IXD / 4; i += 256) {
-        const int h = i / (IXD / 4), c = i % (IXD / 4);
-        qs[c][h] = reinterpret_cast<const float4 *>(a.Qix + ((size_t) bt * IXH + h) * IXD)[c];
+        for (int c = 0; c < CW; ++c) kf[c] = ld_nt(&Bb[((size_t) tile * (IXD / 4) + c) * BT]);
+    }
+    int jn = -1;  // PREP: the block this call's key completes, when this workgroup builds it
+    if constexpr (PREP) {
+        const bool valid = P >= 0 && P < a.max_ctx;
+        if (!valid) {  // past the cache: nothing to append; the status word says so
+            if (blockIdx.y == 0 && threadIdx.x == 0) atomicOr(a.status, FN_STATUS_POS);
+        } else {
+            if (blockIdx.y == 0 && wave == 0)
+                reinterpret_cast<float2 *>(a.IKc + ((size_t) b * a.max_ctx + P) * IXD)[lane] = nk;
+            if ((P + 1) % IXR == 0 && (P / IXR / BT) % (int) gridDim.y == (int) blockIdx.y) jn = P / IXR;
+        }
+        const float2 y = norm_rope_row(x, a.wqn, buf[wave], lane, P, a.nrot, a.inv_freq, a.eps);
+        float *qf = reinterpret_cast<float *>(qs);
+        qf[((2 * lane / 4) * IXH + wave) * 4 + (2 * lane) % 4] = y.x;
+        qf[((2 * lane / 4) * IXH + wave) * 4 + (2 * lane) % 4 + 1] = y.y;
+        if (jn >= 0 && wave == 0) {  // (uniform in the wave)
+            // block_key's sum: the 4 raw keys in order, the last one the new key (its cached copy's bits)
+            float2 sm = make_float2(0.0f, 0.0f);
+#pragma unroll
+            for (int e = 0; e < IXR; ++e) {
+                const float2 v = e < IXR - 1 ? rk[e] : nk;
+                sm.x += v.x;
+                sm.y += v.y;
+            }
+            sm.x /= IXR;
+            sm.y /= IXR;
+            const float2 bk = norm_rope_row(sm, a.wkn, buf[0], lane, jn * IXR, a.nrot, a.inv_freq, a.eps);
+            a.BKc[bk_index(a.max_ctx, b, jn, 2 * lane)] = bk.x;
+            a.BKc[bk_index(a.max_ctx, b, jn, 2 * lane + 1)] = bk.y;
+            buf[0][2 * lane] = bk.x;
+            buf[0][2 * lane + 1] = bk.y;
+        }
+    }
+    if (!live) return;  // (after the appends: a dense query's caches still grow)
+    if constexpr (!PREP) {
+        for (int i = threadIdx.x; i < IXH * IXD / 4; i += 256) {
+            const int h = i / (IXD / 4), c = i % (IXD / 4);
+            qs[c][h] = reinterpret_cast<const float4 *>(a.Qix + ((size_t) bt * IXH + h) * IXD)[c];
+        }
     }
     __syncthreads();
     const float inv = 1.0f / sqrtf((float) IXD);
     float *out = a.scores + (size_t) bt * (a.max_ctx / IXR);
     for (int it = 0; tile < ntiles; tile += gridDim.y, ++it) {
+        if (PREP && jn >= 0 && tile == jn / BT && lane == jn % BT) {  // block jn from this workgroup's own copy
+#pragma unroll
+            for (int c = 0; c < CW; ++c)
+                kf[c] = reinterpret_cast<const float4 *>(buf[0])[wave * CW + c];
+        }
         float s[IXH] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int c = 0; c < CW; ++c)
@@ -461,9 +526,13 @@ int qsa_select_launch(const QsaIndexer &p, float *work, size_t work_bytes, const
     const int tiles = p.max_ctx / IXR / BT;
     const int G = (int) std::max<size_t>(1, std::min<size_t>(tiles, (1024 + bt - 1) / bt));
     const int nbmax = p.max_ctx / IXR;
-    hipLaunchKernelGGL(k_ix_prep, dim3(p.B), dim3(256), 0, st, a);
-    stage_mark(st);
-    hipLaunchKernelGGL(k_ix_score, dim3((unsigned) bt, G), dim3(256), 0, st, a);
+    if (p.nt == 1) {  // the prep inside the scoring launch
+        hipLaunchKernelGGL(k_ix_score<true>, dim3((unsigned) bt, G), dim3(256), 0, st, a);
+    } else {
+        hipLaunchKernelGGL(k_ix_prep, dim3(p.B), dim3(256), 0, st, a);
+        stage_mark(st);
+        hipLaunchKernelGGL(k_ix_score<false>, dim3((unsigned) bt, G), dim3(256), 0, st, a);
+    }
     stage_mark(st);
     if (nbmax <= 1024 * 8)
         hipLaunchKernelGGL(k_ix_select<8>, dim3((unsigned) bt), dim3(1024), 0, st, a);

@@ -11,6 +11,7 @@ Checked separately, so that an exact selection rule is held to an exact standard
 import numpy as np
 import pytest
 
+import hiprt
 import oracle
 
 pytestmark = pytest.mark.gpu
@@ -151,3 +152,88 @@ def test_qsa_select_storage_paths(fnlib, max_ctx, pos, top):
     _say(f"qsa select paths max_ctx={max_ctx} pos={pos} top={top}")
     c = make_case(1, 1, max_ctx, [pos], seed=5 + pos % 7)
     assert run_and_check(fnlib, c, top=top) == 1
+
+
+def test_qsa_one_token_prep_inside_scoring_same_bits(fnlib):
+    """One-token calls run the index query prep inside the scoring launch; a two-token call runs it as its own
+    launch.  Token 0 of the two-token call sees what the one-token call sees, so its scores, its kept blocks and the
+    raw key it appends must be the same bits.  Both positions complete a block (699: block 174, scored by the third
+    scoring workgroup of its query; 131: block 32 by the first, which also appends the raw key) and both queries are
+    sparse at top 32."""
+    _say("qsa one-token prep fused vs two-token call, pos 699 / 131, top 32")
+    c = make_case(2, 2, 768, [699, 131], seed=8)
+    out = []
+    for nt in (2, 1):
+        Kc, Vc, IKc = c["Kc"].copy(), c["Vc"].copy(), c["IKc"].copy()
+        og, sc, mask = fnlib.attn_qsa(c["qg"][:, :nt], c["k"][:, :nt], c["v"][:, :nt], c["wq"], c["wk"], Kc, Vc,
+                                      c["iqk"][:, :nt], c["wqn"], c["wkn"], IKc, c["pos"], top=32)
+        out.append((sc[:, 0], mask[:, 0], IKc))
+    for b, p in enumerate((699, 131)):
+        nb = (p + 1) // 4
+        assert np.array_equal(out[0][0][b, :nb], out[1][0][b, :nb]), b
+        assert np.array_equal(out[0][1][b], out[1][1][b]), b
+        assert np.array_equal(out[0][2][b, p], out[1][2][b, p]), b
+        assert np.array_equal(out[1][2][b, p], c["iqk"][b, 0, 512:]), b
+
+
+def test_qsa_block_keys_written_by_one_token_calls(fnlib):
+    """Consecutive one-token calls on device caches: the block keys the scoring launches write (for dense queries
+    too) equal block keys rebuilt from the raw keys afterwards, bit for bit, and every call's output equals that of a
+    twin whose block keys are rebuilt from its raw keys before each call.  Sequence 0 stays sparse (297 .. 302,
+    completing block 74); sequence 1 starts dense at top 32 (126: 31 blocks; 127 completes block 31 while still
+    dense) and turns sparse at 131, where it scores block 31 as written by the dense call and completes block 32."""
+    B, nq, nkv, hd, max_ctx, top = 2, 16, 2, 256, 768, 32
+    fnlib.dev_status()  # (clears bits earlier tests left)
+    nsplit = fnlib.attn_nsplit(B, nkv, 1, 4 * top + 4)
+    wb = fnlib.attn_qsa_work_bytes(B, nq, 1, nsplit, max_ctx, top)
+    rng = np.random.default_rng(9)
+    cache, ikn, bkn = B * nkv * max_ctx * hd, B * max_ctx * 128, B * max_ctx // 4 * 128
+    w = {n: hiprt.Buf.like(rng.normal(1.0, 0.1, m).astype(np.float32))
+         for n, m in (("wq", hd), ("wk", hd), ("wqn", 128), ("wkn", 128))}
+    twins = []
+    for i in range(2):
+        d = {"K": hiprt.Buf.empty((cache,)), "V": hiprt.Buf.empty((cache,)), "IK": hiprt.Buf.empty((ikn,)),
+             "BK": hiprt.Buf.empty((bkn,)), "work": hiprt.Buf(wb), "og": hiprt.Buf.empty((B, 1, nq, hd)),
+             "pos": hiprt.Buf.empty((B,), np.int32)}
+        for j, key in enumerate(("K", "V", "IK")):
+            fnlib.fill_normal_dev(d[key].ptr, d[key].nbytes // 4, 40 + j)  # the same contents in both twins
+        d["BK"].zero()
+        fnlib.ix_blocks_dev(B, max_ctx, 0, max_ctx // 4, d["IK"].ptr, w["wkn"].ptr, d["BK"].ptr)
+        twins.append(d)
+    pos0 = np.array([297, 126], np.int32)
+    for step in range(6):
+        pos = pos0 + step
+        _say(f"qsa one-token device step {step}: pos {pos.tolist()}")
+        x = {n: hiprt.Buf.like(rng.standard_normal(s).astype(np.float32))
+             for n, s in (("qg", (B, 1, nq, 2, hd)), ("k", (B, 1, nkv, hd)), ("v", (B, 1, nkv, hd)),
+                          ("iqk", (B, 1, 640)))}
+        ogs = []
+        for i, d in enumerate(twins):
+            if i == 1:  # the twin's block keys rebuilt from its raw keys (those not yet complete are not read)
+                fnlib.ix_blocks_dev(B, max_ctx, 0, max_ctx // 4, d["IK"].ptr, w["wkn"].ptr, d["BK"].ptr)
+            d["pos"].upload(pos)
+            fnlib.attn_qsa_dev(B, nq, nkv, 1, max_ctx, d["pos"].ptr, x["qg"].ptr, x["k"].ptr, x["v"].ptr,
+                               w["wq"].ptr, w["wk"].ptr, d["K"].ptr, d["V"].ptr, x["iqk"].ptr, w["wqn"].ptr,
+                               w["wkn"].ptr, d["IK"].ptr, d["BK"].ptr, top, nsplit, d["work"].ptr, wb, d["og"].ptr)
+            hiprt.sync()
+            ogs.append(d["og"].download())
+        assert np.array_equal(ogs[0], ogs[1]), step
+        for b in x.values():
+            b.free()
+    assert fnlib.dev_status() == 0
+    # the written block keys against a rebuild from the final raw keys, every block complete in both sequences
+    a = twins[0]
+    got = a["BK"].download((B, max_ctx // 4 // 64, 32, 64, 4))
+    fnlib.ix_blocks_dev(B, max_ctx, 0, max_ctx // 4, a["IK"].ptr, w["wkn"].ptr, a["BK"].ptr)
+    hiprt.sync()
+    want = a["BK"].download((B, max_ctx // 4 // 64, 32, 64, 4))
+    for b in range(B):
+        nb = (int(pos0[b]) + 6) // 4
+        g = got[b].transpose(0, 2, 1, 3).reshape(-1, 128)[:nb]
+        r = want[b].transpose(0, 2, 1, 3).reshape(-1, 128)[:nb]
+        assert np.array_equal(g, r), b
+    for d in twins:
+        for buf in d.values():
+            buf.free()
+    for buf in w.values():
+        buf.free()
