@@ -327,15 +327,17 @@ __global__ void __launch_bounds__(256) k_argmax_part(const float *__restrict__ l
     }
 }
 
-// grid nt, 64 threads
+// grid nt, 64 threads.  The forward's last kernel: it also moves the sequence position on by nt (one launch fewer
+// than a separate advance; nothing after it in the forward reads the position)
 __global__ void k_argmax_merge(const float *__restrict__ pv, const int32_t *__restrict__ pi, int V,
-                               int32_t *__restrict__ out) {
+                               int32_t *__restrict__ out, int32_t *__restrict__ pos) {
     const int t = blockIdx.x;
     float v = -INFINITY;
     int idx = V;
     for (int k = threadIdx.x; k < AM_CH; k += 64) vi_max(v, idx, pv[t * AM_CH + k], pi[t * AM_CH + k]);
     wave_argmax(v, idx);
     if (threadIdx.x == 0) out[t] = idx == V ? 0 : idx;
+    if (t == 0 && threadIdx.x == 0) pos[0] += (int) gridDim.x;
 }
 
 // ---- forward ----
@@ -541,9 +543,9 @@ int enqueue(Model &m, int nt) {
         return -1;
     if (gemv(m.top.q(LM_HEAD), a.x, nt, a.logits, m.st)) return -1;
     hipLaunchKernelGGL(k_argmax_part, dim3(nt, AM_CH), dim3(256), 0, m.st, a.logits, d.VOCAB, a.amv, a.ami);
-    hipLaunchKernelGGL(k_argmax_merge, dim3(nt), dim3(64), 0, m.st, a.amv, a.ami, d.VOCAB, a.am);
+    hipLaunchKernelGGL(k_argmax_merge, dim3(nt), dim3(64), 0, m.st, a.amv, a.ami, d.VOCAB, a.am, a.pos);
     FN_CK(hipGetLastError());
-    return advance_launch(a.pos, 1, nt, m.st);
+    return 0;
 }
 
 int capture(Model &m, int nt) {
