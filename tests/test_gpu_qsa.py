@@ -237,3 +237,49 @@ def test_qsa_block_keys_written_by_one_token_calls(fnlib):
             buf.free()
     for buf in w.values():
         buf.free()
+
+
+def test_qsa_position_outside_cache_sets_status(fnlib):
+    """A new token at or past max_ctx in a sparse layer (one-token calls with the prep inside the scoring launch, and
+    a three-token call): the status word records FN_STATUS_POS, that sequence's raw and block keys are left as they
+    were, the other sequence appends its raw key (and, at 511, builds its last block's key), and the output is
+    finite."""
+    import fn
+
+    B, nq, nkv, hd, max_ctx, top = 2, 16, 2, 256, 512, 32
+    fnlib.dev_status()  # start clean
+    rng = np.random.default_rng(12)
+    for nt, pos in ((1, [511, 512]), (3, [505, 600])):
+        _say(f"qsa position outside the cache: nt={nt} pos={pos}")
+        nsplit = fnlib.attn_nsplit(B, nkv, nt, 4 * top + 4)
+        wb = fnlib.attn_qsa_work_bytes(B, nq, nt, nsplit, max_ctx, top)
+        cache, ikn, bkn = B * nkv * max_ctx * hd, B * max_ctx * 128, B * max_ctx // 4 * 128
+        K, V = hiprt.Buf.empty((cache,)), hiprt.Buf.empty((cache,))
+        IK, BK = hiprt.Buf.empty((ikn,)), hiprt.Buf.empty((bkn,))
+        for j, buf in enumerate((K, V, IK, BK)):
+            fnlib.fill_normal_dev(buf.ptr, buf.nbytes // 4, 60 + j)
+        hiprt.sync()
+        ik0, bk0 = IK.download((B, max_ctx, 128)), BK.download((B, bkn // B))
+        iqk = rng.standard_normal((B, nt, 640)).astype(np.float32)
+        d = {n: hiprt.Buf.like(x) for n, x in (
+            ("qg", rng.standard_normal((B, nt, nq, 2, hd)).astype(np.float32)),
+            ("k", rng.standard_normal((B, nt, nkv, hd)).astype(np.float32)),
+            ("v", rng.standard_normal((B, nt, nkv, hd)).astype(np.float32)), ("iqk", iqk),
+            ("wq", np.ones(hd, np.float32)), ("wk", np.ones(hd, np.float32)), ("wqn", np.ones(128, np.float32)),
+            ("wkn", np.ones(128, np.float32)), ("pos", np.array(pos, np.int32)))}
+        work, og = hiprt.Buf(wb), hiprt.Buf.empty((B, nt, nq, hd))
+        fnlib.attn_qsa_dev(B, nq, nkv, nt, max_ctx, d["pos"].ptr, d["qg"].ptr, d["k"].ptr, d["v"].ptr, d["wq"].ptr,
+                           d["wk"].ptr, K.ptr, V.ptr, d["iqk"].ptr, d["wqn"].ptr, d["wkn"].ptr, IK.ptr, BK.ptr, top,
+                           nsplit, work.ptr, wb, og.ptr)
+        assert fnlib.dev_status(clear=False) & fn.STATUS_POS
+        assert fnlib.dev_status() & fn.STATUS_POS
+        assert fnlib.dev_status() == 0
+        assert np.isfinite(og.download()).all()
+        ik, bk = IK.download((B, max_ctx, 128)), BK.download((B, bkn // B))
+        assert np.array_equal(ik[1], ik0[1]) and np.array_equal(bk[1], bk0[1])  # the sequence past the cache
+        p0 = pos[0]
+        n_in = min(nt, max_ctx - p0)
+        assert np.array_equal(ik[0, p0:p0 + n_in], iqk[0, :n_in, 512:])
+        assert np.array_equal(ik[0, :p0], ik0[0, :p0])
+        for x in (K, V, IK, BK, work, og, *d.values()):
+            x.free()
