@@ -55,9 +55,6 @@ __device__ __forceinline__ float swz_xor16(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401f));
 }
 
-// value of lane l ^ 32 (a lane permute through the LDS crossbar, no LDS memory)
-__device__ __forceinline__ float shfl_xor32(float v) { return __shfl_xor(v, 32); }
-
 // sum over the 16 lanes of each row, returned to every lane of the row (every lane gets the same bits)
 __device__ __forceinline__ float row_sum(float v) {
     v += dpp_ror<8>(v);
@@ -232,7 +229,6 @@ __device__ __forceinline__ float4 add_scaled(float4 h, float4 y, float s) {
     return make_float4(__builtin_fmaf(y.x, s, h.x), __builtin_fmaf(y.y, s, h.y), __builtin_fmaf(y.z, s, h.z),
                        __builtin_fmaf(y.w, s, h.w));
 }
-__device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }
 
 __device__ __forceinline__ float4 f4(float a) { return make_float4(a, a, a, a); }
 
